@@ -1,0 +1,382 @@
+"""ctypes front end of the CPU oracle (oracle/bitnet_oracle.c).
+
+TEST INFRASTRUCTURE ONLY.  Imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, never by the product package ``loom_amd``.
+
+The C library restates loom's BitNet CPU path (poly/bitnet_cpu.go,
+poly/dense.go, poly/swiglu.go, poly/norm.go, poly/entity_bitnet.go); each C
+function cites the reference line it follows.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from dataclasses import dataclass
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "build", "libbitnet_oracle.so")
+
+ACT_RELU, ACT_SILU, ACT_GELU, ACT_TANH, ACT_SIGMOID, ACT_LEAKY_RELU, ACT_RELU2 = range(7)
+ACT_LINEAR = -1
+
+_lib = None
+
+
+def build() -> str:
+    """Compile the oracle with its Makefile (gcc); returns the library path."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = C.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+P = C.c_void_p
+
+
+def _declare(L: C.CDLL) -> None:
+    i, f, d, u8, sz = C.c_int, C.c_float, C.c_double, C.c_uint8, C.c_size_t
+    sig = {
+        "orc_act_maxabs_f32": (f, [P, i]),
+        "orc_act_maxabs_f64": (f, [P, i]),
+        "orc_quant_value_act": (C.c_int8, [d, f]),
+        "orc_quant_act_f32": (f, [P, i, P]),
+        "orc_quant_act_f64": (f, [P, i, P]),
+        "orc_ternary_scale": (f, [P, C.c_long]),
+        "orc_quant_value": (u8, [f, f]),
+        "orc_storage_to_code": (u8, [u8]),
+        "orc_pack_ternary_rows": (None, [P, i, i, P]),
+        "orc_pack_float32": (f, [P, i, i, P]),
+        "orc_pack_ms_offline_bytes": (None, [P, i, i, P]),
+        "orc_pack_ms_offline_float_slots": (None, [P, i, i, P]),
+        "orc_output_scale": (d, [f, f]),
+        "orc_matvec_scalar": (None, [P, i, i, i, P, d, P, P]),
+        "orc_codes_stride": (i, [i]),
+        "orc_ensure_codes": (None, [P, i, i, i, P]),
+        "orc_code_row_dot_go": (C.c_int32, [P, P, i]),
+        "orc_code_row_dot_avx2": (C.c_int32, [P, P, i]),
+        "orc_simd_available": (i, []),
+        "orc_matvec_simd": (None, [P, i, i, P, d, P, P, i]),
+        "orc_run_rows_plan": (None, [i, i, i, P, P]),
+        "orc_dense_forward": (None, [P, P, i, i, i, i, P, P, P, P, P]),
+        "orc_activate_f32": (f, [f, i]),
+        "orc_swiglu_gate_product": (d, [d, d, i]),
+        "orc_bitnet_rmsnorm_row_f32": (None, [P, i, P, d]),
+        "orc_bitnet_rmsnorm_f64": (None, [P, i, P, d]),
+        "orc_swiglu_forward": (None, [P, P, P, P, P, d, i, P, i, i, i,
+                                      P, P, P, P, P, P, P, P, P]),
+        "orc_rmsnorm_forward": (None, [P, i, i, P, d, P, P]),
+        "orc_entity_blob_bytes": (sz, [i]),
+        "orc_entity_encode": (sz, [i, i, i, f, i, P, i, P]),
+        "orc_entity_decode_header": (i, [P, sz, P, P, P, P, P, P]),
+        "orc_deterministic_weights": (None, [P, i]),
+        "orc_fill_normal_f32": (None, [P, C.c_long, C.c_uint64]),
+        "orc_fill_ternary_codes": (None, [P, C.c_long, C.c_uint64]),
+        "orc_fill_uniform_f32": (None, [P, C.c_long, f, f, C.c_uint64]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(P)
+
+
+# ---------------------------------------------------------------- inputs
+def deterministic_weights(n: int) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().orc_deterministic_weights(_p(out), n)
+    return out
+
+
+def normal_f32(n: int, seed: int) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().orc_fill_normal_f32(_p(out), n, seed)
+    return out
+
+
+def uniform_f32(n: int, lo: float, hi: float, seed: int) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().orc_fill_uniform_f32(_p(out), n, lo, hi, seed)
+    return out
+
+
+def ternary_native(n: int, seed: int) -> np.ndarray:
+    """uint8(int8) ternary storage values, P(0)=.5, P(+1)=P(-1)=.25."""
+    out = np.empty(n, np.uint8)
+    lib().orc_fill_ternary_codes(_p(out), n, seed)
+    return out
+
+
+# ---------------------------------------------------------------- matrix
+@dataclass
+class Matrix:
+    """BitNetTernaryMatrix (poly/bitnet_cpu.go:14-43): row-major packed words."""
+    rows: int
+    cols: int
+    scale: float
+    words: np.ndarray  # uint32, rows*row_words
+    codes: np.ndarray | None = None
+
+    @property
+    def row_words(self) -> int:
+        return (self.cols + 15) // 16
+
+    def ensure_codes(self) -> np.ndarray:
+        if self.codes is None:
+            stride = lib().orc_codes_stride(self.cols)
+            self.codes = np.empty(self.rows * stride, np.uint8)
+            lib().orc_ensure_codes(_p(self.words), self.rows, self.cols, self.row_words,
+                                   _p(self.codes))
+        return self.codes
+
+    def _c(self, simd: bool):
+        class _M(C.Structure):
+            _fields_ = [("rows", C.c_int), ("cols", C.c_int), ("row_words", C.c_int),
+                        ("scale", C.c_float), ("words", P), ("codes", P)]
+        codes = self.ensure_codes() if simd else None
+        return _M(self.rows, self.cols, self.row_words, self.scale, _p(self.words), _p(codes))
+
+    def entity_blob(self, offset: int = 0) -> bytes:
+        return entity_encode(self.rows, self.cols, offset, self.scale, self.row_words, self.words)
+
+
+def pack_native(native: np.ndarray, rows: int, cols: int, scale: float) -> Matrix:
+    """packNativeTernaryToBitNetMatrix (poly/bitnet_cpu.go:918-932)."""
+    native = np.ascontiguousarray(native, np.uint8)
+    words = np.empty(rows * ((cols + 15) // 16), np.uint32)
+    lib().orc_pack_ternary_rows(_p(native), rows, cols, _p(words))
+    return Matrix(rows, cols, float(np.float32(scale if scale != 0 else 1.0)), words)
+
+
+def pack_float32(master: np.ndarray, rows: int, cols: int) -> Matrix:
+    """packFloat32AsBitNetTernaryMatrix (poly/bitnet_cpu.go:934-962)."""
+    master = np.ascontiguousarray(master, np.float32)
+    words = np.empty(rows * ((cols + 15) // 16), np.uint32)
+    scale = lib().orc_pack_float32(_p(master), rows, cols, _p(words))
+    return Matrix(rows, cols, float(scale), words)
+
+
+def pack_ms_offline_bytes(packed: np.ndarray, rows: int, cols: int, scale: float = 1.0) -> Matrix:
+    packed = np.ascontiguousarray(packed, np.uint8)
+    words = np.empty(rows * ((cols + 15) // 16), np.uint32)
+    lib().orc_pack_ms_offline_bytes(_p(packed), rows, cols, _p(words))
+    return Matrix(rows, cols, scale, words)
+
+
+def pack_ms_offline_float_slots(packed: np.ndarray, rows: int, cols: int, scale: float = 1.0) -> Matrix:
+    packed = np.ascontiguousarray(packed, np.float32)
+    words = np.empty(rows * ((cols + 15) // 16), np.uint32)
+    lib().orc_pack_ms_offline_float_slots(_p(packed), rows, cols, _p(words))
+    return Matrix(rows, cols, scale, words)
+
+
+def random_matrix(rows: int, cols: int, seed: int, alpha: float = 0.02) -> Matrix:
+    """Synthetic BitNet weights: ternary codes times alpha, packed by loom's
+    float32 packer so Scale is loom's absmean of the master."""
+    native = ternary_native(rows * cols, seed)
+    master = native.view(np.int8).astype(np.float32) * np.float32(alpha)
+    return pack_float32(master, rows, cols)
+
+
+# ---------------------------------------------------------------- quant
+def act_maxabs(x: np.ndarray) -> float:
+    x = np.ascontiguousarray(x)
+    if x.dtype == np.float64:
+        return float(lib().orc_act_maxabs_f64(_p(x), x.size))
+    x = x.astype(np.float32, copy=False)
+    return float(lib().orc_act_maxabs_f32(_p(x), x.size))
+
+
+def quant_act(x: np.ndarray) -> tuple[np.ndarray, float]:
+    x = np.ascontiguousarray(x)
+    q = np.empty(x.size, np.int8)
+    if x.dtype == np.float64:
+        amax = lib().orc_quant_act_f64(_p(x), x.size, _p(q))
+    else:
+        x = x.astype(np.float32, copy=False)
+        amax = lib().orc_quant_act_f32(_p(x), x.size, _p(q))
+    return q, float(amax)
+
+
+def quant_act_rows(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    x = np.ascontiguousarray(x, np.float32)
+    q = np.empty(x.shape, np.int8)
+    amax = np.empty(x.shape[0], np.float32)
+    for r in range(x.shape[0]):
+        amax[r] = lib().orc_quant_act_f32(_p(x[r]), x.shape[1], _p(q[r]))
+    return q, amax
+
+
+def ternary_scale(w: np.ndarray) -> float:
+    w = np.ascontiguousarray(w, np.float32)
+    return float(lib().orc_ternary_scale(_p(w), w.size))
+
+
+def quant_value(v: float, scale: float) -> int:
+    return int(np.uint8(lib().orc_quant_value(v, scale)).view(np.int8))
+
+
+def output_scale(weight_scale: float, amax: float) -> float:
+    return float(lib().orc_output_scale(weight_scale, amax))
+
+
+# ---------------------------------------------------------------- matvec
+def matvec_scalar(m: Matrix, xq: np.ndarray, output_scale_: float):
+    xq = np.ascontiguousarray(xq, np.int8)
+    out = np.empty(m.rows, np.float64)
+    acc = np.empty(m.rows, np.int32)
+    lib().orc_matvec_scalar(_p(m.words), m.rows, m.cols, m.row_words, _p(xq),
+                            output_scale_, _p(out), _p(acc))
+    return out, acc
+
+
+def matvec_simd(m: Matrix, xq: np.ndarray, output_scale_: float, workers: int = 0):
+    xq = np.ascontiguousarray(xq, np.int8)
+    codes = m.ensure_codes()
+    out = np.empty(m.rows, np.float64)
+    acc = np.empty(m.rows, np.int32)
+    lib().orc_matvec_simd(_p(codes), m.rows, m.cols, _p(xq), output_scale_, _p(out), _p(acc),
+                          workers or (os.cpu_count() or 1))
+    return out, acc
+
+
+def code_row_dot(codes: np.ndarray, acts: np.ndarray, avx2: bool) -> int:
+    codes = np.ascontiguousarray(codes, np.uint8)
+    acts = np.ascontiguousarray(acts, np.int8)
+    fn = lib().orc_code_row_dot_avx2 if avx2 else lib().orc_code_row_dot_go
+    return int(fn(_p(codes), _p(acts), codes.size))
+
+
+def simd_available() -> bool:
+    return bool(lib().orc_simd_available())
+
+
+# ---------------------------------------------------------------- layers
+@dataclass
+class DenseResult:
+    pre: np.ndarray
+    post: np.ndarray
+    xq: np.ndarray
+    amax: np.ndarray
+    acc: np.ndarray
+
+
+def dense_forward(m: Matrix, x: np.ndarray, activation: int = ACT_LINEAR, simd: bool = True,
+                  workers: int = 0) -> DenseResult:
+    """DenseForwardPackedTernaryCPU (poly/dense.go:66-101)."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, m.cols)
+    M = x.shape[0]
+    pre = np.empty((M, m.rows), np.float32)
+    post = np.empty((M, m.rows), np.float32)
+    xq = np.empty((M, m.cols), np.int8)
+    amax = np.empty(M, np.float32)
+    acc = np.empty((M, m.rows), np.int32)
+    cm = m._c(simd)
+    lib().orc_dense_forward(C.byref(cm), _p(x), M, activation, int(simd),
+                            workers or (os.cpu_count() or 1),
+                            _p(pre), _p(post), _p(xq), _p(amax), _p(acc))
+    return DenseResult(pre, post, xq, amax, acc)
+
+
+@dataclass
+class SwiGLUResult:
+    out: np.ndarray
+    h: np.ndarray
+    xq: np.ndarray
+    amax: np.ndarray
+    hq: np.ndarray
+    hamax: np.ndarray
+    acc_gate: np.ndarray
+    acc_up: np.ndarray
+    acc_down: np.ndarray
+
+
+def swiglu_forward(gate: Matrix, up: Matrix, down: Matrix, x: np.ndarray,
+                   inner_norm: np.ndarray | None = None, bias: np.ndarray | None = None,
+                   eps: float = 1e-5, activation: int = ACT_SILU, simd: bool = True,
+                   workers: int = 0) -> SwiGLUResult:
+    """SwiGLUForwardPackedTernaryCPU (poly/swiglu.go:270-322)."""
+    hidden, inter = gate.cols, gate.rows
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, hidden)
+    M = x.shape[0]
+    out = np.empty((M, hidden), np.float32)
+    h = np.empty((M, inter), np.float32)
+    xq = np.empty((M, hidden), np.int8)
+    amax = np.empty(M, np.float32)
+    hq = np.empty((M, inter), np.int8)
+    hamax = np.empty(M, np.float32)
+    ag = np.empty((M, inter), np.int32)
+    au = np.empty((M, inter), np.int32)
+    ad = np.empty((M, hidden), np.int32)
+    cg, cu, cd = gate._c(simd), up._c(simd), down._c(simd)
+    nw = None if inner_norm is None else np.ascontiguousarray(inner_norm, np.float32)
+    bs = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    lib().orc_swiglu_forward(C.byref(cg), C.byref(cu), C.byref(cd), _p(bs), _p(nw), eps,
+                             activation, _p(x), M, int(simd), workers or (os.cpu_count() or 1),
+                             _p(out), _p(h), _p(xq), _p(amax), _p(hq), _p(hamax),
+                             _p(ag), _p(au), _p(ad))
+    return SwiGLUResult(out, h, xq, amax, hq, hamax, ag, au, ad)
+
+
+def swiglu_gate_product(g: float, u: float, activation: int = ACT_SILU) -> float:
+    return float(lib().orc_swiglu_gate_product(g, u, activation))
+
+
+def bitnet_rmsnorm_row(h: np.ndarray, weight: np.ndarray | None, eps: float) -> np.ndarray:
+    h = np.array(h, np.float32, copy=True)
+    w = None if weight is None else np.ascontiguousarray(weight, np.float32)
+    lib().orc_bitnet_rmsnorm_row_f32(_p(h), h.size, _p(w), eps)
+    return h
+
+
+def rmsnorm_forward(x: np.ndarray, gain: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    rows, n = x.shape
+    g = np.ascontiguousarray(gain, np.float32)
+    y = np.empty_like(x)
+    lib().orc_rmsnorm_forward(_p(x), rows, n, _p(g), eps, _p(y), None)
+    return y
+
+
+def activate(v: float, activation: int) -> float:
+    return float(lib().orc_activate_f32(v, activation))
+
+
+# ---------------------------------------------------------------- entity blob
+def entity_encode(rows: int, cols: int, offset: int, scale: float, row_words: int,
+                  words: np.ndarray) -> bytes:
+    words = np.ascontiguousarray(words, np.uint32)
+    n = int(lib().orc_entity_blob_bytes(words.size))
+    raw = np.empty(n, np.uint8)
+    lib().orc_entity_encode(rows, cols, offset, scale, row_words, _p(words), words.size, _p(raw))
+    return raw.tobytes()
+
+
+def entity_decode(raw: bytes) -> tuple[Matrix, int]:
+    buf = np.frombuffer(raw, np.uint8)
+    vals = [C.c_int() for _ in range(5)]
+    scale = C.c_float()
+    rc = lib().orc_entity_decode_header(_p(buf), buf.size, C.byref(vals[0]), C.byref(vals[1]),
+                                        C.byref(vals[2]), C.byref(scale), C.byref(vals[3]),
+                                        C.byref(vals[4]))
+    if rc == -1:
+        raise ValueError("bitnet ternary blob too short")
+    if rc == -2:
+        raise ValueError("bitnet ternary blob truncated")
+    rows, cols, offset, row_words, n_words = (v.value for v in vals)
+    words = np.frombuffer(raw, np.uint32, count=n_words, offset=24).copy()
+    m = Matrix(rows, cols, scale.value, words)
+    return m, offset

@@ -1,0 +1,310 @@
+"""Pins the CPU oracle to loom's own known-answer tests and to closed forms.
+
+Each test names the reference test (or the mathematical fact) it checks.
+Citations are relative to the loom v0.83.0 tree.
+"""
+import math
+
+import numpy as np
+import pytest
+
+
+# ---------------------------------------------------------------- weight quant
+def test_absmean_quantizer_kat(orc):
+    # TestBitNetTernaryQuantizerUsesAbsMean (poly/tests/bitnet_cpu_test.go:134-153)
+    master = np.array([-0.2, -0.8, 0.1, 0.8], np.float32)
+    scale = orc.ternary_scale(master)
+    assert abs(scale - 0.475) <= 1e-6
+    assert [orc.quant_value(v, scale) for v in master] == [0, -1, 0, 1]
+
+
+def test_absmean_scale_closed_forms(orc):
+    # bitNetTernaryScale: empty and all-zero masters give 1.0; absmean otherwise.
+    assert orc.ternary_scale(np.zeros(0, np.float32)) == 1.0
+    assert orc.ternary_scale(np.zeros(9, np.float32)) == 1.0
+    w = np.array([3.0, -1.0, 0.0, 4.0], np.float32)
+    assert orc.ternary_scale(w) == np.float32(2.0)
+
+
+def test_quant_value_rounds_half_away(orc):
+    # math.Round is half away from zero: v/scale = +-0.5 -> +-1 (ties-to-even gives 0).
+    assert orc.quant_value(1.0, 2.0) == 1
+    assert orc.quant_value(-1.0, 2.0) == -1
+    assert orc.quant_value(0.999, 2.0) == 0
+    assert orc.quant_value(100.0, 1.0) == 1
+    assert orc.quant_value(-100.0, 1.0) == -1
+    assert orc.quant_value(0.5, 0.0) == 1  # scale 0 -> 1
+
+
+def test_already_ternary_master_packs_at_unit_scale(orc):
+    # packFloat32AsBitNetTernaryMatrix alreadyTernary quirk (poly/bitnet_cpu.go:941-954)
+    master = np.array([1, 0, -1, 1, 1, 0, 0, -1], np.float32)
+    m = orc.pack_float32(master, 2, 4)
+    assert m.scale == 1.0
+    # codes: -1 -> 0, 0 -> 1, +1 -> 2 at bits 2*(c%16)
+    assert m.words[0] == (2 | 1 << 2 | 0 << 4 | 2 << 6)
+    assert m.words[1] == (2 | 1 << 2 | 1 << 4 | 0 << 6)
+    # the same values times 0.02 use the absmean scale instead
+    m2 = orc.pack_float32(master * np.float32(0.02), 2, 4)
+    assert m2.scale != 1.0
+    assert np.array_equal(m2.words, m.words)
+
+
+# ---------------------------------------------------------------- packers
+def test_microsoft_offline_decode_kat(orc):
+    # TestMicrosoftOfflinePackedBitNetRowsDecode (poly/tests/bitnet_cpu_test.go:334-362)
+    packed = np.array([0b10100001, 0b00011000, 0b10010000, 0b00001010], np.float32)
+    m = orc.pack_ms_offline_float_slots(packed, 8, 2, scale=0.5)
+    xq = np.array([2, -3], np.int8)
+    out, _ = orc.matvec_scalar(m, xq, orc.output_scale(m.scale, 127.0))
+    assert np.allclose(out, [1.5, -2.5, -2.5, -2.5, 1, 1.5, 2.5, 2.5], atol=1e-6, rtol=0)
+
+
+def test_microsoft_bytes_match_float_slots(orc):
+    # TestSetMicrosoftBitNetPackedMatrixBytesMatchesFloatU8Slots (:284-315)
+    b = np.array([(i * 17) & 0xFF for i in range(8)], np.uint8)
+    a = orc.pack_ms_offline_bytes(b, 8, 4)
+    f = orc.pack_ms_offline_float_slots(b.astype(np.float32), 8, 4)
+    assert np.array_equal(a.words, f.words)
+
+
+def test_microsoft_offline_without_master(orc):
+    # TestGetBitNetTernaryMatrixFindsOfflinePackedWithoutMasterSlab (:317-332)
+    m = orc.pack_ms_offline_float_slots(np.array([0x01, 0x10], np.float32), 4, 2)
+    assert (m.rows, m.cols, m.row_words, m.words.size) == (4, 2, 1, 4)
+    # code 3 maps to code 1 (ternary 0): byte 0xFF decodes to zeros
+    z = orc.pack_ms_offline_bytes(np.array([0xFF, 0xFF], np.uint8), 4, 2)
+    assert np.all(z.words == (1 | 1 << 2))
+
+
+# ---------------------------------------------------------------- matvec
+def _decode(m):
+    """Decode packed words to int ternary values by the documented bit layout."""
+    w = np.zeros((m.rows, m.cols), np.int64)
+    rw = m.row_words
+    for r in range(m.rows):
+        for c in range(m.cols):
+            code = (int(m.words[r * rw + c // 16]) >> (2 * (c % 16))) & 3
+            w[r, c] = code - 1
+    return w
+
+
+def test_tail_columns_brute_force(orc):
+    # TestBitNetTernaryKernelHandlesTailColumns (:216-247): 3x17 against the
+    # closed form sum over quantized weights.
+    rows, cols = 3, 17
+    weights = orc.deterministic_weights(rows * cols)
+    m = orc.pack_float32(weights, rows, cols)
+    xq, amax = orc.quant_act(orc.deterministic_weights(cols))
+    os_ = orc.output_scale(m.scale, amax)
+    got, acc = orc.matvec_scalar(m, xq, os_)
+    for r in range(rows):
+        s = 0
+        for c in range(cols):
+            q = orc.quant_value(float(weights[r * cols + c]), m.scale)
+            s += int(xq[c]) * q
+        assert acc[r] == s
+        assert got[r] == float(s) * os_
+
+
+@pytest.mark.parametrize("rows,cols", [(40, 70), (8, 64), (33, 65), (16, 128),
+                                       (64, 2560), (128, 6912), (7, 191), (3, 17)])
+def test_simd_matches_scalar_bit_identical(orc, rows, cols):
+    # TestBitNetPackedMatVecMatchesScalar / TestBitNetTernaryDenseSimdMatchesScalar
+    # (poly/tests/bitnet_packed_test.go:15-52; bitnet_simd_test.go:13-45)
+    weights = orc.deterministic_weights(rows * cols)
+    x = orc.deterministic_weights(2 * cols).reshape(2, cols)
+    m = orc.pack_float32(weights, rows, cols)
+    scalar = orc.dense_forward(m, x, simd=False)
+    simd = orc.dense_forward(m, x, simd=True, workers=8)
+    assert np.array_equal(scalar.pre.view(np.uint32), simd.pre.view(np.uint32))
+    assert np.array_equal(scalar.acc, simd.acc)
+    # and both equal the brute-force integer product over the decoded weights
+    w = _decode(m)
+    ref = scalar.xq.astype(np.int64) @ w.T
+    assert np.array_equal(ref, scalar.acc.astype(np.int64))
+
+
+@pytest.mark.parametrize("n_bytes", [32, 64, 96, 512, 1536, 4096])
+def test_code_row_dot_avx2_matches_go(orc, n_bytes):
+    # TestBitNetTernaryKernelMatchesGo (poly/simd/bitnet_ternary_test.go:11-36);
+    # Go's math/rand stream (seed 42) cannot be reproduced, so numpy draws the
+    # same distributions: codes in {0,1,2}, acts in [-128,127].
+    if not orc.simd_available():
+        pytest.skip("no AVX2")
+    rng = np.random.default_rng(42)
+    for _ in range(200):
+        codes = rng.integers(0, 3, n_bytes).astype(np.uint8)
+        acts = rng.integers(-128, 128, n_bytes).astype(np.int8)
+        want = int(codes.astype(np.int64) @ acts.astype(np.int64))
+        assert orc.code_row_dot(codes, acts, avx2=False) == want
+        assert orc.code_row_dot(codes, acts, avx2=True) == want
+
+
+def test_run_rows_plan(orc):
+    # bitNetRunRows (poly/bitnet_cpu.go:780-808) chunking thresholds
+    import ctypes as C
+    n, c = C.c_int(), C.c_int()
+    orc.lib().orc_run_rows_plan(6912, 2560, 8, C.byref(n), C.byref(c))
+    assert (n.value, c.value) == (8, 864)
+    orc.lib().orc_run_rows_plan(100, 2000, 8, C.byref(n), C.byref(c))  # work < 262144
+    assert (n.value, c.value) == (1, 100)
+    orc.lib().orc_run_rows_plan(3, 200000, 8, C.byref(n), C.byref(c))  # rows < 4
+    assert (n.value, c.value) == (1, 3)
+    orc.lib().orc_run_rows_plan(10, 100000, 4, C.byref(n), C.byref(c))
+    assert (n.value, c.value) == (4, 3)
+
+
+# ---------------------------------------------------------------- activation quant
+def test_activation_quant_closed_forms(orc):
+    # bitNetQuantizedActivation (poly/bitnet_cpu.go:73-95)
+    q, amax = orc.quant_act(np.array([3.0, -3.0, 0.0, 1.5], np.float32))
+    assert amax == 3.0
+    assert q.tolist() == [127, -127, 0, 64]  # 1.5*127/3 = 63.5 -> 64 (half away)
+    q, amax = orc.quant_act(np.array([-1.5, 0.5, -0.5, 127.0], np.float32))
+    assert amax == 127.0  # scale 1.0: exercises the tie rule directly
+    assert q.tolist() == [-2, 1, -1, 127]
+    q, amax = orc.quant_act(np.zeros(5, np.float32))
+    assert amax == np.float32(1e-5) and not q.any()
+    q, amax = orc.quant_act(np.array([1e-6, -2e-6], np.float32))
+    assert amax == np.float32(1e-5)
+    # NaN never wins the max and converts through Go's amd64 int64 indefinite to -128
+    q, amax = orc.quant_act(np.array([np.nan, 2.0, -1.0], np.float32))
+    assert amax == 2.0 and q.tolist() == [-128, 127, -64]
+
+
+def test_activation_quant_float64_rounds_abs_to_f32(orc):
+    x = np.array([1.0000000001, -0.5], np.float64)
+    q, amax = orc.quant_act(x)
+    assert amax == np.float32(1.0000000001)
+    assert q.tolist() == [127, -64]
+
+
+def test_activation_quant_matches_numpy_restatement(orc):
+    # property: per-element formula holds over a large random row
+    x = orc.normal_f32(4096, 7)
+    q, amax = orc.quant_act(x)
+    assert amax == np.float32(np.max(np.abs(x)))
+    v = x.astype(np.float64) * (127.0 / np.float64(amax))
+    ref = np.clip(np.where(v >= 0, np.floor(v + 0.5), np.ceil(v - 0.5)), -128, 127)
+    assert np.array_equal(q.astype(np.int64), ref.astype(np.int64))
+
+
+# ---------------------------------------------------------------- dense
+def test_packed_dense_matches_dequantized(orc):
+    # TestPackedTernaryDenseMatchesDequantizedPath (poly/tests/bitnet_cpu_test.go:184-214)
+    weights = orc.deterministic_weights(15)
+    scale = orc.ternary_scale(weights)
+    deq = np.array([orc.quant_value(v, scale) for v in weights], np.float32) * np.float32(scale)
+    x = np.array([0.1, -0.2, 0.3, -0.4, 0.5, 0.6, -0.7, 0.8, -0.9, 1.0], np.float32).reshape(2, 5)
+    ref = x.astype(np.float64) @ deq.reshape(3, 5).T.astype(np.float64)
+    got = orc.dense_forward(orc.pack_float32(weights, 3, 5), x, simd=True)
+    assert np.max(np.abs(ref - got.post)) <= 5e-3
+
+
+def test_dense_rows_are_independent(orc):
+    # loom processes batch rows one by one (poly/dense.go:83-99): row b of an
+    # M-row forward equals a 1-row forward of row b.
+    m = orc.random_matrix(96, 200, seed=3)
+    x = orc.normal_f32(4 * 200, 5).reshape(4, 200)
+    full = orc.dense_forward(m, x)
+    for b in range(4):
+        one = orc.dense_forward(m, x[b:b + 1])
+        assert np.array_equal(one.pre[0].view(np.uint32), full.pre[b].view(np.uint32))
+
+
+def test_dense_activations(orc):
+    m = orc.random_matrix(32, 64, seed=9)
+    x = orc.normal_f32(64, 1).reshape(1, 64)
+    lin = orc.dense_forward(m, x, activation=orc.ACT_LINEAR)
+    relu = orc.dense_forward(m, x, activation=orc.ACT_RELU)
+    relu2 = orc.dense_forward(m, x, activation=orc.ACT_RELU2)
+    assert np.array_equal(relu.post, np.where(lin.pre < 0, np.float32(0), lin.pre))
+    assert np.array_equal(relu2.post, np.where(lin.pre < 0, np.float32(0), lin.pre * lin.pre))
+    assert np.array_equal(lin.post, lin.pre)
+
+
+# ---------------------------------------------------------------- swiglu pieces
+def test_gate_product_closed_forms(orc):
+    assert orc.swiglu_gate_product(0.0, 5.0) == 0.0
+    assert orc.swiglu_gate_product(3.0, 0.0) == 0.0
+    assert orc.swiglu_gate_product(-2.0, 3.0, orc.ACT_RELU2) == 0.0
+    assert orc.swiglu_gate_product(2.0, 3.0, orc.ACT_RELU2) == 12.0
+    # sigma(40) rounds to 1 in fp64 -> product is g*u exactly
+    assert orc.swiglu_gate_product(40.0, 0.5) == 20.0
+    g = 0.75
+    assert orc.swiglu_gate_product(g, 2.0) == (g * (1.0 / (1.0 + math.exp(-g)))) * 2.0
+
+
+def test_inner_norm_closed_form(orc):
+    # constant row c: scale = 1/sqrt(c^2 + eps); unit weights
+    n, c, eps = 6912, 0.25, 1e-5
+    h = orc.bitnet_rmsnorm_row(np.full(n, c, np.float32), None, eps)
+    want = np.float32(np.float64(c) * (1.0 / math.sqrt(c * c + eps)))
+    assert np.all(h == want)
+    # weights multiply after the scale: w=2 doubles (exactly, power of two)
+    h2 = orc.bitnet_rmsnorm_row(np.full(n, c, np.float32), np.full(n, 2.0, np.float32), eps)
+    assert np.all(h2 == np.float32(2 * np.float64(want)))
+    # eps <= 0 defaults to 1e-5
+    h3 = orc.bitnet_rmsnorm_row(np.full(8, c, np.float32), None, 0.0)
+    assert np.all(h3 == want)
+
+
+def test_rmsnorm_layer_closed_form(orc):
+    x = np.full((2, 8), 3.0, np.float32)
+    y = orc.rmsnorm_forward(x, np.ones(8, np.float32), eps=1e-6)
+    assert np.all(y == np.float32(3.0 / math.sqrt(9.0 + 1e-6)))
+
+
+def test_swiglu_stages_compose(orc):
+    # the SwiGLU oracle is exactly: quant -> gate/up matvec -> gate product ->
+    # inner norm -> quant -> down matvec, each stage checked against the
+    # stand-alone oracle pieces pinned above.
+    H, I = 64, 96
+    g = orc.random_matrix(I, H, 11)
+    u = orc.random_matrix(I, H, 12)
+    d = orc.random_matrix(H, I, 13)
+    x = orc.normal_f32(3 * H, 14).reshape(3, H)
+    nw = orc.uniform_f32(I, 0.5, 1.5, 15)
+    r = orc.swiglu_forward(g, u, d, x, inner_norm=nw, eps=1e-5)
+    for s in range(3):
+        xq, amax = orc.quant_act(x[s])
+        assert np.array_equal(xq, r.xq[s]) and amax == r.amax[s]
+        gv, ga = orc.matvec_scalar(g, xq, orc.output_scale(g.scale, amax))
+        uv, ua = orc.matvec_scalar(u, xq, orc.output_scale(u.scale, amax))
+        assert np.array_equal(ga, r.acc_gate[s]) and np.array_equal(ua, r.acc_up[s])
+        h = np.array([orc.swiglu_gate_product(a, b) for a, b in zip(gv, uv)], np.float32)
+        h = orc.bitnet_rmsnorm_row(h, nw, 1e-5)
+        assert np.array_equal(h.view(np.uint32), r.h[s].view(np.uint32))
+        hq, hamax = orc.quant_act(h)
+        assert np.array_equal(hq, r.hq[s])
+        dv, da = orc.matvec_scalar(d, hq, orc.output_scale(d.scale, hamax))
+        assert np.array_equal(da, r.acc_down[s])
+        assert np.array_equal(dv.astype(np.float32).view(np.uint32), r.out[s].view(np.uint32))
+
+
+# ---------------------------------------------------------------- entity blob
+def test_entity_blob_round_trip(orc):
+    # TestEntityBitNetTernaryBlobRoundTrip (poly/tests/entity_test.go:331-348)
+    words = np.array([0x49249249, 0x92492492, 0x24924924, 0x49249249, 0x92492492,
+                      0x24924924, 0x49249249, 0x92492492], np.uint32)
+    raw = orc.entity_encode(8, 4, 0, 0.05, 1, words)
+    assert len(raw) == 24 + 32
+    m, off = orc.entity_decode(raw)
+    assert (m.rows, m.cols, off, m.row_words) == (8, 4, 0, 1)
+    assert m.scale == np.float32(0.05)
+    assert np.array_equal(m.words, words)
+    # header layout: little endian u32 fields, scale as fp32 bits
+    assert raw[:4] == (8).to_bytes(4, "little")
+    assert raw[12:16] == np.float32(0.05).tobytes()
+    with pytest.raises(ValueError):
+        orc.entity_decode(raw[:20])
+    with pytest.raises(ValueError):
+        orc.entity_decode(raw[:40])
+
+
+def test_entity_large_offset(orc):
+    # TestEntityBitNetCollectLargeOffsetKeys (:352-412): offsets beyond 20000 survive
+    raw = orc.entity_encode(4, 8, 6553600, 2.0, 1, np.array([9, 10, 11, 12], np.uint32))
+    m, off = orc.entity_decode(raw)
+    assert off == 6553600 and m.scale == 2.0
