@@ -1,0 +1,104 @@
+"""ctypes binding of libloom_accel_amd.so (the C-ABI of include/loom_accel.h and
+include/loom_accel_amd.h).
+
+The shared library is built in-tree by loom_amd.build (hipcc, gfx950).  There is
+no fallback: if the library is missing, every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+from . import build as _build
+
+LIB_PATH = _build.LIB_PATH
+
+_lib: C.CDLL | None = None
+
+P = C.c_void_p
+i32 = C.c_int
+f32 = C.c_float
+f64 = C.c_double
+sz = C.c_size_t
+cstr = C.c_char_p
+
+
+class LibraryMissing(RuntimeError):
+    pass
+
+
+class LayerDesc(C.Structure):
+    """loom_accel_layer_desc (poly/accel/include/loom_accel.h:16-20)."""
+    _fields_ = [("layer_name", cstr), ("dtype", cstr), ("size_label", cstr)]
+
+
+class DenseTaps(C.Structure):
+    _fields_ = [("xq", P), ("amax", P), ("acc", P)]
+
+
+class SwiGLUTaps(C.Structure):
+    _fields_ = [("xq", P), ("amax", P), ("acc_gate", P), ("acc_up", P), ("hq", P),
+                ("hamax", P), ("acc_down", P)]
+
+
+# name -> (restype, argtypes); every symbol declared in include/*.h.
+SIGNATURES = {
+    # loom_accel.h (v2 plugin ABI)
+    "loom_accel_api_version": (i32, []),
+    "loom_accel_vendor_id": (cstr, []),
+    "loom_accel_npu_available": (i32, []),
+    "loom_accel_plugin_open": (P, [cstr]),
+    "loom_accel_plugin_close": (None, [P]),
+    "loom_accel_weight_bytes": (sz, [C.POINTER(LayerDesc)]),
+    "loom_accel_compile_layer": (i32, [P, C.POINTER(LayerDesc), P, sz, C.POINTER(P),
+                                       C.POINTER(f64), C.c_char_p, sz]),
+    "loom_accel_release_layer": (None, [P]),
+    "loom_accel_layer_io_bytes": (i32, [P, C.POINTER(sz), C.POINTER(sz), C.c_char_p, sz]),
+    "loom_accel_first_infer": (i32, [P, C.POINTER(f64), C.c_char_p, sz]),
+    "loom_accel_infer": (i32, [P, P, sz, P, sz, C.POINTER(f64), C.c_char_p, sz]),
+    "loom_accel_last_error": (cstr, [P]),
+    # loom_accel_amd.h (device-resident extension)
+    "loom_amd_last_error": (cstr, []),
+    "loom_amd_device_count": (i32, []),
+    "loom_amd_kernel_variant": (cstr, [i32]),
+    "loom_amd_matrix_create": (i32, [i32, P, sz, i32, i32, i32, f32, C.POINTER(P)]),
+    "loom_amd_matrix_from_entity_blob": (i32, [i32, P, sz, C.POINTER(P), C.POINTER(sz)]),
+    "loom_amd_matrix_release": (None, [P]),
+    "loom_amd_matrix_shape": (i32, [P, C.POINTER(i32), C.POINTER(i32), C.POINTER(f32),
+                                    C.POINTER(sz)]),
+    "loom_amd_matrix_tiles": (P, [P]),
+    "loom_amd_quantize_rows": (i32, [P, i32, i32, P, i32, P, P, P]),
+    "loom_amd_quantize_rows_f64": (i32, [P, i32, i32, P, i32, P, P, P]),
+    "loom_amd_ternary_matmul": (i32, [P, P, i32, P, P, i32, P, P, P]),
+    "loom_amd_norm_quant_rows": (i32, [P, i32, i32, P, f64, i32, P, i32, P, P, P]),
+    "loom_amd_dense_forward": (i32, [P, P, i32, i32, P, P, P, C.POINTER(DenseTaps), P]),
+    "loom_amd_swiglu_forward": (i32, [P, P, P, P, P, f64, i32, i32, P, i32, P, P, P,
+                                      C.POINTER(SwiGLUTaps), P]),
+}
+
+
+def lib() -> C.CDLL:
+    """Load the in-tree library (raises LibraryMissing if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise LibraryMissing(
+                f"{LIB_PATH} is missing: build it with `python -m loom_amd.build` "
+                "(hipcc, gfx950); loom_amd has no CPU fallback")
+        handle = C.CDLL(LIB_PATH, mode=os.RTLD_NOW | os.RTLD_LOCAL)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+class AMDError(RuntimeError):
+    pass
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != 0:
+        msg = lib().loom_amd_last_error().decode(errors="replace")
+        raise AMDError(f"{what}: {msg}" if what else msg)

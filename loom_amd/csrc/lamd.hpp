@@ -1,0 +1,101 @@
+// lamd.hpp -- internal declarations of libloom_accel_amd.so (gfx950 only).
+//
+// Weight layout in HBM ("tile layout"), built once per matrix by repack_tiles:
+//   * the matrix (rows = N outputs, cols = K inputs) is cut into tiles of
+//     16 rows x 256 columns; rows pad to Np = 16*ceil(N/16), columns to
+//     Kp = 256*ceil(K/256);
+//   * tiles are stored row-tile major: tile (nt, kt) starts at word
+//     (nt*ktiles + kt) * 256 and holds 64 lanes x 4 words (1 KiB), so one
+//     wavefront reads a tile with one fully coalesced 128-bit load per lane;
+//   * lane l of a tile owns weight row 16*nt + (l & 15) and columns
+//     256*kt + 64*(l >> 4) + 16*t + c for word t (0..3), c (0..15);
+//   * inside a word, the 2-bit code of column c = 4*d + j sits at bit
+//     8*j + 2*d, so (word >> 2*d) & 0x03030303 is four int8 codes for the
+//     K-contiguous columns 4d..4d+3 -- one shift and one AND per dword, and
+//     the four dwords of a word are exactly one MFMA 16x16x64 i8 operand.
+//   Codes keep loom's meaning (0 -> -1, 1 -> 0, 2 -> +1, poly/bitnet_cpu.go:
+//   498-507); the kernels multiply the raw codes and subtract sum(xq) per
+//   token row, the identity loom's amd64 path uses (poly/bitnet_cpu.go:733-750).
+//   Padding columns carry code 0 and meet zero activations.
+//
+// Activations: int8 rows of Kp bytes (zero padded), one fp32 amax and one
+// int32 sum(xq) per row.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+
+namespace lamd {
+
+constexpr int kTileRows = 16;
+constexpr int kTileCols = 256;
+constexpr int kTileWords = 256;  // 64 lanes x 4 u32
+
+inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+inline int pad_cols(int k) { return ceil_div(k, kTileCols) * kTileCols; }
+
+// Device-resident repacked ternary matrix.
+struct Matrix {
+    int rows = 0;      // N (outputs)
+    int cols = 0;      // K (inputs)
+    int ntiles = 0;    // ceil(N/16)
+    int ktiles = 0;    // ceil(K/256)
+    float scale = 1.0f;
+    uint32_t* tiles = nullptr;  // ntiles*ktiles*256 words (device)
+    int device = 0;
+    size_t bytes() const { return (size_t)ntiles * ktiles * kTileWords * 4; }
+};
+
+// Quantized activations for one matmul call (device pointers).
+struct QuantAct {
+    const int8_t* xq;    // rows x ldq
+    int ldq;             // row stride in bytes (multiple of 256, >= Kp)
+    const float* amax;   // per row
+    const int32_t* xsum; // per row
+};
+
+// Epilogue selector of the matmul kernels.
+enum EpiKind : int {
+    EPI_DENSE = 0,   // pre = fp32(fp64(acc)*os) [+bias]; post = Activate(pre); [+residual]
+    EPI_SWIGLU = 1,  // h = fp32(gateprod(fp64(acc_g)*os_g + bg, fp64(acc_u)*os_u + bu))
+};
+
+struct Epilogue {
+    int kind = EPI_DENSE;
+    int activation = -1;       // loom ActivationType
+    const float* bias0 = nullptr;  // dense bias or gate bias (length N)
+    const float* bias1 = nullptr;  // up bias (length N)
+    const float* residual = nullptr;  // M x N, added in fp32 after the cast
+    float* out = nullptr;      // M x ldo (pre-activation / h)
+    float* post = nullptr;     // M x ldo (post-activation), optional
+    int ldo = 0;
+    int32_t* acc0 = nullptr;   // M x N debug tap (acc of matrix 0), optional
+    int32_t* acc1 = nullptr;   // M x N debug tap (acc of matrix 1), optional
+};
+
+// ---- launchers (ternary_kernels.hip) ----
+hipError_t launch_repack(const uint32_t* words, int rows, int cols, int row_words,
+                         Matrix* m, hipStream_t s);
+hipError_t launch_act_quant(const float* x, int ldx, int m, int k, int8_t* xq, int ldq,
+                            float* amax, int32_t* xsum, hipStream_t s);
+hipError_t launch_act_quant_f64(const double* x, int ldx, int m, int k, int8_t* xq,
+                                int ldq, float* amax, int32_t* xsum, hipStream_t s);
+// One (NMAT=1) or two (NMAT=2, same shape, EPI_SWIGLU) matrices against the
+// same quantized activations.  M is the number of token rows.
+hipError_t launch_matmul(const Matrix* w0, const Matrix* w1, const QuantAct& a, int m,
+                         const Epilogue& epi, hipStream_t s);
+// Inner RMSNorm + requantization of SwiGLU rows (poly/bitnet_cpu.go:893-913 then
+// poly/bitnet_cpu.go:97-106).  In place on h (M x n fp32, row stride ldh).
+hipError_t launch_norm_quant(float* h, int ldh, int m, int n, const float* weight, double eps,
+                             int strict, int8_t* hq, int ldq, float* amax, int32_t* xsum,
+                             hipStream_t s);
+
+// Per-device scratch arena for the device-resident entry points.
+void* scratch(int device, size_t bytes, std::string* err);
+
+const char* kernel_variant(int m);  // name of the matmul path chosen for M rows
+
+}  // namespace lamd

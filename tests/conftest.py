@@ -17,3 +17,12 @@ def orc():
     from oracle import oracle as o
     o.lib()
     return o
+
+
+@pytest.fixture(scope="session")
+def amd_lib():
+    """The in-tree libloom_accel_amd.so; built here only if nothing is built."""
+    from loom_amd import _lib, build
+    if not os.path.exists(_lib.LIB_PATH):
+        build.build()
+    return _lib.lib()

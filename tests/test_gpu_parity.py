@@ -1,0 +1,386 @@
+"""Parity of the gfx950 HIP path against the CPU oracle (loom's CPU path restated).
+
+Bar (stated per test):
+  * int8 activations, per-row amax, int32 accumulators: bit-exact;
+  * fp32 Dense outputs: bit-exact -- the rescale is loom's fp64 multiply in its
+    operation order, then one fp64 -> fp32 rounding;
+  * SwiGLU: every integer stage bit-exact; the gate product uses exp(), whose
+    last fp64 bit differs between libraries (Go math.Exp, glibc, ROCm ocml), so
+    the normalized rows h are compared within 1 fp32 ulp and the stages after
+    h are checked bit-exact against the oracle fed the GPU's own h.
+Citations are relative to the loom v0.83.0 tree.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+# loom's parity shapes rows x cols (poly/tests/bitnet_packed_test.go:19-21,
+# poly/tests/bitnet_cpu_test.go:217) plus the BitNet-2B FFN shapes.
+LOOM_SHAPES = [(40, 70), (8, 64), (33, 65), (16, 128), (64, 2560), (128, 6912), (7, 191), (3, 17)]
+M_EDGES = [1, 2, 4, 5, 15, 16, 17, 31, 32, 33, 63, 64, 65, 127, 128, 129, 200]
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a visible MI355X"
+    from loom_amd import _lib
+    assert _lib.lib().loom_amd_device_count() >= 1, "no gfx950 device visible to the library"
+    return torch
+
+
+@pytest.fixture(scope="module")
+def bn(torch_dev):
+    from loom_amd import bitnet
+    return bitnet
+
+
+def to_dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def gpu_matrix(bn, m):
+    return bn.TernaryMatrix.from_words(m.words, m.rows, m.cols, m.scale)
+
+
+def ulp_diff_f32(a, b):
+    a = np.ascontiguousarray(a, np.float32).view(np.int32).astype(np.int64)
+    b = np.ascontiguousarray(b, np.float32).view(np.int32).astype(np.int64)
+    a = np.where(a < 0, np.int64(-2**31) - a, a)
+    b = np.where(b < 0, np.int64(-2**31) - b, b)
+    return np.abs(a - b)
+
+
+# ---------------------------------------------------------------- quantization
+def test_quantize_rows_bit_exact(orc, torch_dev, bn):
+    torch = torch_dev
+    k = 2560
+    rows = [orc.normal_f32(k, 100 + i) for i in range(6)]
+    rows.append(np.zeros(k, np.float32))                       # amax floor 1e-5
+    rows.append(np.full(k, 3e-6, np.float32))                  # below the floor
+    spike = orc.normal_f32(k, 7) * np.float32(1e-3)
+    spike[17] = np.float32(-50.0)
+    rows.append(spike)
+    nan_row = orc.normal_f32(k, 8)
+    nan_row[5] = np.nan                                        # NaN -> -128, ignored by amax
+    rows.append(nan_row)
+    inf_row = orc.normal_f32(k, 9)
+    inf_row[3] = np.inf                                        # amax = inf, scale 0
+    rows.append(inf_row)
+    half = np.arange(k, dtype=np.float32) - np.float32(k / 2)  # exact .5 ties
+    rows.append(half)
+    x = np.stack(rows)
+    q = bn.quantize_activation(to_dev(torch, x))
+    torch.cuda.synchronize()
+    xq = q.unpadded().cpu().numpy()
+    for i, r in enumerate(rows):
+        eq, eamax = orc.quant_act(r)
+        assert np.array_equal(xq[i], eq), f"row {i}"
+        assert np.float32(q.amax[i].item()).tobytes() == np.float32(eamax).tobytes(), f"row {i}"
+        assert int(q.xsum[i].item()) == int(eq.astype(np.int64).sum()), f"row {i}"
+    assert not q.xq[:, k:].any().item() if q.xq.shape[1] > k else True
+
+
+def test_quantize_rows_f64_bit_exact(orc, torch_dev, bn):
+    torch = torch_dev
+    k = 640
+    x = np.stack([orc.normal_f32(k, 300 + i).astype(np.float64) * 1.000000001 for i in range(5)])
+    q = bn.quantize_activation(to_dev(torch, x))
+    torch.cuda.synchronize()
+    for i in range(x.shape[0]):
+        eq, eamax = orc.quant_act(x[i])
+        assert np.array_equal(q.unpadded()[i].cpu().numpy(), eq)
+        assert np.float32(q.amax[i].item()) == np.float32(eamax)
+
+
+# ---------------------------------------------------------------- matvec KATs
+def _manual_rows(torch, bn, xq_rows, amax):
+    xq_rows = np.atleast_2d(np.asarray(xq_rows, np.int8))
+    m, k = xq_rows.shape
+    pad = np.zeros((m, bn.padded_cols(k)), np.int8)
+    pad[:, :k] = xq_rows
+    return bn.QuantizedRows(to_dev(torch, pad), to_dev(torch, np.asarray(amax, np.float32)),
+                            to_dev(torch, xq_rows.astype(np.int32).sum(axis=1).astype(np.int32)), k)
+
+
+def test_microsoft_offline_kat(orc, torch_dev, bn):
+    # TestMicrosoftOfflinePackedBitNetRowsDecode (poly/tests/bitnet_cpu_test.go:334-362):
+    # 8x2, Scale 0.5, xq {2,-3}, amax 127 -> {1.5,-2.5,-2.5,-2.5,1,1.5,2.5,2.5}
+    torch = torch_dev
+    packed = np.array([0b10100001, 0b00011000, 0b10010000, 0b00001010], np.float32)
+    m = orc.pack_ms_offline_float_slots(packed, 8, 2, scale=0.5)
+    w = gpu_matrix(bn, m)
+    out, acc = bn.ternary_matvec_quantized(w, _manual_rows(torch, bn, [2, -3], [127.0]), want_acc=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy()[0],
+                          np.array([1.5, -2.5, -2.5, -2.5, 1, 1.5, 2.5, 2.5], np.float32))
+    assert np.array_equal(acc.cpu().numpy()[0], [3, -5, -5, -5, 2, 3, 5, 5])
+
+
+def test_tail_columns_brute_force(orc, torch_dev, bn):
+    # Tail-column closed form (poly/tests/bitnet_cpu_test.go:216-247): 3x17.
+    torch = torch_dev
+    rows, cols = 3, 17
+    master = orc.deterministic_weights(rows * cols)
+    m = orc.pack_float32(master, rows, cols)
+    x = orc.deterministic_weights(cols + 5)[5:]
+    xq, amax = orc.quant_act(x)
+    w = gpu_matrix(bn, m)
+    out, acc = bn.ternary_matvec_quantized(w, _manual_rows(torch, bn, xq, [amax]), want_acc=True)
+    torch.cuda.synchronize()
+    codes = np.array([[orc.quant_value(v, m.scale) for v in master[r * cols:(r + 1) * cols]]
+                      for r in range(rows)], np.int64)
+    brute = codes @ xq.astype(np.int64)
+    assert np.array_equal(acc.cpu().numpy()[0], brute)
+    os_ = orc.output_scale(m.scale, amax)
+    assert np.array_equal(out.cpu().numpy()[0], (brute.astype(np.float64) * os_).astype(np.float32))
+
+
+# ---------------------------------------------------------------- dense
+def _check_dense(orc, torch, bn, m, x, activation=-1, residual=None):
+    w = gpu_matrix(bn, m)
+    pre, post, taps = bn.dense_forward_packed_ternary(
+        w, to_dev(torch, x), activation=activation,
+        residual=None if residual is None else to_dev(torch, residual), taps=True)
+    torch.cuda.synchronize()
+    ref = orc.dense_forward(m, x, activation=activation, simd=True)
+    M = x.shape[0]
+    assert np.array_equal(taps.xq.cpu().numpy(), ref.xq), "int8 activations"
+    assert taps.amax.cpu().numpy().tobytes() == ref.amax.tobytes(), "amax"
+    acc = taps.acc.cpu().numpy()
+    assert np.array_equal(acc, ref.acc), f"int32 accumulators ({np.count_nonzero(acc != ref.acc)} differ of {acc.size})"
+    want_pre = ref.pre if residual is None else (ref.pre + residual).astype(np.float32)
+    assert pre.cpu().numpy().tobytes() == want_pre.tobytes(), "fp32 pre-activation (bit-exact)"
+    if activation != -1:
+        if residual is None:
+            got = post.cpu().numpy()
+            if activation in (0, 6):
+                assert got.tobytes() == ref.post.tobytes()
+            else:  # exp/tanh last-bit freedom: <= 1 ulp
+                assert ulp_diff_f32(got, ref.post).max() <= 1
+    return M
+
+
+@pytest.mark.parametrize("rows,cols", LOOM_SHAPES)
+def test_dense_loom_shapes_bit_exact(orc, torch_dev, bn, rows, cols):
+    m = orc.random_matrix(rows, cols, seed=rows * 1000 + cols)
+    for M in (1, 7, 64, 130):
+        x = orc.normal_f32(M * cols, seed=M + rows).reshape(M, cols)
+        _check_dense(orc, torch_dev, bn, m, x)
+
+
+def test_dense_deterministic_weights(orc, torch_dev, bn):
+    # deterministicWeights inputs (poly/tests/bitnet_cpu_test.go:10-20), 512x512
+    # as BenchmarkPackedTernaryDenseForward, several batch sizes.
+    rows = cols = 512
+    m = orc.pack_float32(orc.deterministic_weights(rows * cols), rows, cols)
+    for M in (1, 3, 96):
+        x = orc.deterministic_weights(M * cols + 11)[11:].reshape(M, cols)
+        _check_dense(orc, torch_dev, bn, m, x)
+
+
+@pytest.mark.parametrize("M", M_EDGES)
+def test_dense_batch_edges(orc, torch_dev, bn, M):
+    # every kernel variant boundary (skinny 16/32/64, gemm) on a ragged shape
+    m = orc.random_matrix(200, 300, seed=77)
+    x = orc.normal_f32(M * 300, seed=M).reshape(M, 300)
+    _check_dense(orc, torch_dev, bn, m, x)
+
+
+@pytest.mark.parametrize("act", [0, 1, 6])
+def test_dense_activation_and_residual(orc, torch_dev, bn, act):
+    m = orc.random_matrix(96, 160, seed=5)
+    x = orc.normal_f32(9 * 160, seed=6).reshape(9, 160)
+    _check_dense(orc, torch_dev, bn, m, x, activation=act)
+    res = orc.normal_f32(9 * 96, seed=8).reshape(9, 96)
+    _check_dense(orc, torch_dev, bn, m, x, residual=res)
+
+
+def test_config0_gemv_bit_exact(orc, torch_dev, bn):
+    # M=1, K=2560, N=6912.
+    m = orc.random_matrix(6912, 2560, seed=0xC0)
+    x = orc.normal_f32(2560, seed=0xC1).reshape(1, 2560)
+    _check_dense(orc, torch_dev, bn, m, x)
+
+
+@pytest.mark.parametrize("shape", [(6912, 2560), (2560, 6912)], ids=["up_gate", "down"])
+@pytest.mark.parametrize("M", [1, 8, 64, 512, 4096])
+def test_config1_sweep_bit_exact(orc, torch_dev, bn, shape, M):
+    # M in {1,8,64,512,4096} on both FFN shapes, int32 bit-exact.
+    n, k = shape
+    m = orc.random_matrix(n, k, seed=n + k)
+    x = orc.normal_f32(M * k, seed=M * 31 + k).reshape(M, k)
+    _check_dense(orc, torch_dev, bn, m, x)
+
+
+# ---------------------------------------------------------------- norm + requant
+@pytest.mark.parametrize("n", [160, 2560, 6912])
+def test_norm_quant_strict_bit_exact(orc, torch_dev, bn, n):
+    torch = torch_dev
+    M = 5
+    h = orc.normal_f32(M * n, seed=n).reshape(M, n) * np.float32(3.0)
+    wt = orc.uniform_f32(n, 0.5, 1.5, seed=n + 1)
+    for weight in (None, wt):
+        hd = to_dev(torch, h.copy())
+        q = bn.norm_quant_rows(hd, None if weight is None else to_dev(torch, weight), eps=1e-5,
+                               norm="strict")
+        torch.cuda.synchronize()
+        got = hd.cpu().numpy()
+        for i in range(M):
+            want = orc.bitnet_rmsnorm_row(h[i], weight, 1e-5)
+            assert got[i].tobytes() == want.tobytes(), f"row {i} normalized values"
+            eq, eamax = orc.quant_act(want)
+            assert np.array_equal(q.unpadded()[i].cpu().numpy(), eq)
+            assert np.float32(q.amax[i].item()) == np.float32(eamax)
+
+
+def test_norm_quant_fast_within_one_ulp(orc, torch_dev, bn):
+    torch = torch_dev
+    n, M = 6912, 16
+    h = orc.normal_f32(M * n, seed=99).reshape(M, n)
+    hd = to_dev(torch, h.copy())
+    q = bn.norm_quant_rows(hd, None, eps=1e-5, norm="fast")
+    torch.cuda.synchronize()
+    got = hd.cpu().numpy()
+    want = np.stack([orc.bitnet_rmsnorm_row(h[i], None, 1e-5) for i in range(M)])
+    assert ulp_diff_f32(got, want).max() <= 1
+    # requantization of the GPU's own rows is bit-exact
+    for i in range(M):
+        eq, _ = orc.quant_act(got[i])
+        assert np.array_equal(q.unpadded()[i].cpu().numpy(), eq)
+
+
+# ---------------------------------------------------------------- SwiGLU
+def _swiglu_case(orc, torch, bn, hidden, inter, M, seed, norm, with_norm_w, act=1):
+    g = orc.random_matrix(inter, hidden, seed=seed)
+    u = orc.random_matrix(inter, hidden, seed=seed + 1)
+    d = orc.random_matrix(hidden, inter, seed=seed + 2)
+    wn = orc.uniform_f32(inter, 0.5, 1.5, seed=seed + 3) if with_norm_w else None
+    x = orc.normal_f32(M * hidden, seed=seed + 4).reshape(M, hidden)
+    G, U, D = gpu_matrix(bn, g), gpu_matrix(bn, u), gpu_matrix(bn, d)
+    h, out, t = bn.swiglu_forward_packed_ternary(
+        G, U, D, to_dev(torch, x), inner_norm=None if wn is None else to_dev(torch, wn),
+        eps=1e-5, activation=act, norm=norm, taps=True)
+    torch.cuda.synchronize()
+    ref = orc.swiglu_forward(g, u, d, x, inner_norm=wn, eps=1e-5, activation=act, simd=True)
+    # integer stages before the gate: bit-exact
+    assert np.array_equal(t.xq.cpu().numpy(), ref.xq)
+    assert t.amax.cpu().numpy().tobytes() == ref.amax.tobytes()
+    assert np.array_equal(t.acc_gate.cpu().numpy(), ref.acc_gate)
+    assert np.array_equal(t.acc_up.cpu().numpy(), ref.acc_up)
+    # normalized gate product: <= 1 fp32 ulp (exp last bit; fast-mode sum order)
+    hg = h.cpu().numpy()
+    assert ulp_diff_f32(hg, ref.h).max() <= 1
+    # stages after h, against the oracle fed the GPU's own h: bit-exact
+    hq_ref, hamax_ref = orc.quant_act_rows(hg)
+    assert np.array_equal(t.hq.cpu().numpy(), hq_ref)
+    assert t.hamax.cpu().numpy().tobytes() == hamax_ref.tobytes()
+    acc_down_ref = np.stack([orc.matvec_scalar(d, hq_ref[i], orc.output_scale(d.scale, hamax_ref[i]))[1]
+                             for i in range(M)])
+    assert np.array_equal(t.acc_down.cpu().numpy(), acc_down_ref)
+    out_ref = np.stack([(acc_down_ref[i].astype(np.float64) * orc.output_scale(d.scale, hamax_ref[i]))
+                        .astype(np.float32) for i in range(M)])
+    assert out.cpu().numpy().tobytes() == out_ref.tobytes()
+    return hg, ref
+
+
+@pytest.mark.parametrize("norm", ["strict", "fast"])
+@pytest.mark.parametrize("M", [1, 5, 64, 100])
+def test_swiglu_small(orc, torch_dev, bn, norm, M):
+    _swiglu_case(orc, torch_dev, bn, hidden=64, inter=160, M=M, seed=11 + M, norm=norm,
+                 with_norm_w=True)
+
+
+@pytest.mark.parametrize("act", [1, 6])
+def test_swiglu_relu2_and_silu(orc, torch_dev, bn, act):
+    _swiglu_case(orc, torch_dev, bn, hidden=128, inter=320, M=3, seed=21, norm="strict",
+                 with_norm_w=False, act=act)
+
+
+@pytest.mark.parametrize("M", [1, 64, 256])
+def test_swiglu_bitnet_2b_shape(orc, torch_dev, bn, M):
+    hg, ref = _swiglu_case(orc, torch_dev, bn, hidden=2560, inter=6912, M=M, seed=1234 + M,
+                           norm="strict", with_norm_w=True)
+    # with strict summation the only freedom is exp's last fp64 bit, which
+    # essentially never survives the fp32 cast: report how many h differ
+    assert np.count_nonzero(hg != ref.h) <= max(1, hg.size // 100000)
+
+
+# ---------------------------------------------------------------- plugin ABI on the GPU
+def test_plugin_bitnet_linear(orc, torch_dev):
+    from loom_amd import accel
+    m = orc.random_matrix(384, 512, seed=3)
+    M = 4
+    x = orc.normal_f32(M * 512, seed=4).reshape(M, 512)
+    p = accel.open_amd(device="GPU")
+    try:
+        assert p.vendor_id() == "amd"
+        desc = accel.LayerDesc("BitNetLinear", "TERNARY", f"m={M},k=512,n=384")
+        blob = m.entity_blob()
+        assert p.weight_bytes(desc) == len(blob)
+        res = p.compile_layer(desc, blob)
+        assert (res.in_bytes, res.out_bytes) == (M * 512 * 4, M * 384 * 4)
+        out = bytearray(res.out_bytes)
+        r = res.layer.infer(x.tobytes(), out)
+        assert r.infer_ms >= 0
+        ref = orc.dense_forward(m, x, simd=True)
+        assert bytes(out) == ref.pre.tobytes()
+        with pytest.raises(accel.AccelError, match="input byte size mismatch|buffer size mismatch"):
+            res.layer.infer(x[:1].tobytes(), out)
+        res.layer.release()
+    finally:
+        p.close()
+
+
+def test_plugin_bitnet_swiglu(orc, torch_dev):
+    from loom_amd import accel
+    hidden, inter, M = 128, 320, 3
+    g = orc.random_matrix(inter, hidden, seed=31)
+    u = orc.random_matrix(inter, hidden, seed=32)
+    d = orc.random_matrix(hidden, inter, seed=33)
+    wn = orc.uniform_f32(inter, 0.5, 1.5, seed=34)
+    x = orc.normal_f32(M * hidden, seed=35).reshape(M, hidden)
+    p = accel.open_amd(device="GPU")
+    try:
+        desc = accel.LayerDesc("BitNetSwiGLU", "TERNARY", f"m={M},k={hidden},n={inter},eps=1e-5")
+        blob = g.entity_blob() + u.entity_blob() + d.entity_blob() + wn.tobytes()
+        assert p.weight_bytes(desc) == len(blob)
+        res = p.compile_layer(desc, blob)
+        out = bytearray(res.out_bytes)
+        res.layer.infer(x.tobytes(), out)
+        ref = orc.swiglu_forward(g, u, d, x, inner_norm=wn, eps=1e-5, simd=True)
+        got = np.frombuffer(bytes(out), np.float32).reshape(M, hidden)
+        assert ulp_diff_f32(got, ref.out).max() <= 1 or np.array_equal(got, ref.out)
+        res.layer.release()
+    finally:
+        p.close()
+
+
+def test_entity_blob_upload_matches_words(orc, torch_dev, bn):
+    torch = torch_dev
+    m = orc.random_matrix(48, 300, seed=41)
+    a = bn.TernaryMatrix.from_entity_blob(m.entity_blob(offset=10000))
+    b = gpu_matrix(bn, m)
+    assert (a.rows, a.cols, a.scale) == (b.rows, b.cols, b.scale)
+    q = bn.quantize_activation(to_dev(torch, orc.normal_f32(300, 1).reshape(1, 300)))
+    oa = bn.ternary_matvec_quantized(a, q)
+    ob = bn.ternary_matvec_quantized(b, q)
+    torch.cuda.synchronize()
+    assert torch.equal(oa, ob)
+
+
+def test_library_errors_are_loud(orc, torch_dev, bn):
+    from loom_amd import _lib
+    torch = torch_dev
+    m = orc.random_matrix(16, 32, seed=1)
+    w = gpu_matrix(bn, m)
+    with pytest.raises(ValueError):
+        bn.dense_forward_packed_ternary(w, torch.zeros((2, 31), device="cuda"))
+    with pytest.raises(_lib.AMDError, match="word count"):
+        bn.TernaryMatrix.from_words(m.words[:3], 16, 32, 1.0)
+    with pytest.raises(_lib.AMDError, match="truncated"):
+        bn.TernaryMatrix.from_entity_blob(m.entity_blob()[:-4])
+    assert _lib.lib().loom_amd_ternary_matmul(None, None, 256, None, None, 1, None, None, None) == -1
