@@ -54,22 +54,46 @@ def cpu_cores() -> int:
 
 
 class Timer:
-    """HIP-event timing of a callable on torch's current stream (the stream every
-    loom_amd launch uses)."""
+    """HIP-event timing on the stream every loom_amd launch uses (torch's current
+    stream).  Steps are captured into a HIP graph of `per_graph` consecutive
+    calls and the graph is replayed, so the measurement is the device's
+    back-to-back throughput, not the Python launch rate."""
 
     def __init__(self, torch):
         self.torch = torch
 
-    def run(self, fn, steps: int, warmup: int) -> float:
+    def _capture(self, fn, first: int, count: int):
+        graph = self.torch.cuda.CUDAGraph()
+        with self.torch.cuda.graph(graph):
+            for i in range(first, first + count):
+                fn(i)
+        return graph
+
+    def run(self, fn, steps: int, warmup: int, per_graph: int = 64) -> float:
+        """Mean ms per call over exactly `steps` calls (after `warmup` calls)."""
         torch = self.torch
-        for i in range(warmup):
-            fn(i)
+        per_graph = max(1, min(per_graph, steps))
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for i in range(max(1, warmup)):
+                fn(i)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        full, rest = divmod(steps, per_graph)
+        graph = self._capture(fn, 0, per_graph) if full else None
+        tail = self._capture(fn, full * per_graph, rest) if rest else None
+        for g in (graph, tail):
+            if g is not None:
+                g.replay()  # untimed: first replay uploads the graph
         torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         start.record()
-        for i in range(steps):
-            fn(i)
+        for _ in range(full):
+            graph.replay()
+        if tail is not None:
+            tail.replay()
         end.record()
         torch.cuda.synchronize()
         return start.elapsed_time(end) / steps  # ms per call
@@ -126,7 +150,7 @@ def main() -> int:
     def step_dense(i):
         bn.dense_forward_packed_ternary(ups[i % rot], x1, out=out1)
 
-    ms_step = timer.run(step_dense, args.steps, args.warmup)
+    ms_step = timer.run(step_dense, args.steps, args.warmup, per_graph=rot)
     b1 = gemv_bytes(1, n, k)
     value = b1 / (ms_step * 1e-3) / 1e9
     log(f"dense M=1 up: {ms_step * 1e3:.2f} us/step, {value:.0f} GB/s")
@@ -137,7 +161,7 @@ def main() -> int:
     def step_gemv(i):
         bn.ternary_matvec_quantized(ups[i % rot], q1)
 
-    ms_kernel = timer.run(step_gemv, args.steps, args.warmup)
+    ms_kernel = timer.run(step_gemv, args.steps, args.warmup, per_graph=rot)
     achieved = b1 / (ms_kernel * 1e-3) / 1e9
     log(f"gemv kernel M=1 up: {ms_kernel * 1e3:.2f} us/launch, {achieved:.0f} GB/s")
 
@@ -176,9 +200,9 @@ def main() -> int:
                 steps = max(20, min(args.steps, int(2e5 / M)))
                 nm = len(mats) if M <= 64 else 1
                 t_k = timer.run(lambda i: bn.ternary_matvec_quantized(mats[i % nm], q),
-                                steps, max(5, steps // 10))
+                                steps, max(5, steps // 10), per_graph=min(nm, 64) if nm > 1 else 16)
                 t_d = timer.run(lambda i: bn.dense_forward_packed_ternary(mats[i % nm], x, out=o),
-                                steps, max(5, steps // 10))
+                                steps, max(5, steps // 10), per_graph=min(nm, 64) if nm > 1 else 16)
                 ent = {"shape": shape_name, "M": M, "K": kk, "N": nn,
                        "kernel": _lib.lib().loom_amd_kernel_variant(M).decode(),
                        "us_kernel": round(t_k * 1e3, 3), "us_dense": round(t_d * 1e3, 3)}
@@ -202,7 +226,7 @@ def main() -> int:
             for norm in ("strict", "fast"):
                 steps = max(10, min(500, int(5e4 / M)))
                 t = timer.run(lambda i: bn.swiglu_forward_packed_ternary(g0, u0, d0, x, norm=norm),
-                              steps, max(3, steps // 10))
+                              steps, max(3, steps // 10), per_graph=8)
                 ffn.append({"M": M, "norm": norm, "us": round(t * 1e3, 2),
                             "TOPS": round(3 * 2.0 * M * 2560 * 6912 / (t * 1e-3) / 1e12, 2)})
                 log(f"swiglu {ffn[-1]}")

@@ -44,7 +44,8 @@ const char* loom_amd_last_error(void);
 int loom_amd_device_count(void);
 
 /* Kernel family the matmul dispatcher uses for m token rows
- * ("skinny_m16", "skinny_m32", "skinny_m64", "gemm_128"). */
+ * ("skinny_m16_fusedq" -- quantization fused into the matmul launch when the
+ * fp32 rows allow it --, "skinny_m16", "skinny_m32", "skinny_m64", "gemm"). */
 const char* loom_amd_kernel_variant(int m);
 
 /* ---- weights --------------------------------------------------------- */

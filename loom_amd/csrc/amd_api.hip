@@ -280,8 +280,8 @@ int loom_amd_norm_quant_rows(float* h, int m, int n, const float* weight, double
     if (!h || !hq || !amax || !xsum) return fail("null buffer");
     if (check_ldq(n, ldq)) return -1;
     if (((uintptr_t)hq & 15) != 0) return fail("hq must be 16-byte aligned");
-    if (norm_mode == LOOM_AMD_NORM_STRICT && (size_t)n * 4 > 64 * 1024) {
-        return fail("strict norm supports rows of at most 16384 values");
+    if (n > kMaxNormCols || (norm_mode == LOOM_AMD_NORM_STRICT && n > kMaxStrictNormCols)) {
+        return fail("norm rows are limited to 8192 values (strict: 8064)");
     }
     hipError_t e = launch_norm_quant(h, n, m, n, weight, eps, norm_mode == LOOM_AMD_NORM_STRICT,
                                      hq, ldq, amax, xsum, (hipStream_t)stream);
@@ -297,6 +297,21 @@ int loom_amd_dense_forward(const loom_amd_matrix* w, const float* x, int m, int 
     if (!x || !pre) return fail("null buffer");
     const Matrix& W = w->m;
     DeviceGuard guard(W.device);
+    hipStream_t s = (hipStream_t)stream;
+    Epilogue epi;
+    epi.kind = EPI_DENSE;
+    epi.activation = activation;
+    epi.residual = residual;
+    epi.out = pre;
+    epi.post = post;
+    epi.ldo = W.rows;
+    epi.acc0 = taps ? taps->acc : nullptr;
+    if (fused_quant_ok(m, W.cols, x)) {
+        // decode-sized batches: quantization runs inside the matmul launch
+        hipError_t e = launch_matmul_fused(&W, nullptr, x, m, epi, taps ? taps->xq : nullptr,
+                                           taps ? taps->amax : nullptr, s);
+        return e == hipSuccess ? 0 : fail_hip("dense_forward fused", e);
+    }
     const int ldq = ld_for(W.cols);
     Layout L;
     const size_t o_xq = L.take((size_t)m * ldq);
@@ -308,18 +323,9 @@ int loom_amd_dense_forward(const loom_amd_matrix* w, const float* x, int m, int 
     int8_t* xq = (int8_t*)(base + o_xq);
     float* am = (float*)(base + o_am);
     int32_t* xs = (int32_t*)(base + o_xs);
-    hipStream_t s = (hipStream_t)stream;
     hipError_t e = launch_act_quant(x, W.cols, m, W.cols, xq, ldq, am, xs, s);
     if (e != hipSuccess) return fail_hip("dense_forward quantize", e);
     QuantAct a{xq, ldq, am, xs};
-    Epilogue epi;
-    epi.kind = EPI_DENSE;
-    epi.activation = activation;
-    epi.residual = residual;
-    epi.out = pre;
-    epi.post = post;
-    epi.ldo = W.rows;
-    epi.acc0 = taps ? taps->acc : nullptr;
     e = launch_matmul(&W, nullptr, a, m, epi, s);
     if (e != hipSuccess) return fail_hip("dense_forward matmul", e);
     if (taps && taps->xq) {
@@ -354,8 +360,8 @@ int loom_amd_swiglu_forward(const loom_amd_matrix* gate, const loom_amd_matrix* 
     if (m == 0) return 0;
     if (!x || !out) return fail("null buffer");
     const int strict = norm_mode == LOOM_AMD_NORM_STRICT;
-    if (strict && (size_t)inter * 4 > 64 * 1024) {
-        return fail("strict norm supports rows of at most 16384 values");
+    if (inter > kMaxNormCols || (strict && inter > kMaxStrictNormCols)) {
+        return fail("swiglu intermediate width is limited to 8192 (strict norm: 8064)");
     }
     DeviceGuard guard(G.device);
     const int ldx = ld_for(hidden), ldh = ld_for(inter);
@@ -379,9 +385,6 @@ int loom_amd_swiglu_forward(const loom_amd_matrix* gate, const loom_amd_matrix* 
     int32_t* hs = (int32_t*)(base + o_hs);
     hipStream_t s = (hipStream_t)stream;
 
-    hipError_t e = launch_act_quant(x, hidden, m, hidden, xq, ldx, am, xs, s);
-    if (e != hipSuccess) return fail_hip("swiglu quantize", e);
-    QuantAct a{xq, ldx, am, xs};
     Epilogue gu;
     gu.kind = EPI_SWIGLU;
     gu.activation = activation;
@@ -391,7 +394,17 @@ int loom_amd_swiglu_forward(const loom_amd_matrix* gate, const loom_amd_matrix* 
     gu.ldo = inter;
     gu.acc0 = taps ? taps->acc_gate : nullptr;
     gu.acc1 = taps ? taps->acc_up : nullptr;
-    e = launch_matmul(&G, &U, a, m, gu, s);
+    const bool fused = fused_quant_ok(m, hidden, x);
+    hipError_t e;
+    if (fused) {
+        e = launch_matmul_fused(&G, &U, x, m, gu, taps ? taps->xq : nullptr,
+                                taps ? taps->amax : nullptr, s);
+    } else {
+        e = launch_act_quant(x, hidden, m, hidden, xq, ldx, am, xs, s);
+        if (e != hipSuccess) return fail_hip("swiglu quantize", e);
+        QuantAct a{xq, ldx, am, xs};
+        e = launch_matmul(&G, &U, a, m, gu, s);
+    }
     if (e != hipSuccess) return fail_hip("swiglu gate/up", e);
     e = launch_norm_quant(h, inter, m, inter, inner_norm, eps, strict, hq, ldh, ham, hs, s);
     if (e != hipSuccess) return fail_hip("swiglu inner norm", e);
@@ -407,8 +420,8 @@ int loom_amd_swiglu_forward(const loom_amd_matrix* gate, const loom_amd_matrix* 
     e = launch_matmul(&D, nullptr, b, m, dn, s);
     if (e != hipSuccess) return fail_hip("swiglu down", e);
     if (taps) {
-        if (taps->xq) e = hipMemcpy2DAsync(taps->xq, hidden, xq, ldx, hidden, m, hipMemcpyDeviceToDevice, s);
-        if (e == hipSuccess && taps->amax) e = hipMemcpyAsync(taps->amax, am, (size_t)m * 4, hipMemcpyDeviceToDevice, s);
+        if (!fused && taps->xq) e = hipMemcpy2DAsync(taps->xq, hidden, xq, ldx, hidden, m, hipMemcpyDeviceToDevice, s);
+        if (e == hipSuccess && !fused && taps->amax) e = hipMemcpyAsync(taps->amax, am, (size_t)m * 4, hipMemcpyDeviceToDevice, s);
         if (e == hipSuccess && taps->hq) e = hipMemcpy2DAsync(taps->hq, inter, hq, ldh, inter, m, hipMemcpyDeviceToDevice, s);
         if (e == hipSuccess && taps->hamax) e = hipMemcpyAsync(taps->hamax, ham, (size_t)m * 4, hipMemcpyDeviceToDevice, s);
         if (e != hipSuccess) return fail_hip("swiglu taps", e);

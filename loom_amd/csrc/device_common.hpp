@@ -1,0 +1,206 @@
+// device_common.hpp -- device helpers shared by the gfx950 kernels.
+//
+// All fp64 expressions follow the reference's operation order; the library is
+// compiled with -ffp-contract=off so no multiply-add is fused.
+#pragma once
+
+#include <math.h>
+
+#include "lamd.hpp"
+
+#pragma clang fp contract(off)
+
+namespace lamd {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// Four K-contiguous int8 codes per dword: the tile layout puts column 4d+j of
+// a 16-column word at bit 8j+2d, so dword d is one shift and one AND away.
+__device__ __forceinline__ v4i unpack_codes(uint32_t w) {
+    v4i b;
+    b[0] = (int)(w & 0x03030303u);
+    b[1] = (int)((w >> 2) & 0x03030303u);
+    b[2] = (int)((w >> 4) & 0x03030303u);
+    b[3] = (int)((w >> 6) & 0x03030303u);
+    return b;
+}
+
+__device__ __forceinline__ uint32_t word_of(const uint4& q, int t) {
+    return t == 0 ? q.x : t == 1 ? q.y : t == 2 ? q.z : q.w;
+}
+
+// D(16x16 i32) += A(16x64 i8) * B(64x16 i8).  Lane l supplies A row l&15 and B
+// column l&15 for one 16-wide K group (l>>4); D element v of lane l is
+// row 4*(l>>4)+v, column l&15.
+__device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// bitNetQuantizedActivation (poly/bitnet_cpu.go:73-84) with Go's int(float64)
+// on amd64 (CVTTSD2SQ): NaN and out-of-range values become INT64_MIN, which
+// loom then clamps to -128.
+__device__ __forceinline__ int quant_one(double v, double scale) {
+    const double r = round(v * scale);
+    if (!(r >= -9223372036854775808.0 && r < 9223372036854775808.0)) return -128;
+    if (r < -128.0) return -128;
+    if (r > 127.0) return 127;
+    return (int)r;
+}
+
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+           ((uint32_t)(d & 0xff) << 24);
+}
+
+// loom's "a > maxAbs" update: NaN never replaces the running maximum.
+__device__ __forceinline__ float max_nan_skip(float m, float a) { return a > m ? a : m; }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = max_nan_skip(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Block reductions over blockDim.x threads (a multiple of 64, at most 1024).
+__device__ inline float block_max(float v, float* sh) {
+    v = wave_max(v);
+    const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    if ((threadIdx.x & 63) == 0) sh[w] = v;
+    __syncthreads();
+    float r = sh[0];
+    for (int i = 1; i < nw; ++i) r = max_nan_skip(r, sh[i]);
+    __syncthreads();
+    return r;
+}
+
+__device__ inline int block_sum_i(int v, int* sh) {
+    v = wave_sum_i(v);
+    const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    if ((threadIdx.x & 63) == 0) sh[w] = v;
+    __syncthreads();
+    int r = 0;
+    for (int i = 0; i < nw; ++i) r += sh[i];
+    __syncthreads();
+    return r;
+}
+
+// loom Activate for float32 (poly/poly.go:167-200).
+__device__ inline float activate_f32(float v, int act) {
+    switch (act) {
+        case 0:
+            return v < 0.0f ? 0.0f : v;
+        case 1:
+            return v * (float)(1.0 / (1.0 + exp(-(double)v)));
+        case 2: {
+            const double v64 = (double)v;
+            return (float)(0.5 * v64 *
+                           (1.0 + tanh(sqrt(2.0 / M_PI) * (v64 + 0.044715 * pow(v64, 3.0)))));
+        }
+        case 3:
+            return (float)tanh((double)v);
+        case 4:
+            return (float)(1.0 / (1.0 + exp(-(double)v)));
+        case 5:
+            return v < 0.0f ? (float)((double)v * 0.01) : v;
+        case 6:
+            return v < 0.0f ? 0.0f : v * v;
+        default:
+            return v;
+    }
+}
+
+// swigluGateProduct (poly/swiglu.go:37-46).
+__device__ __forceinline__ double gate_product(double g, double u, int act) {
+    if (act == 6) {
+        if (g < 0.0) g = 0.0;
+        return (g * g) * u;
+    }
+    const double sig = 1.0 / (1.0 + exp(-g));
+    return (g * sig) * u;
+}
+
+// bitNetTernaryMatVecQuantized output scale (poly/bitnet_cpu.go:540-543).
+__device__ __forceinline__ double output_scale(float wscale, float amax) {
+    const double s = (double)wscale * (double)amax / 127.0;
+    return s == 0.0 ? 1.0 : s;
+}
+
+// Epilogue parameters shared by every matmul kernel.
+struct EpiDev {
+    int kind;
+    int activation;
+    int m, n;
+    float scale0, scale1;
+    const float* amax;
+    const int32_t* xsum;
+    const float* bias0;
+    const float* bias1;
+    const float* residual;
+    float* out;
+    float* post;
+    int ldo;
+    int32_t* acc0;
+    int32_t* acc1;
+};
+
+// Per-token-row constants of the epilogue: loom's output scales of matrix
+// 0/1 for the row's amax, and the row's sum(xq).
+struct RowScale {
+    double os0, os1;
+    int xs;
+};
+
+__device__ __forceinline__ RowScale row_scale(const EpiDev& e, float am, int xs) {
+    RowScale rs;
+    rs.os0 = output_scale(e.scale0, am);
+    rs.os1 = e.kind == EPI_SWIGLU ? output_scale(e.scale1, am) : 0.0;
+    rs.xs = xs;
+    return rs;
+}
+
+// raw0/raw1: sum(code * xq) of matrix 0/1 for token row i, output n.  Codes
+// are weight+1, so acc = raw - sum(xq).
+__device__ __forceinline__ void epilogue_store(const EpiDev& e, int i, int n, int raw0, int raw1,
+                                               const RowScale& rs) {
+    const int acc0 = raw0 - rs.xs;
+    const size_t o = (size_t)i * e.ldo + n;
+    if (e.acc0) e.acc0[(size_t)i * e.n + n] = acc0;
+    if (e.kind == EPI_SWIGLU) {
+        const int acc1 = raw1 - rs.xs;
+        if (e.acc1) e.acc1[(size_t)i * e.n + n] = acc1;
+        // g := gate[o] + bias; u := up[o] + bias   (poly/swiglu.go:306-309)
+        const double g = (double)acc0 * rs.os0 + (e.bias0 ? (double)e.bias0[n] : 0.0);
+        const double u = (double)acc1 * rs.os1 + (e.bias1 ? (double)e.bias1[n] : 0.0);
+        e.out[o] = (float)gate_product(g, u, e.activation);
+        return;
+    }
+    double d = (double)acc0 * rs.os0;
+    if (e.bias0) d = d + (double)e.bias0[n];
+    float v = (float)d;
+    if (e.residual) v = v + e.residual[o];
+    e.out[o] = v;
+    if (e.post) e.post[o] = activate_f32(v, e.activation);
+}
+
+// Arguments of the matmul kernels.
+struct MatArgs {
+    const uint4* w0;
+    const uint4* w1;
+    int ktiles;
+    int ntiles;
+    const int8_t* xq;  // quantized rows (unfused paths)
+    int ldq;
+    const float* x;    // fp32 rows (fused-quantization path), ldx = K
+    int k;
+    int8_t* xq_tap;    // fused path: quantized rows written by workgroup 0 (optional)
+    float* amax_tap;
+    EpiDev e;
+};
+
+}  // namespace lamd

@@ -33,6 +33,8 @@ namespace lamd {
 constexpr int kTileRows = 16;
 constexpr int kTileCols = 256;
 constexpr int kTileWords = 256;  // 64 lanes x 4 u32
+constexpr int kMaxNormCols = 8192;        // row width of the norm kernels (256 x 32 in registers)
+constexpr int kMaxStrictNormCols = 8064;  // strict mode keeps n fp64 squares in 64 KB of LDS
 
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 inline int pad_cols(int k) { return ceil_div(k, kTileCols) * kTileCols; }
@@ -76,7 +78,7 @@ struct Epilogue {
     int32_t* acc1 = nullptr;   // M x N debug tap (acc of matrix 1), optional
 };
 
-// ---- launchers (ternary_kernels.hip) ----
+// ---- launchers (quant_norm.hip, matmul_skinny.hip, matmul_gemm.hip) ----
 hipError_t launch_repack(const uint32_t* words, int rows, int cols, int row_words,
                          Matrix* m, hipStream_t s);
 hipError_t launch_act_quant(const float* x, int ldx, int m, int k, int8_t* xq, int ldq,
@@ -87,6 +89,13 @@ hipError_t launch_act_quant_f64(const double* x, int ldx, int m, int k, int8_t* 
 // same quantized activations.  M is the number of token rows.
 hipError_t launch_matmul(const Matrix* w0, const Matrix* w1, const QuantAct& a, int m,
                          const Epilogue& epi, hipStream_t s);
+// Same, quantizing fp32 rows x (M x K, row stride K) inside the matmul kernel
+// (one launch).  Only for the shapes fused_quant_ok accepts.  xq_tap (M x K)
+// and amax_tap (M) optionally receive the quantized rows.
+bool fused_quant_ok(int m, int k, const float* x);
+hipError_t launch_matmul_fused(const Matrix* w0, const Matrix* w1, const float* x, int m,
+                               const Epilogue& epi, int8_t* xq_tap, float* amax_tap,
+                               hipStream_t s);
 // Inner RMSNorm + requantization of SwiGLU rows (poly/bitnet_cpu.go:893-913 then
 // poly/bitnet_cpu.go:97-106).  In place on h (M x n fp32, row stride ldh).
 hipError_t launch_norm_quant(float* h, int ldh, int m, int n, const float* weight, double eps,

@@ -1,0 +1,355 @@
+// matmul_skinny.hip -- ternary matmul for few token rows (decode, M <= 64) and
+// the matmul dispatcher.
+//
+// One workgroup per 16-row weight tile; its WAVES waves split the K tiles and
+// merge partial sums with LDS integer adds (order-free, so exact).  Each wave
+// issues the 128-bit loads of all its weight tiles first.
+//
+// FUSEQ (M <= 4, K % 4 == 0): the workgroup quantizes the fp32 rows itself
+// while its weight loads are in flight -- row absmax over the whole row, then
+// loom's int8 rounding into an LDS copy of the quantized rows -- so a Dense
+// forward is one launch.  Every workgroup derives the same amax, xq and sum(xq)
+// from the same fp32 row, so all outputs agree with a separate quantization.
+#include "device_common.hpp"
+
+namespace lamd {
+
+hipError_t launch_gemm(const MatArgs& p, bool two, hipStream_t s);
+
+constexpr int kFusedMaxRows = 4;
+constexpr int kFusedVec = 16;  // float4 per thread in the fused prologue
+
+template <int NMAT, int MSUB, int WAVES, bool FUSEQ>
+__global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
+    constexpr int T = WAVES * 64;
+    constexpr int U = 4 / MSUB;  // K tiles per batch per wave
+    extern __shared__ __align__(16) int8_t xq_s[];  // FUSEQ: M rows x ldq
+    __shared__ int red[NMAT][MSUB * 16][16];
+    __shared__ unsigned amax_bits[kFusedMaxRows];
+    __shared__ int xsum_s[kFusedMaxRows];
+    const int nt = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int r = lane & 15;
+    const int g = lane >> 4;
+    const int M = p.e.m;
+    const int ktiles = p.ktiles;
+    const size_t tile0 = (size_t)nt * ktiles * 64 + lane;
+
+    // FUSEQ: the fp32 rows are loaded first, so waiting for them does not also
+    // wait for the weight loads queued behind them (loads retire in order).
+    const int k = p.k;
+    const int row4 = k >> 2;            // float4 per row (k % 4 == 0)
+    const int n4 = FUSEQ ? M * row4 : 0;
+    float4 xv[FUSEQ ? kFusedVec : 1];
+    if (FUSEQ) {
+        const float4* x4 = (const float4*)p.x;
+#pragma unroll
+        for (int j = 0; j < kFusedVec; ++j) {
+            const int idx = tid + j * T;
+            if (idx < n4) xv[j] = x4[idx];
+        }
+    }
+
+    // weights of the first batch
+    uint4 wv[NMAT][U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int kt = wave + u * WAVES;
+        if (kt < ktiles) {
+            wv[0][u] = p.w0[tile0 + (size_t)kt * 64];
+            if (NMAT == 2) wv[NMAT - 1][u] = p.w1[tile0 + (size_t)kt * 64];
+        }
+    }
+
+    for (int i = tid; i < NMAT * MSUB * 16 * 16; i += T) (&red[0][0][0])[i] = 0;
+    if (FUSEQ) {
+        if (tid < kFusedMaxRows) {
+            amax_bits[tid] = 0u;
+            xsum_s[tid] = 0;
+        }
+        __syncthreads();
+        // bitNetActivationMaxAbs per row (poly/bitnet_cpu.go:45-57).
+        float lm[kFusedMaxRows] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < kFusedVec; ++j) {
+            const int idx = tid + j * T;
+            if (idx < n4) {
+                float a = max_nan_skip(0.0f, fabsf(xv[j].x));
+                a = max_nan_skip(a, fabsf(xv[j].y));
+                a = max_nan_skip(a, fabsf(xv[j].z));
+                a = max_nan_skip(a, fabsf(xv[j].w));
+                const int row = (idx >= row4) + (idx >= 2 * row4) + (idx >= 3 * row4);
+#pragma unroll
+                for (int rr = 0; rr < kFusedMaxRows; ++rr)
+                    if (rr == row) lm[rr] = max_nan_skip(lm[rr], a);
+            }
+        }
+        // non-negative, non-NaN floats order like their bit patterns
+#pragma unroll
+        for (int rr = 0; rr < kFusedMaxRows; ++rr) {
+            const float wm = wave_max(lm[rr]);
+            if (rr < M && lane == 0 && wm > 0.0f) atomicMax(&amax_bits[rr], __float_as_uint(wm));
+        }
+        __syncthreads();
+        // bitNetQuantizedActivation (poly/bitnet_cpu.go:73-84) into LDS.
+        double sc[kFusedMaxRows];
+#pragma unroll
+        for (int rr = 0; rr < kFusedMaxRows; ++rr) {
+            float am = __uint_as_float(amax_bits[rr]);
+            if (am < 1e-5f) am = 1e-5f;
+            sc[rr] = rr < M ? 127.0 / (double)am : 0.0;
+        }
+        int ls[kFusedMaxRows] = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < kFusedVec; ++j) {
+            const int idx = tid + j * T;
+            if (idx < n4) {
+                const int row = (idx >= row4) + (idx >= 2 * row4) + (idx >= 3 * row4);
+                double s = sc[0];
+#pragma unroll
+                for (int rr = 1; rr < kFusedMaxRows; ++rr)
+                    if (rr == row) s = sc[rr];
+                const int q0 = quant_one((double)xv[j].x, s);
+                const int q1 = quant_one((double)xv[j].y, s);
+                const int q2 = quant_one((double)xv[j].z, s);
+                const int q3 = quant_one((double)xv[j].w, s);
+                *(uint32_t*)(xq_s + row * p.ldq + 4 * (idx - row * row4)) = pack4(q0, q1, q2, q3);
+#pragma unroll
+                for (int rr = 0; rr < kFusedMaxRows; ++rr)
+                    if (rr == row) ls[rr] += q0 + q1 + q2 + q3;
+            }
+        }
+        // zero the padding columns k .. ldq of every row
+        const int pad4 = (p.ldq - k) >> 2;
+        for (int i = tid; i < M * pad4; i += T) {
+            const int row = i / pad4;
+            *(uint32_t*)(xq_s + row * p.ldq + k + 4 * (i - row * pad4)) = 0u;
+        }
+#pragma unroll
+        for (int rr = 0; rr < kFusedMaxRows; ++rr) {
+            const int v = wave_sum_i(ls[rr]);
+            if (rr < M && lane == 0 && v != 0) atomicAdd(&xsum_s[rr], v);
+        }
+        __syncthreads();
+        if (blockIdx.x == 0) {
+            if (p.xq_tap) {
+                for (int i = tid; i < M * k; i += T) p.xq_tap[i] = xq_s[(i / k) * p.ldq + (i % k)];
+            }
+            if (p.amax_tap && tid < M) {
+                float am = __uint_as_float(amax_bits[tid]);
+                p.amax_tap[tid] = am < 1e-5f ? 1e-5f : am;
+            }
+        }
+    }
+
+    v4i acc[NMAT][MSUB];
+#pragma unroll
+    for (int a = 0; a < NMAT; ++a)
+#pragma unroll
+        for (int ms = 0; ms < MSUB; ++ms) acc[a][ms] = v4i{0, 0, 0, 0};
+
+    const int8_t* xbase[MSUB];
+    bool xval[MSUB];
+#pragma unroll
+    for (int ms = 0; ms < MSUB; ++ms) {
+        const int row = ms * 16 + r;
+        xval[ms] = row < M;
+        const int rr = xval[ms] ? row : 0;
+        xbase[ms] = (FUSEQ ? (const int8_t*)xq_s : p.xq) + (size_t)rr * p.ldq + g * 64;
+    }
+
+    for (int kb = wave; kb < ktiles; kb += WAVES * U) {
+        // next batch's weights, issued before this batch's MFMAs
+        uint4 wn[NMAT][U];
+        const int kn = kb + WAVES * U;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int kt = kn + u * WAVES;
+            if (kt < ktiles) {
+                wn[0][u] = p.w0[tile0 + (size_t)kt * 64];
+                if (NMAT == 2) wn[NMAT - 1][u] = p.w1[tile0 + (size_t)kt * 64];
+            }
+        }
+        v4i a[MSUB][U][4];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int kt = kb + u * WAVES;
+            if (kt < ktiles) {
+#pragma unroll
+                for (int ms = 0; ms < MSUB; ++ms) {
+                    const v4i* xp = (const v4i*)(xbase[ms] + (size_t)kt * kTileCols);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) a[ms][u][t] = xval[ms] ? xp[t] : v4i{0, 0, 0, 0};
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int kt = kb + u * WAVES;
+            if (kt < ktiles) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                    for (int mat = 0; mat < NMAT; ++mat) {
+                        const v4i b = unpack_codes(word_of(wv[mat][u], t));
+#pragma unroll
+                        for (int ms = 0; ms < MSUB; ++ms)
+                            acc[mat][ms] = mfma_i8(a[ms][u][t], b, acc[mat][ms]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+            for (int u = 0; u < U; ++u) wv[mat][u] = wn[mat][u];
+    }
+
+    __syncthreads();
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+        for (int ms = 0; ms < MSUB; ++ms)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int tok = ms * 16 + 4 * g + v;
+                if (tok < M) atomicAdd(&red[mat][tok][r], acc[mat][ms][v]);
+            }
+    __syncthreads();
+
+    for (int idx = tid; idx < M * 16; idx += T) {
+        const int tok = idx >> 4;
+        const int col = idx & 15;
+        const int n = nt * kTileRows + col;
+        if (n >= p.e.n) continue;
+        float am;
+        int xs;
+        if (FUSEQ) {
+            am = __uint_as_float(amax_bits[tok]);
+            if (am < 1e-5f) am = 1e-5f;
+            xs = xsum_s[tok];
+        } else {
+            am = p.e.amax[tok];
+            xs = p.e.xsum[tok];
+        }
+        epilogue_store(p.e, tok, n, red[0][tok][col], red[NMAT - 1][tok][col], row_scale(p.e, am, xs));
+    }
+}
+
+// ------------------------------------------------------------------------
+// dispatch
+// ------------------------------------------------------------------------
+
+// Split-K width: enough waves for ~2048 in flight over the chip, never more
+// waves than K tiles, and at most `cap` (register budget of wide tiles).
+static int pick_waves(int ntiles, int ktiles, int cap) {
+    const int want = (2048 + ntiles - 1) / ntiles;
+    int w = 1;
+    while (w < want && w < cap && w < ktiles) w <<= 1;
+    return w;
+}
+
+template <int NMAT, int MSUB, bool FUSEQ>
+static hipError_t launch_skinny(const MatArgs& p, hipStream_t s) {
+    // 1024-thread workgroups leave 128 VGPRs per lane: only the one-matrix kernels fit.
+    constexpr int kCap = NMAT == 1 ? 16 : 8;
+    int w = pick_waves(p.ntiles, p.ktiles, kCap);
+    if (FUSEQ) {
+        // the fused prologue holds M*K/4 float4 over kFusedVec registers per thread
+        while (w < kCap && (size_t)p.e.m * p.k > (size_t)4 * kFusedVec * 64 * w) w <<= 1;
+    }
+    const size_t shm = FUSEQ ? (size_t)p.e.m * p.ldq : 0;
+    const dim3 grid(p.ntiles);
+    switch (w) {
+        case 1:
+            hipLaunchKernelGGL((skinny_kernel<NMAT, MSUB, 1, FUSEQ>), grid, dim3(64), shm, s, p);
+            break;
+        case 2:
+            hipLaunchKernelGGL((skinny_kernel<NMAT, MSUB, 2, FUSEQ>), grid, dim3(128), shm, s, p);
+            break;
+        case 4:
+            hipLaunchKernelGGL((skinny_kernel<NMAT, MSUB, 4, FUSEQ>), grid, dim3(256), shm, s, p);
+            break;
+        case 8:
+            hipLaunchKernelGGL((skinny_kernel<NMAT, MSUB, 8, FUSEQ>), grid, dim3(512), shm, s, p);
+            break;
+        default:
+            if constexpr (kCap == 16) {
+                hipLaunchKernelGGL((skinny_kernel<NMAT, MSUB, 16, FUSEQ>), grid, dim3(1024), shm, s, p);
+            }
+            break;
+    }
+    return hipGetLastError();
+}
+
+const char* kernel_variant(int m) {
+    if (m <= kFusedMaxRows) return "skinny_m16_fusedq";
+    if (m <= 16) return "skinny_m16";
+    if (m <= 32) return "skinny_m32";
+    if (m <= 64) return "skinny_m64";
+    return "gemm";
+}
+
+static MatArgs make_args(const Matrix* w0, const Matrix* w1, int m, const Epilogue& epi) {
+    MatArgs p{};
+    p.w0 = (const uint4*)w0->tiles;
+    p.w1 = (const uint4*)(w1 ? w1->tiles : w0->tiles);
+    p.ktiles = w0->ktiles;
+    p.ntiles = w0->ntiles;
+    p.k = w0->cols;
+    EpiDev& e = p.e;
+    e.kind = epi.kind;
+    e.activation = epi.activation;
+    e.m = m;
+    e.n = w0->rows;
+    e.scale0 = w0->scale;
+    e.scale1 = w1 ? w1->scale : w0->scale;
+    e.bias0 = epi.bias0;
+    e.bias1 = epi.bias1;
+    e.residual = epi.residual;
+    e.out = epi.out;
+    e.post = epi.post;
+    e.ldo = epi.ldo > 0 ? epi.ldo : w0->rows;
+    e.acc0 = epi.acc0;
+    e.acc1 = epi.acc1;
+    return p;
+}
+
+hipError_t launch_matmul(const Matrix* w0, const Matrix* w1, const QuantAct& a, int m,
+                         const Epilogue& epi, hipStream_t s) {
+    if (m <= 0) return hipSuccess;
+    MatArgs p = make_args(w0, w1, m, epi);
+    p.xq = a.xq;
+    p.ldq = a.ldq;
+    p.e.amax = a.amax;
+    p.e.xsum = a.xsum;
+    const bool two = epi.kind == EPI_SWIGLU;
+    if (m <= 16) return two ? launch_skinny<2, 1, false>(p, s) : launch_skinny<1, 1, false>(p, s);
+    if (m <= 32) return two ? launch_skinny<2, 2, false>(p, s) : launch_skinny<1, 2, false>(p, s);
+    if (m <= 64) return two ? launch_skinny<2, 4, false>(p, s) : launch_skinny<1, 4, false>(p, s);
+    return launch_gemm(p, two, s);
+}
+
+// The fused prologue holds the M x K rows in registers (kFusedVec float4 per
+// thread of a 512-thread workgroup) and their int8 copy in LDS.
+bool fused_quant_ok(int m, int k, const float* x) {
+    return m >= 1 && m <= kFusedMaxRows && k % 4 == 0 && ((uintptr_t)x & 15) == 0 &&
+           (size_t)m * k <= (size_t)4 * kFusedVec * 512 && pad_cols(k) * (size_t)m <= 64 * 1024;
+}
+
+hipError_t launch_matmul_fused(const Matrix* w0, const Matrix* w1, const float* x, int m,
+                               const Epilogue& epi, int8_t* xq_tap, float* amax_tap,
+                               hipStream_t s) {
+    if (m <= 0) return hipSuccess;
+    if (!fused_quant_ok(m, w0->cols, x)) return hipErrorInvalidValue;
+    MatArgs p = make_args(w0, w1, m, epi);
+    p.x = x;
+    p.ldq = pad_cols(w0->cols);
+    p.xq_tap = xq_tap;
+    p.amax_tap = amax_tap;
+    return epi.kind == EPI_SWIGLU ? launch_skinny<2, 1, true>(p, s) : launch_skinny<1, 1, true>(p, s);
+}
+
+}  // namespace lamd

@@ -1,0 +1,275 @@
+// quant_norm.hip -- weight repack, activation quantization and the SwiGLU
+// inner RMSNorm + requantization (gfx950).
+#include "device_common.hpp"
+
+namespace lamd {
+
+// ------------------------------------------------------------------------
+// repack: loom row-major Words (poly/bitnet_cpu.go:14-43) -> tile layout
+// ------------------------------------------------------------------------
+
+__global__ void repack_tiles_kernel(const uint32_t* __restrict__ words, int rows, int cols,
+                                    int row_words, int ktiles, long total,
+                                    uint32_t* __restrict__ out) {
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int t = (int)(idx & 3);
+    const int lane = (int)((idx >> 2) & 63);
+    const long tile = idx >> 8;
+    const int kt = (int)(tile % ktiles);
+    const int nt = (int)(tile / ktiles);
+    const int n = nt * kTileRows + (lane & 15);
+    const int k0 = kt * kTileCols + (lane >> 4) * 64 + t * 16;
+    uint32_t src = 0;
+    if (n < rows && k0 < cols) {
+        src = words[(long)n * row_words + (k0 >> 4)];
+        const int valid = cols - k0;
+        if (valid < 16) src &= (1u << (2 * valid)) - 1u;
+    }
+    uint32_t o = 0;
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+        const uint32_t code = (src >> (2 * c)) & 3u;
+        o |= code << (8 * (c & 3) + 2 * (c >> 2));
+    }
+    out[idx] = o;
+}
+
+hipError_t launch_repack(const uint32_t* words, int rows, int cols, int row_words, Matrix* m,
+                         hipStream_t s) {
+    const long total = (long)m->ntiles * m->ktiles * kTileWords;
+    if (total == 0) return hipSuccess;
+    const int threads = 256;
+    const long blocks = (total + threads - 1) / threads;
+    hipLaunchKernelGGL(repack_tiles_kernel, dim3((unsigned)blocks), dim3(threads), 0, s, words,
+                       rows, cols, row_words, m->ktiles, total, m->tiles);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------
+// activation quantization (poly/bitnet_cpu.go:45-117): one workgroup of 256
+// threads per token row; every load of the row is issued before the max.
+// VPT = values per thread held in registers (k <= 256*VPT); VPT 0 = loop.
+// ------------------------------------------------------------------------
+
+template <typename T, int VPT>
+__global__ __launch_bounds__(256) void act_quant_kernel(const T* __restrict__ x, int ldx, int k,
+                                                        int ldq, int8_t* __restrict__ xq,
+                                                        float* __restrict__ amax_out,
+                                                        int32_t* __restrict__ xsum_out) {
+    __shared__ float shf[4];
+    __shared__ int shi[4];
+    const int row = blockIdx.x;
+    const T* xr = x + (size_t)row * ldx;
+    int8_t* qr = xq + (size_t)row * ldq;
+    float m = 0.0f;
+    int s = 0;
+    if (VPT > 0) {
+        T v[VPT > 0 ? VPT : 1];
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int i = threadIdx.x + j * 256;
+            v[j] = i < k ? xr[i] : (T)0;
+        }
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            // float32(|float64(v)|): exact for fp32 input, one rounding for fp64.
+            if (threadIdx.x + j * 256 < k) m = max_nan_skip(m, (float)fabs((double)v[j]));
+        }
+        m = block_max(m, shf);
+        if (m < 1e-5f) m = 1e-5f;
+        const double scale = 127.0 / (double)m;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int i = threadIdx.x + j * 256;
+            if (i < k) {
+                const int q = quant_one((double)v[j], scale);
+                s += q;
+                qr[i] = (int8_t)q;
+            }
+        }
+    } else {
+        for (int i = threadIdx.x; i < k; i += 256) m = max_nan_skip(m, (float)fabs((double)xr[i]));
+        m = block_max(m, shf);
+        if (m < 1e-5f) m = 1e-5f;
+        const double scale = 127.0 / (double)m;
+        for (int i = threadIdx.x; i < k; i += 256) {
+            const int q = quant_one((double)xr[i], scale);
+            s += q;
+            qr[i] = (int8_t)q;
+        }
+    }
+    for (int i = k + threadIdx.x; i < ldq; i += 256) qr[i] = 0;
+    s = block_sum_i(s, shi);
+    if (threadIdx.x == 0) {
+        amax_out[row] = m;
+        xsum_out[row] = s;
+    }
+}
+
+template <typename T>
+static hipError_t launch_quant_t(const T* x, int ldx, int m, int k, int8_t* xq, int ldq,
+                                 float* amax, int32_t* xsum, hipStream_t s) {
+    if (m <= 0) return hipSuccess;
+    const dim3 g(m), b(256);
+    if (k <= 256 * 4) {
+        hipLaunchKernelGGL((act_quant_kernel<T, 4>), g, b, 0, s, x, ldx, k, ldq, xq, amax, xsum);
+    } else if (k <= 256 * 8) {
+        hipLaunchKernelGGL((act_quant_kernel<T, 8>), g, b, 0, s, x, ldx, k, ldq, xq, amax, xsum);
+    } else if (k <= 256 * 16) {
+        hipLaunchKernelGGL((act_quant_kernel<T, 16>), g, b, 0, s, x, ldx, k, ldq, xq, amax, xsum);
+    } else if (k <= 256 * 32) {
+        hipLaunchKernelGGL((act_quant_kernel<T, 32>), g, b, 0, s, x, ldx, k, ldq, xq, amax, xsum);
+    } else {
+        hipLaunchKernelGGL((act_quant_kernel<T, 0>), g, b, 0, s, x, ldx, k, ldq, xq, amax, xsum);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_act_quant(const float* x, int ldx, int m, int k, int8_t* xq, int ldq,
+                            float* amax, int32_t* xsum, hipStream_t s) {
+    return launch_quant_t<float>(x, ldx, m, k, xq, ldq, amax, xsum, s);
+}
+
+hipError_t launch_act_quant_f64(const double* x, int ldx, int m, int k, int8_t* xq, int ldq,
+                                float* amax, int32_t* xsum, hipStream_t s) {
+    return launch_quant_t<double>(x, ldx, m, k, xq, ldq, amax, xsum, s);
+}
+
+// ------------------------------------------------------------------------
+// SwiGLU inner RMSNorm + requantization (poly/bitnet_cpu.go:893-913, then
+// poly/bitnet_cpu.go:97-106), one 256-thread workgroup per row, in place.
+//
+// strict: the sum of squares is loom's sequential fp64 chain in column
+//   order.  The squares f*f are exact in fp64 (24-bit x 24-bit significands),
+//   so all threads form them in parallel into LDS and one lane performs only
+//   the ordered additions.
+// fast:  thread t sums columns t, t+256, ... then a fixed binary tree; the
+//   result is deterministic but rounds differently from the chain, which moves
+//   normalized values by at most one fp32 ulp.
+// VPT = values per thread in registers (n <= 256*VPT).
+// ------------------------------------------------------------------------
+
+template <int STRICT, int VPT>
+__global__ __launch_bounds__(256) void norm_quant_kernel(float* __restrict__ h, int ldh, int n,
+                                                         const float* __restrict__ weight,
+                                                         double eps, int8_t* __restrict__ hq,
+                                                         int ldq, float* __restrict__ amax_out,
+                                                         int32_t* __restrict__ xsum_out) {
+    extern __shared__ double dsh[];  // STRICT: n squares; fast: 256 partial sums
+    __shared__ float shf[4];
+    __shared__ int shi[4];
+    __shared__ double total;
+    const int row = blockIdx.x;
+    float* hr = h + (size_t)row * ldh;
+    float v[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int i = threadIdx.x + j * 256;
+        v[j] = i < n ? hr[i] : 0.0f;
+    }
+    if (STRICT) {
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int i = threadIdx.x + j * 256;
+            if (i < n) {
+                const double f = (double)v[j];
+                dsh[i] = f * f;
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            double s = 0.0;
+            const double2* sq = (const double2*)dsh;
+            const int pairs = n >> 1;
+            for (int i = 0; i < pairs; ++i) {
+                const double2 p = sq[i];
+                s += p.x;
+                s += p.y;
+            }
+            if (n & 1) s += dsh[n - 1];
+            total = s;
+        }
+        __syncthreads();
+    } else {
+        double s = 0.0;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const double f = (double)v[j];  // zero past n
+            s += f * f;
+        }
+        dsh[threadIdx.x] = s;
+        __syncthreads();
+        for (int width = 128; width > 0; width >>= 1) {
+            if (threadIdx.x < width) dsh[threadIdx.x] = dsh[threadIdx.x] + dsh[threadIdx.x + width];
+            __syncthreads();
+        }
+        if (threadIdx.x == 0) total = dsh[0];
+        __syncthreads();
+    }
+
+    const double scale = 1.0 / sqrt(total / (double)n + eps);
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int i = threadIdx.x + j * 256;
+        if (i < n) {
+            const double w = weight ? (double)weight[i] : 1.0;
+            v[j] = (float)((double)v[j] * scale * w);
+            hr[i] = v[j];
+            m = max_nan_skip(m, fabsf(v[j]));
+        }
+    }
+    m = block_max(m, shf);
+    if (m < 1e-5f) m = 1e-5f;
+    const double qs = 127.0 / (double)m;
+    int s = 0;
+    int8_t* qr = hq + (size_t)row * ldq;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int i = threadIdx.x + j * 256;
+        if (i < n) {
+            const int q = quant_one((double)v[j], qs);
+            s += q;
+            qr[i] = (int8_t)q;
+        }
+    }
+    for (int i = n + threadIdx.x; i < ldq; i += 256) qr[i] = 0;
+    s = block_sum_i(s, shi);
+    if (threadIdx.x == 0) {
+        amax_out[row] = m;
+        xsum_out[row] = s;
+    }
+}
+
+template <int STRICT>
+static hipError_t launch_norm_t(float* h, int ldh, int m, int n, const float* weight, double eps,
+                                int8_t* hq, int ldq, float* amax, int32_t* xsum, hipStream_t s) {
+    const size_t shm = STRICT ? (size_t)n * sizeof(double) : 256 * sizeof(double);
+    const dim3 g(m), b(256);
+    if (n <= 256 * 8) {
+        hipLaunchKernelGGL((norm_quant_kernel<STRICT, 8>), g, b, shm, s, h, ldh, n, weight, eps, hq,
+                           ldq, amax, xsum);
+    } else if (n <= 256 * 16) {
+        hipLaunchKernelGGL((norm_quant_kernel<STRICT, 16>), g, b, shm, s, h, ldh, n, weight, eps,
+                           hq, ldq, amax, xsum);
+    } else if (n <= 256 * 32) {
+        hipLaunchKernelGGL((norm_quant_kernel<STRICT, 32>), g, b, shm, s, h, ldh, n, weight, eps,
+                           hq, ldq, amax, xsum);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_norm_quant(float* h, int ldh, int m, int n, const float* weight, double eps,
+                             int strict, int8_t* hq, int ldq, float* amax, int32_t* xsum,
+                             hipStream_t s) {
+    if (m <= 0) return hipSuccess;
+    if (eps <= 0.0) eps = 1e-5;
+    if (n > kMaxNormCols) return hipErrorInvalidValue;
+    return strict ? launch_norm_t<1>(h, ldh, m, n, weight, eps, hq, ldq, amax, xsum, s)
+                  : launch_norm_t<0>(h, ldh, m, n, weight, eps, hq, ldq, amax, xsum, s);
+}
+
+}  // namespace lamd

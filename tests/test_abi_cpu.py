@@ -82,9 +82,10 @@ def test_amd_extension_errors_without_gpu(amd_lib):
     words = (C.c_uint32 * 4)()
     assert amd_lib.loom_amd_matrix_create(0, words, 4, 1, 64, 4, 1.0, C.byref(out)) == -1
     assert b"not visible" in amd_lib.loom_amd_last_error()
-    assert amd_lib.loom_amd_kernel_variant(1) == b"skinny_m16"
+    assert amd_lib.loom_amd_kernel_variant(1) == b"skinny_m16_fusedq"
+    assert amd_lib.loom_amd_kernel_variant(5) == b"skinny_m16"
     assert amd_lib.loom_amd_kernel_variant(64) == b"skinny_m64"
-    assert amd_lib.loom_amd_kernel_variant(65) == b"gemm_128"
+    assert amd_lib.loom_amd_kernel_variant(65) == b"gemm"
 
 
 def test_python_accel_mirror_refuses_cpu(amd_lib):

@@ -190,6 +190,35 @@ def test_dense_batch_edges(orc, torch_dev, bn, M):
     _check_dense(orc, torch_dev, bn, m, x)
 
 
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_dense_fused_quant_edge_rows(orc, torch_dev, bn, M):
+    # M <= 4 with K % 4 == 0 quantizes inside the matmul launch: the same
+    # loom edge semantics as the standalone quantizer (zero row -> 1e-5 floor,
+    # NaN ignored by amax and quantized to -128, inf amax -> scale 0).
+    assert bn._lib.lib().loom_amd_kernel_variant(M) == b"skinny_m16_fusedq"
+    k = 2560
+    m = orc.random_matrix(96, k, seed=12)
+    specials = [np.zeros(k, np.float32), np.full(k, 2e-6, np.float32)]
+    r = orc.normal_f32(k, 3)
+    r[10] = np.nan
+    specials.append(r)
+    r = orc.normal_f32(k, 4)
+    r[11] = -np.inf
+    specials.append(r)
+    for start in range(0, len(specials)):
+        rows = [specials[(start + i) % len(specials)] for i in range(M)]
+        x = np.stack(rows)
+        with np.errstate(invalid="ignore"):
+            ref = orc.dense_forward(m, x, simd=True)
+        w = gpu_matrix(bn, m)
+        pre, _, taps = bn.dense_forward_packed_ternary(w, to_dev(torch_dev, x), taps=True)
+        torch_dev.cuda.synchronize()
+        assert np.array_equal(taps.xq.cpu().numpy(), ref.xq)
+        assert taps.amax.cpu().numpy().tobytes() == ref.amax.tobytes()
+        assert np.array_equal(taps.acc.cpu().numpy(), ref.acc)
+        assert pre.cpu().numpy().tobytes() == ref.pre.tobytes()
+
+
 @pytest.mark.parametrize("act", [0, 1, 6])
 def test_dense_activation_and_residual(orc, torch_dev, bn, act):
     m = orc.random_matrix(96, 160, seed=5)
