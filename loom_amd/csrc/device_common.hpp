@@ -16,6 +16,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 // Four K-contiguous int8 codes per dword: the tile layout puts column 4d+j of
 // a 16-column word at bit 8j+2d, so dword d is one shift and one AND away.
+// Word t of a lane with K group g = lane>>4 holds tile columns 64t+16g .. +15.
 __device__ __forceinline__ v4i unpack_codes(uint32_t w) {
     v4i b;
     b[0] = (int)(w & 0x03030303u);
@@ -30,8 +31,8 @@ __device__ __forceinline__ uint32_t word_of(const uint4& q, int t) {
 }
 
 // D(16x16 i32) += A(16x64 i8) * B(64x16 i8).  Lane l supplies A row l&15 and B
-// column l&15 for one 16-wide K group (l>>4); D element v of lane l is
-// row 4*(l>>4)+v, column l&15.
+// column l&15 for the 16-wide K group l>>4 (the same 16 K indices on both
+// sides); D element v of lane l is row 4*(l>>4)+v, column l&15.
 __device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }

@@ -8,7 +8,8 @@
 //     (nt*ktiles + kt) * 256 and holds 64 lanes x 4 words (1 KiB), so one
 //     wavefront reads a tile with one fully coalesced 128-bit load per lane;
 //   * lane l of a tile owns weight row 16*nt + (l & 15) and columns
-//     256*kt + 64*(l >> 4) + 16*t + c for word t (0..3), c (0..15);
+//     256*kt + 64*t + 16*(l >> 4) + c for word t (0..3), c (0..15): word t of
+//     the 64 lanes covers the contiguous K step [64t, 64t+64) of the tile;
 //   * inside a word, the 2-bit code of column c = 4*d + j sits at bit
 //     8*j + 2*d, so (word >> 2*d) & 0x03030303 is four int8 codes for the
 //     K-contiguous columns 4d..4d+3 -- one shift and one AND per dword, and

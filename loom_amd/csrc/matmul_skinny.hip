@@ -157,7 +157,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
         const int row = ms * 16 + r;
         xval[ms] = row < M;
         const int rr = xval[ms] ? row : 0;
-        xbase[ms] = (FUSEQ ? (const int8_t*)xq_s : p.xq) + (size_t)rr * p.ldq + g * 64;
+        xbase[ms] = (FUSEQ ? (const int8_t*)xq_s : p.xq) + (size_t)rr * p.ldq + g * 16;
     }
 
     for (int kb = wave; kb < ktiles; kb += WAVES * U) {
@@ -179,9 +179,10 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
             if (kt < ktiles) {
 #pragma unroll
                 for (int ms = 0; ms < MSUB; ++ms) {
-                    const v4i* xp = (const v4i*)(xbase[ms] + (size_t)kt * kTileCols);
+                    const int8_t* xp = xbase[ms] + (size_t)kt * kTileCols;
 #pragma unroll
-                    for (int t = 0; t < 4; ++t) a[ms][u][t] = xval[ms] ? xp[t] : v4i{0, 0, 0, 0};
+                    for (int t = 0; t < 4; ++t)
+                        a[ms][u][t] = xval[ms] ? *(const v4i*)(xp + 64 * t) : v4i{0, 0, 0, 0};
                 }
             }
         }
@@ -289,7 +290,7 @@ const char* kernel_variant(int m) {
     if (m <= 16) return "skinny_m16";
     if (m <= 32) return "skinny_m32";
     if (m <= 64) return "skinny_m64";
-    return "gemm";
+    return "gemm";  // gemm512 (256x256 tiles) when they fill the chip, else gemm128
 }
 
 static MatArgs make_args(const Matrix* w0, const Matrix* w1, int m, const Epilogue& epi) {

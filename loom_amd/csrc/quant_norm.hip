@@ -19,7 +19,7 @@ __global__ void repack_tiles_kernel(const uint32_t* __restrict__ words, int rows
     const int kt = (int)(tile % ktiles);
     const int nt = (int)(tile / ktiles);
     const int n = nt * kTileRows + (lane & 15);
-    const int k0 = kt * kTileCols + (lane >> 4) * 64 + t * 16;
+    const int k0 = kt * kTileCols + t * 64 + (lane >> 4) * 16;
     uint32_t src = 0;
     if (n < rows && k0 < cols) {
         src = words[(long)n * row_words + (k0 >> 4)];

@@ -154,6 +154,12 @@ def _check_dense(orc, torch, bn, m, x, activation=-1, residual=None):
     assert np.array_equal(acc, ref.acc), f"int32 accumulators ({np.count_nonzero(acc != ref.acc)} differ of {acc.size})"
     want_pre = ref.pre if residual is None else (ref.pre + residual).astype(np.float32)
     assert pre.cpu().numpy().tobytes() == want_pre.tobytes(), "fp32 pre-activation (bit-exact)"
+    # without debug taps the kernels take their plain epilogue: same bytes
+    pre2, _ = bn.dense_forward_packed_ternary(
+        w, to_dev(torch, x), activation=activation,
+        residual=None if residual is None else to_dev(torch, residual))
+    torch.cuda.synchronize()
+    assert pre2.cpu().numpy().tobytes() == want_pre.tobytes(), "fp32 output without taps"
     if activation != -1:
         if residual is None:
             got = post.cpu().numpy()
@@ -413,3 +419,27 @@ def test_library_errors_are_loud(orc, torch_dev, bn):
     with pytest.raises(_lib.AMDError, match="truncated"):
         bn.TernaryMatrix.from_entity_blob(m.entity_blob()[:-4])
     assert _lib.lib().loom_amd_ternary_matmul(None, None, 256, None, None, 1, None, None, None) == -1
+
+
+# ---------------------------------------------------------------- 256x256-tile GEMM paths
+def test_gemm512_ragged_rows_and_tiles(orc, torch_dev, bn):
+    # M and N not multiples of the 256-row / 16-row tiles: clamped loads must
+    # only ever feed outputs that are not stored.
+    m = orc.random_matrix(6900, 2560, seed=91)
+    x = orc.normal_f32(4100 * 2560, seed=92).reshape(4100, 2560)
+    _check_dense(orc, torch_dev, bn, m, x)
+
+
+def test_gemm512_general_epilogue(orc, torch_dev, bn):
+    # residual + activation force the general epilogue of the large-tile kernel
+    m = orc.random_matrix(4096, 512, seed=93)
+    x = orc.normal_f32(4096 * 512, seed=94).reshape(4096, 512)
+    res = orc.normal_f32(4096 * 4096, seed=95).reshape(4096, 4096)
+    _check_dense(orc, torch_dev, bn, m, x, activation=0)
+    _check_dense(orc, torch_dev, bn, m, x, residual=res)
+
+
+def test_swiglu_large_tiles(orc, torch_dev, bn):
+    # gate|up at M=4096 x inter=4096 runs the two-matrix large-tile kernel
+    _swiglu_case(orc, torch_dev, bn, hidden=640, inter=4096, M=4096, seed=97, norm="fast",
+                 with_norm_w=True)
