@@ -751,3 +751,207 @@ void orc_fill_uniform_f32(float* out, long n, float lo, float hi, uint64_t seed)
         out[i] = (float)((double)lo + ((double)hi - (double)lo) * u);
     }
 }
+
+/* ------------------------------------------------------------------ */
+/* Attention, decoder block, LM head                                   */
+/* ------------------------------------------------------------------ */
+
+/* bitNetRMSNormFloat64Weighted + bitNetQuantizeActivationFloat64 are above. */
+
+/* MHAForwardPackedTernaryCPU (poly/mha.go:204-371) for one batch row of
+ * `seq` tokens.  Per-head Q/K norms are not supported (BitNet has none).
+ * The KV cache is a ring of msl rows (pos % msl), prepared as
+ * mhaPrepareKVForForward does (poly/mha_layout.go:62-70): a pass that is not
+ * a warm single-token step resets kv_offset to 0. */
+void orc_mha_forward(orc_mha* L, const float* in, int seq, int simd, int workers,
+                     float* pre, float* post, double* q_out, double* attn_out) {
+    const int d_model = L->d_model;
+    const int heads = L->num_heads;
+    const int kv_heads = L->num_kv_heads > 0 ? L->num_kv_heads : heads;
+    const int hd = L->head_dim;
+    const int q_dim = heads * hd;
+    const int kv_dim = kv_heads * hd;
+    const int msl = L->msl > 0 ? L->msl : 512;
+    const int incremental = (seq == 1 && L->kv_offset > 0);
+    if (!incremental) {
+        memset(L->cache_k, 0, (size_t)msl * kv_dim * sizeof(float));
+        memset(L->cache_v, 0, (size_t)msl * kv_dim * sizeof(float));
+        L->kv_offset = 0;
+    }
+    const int seq_base = L->kv_offset;
+    double* Q = (double*)malloc((size_t)seq * q_dim * sizeof(double));
+    double* tq = (double*)malloc((size_t)q_dim * sizeof(double));
+    double* tk = (double*)malloc((size_t)kv_dim * sizeof(double));
+    double* tv = (double*)malloc((size_t)kv_dim * sizeof(double));
+    int8_t* xq = (int8_t*)malloc((size_t)d_model);
+    const double theta = L->theta > 0 ? L->theta : 10000.0;
+    const int half = hd / 2;
+    for (int s = 0; s < seq; s++) {
+        const int pos = seq_base + s;
+        const float* row = in + (size_t)s * d_model;
+        float* krow = L->cache_k + (size_t)(pos % msl) * kv_dim;
+        float* vrow = L->cache_v + (size_t)(pos % msl) * kv_dim;
+        float amax = orc_quant_act_f32(row, d_model, xq);
+        matvec_quantized(L->q, xq, amax, simd, workers, tq, NULL);
+        for (int i = 0; i < q_dim; i++) {
+            Q[(size_t)s * q_dim + i] = tq[i] + (L->bias_q ? (double)L->bias_q[i] : 0.0);
+        }
+        matvec_quantized(L->k, xq, amax, simd, workers, tk, NULL);
+        matvec_quantized(L->v, xq, amax, simd, workers, tv, NULL);
+        for (int i = 0; i < kv_dim; i++) {
+            krow[i] = (float)(tk[i] + (L->bias_k ? (double)L->bias_k[i] : 0.0));
+            vrow[i] = (float)(tv[i] + (L->bias_v ? (double)L->bias_v[i] : 0.0));
+        }
+        for (int h = 0; h < heads; h++) {
+            for (int d = 0; d < half; d++) {
+                double angle = (double)pos / pow(theta, (double)(2 * d) / (double)hd);
+                double c = cos(angle), sv = sin(angle);
+                size_t off = (size_t)s * q_dim + (size_t)h * hd + d;
+                double v0 = Q[off], v1 = Q[off + half];
+                Q[off] = v0 * c - v1 * sv;
+                Q[off + half] = v0 * sv + v1 * c;
+            }
+        }
+        for (int h = 0; h < kv_heads; h++) {
+            for (int d = 0; d < half; d++) {
+                double angle = (double)pos / pow(theta, (double)(2 * d) / (double)hd);
+                double c = cos(angle), sv = sin(angle);
+                int off = h * hd + d;
+                double v0 = (double)krow[off], v1 = (double)krow[off + half];
+                krow[off] = (float)(v0 * c - v1 * sv);
+                krow[off + half] = (float)(v0 * sv + v1 * c);
+            }
+        }
+    }
+    if (q_out) memcpy(q_out, Q, (size_t)seq * q_dim * sizeof(double));
+    const int per_kv = heads / kv_heads;
+    const double scale = 1.0 / sqrt((double)hd);
+    double* attn = (double*)malloc((size_t)seq * q_dim * sizeof(double));
+    double* scores = (double*)malloc((size_t)(seq_base + seq) * sizeof(double));
+    for (int s = 0; s < seq; s++) {
+        const int total = seq_base + s;
+        for (int h = 0; h < heads; h++) {
+            const int kvh = h / per_kv;
+            double max_score = -1e9;
+            for (int kp = 0; kp <= total; kp++) {
+                const float* kr = L->cache_k + (size_t)(kp % msl) * kv_dim + (size_t)kvh * hd;
+                const double* qr = Q + (size_t)s * q_dim + (size_t)h * hd;
+                double dot = 0.0;
+                for (int d = 0; d < hd; d++) dot += qr[d] * (double)kr[d];
+                double score = dot * scale;
+                scores[kp] = score;
+                if (score > max_score) max_score = score;
+            }
+            double exp_sum = 0.0;
+            for (int kp = 0; kp <= total; kp++) {
+                scores[kp] = exp(scores[kp] - max_score);
+                exp_sum += scores[kp];
+            }
+            for (int d = 0; d < hd; d++) {
+                double sum = 0.0;
+                for (int kp = 0; kp <= total; kp++) {
+                    sum += scores[kp] *
+                           (double)L->cache_v[(size_t)(kp % msl) * kv_dim + (size_t)kvh * hd + d];
+                }
+                attn[(size_t)s * q_dim + (size_t)h * hd + d] = sum / exp_sum;
+            }
+        }
+    }
+    if (attn_out) memcpy(attn_out, attn, (size_t)seq * q_dim * sizeof(double));
+    double* to = (double*)malloc((size_t)d_model * sizeof(double));
+    int8_t* aq = (int8_t*)malloc((size_t)q_dim);
+    for (int s = 0; s < seq; s++) {
+        double* ar = attn + (size_t)s * q_dim;
+        orc_bitnet_rmsnorm_f64(ar, q_dim, L->inner_norm, L->eps);
+        float amax = orc_quant_act_f64(ar, q_dim, aq);
+        matvec_quantized(L->o, aq, amax, simd, workers, to, NULL);
+        for (int i = 0; i < d_model; i++) {
+            if (pre) pre[(size_t)s * d_model + i] = (float)ar[i];
+            post[(size_t)s * d_model + i] = (float)(to[i] + (L->bias_o ? (double)L->bias_o[i] : 0.0));
+        }
+    }
+    L->kv_offset = seq_base + seq;
+    free(aq);
+    free(to);
+    free(scores);
+    free(attn);
+    free(xq);
+    free(tv);
+    free(tk);
+    free(tq);
+    free(Q);
+}
+
+/* One decoder block (poly/transformer_forward.go:228-245) on seq rows of x,
+ * in place: x += MHA(RMSNorm1(x)); x += SwiGLU(RMSNorm2(x)).  Tensor.Add is an
+ * fp32 add (poly/poly.go:481-494). */
+void orc_block_forward(orc_block* B, float* x, int seq, int simd, int workers) {
+    const int n = B->hidden;
+    const size_t cnt = (size_t)seq * n;
+    float* y = (float*)malloc(cnt * sizeof(float));
+    float* o = (float*)malloc(cnt * sizeof(float));
+    orc_rmsnorm_forward(x, seq, n, B->norm1, B->norm_eps, y, NULL);
+    orc_mha_forward(&B->mha, y, seq, simd, workers, NULL, o, NULL, NULL);
+    for (size_t i = 0; i < cnt; i++) x[i] = o[i] + x[i];
+    orc_rmsnorm_forward(x, seq, n, B->norm2, B->norm_eps, y, NULL);
+    const int inter = B->gate->rows;
+    float* h = (float*)malloc((size_t)seq * inter * sizeof(float));
+    orc_swiglu_forward(B->gate, B->up, B->down, NULL, B->ffn_inner_norm, B->ffn_eps,
+                       B->ffn_activation, y, seq, simd, workers, o, h, NULL, NULL, NULL, NULL,
+                       NULL, NULL, NULL);
+    for (size_t i = 0; i < cnt; i++) x[i] = o[i] + x[i];
+    free(h);
+    free(o);
+    free(y);
+}
+
+/* applyFP32LMHeadRows, SIMD off (poly/transformer.go:683-689): sequential fp64. */
+void orc_lm_head_seq(const float* hidden, const float* lm, int vocab, int h, float* logits) {
+#pragma omp parallel for schedule(static)
+    for (int v = 0; v < vocab; v++) {
+        const float* w = lm + (size_t)v * h;
+        double sum = 0.0;
+        for (int d = 0; d < h; d++) sum += (double)hidden[d] * (double)w[d];
+        logits[v] = (float)sum;
+    }
+}
+
+/* DotTile with SIMD on amd64 (poly/simd/avx2_amd64.s:14-79): eight strided
+ * fp64 partials p_l = sum over 8-element chunks of x[8c+l]*w[8c+l] (the
+ * products are exact in fp64, so the FMAs equal multiply-then-add), reduced
+ * as ((p0+p4)+(p2+p6)) + ((p1+p5)+(p3+p7)), plus prev, then the n%8 tail
+ * added in order. */
+double orc_dot_tile(const float* x, const float* w, int n, double prev) {
+    double p[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int i = 0;
+    for (; i + 8 <= n; i += 8) {
+        for (int l = 0; l < 8; l++) p[l] += (double)x[i + l] * (double)w[i + l];
+    }
+    double x0 = p[0] + p[4], x1 = p[1] + p[5];
+    double x2 = p[2] + p[6], x3 = p[3] + p[7];
+    double t0 = x0 + x2, t1 = x1 + x3;
+    double r = (t0 + t1) + prev;
+    for (; i < n; i++) r += (double)x[i] * (double)w[i];
+    return r;
+}
+
+/* applyFP32LMHeadRows with UseSimdForward (poly/transformer.go:679-681). */
+void orc_lm_head_dottile(const float* hidden, const float* lm, int vocab, int h, float* logits) {
+#pragma omp parallel for schedule(static)
+    for (int v = 0; v < vocab; v++) {
+        logits[v] = (float)orc_dot_tile(hidden, lm + (size_t)v * h, h, 0.0);
+    }
+}
+
+/* SampleTopK greedy branch (poly/sampling.go:44-55): first strict maximum. */
+int orc_argmax_first(const float* logits, int n) {
+    int idx = 0;
+    float best = logits[0];
+    for (int i = 0; i < n; i++) {
+        if (logits[i] > best) {
+            best = logits[i];
+            idx = i;
+        }
+    }
+    return idx;
+}

@@ -126,6 +126,42 @@ void orc_swiglu_forward(const orc_matrix* gate, const orc_matrix* up,
 void orc_rmsnorm_forward(const float* x, int rows, int n, const float* gain,
                          double eps, float* y, float* rms_out);
 
+/* ---- attention, decoder block, LM head (poly/mha.go:204-371,
+ *      poly/transformer_forward.go:220-253, poly/transformer.go:635-719,
+ *      poly/simd/avx2_amd64.s:14-79, poly/sampling.go:44-55) ---- */
+typedef struct orc_mha {
+    int d_model, num_heads, num_kv_heads, head_dim, msl;
+    double theta;              /* RoPE base; <= 0 -> 10000 */
+    double eps;                /* inner RMSNorm eps; <= 0 -> 1e-5 */
+    const orc_matrix *q, *k, *v, *o;
+    const float *bias_q, *bias_k, *bias_v, *bias_o; /* NULL -> 0 */
+    const float* inner_norm;   /* NULL -> weight 1 */
+    float* cache_k;            /* msl * kv_dim, caller-owned */
+    float* cache_v;
+    int kv_offset;             /* tokens already cached (in/out) */
+} orc_mha;
+
+void orc_mha_forward(orc_mha* L, const float* in, int seq, int simd, int workers,
+                     float* pre, float* post, double* q_out, double* attn_out);
+
+typedef struct orc_block {
+    int hidden;
+    const float* norm1;
+    const float* norm2;
+    double norm_eps;           /* RMSNorm layers; <= 0 -> 1e-6 */
+    orc_mha mha;
+    const orc_matrix *gate, *up, *down;
+    const float* ffn_inner_norm;
+    double ffn_eps;
+    int ffn_activation;
+} orc_block;
+
+void orc_block_forward(orc_block* B, float* x, int seq, int simd, int workers);
+void orc_lm_head_seq(const float* hidden, const float* lm, int vocab, int h, float* logits);
+double orc_dot_tile(const float* x, const float* w, int n, double prev);
+void orc_lm_head_dottile(const float* hidden, const float* lm, int vocab, int h, float* logits);
+int orc_argmax_first(const float* logits, int n);
+
 /* ---- .entity BITNET_TERNARY blob codec (poly/entity_bitnet.go:38-88) ---- */
 size_t orc_entity_blob_bytes(int n_words);
 size_t orc_entity_encode(int rows, int cols, int offset, float scale, int row_words,

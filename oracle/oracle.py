@@ -76,6 +76,12 @@ def _declare(L: C.CDLL) -> None:
         "orc_swiglu_forward": (None, [P, P, P, P, P, d, i, P, i, i, i,
                                       P, P, P, P, P, P, P, P, P]),
         "orc_rmsnorm_forward": (None, [P, i, i, P, d, P, P]),
+        "orc_mha_forward": (None, [P, P, i, i, i, P, P, P, P]),
+        "orc_block_forward": (None, [P, P, i, i, i]),
+        "orc_lm_head_seq": (None, [P, P, i, i, P]),
+        "orc_dot_tile": (d, [P, P, i, d]),
+        "orc_lm_head_dottile": (None, [P, P, i, i, P]),
+        "orc_argmax_first": (i, [P, i]),
         "orc_entity_blob_bytes": (sz, [i]),
         "orc_entity_encode": (sz, [i, i, i, f, i, P, i, P]),
         "orc_entity_decode_header": (i, [P, sz, P, P, P, P, P, P]),
@@ -380,3 +386,114 @@ def entity_decode(raw: bytes) -> tuple[Matrix, int]:
     words = np.frombuffer(raw, np.uint32, count=n_words, offset=24).copy()
     m = Matrix(rows, cols, scale.value, words)
     return m, offset
+
+
+# ---------------------------------------------------------------- attention, block, LM head
+class _CMatrix(C.Structure):
+    _fields_ = [("rows", C.c_int), ("cols", C.c_int), ("row_words", C.c_int),
+                ("scale", C.c_float), ("words", P), ("codes", P)]
+
+
+class _CMHA(C.Structure):
+    _fields_ = [("d_model", C.c_int), ("num_heads", C.c_int), ("num_kv_heads", C.c_int),
+                ("head_dim", C.c_int), ("msl", C.c_int), ("theta", C.c_double),
+                ("eps", C.c_double), ("q", P), ("k", P), ("v", P), ("o", P),
+                ("bias_q", P), ("bias_k", P), ("bias_v", P), ("bias_o", P),
+                ("inner_norm", P), ("cache_k", P), ("cache_v", P), ("kv_offset", C.c_int)]
+
+
+class _CBlock(C.Structure):
+    _fields_ = [("hidden", C.c_int), ("norm1", P), ("norm2", P), ("norm_eps", C.c_double),
+                ("mha", _CMHA), ("gate", P), ("up", P), ("down", P), ("ffn_inner_norm", P),
+                ("ffn_eps", C.c_double), ("ffn_activation", C.c_int)]
+
+
+def _cmat(m: Matrix, simd: bool) -> _CMatrix:
+    codes = m.ensure_codes() if simd else None
+    return _CMatrix(m.rows, m.cols, m.row_words, m.scale, _p(m.words), _p(codes))
+
+
+class MHA:
+    """MHAForwardPackedTernaryCPU (poly/mha.go:204-371) with its KV ring cache."""
+
+    def __init__(self, q: Matrix, k: Matrix, v: Matrix, o: Matrix, num_heads: int,
+                 num_kv_heads: int, head_dim: int, msl: int, theta: float = 500000.0,
+                 eps: float = 1e-5, inner_norm: np.ndarray | None = None, simd: bool = True):
+        self.mats = (q, k, v, o)
+        self.simd = simd
+        self.d_model = q.cols
+        self.num_heads, self.num_kv_heads, self.head_dim, self.msl = (
+            num_heads, num_kv_heads, head_dim, msl)
+        kv_dim = num_kv_heads * head_dim
+        self.cache_k = np.zeros(msl * kv_dim, np.float32)
+        self.cache_v = np.zeros(msl * kv_dim, np.float32)
+        self.inner_norm = None if inner_norm is None else np.ascontiguousarray(inner_norm, np.float32)
+        self._cm = [_cmat(m, simd) for m in self.mats]
+        self.c = _CMHA(self.d_model, num_heads, num_kv_heads, head_dim, msl, theta, eps,
+                       *(C.cast(C.pointer(cm), P) for cm in self._cm),
+                       None, None, None, None, _p(self.inner_norm), _p(self.cache_k),
+                       _p(self.cache_v), 0)
+
+    @property
+    def kv_offset(self) -> int:
+        return self.c.kv_offset
+
+    def forward(self, x: np.ndarray, workers: int = 0):
+        """Returns (pre, post, q_after_rope, attn_before_norm)."""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, self.d_model)
+        seq = x.shape[0]
+        q_dim = self.num_heads * self.head_dim
+        pre = np.empty((seq, self.d_model), np.float32)
+        post = np.empty((seq, self.d_model), np.float32)
+        q = np.empty((seq, q_dim), np.float64)
+        attn = np.empty((seq, q_dim), np.float64)
+        lib().orc_mha_forward(C.byref(self.c), _p(x), seq, int(self.simd),
+                              workers or (os.cpu_count() or 1), _p(pre), _p(post), _p(q), _p(attn))
+        return pre, post, q, attn
+
+
+class Block:
+    """One decoder block (poly/transformer_forward.go:228-245)."""
+
+    def __init__(self, mha: MHA, norm1: np.ndarray, norm2: np.ndarray, gate: Matrix, up: Matrix,
+                 down: Matrix, ffn_inner_norm: np.ndarray | None = None, norm_eps: float = 1e-5,
+                 ffn_eps: float = 1e-5, ffn_activation: int = ACT_SILU):
+        self.mha = mha
+        self.norm1 = np.ascontiguousarray(norm1, np.float32)
+        self.norm2 = np.ascontiguousarray(norm2, np.float32)
+        self.ffn = (gate, up, down)
+        self._fm = [_cmat(m, mha.simd) for m in self.ffn]
+        self.ffn_inner_norm = (None if ffn_inner_norm is None
+                               else np.ascontiguousarray(ffn_inner_norm, np.float32))
+        self.c = _CBlock(mha.d_model, _p(self.norm1), _p(self.norm2), norm_eps, mha.c,
+                         *(C.cast(C.pointer(cm), P) for cm in self._fm),
+                         _p(self.ffn_inner_norm), ffn_eps, ffn_activation)
+
+    def forward(self, x: np.ndarray, workers: int = 0) -> np.ndarray:
+        x = np.array(x, np.float32, copy=True).reshape(-1, self.mha.d_model)
+        lib().orc_block_forward(C.byref(self.c), _p(x), x.shape[0], int(self.mha.simd),
+                                workers or (os.cpu_count() or 1))
+        self.mha.c.kv_offset = self.c.mha.kv_offset
+        return x
+
+
+def dot_tile(x: np.ndarray, w: np.ndarray, prev: float = 0.0) -> float:
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    return float(lib().orc_dot_tile(_p(x), _p(w), x.size, prev))
+
+
+def lm_head(hidden: np.ndarray, table: np.ndarray, simd: bool = True) -> np.ndarray:
+    """applyFP32LMHeadRows (poly/transformer.go:664-719): DotTile order with SIMD on."""
+    hidden = np.ascontiguousarray(hidden, np.float32)
+    table = np.ascontiguousarray(table, np.float32)
+    vocab = table.size // hidden.size
+    out = np.empty(vocab, np.float32)
+    fn = lib().orc_lm_head_dottile if simd else lib().orc_lm_head_seq
+    fn(_p(hidden), _p(table), vocab, hidden.size, _p(out))
+    return out
+
+
+def argmax_first(logits: np.ndarray) -> int:
+    logits = np.ascontiguousarray(logits, np.float32)
+    return int(lib().orc_argmax_first(_p(logits), logits.size))

@@ -1,0 +1,209 @@
+"""Pins the oracle's attention / block / LM-head restatements (CPU only).
+
+Checks come from loom's own tests where they exist (DotTile order, LM head
+SIMD-vs-scalar bar) and otherwise from what the mathematics fixes: closed
+forms (one cached position, RoPE at position 0), an independent numpy
+formulation (complex rotation for RoPE, matrix softmax attention with GQA
+grouping), and invariants (incremental decode == full-sequence pass).
+Citations are relative to the loom v0.83.0 tree.
+"""
+import math
+
+import numpy as np
+import pytest
+
+
+# ---------------------------------------------------------------- DotTile / LM head
+def avx2_order_reference(x, w, prev):
+    """avx2OrderReference from poly/simd/dot_test.go:14-36 (loom's own spec of
+    the amd64 kernel's order): two 4-lane accumulators over 8-wide blocks."""
+    n = len(x)
+    y0 = [0.0] * 4
+    y1 = [0.0] * 4
+    i = 0
+    while i + 8 <= n:
+        for j in range(4):
+            y0[j] += float(x[i + j]) * float(w[i + j])
+        for j in range(4):
+            y1[j] += float(x[i + 4 + j]) * float(w[i + 4 + j])
+        i += 8
+    s = [y0[j] + y1[j] for j in range(4)]
+    acc = (s[0] + s[2]) + (s[1] + s[3])
+    acc += prev
+    while i < n:
+        acc += float(x[i]) * float(w[i])
+        i += 1
+    return acc
+
+
+def test_dot_tile_matches_loom_avx2_order(orc):
+    # TestDotTileMatchesAVX2Order (poly/simd/dot_test.go:38-60): bit-identical.
+    rng = np.random.default_rng(1)
+    for n in [0, 1, 2, 3, 7, 8, 9, 15, 16, 17, 31, 33, 64, 100, 257, 576, 1000, 1536]:
+        for _ in range(20):
+            x = rng.standard_normal(n).astype(np.float32)
+            w = rng.standard_normal(n).astype(np.float32)
+            prev = float(rng.standard_normal() * 3)
+            got = orc.dot_tile(x, w, prev)
+            want = avx2_order_reference(x, w, prev)
+            assert np.float64(got).tobytes() == np.float64(want).tobytes(), (n, got, want)
+
+
+def test_dot_tile_order_differs_from_sequential(orc):
+    # A case where the tree and the sequential chain round differently, so a
+    # plain sequential implementation cannot pass the test above by accident.
+    x = np.array([1e16, 1, -1e16, 1, 1, 1, 1, 1] * 2, np.float32)
+    w = np.ones(16, np.float32)
+    seq = 0.0
+    for a in x:
+        seq += float(a)
+    assert orc.dot_tile(x, w) != seq
+
+
+def test_lm_head_simd_close_to_scalar(orc):
+    # TestLMHeadFP32SimdMatchesScalar (poly/tests/lmhead_simd_test.go:16-57):
+    # H=320, V=700, SIMD vs scalar within 1e-3; both within fp64 rounding of the exact sums.
+    H, V = 320, 700
+    table = orc.normal_f32(V * H, 3) * np.float32(0.05)
+    hidden = orc.normal_f32(H, 4) * np.float32(0.1)
+    a = orc.lm_head(hidden, table, simd=False)
+    b = orc.lm_head(hidden, table, simd=True)
+    assert np.abs(a - b).max() < 1e-3
+    exact = np.array([math.fsum(float(h) * float(t) for h, t in zip(hidden, table[v * H:(v + 1) * H]))
+                      for v in range(V)], np.float32)
+    assert np.abs(a - exact).max() <= 1e-6 and np.abs(b - exact).max() <= 1e-6
+
+
+def test_argmax_first_strict_max(orc):
+    # SampleTopK greedy (poly/sampling.go:44-55): first strict maximum wins.
+    assert orc.argmax_first(np.array([1, 3, 3, 2], np.float32)) == 1
+    assert orc.argmax_first(np.array([5, 3, 5], np.float32)) == 0
+    assert orc.argmax_first(np.array([np.nan, 3, 9], np.float32)) == 0  # NaN at 0 is never beaten
+    assert orc.argmax_first(np.array([1, np.nan, 9], np.float32)) == 2  # NaN never wins
+    assert orc.argmax_first(np.array([-np.inf, -3], np.float32)) == 1
+
+
+# ---------------------------------------------------------------- MHA
+HID, HEADS, KV, HD, MSL = 128, 4, 2, 32, 64
+
+
+def make_mha(orc, seed=1, simd=True, msl=MSL):
+    q = orc.random_matrix(HEADS * HD, HID, seed=seed)
+    k = orc.random_matrix(KV * HD, HID, seed=seed + 1)
+    v = orc.random_matrix(KV * HD, HID, seed=seed + 2)
+    o = orc.random_matrix(HID, HEADS * HD, seed=seed + 3)
+    wn = orc.uniform_f32(HEADS * HD, 0.5, 1.5, seed=seed + 4)
+    return orc.MHA(q, k, v, o, HEADS, KV, HD, msl, theta=500000.0, eps=1e-5, inner_norm=wn,
+                   simd=simd)
+
+
+def test_mha_single_position_attention_is_v(orc):
+    # One cached position: softmax weight exp(0)/exp(0) = 1 exactly, so the
+    # attention output is float64(V) of that position, head by head (GQA).
+    m = make_mha(orc)
+    x = orc.normal_f32(HID, 7).reshape(1, HID)
+    _, _, _, attn = m.forward(x)
+    v_row = m.cache_v[: KV * HD].astype(np.float64)
+    for h in range(HEADS):
+        kvh = h // (HEADS // KV)
+        assert np.array_equal(attn[0, h * HD:(h + 1) * HD], v_row[kvh * HD:(kvh + 1) * HD])
+
+
+def test_mha_rope_identity_at_position_zero(orc):
+    # angle 0 -> cos 1, sin 0: the cached K row at position 0 is the K
+    # projection itself, i.e. loom's Dense packed path output.
+    m = make_mha(orc)
+    x = orc.normal_f32(HID, 8).reshape(1, HID)
+    m.forward(x)
+    kproj = orc.dense_forward(m.mats[1], x, simd=True).pre[0]
+    assert np.array_equal(m.cache_k[: KV * HD], kproj)
+
+
+def test_mha_rope_matches_complex_rotation(orc):
+    # RoPE (poly/mha.go:292-313) is a rotation of the half-split pairs by
+    # pos / theta^(2d/headDim): compare with numpy complex multiplication.
+    m = make_mha(orc)
+    S = 5
+    x = orc.normal_f32(S * HID, 9).reshape(S, HID)
+    m.forward(x)
+    kproj = orc.dense_forward(m.mats[1], x, simd=True).pre  # before RoPE, fp32
+    half = HD // 2
+    for pos in range(S):
+        got = m.cache_k[pos * KV * HD:(pos + 1) * KV * HD].reshape(KV, HD)
+        raw = kproj[pos].reshape(KV, HD).astype(np.float64)
+        d = np.arange(half)
+        ang = pos / np.power(500000.0, 2 * d / HD)
+        z = (raw[:, :half] + 1j * raw[:, half:]) * np.exp(1j * ang)
+        want = np.concatenate([z.real, z.imag], axis=1).astype(np.float32)
+        assert np.allclose(got, want, rtol=2e-6, atol=1e-7)
+
+
+def test_mha_attention_matches_numpy_softmax(orc):
+    # Independent formulation: softmax(Q K^T / sqrt(hd)) V over the causal cache,
+    # with GQA grouping h -> h // (heads / kv_heads).
+    m = make_mha(orc, seed=11)
+    S = 9
+    x = orc.normal_f32(S * HID, 12).reshape(S, HID)
+    _, _, q, attn = m.forward(x)
+    K = m.cache_k[: S * KV * HD].reshape(S, KV, HD).astype(np.float64)
+    V = m.cache_v[: S * KV * HD].reshape(S, KV, HD).astype(np.float64)
+    for s in range(S):
+        for h in range(HEADS):
+            kvh = h // (HEADS // KV)
+            qh = q[s, h * HD:(h + 1) * HD]
+            sc = K[: s + 1, kvh] @ qh / math.sqrt(HD)
+            p = np.exp(sc - sc.max())
+            want = (p[:, None] * V[: s + 1, kvh]).sum(0) / p.sum()
+            assert np.allclose(attn[s, h * HD:(h + 1) * HD], want, rtol=1e-12, atol=1e-14)
+
+
+def test_mha_incremental_equals_full_pass(orc):
+    # Decoding token by token through the warm KV cache gives the same bits as
+    # one full-sequence pass (poly/mha_layout.go:62-70: seq 1 + warm cache is
+    # incremental, anything else resets).
+    S = 7
+    x = orc.normal_f32(S * HID, 13).reshape(S, HID)
+    full = make_mha(orc, seed=21)
+    pre_f, post_f, _, _ = full.forward(x)
+    inc = make_mha(orc, seed=21)
+    inc.forward(x[:3])
+    outs = []
+    for s in range(3, S):
+        pre_i, post_i, _, _ = inc.forward(x[s:s + 1])
+        outs.append(post_i[0])
+        assert inc.kv_offset == s + 1
+    assert np.array_equal(np.stack(outs), post_f[3:])
+    assert np.array_equal(inc.cache_k, full.cache_k)
+
+
+def test_mha_prefill_resets_cache(orc):
+    m = make_mha(orc, seed=31)
+    x = orc.normal_f32(4 * HID, 32).reshape(4, HID)
+    _, a, _, _ = m.forward(x)
+    _, b, _, _ = m.forward(x)  # seq > 1 resets: same outputs again
+    assert np.array_equal(a, b) and m.kv_offset == 4
+
+
+# ---------------------------------------------------------------- block
+def test_block_is_norm_mha_add_norm_swiglu_add(orc):
+    # forwardOnCPUNormal (poly/transformer_forward.go:228-245) composed from
+    # the separately pinned pieces: bit-identical.
+    S, inter = 6, 256
+    n1 = orc.uniform_f32(HID, 0.5, 1.5, 41)
+    n2 = orc.uniform_f32(HID, 0.5, 1.5, 42)
+    g = orc.random_matrix(inter, HID, 43)
+    u = orc.random_matrix(inter, HID, 44)
+    d = orc.random_matrix(HID, inter, 45)
+    fn = orc.uniform_f32(inter, 0.5, 1.5, 46)
+    blk = orc.Block(make_mha(orc, seed=51), n1, n2, g, u, d, fn)
+    x = orc.normal_f32(S * HID, 47).reshape(S, HID)
+    got = blk.forward(x)
+
+    mha = make_mha(orc, seed=51)
+    y = orc.rmsnorm_forward(x, n1, 1e-5)
+    _, o, _, _ = mha.forward(y)
+    h = (o + x).astype(np.float32)
+    y2 = orc.rmsnorm_forward(h, n2, 1e-5)
+    f = orc.swiglu_forward(g, u, d, y2, inner_norm=fn, eps=1e-5).out
+    want = (f + h).astype(np.float32)
+    assert np.array_equal(got, want)
