@@ -134,6 +134,137 @@ int loom_amd_swiglu_forward(const loom_amd_matrix* gate, const loom_amd_matrix* 
                             const float* residual, float* h_out,
                             const loom_amd_swiglu_taps* taps, void* stream);
 
+/* ---- decoder block (poly/transformer_forward.go:228-245) -------------- */
+
+typedef struct loom_amd_block loom_amd_block;
+
+/* Shape and numerics of one BitNet decoder block:
+ *   x += O(InnerNorm(Attention(RoPE(Q,K,V)(RMSNorm1(x)))))
+ *   x += SwiGLU(RMSNorm2(x))
+ * Sequential fp64 sums of the reference (RMSNorms, inner norms, softmax
+ * sums) follow norm_mode: STRICT adds in the reference's order; FAST uses a
+ * fixed parallel order.  exp/pow/sin/cos are the device libm's (within 1 ulp
+ * of the host's, not bit-identical). */
+typedef struct loom_amd_block_desc {
+    int hidden;         /* d_model */
+    int num_heads;
+    int num_kv_heads;   /* 0 = num_heads; must divide num_heads */
+    int head_dim;       /* multiple of 4, <= 256 */
+    int intermediate;   /* SwiGLU width */
+    int max_seq_len;    /* KV ring rows, loom MaxSeqLen (0 = 512), at most 7424; a call
+                           whose positions would pass it is refused (loom wraps the ring) */
+    int max_batch;      /* independent sequences per call (0 = 1) */
+    double rope_theta;  /* 0 = 10000 */
+    double norm_eps;    /* RMSNorm1/2 eps (<= 0: 1e-6, poly/norm.go:104) */
+    double attn_eps;    /* MHA inner norm eps (<= 0: 1e-5) */
+    double ffn_eps;     /* SwiGLU inner norm eps (<= 0: 1e-5) */
+    int ffn_activation; /* gate activation: 1 SiLU, 6 ReLU2 */
+    int norm_mode;      /* LOOM_AMD_NORM_STRICT or LOOM_AMD_NORM_FAST */
+} loom_amd_block_desc;
+
+/* Weights of one block.  Matrices are copied into the block at create time
+ * (the caller may release them afterwards); the float arrays are HOST
+ * memory, copied at create time. */
+typedef struct loom_amd_block_weights {
+    const loom_amd_matrix* q;    /* q_dim x hidden */
+    const loom_amd_matrix* k;    /* kv_dim x hidden */
+    const loom_amd_matrix* v;    /* kv_dim x hidden */
+    const loom_amd_matrix* o;    /* hidden x q_dim */
+    const loom_amd_matrix* gate; /* intermediate x hidden */
+    const loom_amd_matrix* up;   /* intermediate x hidden */
+    const loom_amd_matrix* down; /* hidden x intermediate */
+    const float* norm1;           /* hidden */
+    const float* norm2;           /* hidden */
+    const float* attn_inner_norm; /* q_dim, NULL = ones */
+    const float* ffn_inner_norm;  /* intermediate, NULL = ones */
+    const float* bias_q;          /* q_dim, optional */
+    const float* bias_k;          /* kv_dim, optional */
+    const float* bias_v;          /* kv_dim, optional */
+    const float* bias_o;          /* hidden, optional */
+} loom_amd_block_weights;
+
+/* Optional device copies of block intermediates (rows = batch*seq). */
+typedef struct loom_amd_block_taps {
+    float* y1;    /* rows x hidden: RMSNorm1 output */
+    double* q;    /* rows x q_dim: Q after bias and RoPE */
+    double* attn; /* rows x q_dim: attention output before the inner norm */
+    float* mid;   /* rows x hidden: x after the attention residual */
+} loom_amd_block_taps;
+
+/* Build a block on device: stacks Q|K|V into one projection, allocates the
+ * KV ring caches (max_batch x max_seq_len x kv_dim fp32, K and V) and the
+ * device position.  Synchronous. */
+int loom_amd_block_create(int device, const loom_amd_block_desc* desc,
+                          const loom_amd_block_weights* w, loom_amd_block** out);
+void loom_amd_block_release(loom_amd_block* b);
+
+/* One block forward on x (DEVICE, batch x seq x hidden fp32, in place).
+ * KV rule of mhaPrepareKVForForward (poly/mha_layout.go:62-70): a call with
+ * seq == 1 on a warm cache continues at the current position; any other
+ * call restarts at position 0.  Each of the batch sequences has its own KV
+ * cache; all of them advance together.  Replaces the block loop body of
+ * forwardOnCPUNormal (poly/transformer_forward.go:228-245) for BitNet layers
+ * (MHAForwardPackedTernaryCPU, poly/mha.go:204-371, and
+ * SwiGLUForwardPackedTernaryCPU, poly/bitnet_cpu.go:915-1002).  May grow the
+ * block's workspace (synchronizing the stream) when rows exceed earlier calls. */
+int loom_amd_block_forward(loom_amd_block* b, float* x, int batch, int seq,
+                           const loom_amd_block_taps* taps, void* stream);
+
+/* Current KV position (loom KVOffset) as the host tracks it. */
+int loom_amd_block_kv_offset(const loom_amd_block* b);
+
+/* Device pointers of the K and V ring of one sequence slot (max_seq_len x kv_dim). */
+int loom_amd_block_kv_cache(const loom_amd_block* b, int slot, const float** k,
+                            const float** v);
+
+/* ---- transformer decode (poly/transformer.go:330-520) ---------------- */
+
+typedef struct loom_amd_model loom_amd_model;
+
+typedef struct loom_amd_model_desc {
+    loom_amd_block_desc block; /* every layer has this shape */
+    int num_layers;
+    int vocab;
+    double final_norm_eps; /* <= 0: 1e-6 */
+    int max_tokens;        /* tokens per sequence the model can hold (prompt + generated) */
+    int max_prefill;       /* largest prompt length per call (0 = max_tokens) */
+} loom_amd_model_desc;
+
+/* Build a model: layers[num_layers] as for loom_amd_block_create, fp32
+ * embeddings (HOST, vocab x hidden), final RMSNorm gain (HOST, hidden, NULL =
+ * no final norm) and fp32 LM head (HOST, vocab x hidden, NULL = tied to the
+ * embeddings, BitNet's weight tying).  All layers share one device position. */
+int loom_amd_model_create(int device, const loom_amd_model_desc* desc,
+                          const loom_amd_block_weights* layers, const float* embeddings,
+                          const float* final_norm, const float* lm_head, loom_amd_model** out);
+void loom_amd_model_release(loom_amd_model* m);
+
+/* Prefill: restart every sequence with batch x n prompt ids (HOST), run the
+ * stack, the final norm and the LM head on each sequence's last row, and
+ * pick the next token greedily (SampleTopK with k<=1, poly/sampling.go:44-55).
+ * logits (DEVICE, batch x vocab) is optional. */
+int loom_amd_model_prefill(loom_amd_model* m, const int32_t* ids, int batch, int n,
+                           float* logits, void* stream);
+
+/* `steps` greedy decode steps: each feeds every sequence's newest token at
+ * the current position, runs the stack, the LM head and the argmax, and
+ * appends the result.  use_graph != 0 replays one captured HIP graph per
+ * step (positions live on the device).  logits (DEVICE, batch x vocab) is
+ * optional and holds the last step's logits. */
+int loom_amd_model_decode(loom_amd_model* m, int steps, int use_graph, float* logits,
+                          void* stream);
+
+/* Copy the tokens of every sequence (HOST, batch x count: prompt then
+ * generated ids).  Synchronous on stream.  count = current position + 1. */
+int loom_amd_model_tokens(const loom_amd_model* m, int32_t* out, int count, void* stream);
+
+/* Current position (tokens fed through the stack per sequence). */
+int loom_amd_model_position(const loom_amd_model* m);
+
+/* Final hidden rows of the last call (DEVICE, batch x hidden: each
+ * sequence's last row after the final norm). */
+const float* loom_amd_model_last_hidden(const loom_amd_model* m);
+
 #ifdef __cplusplus
 }
 #endif

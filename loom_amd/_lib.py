@@ -41,6 +41,31 @@ class SwiGLUTaps(C.Structure):
                 ("hamax", P), ("acc_down", P)]
 
 
+class BlockDesc(C.Structure):
+    """loom_amd_block_desc."""
+    _fields_ = [("hidden", i32), ("num_heads", i32), ("num_kv_heads", i32), ("head_dim", i32),
+                ("intermediate", i32), ("max_seq_len", i32), ("max_batch", i32),
+                ("rope_theta", f64), ("norm_eps", f64), ("attn_eps", f64), ("ffn_eps", f64),
+                ("ffn_activation", i32), ("norm_mode", i32)]
+
+
+class BlockWeights(C.Structure):
+    """loom_amd_block_weights (matrix handles + host fp32 arrays)."""
+    _fields_ = [("q", P), ("k", P), ("v", P), ("o", P), ("gate", P), ("up", P), ("down", P),
+                ("norm1", P), ("norm2", P), ("attn_inner_norm", P), ("ffn_inner_norm", P),
+                ("bias_q", P), ("bias_k", P), ("bias_v", P), ("bias_o", P)]
+
+
+class BlockTaps(C.Structure):
+    _fields_ = [("y1", P), ("q", P), ("attn", P), ("mid", P)]
+
+
+class ModelDesc(C.Structure):
+    """loom_amd_model_desc."""
+    _fields_ = [("block", BlockDesc), ("num_layers", i32), ("vocab", i32),
+                ("final_norm_eps", f64), ("max_tokens", i32), ("max_prefill", i32)]
+
+
 # name -> (restype, argtypes); every symbol declared in include/*.h.
 SIGNATURES = {
     # loom_accel.h (v2 plugin ABI)
@@ -74,6 +99,20 @@ SIGNATURES = {
     "loom_amd_dense_forward": (i32, [P, P, i32, i32, P, P, P, C.POINTER(DenseTaps), P]),
     "loom_amd_swiglu_forward": (i32, [P, P, P, P, P, f64, i32, i32, P, i32, P, P, P,
                                       C.POINTER(SwiGLUTaps), P]),
+    "loom_amd_block_create": (i32, [i32, C.POINTER(BlockDesc), C.POINTER(BlockWeights),
+                                    C.POINTER(P)]),
+    "loom_amd_block_release": (None, [P]),
+    "loom_amd_block_forward": (i32, [P, P, i32, i32, C.POINTER(BlockTaps), P]),
+    "loom_amd_block_kv_offset": (i32, [P]),
+    "loom_amd_block_kv_cache": (i32, [P, i32, C.POINTER(P), C.POINTER(P)]),
+    "loom_amd_model_create": (i32, [i32, C.POINTER(ModelDesc), C.POINTER(BlockWeights), P, P, P,
+                                    C.POINTER(P)]),
+    "loom_amd_model_release": (None, [P]),
+    "loom_amd_model_prefill": (i32, [P, P, i32, i32, P, P]),
+    "loom_amd_model_decode": (i32, [P, i32, i32, P, P]),
+    "loom_amd_model_tokens": (i32, [P, P, i32, P]),
+    "loom_amd_model_position": (i32, [P]),
+    "loom_amd_model_last_hidden": (P, [P]),
 }
 
 

@@ -1,4 +1,5 @@
 // amd_api.hip -- device-resident loom_amd_* entry points (include/loom_accel_amd.h).
+#include "api_util.hpp"
 #include "lamd.hpp"
 #include "loom_accel_amd.h"
 
@@ -8,37 +9,11 @@
 #include <string>
 #include <vector>
 
-struct loom_amd_matrix {
-    lamd::Matrix m;
-};
-
 namespace lamd {
 
 thread_local std::string g_amd_error;
 
-static int fail(const std::string& msg) {
-    g_amd_error = msg;
-    return -1;
-}
-
-static int fail_hip(const char* what, hipError_t e) {
-    return fail(std::string(what) + ": " + hipGetErrorString(e));
-}
-
-// Restores the caller's current device on scope exit.
-struct DeviceGuard {
-    int prev = -1;
-    explicit DeviceGuard(int dev) {
-        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
-        if (prev != dev) (void)hipSetDevice(dev);
-    }
-    ~DeviceGuard() {
-        int cur = -1;
-        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
-    }
-};
-
-static bool is_gfx950(int dev) {
+bool is_gfx950(int dev) {
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return false;
     return strncmp(prop.gcnArchName, "gfx950", 6) == 0;
@@ -89,16 +64,6 @@ void* scratch(int device, size_t bytes, std::string* err) {
     a.bytes = want;
     return a.ptr;
 }
-
-// Bump layout of one call's scratch needs, 256-byte aligned.
-struct Layout {
-    size_t off = 0;
-    size_t take(size_t bytes) {
-        size_t at = off;
-        off += (bytes + 255) & ~(size_t)255;
-        return at;
-    }
-};
 
 static int ld_for(int k) { return pad_cols(k); }
 

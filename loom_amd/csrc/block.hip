@@ -1,0 +1,670 @@
+// block.hip -- gfx950 kernels of loom's BitNet decoder block and decode step
+// (poly/transformer_forward.go:220-253, poly/mha.go:204-371, poly/norm.go:102-138,
+// poly/transformer.go:551-577,635-719, poly/sampling.go:44-55).
+//
+// Sequential fp64 sums of the reference (RMSNorm, inner norms, softmax) have
+// two modes: STRICT reproduces the reference's left-to-right chain (terms are
+// formed in parallel, one lane adds them in order); fast uses a fixed-order
+// tree (deterministic, last-bit differences only).  The KV position of each
+// call is read from device memory so a decode step can be graph-replayed.
+#include "block.hpp"
+#include "device_common.hpp"
+
+namespace lamd {
+
+// ------------------------------------------------------------------------
+// shared: ordered / tree fp64 sum of n terms held in LDS (256 threads)
+// ------------------------------------------------------------------------
+
+template <int STRICT>
+__device__ double lds_sum(const double* terms, int n, double* scratch256) {
+    __shared__ double result;
+    __syncthreads();
+    if (STRICT) {
+        if (threadIdx.x == 0) {
+            // terms must be 16-byte aligned: pairs are read two at a time,
+            // the additions stay in index order
+            const double2* t2 = (const double2*)terms;
+            double s = 0.0;
+            int i = 0;
+            for (; i + 2 <= n; i += 2) {
+                const double2 p = t2[i >> 1];
+                s += p.x;
+                s += p.y;
+            }
+            if (i < n) s += terms[i];
+            result = s;
+        }
+        __syncthreads();
+        return result;
+    }
+    double s = 0.0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) s += terms[i];
+    scratch256[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = blockDim.x >> 1; w > 0; w >>= 1) {
+        if (threadIdx.x < w) scratch256[threadIdx.x] = scratch256[threadIdx.x] + scratch256[threadIdx.x + w];
+        __syncthreads();
+    }
+    const double r = scratch256[0];
+    __syncthreads();
+    return r;
+}
+
+// ------------------------------------------------------------------------
+// RMSNorm layer (poly/norm.go:102-138) fused with the following projection's
+// int8 quantization (poly/bitnet_cpu.go:45-106): one workgroup per row.
+// y = fp32((x / rms) * g), rms = sqrt(sum(x^2)/n + eps).  xq may be null
+// (final norm: y only); y may be null (only the quantized row is needed).
+// ------------------------------------------------------------------------
+
+template <int STRICT, int VPT>
+__global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float* __restrict__ x, long ldx, int n,
+                                                            const float* __restrict__ gain,
+                                                            double eps, float* __restrict__ y,
+                                                            int8_t* __restrict__ xq, int ldq,
+                                                            float* __restrict__ amax_out,
+                                                            int32_t* __restrict__ xsum_out) {
+    extern __shared__ double sq[];  // STRICT: n squares; fast: 256 partials
+    __shared__ double red[256];
+    __shared__ float shf[4];
+    __shared__ int shi[4];
+    const int row = blockIdx.x;
+    const float* xr = x + (size_t)row * ldx;
+    float v[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int i = threadIdx.x + j * 256;
+        v[j] = i < n ? xr[i] : 0.0f;
+    }
+    double total;
+    if (STRICT) {
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int i = threadIdx.x + j * 256;
+            if (i < n) {
+                const double f = (double)v[j];
+                sq[i] = f * f;  // exact: 24-bit significands
+            }
+        }
+        total = lds_sum<1>(sq, n, red);
+    } else {
+        double s = 0.0;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const double f = (double)v[j];
+            s += f * f;
+        }
+        red[threadIdx.x] = s;
+        __syncthreads();
+        for (int w = 128; w > 0; w >>= 1) {
+            if (threadIdx.x < w) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + w];
+            __syncthreads();
+        }
+        total = red[0];
+    }
+    const double rms = sqrt(total / (double)n + eps);
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int i = threadIdx.x + j * 256;
+        if (i < n) {
+            const double normed = (double)v[j] / rms;
+            v[j] = (float)(normed * (double)gain[i]);
+            if (y) y[(size_t)row * n + i] = v[j];
+            m = max_nan_skip(m, fabsf(v[j]));
+        }
+    }
+    if (!xq) return;
+    m = block_max(m, shf);
+    if (m < 1e-5f) m = 1e-5f;
+    const double qs = 127.0 / (double)m;
+    int s = 0;
+    int8_t* qr = xq + (size_t)row * ldq;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int i = threadIdx.x + j * 256;
+        if (i < n) {
+            const int q = quant_one((double)v[j], qs);
+            s += q;
+            qr[i] = (int8_t)q;
+        }
+    }
+    for (int i = n + threadIdx.x; i < ldq; i += 256) qr[i] = 0;
+    s = block_sum_i(s, shi);
+    if (threadIdx.x == 0) {
+        amax_out[row] = m;
+        xsum_out[row] = s;
+    }
+}
+
+template <int STRICT>
+static hipError_t launch_rmsnorm_t(const float* x, long ldx, int m, int n, const float* gain,
+                                   double eps, float* y, int8_t* xq, int ldq, float* amax,
+                                   int32_t* xsum, hipStream_t s) {
+    const size_t shm = STRICT ? (size_t)n * sizeof(double) : 0;
+    const dim3 g(m), b(256);
+    if (n <= 256 * 4) {
+        hipLaunchKernelGGL((rmsnorm_quant_kernel<STRICT, 4>), g, b, shm, s, x, ldx, n, gain, eps, y, xq, ldq, amax, xsum);
+    } else if (n <= 256 * 8) {
+        hipLaunchKernelGGL((rmsnorm_quant_kernel<STRICT, 8>), g, b, shm, s, x, ldx, n, gain, eps, y, xq, ldq, amax, xsum);
+    } else if (n <= 256 * 16) {
+        hipLaunchKernelGGL((rmsnorm_quant_kernel<STRICT, 16>), g, b, shm, s, x, ldx, n, gain, eps, y, xq, ldq, amax, xsum);
+    } else if (n <= 256 * 32) {
+        hipLaunchKernelGGL((rmsnorm_quant_kernel<STRICT, 32>), g, b, shm, s, x, ldx, n, gain, eps, y, xq, ldq, amax, xsum);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_quant(const float* x, long ldx, int m, int n, const float* gain,
+                                double eps, int strict, float* y, int8_t* xq, int ldq, float* amax,
+                                int32_t* xsum, hipStream_t s) {
+    if (m <= 0) return hipSuccess;
+    if (eps <= 0.0) eps = 1e-6;  // RMSNormForwardPolymorphic default
+    if (n > kMaxNormCols || (strict && n > kMaxStrictNormCols)) return hipErrorInvalidValue;
+    return strict ? launch_rmsnorm_t<1>(x, ldx, m, n, gain, eps, y, xq, ldq, amax, xsum, s)
+                  : launch_rmsnorm_t<0>(x, ldx, m, n, gain, eps, y, xq, ldq, amax, xsum, s);
+}
+
+// ------------------------------------------------------------------------
+// Q/K/V epilogue of the stacked projection (poly/mha.go:258-313).  acc holds
+// the int32 accumulators of the stacked [Q; K; V] ternary matrix for `seq`
+// token rows (row stride q_dim + 2*kv_dim).  Per token at position pos:
+//   Q = fp64(acc)*os_q + bias_q (fp64, kept), rotated in fp64;
+//   K = fp32(fp64(acc)*os_k + bias_k), rotated from fp64 back to fp32;
+//   V = fp32(fp64(acc)*os_v + bias_v);
+// RoPE rotates the half-split pairs (d, d + hd/2) by pos / theta^(2d/hd).
+// K and V go to ring row pos % msl of the row's sequence slot (batch index);
+// when one call holds more than msl tokens only the last token of each ring
+// row is written (the reference writes them in order, so the last one
+// stays).  One thread per Q pair, K pair or V element.
+// ------------------------------------------------------------------------
+
+__device__ __forceinline__ void rope_angle(int pos, int d, int hd, double theta, double* c,
+                                           double* sn) {
+    const double angle = (double)pos / pow(theta, (double)(2 * d) / (double)hd);
+    *c = cos(angle);
+    *sn = sin(angle);
+}
+
+__global__ void qkv_rope_kernel(const int32_t* __restrict__ acc, const float* __restrict__ amax,
+                                float sq, float sk, float sv, const float* __restrict__ bq,
+                                const float* __restrict__ bk, const float* __restrict__ bv,
+                                int batch, int seq, const int* __restrict__ pos0, int msl,
+                                int heads, int kv_heads, int hd, double theta,
+                                double* __restrict__ q, float* __restrict__ cache_k,
+                                float* __restrict__ cache_v) {
+    const int half = hd >> 1;
+    const int q_dim = heads * hd, kv_dim = kv_heads * hd;
+    const int qp = heads * half, kp = kv_heads * half;
+    const int per_row = qp + kp + kv_dim;
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long)batch * seq * per_row) return;
+    const int row = (int)(idx / per_row);  // token row b*seq + s
+    const int r = (int)(idx % per_row);
+    const int b = row / seq, s = row % seq;
+    const int base = *pos0;
+    const int pos = base + s;
+    const int32_t* ar = acc + (size_t)row * (q_dim + 2 * kv_dim);
+    const float am = amax[row];
+    cache_k += (size_t)b * msl * kv_dim;
+    cache_v += (size_t)b * msl * kv_dim;
+    const bool latest = pos + msl >= base + seq;
+    if (r < qp) {
+        const int h = r / half, d = r % half;
+        const int j0 = h * hd + d, j1 = j0 + half;
+        const double os = output_scale(sq, am);
+        const double v0 = (double)ar[j0] * os + (bq ? (double)bq[j0] : 0.0);
+        const double v1 = (double)ar[j1] * os + (bq ? (double)bq[j1] : 0.0);
+        double c, sn;
+        rope_angle(pos, d, hd, theta, &c, &sn);
+        double* qr = q + (size_t)row * q_dim;
+        qr[j0] = v0 * c - v1 * sn;
+        qr[j1] = v0 * sn + v1 * c;
+    } else if (r < qp + kp) {
+        const int t = r - qp;
+        const int h = t / half, d = t % half;
+        const int j0 = h * hd + d, j1 = j0 + half;
+        const double os = output_scale(sk, am);
+        const float k0 = (float)((double)ar[q_dim + j0] * os + (bk ? (double)bk[j0] : 0.0));
+        const float k1 = (float)((double)ar[q_dim + j1] * os + (bk ? (double)bk[j1] : 0.0));
+        double c, sn;
+        rope_angle(pos, d, hd, theta, &c, &sn);
+        const double v0 = (double)k0, v1 = (double)k1;
+        if (latest) {
+            float* kr = cache_k + (size_t)(pos % msl) * kv_dim;
+            kr[j0] = (float)(v0 * c - v1 * sn);
+            kr[j1] = (float)(v0 * sn + v1 * c);
+        }
+    } else {
+        const int j = r - qp - kp;
+        const double os = output_scale(sv, am);
+        if (latest) {
+            cache_v[(size_t)(pos % msl) * kv_dim + j] =
+                (float)((double)ar[q_dim + kv_dim + j] * os + (bv ? (double)bv[j] : 0.0));
+        }
+    }
+}
+
+hipError_t launch_qkv_rope(const int32_t* acc, const float* amax, float sq, float sk, float sv,
+                           const float* bq, const float* bk, const float* bv, int batch, int seq,
+                           const int* pos0, int msl, int heads, int kv_heads, int hd, double theta,
+                           double* q, float* cache_k, float* cache_v, hipStream_t s) {
+    const long total =
+        (long)batch * seq * (heads * (hd / 2) + kv_heads * (hd / 2) + kv_heads * hd);
+    if (total <= 0) return hipSuccess;
+    if (hd % 2 != 0) return hipErrorInvalidValue;
+    if (theta <= 0.0) theta = 10000.0;
+    const int threads = 256;
+    hipLaunchKernelGGL(qkv_rope_kernel, dim3((unsigned)((total + threads - 1) / threads)),
+                       dim3(threads), 0, s, acc, amax, sq, sk, sv, bq, bk, bv, batch, seq, pos0,
+                       msl, heads, kv_heads, hd, theta, q, cache_k, cache_v);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------
+// Attention (poly/mha.go:316-354): one 256-thread workgroup per (head, query).
+// scores over positions 0..pos: fp64 dot over d in order, times 1/sqrt(hd);
+// running max from -1e9; exp(score - max); expSum over positions in order;
+// out[d] = sum over positions in order of p*V / expSum.  The GQA group of
+// head h is h / (heads / kv_heads).  Position kp reads ring row kp % msl of
+// the query's sequence slot (blockIdx.z).
+// The scores of one query live in LDS: `span` bounds the number of
+// positions a launch may see; a query past it gets NaN rows (the host
+// checks the span before launching, so this never happens in a valid call).
+// ------------------------------------------------------------------------
+
+template <int STRICT>
+__global__ __launch_bounds__(256) void attention_kernel(const double* __restrict__ q,
+                                                        const float* __restrict__ cache_k,
+                                                        const float* __restrict__ cache_v,
+                                                        const int* __restrict__ pos0, int msl,
+                                                        int span, int heads, int kv_heads, int hd,
+                                                        double* __restrict__ out) {
+    extern __shared__ double lds[];  // q[hd] then scores[span]
+    __shared__ double red[256];
+    const int h = blockIdx.x;
+    const int s = blockIdx.y;
+    const int b = blockIdx.z;
+    const int row = b * gridDim.y + s;
+    const int q_dim = heads * hd, kv_dim = kv_heads * hd;
+    const int kvh = h / (heads / kv_heads);
+    const int L = *pos0 + s + 1;  // positions 0..pos0+s
+    cache_k += (size_t)b * msl * kv_dim;
+    cache_v += (size_t)b * msl * kv_dim;
+    double* orow = out + (size_t)row * q_dim + (size_t)h * hd;
+    if (L > span) {
+        for (int d = threadIdx.x; d < hd; d += 256) orow[d] = __builtin_nan("");
+        return;
+    }
+    double* qs = lds;
+    double* scores = lds + ((hd + 1) & ~1);  // 16-byte aligned
+    const double* qrow = q + (size_t)row * q_dim + (size_t)h * hd;
+    for (int d = threadIdx.x; d < hd; d += 256) qs[d] = qrow[d];
+    __syncthreads();
+    const double scale = 1.0 / sqrt((double)hd);
+    double local_max = -1e9;
+    for (int kp = threadIdx.x; kp < L; kp += 256) {
+        const float* kr = cache_k + (size_t)(kp % msl) * kv_dim + (size_t)kvh * hd;
+        double dot = 0.0;
+        for (int d = 0; d < hd; d += 4) {
+            const float4 k4 = *(const float4*)(kr + d);
+            dot += qs[d] * (double)k4.x;
+            dot += qs[d + 1] * (double)k4.y;
+            dot += qs[d + 2] * (double)k4.z;
+            dot += qs[d + 3] * (double)k4.w;
+        }
+        const double sc = dot * scale;
+        scores[kp] = sc;
+        if (sc > local_max) local_max = sc;
+    }
+    // the maximum is exact in any order; NaN never replaces it
+    red[threadIdx.x] = local_max;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (threadIdx.x < w) {
+            const double o = red[threadIdx.x + w];
+            if (o > red[threadIdx.x]) red[threadIdx.x] = o;
+        }
+        __syncthreads();
+    }
+    const double mx = red[0];
+    for (int kp = threadIdx.x; kp < L; kp += 256) scores[kp] = exp(scores[kp] - mx);
+    const double exp_sum = lds_sum<STRICT>(scores, L, red);
+    const float* vbase = cache_v + (size_t)kvh * hd;
+    if (STRICT) {
+        // one lane per d sums its column in position order
+        for (int d = threadIdx.x; d < hd; d += 256) {
+            double sum = 0.0;
+            for (int kp = 0; kp < L; ++kp) sum += scores[kp] * (double)vbase[(size_t)(kp % msl) * kv_dim + d];
+            orow[d] = sum / exp_sum;
+        }
+    } else {
+        // 256 threads = (256 / hd) position slices x hd columns, slices then
+        // combined in slice order
+        const int slices = 256 / hd;
+        const int d = threadIdx.x % hd;
+        const int sl = threadIdx.x / hd;
+        double sum = 0.0;
+        if (sl < slices) {
+            for (int kp = sl; kp < L; kp += slices) sum += scores[kp] * (double)vbase[(size_t)(kp % msl) * kv_dim + d];
+        }
+        red[threadIdx.x] = sum;
+        __syncthreads();
+        if (threadIdx.x < hd) {
+            double t = red[threadIdx.x];
+            for (int k = 1; k < slices; ++k) t = t + red[k * hd + threadIdx.x];
+            orow[threadIdx.x] = t / exp_sum;
+        }
+    }
+}
+
+// LDS bytes of one attention workgroup for `span` positions.
+size_t attention_lds_bytes(int hd, int span) {
+    return ((size_t)((hd + 1) & ~1) + (size_t)span) * sizeof(double);
+}
+
+hipError_t launch_attention(const double* q, const float* cache_k, const float* cache_v,
+                            int batch, int seq, const int* pos0, int msl, int span, int heads,
+                            int kv_heads, int hd, int strict, double* out, hipStream_t s) {
+    if (seq <= 0 || batch <= 0) return hipSuccess;
+    if (hd % 4 != 0 || hd > 256 || kv_heads <= 0 || heads % kv_heads != 0) return hipErrorInvalidValue;
+    const size_t shm = attention_lds_bytes(hd, span);
+    if (shm > kMaxAttnLds) return hipErrorInvalidValue;
+    const dim3 grid(heads, seq, batch);
+    if (strict) {
+        hipLaunchKernelGGL(attention_kernel<1>, grid, dim3(256), shm, s, q, cache_k, cache_v, pos0,
+                           msl, span, heads, kv_heads, hd, out);
+    } else {
+        hipLaunchKernelGGL(attention_kernel<0>, grid, dim3(256), shm, s, q, cache_k, cache_v, pos0,
+                           msl, span, heads, kv_heads, hd, out);
+    }
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------
+// MHA inner norm on fp64 rows (bitNetRMSNormFloat64Weighted,
+// poly/bitnet_cpu.go:868-887: data *= scale*w) + fp64 requantization
+// (bitNetQuantizeActivationFloat64, poly/bitnet_cpu.go:59-71,108-117).
+// pre (optional) receives fp32(normalized), loom's MHA preAct.
+// ------------------------------------------------------------------------
+
+template <int STRICT, int VPT>
+__global__ __launch_bounds__(256) void norm_quant_f64_kernel(double* __restrict__ a, int n,
+                                                             const float* __restrict__ weight,
+                                                             double eps, float* __restrict__ pre,
+                                                             int8_t* __restrict__ xq, int ldq,
+                                                             float* __restrict__ amax_out,
+                                                             int32_t* __restrict__ xsum_out) {
+    extern __shared__ double sq[];
+    __shared__ double red[256];
+    __shared__ float shf[4];
+    __shared__ int shi[4];
+    const int row = blockIdx.x;
+    double* ar = a + (size_t)row * n;
+    double v[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int i = threadIdx.x + j * 256;
+        v[j] = i < n ? ar[i] : 0.0;
+    }
+    double total;
+    if (STRICT) {
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int i = threadIdx.x + j * 256;
+            if (i < n) sq[i] = v[j] * v[j];
+        }
+        total = lds_sum<1>(sq, n, red);
+    } else {
+        double s = 0.0;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) s += v[j] * v[j];
+        red[threadIdx.x] = s;
+        __syncthreads();
+        for (int w = 128; w > 0; w >>= 1) {
+            if (threadIdx.x < w) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + w];
+            __syncthreads();
+        }
+        total = red[0];
+    }
+    const double scale = 1.0 / sqrt(total / (double)n + eps);
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int i = threadIdx.x + j * 256;
+        if (i < n) {
+            const double w = weight ? (double)weight[i] : 1.0;
+            v[j] = v[j] * (scale * w);
+            ar[i] = v[j];
+            if (pre) pre[(size_t)row * n + i] = (float)v[j];
+            m = max_nan_skip(m, (float)fabs(v[j]));
+        }
+    }
+    m = block_max(m, shf);
+    if (m < 1e-5f) m = 1e-5f;
+    const double qs = 127.0 / (double)m;
+    int s = 0;
+    int8_t* qr = xq + (size_t)row * ldq;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int i = threadIdx.x + j * 256;
+        if (i < n) {
+            const int q = quant_one(v[j], qs);
+            s += q;
+            qr[i] = (int8_t)q;
+        }
+    }
+    for (int i = n + threadIdx.x; i < ldq; i += 256) qr[i] = 0;
+    s = block_sum_i(s, shi);
+    if (threadIdx.x == 0) {
+        amax_out[row] = m;
+        xsum_out[row] = s;
+    }
+}
+
+template <int STRICT>
+static hipError_t launch_norm_f64_t(double* a, int m, int n, const float* w, double eps, float* pre,
+                                    int8_t* xq, int ldq, float* amax, int32_t* xsum, hipStream_t s) {
+    const size_t shm = STRICT ? (size_t)n * sizeof(double) : 0;
+    const dim3 g(m), b(256);
+    if (n <= 256 * 4) {
+        hipLaunchKernelGGL((norm_quant_f64_kernel<STRICT, 4>), g, b, shm, s, a, n, w, eps, pre, xq, ldq, amax, xsum);
+    } else if (n <= 256 * 8) {
+        hipLaunchKernelGGL((norm_quant_f64_kernel<STRICT, 8>), g, b, shm, s, a, n, w, eps, pre, xq, ldq, amax, xsum);
+    } else if (n <= 256 * 16) {
+        hipLaunchKernelGGL((norm_quant_f64_kernel<STRICT, 16>), g, b, shm, s, a, n, w, eps, pre, xq, ldq, amax, xsum);
+    } else if (n <= 256 * 32) {
+        hipLaunchKernelGGL((norm_quant_f64_kernel<STRICT, 32>), g, b, shm, s, a, n, w, eps, pre, xq, ldq, amax, xsum);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_norm_quant_f64(double* a, int m, int n, const float* w, double eps, int strict,
+                                 float* pre, int8_t* xq, int ldq, float* amax, int32_t* xsum,
+                                 hipStream_t s) {
+    if (m <= 0) return hipSuccess;
+    if (eps <= 0.0) eps = 1e-5;  // bitNetRMSNormFloat64Weighted default
+    if (n > kMaxNormCols || (strict && n > kMaxStrictNormCols)) return hipErrorInvalidValue;
+    return strict ? launch_norm_f64_t<1>(a, m, n, w, eps, pre, xq, ldq, amax, xsum, s)
+                  : launch_norm_f64_t<0>(a, m, n, w, eps, pre, xq, ldq, amax, xsum, s);
+}
+
+// ------------------------------------------------------------------------
+// embeddings (poly/transformer.go:551-577): rows of the fp32 table; an id
+// outside the table gives a zero row.
+// ------------------------------------------------------------------------
+
+__global__ void embed_kernel(const float* __restrict__ table, int vocab, int hidden,
+                             const int* __restrict__ tokens, int cap, const int* __restrict__ pos0,
+                             int batch, int seq, float* __restrict__ out) {
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long)batch * seq * hidden) return;
+    const int r = (int)(idx / hidden);  // token row b*seq + s
+    const int c = (int)(idx % hidden);
+    const int b = r / seq, s = r % seq;
+    const int p = (pos0 ? *pos0 : 0) + s;
+    const int id = p < cap ? tokens[(size_t)b * cap + p] : -1;
+    out[idx] = (id >= 0 && id < vocab) ? table[(size_t)id * hidden + c] : 0.0f;
+}
+
+hipError_t launch_embed(const float* table, int vocab, int hidden, const int* tokens, int cap,
+                        const int* pos0, int batch, int seq, float* out, hipStream_t s) {
+    const long total = (long)batch * seq * hidden;
+    if (total <= 0) return hipSuccess;
+    hipLaunchKernelGGL(embed_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, table,
+                       vocab, hidden, tokens, cap, pos0, batch, seq, out);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------
+// fp32 LM head in loom's amd64 DotTile order (poly/simd/avx2_amd64.s:14-79):
+// for each logit, eight fp64 lane partials p_l over the 8-column chunks in
+// chunk order, then ((p0+p4)+(p2+p6)) + ((p1+p5)+(p3+p7)) + 0, then the n%8
+// tail in order.  A workgroup owns 32 logits x 8 lanes; each 256-column slab
+// of its 32 table rows is staged through LDS with coalesced loads so every
+// lane still consumes its chunks in order.
+// ------------------------------------------------------------------------
+
+constexpr int kLmRows = 32;
+constexpr int kLmSlab = 256;  // columns per LDS slab
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void lm_head_kernel(const float* __restrict__ table, int vocab,
+                                                      int hidden, const float* __restrict__ x,
+                                                      float* __restrict__ logits) {
+    __shared__ float slab[kLmRows][kLmSlab + 4];
+    extern __shared__ float xs[];  // hidden
+    const int tid = threadIdx.x;
+    const int v0 = blockIdx.x * kLmRows;
+    x += (size_t)blockIdx.y * hidden;
+    logits += (size_t)blockIdx.y * vocab;
+    for (int i = tid; i < hidden; i += 256) xs[i] = x[i];
+    const int row = tid >> 3;   // logit within the workgroup
+    const int lane = tid & 7;   // DotTile lane
+    const int full = (hidden / 8) * 8;
+    double p = 0.0;
+    for (int c0 = 0; c0 < full; c0 += kLmSlab) {
+        const int width = min(kLmSlab, full - c0);
+        __syncthreads();
+        // coalesced slab load: kLmRows rows x width columns, 4 columns a thread
+#pragma unroll
+        for (int it = 0; it < kLmRows * (kLmSlab / 4) / 256; ++it) {
+            const int i = tid + it * 256;
+            const int r = i / (kLmSlab / 4);
+            const int c4 = (i % (kLmSlab / 4)) * 4;
+            const int v = min(v0 + r, vocab - 1);
+            if (c4 < width) {
+                const float* src = table + (size_t)v * hidden + c0 + c4;
+                if (VEC) {
+                    *(float4*)&slab[r][c4] = *(const float4*)src;
+                } else {
+                    slab[r][c4] = src[0];
+                    slab[r][c4 + 1] = src[1];
+                    slab[r][c4 + 2] = src[2];
+                    slab[r][c4 + 3] = src[3];
+                }
+            }
+        }
+        __syncthreads();
+        for (int c = lane; c < width; c += 8) p += (double)xs[c0 + c] * (double)slab[row][c];
+    }
+    // lanes 0..3: x_l = p_l + p_{l+4}; lanes 0,1: t0 = x0 + x2, t1 = x1 + x3
+    const double p4 = __shfl_down(p, 4, 8);
+    const double xl = p + p4;
+    const double x2 = __shfl_down(xl, 2, 8);
+    const double t = xl + x2;
+    const double t1 = __shfl_down(t, 1, 8);
+    if (lane == 0) {
+        double r = (t + t1) + 0.0;
+        const float* w = table + (size_t)min(v0 + row, vocab - 1) * hidden;
+        for (int i = full; i < hidden; ++i) r += (double)xs[i] * (double)w[i];
+        if (v0 + row < vocab) logits[v0 + row] = (float)r;
+    }
+}
+
+hipError_t launch_lm_head(const float* table, int vocab, int hidden, const float* x, int rows,
+                          float* logits, hipStream_t s) {
+    if (vocab <= 0 || hidden <= 0 || rows <= 0) return hipSuccess;
+    const size_t shm = (size_t)hidden * sizeof(float);
+    if (shm > 64 * 1024) return hipErrorInvalidValue;
+    const dim3 g((unsigned)ceil_div(vocab, kLmRows), rows), b(256);
+    if (hidden % 4 == 0 && ((uintptr_t)table & 15) == 0) {
+        hipLaunchKernelGGL(lm_head_kernel<true>, g, b, shm, s, table, vocab, hidden, x, logits);
+    } else {
+        hipLaunchKernelGGL(lm_head_kernel<false>, g, b, shm, s, table, vocab, hidden, x, logits);
+    }
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------
+// greedy SampleTopK (poly/sampling.go:44-55): first strict maximum.  Equal to
+// the smallest index holding the largest non-NaN value, except that a NaN at
+// index 0 is never replaced.  One 1024-thread workgroup.
+// ------------------------------------------------------------------------
+
+__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ logits, int n,
+                                                      int* __restrict__ tokens, int cap,
+                                                      const int* __restrict__ pos0, int offset) {
+    __shared__ float bv[1024];
+    __shared__ int bi[1024];
+    logits += (size_t)blockIdx.x * n;
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = threadIdx.x; i < n; i += 1024) {
+        const float v = logits[i];
+        if (v > best || (v == best && i < idx)) {
+            best = v;
+            idx = i;
+        }
+    }
+    bv[threadIdx.x] = best;
+    bi[threadIdx.x] = idx;
+    __syncthreads();
+    for (int w = 512; w > 0; w >>= 1) {
+        if (threadIdx.x < w) {
+            const float o = bv[threadIdx.x + w];
+            const int oi = bi[threadIdx.x + w];
+            if (o > bv[threadIdx.x] || (o == bv[threadIdx.x] && oi < bi[threadIdx.x])) {
+                bv[threadIdx.x] = o;
+                bi[threadIdx.x] = oi;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const float first = logits[0];
+        int r = bi[0];
+        if (first != first || r == 0x7fffffff) r = 0;  // NaN at 0, or nothing comparable
+        const int p = (pos0 ? *pos0 : 0) + offset;
+        if (p < cap) tokens[(size_t)blockIdx.x * cap + p] = r;
+    }
+}
+
+hipError_t launch_argmax(const float* logits, int n, int rows, int* tokens, int cap,
+                         const int* pos0, int offset, hipStream_t s) {
+    if (n <= 0 || rows <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(1024), 0, s, logits, n, tokens, cap, pos0,
+                       offset);
+    return hipGetLastError();
+}
+
+// position bookkeeping on the device (graph-replayable)
+__global__ void set_int_kernel(int* p, int v) { *p = v; }
+__global__ void add_int_kernel(int* p, int v) { *p += v; }
+
+hipError_t launch_set_int(int* p, int v, hipStream_t s) {
+    hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, s, p, v);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_int(int* p, int v, hipStream_t s) {
+    hipLaunchKernelGGL(add_int_kernel, dim3(1), dim3(1), 0, s, p, v);
+    return hipGetLastError();
+}
+
+}  // namespace lamd

@@ -1,0 +1,63 @@
+// block.hpp -- launchers of the decoder-block and decode-step kernels (block.hip).
+//
+// Device positions: every kernel that depends on the KV position reads it from
+// an int in device memory (pos0), so a captured decode step replays unchanged
+// while the position advances on the device.
+#pragma once
+
+#include "lamd.hpp"
+
+namespace lamd {
+
+constexpr size_t kMaxAttnLds = 60 * 1024;  // dynamic LDS of one attention workgroup (q row + scores)
+constexpr int kMaxAttnSpan = 7424;         // positions: (60 KiB / 8) - 256
+
+// RMSNormForwardPolymorphic (poly/norm.go:102-138) on m rows of n, optionally
+// followed by the int8 quantization of the normalized row.  y and xq may each
+// be null.  eps <= 0 selects the reference default 1e-6.
+// x rows are ldx floats apart; y rows are dense (n).
+hipError_t launch_rmsnorm_quant(const float* x, long ldx, int m, int n, const float* gain,
+                                double eps, int strict, float* y, int8_t* xq, int ldq, float* amax,
+                                int32_t* xsum, hipStream_t s);
+
+// Rescale + bias + RoPE of the stacked Q/K/V accumulators (batch*seq rows of
+// q_dim + 2*kv_dim int32): Q rows to q (fp64, rows x q_dim), K/V rows into
+// the fp32 ring caches (batch slots of msl x kv_dim) at positions *pos0 + s.
+hipError_t launch_qkv_rope(const int32_t* acc, const float* amax, float sq, float sk, float sv,
+                           const float* bq, const float* bk, const float* bv, int batch, int seq,
+                           const int* pos0, int msl, int heads, int kv_heads, int hd, double theta,
+                           double* q, float* cache_k, float* cache_v, hipStream_t s);
+
+// Causal attention of batch x seq queries at positions *pos0 + s over each
+// sequence's ring cache.  span >= *pos0 + seq must hold (LDS holds span scores).
+size_t attention_lds_bytes(int hd, int span);
+hipError_t launch_attention(const double* q, const float* cache_k, const float* cache_v,
+                            int batch, int seq, const int* pos0, int msl, int span, int heads,
+                            int kv_heads, int hd, int strict, double* out, hipStream_t s);
+
+// MHA inner norm on fp64 rows in place (data *= scale*w) + fp64 requantization.
+// pre (optional) receives fp32 of the normalized rows.  eps <= 0 selects 1e-5.
+hipError_t launch_norm_quant_f64(double* a, int m, int n, const float* w, double eps, int strict,
+                                 float* pre, int8_t* xq, int ldq, float* amax, int32_t* xsum,
+                                 hipStream_t s);
+
+// Embedding rows of batch x seq tokens: row (b, s) takes the id at
+// tokens[b*cap + *pos0 + s] (pos0 null = 0); ids outside the table give zero
+// rows (poly/transformer.go:563-577).
+hipError_t launch_embed(const float* table, int vocab, int hidden, const int* tokens, int cap,
+                        const int* pos0, int batch, int seq, float* out, hipStream_t s);
+
+// fp32 LM head over `rows` hidden rows (row stride hidden) in loom's amd64
+// DotTile order; logits rows are vocab apart.
+hipError_t launch_lm_head(const float* table, int vocab, int hidden, const float* x, int rows,
+                          float* logits, hipStream_t s);
+
+// Greedy sampling per logits row b: first strict maximum (index 0 when
+// logits[0] is NaN), written to tokens[b*cap + *pos0 + offset] when < cap.
+hipError_t launch_argmax(const float* logits, int n, int rows, int* tokens, int cap,
+                         const int* pos0, int offset, hipStream_t s);
+
+hipError_t launch_set_int(int* p, int v, hipStream_t s);
+hipError_t launch_add_int(int* p, int v, hipStream_t s);
+
+}  // namespace lamd

@@ -1,0 +1,733 @@
+// block_api.hip -- loom_amd_block_* and loom_amd_model_* entry points
+// (include/loom_accel_amd.h): one BitNet decoder block, and the greedy
+// decode loop of a stack of them, device-resident end to end.
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "api_util.hpp"
+#include "block.hpp"
+#include "lamd.hpp"
+#include "loom_accel_amd.h"
+
+namespace lamd {
+
+// Device state of one block.  Every buffer is owned by the block.
+struct BlockDev {
+    int device = 0;
+    int hidden = 0, heads = 0, kv_heads = 0, hd = 0, inter = 0, msl = 0, max_batch = 1;
+    int q_dim = 0, kv_dim = 0;
+    double theta = 10000.0, norm_eps = 0.0, attn_eps = 0.0, ffn_eps = 0.0;
+    int activation = 1, strict = 1;
+    Matrix qkv, o, gate, up, down;  // tiles point into `weights`
+    float sq = 1.0f, sk = 1.0f, sv = 1.0f;
+    float *norm1 = nullptr, *norm2 = nullptr, *attn_norm = nullptr, *ffn_norm = nullptr;
+    float *bq = nullptr, *bk = nullptr, *bv = nullptr, *bo = nullptr;
+    float *cache_k = nullptr, *cache_v = nullptr;  // max_batch x msl x kv_dim
+    void* weights = nullptr;
+    void* params = nullptr;
+    void* caches = nullptr;
+
+    int span() const { return msl; }
+    size_t cache_slot() const { return (size_t)msl * kv_dim; }
+};
+
+// Per-call intermediates for `rows` token rows.
+struct Workspace {
+    void* base = nullptr;
+    size_t bytes = 0;
+    int rows = 0;
+    int8_t* xq = nullptr;  // rows x pad(hidden)
+    float* amax = nullptr;
+    int32_t* xsum = nullptr;
+    int32_t* acc = nullptr;  // rows x (q_dim + 2 kv_dim)
+    double* q = nullptr;     // rows x q_dim
+    double* attn = nullptr;  // rows x q_dim
+    int8_t* aq = nullptr;    // rows x pad(q_dim)
+    float* amax2 = nullptr;
+    int32_t* xsum2 = nullptr;
+    float* h = nullptr;      // rows x inter
+    int8_t* hq = nullptr;    // rows x pad(inter)
+    float* amax3 = nullptr;
+    int32_t* xsum3 = nullptr;
+};
+
+static size_t workspace_layout(const BlockDev& B, int rows, Workspace* W, char* base) {
+    Layout L;
+    const size_t r = (size_t)rows;
+    const size_t o_xq = L.take(r * pad_cols(B.hidden));
+    const size_t o_am = L.take(r * 4);
+    const size_t o_xs = L.take(r * 4);
+    const size_t o_acc = L.take(r * (B.q_dim + 2 * B.kv_dim) * 4);
+    const size_t o_q = L.take(r * B.q_dim * 8);
+    const size_t o_at = L.take(r * B.q_dim * 8);
+    const size_t o_aq = L.take(r * pad_cols(B.q_dim));
+    const size_t o_am2 = L.take(r * 4);
+    const size_t o_xs2 = L.take(r * 4);
+    const size_t o_h = L.take(r * B.inter * 4);
+    const size_t o_hq = L.take(r * pad_cols(B.inter));
+    const size_t o_am3 = L.take(r * 4);
+    const size_t o_xs3 = L.take(r * 4);
+    if (W && base) {
+        W->base = base;
+        W->bytes = L.off;
+        W->rows = rows;
+        W->xq = (int8_t*)(base + o_xq);
+        W->amax = (float*)(base + o_am);
+        W->xsum = (int32_t*)(base + o_xs);
+        W->acc = (int32_t*)(base + o_acc);
+        W->q = (double*)(base + o_q);
+        W->attn = (double*)(base + o_at);
+        W->aq = (int8_t*)(base + o_aq);
+        W->amax2 = (float*)(base + o_am2);
+        W->xsum2 = (int32_t*)(base + o_xs2);
+        W->h = (float*)(base + o_h);
+        W->hq = (int8_t*)(base + o_hq);
+        W->amax3 = (float*)(base + o_am3);
+        W->xsum3 = (int32_t*)(base + o_xs3);
+    }
+    return L.off;
+}
+
+static int alloc_workspace(const BlockDev& B, int rows, Workspace* W) {
+    const size_t bytes = workspace_layout(B, rows, nullptr, nullptr);
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) return fail_hip("block workspace", e);
+    workspace_layout(B, rows, W, (char*)p);
+    return 0;
+}
+
+static void free_workspace(Workspace* W) {
+    if (W->base) (void)hipFree(W->base);
+    *W = Workspace{};
+}
+
+static void free_block(BlockDev* B) {
+    if (B->weights) (void)hipFree(B->weights);
+    if (B->params) (void)hipFree(B->params);
+    if (B->caches) (void)hipFree(B->caches);
+    B->weights = B->params = B->caches = nullptr;
+}
+
+static int check_desc(const loom_amd_block_desc* d) {
+    if (!d) return fail("block desc is null");
+    if (d->hidden <= 0 || d->num_heads <= 0 || d->head_dim <= 0 || d->intermediate <= 0) {
+        return fail("block desc: hidden, num_heads, head_dim and intermediate must be positive");
+    }
+    const int kvh = d->num_kv_heads > 0 ? d->num_kv_heads : d->num_heads;
+    if (d->num_heads % kvh != 0) return fail("block desc: num_kv_heads must divide num_heads");
+    if (d->head_dim % 4 != 0 || d->head_dim > 256) {
+        return fail("block desc: head_dim must be a multiple of 4 and at most 256");
+    }
+    const int msl = d->max_seq_len > 0 ? d->max_seq_len : 512;
+    if (msl > kMaxAttnSpan) {
+        return fail("block desc: max_seq_len is limited to " + std::to_string(kMaxAttnSpan));
+    }
+    if (d->max_batch < 0) return fail("block desc: max_batch must be >= 0");
+    const int strict = d->norm_mode == LOOM_AMD_NORM_STRICT;
+    const int q_dim = d->num_heads * d->head_dim;
+    const int widest = d->hidden > q_dim ? (d->hidden > d->intermediate ? d->hidden : d->intermediate)
+                                         : (q_dim > d->intermediate ? q_dim : d->intermediate);
+    if (widest > kMaxNormCols || (strict && widest > kMaxStrictNormCols)) {
+        return fail("block desc: normalized widths are limited to 8192 (strict: 8064)");
+    }
+    if ((q_dim % kTileRows) != 0 || ((kvh * d->head_dim) % kTileRows) != 0) {
+        return fail("block desc: q_dim and kv_dim must be multiples of 16");
+    }
+    return 0;
+}
+
+static int expect_shape(const loom_amd_matrix* w, const char* name, int rows, int cols, int dev) {
+    if (w == nullptr || w->m.tiles == nullptr) return fail(std::string(name) + " matrix is null");
+    if (w->m.rows != rows || w->m.cols != cols) {
+        return fail(std::string(name) + " matrix is " + std::to_string(w->m.rows) + "x" +
+                    std::to_string(w->m.cols) + ", want " + std::to_string(rows) + "x" +
+                    std::to_string(cols));
+    }
+    if (w->m.device != dev) return fail(std::string(name) + " matrix is on another device");
+    return 0;
+}
+
+// Builds the device state of one block (synchronous).
+static int build_block(int device, const loom_amd_block_desc* d, const loom_amd_block_weights* w,
+                       BlockDev* B) {
+    if (check_desc(d)) return -1;
+    if (!w) return fail("block weights are null");
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev) {
+        return fail("device " + std::to_string(device) + " is not visible");
+    }
+    if (!is_gfx950(device)) return fail("device is not gfx950");
+    B->device = device;
+    B->hidden = d->hidden;
+    B->heads = d->num_heads;
+    B->kv_heads = d->num_kv_heads > 0 ? d->num_kv_heads : d->num_heads;
+    B->hd = d->head_dim;
+    B->inter = d->intermediate;
+    B->msl = d->max_seq_len > 0 ? d->max_seq_len : 512;
+    B->max_batch = d->max_batch > 0 ? d->max_batch : 1;
+    B->q_dim = B->heads * B->hd;
+    B->kv_dim = B->kv_heads * B->hd;
+    B->theta = d->rope_theta > 0 ? d->rope_theta : 10000.0;
+    B->norm_eps = d->norm_eps;
+    B->attn_eps = d->attn_eps;
+    B->ffn_eps = d->ffn_eps;
+    B->activation = d->ffn_activation;
+    B->strict = d->norm_mode == LOOM_AMD_NORM_STRICT;
+    const int H = B->hidden;
+    if (expect_shape(w->q, "q", B->q_dim, H, device) || expect_shape(w->k, "k", B->kv_dim, H, device) ||
+        expect_shape(w->v, "v", B->kv_dim, H, device) || expect_shape(w->o, "o", H, B->q_dim, device) ||
+        expect_shape(w->gate, "gate", B->inter, H, device) ||
+        expect_shape(w->up, "up", B->inter, H, device) ||
+        expect_shape(w->down, "down", H, B->inter, device)) {
+        return -1;
+    }
+    if (!w->norm1 || !w->norm2) return fail("norm1 and norm2 gains are required");
+    DeviceGuard guard(device);
+
+    // weights: stacked [Q; K; V] then O, gate, up, down, each 256-byte aligned
+    Layout L;
+    const size_t o_qkv = L.take(w->q->m.bytes() + w->k->m.bytes() + w->v->m.bytes());
+    const size_t o_o = L.take(w->o->m.bytes());
+    const size_t o_g = L.take(w->gate->m.bytes());
+    const size_t o_u = L.take(w->up->m.bytes());
+    const size_t o_d = L.take(w->down->m.bytes());
+    hipError_t e = hipMalloc(&B->weights, L.off);
+    if (e != hipSuccess) return fail_hip("block weights", e);
+    char* wb = (char*)B->weights;
+    size_t at = o_qkv;
+    for (const loom_amd_matrix* m : {w->q, w->k, w->v}) {
+        if (e == hipSuccess) e = hipMemcpy(wb + at, m->m.tiles, m->m.bytes(), hipMemcpyDeviceToDevice);
+        at += m->m.bytes();
+    }
+    auto place = [&](Matrix* dst, const loom_amd_matrix* src, size_t off) {
+        *dst = src->m;
+        dst->tiles = (uint32_t*)(wb + off);
+        if (e == hipSuccess) e = hipMemcpy(dst->tiles, src->m.tiles, src->m.bytes(), hipMemcpyDeviceToDevice);
+    };
+    place(&B->o, w->o, o_o);
+    place(&B->gate, w->gate, o_g);
+    place(&B->up, w->up, o_u);
+    place(&B->down, w->down, o_d);
+    B->qkv = w->q->m;
+    B->qkv.rows = B->q_dim + 2 * B->kv_dim;
+    B->qkv.ntiles = B->qkv.rows / kTileRows;
+    B->qkv.tiles = (uint32_t*)(wb + o_qkv);
+    B->qkv.scale = 1.0f;  // EPI_ACC: the Q/K/V scales are applied by qkv_rope
+    B->sq = w->q->m.scale;
+    B->sk = w->k->m.scale;
+    B->sv = w->v->m.scale;
+    if (e != hipSuccess) {
+        free_block(B);
+        return fail_hip("block weight copy", e);
+    }
+
+    // small fp32 parameters
+    Layout P;
+    const size_t p_n1 = P.take((size_t)H * 4);
+    const size_t p_n2 = P.take((size_t)H * 4);
+    const size_t p_an = P.take(w->attn_inner_norm ? (size_t)B->q_dim * 4 : 0);
+    const size_t p_fn = P.take(w->ffn_inner_norm ? (size_t)B->inter * 4 : 0);
+    const size_t p_bq = P.take(w->bias_q ? (size_t)B->q_dim * 4 : 0);
+    const size_t p_bk = P.take(w->bias_k ? (size_t)B->kv_dim * 4 : 0);
+    const size_t p_bv = P.take(w->bias_v ? (size_t)B->kv_dim * 4 : 0);
+    const size_t p_bo = P.take(w->bias_o ? (size_t)H * 4 : 0);
+    e = hipMalloc(&B->params, P.off);
+    if (e != hipSuccess) {
+        free_block(B);
+        return fail_hip("block parameters", e);
+    }
+    char* pb = (char*)B->params;
+    auto up = [&](float** dst, const float* src, size_t off, size_t n) {
+        if (!src) return;
+        *dst = (float*)(pb + off);
+        if (e == hipSuccess) e = hipMemcpy(*dst, src, n * 4, hipMemcpyHostToDevice);
+    };
+    up(&B->norm1, w->norm1, p_n1, H);
+    up(&B->norm2, w->norm2, p_n2, H);
+    up(&B->attn_norm, w->attn_inner_norm, p_an, B->q_dim);
+    up(&B->ffn_norm, w->ffn_inner_norm, p_fn, B->inter);
+    up(&B->bq, w->bias_q, p_bq, B->q_dim);
+    up(&B->bk, w->bias_k, p_bk, B->kv_dim);
+    up(&B->bv, w->bias_v, p_bv, B->kv_dim);
+    up(&B->bo, w->bias_o, p_bo, H);
+
+    // KV rings, zeroed like a fresh loom cache
+    const size_t cache_bytes = (size_t)B->max_batch * B->cache_slot() * 4;
+    if (e == hipSuccess) e = hipMalloc(&B->caches, 2 * cache_bytes);
+    if (e == hipSuccess) e = hipMemset(B->caches, 0, 2 * cache_bytes);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        free_block(B);
+        return fail_hip("block parameters", e);
+    }
+    B->cache_k = (float*)B->caches;
+    B->cache_v = (float*)((char*)B->caches + cache_bytes);
+    return 0;
+}
+
+static hipError_t tap_copy(void* dst, const void* src, size_t bytes, hipStream_t s) {
+    if (!dst) return hipSuccess;
+    return hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s);
+}
+
+// Enqueues one block forward on x (rows = batch*seq) at device position *pos.
+static int block_forward_dev(const BlockDev& B, const Workspace& W, float* x, int batch, int seq,
+                             const int* pos, const loom_amd_block_taps* taps, hipStream_t s) {
+    const int R = batch * seq;
+    const int ldh = pad_cols(B.hidden), ldqd = pad_cols(B.q_dim), ldi = pad_cols(B.inter);
+    hipError_t e;
+    // x := x + MHA(RMSNorm1(x))
+    e = launch_rmsnorm_quant(x, B.hidden, R, B.hidden, B.norm1, B.norm_eps, B.strict,
+                             taps ? taps->y1 : nullptr, W.xq, ldh, W.amax, W.xsum, s);
+    if (e != hipSuccess) return fail_hip("block rmsnorm1", e);
+    {
+        Epilogue ep;
+        ep.kind = EPI_ACC;
+        ep.acc0 = W.acc;
+        QuantAct a{W.xq, ldh, W.amax, W.xsum};
+        e = launch_matmul(&B.qkv, nullptr, a, R, ep, s);
+        if (e != hipSuccess) return fail_hip("block qkv projection", e);
+    }
+    e = launch_qkv_rope(W.acc, W.amax, B.sq, B.sk, B.sv, B.bq, B.bk, B.bv, batch, seq, pos, B.msl,
+                        B.heads, B.kv_heads, B.hd, B.theta, W.q, B.cache_k, B.cache_v, s);
+    if (e != hipSuccess) return fail_hip("block qkv rope", e);
+    if (taps && (e = tap_copy(taps->q, W.q, (size_t)R * B.q_dim * 8, s)) != hipSuccess) {
+        return fail_hip("block taps", e);
+    }
+    e = launch_attention(W.q, B.cache_k, B.cache_v, batch, seq, pos, B.msl, B.span(), B.heads,
+                         B.kv_heads, B.hd, B.strict, W.attn, s);
+    if (e != hipSuccess) return fail_hip("block attention", e);
+    if (taps && (e = tap_copy(taps->attn, W.attn, (size_t)R * B.q_dim * 8, s)) != hipSuccess) {
+        return fail_hip("block taps", e);
+    }
+    e = launch_norm_quant_f64(W.attn, R, B.q_dim, B.attn_norm, B.attn_eps, B.strict, nullptr, W.aq,
+                              ldqd, W.amax2, W.xsum2, s);
+    if (e != hipSuccess) return fail_hip("block attention inner norm", e);
+    {
+        Epilogue ep;
+        ep.kind = EPI_DENSE;
+        ep.bias0 = B.bo;
+        ep.residual = x;
+        ep.out = x;
+        ep.ldo = B.hidden;
+        QuantAct a{W.aq, ldqd, W.amax2, W.xsum2};
+        e = launch_matmul(&B.o, nullptr, a, R, ep, s);
+        if (e != hipSuccess) return fail_hip("block o projection", e);
+    }
+    if (taps && (e = tap_copy(taps->mid, x, (size_t)R * B.hidden * 4, s)) != hipSuccess) {
+        return fail_hip("block taps", e);
+    }
+    // x := x + SwiGLU(RMSNorm2(x))
+    e = launch_rmsnorm_quant(x, B.hidden, R, B.hidden, B.norm2, B.norm_eps, B.strict, nullptr,
+                             W.xq, ldh, W.amax, W.xsum, s);
+    if (e != hipSuccess) return fail_hip("block rmsnorm2", e);
+    {
+        Epilogue ep;
+        ep.kind = EPI_SWIGLU;
+        ep.activation = B.activation;
+        ep.out = W.h;
+        ep.ldo = B.inter;
+        QuantAct a{W.xq, ldh, W.amax, W.xsum};
+        e = launch_matmul(&B.gate, &B.up, a, R, ep, s);
+        if (e != hipSuccess) return fail_hip("block gate/up", e);
+    }
+    e = launch_norm_quant(W.h, B.inter, R, B.inter, B.ffn_norm, B.ffn_eps, B.strict, W.hq, ldi,
+                          W.amax3, W.xsum3, s);
+    if (e != hipSuccess) return fail_hip("block ffn inner norm", e);
+    {
+        Epilogue ep;
+        ep.kind = EPI_DENSE;
+        ep.residual = x;
+        ep.out = x;
+        ep.ldo = B.hidden;
+        QuantAct a{W.hq, ldi, W.amax3, W.xsum3};
+        e = launch_matmul(&B.down, nullptr, a, R, ep, s);
+        if (e != hipSuccess) return fail_hip("block down", e);
+    }
+    return 0;
+}
+
+// Host-side position rule of mhaPrepareKVForForward: continue only for a
+// single-token call on a warm cache.
+static int next_base(int shadow, int seq) { return (seq == 1 && shadow > 0) ? shadow : 0; }
+
+}  // namespace lamd
+
+using namespace lamd;
+
+struct loom_amd_block {
+    BlockDev dev;
+    Workspace ws;
+    int* pos = nullptr;  // device
+    int shadow = 0;      // host copy of the KV position
+};
+
+struct loom_amd_model {
+    int device = 0;
+    int layers_n = 0, vocab = 0, hidden = 0, max_tokens = 0, max_prefill = 0;
+    double final_eps = 0.0;
+    int strict = 1;
+    std::vector<BlockDev> layers;
+    Workspace ws;
+    float* embeddings = nullptr;
+    float* lm_head = nullptr;     // == embeddings when tied
+    float* final_norm = nullptr;  // null: no final norm
+    float* x = nullptr;           // max_batch*max_prefill x hidden
+    float* fin = nullptr;         // max_batch x hidden
+    float* logits = nullptr;      // max_batch x vocab
+    int* tokens = nullptr;        // max_batch x max_tokens
+    int* pos = nullptr;           // device position shared by every layer
+    void* misc = nullptr;
+    int batch = 0;                // batch of the current sequences
+    int shadow = 0;               // host copy of the position
+    hipStream_t own = nullptr;
+    hipGraphExec_t graph = nullptr;
+    int graph_batch = 0;
+};
+
+extern "C" {
+
+int loom_amd_block_create(int device, const loom_amd_block_desc* desc,
+                          const loom_amd_block_weights* w, loom_amd_block** out) {
+    if (!out) return fail("out is null");
+    *out = nullptr;
+    auto* b = new loom_amd_block();
+    if (build_block(device, desc, w, &b->dev)) {
+        delete b;
+        return -1;
+    }
+    DeviceGuard guard(device);
+    hipError_t e = hipMalloc(&b->pos, sizeof(int));
+    if (e == hipSuccess) e = hipMemset(b->pos, 0, sizeof(int));
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        free_block(&b->dev);
+        if (b->pos) (void)hipFree(b->pos);
+        delete b;
+        return fail_hip("block position", e);
+    }
+    *out = b;
+    return 0;
+}
+
+void loom_amd_block_release(loom_amd_block* b) {
+    if (!b) return;
+    DeviceGuard guard(b->dev.device);
+    (void)hipDeviceSynchronize();
+    free_workspace(&b->ws);
+    free_block(&b->dev);
+    if (b->pos) (void)hipFree(b->pos);
+    delete b;
+}
+
+int loom_amd_block_forward(loom_amd_block* b, float* x, int batch, int seq,
+                           const loom_amd_block_taps* taps, void* stream) {
+    if (!b) return fail("block is null");
+    if (!x) return fail("x is null");
+    if (batch <= 0 || seq <= 0) return fail("batch and seq must be positive");
+    const BlockDev& B = b->dev;
+    if (batch > B.max_batch) {
+        return fail("batch " + std::to_string(batch) + " > max_batch " + std::to_string(B.max_batch));
+    }
+    const int base = next_base(b->shadow, seq);
+    if (base + seq > B.span()) {
+        return fail("positions " + std::to_string(base) + ".." + std::to_string(base + seq - 1) +
+                    " pass max_seq_len " + std::to_string(B.msl));
+    }
+    DeviceGuard guard(B.device);
+    hipStream_t s = (hipStream_t)stream;
+    const int rows = batch * seq;
+    if (b->ws.rows < rows) {
+        hipError_t e = hipDeviceSynchronize();  // queued calls may still use the old workspace
+        if (e != hipSuccess) return fail_hip("block workspace", e);
+        free_workspace(&b->ws);
+        if (alloc_workspace(B, rows, &b->ws)) return -1;
+    }
+    hipError_t e = hipSuccess;
+    if (base == 0) e = launch_set_int(b->pos, 0, s);
+    if (e != hipSuccess) return fail_hip("block position", e);
+    if (block_forward_dev(B, b->ws, x, batch, seq, b->pos, taps, s)) return -1;
+    e = launch_add_int(b->pos, seq, s);
+    if (e != hipSuccess) return fail_hip("block position", e);
+    b->shadow = base + seq;
+    return 0;
+}
+
+int loom_amd_block_kv_offset(const loom_amd_block* b) { return b ? b->shadow : -1; }
+
+int loom_amd_block_kv_cache(const loom_amd_block* b, int slot, const float** k, const float** v) {
+    if (!b) return fail("block is null");
+    if (slot < 0 || slot >= b->dev.max_batch) return fail("slot out of range");
+    if (k) *k = b->dev.cache_k + (size_t)slot * b->dev.cache_slot();
+    if (v) *v = b->dev.cache_v + (size_t)slot * b->dev.cache_slot();
+    return 0;
+}
+
+// ---- model -----------------------------------------------------------------
+
+static void free_model(loom_amd_model* m) {
+    DeviceGuard guard(m->device);
+    (void)hipDeviceSynchronize();
+    if (m->graph) (void)hipGraphExecDestroy(m->graph);
+    for (auto& L : m->layers) free_block(&L);
+    free_workspace(&m->ws);
+    if (m->misc) (void)hipFree(m->misc);
+    if (m->own) (void)hipStreamDestroy(m->own);
+    delete m;
+}
+
+int loom_amd_model_create(int device, const loom_amd_model_desc* desc,
+                          const loom_amd_block_weights* layers, const float* embeddings,
+                          const float* final_norm, const float* lm_head, loom_amd_model** out) {
+    if (!out) return fail("out is null");
+    *out = nullptr;
+    if (!desc) return fail("model desc is null");
+    if (desc->num_layers < 0 || desc->vocab <= 0) return fail("model desc: bad layer count or vocab");
+    if (desc->num_layers > 0 && !layers) return fail("layers are null");
+    if (!embeddings) return fail("embeddings are null");
+    if (check_desc(&desc->block)) return -1;
+    const loom_amd_block_desc& bd = desc->block;
+    const int msl = bd.max_seq_len > 0 ? bd.max_seq_len : 512;
+    const int max_tokens = desc->max_tokens > 0 ? desc->max_tokens : msl + 1;
+    const int max_prefill = desc->max_prefill > 0 ? desc->max_prefill : (max_tokens < msl ? max_tokens : msl);
+    const int max_batch = bd.max_batch > 0 ? bd.max_batch : 1;
+    const int H = bd.hidden;
+    if ((size_t)H * 4 > 64 * 1024) return fail("model: hidden is limited to 16384 for the LM head");
+    auto* m = new loom_amd_model();
+    m->device = device;
+    m->layers_n = desc->num_layers;
+    m->vocab = desc->vocab;
+    m->hidden = H;
+    m->max_tokens = max_tokens;
+    m->max_prefill = max_prefill;
+    m->final_eps = desc->final_norm_eps;
+    m->strict = bd.norm_mode == LOOM_AMD_NORM_STRICT;
+    m->layers.resize(desc->num_layers);
+    for (int i = 0; i < desc->num_layers; ++i) {
+        if (build_block(device, &bd, &layers[i], &m->layers[i])) {
+            const std::string msg = "layer " + std::to_string(i) + ": " + g_amd_error;
+            free_model(m);
+            return fail(msg);
+        }
+    }
+    DeviceGuard guard(device);
+    Layout L;
+    const size_t o_emb = L.take((size_t)desc->vocab * H * 4);
+    const size_t o_lm = L.take(lm_head ? (size_t)desc->vocab * H * 4 : 0);
+    const size_t o_fn = L.take(final_norm ? (size_t)H * 4 : 0);
+    const size_t o_x = L.take((size_t)max_batch * max_prefill * H * 4);
+    const size_t o_fin = L.take((size_t)max_batch * H * 4);
+    const size_t o_lg = L.take((size_t)max_batch * desc->vocab * 4);
+    const size_t o_tok = L.take((size_t)max_batch * max_tokens * 4);
+    const size_t o_pos = L.take(4);
+    hipError_t e = hipMalloc(&m->misc, L.off);
+    if (e != hipSuccess) {
+        free_model(m);
+        return fail_hip("model buffers", e);
+    }
+    char* base = (char*)m->misc;
+    m->embeddings = (float*)(base + o_emb);
+    m->lm_head = lm_head ? (float*)(base + o_lm) : m->embeddings;
+    m->final_norm = final_norm ? (float*)(base + o_fn) : nullptr;
+    m->x = (float*)(base + o_x);
+    m->fin = (float*)(base + o_fin);
+    m->logits = (float*)(base + o_lg);
+    m->tokens = (int*)(base + o_tok);
+    m->pos = (int*)(base + o_pos);
+    e = hipMemcpy(m->embeddings, embeddings, (size_t)desc->vocab * H * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess && lm_head) {
+        e = hipMemcpy(m->lm_head, lm_head, (size_t)desc->vocab * H * 4, hipMemcpyHostToDevice);
+    }
+    if (e == hipSuccess && final_norm) {
+        e = hipMemcpy(m->final_norm, final_norm, (size_t)H * 4, hipMemcpyHostToDevice);
+    }
+    if (e == hipSuccess) e = hipMemset(m->tokens, 0, (size_t)max_batch * max_tokens * 4);
+    if (e == hipSuccess) e = hipMemset(m->pos, 0, sizeof(int));
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&m->own, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        free_model(m);
+        return fail_hip("model upload", e);
+    }
+    if (desc->num_layers > 0 && alloc_workspace(m->layers[0], max_batch * max_prefill, &m->ws)) {
+        free_model(m);
+        return -1;
+    }
+    *out = m;
+    return 0;
+}
+
+void loom_amd_model_release(loom_amd_model* m) {
+    if (m) free_model(m);
+}
+
+// Final norm + LM head + argmax of each sequence's last row (row stride ld
+// floats between sequences), writing the token at *pos + offset.
+static int model_head(loom_amd_model* m, const float* last, long ld, int batch, int offset,
+                      hipStream_t s) {
+    hipError_t e;
+    const float* h = last;
+    if (m->final_norm) {
+        e = launch_rmsnorm_quant(last, ld, batch, m->hidden, m->final_norm, m->final_eps, m->strict,
+                                 m->fin, nullptr, 0, nullptr, nullptr, s);
+        if (e != hipSuccess) return fail_hip("model final norm", e);
+    } else {
+        e = hipSuccess;
+        for (int b = 0; b < batch && e == hipSuccess; ++b) {
+            e = hipMemcpyAsync(m->fin + (size_t)b * m->hidden, last + (size_t)b * ld,
+                               (size_t)m->hidden * 4, hipMemcpyDeviceToDevice, s);
+        }
+        if (e != hipSuccess) return fail_hip("model last rows", e);
+    }
+    h = m->fin;
+    e = launch_lm_head(m->lm_head, m->vocab, m->hidden, h, batch, m->logits, s);
+    if (e != hipSuccess) return fail_hip("model lm head", e);
+    e = launch_argmax(m->logits, m->vocab, batch, m->tokens, m->max_tokens, m->pos, offset, s);
+    if (e != hipSuccess) return fail_hip("model argmax", e);
+    return 0;
+}
+
+int loom_amd_model_prefill(loom_amd_model* m, const int32_t* ids, int batch, int n,
+                           float* logits, void* stream) {
+    if (!m) return fail("model is null");
+    if (!ids) return fail("ids are null");
+    const int max_batch = m->layers_n > 0 ? m->layers[0].max_batch : 1;
+    if (batch <= 0 || batch > max_batch) return fail("batch out of range (max_batch " + std::to_string(max_batch) + ")");
+    if (n <= 0 || n > m->max_prefill) return fail("prompt length out of range (max_prefill " + std::to_string(m->max_prefill) + ")");
+    if (n >= m->max_tokens) return fail("prompt leaves no room for a generated token (max_tokens)");
+    if (m->layers_n > 0 && n > m->layers[0].span()) return fail("prompt longer than max_seq_len");
+    DeviceGuard guard(m->device);
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = launch_set_int(m->pos, 0, s);
+    if (e == hipSuccess) {
+        e = hipMemcpy2DAsync(m->tokens, (size_t)m->max_tokens * 4, ids, (size_t)n * 4, (size_t)n * 4,
+                             batch, hipMemcpyHostToDevice, s);
+    }
+    if (e == hipSuccess) {
+        e = launch_embed(m->embeddings, m->vocab, m->hidden, m->tokens, m->max_tokens, m->pos, batch,
+                         n, m->x, s);
+    }
+    if (e != hipSuccess) return fail_hip("model prefill", e);
+    for (int i = 0; i < m->layers_n; ++i) {
+        if (block_forward_dev(m->layers[i], m->ws, m->x, batch, n, m->pos, nullptr, s)) {
+            return fail("layer " + std::to_string(i) + ": " + g_amd_error);
+        }
+    }
+    if (model_head(m, m->x + (size_t)(n - 1) * m->hidden, (long)n * m->hidden, batch, n, s)) return -1;
+    e = launch_add_int(m->pos, n, s);
+    if (e == hipSuccess && logits) {
+        e = hipMemcpyAsync(logits, m->logits, (size_t)batch * m->vocab * 4, hipMemcpyDeviceToDevice, s);
+    }
+    if (e != hipSuccess) return fail_hip("model prefill", e);
+    m->batch = batch;
+    m->shadow = n;
+    return 0;
+}
+
+// One decode step on stream s (graph-capturable: kernels only).
+static int decode_step(loom_amd_model* m, hipStream_t s) {
+    const int batch = m->batch;
+    hipError_t e = launch_embed(m->embeddings, m->vocab, m->hidden, m->tokens, m->max_tokens, m->pos,
+                                batch, 1, m->x, s);
+    if (e != hipSuccess) return fail_hip("model embed", e);
+    for (int i = 0; i < m->layers_n; ++i) {
+        if (block_forward_dev(m->layers[i], m->ws, m->x, batch, 1, m->pos, nullptr, s)) {
+            return fail("layer " + std::to_string(i) + ": " + g_amd_error);
+        }
+    }
+    if (model_head(m, m->x, m->hidden, batch, 1, s)) return -1;
+    e = launch_add_int(m->pos, 1, s);
+    if (e != hipSuccess) return fail_hip("model position", e);
+    return 0;
+}
+
+int loom_amd_model_decode(loom_amd_model* m, int steps, int use_graph, float* logits,
+                          void* stream) {
+    if (!m) return fail("model is null");
+    if (steps < 0) return fail("steps must be >= 0");
+    if (m->batch <= 0 || m->shadow <= 0) return fail("decode needs a prefill first");
+    const int limit_seq = m->layers_n > 0 ? m->layers[0].span() : m->max_tokens;
+    if (m->shadow + steps > limit_seq || m->shadow + steps >= m->max_tokens) {
+        return fail("decode would pass max_seq_len or max_tokens");
+    }
+    if (steps == 0) return 0;
+    DeviceGuard guard(m->device);
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = hipSuccess;
+    if (use_graph) {
+        // capture on the model's own stream, ordered after the caller's work
+        hipStream_t cs = m->own;
+        hipEvent_t ev = nullptr;
+        e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        if (e == hipSuccess) e = hipEventRecord(ev, s);
+        if (e == hipSuccess) e = hipStreamWaitEvent(cs, ev, 0);
+        if (e != hipSuccess) {
+            if (ev) (void)hipEventDestroy(ev);
+            return fail_hip("model decode", e);
+        }
+        if (!m->graph || m->graph_batch != m->batch) {
+            if (m->graph) {
+                (void)hipGraphExecDestroy(m->graph);
+                m->graph = nullptr;
+            }
+            hipGraph_t g = nullptr;
+            e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
+            if (e != hipSuccess) {
+                (void)hipEventDestroy(ev);
+                return fail_hip("model decode capture", e);
+            }
+            const int rc = decode_step(m, cs);
+            hipError_t ec = hipStreamEndCapture(cs, &g);
+            if (rc || ec != hipSuccess) {
+                if (g) (void)hipGraphDestroy(g);
+                (void)hipEventDestroy(ev);
+                return rc ? -1 : fail_hip("model decode capture", ec);
+            }
+            e = hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            if (e != hipSuccess) {
+                m->graph = nullptr;
+                (void)hipEventDestroy(ev);
+                return fail_hip("model decode instantiate", e);
+            }
+            m->graph_batch = m->batch;
+        }
+        for (int i = 0; i < steps && e == hipSuccess; ++i) e = hipGraphLaunch(m->graph, cs);
+        if (e == hipSuccess) e = hipEventRecord(ev, cs);
+        if (e == hipSuccess) e = hipStreamWaitEvent(s, ev, 0);
+        (void)hipEventDestroy(ev);
+        if (e != hipSuccess) return fail_hip("model decode replay", e);
+    } else {
+        for (int i = 0; i < steps; ++i) {
+            if (decode_step(m, s)) return -1;
+        }
+    }
+    if (logits) {
+        e = hipMemcpyAsync(logits, m->logits, (size_t)m->batch * m->vocab * 4, hipMemcpyDeviceToDevice, s);
+        if (e != hipSuccess) return fail_hip("model logits", e);
+    }
+    m->shadow += steps;
+    return 0;
+}
+
+int loom_amd_model_tokens(const loom_amd_model* m, int32_t* out, int count, void* stream) {
+    if (!m) return fail("model is null");
+    if (!out) return fail("out is null");
+    if (count <= 0 || count > m->max_tokens) return fail("count out of range");
+    DeviceGuard guard(m->device);
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = hipMemcpy2DAsync(out, (size_t)count * 4, m->tokens, (size_t)m->max_tokens * 4,
+                                    (size_t)count * 4, m->batch > 0 ? m->batch : 1,
+                                    hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    return e == hipSuccess ? 0 : fail_hip("model tokens", e);
+}
+
+int loom_amd_model_position(const loom_amd_model* m) { return m ? m->shadow : -1; }
+
+const float* loom_amd_model_last_hidden(const loom_amd_model* m) { return m ? m->fin : nullptr; }
+
+}  // extern "C"

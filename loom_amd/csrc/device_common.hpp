@@ -172,6 +172,7 @@ __device__ __forceinline__ void epilogue_store(const EpiDev& e, int i, int n, in
     const int acc0 = raw0 - rs.xs;
     const size_t o = (size_t)i * e.ldo + n;
     if (e.acc0) e.acc0[(size_t)i * e.n + n] = acc0;
+    if (e.kind == EPI_ACC) return;
     if (e.kind == EPI_SWIGLU) {
         const int acc1 = raw1 - rs.xs;
         if (e.acc1) e.acc1[(size_t)i * e.n + n] = acc1;

@@ -64,6 +64,7 @@ struct QuantAct {
 enum EpiKind : int {
     EPI_DENSE = 0,   // pre = fp32(fp64(acc)*os) [+bias]; post = Activate(pre); [+residual]
     EPI_SWIGLU = 1,  // h = fp32(gateprod(fp64(acc_g)*os_g + bg, fp64(acc_u)*os_u + bu))
+    EPI_ACC = 2,     // only the int32 accumulators (acc0, M x N); the caller rescales
 };
 
 struct Epilogue {

@@ -758,6 +758,71 @@ void orc_fill_uniform_f32(float* out, long n, float lo, float hi, uint64_t seed)
 
 /* bitNetRMSNormFloat64Weighted + bitNetQuantizeActivationFloat64 are above. */
 
+/* Attention of MHAForwardPackedTernaryCPU (poly/mha.go:316-354) for `seq`
+ * queries at positions seq_base + s over the ring caches (row kp % msl):
+ * fp64 dot over d in order times 1/sqrt(hd), running max from -1e9,
+ * exp(score - max), expSum in position order, out[d] = sum in position order
+ * of p*V / expSum.  GQA group of head h: h / (heads / kv_heads). */
+void orc_attention(const double* Q, const float* cache_k, const float* cache_v, int seq,
+                   int seq_base, int msl, int heads, int kv_heads, int hd, double* attn) {
+    const int q_dim = heads * hd, kv_dim = kv_heads * hd;
+    const int per_kv = heads / kv_heads;
+    const double scale = 1.0 / sqrt((double)hd);
+    double* scores = (double*)malloc((size_t)(seq_base + seq) * sizeof(double));
+    for (int s = 0; s < seq; s++) {
+        const int total = seq_base + s;
+        for (int h = 0; h < heads; h++) {
+            const int kvh = h / per_kv;
+            double max_score = -1e9;
+            for (int kp = 0; kp <= total; kp++) {
+                const float* kr = cache_k + (size_t)(kp % msl) * kv_dim + (size_t)kvh * hd;
+                const double* qr = Q + (size_t)s * q_dim + (size_t)h * hd;
+                double dot = 0.0;
+                for (int d = 0; d < hd; d++) dot += qr[d] * (double)kr[d];
+                double score = dot * scale;
+                scores[kp] = score;
+                if (score > max_score) max_score = score;
+            }
+            double exp_sum = 0.0;
+            for (int kp = 0; kp <= total; kp++) {
+                scores[kp] = exp(scores[kp] - max_score);
+                exp_sum += scores[kp];
+            }
+            for (int d = 0; d < hd; d++) {
+                double sum = 0.0;
+                for (int kp = 0; kp <= total; kp++) {
+                    sum += scores[kp] * (double)cache_v[(size_t)(kp % msl) * kv_dim + (size_t)kvh * hd + d];
+                }
+                attn[(size_t)s * q_dim + (size_t)h * hd + d] = sum / exp_sum;
+            }
+        }
+    }
+    free(scores);
+}
+
+/* Output stage of MHAForwardPackedTernaryCPU (poly/mha.go:356-368): per row,
+ * bitNetRMSNormFloat64Weighted in place, fp64 requantization, O matvec,
+ * pre = fp32(normalized row), post = fp32(O + bias).  attn is modified. */
+void orc_attn_out(const orc_matrix* o, const float* bias_o, const float* inner_norm, double eps,
+                  double* attn, int seq, int q_dim, int simd, int workers, float* pre,
+                  float* post) {
+    const int d_model = o->rows;
+    double* to = (double*)malloc((size_t)d_model * sizeof(double));
+    int8_t* aq = (int8_t*)malloc((size_t)q_dim);
+    for (int s = 0; s < seq; s++) {
+        double* ar = attn + (size_t)s * q_dim;
+        orc_bitnet_rmsnorm_f64(ar, q_dim, inner_norm, eps);
+        float amax = orc_quant_act_f64(ar, q_dim, aq);
+        matvec_quantized(o, aq, amax, simd, workers, to, NULL);
+        for (int i = 0; i < d_model; i++) {
+            if (pre) pre[(size_t)s * d_model + i] = (float)ar[i];
+            post[(size_t)s * d_model + i] = (float)(to[i] + (bias_o ? (double)bias_o[i] : 0.0));
+        }
+    }
+    free(aq);
+    free(to);
+}
+
 /* MHAForwardPackedTernaryCPU (poly/mha.go:204-371) for one batch row of
  * `seq` tokens.  Per-head Q/K norms are not supported (BitNet has none).
  * The KV cache is a ring of msl rows (pos % msl), prepared as
@@ -824,56 +889,12 @@ void orc_mha_forward(orc_mha* L, const float* in, int seq, int simd, int workers
         }
     }
     if (q_out) memcpy(q_out, Q, (size_t)seq * q_dim * sizeof(double));
-    const int per_kv = heads / kv_heads;
-    const double scale = 1.0 / sqrt((double)hd);
     double* attn = (double*)malloc((size_t)seq * q_dim * sizeof(double));
-    double* scores = (double*)malloc((size_t)(seq_base + seq) * sizeof(double));
-    for (int s = 0; s < seq; s++) {
-        const int total = seq_base + s;
-        for (int h = 0; h < heads; h++) {
-            const int kvh = h / per_kv;
-            double max_score = -1e9;
-            for (int kp = 0; kp <= total; kp++) {
-                const float* kr = L->cache_k + (size_t)(kp % msl) * kv_dim + (size_t)kvh * hd;
-                const double* qr = Q + (size_t)s * q_dim + (size_t)h * hd;
-                double dot = 0.0;
-                for (int d = 0; d < hd; d++) dot += qr[d] * (double)kr[d];
-                double score = dot * scale;
-                scores[kp] = score;
-                if (score > max_score) max_score = score;
-            }
-            double exp_sum = 0.0;
-            for (int kp = 0; kp <= total; kp++) {
-                scores[kp] = exp(scores[kp] - max_score);
-                exp_sum += scores[kp];
-            }
-            for (int d = 0; d < hd; d++) {
-                double sum = 0.0;
-                for (int kp = 0; kp <= total; kp++) {
-                    sum += scores[kp] *
-                           (double)L->cache_v[(size_t)(kp % msl) * kv_dim + (size_t)kvh * hd + d];
-                }
-                attn[(size_t)s * q_dim + (size_t)h * hd + d] = sum / exp_sum;
-            }
-        }
-    }
+    orc_attention(Q, L->cache_k, L->cache_v, seq, seq_base, msl, heads, kv_heads, hd, attn);
     if (attn_out) memcpy(attn_out, attn, (size_t)seq * q_dim * sizeof(double));
-    double* to = (double*)malloc((size_t)d_model * sizeof(double));
-    int8_t* aq = (int8_t*)malloc((size_t)q_dim);
-    for (int s = 0; s < seq; s++) {
-        double* ar = attn + (size_t)s * q_dim;
-        orc_bitnet_rmsnorm_f64(ar, q_dim, L->inner_norm, L->eps);
-        float amax = orc_quant_act_f64(ar, q_dim, aq);
-        matvec_quantized(L->o, aq, amax, simd, workers, to, NULL);
-        for (int i = 0; i < d_model; i++) {
-            if (pre) pre[(size_t)s * d_model + i] = (float)ar[i];
-            post[(size_t)s * d_model + i] = (float)(to[i] + (L->bias_o ? (double)L->bias_o[i] : 0.0));
-        }
-    }
+    orc_attn_out(L->o, L->bias_o, L->inner_norm, L->eps, attn, seq, q_dim, simd, workers, pre,
+                 post);
     L->kv_offset = seq_base + seq;
-    free(aq);
-    free(to);
-    free(scores);
     free(attn);
     free(xq);
     free(tv);

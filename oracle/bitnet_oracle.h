@@ -141,6 +141,11 @@ typedef struct orc_mha {
     int kv_offset;             /* tokens already cached (in/out) */
 } orc_mha;
 
+void orc_attention(const double* Q, const float* cache_k, const float* cache_v, int seq,
+                   int seq_base, int msl, int heads, int kv_heads, int hd, double* attn);
+void orc_attn_out(const orc_matrix* o, const float* bias_o, const float* inner_norm, double eps,
+                  double* attn, int seq, int q_dim, int simd, int workers, float* pre,
+                  float* post);
 void orc_mha_forward(orc_mha* L, const float* in, int seq, int simd, int workers,
                      float* pre, float* post, double* q_out, double* attn_out);
 

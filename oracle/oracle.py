@@ -76,6 +76,8 @@ def _declare(L: C.CDLL) -> None:
         "orc_swiglu_forward": (None, [P, P, P, P, P, d, i, P, i, i, i,
                                       P, P, P, P, P, P, P, P, P]),
         "orc_rmsnorm_forward": (None, [P, i, i, P, d, P, P]),
+        "orc_attention": (None, [P, P, P, i, i, i, i, i, i, P]),
+        "orc_attn_out": (None, [P, P, P, d, P, i, i, i, i, P, P]),
         "orc_mha_forward": (None, [P, P, i, i, i, P, P, P, P]),
         "orc_block_forward": (None, [P, P, i, i, i]),
         "orc_lm_head_seq": (None, [P, P, i, i, P]),
@@ -411,6 +413,35 @@ class _CBlock(C.Structure):
 def _cmat(m: Matrix, simd: bool) -> _CMatrix:
     codes = m.ensure_codes() if simd else None
     return _CMatrix(m.rows, m.cols, m.row_words, m.scale, _p(m.words), _p(codes))
+
+
+def attention(q: np.ndarray, cache_k: np.ndarray, cache_v: np.ndarray, seq_base: int, msl: int,
+              num_heads: int, num_kv_heads: int, head_dim: int) -> np.ndarray:
+    """Attention stage of MHAForwardPackedTernaryCPU (poly/mha.go:316-354):
+    q [seq, q_dim] fp64 after RoPE, caches [msl, kv_dim] fp32; returns fp64."""
+    q = np.ascontiguousarray(q, np.float64).reshape(-1, num_heads * head_dim)
+    ck = np.ascontiguousarray(cache_k, np.float32)
+    cv = np.ascontiguousarray(cache_v, np.float32)
+    out = np.empty_like(q)
+    lib().orc_attention(_p(q), _p(ck), _p(cv), q.shape[0], seq_base, msl, num_heads,
+                        num_kv_heads, head_dim, _p(out))
+    return out
+
+
+def attn_out(o: Matrix, attn: np.ndarray, inner_norm: np.ndarray | None = None,
+             eps: float = 1e-5, bias_o: np.ndarray | None = None, simd: bool = True):
+    """Output stage of MHAForwardPackedTernaryCPU (poly/mha.go:356-368):
+    returns (pre, post) fp32 for fp64 attention rows (before the inner norm)."""
+    a = np.array(attn, np.float64, copy=True).reshape(-1, o.cols)
+    seq = a.shape[0]
+    pre = np.empty((seq, o.cols), np.float32)
+    post = np.empty((seq, o.rows), np.float32)
+    cm = _cmat(o, simd)
+    wn = None if inner_norm is None else np.ascontiguousarray(inner_norm, np.float32)
+    bo = None if bias_o is None else np.ascontiguousarray(bias_o, np.float32)
+    lib().orc_attn_out(C.byref(cm), _p(bo), _p(wn), eps, _p(a), seq, o.cols, int(simd),
+                       os.cpu_count() or 1, _p(pre), _p(post))
+    return pre, post
 
 
 class MHA:

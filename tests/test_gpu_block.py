@@ -1,0 +1,418 @@
+"""Parity of the gfx950 decoder block and decode loop against the CPU oracle
+(loom's MHAForwardPackedTernaryCPU / forwardOnCPUNormal / Generate restated).
+
+Bar, stage by stage (strict norm mode):
+  * RMSNorm outputs, int8 quantization, int32 accumulators, the O projection
+    with its residual and the whole FFN half (ReLU2 gate): bit-exact, each
+    stage fed the GPU's own input to it;
+  * RoPE uses pow/cos/sin and softmax uses exp, whose last fp64 bit differs
+    between libm implementations (Go, glibc, ROCm ocml): Q is checked within
+    1e-12 relative to its row scale (bit-exact at position 0, where the
+    rotation is the identity), cached K within 1 fp32 ulp (V bit-exact), and
+    attention within 1e-12 relative against the oracle fed the GPU's Q and
+    caches;
+  * the LM head is bit-exact (loom's amd64 DotTile order) and the greedy token
+    is the oracle's argmax of the GPU logits.
+End to end, the last-bit libm differences can move an int8 code across a
+rounding boundary, so the whole block is compared with a stated tolerance.
+Citations are relative to the loom v0.83.0 tree.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+ACT_SILU, ACT_RELU2 = 1, 6
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a visible MI355X"
+    from loom_amd import _lib
+    assert _lib.lib().loom_amd_device_count() >= 1, "no gfx950 device visible to the library"
+    return torch
+
+
+@pytest.fixture(scope="module")
+def tf(torch_dev):
+    from loom_amd import transformer
+    return transformer
+
+
+class Shape:
+    def __init__(self, hidden, heads, kv, hd, inter, msl, theta=500000.0):
+        self.hidden, self.heads, self.kv, self.hd, self.inter, self.msl = hidden, heads, kv, hd, inter, msl
+        self.theta = theta
+        self.q_dim, self.kv_dim = heads * hd, kv * hd
+
+
+SMALL = Shape(256, 4, 2, 64, 512, 64)
+BITNET_2B = Shape(2560, 20, 5, 128, 6912, 640)  # BitNet-b1.58-2B block (config 2)
+
+
+class Weights:
+    """Oracle matrices + fp32 vectors of one block (seeded)."""
+
+    def __init__(self, orc, sh: Shape, seed: int, act: int = ACT_RELU2, bias: bool = False):
+        self.sh, self.act = sh, act
+        self.q = orc.random_matrix(sh.q_dim, sh.hidden, seed)
+        self.k = orc.random_matrix(sh.kv_dim, sh.hidden, seed + 1)
+        self.v = orc.random_matrix(sh.kv_dim, sh.hidden, seed + 2)
+        self.o = orc.random_matrix(sh.hidden, sh.q_dim, seed + 3)
+        self.g = orc.random_matrix(sh.inter, sh.hidden, seed + 4)
+        self.u = orc.random_matrix(sh.inter, sh.hidden, seed + 5)
+        self.d = orc.random_matrix(sh.hidden, sh.inter, seed + 6)
+        self.n1 = orc.uniform_f32(sh.hidden, 0.5, 1.5, seed + 7)
+        self.n2 = orc.uniform_f32(sh.hidden, 0.5, 1.5, seed + 8)
+        self.an = orc.uniform_f32(sh.q_dim, 0.5, 1.5, seed + 9)
+        self.fn = orc.uniform_f32(sh.inter, 0.5, 1.5, seed + 10)
+        self.bias = None
+        if bias:
+            self.bias = [orc.normal_f32(n, seed + 11 + i) * np.float32(0.1)
+                         for i, n in enumerate([sh.q_dim, sh.kv_dim, sh.kv_dim, sh.hidden])]
+
+    def gpu(self, tf):
+        from loom_amd.bitnet import TernaryMatrix
+
+        def m(x):
+            return TernaryMatrix.from_words(x.words, x.rows, x.cols, x.scale)
+
+        b = self.bias or [None] * 4
+        return tf.BlockWeights(m(self.q), m(self.k), m(self.v), m(self.o), m(self.g), m(self.u),
+                               m(self.d), self.n1, self.n2, self.an, self.fn, *b)
+
+    def cfg(self, tf, norm="strict", max_batch=1):
+        sh = self.sh
+        return tf.BlockConfig(sh.hidden, sh.heads, sh.kv, sh.hd, sh.inter, max_seq_len=sh.msl,
+                              max_batch=max_batch, rope_theta=sh.theta, norm_eps=1e-5,
+                              attn_eps=1e-5, ffn_eps=1e-5, ffn_activation=self.act, norm=norm)
+
+    def oracle_mha(self, orc):
+        sh = self.sh
+        m = orc.MHA(self.q, self.k, self.v, self.o, sh.heads, sh.kv, sh.hd, sh.msl,
+                    theta=sh.theta, eps=1e-5, inner_norm=self.an)
+        if self.bias:
+            # the oracle MHA wrapper has no bias arguments: set them on its C struct
+            self._bias_keep = [np.ascontiguousarray(b, np.float32) for b in self.bias]
+            from oracle.oracle import _p
+            m.c.bias_q, m.c.bias_k, m.c.bias_v, m.c.bias_o = (_p(b) for b in self._bias_keep)
+        return m
+
+    def oracle_block(self, orc):
+        return orc.Block(self.oracle_mha(orc), self.n1, self.n2, self.g, self.u, self.d, self.fn,
+                         norm_eps=1e-5, ffn_eps=1e-5, ffn_activation=self.act)
+
+
+def ulp_diff_f32(a, b):
+    a = np.ascontiguousarray(a, np.float32).view(np.int32).astype(np.int64)
+    b = np.ascontiguousarray(b, np.float32).view(np.int32).astype(np.int64)
+    a = np.where(a < 0, np.int64(-2**31) - a, a)
+    b = np.where(b < 0, np.int64(-2**31) - b, b)
+    return np.abs(a - b)
+
+
+def to_dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def check_stages(orc, w: Weights, mha_ref, x_in, taps, out, cache_k, cache_v, base, strict=True):
+    """Stage-wise parity of one GPU block call (rows = seq tokens at positions
+    base..base+seq-1 of one sequence).  mha_ref is an oracle MHA whose
+    kv_offset equals base; it is advanced by this call."""
+    sh = w.sh
+    seq = x_in.shape[0]
+    y1 = taps.y1.cpu().numpy()
+    q = taps.q.cpu().numpy()
+    attn = taps.attn.cpu().numpy()
+    mid = taps.mid.cpu().numpy()
+    # RMSNorm1 (poly/norm.go:102-138)
+    y1_ref = orc.rmsnorm_forward(x_in, w.n1, 1e-5)
+    if strict:
+        assert np.array_equal(y1, y1_ref), "rmsnorm1 not bit-exact"
+    else:
+        assert ulp_diff_f32(y1, y1_ref).max() <= 1
+    # Q/K/V + RoPE: the oracle fed the GPU's y1
+    _, _, q_ref, _ = mha_ref.forward(y1)
+    assert mha_ref.kv_offset == base + seq
+    scale = np.abs(q_ref).max(axis=1, keepdims=True)
+    assert np.all(np.abs(q - q_ref) <= 1e-12 * scale), "Q after RoPE off by more than 1e-12"
+    if base == 0:
+        # position 0: cos = 1, sin = 0 exactly -> the rotation is the identity
+        assert np.array_equal(q[0], q_ref[0])
+    kd = sh.kv_dim
+    ck_ref = mha_ref.cache_k.reshape(sh.msl, kd)
+    cv_ref = mha_ref.cache_v.reshape(sh.msl, kd)
+    rows = slice(base, base + seq)
+    assert np.array_equal(cache_v[rows], cv_ref[rows]), "V cache not bit-exact"
+    assert ulp_diff_f32(cache_k[rows], ck_ref[rows]).max() <= 1, "K cache beyond 1 ulp"
+    if base == 0:
+        assert np.array_equal(cache_k[0], ck_ref[0])
+    # attention (poly/mha.go:316-354), the oracle fed the GPU's Q and caches
+    attn_ref = orc.attention(q, cache_k, cache_v, base, sh.msl, sh.heads, sh.kv, sh.hd)
+    ascale = np.abs(attn_ref).max(axis=1, keepdims=True)
+    assert np.all(np.abs(attn - attn_ref) <= 1e-12 * ascale), "attention off by more than 1e-12"
+    # inner norm + requant + O + residual (poly/mha.go:356-368, transformer_forward.go:236)
+    bo = w.bias[3] if w.bias else None
+    _, post = orc.attn_out(w.o, attn, inner_norm=w.an, eps=1e-5, bias_o=bo)
+    mid_ref = (post + x_in).astype(np.float32)
+    if strict:
+        assert np.array_equal(mid, mid_ref), "O projection + residual not bit-exact"
+    else:
+        assert np.mean(mid == mid_ref) > 0.9
+    # RMSNorm2 + SwiGLU + residual (transformer_forward.go:238-245)
+    y2 = orc.rmsnorm_forward(mid, w.n2, 1e-5)
+    f = orc.swiglu_forward(w.g, w.u, w.d, y2, inner_norm=w.fn, eps=1e-5, activation=w.act).out
+    out_ref = (f + mid).astype(np.float32)
+    if strict and w.act == ACT_RELU2:
+        assert np.array_equal(out, out_ref), "FFN half not bit-exact"
+    else:
+        # SiLU gate: exp() last bits (h within 1 ulp), which can move an int8 code
+        assert np.mean(out == out_ref) > 0.9
+        assert np.abs(out - out_ref).max() <= 0.05 * np.abs(out_ref).max()
+
+
+def run_block_case(orc, torch, tf, w: Weights, seqs, seed, strict=True):
+    """Prefill seqs[0] tokens then single-token steps for the rest."""
+    sh = w.sh
+    blk = tf.BitNetBlock(w.cfg(tf, "strict" if strict else "fast"), w.gpu(tf))
+    mha_ref = w.oracle_mha(orc)
+    base = 0
+    for i, seq in enumerate(seqs):
+        x_in = orc.normal_f32(seq * sh.hidden, seed + i).reshape(seq, sh.hidden)
+        x = to_dev(torch, x_in)
+        print(f"  block call {i}: seq={seq} base={base}", flush=True)
+        _, taps = blk.forward(x, taps=True)
+        torch.cuda.synchronize()
+        assert blk.kv_offset == base + seq
+        ck, cv = (t.cpu().numpy() for t in blk.kv_cache(0))
+        check_stages(orc, w, mha_ref, x_in, taps, x.cpu().numpy(), ck, cv, base, strict)
+        base += seq
+    blk.release()
+
+
+@pytest.mark.parametrize("seqs", [[1], [5], [9, 1, 1, 1], [64]])
+def test_block_stages_small(orc, torch_dev, tf, seqs):
+    w = Weights(orc, SMALL, seed=101)
+    run_block_case(orc, torch_dev, tf, w, seqs, seed=900)
+
+
+def test_block_stages_bias_and_silu(orc, torch_dev, tf):
+    # MHA biases (poly/mha.go:273-282) and the SiLU gate
+    w = Weights(orc, SMALL, seed=131, act=ACT_SILU, bias=True)
+    run_block_case(orc, torch_dev, tf, w, [7, 1, 1], seed=910)
+
+
+def test_block_stages_mha_no_gqa(orc, torch_dev, tf):
+    # num_kv_heads == num_heads, head_dim 32
+    sh = Shape(128, 4, 4, 32, 256, 32)
+    w = Weights(orc, sh, seed=141)
+    run_block_case(orc, torch_dev, tf, w, [6, 1], seed=920)
+
+
+def test_block_stages_fast_norm(orc, torch_dev, tf):
+    w = Weights(orc, SMALL, seed=151)
+    run_block_case(orc, torch_dev, tf, w, [12, 1], seed=930, strict=False)
+
+
+def test_block_stages_bitnet_2b_shape(orc, torch_dev, tf):
+    # config 2's block shape: hidden 2560, 20 heads / 5 KV heads x 128, FFN 6912
+    w = Weights(orc, BITNET_2B, seed=161)
+    run_block_case(orc, torch_dev, tf, w, [16, 1, 1], seed=940)
+
+
+def test_block_bitnet_2b_seq512(orc, torch_dev, tf):
+    # config 2 at its full length: seq 512, batch 1 (stage-wise, strict)
+    w = Weights(orc, BITNET_2B, seed=171)
+    run_block_case(orc, torch_dev, tf, w, [512], seed=950)
+
+
+def test_block_end_to_end_tolerance(orc, torch_dev, tf):
+    # Whole block vs the oracle's own chain.  Only libm last bits differ, so
+    # almost every element is identical; a moved int8 code changes a row by
+    # about one quantization step.
+    torch = torch_dev
+    w = Weights(orc, SMALL, seed=181)
+    blk = tf.BitNetBlock(w.cfg(tf), w.gpu(tf))
+    ref = w.oracle_block(orc)
+    for i, seq in enumerate([10, 1, 1]):
+        x_in = orc.normal_f32(seq * SMALL.hidden, 960 + i).reshape(seq, SMALL.hidden)
+        x = to_dev(torch, x_in)
+        blk.forward(x)
+        got = x.cpu().numpy()
+        want = ref.forward(x_in)
+        eq = np.mean(got == want)
+        err = np.abs(got - want).max() / np.abs(want).max()
+        print(f"  call {i}: identical {eq:.4f}, max rel err {err:.2e}", flush=True)
+        assert eq > 0.95 and err < 1e-2
+    blk.release()
+
+
+def test_block_batch_equals_separate_sequences(orc, torch_dev, tf):
+    # batch sequences each own a KV cache: a batch-3 call equals three batch-1
+    # calls, prefill and decode, bit for bit.
+    torch = torch_dev
+    w = Weights(orc, SMALL, seed=191)
+    gw = w.gpu(tf)
+    big = tf.BitNetBlock(w.cfg(tf, max_batch=3), gw)
+    singles = [tf.BitNetBlock(w.cfg(tf), gw) for _ in range(3)]
+    for step, seq in enumerate([8, 1, 1]):
+        xs = [orc.normal_f32(seq * SMALL.hidden, 1000 + 10 * step + b).reshape(seq, SMALL.hidden)
+              for b in range(3)]
+        xb = to_dev(torch, np.stack(xs))
+        big.forward(xb)
+        for b in range(3):
+            xi = to_dev(torch, xs[b])
+            singles[b].forward(xi)
+            assert np.array_equal(xb[b].cpu().numpy(), xi.cpu().numpy())
+    for b in range(3):
+        kb, vb = (t.cpu().numpy() for t in big.kv_cache(b))
+        ks, vs = (t.cpu().numpy() for t in singles[b].kv_cache(0))
+        assert np.array_equal(kb[:10], ks[:10]) and np.array_equal(vb[:10], vs[:10])
+
+
+def test_block_prefill_resets_cache(orc, torch_dev, tf):
+    # mhaPrepareKVForForward: any call that is not a warm single-token step
+    # restarts at position 0 (same outputs again).
+    torch = torch_dev
+    w = Weights(orc, SMALL, seed=201)
+    blk = tf.BitNetBlock(w.cfg(tf), w.gpu(tf))
+    x_in = orc.normal_f32(4 * SMALL.hidden, 1100).reshape(4, SMALL.hidden)
+    a = to_dev(torch, x_in)
+    blk.forward(a)
+    blk.forward(to_dev(torch, x_in[:1]))
+    assert blk.kv_offset == 5
+    b = to_dev(torch, x_in)
+    blk.forward(b)
+    assert blk.kv_offset == 4
+    assert np.array_equal(a.cpu().numpy(), b.cpu().numpy())
+
+
+def test_block_refuses_positions_past_ring(orc, torch_dev, tf):
+    from loom_amd._lib import AMDError
+    torch = torch_dev
+    w = Weights(orc, SMALL, seed=211)
+    blk = tf.BitNetBlock(w.cfg(tf), w.gpu(tf))
+    with pytest.raises(AMDError, match="max_seq_len"):
+        blk.forward(to_dev(torch, np.zeros((SMALL.msl + 1, SMALL.hidden), np.float32)))
+    with pytest.raises(AMDError, match="max_batch"):
+        blk.forward(to_dev(torch, np.zeros((2, 3, SMALL.hidden), np.float32)))
+
+
+# ---------------------------------------------------------------- model / decode loop
+class Model:
+    def __init__(self, orc, sh: Shape, layers: int, vocab: int, seed: int):
+        self.sh, self.vocab = sh, vocab
+        self.layers = [Weights(orc, sh, seed + 100 * i) for i in range(layers)]
+        self.emb = orc.normal_f32(vocab * sh.hidden, seed + 7) * np.float32(0.5)
+        self.fn = orc.uniform_f32(sh.hidden, 0.5, 1.5, seed + 8)
+
+    def gpu(self, tf, max_tokens, max_batch=1, norm="strict"):
+        cfg = self.layers[0].cfg(tf, norm=norm, max_batch=max_batch)
+        return tf.Transformer(cfg, [w.gpu(tf) for w in self.layers], self.emb, self.fn,
+                              vocab=self.vocab, final_norm_eps=1e-6, max_tokens=max_tokens)
+
+
+def test_model_prefill_head_and_greedy_token(orc, torch_dev, tf):
+    torch = torch_dev
+    sh = SMALL
+    M = Model(orc, sh, layers=2, vocab=1000, seed=301)
+    model = M.gpu(tf, max_tokens=40)
+    ids = (np.arange(12) * 37 + 5) % 1000
+    logits = model.prefill(ids, logits=True).cpu().numpy()[0]
+    hid = model.last_hidden().cpu().numpy()[0]
+    # stack plumbing: embeddings -> the same blocks one by one -> final norm
+    blocks = [tf.BitNetBlock(w.cfg(tf), w.gpu(tf)) for w in M.layers]
+    x = to_dev(torch, M.emb.reshape(1000, sh.hidden)[ids])
+    for b in blocks:
+        b.forward(x)
+    last = x.cpu().numpy()[-1:]
+    assert np.array_equal(hid, orc.rmsnorm_forward(last, M.fn, 1e-6)[0])
+    # LM head in DotTile order (poly/transformer.go:679-681) and greedy pick
+    table = M.emb
+    assert np.array_equal(logits, orc.lm_head(hid, table, simd=True))
+    toks = model.tokens()[0]
+    assert np.array_equal(toks[:12], ids)
+    assert toks[12] == orc.argmax_first(logits)
+    # close to the oracle's own full chain (libm last bits only)
+    ref_x = M.emb.reshape(1000, sh.hidden)[ids].copy()
+    for w in M.layers:
+        ref_x = w.oracle_block(orc).forward(ref_x)
+    ref_logits = orc.lm_head(orc.rmsnorm_forward(ref_x[-1:], M.fn, 1e-6)[0], table, simd=True)
+    err = np.abs(ref_logits - logits).max() / np.abs(ref_logits).max()
+    print(f"  prefill logits vs oracle chain: max rel err {err:.2e}", flush=True)
+    assert err < 1e-2
+
+
+def test_model_decode_graph_matches_eager(orc, torch_dev, tf):
+    torch = torch_dev
+    M = Model(orc, SMALL, layers=2, vocab=1000, seed=401)
+    model = M.gpu(tf, max_tokens=48)
+    prompt = (np.arange(9) * 101 + 3) % 1000
+    model.prefill(prompt)
+    lg_graph = model.decode(20, use_graph=True, logits=True).cpu().numpy()
+    t_graph = model.tokens()
+    assert model.position == 29
+    model.prefill(prompt)
+    lg_eager = model.decode(20, use_graph=False, logits=True).cpu().numpy()
+    t_eager = model.tokens()
+    assert np.array_equal(t_graph, t_eager)
+    assert np.array_equal(lg_graph, lg_eager)
+    # each decode step: LM head of the final hidden row, then argmax
+    hid = model.last_hidden().cpu().numpy()[0]
+    assert np.array_equal(lg_eager[0], orc.lm_head(hid, M.emb, simd=True))
+    assert t_eager[0, 29] == orc.argmax_first(lg_eager[0])
+    # graph replays continue from where eager steps stopped
+    model.decode(3, use_graph=True)
+    assert model.position == 32
+
+
+def test_model_decode_step_equals_block_chain(orc, torch_dev, tf):
+    # one decode step == embedding of the newest token through the same
+    # blocks (warm caches), final norm, LM head
+    torch = torch_dev
+    sh = SMALL
+    M = Model(orc, sh, layers=2, vocab=500, seed=501)
+    model = M.gpu(tf, max_tokens=32)
+    prompt = (np.arange(6) * 13 + 1) % 500
+    model.prefill(prompt)
+    model.decode(2, use_graph=True)
+    toks = model.tokens()[0]
+    blocks = [tf.BitNetBlock(w.cfg(tf), w.gpu(tf)) for w in M.layers]
+    table = M.emb.reshape(500, sh.hidden)
+    x = to_dev(torch, table[prompt])
+    for b in blocks:
+        b.forward(x)
+    for step in range(2):
+        x = to_dev(torch, table[toks[6 + step]][None])
+        for b in blocks:
+            b.forward(x)
+    hid = orc.rmsnorm_forward(x.cpu().numpy(), M.fn, 1e-6)[0]
+    assert np.array_equal(model.last_hidden().cpu().numpy()[0], hid)
+    assert toks[8] == orc.argmax_first(orc.lm_head(hid, M.emb, simd=True))
+
+
+def test_model_batch_generate_equals_single(orc, torch_dev, tf):
+    M = Model(orc, SMALL, layers=1, vocab=700, seed=601)
+    prompts = np.stack([(np.arange(7) * (17 + b) + b) % 700 for b in range(3)])
+    big = M.gpu(tf, max_tokens=24, max_batch=3)
+    got = big.generate(prompts, 10)
+    for b in range(3):
+        one = M.gpu(tf, max_tokens=24)
+        assert np.array_equal(got[b], one.generate(prompts[b], 10)[0])
+
+
+def test_model_refuses_bad_calls(orc, torch_dev, tf):
+    from loom_amd._lib import AMDError
+    M = Model(orc, SMALL, layers=1, vocab=300, seed=701)
+    model = M.gpu(tf, max_tokens=16)
+    with pytest.raises(AMDError, match="prefill first"):
+        model.decode(1)
+    with pytest.raises(AMDError, match="prompt"):
+        model.prefill(np.zeros(16, np.int32))
+    model.prefill(np.zeros(10, np.int32))
+    with pytest.raises(AMDError, match="max_tokens"):
+        model.decode(6)
+    # ids outside the table embed as zero rows (poly/transformer.go:568-571)
+    model.prefill(np.array([5, 299, 300, -1, 1 << 30], np.int32))
+    model.decode(1)

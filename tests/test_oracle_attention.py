@@ -207,3 +207,17 @@ def test_block_is_norm_mha_add_norm_swiglu_add(orc):
     f = orc.swiglu_forward(g, u, d, y2, inner_norm=fn, eps=1e-5).out
     want = (f + h).astype(np.float32)
     assert np.array_equal(got, want)
+
+
+def test_mha_stages_compose_to_forward(orc):
+    # The stage entry points used by the GPU stage checks (attention, output
+    # projection) reproduce MHA.forward bit for bit.
+    m = make_mha(orc, seed=61)
+    S = 6
+    x = orc.normal_f32(S * HID, 62).reshape(S, HID)
+    pre, post, q, attn = m.forward(x)
+    a = orc.attention(q, m.cache_k.reshape(MSL, KV * HD), m.cache_v.reshape(MSL, KV * HD), 0, MSL,
+                      HEADS, KV, HD)
+    assert np.array_equal(a, attn)
+    p2, o2 = orc.attn_out(m.mats[3], attn, inner_norm=m.inner_norm, eps=1e-5)
+    assert np.array_equal(p2, pre) and np.array_equal(o2, post)
