@@ -12,8 +12,11 @@ bytes = N*ceil(K/16)*4 + 4*M*(K+N) (packed weights + fp32 in + fp32 out).
 
 Also reported: the dominant kernel's roofline (per-launch time from HIP events
 on the launch stream), the config-1 sweep (M in {1,8,64,512,4096} on both FFN
-shapes: GB/s for M <= 8, int8 TOPS for M >= 64), the fused SwiGLU FFN, and the
-CPU baseline: the oracle's restatement of loom's bitnet_simd path (AVX2 byte
+shapes: GB/s for M <= 8, int8 TOPS for M >= 64), the fused SwiGLU FFN, the
+config-2 decoder block (seq 512), the config-3 greedy decode (30 layers, vocab
+128256, 2048-token prompt, 256 tokens; tok/s) and the config-4 prefill (batch
+8 x 2048; tok/s and int8 TOPS of the ternary projections), and the CPU
+baseline: the oracle's restatement of loom's bitnet_simd path (AVX2 byte
 codes, row fan-out over the host cores) on a bounded sample of config 0.
 """
 from __future__ import annotations
@@ -103,6 +106,148 @@ def make_matrix(orc, n, k, seed):
     return orc.random_matrix(n, k, seed=seed)
 
 
+def random_ternary_words(rng, rows: int, cols: int):
+    """loom BitNetTernaryMatrix words with P(0)=.5, P(+1)=P(-1)=.25: each 2-bit
+    field f of a uniform word maps to code 01 (zero) for f<2, 10 (+1) for f=2,
+    00 (-1) for f=3 (codes 0/1/2 = -1/0/+1, poly/bitnet_cpu.go:498-507)."""
+    import numpy as np
+    rw = (cols + 15) // 16
+    w = rng.integers(0, 1 << 32, size=rows * rw, dtype=np.uint64).astype(np.uint32)
+    lo = w & np.uint32(0x55555555)
+    hi = (w >> np.uint32(1)) & np.uint32(0x55555555)
+    code = ((hi & ~lo & np.uint32(0x55555555)) << np.uint32(1)) | (~hi & np.uint32(0x55555555))
+    if cols % 16:
+        keep = np.uint32((1 << (2 * (cols % 16))) - 1)
+        code.reshape(rows, rw)[:, -1] &= keep
+    return code
+
+
+BITNET_2B = dict(hidden=2560, heads=20, kv_heads=5, head_dim=128, inter=6912, vocab=128256,
+                 layers=30, theta=500000.0)
+
+
+def ternary_ops_per_token(c) -> float:
+    """2 x (ternary weights per layer) x layers: int8 ops of the projections."""
+    h, q, kv, f = c["hidden"], c["heads"] * c["head_dim"], c["kv_heads"] * c["head_dim"], c["inter"]
+    per_layer = h * (q + 2 * kv) + q * h + 3 * h * f
+    return 2.0 * per_layer * c["layers"]
+
+
+def bench_model(args, torch, timer, log):
+    """Configs 2-4 on a random-init BitNet-2B-shape model."""
+    import numpy as np
+
+    from loom_amd import transformer as tf
+    from loom_amd.bitnet import TernaryMatrix
+
+    c = dict(BITNET_2B)
+    c["layers"] = args.model_layers
+    h, q_dim, kv_dim, inter = c["hidden"], c["heads"] * c["head_dim"], c["kv_heads"] * c["head_dim"], c["inter"]
+    prompt, gen, batch = 2048, 256, 8
+    msl = prompt + gen
+    rng = np.random.default_rng(2025)
+    t0 = time.perf_counter()
+
+    def mat(rows, cols):
+        return TernaryMatrix.from_words(random_ternary_words(rng, rows, cols), rows, cols,
+                                        float(rng.uniform(0.01, 0.03)))
+
+    def layer():
+        return tf.BlockWeights(
+            mat(q_dim, h), mat(kv_dim, h), mat(kv_dim, h), mat(h, q_dim), mat(inter, h),
+            mat(inter, h), mat(h, inter),
+            rng.uniform(0.5, 1.5, h).astype(np.float32), rng.uniform(0.5, 1.5, h).astype(np.float32),
+            rng.uniform(0.5, 1.5, q_dim).astype(np.float32),
+            rng.uniform(0.5, 1.5, inter).astype(np.float32))
+
+    out = {}
+    # ---- config 2: one block, seq 512, batch 1 -------------------------------
+    w0 = layer()
+    blocks = {}
+    for norm in ("strict", "fast"):
+        cfg = tf.BlockConfig(h, c["heads"], c["kv_heads"], c["head_dim"], inter, max_seq_len=512,
+                             rope_theta=c["theta"], norm_eps=1e-5, ffn_activation=6, norm=norm)
+        blocks[norm] = tf.BitNetBlock(cfg, w0)
+    x512 = torch.from_numpy(rng.standard_normal((512, h), dtype=np.float32)).cuda()
+    xs = x512.clone()
+    blk_res = []
+    for norm, blk in blocks.items():
+        def fwd(i, blk=blk):
+            xs.copy_(x512)
+            blk.forward(xs)
+        steps = 10
+        ms = timer.run(fwd, steps, 2, per_graph=5)
+        ops = ternary_ops_per_token(dict(c, layers=1)) * 512
+        blk_res.append({"norm": norm, "ms": round(ms, 3), "tok_s": round(512 / (ms * 1e-3), 1),
+                        "int8_TOPS_projections": round(ops / (ms * 1e-3) / 1e12, 2)})
+        log(f"config2 block seq512 {blk_res[-1]}")
+        blk.release()
+    out["block_seq512"] = {"config": "config2 BitNet-2B block (hidden 2560, 20/5 heads x 128, "
+                                     "FFN 6912 ReLU2-gated), seq 512, batch 1, fp32 norms, fp64 "
+                                     "attention", "runs": blk_res}
+
+    # ---- configs 3 and 4: the full stack ---------------------------------------
+    layers = [w0] + [layer() for _ in range(c["layers"] - 1)]
+    emb = rng.standard_normal((c["vocab"], h), dtype=np.float32)
+    fnorm = rng.uniform(0.5, 1.5, h).astype(np.float32)
+    log(f"model weights generated in {time.perf_counter() - t0:.1f}s")
+    res3, res4 = [], []
+    for norm in args.model_norms.split(","):
+        cfg = tf.BlockConfig(h, c["heads"], c["kv_heads"], c["head_dim"], inter, max_seq_len=msl,
+                             max_batch=batch, rope_theta=c["theta"], norm_eps=1e-5,
+                             ffn_activation=6, norm=norm)
+        t1 = time.perf_counter()
+        model = tf.Transformer(cfg, layers, emb, fnorm, vocab=c["vocab"], final_norm_eps=1e-5,
+                               max_tokens=msl + 1, max_prefill=prompt)
+        log(f"model ({norm}) on device in {time.perf_counter() - t1:.1f}s")
+        ids1 = rng.integers(0, c["vocab"], size=(1, prompt)).astype(np.int32)
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        # config 3: prefill 2048, then 256 greedy tokens through the captured step
+        model.prefill(ids1)
+        model.decode(4, use_graph=True)  # capture + upload the step graph
+        torch.cuda.synchronize()
+        ev0.record()
+        model.prefill(ids1)
+        ev1.record()
+        torch.cuda.synchronize()
+        t_pre1 = ev0.elapsed_time(ev1)
+        ev0.record()
+        model.decode(gen, use_graph=True)
+        ev1.record()
+        torch.cuda.synchronize()
+        t_dec = ev0.elapsed_time(ev1)
+        toks = model.tokens()
+        res3.append({"norm": norm, "decode_tok_s": round(gen / (t_dec * 1e-3), 2),
+                     "ms_per_token": round(t_dec / gen, 4), "prefill_ms": round(t_pre1, 2),
+                     "prefill_tok_s": round(prompt / (t_pre1 * 1e-3), 1),
+                     "last_tokens": toks[0, -4:].tolist()})
+        log(f"config3 decode {res3[-1]}")
+        # config 4: batch 8 x 2048 prefill
+        ids8 = rng.integers(0, c["vocab"], size=(batch, prompt)).astype(np.int32)
+        model.prefill(ids8)
+        torch.cuda.synchronize()
+        reps = 2
+        ev0.record()
+        for _ in range(reps):
+            model.prefill(ids8)
+        ev1.record()
+        torch.cuda.synchronize()
+        t4 = ev0.elapsed_time(ev1) / reps
+        ntok = batch * prompt
+        res4.append({"norm": norm, "ms": round(t4, 2), "tok_s": round(ntok / (t4 * 1e-3), 1),
+                     "int8_TOPS_projections": round(ternary_ops_per_token(c) * ntok / (t4 * 1e-3) / 1e12, 2)})
+        log(f"config4 prefill {res4[-1]}")
+        model.release()
+    out["decode"] = {"config": f"config3: {c['layers']} layers, vocab {c['vocab']}, tied fp32 "
+                               f"LM head, greedy, {prompt}-token random prompt, {gen} tokens, "
+                               "one HIP graph per token, positions on device",
+                     "runs": res3}
+    out["prefill"] = {"config": f"config4: batch {batch} x {prompt} random ids, M={batch * prompt} "
+                                "rows per ternary GEMM, KV cache per sequence",
+                      "runs": res4}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -110,6 +255,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-model", action="store_true", help="skip configs 2-4")
+    ap.add_argument("--model-layers", type=int, default=30)
+    ap.add_argument("--model-norms", default="fast,strict")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -231,6 +379,10 @@ def main() -> int:
                             "TOPS": round(3 * 2.0 * M * 2560 * 6912 / (t * 1e-3) / 1e12, 2)})
                 log(f"swiglu {ffn[-1]}")
         result["swiglu_ffn"] = ffn
+
+    # ---------------- configs 2-4: block, decode loop, batched prefill ------------
+    if not args.no_model:
+        result.update(bench_model(args, torch, timer, log))
 
     # ---------------- CPU baseline (oracle port of loom's bitnet_simd path) -------
     cores = cpu_cores()

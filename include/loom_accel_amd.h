@@ -217,6 +217,20 @@ int loom_amd_block_kv_offset(const loom_amd_block* b);
 int loom_amd_block_kv_cache(const loom_amd_block* b, int slot, const float** k,
                             const float** v);
 
+/* ---- LM head and greedy sampling -------------------------------------- */
+
+/* fp32 LM head (applyFP32LMHeadRows with SIMD on amd64,
+ * poly/transformer.go:673-720): logits[r][v] = DotTile(x[r], table[v]) with
+ * loom's eight-lane fp64 order (poly/simd/avx2_amd64.s:14-79).  table is
+ * vocab x hidden, x rows x hidden, logits rows x vocab (all DEVICE). */
+int loom_amd_lm_head(const float* table, int vocab, int hidden, const float* x, int rows,
+                     float* logits, void* stream);
+
+/* Greedy SampleTopK (k <= 1, poly/sampling.go:44-55) per row: the first
+ * index of the largest logit, 0 when logits[r][0] is NaN.  ids (DEVICE) gets
+ * one int32 per row. */
+int loom_amd_greedy_sample(const float* logits, int n, int rows, int32_t* ids, void* stream);
+
 /* ---- transformer decode (poly/transformer.go:330-520) ---------------- */
 
 typedef struct loom_amd_model loom_amd_model;

@@ -105,6 +105,8 @@ SIGNATURES = {
     "loom_amd_block_forward": (i32, [P, P, i32, i32, C.POINTER(BlockTaps), P]),
     "loom_amd_block_kv_offset": (i32, [P]),
     "loom_amd_block_kv_cache": (i32, [P, i32, C.POINTER(P), C.POINTER(P)]),
+    "loom_amd_lm_head": (i32, [P, i32, i32, P, i32, P, P]),
+    "loom_amd_greedy_sample": (i32, [P, i32, i32, P, P]),
     "loom_amd_model_create": (i32, [i32, C.POINTER(ModelDesc), C.POINTER(BlockWeights), P, P, P,
                                     C.POINTER(P)]),
     "loom_amd_model_release": (None, [P]),

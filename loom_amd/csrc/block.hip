@@ -265,17 +265,154 @@ hipError_t launch_qkv_rope(const int32_t* acc, const float* amax, float sq, floa
 }
 
 // ------------------------------------------------------------------------
-// Attention (poly/mha.go:316-354): one 256-thread workgroup per (head, query).
-// scores over positions 0..pos: fp64 dot over d in order, times 1/sqrt(hd);
-// running max from -1e9; exp(score - max); expSum over positions in order;
-// out[d] = sum over positions in order of p*V / expSum.  The GQA group of
-// head h is h / (heads / kv_heads).  Position kp reads ring row kp % msl of
-// the query's sequence slot (blockIdx.z).
-// The scores of one query live in LDS: `span` bounds the number of
-// positions a launch may see; a query past it gets NaN rows (the host
-// checks the span before launching, so this never happens in a valid call).
+// Attention (poly/mha.go:316-354).  For query row (b, s) at position pos0+s,
+// head h (GQA group kvh = h / (heads / kv_heads)), over positions
+// kp = 0..pos0+s of the sequence's ring (row kp; the host keeps every
+// position below msl, so no wrap occurs):
+//   score_kp = (sum over d in order of q_d * k_kp,d) * (1/sqrt(hd))
+//   max from -1e9; p_kp = exp(score_kp - max); expSum = sum over kp in order
+//   out_d = (sum over kp in order of p_kp * v_kp,d) / expSum
+// STRICT keeps every fp64 sum in that order; fast splits the position sums
+// into fixed slices combined in slice order.  The scores of one query live in
+// LDS: `span` bounds the positions a launch may see; a query past it gets NaN
+// rows (the host checks the span first, so a valid call never does).
+//
+// Two launch shapes: few query rows (decode) use a scores kernel with one
+// wave per 64 positions and a softmax/PV kernel of 1024 threads per head;
+// many rows (prefill) use one fused 256-thread workgroup per (head, row).
 // ------------------------------------------------------------------------
 
+// Sequential fp64 dot of a K row (fp32) with q (fp64 in LDS), d in order.
+// Loads run 16 floats ahead of the chain.
+__device__ __forceinline__ double dot_q_k(const double* __restrict__ qs,
+                                          const float* __restrict__ kr, int hd) {
+    double dot = 0.0;
+    int d = 0;
+    for (; d + 16 <= hd; d += 16) {
+        const float4 a = *(const float4*)(kr + d);
+        const float4 b = *(const float4*)(kr + d + 4);
+        const float4 c = *(const float4*)(kr + d + 8);
+        const float4 e = *(const float4*)(kr + d + 12);
+        dot += qs[d] * (double)a.x;
+        dot += qs[d + 1] * (double)a.y;
+        dot += qs[d + 2] * (double)a.z;
+        dot += qs[d + 3] * (double)a.w;
+        dot += qs[d + 4] * (double)b.x;
+        dot += qs[d + 5] * (double)b.y;
+        dot += qs[d + 6] * (double)b.z;
+        dot += qs[d + 7] * (double)b.w;
+        dot += qs[d + 8] * (double)c.x;
+        dot += qs[d + 9] * (double)c.y;
+        dot += qs[d + 10] * (double)c.z;
+        dot += qs[d + 11] * (double)c.w;
+        dot += qs[d + 12] * (double)e.x;
+        dot += qs[d + 13] * (double)e.y;
+        dot += qs[d + 14] * (double)e.z;
+        dot += qs[d + 15] * (double)e.w;
+    }
+    for (; d < hd; d += 4) {
+        const float4 a = *(const float4*)(kr + d);
+        dot += qs[d] * (double)a.x;
+        dot += qs[d + 1] * (double)a.y;
+        dot += qs[d + 2] * (double)a.z;
+        dot += qs[d + 3] * (double)a.w;
+    }
+    return dot;
+}
+
+// sum over kp in [k0, k1) in order of p[kp] * v[kp * ld] (v already offset by d);
+// eight V loads are issued ahead of the chain.
+__device__ __forceinline__ double pv_chain(const double* __restrict__ p, const float* __restrict__ v,
+                                           size_t ld, int k0, int k1, double sum) {
+    int kp = k0;
+    for (; kp + 8 <= k1; kp += 8) {
+        float t[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[j] = v[(size_t)(kp + j) * ld];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sum += p[kp + j] * (double)t[j];
+    }
+    for (; kp < k1; ++kp) sum += p[kp] * (double)v[(size_t)kp * ld];
+    return sum;
+}
+
+// max over [0, L) of LDS values, starting from -1e9 (NaN never wins)
+template <int T>
+__device__ __forceinline__ double block_max_f64(double v, double* red) {
+    red[threadIdx.x] = v;
+    __syncthreads();
+    for (int w = T >> 1; w > 0; w >>= 1) {
+        if (threadIdx.x < w) {
+            const double o = red[threadIdx.x + w];
+            if (o > red[threadIdx.x]) red[threadIdx.x] = o;
+        }
+        __syncthreads();
+    }
+    const double r = red[0];
+    __syncthreads();
+    return r;
+}
+
+template <int T>
+__device__ __forceinline__ double block_sum_f64(double v, double* red) {
+    red[threadIdx.x] = v;
+    __syncthreads();
+    for (int w = T >> 1; w > 0; w >>= 1) {
+        if (threadIdx.x < w) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + w];
+        __syncthreads();
+    }
+    const double r = red[0];
+    __syncthreads();
+    return r;
+}
+
+// softmax + PV over p[0..L) (scores in LDS on entry, probabilities after), T threads.
+template <int STRICT, int T>
+__device__ void softmax_pv(double* p, int L, const float* __restrict__ vbase, size_t ld, int hd,
+                           double* red, double* orow) {
+    double mx = -1e9;
+    for (int kp = threadIdx.x; kp < L; kp += T) {
+        const double v = p[kp];
+        if (v > mx) mx = v;
+    }
+    mx = block_max_f64<T>(mx, red);
+    for (int kp = threadIdx.x; kp < L; kp += T) p[kp] = exp(p[kp] - mx);
+    __syncthreads();
+    __shared__ double exp_sum_sh;
+    if (STRICT) {
+        // value chains on the first hd lanes, the expSum chain on the last wave
+        double sum = 0.0;
+        if ((int)threadIdx.x < hd) sum = pv_chain(p, vbase + threadIdx.x, ld, 0, L, 0.0);
+        if ((int)threadIdx.x == T - 64) {
+            double es = 0.0;
+            for (int kp = 0; kp < L; ++kp) es += p[kp];
+            exp_sum_sh = es;
+        }
+        __syncthreads();
+        if ((int)threadIdx.x < hd) orow[threadIdx.x] = sum / exp_sum_sh;
+    } else {
+        double es = 0.0;
+        for (int kp = threadIdx.x; kp < L; kp += T) es += p[kp];
+        es = block_sum_f64<T>(es, red);
+        const int slices = T / hd;  // hd <= 256 <= T
+        const int d = threadIdx.x % hd, sl = threadIdx.x / hd;
+        const int chunk = (L + slices - 1) / slices;
+        double sum = 0.0;
+        if (sl < slices) {
+            const int k0 = min(L, sl * chunk), k1 = min(L, k0 + chunk);
+            sum = pv_chain(p, vbase + d, ld, k0, k1, 0.0);
+        }
+        red[threadIdx.x] = sum;
+        __syncthreads();
+        if ((int)threadIdx.x < hd) {
+            double t = red[threadIdx.x];
+            for (int k = 1; k < slices; ++k) t = t + red[k * hd + threadIdx.x];
+            orow[threadIdx.x] = t / es;
+        }
+    }
+}
+
+// fused: one workgroup per (head, row); grid (heads, seq, batch)
 template <int STRICT>
 __global__ __launch_bounds__(256) void attention_kernel(const double* __restrict__ q,
                                                         const float* __restrict__ cache_k,
@@ -285,92 +422,110 @@ __global__ __launch_bounds__(256) void attention_kernel(const double* __restrict
                                                         double* __restrict__ out) {
     extern __shared__ double lds[];  // q[hd] then scores[span]
     __shared__ double red[256];
-    const int h = blockIdx.x;
-    const int s = blockIdx.y;
-    const int b = blockIdx.z;
+    const int h = blockIdx.x, s = blockIdx.y, b = blockIdx.z;
     const int row = b * gridDim.y + s;
     const int q_dim = heads * hd, kv_dim = kv_heads * hd;
     const int kvh = h / (heads / kv_heads);
-    const int L = *pos0 + s + 1;  // positions 0..pos0+s
-    cache_k += (size_t)b * msl * kv_dim;
-    cache_v += (size_t)b * msl * kv_dim;
+    const int L = *pos0 + s + 1;
     double* orow = out + (size_t)row * q_dim + (size_t)h * hd;
     if (L > span) {
         for (int d = threadIdx.x; d < hd; d += 256) orow[d] = __builtin_nan("");
         return;
     }
+    const float* kb = cache_k + (size_t)b * msl * kv_dim + (size_t)kvh * hd;
+    const float* vb = cache_v + (size_t)b * msl * kv_dim + (size_t)kvh * hd;
     double* qs = lds;
-    double* scores = lds + ((hd + 1) & ~1);  // 16-byte aligned
+    double* p = lds + ((hd + 1) & ~1);
     const double* qrow = q + (size_t)row * q_dim + (size_t)h * hd;
     for (int d = threadIdx.x; d < hd; d += 256) qs[d] = qrow[d];
     __syncthreads();
     const double scale = 1.0 / sqrt((double)hd);
-    double local_max = -1e9;
-    for (int kp = threadIdx.x; kp < L; kp += 256) {
-        const float* kr = cache_k + (size_t)(kp % msl) * kv_dim + (size_t)kvh * hd;
-        double dot = 0.0;
-        for (int d = 0; d < hd; d += 4) {
-            const float4 k4 = *(const float4*)(kr + d);
-            dot += qs[d] * (double)k4.x;
-            dot += qs[d + 1] * (double)k4.y;
-            dot += qs[d + 2] * (double)k4.z;
-            dot += qs[d + 3] * (double)k4.w;
-        }
-        const double sc = dot * scale;
-        scores[kp] = sc;
-        if (sc > local_max) local_max = sc;
-    }
-    // the maximum is exact in any order; NaN never replaces it
-    red[threadIdx.x] = local_max;
+    for (int kp = threadIdx.x; kp < L; kp += 256) p[kp] = dot_q_k(qs, kb + (size_t)kp * kv_dim, hd) * scale;
     __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-        if (threadIdx.x < w) {
-            const double o = red[threadIdx.x + w];
-            if (o > red[threadIdx.x]) red[threadIdx.x] = o;
-        }
-        __syncthreads();
-    }
-    const double mx = red[0];
-    for (int kp = threadIdx.x; kp < L; kp += 256) scores[kp] = exp(scores[kp] - mx);
-    const double exp_sum = lds_sum<STRICT>(scores, L, red);
-    const float* vbase = cache_v + (size_t)kvh * hd;
-    if (STRICT) {
-        // one lane per d sums its column in position order
-        for (int d = threadIdx.x; d < hd; d += 256) {
-            double sum = 0.0;
-            for (int kp = 0; kp < L; ++kp) sum += scores[kp] * (double)vbase[(size_t)(kp % msl) * kv_dim + d];
-            orow[d] = sum / exp_sum;
-        }
-    } else {
-        // 256 threads = (256 / hd) position slices x hd columns, slices then
-        // combined in slice order
-        const int slices = 256 / hd;
-        const int d = threadIdx.x % hd;
-        const int sl = threadIdx.x / hd;
-        double sum = 0.0;
-        if (sl < slices) {
-            for (int kp = sl; kp < L; kp += slices) sum += scores[kp] * (double)vbase[(size_t)(kp % msl) * kv_dim + d];
-        }
-        red[threadIdx.x] = sum;
-        __syncthreads();
-        if (threadIdx.x < hd) {
-            double t = red[threadIdx.x];
-            for (int k = 1; k < slices; ++k) t = t + red[k * hd + threadIdx.x];
-            orow[threadIdx.x] = t / exp_sum;
-        }
+    softmax_pv<STRICT, 256>(p, L, vb, kv_dim, hd, red, orow);
+}
+
+// decode, part 1: scores of one head for 64 positions per wave;
+// grid (heads, ceil(span/64), rows), scores laid out rows x heads x span
+__global__ __launch_bounds__(64) void attn_scores_kernel(const double* __restrict__ q,
+                                                         const float* __restrict__ cache_k,
+                                                         const int* __restrict__ pos0, int msl,
+                                                         int span, int heads, int kv_heads, int hd,
+                                                         int seq, double* __restrict__ scores) {
+    __shared__ double qs[256];
+    const int h = blockIdx.x, row = blockIdx.z;
+    const int b = row / seq, s = row % seq;
+    const int kvh = h / (heads / kv_heads);
+    const int q_dim = heads * hd, kv_dim = kv_heads * hd;
+    const int L = min(*pos0 + s + 1, span);
+    const int kp = blockIdx.y * 64 + threadIdx.x;
+    if (blockIdx.y * 64 >= L) return;  // uniform over the workgroup
+    const double* qrow = q + (size_t)row * q_dim + (size_t)h * hd;
+    for (int d = threadIdx.x; d < hd; d += 64) qs[d] = qrow[d];
+    __syncthreads();
+    if (kp < L) {
+        const float* kr = cache_k + (size_t)b * msl * kv_dim + (size_t)kp * kv_dim + (size_t)kvh * hd;
+        scores[((size_t)row * heads + h) * span + kp] = dot_q_k(qs, kr, hd) * (1.0 / sqrt((double)hd));
     }
 }
 
-// LDS bytes of one attention workgroup for `span` positions.
+// decode, part 2: softmax + PV of one (head, row) with 1024 threads
+template <int STRICT>
+__global__ __launch_bounds__(1024) void attn_pv_kernel(const double* __restrict__ scores,
+                                                       const float* __restrict__ cache_v,
+                                                       const int* __restrict__ pos0, int msl,
+                                                       int span, int heads, int kv_heads, int hd,
+                                                       int seq, double* __restrict__ out) {
+    extern __shared__ double p[];  // span
+    __shared__ double red[1024];
+    const int h = blockIdx.x, row = blockIdx.y;
+    const int b = row / seq, s = row % seq;
+    const int kvh = h / (heads / kv_heads);
+    const int q_dim = heads * hd, kv_dim = kv_heads * hd;
+    const int L = *pos0 + s + 1;
+    double* orow = out + (size_t)row * q_dim + (size_t)h * hd;
+    if (L > span) {
+        for (int d = threadIdx.x; d < hd; d += 1024) orow[d] = __builtin_nan("");
+        return;
+    }
+    const double* sc = scores + ((size_t)row * heads + h) * span;
+    for (int kp = threadIdx.x; kp < L; kp += 1024) p[kp] = sc[kp];
+    __syncthreads();
+    const float* vb = cache_v + (size_t)b * msl * kv_dim + (size_t)kvh * hd;
+    softmax_pv<STRICT, 1024>(p, L, vb, kv_dim, hd, red, orow);
+}
+
+// LDS bytes of one fused attention workgroup for `span` positions.
 size_t attention_lds_bytes(int hd, int span) {
     return ((size_t)((hd + 1) & ~1) + (size_t)span) * sizeof(double);
 }
 
+size_t attention_scratch_bytes(int rows, int heads, int span) {
+    return rows <= kSplitMaxRows ? (size_t)rows * heads * span * sizeof(double) : 0;
+}
+
 hipError_t launch_attention(const double* q, const float* cache_k, const float* cache_v,
                             int batch, int seq, const int* pos0, int msl, int span, int heads,
-                            int kv_heads, int hd, int strict, double* out, hipStream_t s) {
+                            int kv_heads, int hd, int strict, double* scratch, double* out,
+                            hipStream_t s) {
     if (seq <= 0 || batch <= 0) return hipSuccess;
     if (hd % 4 != 0 || hd > 256 || kv_heads <= 0 || heads % kv_heads != 0) return hipErrorInvalidValue;
+    if (span > kMaxAttnSpan || span > msl) return hipErrorInvalidValue;
+    const int rows = batch * seq;
+    if (rows <= kSplitMaxRows) {
+        if (!scratch) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(attn_scores_kernel, dim3(heads, ceil_div(span, 64), rows), dim3(64), 0, s,
+                           q, cache_k, pos0, msl, span, heads, kv_heads, hd, seq, scratch);
+        const size_t shm = (size_t)span * sizeof(double);
+        if (strict) {
+            hipLaunchKernelGGL(attn_pv_kernel<1>, dim3(heads, rows), dim3(1024), shm, s, scratch,
+                               cache_v, pos0, msl, span, heads, kv_heads, hd, seq, out);
+        } else {
+            hipLaunchKernelGGL(attn_pv_kernel<0>, dim3(heads, rows), dim3(1024), shm, s, scratch,
+                               cache_v, pos0, msl, span, heads, kv_heads, hd, seq, out);
+        }
+        return hipGetLastError();
+    }
     const size_t shm = attention_lds_bytes(hd, span);
     if (shm > kMaxAttnLds) return hipErrorInvalidValue;
     const dim3 grid(heads, seq, batch);
@@ -544,6 +699,7 @@ __global__ __launch_bounds__(256) void lm_head_kernel(const float* __restrict__ 
     x += (size_t)blockIdx.y * hidden;
     logits += (size_t)blockIdx.y * vocab;
     for (int i = tid; i < hidden; i += 256) xs[i] = x[i];
+    __syncthreads();
     const int row = tid >> 3;   // logit within the workgroup
     const int lane = tid & 7;   // DotTile lane
     const int full = (hidden / 8) * 8;
@@ -607,17 +763,24 @@ hipError_t launch_lm_head(const float* table, int vocab, int hidden, const float
 // index 0 is never replaced.  One 1024-thread workgroup.
 // ------------------------------------------------------------------------
 
-__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ logits, int n,
-                                                      int* __restrict__ tokens, int cap,
-                                                      const int* __restrict__ pos0, int offset) {
-    __shared__ float bv[1024];
-    __shared__ int bi[1024];
-    logits += (size_t)blockIdx.x * n;
+// (value, index) order of the greedy pick: larger value first, then the
+// smaller index; NaN never wins.
+__device__ __forceinline__ bool beats(float v, int i, float bv, int bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
+// stage 1: partial argmax of `chunk` consecutive logits per workgroup
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ logits, int n,
+                                                             int chunk, float2* __restrict__ part) {
+    __shared__ float bv[256];
+    __shared__ int bi[256];
+    const float* lg = logits + (size_t)blockIdx.y * n;
+    const int i0 = blockIdx.x * chunk, i1 = min(n, i0 + chunk);
     float best = -INFINITY;
     int idx = 0x7fffffff;
-    for (int i = threadIdx.x; i < n; i += 1024) {
-        const float v = logits[i];
-        if (v > best || (v == best && i < idx)) {
+    for (int i = i0 + threadIdx.x; i < i1; i += 256) {
+        const float v = lg[i];
+        if (beats(v, i, best, idx)) {
             best = v;
             idx = i;
         }
@@ -625,31 +788,61 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
     bv[threadIdx.x] = best;
     bi[threadIdx.x] = idx;
     __syncthreads();
-    for (int w = 512; w > 0; w >>= 1) {
-        if (threadIdx.x < w) {
-            const float o = bv[threadIdx.x + w];
-            const int oi = bi[threadIdx.x + w];
-            if (o > bv[threadIdx.x] || (o == bv[threadIdx.x] && oi < bi[threadIdx.x])) {
-                bv[threadIdx.x] = o;
-                bi[threadIdx.x] = oi;
-            }
+    for (int w = 128; w > 0; w >>= 1) {
+        if (threadIdx.x < w && beats(bv[threadIdx.x + w], bi[threadIdx.x + w], bv[threadIdx.x], bi[threadIdx.x])) {
+            bv[threadIdx.x] = bv[threadIdx.x + w];
+            bi[threadIdx.x] = bi[threadIdx.x + w];
         }
         __syncthreads();
     }
     if (threadIdx.x == 0) {
-        const float first = logits[0];
-        int r = bi[0];
+        part[(size_t)blockIdx.y * gridDim.x + blockIdx.x] = make_float2(bv[0], __int_as_float(bi[0]));
+    }
+}
+
+// stage 2: combine the partials of one row and store the token
+__global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restrict__ logits, int n,
+                                                          const float2* __restrict__ part, int parts,
+                                                          int* __restrict__ tokens, int cap,
+                                                          const int* __restrict__ pos0, int offset) {
+    const float2* pr = part + (size_t)blockIdx.x * parts;
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int j = threadIdx.x; j < parts; j += 64) {
+        const float2 e = pr[j];
+        const int i = __float_as_int(e.y);
+        if (beats(e.x, i, best, idx)) {
+            best = e.x;
+            idx = i;
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_down(best, off, 64);
+        const int oi = __shfl_down(idx, off, 64);
+        if (beats(ov, oi, best, idx)) {
+            best = ov;
+            idx = oi;
+        }
+    }
+    if (threadIdx.x == 0) {
+        const float first = logits[(size_t)blockIdx.x * n];
+        int r = idx;
         if (first != first || r == 0x7fffffff) r = 0;  // NaN at 0, or nothing comparable
         const int p = (pos0 ? *pos0 : 0) + offset;
         if (p < cap) tokens[(size_t)blockIdx.x * cap + p] = r;
     }
 }
 
-hipError_t launch_argmax(const float* logits, int n, int rows, int* tokens, int cap,
+int argmax_parts(int n) { return min(kArgmaxMaxParts, max(1, ceil_div(n, 4096))); }
+
+hipError_t launch_argmax(const float* logits, int n, int rows, float2* part, int* tokens, int cap,
                          const int* pos0, int offset, hipStream_t s) {
     if (n <= 0 || rows <= 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(1024), 0, s, logits, n, tokens, cap, pos0,
-                       offset);
+    const int parts = argmax_parts(n);
+    const int chunk = ceil_div(n, parts);
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(parts, rows), dim3(256), 0, s, logits, n, chunk, part);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(rows), dim3(64), 0, s, logits, n, part, parts, tokens,
+                       cap, pos0, offset);
     return hipGetLastError();
 }
 

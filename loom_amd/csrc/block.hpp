@@ -29,11 +29,16 @@ hipError_t launch_qkv_rope(const int32_t* acc, const float* amax, float sq, floa
                            double* q, float* cache_k, float* cache_v, hipStream_t s);
 
 // Causal attention of batch x seq queries at positions *pos0 + s over each
-// sequence's ring cache.  span >= *pos0 + seq must hold (LDS holds span scores).
+// sequence's ring cache.  span >= *pos0 + seq must hold (LDS holds span
+// scores) and span <= msl.  Up to kSplitMaxRows query rows take the split
+// decode path, which needs `scratch` (attention_scratch_bytes).
+constexpr int kSplitMaxRows = 16;
 size_t attention_lds_bytes(int hd, int span);
+size_t attention_scratch_bytes(int rows, int heads, int span);
 hipError_t launch_attention(const double* q, const float* cache_k, const float* cache_v,
                             int batch, int seq, const int* pos0, int msl, int span, int heads,
-                            int kv_heads, int hd, int strict, double* out, hipStream_t s);
+                            int kv_heads, int hd, int strict, double* scratch, double* out,
+                            hipStream_t s);
 
 // MHA inner norm on fp64 rows in place (data *= scale*w) + fp64 requantization.
 // pre (optional) receives fp32 of the normalized rows.  eps <= 0 selects 1e-5.
@@ -54,7 +59,10 @@ hipError_t launch_lm_head(const float* table, int vocab, int hidden, const float
 
 // Greedy sampling per logits row b: first strict maximum (index 0 when
 // logits[0] is NaN), written to tokens[b*cap + *pos0 + offset] when < cap.
-hipError_t launch_argmax(const float* logits, int n, int rows, int* tokens, int cap,
+// Two launches; `part` holds rows x argmax_parts(n) partial results.
+constexpr int kArgmaxMaxParts = 64;
+int argmax_parts(int n);
+hipError_t launch_argmax(const float* logits, int n, int rows, float2* part, int* tokens, int cap,
                          const int* pos0, int offset, hipStream_t s);
 
 hipError_t launch_set_int(int* p, int v, hipStream_t s);

@@ -44,6 +44,7 @@ struct Workspace {
     int32_t* acc = nullptr;  // rows x (q_dim + 2 kv_dim)
     double* q = nullptr;     // rows x q_dim
     double* attn = nullptr;  // rows x q_dim
+    double* scores = nullptr;  // min(rows, kSplitMaxRows) x heads x span (decode attention)
     int8_t* aq = nullptr;    // rows x pad(q_dim)
     float* amax2 = nullptr;
     int32_t* xsum2 = nullptr;
@@ -62,6 +63,8 @@ static size_t workspace_layout(const BlockDev& B, int rows, Workspace* W, char* 
     const size_t o_acc = L.take(r * (B.q_dim + 2 * B.kv_dim) * 4);
     const size_t o_q = L.take(r * B.q_dim * 8);
     const size_t o_at = L.take(r * B.q_dim * 8);
+    const size_t o_sc = L.take(attention_scratch_bytes(rows < kSplitMaxRows ? rows : kSplitMaxRows,
+                                                       B.heads, B.span()));
     const size_t o_aq = L.take(r * pad_cols(B.q_dim));
     const size_t o_am2 = L.take(r * 4);
     const size_t o_xs2 = L.take(r * 4);
@@ -79,6 +82,7 @@ static size_t workspace_layout(const BlockDev& B, int rows, Workspace* W, char* 
         W->acc = (int32_t*)(base + o_acc);
         W->q = (double*)(base + o_q);
         W->attn = (double*)(base + o_at);
+        W->scores = (double*)(base + o_sc);
         W->aq = (int8_t*)(base + o_aq);
         W->amax2 = (float*)(base + o_am2);
         W->xsum2 = (int32_t*)(base + o_xs2);
@@ -298,7 +302,7 @@ static int block_forward_dev(const BlockDev& B, const Workspace& W, float* x, in
         return fail_hip("block taps", e);
     }
     e = launch_attention(W.q, B.cache_k, B.cache_v, batch, seq, pos, B.msl, B.span(), B.heads,
-                         B.kv_heads, B.hd, B.strict, W.attn, s);
+                         B.kv_heads, B.hd, B.strict, W.scores, W.attn, s);
     if (e != hipSuccess) return fail_hip("block attention", e);
     if (taps && (e = tap_copy(taps->attn, W.attn, (size_t)R * B.q_dim * 8, s)) != hipSuccess) {
         return fail_hip("block taps", e);
@@ -379,11 +383,13 @@ struct loom_amd_model {
     float* fin = nullptr;         // max_batch x hidden
     float* logits = nullptr;      // max_batch x vocab
     int* tokens = nullptr;        // max_batch x max_tokens
+    float2* argmax_part = nullptr;  // max_batch x kArgmaxMaxParts
     int* pos = nullptr;           // device position shared by every layer
     void* misc = nullptr;
     int batch = 0;                // batch of the current sequences
     int shadow = 0;               // host copy of the position
     hipStream_t own = nullptr;
+    hipEvent_t ev_in = nullptr, ev_out = nullptr;
     hipGraphExec_t graph = nullptr;
     int graph_batch = 0;
 };
@@ -466,6 +472,29 @@ int loom_amd_block_kv_cache(const loom_amd_block* b, int slot, const float** k, 
     return 0;
 }
 
+int loom_amd_lm_head(const float* table, int vocab, int hidden, const float* x, int rows,
+                     float* logits, void* stream) {
+    if (!table || !x || !logits) return fail("null buffer");
+    if (vocab <= 0 || hidden <= 0 || rows < 0) return fail("bad shape");
+    if ((size_t)hidden * 4 > 64 * 1024) return fail("hidden is limited to 16384");
+    if (rows == 0) return 0;
+    hipError_t e = launch_lm_head(table, vocab, hidden, x, rows, logits, (hipStream_t)stream);
+    return e == hipSuccess ? 0 : fail_hip("lm_head", e);
+}
+
+int loom_amd_greedy_sample(const float* logits, int n, int rows, int32_t* ids, void* stream) {
+    if (!logits || !ids) return fail("null buffer");
+    if (n <= 0 || rows < 0) return fail("bad shape");
+    if (rows == 0) return 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail("no current device");
+    std::string err;
+    void* part = scratch(dev, (size_t)rows * kArgmaxMaxParts * sizeof(float2), &err);
+    if (!part) return fail(err);
+    hipError_t e = launch_argmax(logits, n, rows, (float2*)part, ids, 1, nullptr, 0, (hipStream_t)stream);
+    return e == hipSuccess ? 0 : fail_hip("greedy_sample", e);
+}
+
 // ---- model -----------------------------------------------------------------
 
 static void free_model(loom_amd_model* m) {
@@ -476,6 +505,8 @@ static void free_model(loom_amd_model* m) {
     free_workspace(&m->ws);
     if (m->misc) (void)hipFree(m->misc);
     if (m->own) (void)hipStreamDestroy(m->own);
+    if (m->ev_in) (void)hipEventDestroy(m->ev_in);
+    if (m->ev_out) (void)hipEventDestroy(m->ev_out);
     delete m;
 }
 
@@ -522,6 +553,7 @@ int loom_amd_model_create(int device, const loom_amd_model_desc* desc,
     const size_t o_fin = L.take((size_t)max_batch * H * 4);
     const size_t o_lg = L.take((size_t)max_batch * desc->vocab * 4);
     const size_t o_tok = L.take((size_t)max_batch * max_tokens * 4);
+    const size_t o_part = L.take((size_t)max_batch * kArgmaxMaxParts * sizeof(float2));
     const size_t o_pos = L.take(4);
     hipError_t e = hipMalloc(&m->misc, L.off);
     if (e != hipSuccess) {
@@ -536,6 +568,7 @@ int loom_amd_model_create(int device, const loom_amd_model_desc* desc,
     m->fin = (float*)(base + o_fin);
     m->logits = (float*)(base + o_lg);
     m->tokens = (int*)(base + o_tok);
+    m->argmax_part = (float2*)(base + o_part);
     m->pos = (int*)(base + o_pos);
     e = hipMemcpy(m->embeddings, embeddings, (size_t)desc->vocab * H * 4, hipMemcpyHostToDevice);
     if (e == hipSuccess && lm_head) {
@@ -547,6 +580,8 @@ int loom_amd_model_create(int device, const loom_amd_model_desc* desc,
     if (e == hipSuccess) e = hipMemset(m->tokens, 0, (size_t)max_batch * max_tokens * 4);
     if (e == hipSuccess) e = hipMemset(m->pos, 0, sizeof(int));
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&m->own, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_in, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_out, hipEventDisableTiming);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         free_model(m);
@@ -585,7 +620,8 @@ static int model_head(loom_amd_model* m, const float* last, long ld, int batch, 
     h = m->fin;
     e = launch_lm_head(m->lm_head, m->vocab, m->hidden, h, batch, m->logits, s);
     if (e != hipSuccess) return fail_hip("model lm head", e);
-    e = launch_argmax(m->logits, m->vocab, batch, m->tokens, m->max_tokens, m->pos, offset, s);
+    e = launch_argmax(m->logits, m->vocab, batch, m->argmax_part, m->tokens, m->max_tokens, m->pos,
+                      offset, s);
     if (e != hipSuccess) return fail_hip("model argmax", e);
     return 0;
 }
@@ -658,16 +694,12 @@ int loom_amd_model_decode(loom_amd_model* m, int steps, int use_graph, float* lo
     hipStream_t s = (hipStream_t)stream;
     hipError_t e = hipSuccess;
     if (use_graph) {
-        // capture on the model's own stream, ordered after the caller's work
+        // replay on the model's own stream, ordered after the caller's work and
+        // before the caller's later work by the model's two events
         hipStream_t cs = m->own;
-        hipEvent_t ev = nullptr;
-        e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
-        if (e == hipSuccess) e = hipEventRecord(ev, s);
-        if (e == hipSuccess) e = hipStreamWaitEvent(cs, ev, 0);
-        if (e != hipSuccess) {
-            if (ev) (void)hipEventDestroy(ev);
-            return fail_hip("model decode", e);
-        }
+        e = hipEventRecord(m->ev_in, s);
+        if (e == hipSuccess) e = hipStreamWaitEvent(cs, m->ev_in, 0);
+        if (e != hipSuccess) return fail_hip("model decode", e);
         if (!m->graph || m->graph_batch != m->batch) {
             if (m->graph) {
                 (void)hipGraphExecDestroy(m->graph);
@@ -675,30 +707,24 @@ int loom_amd_model_decode(loom_amd_model* m, int steps, int use_graph, float* lo
             }
             hipGraph_t g = nullptr;
             e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
-            if (e != hipSuccess) {
-                (void)hipEventDestroy(ev);
-                return fail_hip("model decode capture", e);
-            }
+            if (e != hipSuccess) return fail_hip("model decode capture", e);
             const int rc = decode_step(m, cs);
             hipError_t ec = hipStreamEndCapture(cs, &g);
             if (rc || ec != hipSuccess) {
                 if (g) (void)hipGraphDestroy(g);
-                (void)hipEventDestroy(ev);
                 return rc ? -1 : fail_hip("model decode capture", ec);
             }
             e = hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0);
             (void)hipGraphDestroy(g);
             if (e != hipSuccess) {
                 m->graph = nullptr;
-                (void)hipEventDestroy(ev);
                 return fail_hip("model decode instantiate", e);
             }
             m->graph_batch = m->batch;
         }
         for (int i = 0; i < steps && e == hipSuccess; ++i) e = hipGraphLaunch(m->graph, cs);
-        if (e == hipSuccess) e = hipEventRecord(ev, cs);
-        if (e == hipSuccess) e = hipStreamWaitEvent(s, ev, 0);
-        (void)hipEventDestroy(ev);
+        if (e == hipSuccess) e = hipEventRecord(m->ev_out, cs);
+        if (e == hipSuccess) e = hipStreamWaitEvent(s, m->ev_out, 0);
         if (e != hipSuccess) return fail_hip("model decode replay", e);
     } else {
         for (int i = 0; i < steps; ++i) {

@@ -187,6 +187,38 @@ def _clone_device(ptr: int, shape: tuple, device: int, typestr: str = "<f4"):
     return torch.as_tensor(_DeviceView(ptr, shape, typestr), device=f"cuda:{device}").clone()
 
 
+def lm_head(table, x):
+    """applyFP32LMHeadRows (SIMD order) on device: table [vocab, hidden], x
+    [rows, hidden] float32 device tensors -> logits [rows, vocab]."""
+    torch = _torch()
+    for t in (table, x):
+        if t.dtype != torch.float32 or not t.is_cuda or not t.is_contiguous():
+            raise ValueError("table and x must be contiguous float32 device tensors")
+    x2 = x.reshape(-1, x.shape[-1])
+    vocab, hidden = table.shape
+    if x2.shape[1] != hidden:
+        raise ValueError("hidden sizes differ")
+    out = torch.empty(x2.shape[0], vocab, dtype=torch.float32, device=x.device)
+    check(_lib.lib().loom_amd_lm_head(C.c_void_p(table.data_ptr()), vocab, hidden,
+                                      C.c_void_p(x2.data_ptr()), x2.shape[0],
+                                      C.c_void_p(out.data_ptr()), _stream(x.device.index or 0)),
+          "lm_head")
+    return out
+
+
+def greedy_sample(logits):
+    """SampleTopK with k <= 1 per row of a float32 device tensor -> int32 ids."""
+    torch = _torch()
+    lg = logits.reshape(-1, logits.shape[-1])
+    if lg.dtype != torch.float32 or not lg.is_cuda or not lg.is_contiguous():
+        raise ValueError("logits must be a contiguous float32 device tensor")
+    ids = torch.empty(lg.shape[0], dtype=torch.int32, device=lg.device)
+    check(_lib.lib().loom_amd_greedy_sample(C.c_void_p(lg.data_ptr()), lg.shape[1], lg.shape[0],
+                                            C.c_void_p(ids.data_ptr()),
+                                            _stream(lg.device.index or 0)), "greedy_sample")
+    return ids
+
+
 class Transformer:
     """A stack of BitNet blocks with fp32 embeddings, final RMSNorm and fp32 LM
     head (tied to the embeddings when lm_head is None), decoding greedily."""
@@ -277,4 +309,5 @@ class Transformer:
             pass
 
 
-__all__ = ["BlockConfig", "BlockWeights", "BlockTaps", "BitNetBlock", "Transformer", "NORM_STRICT"]
+__all__ = ["BlockConfig", "BlockWeights", "BlockTaps", "BitNetBlock", "Transformer", "NORM_STRICT",
+           "lm_head", "greedy_sample"]

@@ -350,9 +350,12 @@ def test_model_decode_graph_matches_eager(orc, torch_dev, tf):
     model = M.gpu(tf, max_tokens=48)
     prompt = (np.arange(9) * 101 + 3) % 1000
     model.prefill(prompt)
+    model.decode(4, use_graph=True)  # capture, then replay after a new prefill
+    model.prefill(prompt)
     lg_graph = model.decode(20, use_graph=True, logits=True).cpu().numpy()
     t_graph = model.tokens()
     assert model.position == 29
+    assert t_graph.min() >= 0 and t_graph.max() < 1000
     model.prefill(prompt)
     lg_eager = model.decode(20, use_graph=False, logits=True).cpu().numpy()
     t_eager = model.tokens()
@@ -416,3 +419,44 @@ def test_model_refuses_bad_calls(orc, torch_dev, tf):
     # ids outside the table embed as zero rows (poly/transformer.go:568-571)
     model.prefill(np.array([5, 299, 300, -1, 1 << 30], np.int32))
     model.decode(1)
+
+
+# ---------------------------------------------------------------- LM head / sampling
+@pytest.mark.parametrize("vocab,hidden", [(1, 8), (33, 7), (100, 64), (257, 100), (1000, 2560),
+                                          (70, 2567), (5000, 320)])
+def test_lm_head_dottile_order(orc, torch_dev, tf, vocab, hidden):
+    # applyFP32LMHeadRows with SIMD (poly/transformer.go:679-681): DotTile's
+    # eight-lane order (poly/simd/avx2_amd64.s), bit-exact; several rows.
+    torch = torch_dev
+    table = orc.normal_f32(vocab * hidden, 17 + hidden) * np.float32(0.05)
+    rows = [orc.normal_f32(hidden, 29 + r) for r in range(3)]
+    got = tf.lm_head(to_dev(torch, table.reshape(vocab, hidden)), to_dev(torch, np.stack(rows)))
+    got = got.cpu().numpy()
+    for r, x in enumerate(rows):
+        assert np.array_equal(got[r], orc.lm_head(x, table, simd=True)), (vocab, hidden, r)
+
+
+def test_greedy_sample_semantics(orc, torch_dev, tf):
+    # SampleTopK greedy (poly/sampling.go:44-55): first strict maximum; NaN
+    # never wins; a NaN at index 0 is never replaced.  Rows long enough to
+    # span several partial ranges, with ties placed across range borders.
+    torch = torch_dev
+    n = 128256
+    rows = []
+    base = orc.normal_f32(n, 5)
+    rows.append(base.copy())
+    r = base.copy(); r[4007] = 9.0; r[4008] = 9.0; r[100000] = 9.0; rows.append(r)   # tie across ranges
+    r = base.copy(); r[0] = np.nan; r[77] = 50.0; rows.append(r)                     # NaN at 0
+    r = base.copy(); r[5] = np.nan; r[n - 1] = 50.0; rows.append(r)                 # NaN elsewhere, max last
+    r = np.full(n, -np.inf, np.float32); rows.append(r)                              # all -inf
+    r = np.full(n, np.nan, np.float32); r[3] = 1.0; r[0] = 0.5; rows.append(r)
+    r = np.full(n, 2.0, np.float32); rows.append(r)                                  # all equal
+    x = np.stack(rows)
+    ids = tf.greedy_sample(to_dev(torch, x)).cpu().numpy()
+    want = [orc.argmax_first(row) for row in rows]
+    assert ids.tolist() == want
+    assert want[1] == 4007 and want[2] == 0 and want[3] == n - 1 and want[4] == 0
+    for m in (1, 2, 4095, 4096, 4097, 70000):
+        row = orc.normal_f32(m, m)
+        got = tf.greedy_sample(to_dev(torch, row[None])).cpu().numpy()[0]
+        assert got == orc.argmax_first(row), m
