@@ -21,20 +21,7 @@ __device__ double lds_sum(const double* terms, int n, double* scratch256) {
     __shared__ double result;
     __syncthreads();
     if (STRICT) {
-        if (threadIdx.x == 0) {
-            // terms must be 16-byte aligned: pairs are read two at a time,
-            // the additions stay in index order
-            const double2* t2 = (const double2*)terms;
-            double s = 0.0;
-            int i = 0;
-            for (; i + 2 <= n; i += 2) {
-                const double2 p = t2[i >> 1];
-                s += p.x;
-                s += p.y;
-            }
-            if (i < n) s += terms[i];
-            result = s;
-        }
+        if (threadIdx.x == 0) result = ordered_sum(terms, n, 0.0);
         __syncthreads();
         return result;
     }
@@ -445,54 +432,240 @@ __global__ __launch_bounds__(256) void attention_kernel(const double* __restrict
     softmax_pv<STRICT, 256>(p, L, vb, kv_dim, hd, red, orow);
 }
 
-// decode, part 1: scores of one head for 64 positions per wave;
-// grid (heads, ceil(span/64), rows), scores laid out rows x heads x span
+// ---- decode path (few query rows) ----------------------------------------
+// Scratch layout per (row, head): scores[span] (probabilities after the exp
+// step), chunk maxima cmax[nchunk] (64 positions per chunk), and for the
+// fast path partial sums part[nsplit][hd] plus partial expSums pes[nsplit].
+
+struct DecodeScratch {
+    double* scores;  // rows x heads x span
+    double* cmax;    // rows x heads x nchunk
+    double* part;    // rows x heads x nchunk x hd
+    double* pes;     // rows x heads x nchunk
+};
+
+__host__ __device__ inline int attn_nchunk(int span) { return (span + 63) / 64; }
+
+// part 1: scores for 64 positions per wave of one head, and the maximum of
+// each 64-position chunk.  q is wave-uniform, so it is read through the
+// scalar cache; each lane reads its K row (128 floats at a time, all loads
+// issued before the chain).  grid (heads, nchunk, rows)
 __global__ __launch_bounds__(64) void attn_scores_kernel(const double* __restrict__ q,
                                                          const float* __restrict__ cache_k,
                                                          const int* __restrict__ pos0, int msl,
                                                          int span, int heads, int kv_heads, int hd,
-                                                         int seq, double* __restrict__ scores) {
-    __shared__ double qs[256];
+                                                         int seq, DecodeScratch sc) {
     const int h = blockIdx.x, row = blockIdx.z;
-    const int b = row / seq, s = row % seq;
     const int kvh = h / (heads / kv_heads);
+    const int b = row / seq, s = row % seq;
     const int q_dim = heads * hd, kv_dim = kv_heads * hd;
     const int L = min(*pos0 + s + 1, span);
-    const int kp = blockIdx.y * 64 + threadIdx.x;
-    if (blockIdx.y * 64 >= L) return;  // uniform over the workgroup
-    const double* qrow = q + (size_t)row * q_dim + (size_t)h * hd;
-    for (int d = threadIdx.x; d < hd; d += 64) qs[d] = qrow[d];
-    __syncthreads();
+    const int chunk = blockIdx.y;
+    if (chunk * 64 >= L) return;  // uniform over the workgroup
+    const double* qr = q + (size_t)row * q_dim + (size_t)h * hd;
+    const int kp = chunk * 64 + threadIdx.x;
+    const int nchunk = attn_nchunk(span);
+    double dot = 0.0;
     if (kp < L) {
         const float* kr = cache_k + (size_t)b * msl * kv_dim + (size_t)kp * kv_dim + (size_t)kvh * hd;
-        scores[((size_t)row * heads + h) * span + kp] = dot_q_k(qs, kr, hd) * (1.0 / sqrt((double)hd));
+        for (int d0 = 0; d0 < hd; d0 += 128) {
+            const int n4 = min(32, (hd - d0) >> 2);
+            float4 kk[32];
+#pragma unroll
+            for (int i = 0; i < 32; ++i)
+                if (i < n4) kk[i] = *(const float4*)(kr + d0 + 4 * i);
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                if (i < n4) {
+                    const int d = d0 + 4 * i;
+                    dot += qr[d] * (double)kk[i].x;
+                    dot += qr[d + 1] * (double)kk[i].y;
+                    dot += qr[d + 2] * (double)kk[i].z;
+                    dot += qr[d + 3] * (double)kk[i].w;
+                }
+            }
+        }
+    }
+    const size_t rh = (size_t)row * heads + h;
+    double m = -1e9;
+    if (kp < L) {
+        const double v = dot * (1.0 / sqrt((double)hd));
+        sc.scores[rh * span + kp] = v;
+        m = v;
+    }
+    // chunk maximum (exact in any order; NaN never wins)
+    for (int off = 32; off > 0; off >>= 1) {
+        const double o = __shfl_xor(m, off, 64);
+        m = o > m ? o : m;
+    }
+    if (threadIdx.x == 0) sc.cmax[rh * nchunk + chunk] = m;
+}
+
+// maximum over the chunk maxima of (row, head): -1e9 start, NaN never wins
+__device__ __forceinline__ double global_max(const double* cm, int nc, double* red64) {
+    double m = -1e9;
+    for (int c = threadIdx.x; c < nc; c += 64) {
+        const double v = cm[c];
+        m = v > m ? v : m;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const double o = __shfl_xor(m, off, 64);
+        m = o > m ? o : m;
+    }
+    return m;
+}
+
+// fast part 2: probabilities, partial expSum and partial PV of one
+// 64-position chunk; grid (heads, nchunk, rows), 256 threads.
+__global__ __launch_bounds__(256) void attn_pv_partial_kernel(const float* __restrict__ cache_v,
+                                                              const int* __restrict__ pos0, int msl,
+                                                              int span, int heads, int kv_heads,
+                                                              int hd, int seq, DecodeScratch sc) {
+    extern __shared__ float vs[];  // V rows of the chunk: 64 x (hd + 4) floats
+    __shared__ double ps[64];
+    __shared__ double red[256];
+    const int h = blockIdx.x, chunk = blockIdx.y, row = blockIdx.z;
+    const int b = row / seq, s = row % seq;
+    const int kvh = h / (heads / kv_heads);
+    const int kv_dim = kv_heads * hd;
+    const int L = min(*pos0 + s + 1, span);
+    const int k0 = chunk * 64;
+    if (k0 >= L) return;
+    const int n = min(64, L - k0);
+    const int nchunk = attn_nchunk(span);
+    const size_t rh = (size_t)row * heads + h;
+    // V rows of the chunk -> LDS (all loads in flight at once)
+    const float* vb = cache_v + (size_t)b * msl * kv_dim + (size_t)kvh * hd;
+    const int per_row4 = hd / 4;
+    for (int i = threadIdx.x; i < n * per_row4; i += 256) {
+        const int r = i / per_row4, c4 = (i % per_row4) * 4;
+        *(float4*)&vs[r * (hd + 4) + c4] = *(const float4*)(vb + (size_t)(k0 + r) * kv_dim + c4);
+    }
+    if (threadIdx.x < 64) {
+        const int k = k0 + threadIdx.x;
+        const double sv = threadIdx.x < n ? sc.scores[rh * span + k] : 0.0;
+        const double m = global_max(sc.cmax + rh * nchunk, (L + 63) / 64, nullptr);
+        ps[threadIdx.x] = threadIdx.x < n ? exp(sv - m) : 0.0;
+    }
+    __syncthreads();
+    // partial expSum: fixed tree over the 64 probabilities
+    if (threadIdx.x < 64) {
+        double e = ps[threadIdx.x];
+        for (int off = 32; off > 0; off >>= 1) e = e + __shfl_down(e, off, 64);
+        if (threadIdx.x == 0) sc.pes[rh * nchunk + chunk] = e;
+    }
+    // partial PV: (256 / hd) slices of the chunk per column, combined in order
+    const int slices = 256 / hd;
+    const int d = threadIdx.x % hd, sl = threadIdx.x / hd;
+    const int per = (n + slices - 1) / slices;
+    double sum = 0.0;
+    if (sl < slices) {
+        const int a0 = min(n, sl * per), a1 = min(n, a0 + per);
+        for (int k = a0; k < a1; ++k) sum += ps[k] * (double)vs[k * (hd + 4) + d];
+    }
+    red[threadIdx.x] = sum;
+    __syncthreads();
+    if ((int)threadIdx.x < hd) {
+        double t = red[threadIdx.x];
+        for (int k = 1; k < slices; ++k) t = t + red[k * hd + threadIdx.x];
+        sc.part[(rh * nchunk + chunk) * hd + threadIdx.x] = t;
     }
 }
 
-// decode, part 2: softmax + PV of one (head, row) with 1024 threads
-template <int STRICT>
-__global__ __launch_bounds__(1024) void attn_pv_kernel(const double* __restrict__ scores,
-                                                       const float* __restrict__ cache_v,
-                                                       const int* __restrict__ pos0, int msl,
-                                                       int span, int heads, int kv_heads, int hd,
-                                                       int seq, double* __restrict__ out) {
-    extern __shared__ double p[];  // span
-    __shared__ double red[1024];
+// fast part 3: combine the chunk partials in chunk order; grid (heads, rows)
+__global__ __launch_bounds__(256) void attn_combine_kernel(const int* __restrict__ pos0, int span,
+                                                           int heads, int hd, int seq,
+                                                           DecodeScratch sc,
+                                                           double* __restrict__ out) {
     const int h = blockIdx.x, row = blockIdx.y;
+    const int s = row % seq;
+    const int L = *pos0 + s + 1;
+    const int q_dim = heads * hd;
+    double* orow = out + (size_t)row * q_dim + (size_t)h * hd;
+    if (L > span) {
+        for (int d = threadIdx.x; d < hd; d += 256) orow[d] = __builtin_nan("");
+        return;
+    }
+    const int nc = (L + 63) / 64, nchunk = attn_nchunk(span);
+    const size_t rh = (size_t)row * heads + h;
+    // sums in chunk order; eight loads are in flight ahead of each eight adds
+    double es = 0.0;
+    for (int c0 = 0; c0 < nc; c0 += 8) {
+        double v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = c0 + i < nc ? sc.pes[rh * nchunk + c0 + i] : 0.0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (c0 + i < nc) es += v[i];
+    }
+    for (int d = threadIdx.x; d < hd; d += 256) {
+        double t = 0.0;
+        for (int c0 = 0; c0 < nc; c0 += 8) {
+            double v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = c0 + i < nc ? sc.part[(rh * nchunk + c0 + i) * hd + d] : 0.0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (c0 + i < nc) t += v[i];
+        }
+        orow[d] = t / es;
+    }
+}
+
+// strict part 2: probabilities in place of the scores; grid (heads, nchunk, rows), 64 threads
+__global__ __launch_bounds__(64) void attn_exp_kernel(const int* __restrict__ pos0, int span,
+                                                      int heads, int seq, DecodeScratch sc) {
+    const int h = blockIdx.x, chunk = blockIdx.y, row = blockIdx.z;
+    const int s = row % seq;
+    const int L = min(*pos0 + s + 1, span);
+    const int k = chunk * 64 + threadIdx.x;
+    if (chunk * 64 >= L) return;
+    const int nchunk = attn_nchunk(span);
+    const size_t rh = (size_t)row * heads + h;
+    const double m = global_max(sc.cmax + rh * nchunk, (L + 63) / 64, nullptr);
+    if (k < L) sc.scores[rh * span + k] = exp(sc.scores[rh * span + k] - m);
+}
+
+// strict part 3: ND value columns per workgroup; p and the columns are staged
+// in LDS, then one lane per column adds in position order (first wave) and a
+// lane of the second wave forms expSum in position order.
+// grid (heads, hd / ND, rows), 128 threads.
+template <int ND>
+__global__ __launch_bounds__(128) void attn_chain_kernel(const float* __restrict__ cache_v,
+                                                        const int* __restrict__ pos0, int msl,
+                                                        int span, int heads, int kv_heads, int hd,
+                                                        int seq, DecodeScratch sc,
+                                                        double* __restrict__ out) {
+    extern __shared__ double lds[];  // p[span], then ND columns of span floats
+    const int h = blockIdx.x, d0 = blockIdx.y * ND, row = blockIdx.z;
     const int b = row / seq, s = row % seq;
     const int kvh = h / (heads / kv_heads);
     const int q_dim = heads * hd, kv_dim = kv_heads * hd;
     const int L = *pos0 + s + 1;
     double* orow = out + (size_t)row * q_dim + (size_t)h * hd;
     if (L > span) {
-        for (int d = threadIdx.x; d < hd; d += 1024) orow[d] = __builtin_nan("");
+        if (threadIdx.x < ND) orow[d0 + threadIdx.x] = __builtin_nan("");
         return;
     }
-    const double* sc = scores + ((size_t)row * heads + h) * span;
-    for (int kp = threadIdx.x; kp < L; kp += 1024) p[kp] = sc[kp];
+    double* p = lds;
+    float* vc = (float*)(lds + span);
+    const double* pr = sc.scores + ((size_t)row * heads + h) * span;
+    for (int k = threadIdx.x; k < L; k += 128) p[k] = pr[k];
+    const float* vb = cache_v + (size_t)b * msl * kv_dim + (size_t)kvh * hd + d0;
+    for (int i = threadIdx.x; i < L * ND; i += 128) {
+        const int k = i / ND, j = i % ND;
+        vc[j * span + k] = vb[(size_t)k * kv_dim + j];
+    }
     __syncthreads();
-    const float* vb = cache_v + (size_t)b * msl * kv_dim + (size_t)kvh * hd;
-    softmax_pv<STRICT, 1024>(p, L, vb, kv_dim, hd, red, orow);
+    __shared__ double es_sh;
+    double sum = 0.0;
+    if ((int)threadIdx.x < ND) {
+        sum = ordered_dot(p, vc + threadIdx.x * span, L, 0.0);
+    } else if ((int)threadIdx.x == 64) {
+        es_sh = ordered_sum(p, L, 0.0);
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < ND) orow[d0 + threadIdx.x] = sum / es_sh;
 }
 
 // LDS bytes of one fused attention workgroup for `span` positions.
@@ -500,8 +673,30 @@ size_t attention_lds_bytes(int hd, int span) {
     return ((size_t)((hd + 1) & ~1) + (size_t)span) * sizeof(double);
 }
 
-size_t attention_scratch_bytes(int rows, int heads, int span) {
-    return rows <= kSplitMaxRows ? (size_t)rows * heads * span * sizeof(double) : 0;
+static size_t chain_lds(int span, int nd) { return (size_t)span * 8 + (size_t)span * nd * 4; }
+
+static int chain_nd(int span, int hd) {
+    if (hd % 2 == 0 && chain_lds(span, 2) <= kMaxAttnLds) return 2;
+    if (chain_lds(span, 1) <= kMaxAttnLds) return 1;
+    return 0;  // strict decode falls back to the fused kernel
+}
+
+size_t attention_scratch_bytes(int rows, int heads, int hd, int span) {
+    if (rows > kSplitMaxRows) return 0;
+    const size_t rh = (size_t)rows * heads;
+    const size_t nc = attn_nchunk(span);
+    return rh * ((size_t)span + nc + nc * hd + nc) * sizeof(double);
+}
+
+static DecodeScratch decode_scratch(double* base, int rows, int heads, int hd, int span) {
+    const size_t rh = (size_t)rows * heads;
+    const size_t nc = attn_nchunk(span);
+    DecodeScratch sc;
+    sc.scores = base;
+    sc.cmax = sc.scores + rh * span;
+    sc.part = sc.cmax + rh * nc;
+    sc.pes = sc.part + rh * nc * hd;
+    return sc;
 }
 
 hipError_t launch_attention(const double* q, const float* cache_k, const float* cache_v,
@@ -512,17 +707,30 @@ hipError_t launch_attention(const double* q, const float* cache_k, const float* 
     if (hd % 4 != 0 || hd > 256 || kv_heads <= 0 || heads % kv_heads != 0) return hipErrorInvalidValue;
     if (span > kMaxAttnSpan || span > msl) return hipErrorInvalidValue;
     const int rows = batch * seq;
-    if (rows <= kSplitMaxRows) {
+    const int nd = chain_nd(span, hd);
+    if (rows <= kSplitMaxRows && (!strict || nd > 0)) {
         if (!scratch) return hipErrorInvalidValue;
-        hipLaunchKernelGGL(attn_scores_kernel, dim3(heads, ceil_div(span, 64), rows), dim3(64), 0, s,
-                           q, cache_k, pos0, msl, span, heads, kv_heads, hd, seq, scratch);
-        const size_t shm = (size_t)span * sizeof(double);
-        if (strict) {
-            hipLaunchKernelGGL(attn_pv_kernel<1>, dim3(heads, rows), dim3(1024), shm, s, scratch,
-                               cache_v, pos0, msl, span, heads, kv_heads, hd, seq, out);
+        const DecodeScratch sc = decode_scratch(scratch, rows, heads, hd, span);
+        const int nc = attn_nchunk(span);
+        hipLaunchKernelGGL(attn_scores_kernel, dim3(heads, nc, rows), dim3(64), 0, s, q, cache_k, pos0,
+                           msl, span, heads, kv_heads, hd, seq, sc);
+        if (!strict) {
+            hipLaunchKernelGGL(attn_pv_partial_kernel, dim3(heads, nc, rows), dim3(256),
+                               (size_t)64 * (hd + 4) * sizeof(float), s,
+                               cache_v, pos0, msl, span, heads, kv_heads, hd, seq, sc);
+            hipLaunchKernelGGL(attn_combine_kernel, dim3(heads, rows), dim3(256), 0, s, pos0, span,
+                               heads, hd, seq, sc, out);
         } else {
-            hipLaunchKernelGGL(attn_pv_kernel<0>, dim3(heads, rows), dim3(1024), shm, s, scratch,
-                               cache_v, pos0, msl, span, heads, kv_heads, hd, seq, out);
+            hipLaunchKernelGGL(attn_exp_kernel, dim3(heads, nc, rows), dim3(64), 0, s, pos0, span,
+                               heads, seq, sc);
+            const size_t shm = chain_lds(span, nd);
+            if (nd == 2) {
+                hipLaunchKernelGGL(attn_chain_kernel<2>, dim3(heads, hd / 2, rows), dim3(128), shm, s,
+                                   cache_v, pos0, msl, span, heads, kv_heads, hd, seq, sc, out);
+            } else {
+                hipLaunchKernelGGL(attn_chain_kernel<1>, dim3(heads, hd, rows), dim3(128), shm, s,
+                                   cache_v, pos0, msl, span, heads, kv_heads, hd, seq, sc, out);
+            }
         }
         return hipGetLastError();
     }

@@ -34,7 +34,7 @@ hipError_t launch_qkv_rope(const int32_t* acc, const float* amax, float sq, floa
 // decode path, which needs `scratch` (attention_scratch_bytes).
 constexpr int kSplitMaxRows = 16;
 size_t attention_lds_bytes(int hd, int span);
-size_t attention_scratch_bytes(int rows, int heads, int span);
+size_t attention_scratch_bytes(int rows, int heads, int hd, int span);
 hipError_t launch_attention(const double* q, const float* cache_k, const float* cache_v,
                             int batch, int seq, const int* pos0, int msl, int span, int heads,
                             int kv_heads, int hd, int strict, double* scratch, double* out,

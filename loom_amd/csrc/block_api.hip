@@ -64,7 +64,7 @@ static size_t workspace_layout(const BlockDev& B, int rows, Workspace* W, char* 
     const size_t o_q = L.take(r * B.q_dim * 8);
     const size_t o_at = L.take(r * B.q_dim * 8);
     const size_t o_sc = L.take(attention_scratch_bytes(rows < kSplitMaxRows ? rows : kSplitMaxRows,
-                                                       B.heads, B.span()));
+                                                       B.heads, B.hd, B.span()));
     const size_t o_aq = L.take(r * pad_cols(B.q_dim));
     const size_t o_am2 = L.take(r * 4);
     const size_t o_xs2 = L.take(r * 4);
@@ -277,23 +277,37 @@ static hipError_t tap_copy(void* dst, const void* src, size_t bytes, hipStream_t
     return hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s);
 }
 
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
 // Enqueues one block forward on x (rows = batch*seq) at device position *pos.
+// Without taps, few rows take the decode path: each row norm runs inside the
+// matmul that consumes it (launch_matmul_norm).
 static int block_forward_dev(const BlockDev& B, const Workspace& W, float* x, int batch, int seq,
                              const int* pos, const loom_amd_block_taps* taps, hipStream_t s) {
     const int R = batch * seq;
     const int ldh = pad_cols(B.hidden), ldqd = pad_cols(B.q_dim), ldi = pad_cols(B.inter);
+    const double rms_eps = B.norm_eps > 0 ? B.norm_eps : 1e-6;   // RMSNormForwardPolymorphic
+    const double attn_eps = B.attn_eps > 0 ? B.attn_eps : 1e-5;  // bitNetRMSNormFloat64Weighted
+    const double ffn_eps = B.ffn_eps > 0 ? B.ffn_eps : 1e-5;     // bitNetRMSNormTensorRowWeighted
+    const bool fuse = taps == nullptr && aligned16(x);
     hipError_t e;
     // x := x + MHA(RMSNorm1(x))
-    e = launch_rmsnorm_quant(x, B.hidden, R, B.hidden, B.norm1, B.norm_eps, B.strict,
-                             taps ? taps->y1 : nullptr, W.xq, ldh, W.amax, W.xsum, s);
-    if (e != hipSuccess) return fail_hip("block rmsnorm1", e);
     {
         Epilogue ep;
         ep.kind = EPI_ACC;
         ep.acc0 = W.acc;
-        QuantAct a{W.xq, ldh, W.amax, W.xsum};
-        e = launch_matmul(&B.qkv, nullptr, a, R, ep, s);
-        if (e != hipSuccess) return fail_hip("block qkv projection", e);
+        if (fuse && norm_fused_ok(R, B.hidden, B.strict, true)) {
+            e = launch_matmul_norm(&B.qkv, nullptr, x, nullptr, R, NORM_RMS, B.strict, B.norm1,
+                                   rms_eps, ep, W.amax, s);
+            if (e != hipSuccess) return fail_hip("block rmsnorm1 + qkv projection", e);
+        } else {
+            e = launch_rmsnorm_quant(x, B.hidden, R, B.hidden, B.norm1, rms_eps, B.strict,
+                                     taps ? taps->y1 : nullptr, W.xq, ldh, W.amax, W.xsum, s);
+            if (e != hipSuccess) return fail_hip("block rmsnorm1", e);
+            QuantAct a{W.xq, ldh, W.amax, W.xsum};
+            e = launch_matmul(&B.qkv, nullptr, a, R, ep, s);
+            if (e != hipSuccess) return fail_hip("block qkv projection", e);
+        }
     }
     e = launch_qkv_rope(W.acc, W.amax, B.sq, B.sk, B.sv, B.bq, B.bk, B.bv, batch, seq, pos, B.msl,
                         B.heads, B.kv_heads, B.hd, B.theta, W.q, B.cache_k, B.cache_v, s);
@@ -307,9 +321,6 @@ static int block_forward_dev(const BlockDev& B, const Workspace& W, float* x, in
     if (taps && (e = tap_copy(taps->attn, W.attn, (size_t)R * B.q_dim * 8, s)) != hipSuccess) {
         return fail_hip("block taps", e);
     }
-    e = launch_norm_quant_f64(W.attn, R, B.q_dim, B.attn_norm, B.attn_eps, B.strict, nullptr, W.aq,
-                              ldqd, W.amax2, W.xsum2, s);
-    if (e != hipSuccess) return fail_hip("block attention inner norm", e);
     {
         Epilogue ep;
         ep.kind = EPI_DENSE;
@@ -317,39 +328,60 @@ static int block_forward_dev(const BlockDev& B, const Workspace& W, float* x, in
         ep.residual = x;
         ep.out = x;
         ep.ldo = B.hidden;
-        QuantAct a{W.aq, ldqd, W.amax2, W.xsum2};
-        e = launch_matmul(&B.o, nullptr, a, R, ep, s);
-        if (e != hipSuccess) return fail_hip("block o projection", e);
+        if (fuse && norm_fused_ok(R, B.q_dim, B.strict, true)) {
+            e = launch_matmul_norm(&B.o, nullptr, nullptr, W.attn, R, NORM_INNER_F64, B.strict,
+                                   B.attn_norm, attn_eps, ep, nullptr, s);
+            if (e != hipSuccess) return fail_hip("block attention inner norm + o projection", e);
+        } else {
+            e = launch_norm_quant_f64(W.attn, R, B.q_dim, B.attn_norm, attn_eps, B.strict, nullptr,
+                                      W.aq, ldqd, W.amax2, W.xsum2, s);
+            if (e != hipSuccess) return fail_hip("block attention inner norm", e);
+            QuantAct a{W.aq, ldqd, W.amax2, W.xsum2};
+            e = launch_matmul(&B.o, nullptr, a, R, ep, s);
+            if (e != hipSuccess) return fail_hip("block o projection", e);
+        }
     }
     if (taps && (e = tap_copy(taps->mid, x, (size_t)R * B.hidden * 4, s)) != hipSuccess) {
         return fail_hip("block taps", e);
     }
     // x := x + SwiGLU(RMSNorm2(x))
-    e = launch_rmsnorm_quant(x, B.hidden, R, B.hidden, B.norm2, B.norm_eps, B.strict, nullptr,
-                             W.xq, ldh, W.amax, W.xsum, s);
-    if (e != hipSuccess) return fail_hip("block rmsnorm2", e);
     {
         Epilogue ep;
         ep.kind = EPI_SWIGLU;
         ep.activation = B.activation;
         ep.out = W.h;
         ep.ldo = B.inter;
-        QuantAct a{W.xq, ldh, W.amax, W.xsum};
-        e = launch_matmul(&B.gate, &B.up, a, R, ep, s);
-        if (e != hipSuccess) return fail_hip("block gate/up", e);
+        if (fuse && norm_fused_ok(R, B.hidden, B.strict, true)) {
+            e = launch_matmul_norm(&B.gate, &B.up, x, nullptr, R, NORM_RMS, B.strict, B.norm2,
+                                   rms_eps, ep, nullptr, s);
+            if (e != hipSuccess) return fail_hip("block rmsnorm2 + gate/up", e);
+        } else {
+            e = launch_rmsnorm_quant(x, B.hidden, R, B.hidden, B.norm2, rms_eps, B.strict, nullptr,
+                                     W.xq, ldh, W.amax, W.xsum, s);
+            if (e != hipSuccess) return fail_hip("block rmsnorm2", e);
+            QuantAct a{W.xq, ldh, W.amax, W.xsum};
+            e = launch_matmul(&B.gate, &B.up, a, R, ep, s);
+            if (e != hipSuccess) return fail_hip("block gate/up", e);
+        }
     }
-    e = launch_norm_quant(W.h, B.inter, R, B.inter, B.ffn_norm, B.ffn_eps, B.strict, W.hq, ldi,
-                          W.amax3, W.xsum3, s);
-    if (e != hipSuccess) return fail_hip("block ffn inner norm", e);
     {
         Epilogue ep;
         ep.kind = EPI_DENSE;
         ep.residual = x;
         ep.out = x;
         ep.ldo = B.hidden;
-        QuantAct a{W.hq, ldi, W.amax3, W.xsum3};
-        e = launch_matmul(&B.down, nullptr, a, R, ep, s);
-        if (e != hipSuccess) return fail_hip("block down", e);
+        if (fuse && norm_fused_ok(R, B.inter, B.strict, true)) {
+            e = launch_matmul_norm(&B.down, nullptr, W.h, nullptr, R, NORM_INNER_F32, B.strict,
+                                   B.ffn_norm, ffn_eps, ep, nullptr, s);
+            if (e != hipSuccess) return fail_hip("block ffn inner norm + down", e);
+        } else {
+            e = launch_norm_quant(W.h, B.inter, R, B.inter, B.ffn_norm, ffn_eps, B.strict, W.hq, ldi,
+                                  W.amax3, W.xsum3, s);
+            if (e != hipSuccess) return fail_hip("block ffn inner norm", e);
+            QuantAct a{W.hq, ldi, W.amax3, W.xsum3};
+            e = launch_matmul(&B.down, nullptr, a, R, ep, s);
+            if (e != hipSuccess) return fail_hip("block down", e);
+        }
     }
     return 0;
 }

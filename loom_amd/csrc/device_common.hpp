@@ -68,6 +68,103 @@ __device__ __forceinline__ int wave_sum_i(int v) {
     return v;
 }
 
+// DPP wave reductions (full-rate VALU lane moves instead of LDS-crossbar
+// shuffles).  The pattern is fixed: row_shr 1, 2, 4, 8 inside each 16-lane
+// row, then row_bcast 15 and 31 across rows; lane 63 ends with the total,
+// which readlane broadcasts.  Lanes without a source add the identity.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v, int identity) {
+    return __builtin_amdgcn_update_dpp(identity, v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v, double identity) {
+    const long long b = __double_as_longlong(v), id = __double_as_longlong(identity);
+    const int lo = __builtin_amdgcn_update_dpp((int)id, (int)b, CTRL, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp((int)(id >> 32), (int)(b >> 32), CTRL, 0xf, 0xf, false);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
+constexpr int kDppShr1 = 0x111, kDppShr2 = 0x112, kDppShr4 = 0x114, kDppShr8 = 0x118;
+constexpr int kDppBcast15 = 0x142, kDppBcast31 = 0x143;
+
+__device__ __forceinline__ double readlane63_d(double v) {
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int)b, 63);
+    const int hi = __builtin_amdgcn_readlane((int)(b >> 32), 63);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
+
+// fixed-order fp64 wave sum, broadcast to every lane
+__device__ __forceinline__ double wave_sum_f64_dpp(double v) {
+    v = v + dpp_d<kDppShr1>(v, 0.0);
+    v = v + dpp_d<kDppShr2>(v, 0.0);
+    v = v + dpp_d<kDppShr4>(v, 0.0);
+    v = v + dpp_d<kDppShr8>(v, 0.0);
+    v = v + dpp_d<kDppBcast15>(v, 0.0);
+    v = v + dpp_d<kDppBcast31>(v, 0.0);
+    return readlane63_d(v);
+}
+
+__device__ __forceinline__ int wave_sum_i_dpp(int v) {
+    v += dpp_i<kDppShr1>(v, 0);
+    v += dpp_i<kDppShr2>(v, 0);
+    v += dpp_i<kDppShr4>(v, 0);
+    v += dpp_i<kDppShr8>(v, 0);
+    v += dpp_i<kDppBcast15>(v, 0);
+    v += dpp_i<kDppBcast31>(v, 0);
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
+// max of non-negative floats (NaN never wins): compared as float values
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    int b = __float_as_int(v);
+#define LAMD_MAX_STEP(C)                                                        \
+    {                                                                           \
+        const float o = __int_as_float(dpp_i<C>(b, 0));                         \
+        b = __float_as_int(max_nan_skip(__int_as_float(b), o));                 \
+    }
+    LAMD_MAX_STEP(kDppShr1)
+    LAMD_MAX_STEP(kDppShr2)
+    LAMD_MAX_STEP(kDppShr4)
+    LAMD_MAX_STEP(kDppShr8)
+    LAMD_MAX_STEP(kDppBcast15)
+    LAMD_MAX_STEP(kDppBcast31)
+#undef LAMD_MAX_STEP
+    return __int_as_float(__builtin_amdgcn_readlane(b, 63));
+}
+
+// Sum of n fp64 terms in index order (one lane): terms are read from LDS
+// sixteen at a time ahead of the dependent additions.
+__device__ __forceinline__ double ordered_sum(const double* t, int n, double s) {
+    int i = 0;
+    for (; i + 16 <= n; i += 16) {
+        double v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = t[i + j];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s += v[j];
+    }
+    for (; i < n; ++i) s += t[i];
+    return s;
+}
+
+// sum over k in index order of p[k] * (double)v[k] (LDS operands), same read-ahead.
+__device__ __forceinline__ double ordered_dot(const double* p, const float* v, int n, double s) {
+    int i = 0;
+    for (; i + 16 <= n; i += 16) {
+        double a[16];
+        float b[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            a[j] = p[i + j];
+            b[j] = v[i + j];
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s += a[j] * (double)b[j];
+    }
+    for (; i < n; ++i) s += p[i] * (double)v[i];
+    return s;
+}
+
 // Block reductions over blockDim.x threads (a multiple of 64, at most 1024).
 __device__ inline float block_max(float v, float* sh) {
     v = wave_max(v);
@@ -202,6 +299,10 @@ struct MatArgs {
     int k;
     int8_t* xq_tap;    // fused path: quantized rows written by workgroup 0 (optional)
     float* amax_tap;
+    // norm-fused path: the rows are normalized before the quantization
+    const double* x64;  // fp64 rows (NORM_INNER_F64), ldx = K
+    const float* nw;    // gain / inner-norm weight (length K), null = ones
+    double neps;        // eps of the norm
     EpiDev e;
 };
 

@@ -98,6 +98,25 @@ bool fused_quant_ok(int m, int k, const float* x);
 hipError_t launch_matmul_fused(const Matrix* w0, const Matrix* w1, const float* x, int m,
                                const Epilogue& epi, int8_t* xq_tap, float* amax_tap,
                                hipStream_t s);
+// Row norms a decode matmul can apply to its own input rows before the int8
+// quantization (M <= 4 rows), so the norm needs no launch of its own.
+enum RowNorm : int {
+    NORM_NONE = 0,
+    NORM_RMS = 1,        // RMSNormForwardPolymorphic: y = f32((x / rms) * g), fp32 rows
+    NORM_INNER_F32 = 2,  // bitNetRMSNormTensorRowWeighted: y = f32(x * scale * w), fp32 rows
+    NORM_INNER_F64 = 3,  // bitNetRMSNormFloat64Weighted: y = x * (scale * w), fp64 rows
+};
+// Whether launch_matmul_norm takes m rows of width k (x16 is the row pointer's
+// 16-byte alignment).
+bool norm_fused_ok(int m, int k, int strict, bool x16);
+// Matmul whose workgroups normalize (mode, strict summation order, gain nw,
+// eps) and quantize the rows x (fp32) or x64 (fp64, NORM_INNER_F64)
+// themselves.  eps is used as given.  amax_tap (optional, M floats) receives
+// the rows' activation absmax.
+hipError_t launch_matmul_norm(const Matrix* w0, const Matrix* w1, const float* x, const double* x64,
+                              int m, int mode, int strict, const float* nw, double eps,
+                              const Epilogue& epi, float* amax_tap, hipStream_t s);
+
 // Inner RMSNorm + requantization of SwiGLU rows (poly/bitnet_cpu.go:893-913 then
 // poly/bitnet_cpu.go:97-106).  In place on h (M x n fp32, row stride ldh).
 hipError_t launch_norm_quant(float* h, int ldh, int m, int n, const float* weight, double eps,

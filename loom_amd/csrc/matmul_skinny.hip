@@ -17,16 +17,36 @@ namespace lamd {
 hipError_t launch_gemm(const MatArgs& p, bool two, hipStream_t s);
 
 constexpr int kFusedMaxRows = 4;
-constexpr int kFusedVec = 16;  // float4 per thread in the fused prologue
+constexpr int kFusedVec = 16;  // float4 per thread in the fused prologue (max)
 
-template <int NMAT, int MSUB, int WAVES, bool FUSEQ>
+// Row of element group idx (4 elements) among M <= 4 rows of row4 groups.
+__device__ __forceinline__ int row_of(int idx, int row4) {
+    return (idx >= row4) + (idx >= 2 * row4) + (idx >= 3 * row4);
+}
+
+// Fixed-order wave sum: lane 0 gets ((v0+v32)+(v16..))... the same tree in
+// every workgroup.
+__device__ __forceinline__ double wave_sum_f64_lane0(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = v + __shfl_down(v, off, 64);
+    return v;
+}
+
+// NORM: RowNorm applied before the quantization (FUSEQ only).  STRICT sums
+// the squares of the (single) row in element order on one lane, from LDS.
+// FV: element groups (4 values) per thread.
+template <int NMAT, int MSUB, int WAVES, bool FUSEQ, int NORM = NORM_NONE, int STRICT = 0,
+          int FV = kFusedVec>
 __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
     constexpr int T = WAVES * 64;
     constexpr int U = 4 / MSUB;  // K tiles per batch per wave
-    extern __shared__ __align__(16) int8_t xq_s[];  // FUSEQ: M rows x ldq
+    extern __shared__ __align__(16) int8_t xq_s[];  // FUSEQ: M rows x ldq (STRICT: k squares first)
     __shared__ int red[NMAT][MSUB * 16][16];
     __shared__ unsigned amax_bits[kFusedMaxRows];
     __shared__ int xsum_s[kFusedMaxRows];
+    __shared__ double nsum[NORM != NORM_NONE ? WAVES : 1][kFusedMaxRows];
+    __shared__ float wmax[FUSEQ ? WAVES : 1][kFusedMaxRows];
+    __shared__ int wsum[FUSEQ ? WAVES : 1][kFusedMaxRows];
     const int nt = blockIdx.x;
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -37,18 +57,37 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
     const int ktiles = p.ktiles;
     const size_t tile0 = (size_t)nt * ktiles * 64 + lane;
 
-    // FUSEQ: the fp32 rows are loaded first, so waiting for them does not also
-    // wait for the weight loads queued behind them (loads retire in order).
+    // FUSEQ: the rows (and norm weights) are loaded first, so waiting for them
+    // does not also wait for the weight loads queued behind them.
     const int k = p.k;
-    const int row4 = k >> 2;            // float4 per row (k % 4 == 0)
+    const int row4 = k >> 2;            // element groups per row (k % 4 == 0)
     const int n4 = FUSEQ ? M * row4 : 0;
-    float4 xv[FUSEQ ? kFusedVec : 1];
+    constexpr bool F64 = NORM == NORM_INNER_F64;
+    float4 xv[FUSEQ && !F64 ? FV : 1];
+    double xd[F64 ? FV : 1][4];
+    float4 gv[NORM != NORM_NONE ? FV : 1];
     if (FUSEQ) {
         const float4* x4 = (const float4*)p.x;
+        const double2* x2 = (const double2*)p.x64;
+        const float4* w4 = (const float4*)p.nw;
 #pragma unroll
-        for (int j = 0; j < kFusedVec; ++j) {
+        for (int j = 0; j < FV; ++j) {
             const int idx = tid + j * T;
-            if (idx < n4) xv[j] = x4[idx];
+            if (idx < n4) {
+                if (F64) {
+                    const double2 a = x2[2 * idx], b = x2[2 * idx + 1];
+                    xd[j][0] = a.x;
+                    xd[j][1] = a.y;
+                    xd[j][2] = b.x;
+                    xd[j][3] = b.y;
+                } else {
+                    xv[j] = x4[idx];
+                }
+                if (NORM != NORM_NONE) {
+                    const int c4 = idx - row_of(idx, row4) * row4;
+                    gv[j] = w4 ? w4[c4] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+                }
+            }
         }
     }
 
@@ -65,56 +104,178 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
 
     for (int i = tid; i < NMAT * MSUB * 16 * 16; i += T) (&red[0][0][0])[i] = 0;
     if (FUSEQ) {
-        if (tid < kFusedMaxRows) {
-            amax_bits[tid] = 0u;
-            xsum_s[tid] = 0;
+        if (NORM != NORM_NONE) {
+            // ---- sum of squares per row -----------------------------------
+            double tot[kFusedMaxRows];
+            if (STRICT) {
+                // one row: squares to LDS, one lane adds them in element order
+                double* sq = (double*)xq_s;
+#pragma unroll
+                for (int j = 0; j < FV; ++j) {
+                    const int idx = tid + j * T;
+                    if (idx < n4) {
+                        if (F64) {
+#pragma unroll
+                            for (int c = 0; c < 4; ++c) sq[4 * idx + c] = xd[j][c] * xd[j][c];
+                        } else {
+                            const double a = xv[j].x, b = xv[j].y, c = xv[j].z, d = xv[j].w;
+                            sq[4 * idx] = a * a;
+                            sq[4 * idx + 1] = b * b;
+                            sq[4 * idx + 2] = c * c;
+                            sq[4 * idx + 3] = d * d;
+                        }
+                    }
+                }
+                __syncthreads();
+                if (tid == 0) nsum[0][0] = ordered_sum(sq, k, 0.0);
+                __syncthreads();
+                tot[0] = nsum[0][0];
+#pragma unroll
+                for (int rr = 1; rr < kFusedMaxRows; ++rr) tot[rr] = 0.0;
+            } else {
+                double ps[kFusedMaxRows] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+                for (int j = 0; j < FV; ++j) {
+                    const int idx = tid + j * T;
+                    if (idx < n4) {
+                        const int row = row_of(idx, row4);
+                        double q = 0.0;
+                        if (F64) {
+#pragma unroll
+                            for (int c = 0; c < 4; ++c) q = q + xd[j][c] * xd[j][c];
+                        } else {
+                            const double a = xv[j].x, b = xv[j].y, c = xv[j].z, d = xv[j].w;
+                            q = a * a;
+                            q = q + b * b;
+                            q = q + c * c;
+                            q = q + d * d;
+                        }
+#pragma unroll
+                        for (int rr = 0; rr < kFusedMaxRows; ++rr)
+                            if (rr == row) ps[rr] = ps[rr] + q;
+                    }
+                }
+#pragma unroll
+                for (int rr = 0; rr < kFusedMaxRows; ++rr) {
+                    if (rr < M) {
+                        const double w = wave_sum_f64_dpp(ps[rr]);
+                        if (lane == 0) nsum[wave][rr] = w;
+                    }
+                }
+                __syncthreads();
+#pragma unroll
+                for (int rr = 0; rr < kFusedMaxRows; ++rr) {
+                    double t = 0.0;
+                    if (rr < M) {
+                        t = nsum[0][rr];
+                        for (int w = 1; w < WAVES; ++w) t = t + nsum[w][rr];
+                    }
+                    tot[rr] = t;
+                }
+            }
+            // ---- normalize in registers ------------------------------------
+            double f[kFusedMaxRows];
+#pragma unroll
+            for (int rr = 0; rr < kFusedMaxRows; ++rr) {
+                const double ms = tot[rr] / (double)k + p.neps;
+                f[rr] = NORM == NORM_RMS ? sqrt(ms) : 1.0 / sqrt(ms);  // rms, or scale
+            }
+#pragma unroll
+            for (int j = 0; j < FV; ++j) {
+                const int idx = tid + j * T;
+                if (idx < n4) {
+                    const int row = row_of(idx, row4);
+                    double fr = f[0];
+#pragma unroll
+                    for (int rr = 1; rr < kFusedMaxRows; ++rr)
+                        if (rr == row) fr = f[rr];
+                    const double g0 = gv[j].x, g1 = gv[j].y, g2 = gv[j].z, g3 = gv[j].w;
+                    if (NORM == NORM_RMS) {
+                        xv[j].x = (float)(((double)xv[j].x / fr) * g0);
+                        xv[j].y = (float)(((double)xv[j].y / fr) * g1);
+                        xv[j].z = (float)(((double)xv[j].z / fr) * g2);
+                        xv[j].w = (float)(((double)xv[j].w / fr) * g3);
+                    } else if (NORM == NORM_INNER_F32) {
+                        xv[j].x = (float)((double)xv[j].x * fr * g0);
+                        xv[j].y = (float)((double)xv[j].y * fr * g1);
+                        xv[j].z = (float)((double)xv[j].z * fr * g2);
+                        xv[j].w = (float)((double)xv[j].w * fr * g3);
+                    } else {
+                        xd[j][0] = xd[j][0] * (fr * g0);
+                        xd[j][1] = xd[j][1] * (fr * g1);
+                        xd[j][2] = xd[j][2] * (fr * g2);
+                        xd[j][3] = xd[j][3] * (fr * g3);
+                    }
+                }
+            }
         }
         __syncthreads();
-        // bitNetActivationMaxAbs per row (poly/bitnet_cpu.go:45-57).
+        // bitNetActivationMaxAbs per row (poly/bitnet_cpu.go:45-71).
         float lm[kFusedMaxRows] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int j = 0; j < kFusedVec; ++j) {
+        for (int j = 0; j < FV; ++j) {
             const int idx = tid + j * T;
             if (idx < n4) {
-                float a = max_nan_skip(0.0f, fabsf(xv[j].x));
-                a = max_nan_skip(a, fabsf(xv[j].y));
-                a = max_nan_skip(a, fabsf(xv[j].z));
-                a = max_nan_skip(a, fabsf(xv[j].w));
-                const int row = (idx >= row4) + (idx >= 2 * row4) + (idx >= 3 * row4);
+                float a;
+                if (F64) {
+                    a = max_nan_skip(0.0f, (float)fabs(xd[j][0]));
+                    a = max_nan_skip(a, (float)fabs(xd[j][1]));
+                    a = max_nan_skip(a, (float)fabs(xd[j][2]));
+                    a = max_nan_skip(a, (float)fabs(xd[j][3]));
+                } else {
+                    a = max_nan_skip(0.0f, fabsf(xv[j].x));
+                    a = max_nan_skip(a, fabsf(xv[j].y));
+                    a = max_nan_skip(a, fabsf(xv[j].z));
+                    a = max_nan_skip(a, fabsf(xv[j].w));
+                }
+                const int row = row_of(idx, row4);
 #pragma unroll
                 for (int rr = 0; rr < kFusedMaxRows; ++rr)
                     if (rr == row) lm[rr] = max_nan_skip(lm[rr], a);
             }
         }
-        // non-negative, non-NaN floats order like their bit patterns
 #pragma unroll
         for (int rr = 0; rr < kFusedMaxRows; ++rr) {
-            const float wm = wave_max(lm[rr]);
-            if (rr < M && lane == 0 && wm > 0.0f) atomicMax(&amax_bits[rr], __float_as_uint(wm));
+            if (rr < M) {
+                const float wm = wave_max_dpp(lm[rr]);
+                if (lane == 0) wmax[wave][rr] = wm;
+            }
         }
         __syncthreads();
-        // bitNetQuantizedActivation (poly/bitnet_cpu.go:73-84) into LDS.
+        // bitNetQuantizedActivation (poly/bitnet_cpu.go:73-95) into LDS.
         double sc[kFusedMaxRows];
 #pragma unroll
         for (int rr = 0; rr < kFusedMaxRows; ++rr) {
-            float am = __uint_as_float(amax_bits[rr]);
+            float am = 0.0f;
+            if (rr < M) {
+                for (int w = 0; w < WAVES; ++w) am = max_nan_skip(am, wmax[w][rr]);
+            }
+            if (tid == rr) amax_bits[rr] = __float_as_uint(am);  // read after the main loop
             if (am < 1e-5f) am = 1e-5f;
             sc[rr] = rr < M ? 127.0 / (double)am : 0.0;
         }
         int ls[kFusedMaxRows] = {0, 0, 0, 0};
 #pragma unroll
-        for (int j = 0; j < kFusedVec; ++j) {
+        for (int j = 0; j < FV; ++j) {
             const int idx = tid + j * T;
             if (idx < n4) {
-                const int row = (idx >= row4) + (idx >= 2 * row4) + (idx >= 3 * row4);
+                const int row = row_of(idx, row4);
                 double s = sc[0];
 #pragma unroll
                 for (int rr = 1; rr < kFusedMaxRows; ++rr)
                     if (rr == row) s = sc[rr];
-                const int q0 = quant_one((double)xv[j].x, s);
-                const int q1 = quant_one((double)xv[j].y, s);
-                const int q2 = quant_one((double)xv[j].z, s);
-                const int q3 = quant_one((double)xv[j].w, s);
+                int q0, q1, q2, q3;
+                if (F64) {
+                    q0 = quant_one(xd[j][0], s);
+                    q1 = quant_one(xd[j][1], s);
+                    q2 = quant_one(xd[j][2], s);
+                    q3 = quant_one(xd[j][3], s);
+                } else {
+                    q0 = quant_one((double)xv[j].x, s);
+                    q1 = quant_one((double)xv[j].y, s);
+                    q2 = quant_one((double)xv[j].z, s);
+                    q3 = quant_one((double)xv[j].w, s);
+                }
                 *(uint32_t*)(xq_s + row * p.ldq + 4 * (idx - row * row4)) = pack4(q0, q1, q2, q3);
 #pragma unroll
                 for (int rr = 0; rr < kFusedMaxRows; ++rr)
@@ -129,10 +290,18 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
         }
 #pragma unroll
         for (int rr = 0; rr < kFusedMaxRows; ++rr) {
-            const int v = wave_sum_i(ls[rr]);
-            if (rr < M && lane == 0 && v != 0) atomicAdd(&xsum_s[rr], v);
+            if (rr < M) {
+                const int v = wave_sum_i_dpp(ls[rr]);
+                if (lane == 0) wsum[wave][rr] = v;
+            }
         }
         __syncthreads();
+        if (tid < kFusedMaxRows) {
+            int t = 0;
+            if (tid < M)
+                for (int w = 0; w < WAVES; ++w) t += wsum[w][tid];
+            xsum_s[tid] = t;  // read after the main loop's barrier
+        }
         if (blockIdx.x == 0) {
             if (p.xq_tap) {
                 for (int i = tid; i < M * k; i += T) p.xq_tap[i] = xq_s[(i / k) * p.ldq + (i % k)];
@@ -338,6 +507,77 @@ hipError_t launch_matmul(const Matrix* w0, const Matrix* w1, const QuantAct& a, 
 bool fused_quant_ok(int m, int k, const float* x) {
     return m >= 1 && m <= kFusedMaxRows && k % 4 == 0 && ((uintptr_t)x & 15) == 0 &&
            (size_t)m * k <= (size_t)4 * kFusedVec * 512 && pad_cols(k) * (size_t)m <= 64 * 1024;
+}
+
+// ---- norm-fused decode matmuls ------------------------------------------------
+// 512-thread workgroups; FV element groups of 4 per thread hold the rows.
+constexpr int kNormWaves = 8;
+constexpr int kNormThreads = kNormWaves * 64;
+
+static size_t norm_lds(int m, int k, int strict) {
+    const size_t q = (size_t)m * pad_cols(k);
+    const size_t sq = strict ? (size_t)k * 8 : 0;
+    return q > sq ? q : sq;
+}
+
+bool norm_fused_ok(int m, int k, int strict, bool x16) {
+    if (m < 1 || m > kFusedMaxRows || k % 4 != 0 || !x16) return false;
+    // rows held in registers: up to 4 element groups per thread (more spills)
+    if ((size_t)m * (k / 4) > (size_t)4 * kNormThreads) return false;
+    if (strict && m != 1) return false;  // one row of squares in LDS
+    return norm_lds(m, k, strict) <= 60 * 1024;
+}
+
+template <int NMAT, int NORM, int STRICT, int FV>
+static hipError_t launch_norm_t(const MatArgs& p, size_t shm, hipStream_t s) {
+    hipLaunchKernelGGL((skinny_kernel<NMAT, 1, kNormWaves, true, NORM, STRICT, FV>), dim3(p.ntiles),
+                       dim3(kNormThreads), shm, s, p);
+    return hipGetLastError();
+}
+
+template <int NMAT, int NORM, int STRICT>
+static hipError_t launch_norm_fv(const MatArgs& p, size_t shm, hipStream_t s) {
+    const size_t groups = (size_t)p.e.m * (p.k / 4);
+    if (groups <= 2 * kNormThreads) return launch_norm_t<NMAT, NORM, STRICT, 2>(p, shm, s);
+    return launch_norm_t<NMAT, NORM, STRICT, 4>(p, shm, s);
+}
+
+template <int NMAT, int NORM>
+static hipError_t launch_norm_st(const MatArgs& p, int strict, size_t shm, hipStream_t s) {
+    return strict ? launch_norm_fv<NMAT, NORM, 1>(p, shm, s) : launch_norm_fv<NMAT, NORM, 0>(p, shm, s);
+}
+
+hipError_t launch_matmul_norm(const Matrix* w0, const Matrix* w1, const float* x, const double* x64,
+                              int m, int mode, int strict, const float* nw, double eps,
+                              const Epilogue& epi, float* amax_tap, hipStream_t s) {
+    if (m <= 0) return hipSuccess;
+    const void* rows = mode == NORM_INNER_F64 ? (const void*)x64 : (const void*)x;
+    if (!rows || !norm_fused_ok(m, w0->cols, strict, ((uintptr_t)rows & 15) == 0)) {
+        return hipErrorInvalidValue;
+    }
+    if (((uintptr_t)nw & 15) != 0) return hipErrorInvalidValue;
+    MatArgs p = make_args(w0, w1, m, epi);
+    p.x = x;
+    p.x64 = x64;
+    p.nw = nw;
+    p.neps = eps;
+    p.amax_tap = amax_tap;
+    p.ldq = pad_cols(w0->cols);
+    const size_t shm = norm_lds(m, w0->cols, strict);
+    const bool two = epi.kind == EPI_SWIGLU;
+    switch (mode) {
+        case NORM_RMS:
+            return two ? launch_norm_st<2, NORM_RMS>(p, strict, shm, s)
+                       : launch_norm_st<1, NORM_RMS>(p, strict, shm, s);
+        case NORM_INNER_F32:
+            if (two) return hipErrorInvalidValue;
+            return launch_norm_st<1, NORM_INNER_F32>(p, strict, shm, s);
+        case NORM_INNER_F64:
+            if (two) return hipErrorInvalidValue;
+            return launch_norm_st<1, NORM_INNER_F64>(p, strict, shm, s);
+        default:
+            return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_matmul_fused(const Matrix* w0, const Matrix* w1, const float* x, int m,

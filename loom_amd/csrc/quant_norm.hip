@@ -178,18 +178,7 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(float* __restrict__ h, 
             }
         }
         __syncthreads();
-        if (threadIdx.x == 0) {
-            double s = 0.0;
-            const double2* sq = (const double2*)dsh;
-            const int pairs = n >> 1;
-            for (int i = 0; i < pairs; ++i) {
-                const double2 p = sq[i];
-                s += p.x;
-                s += p.y;
-            }
-            if (n & 1) s += dsh[n - 1];
-            total = s;
-        }
+        if (threadIdx.x == 0) total = ordered_sum(dsh, n, 0.0);
         __syncthreads();
     } else {
         double s = 0.0;
