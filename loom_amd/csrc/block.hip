@@ -626,59 +626,98 @@ __global__ __launch_bounds__(64) void attn_exp_kernel(const int* __restrict__ po
     if (k < L) sc.scores[rh * span + k] = exp(sc.scores[rh * span + k] - m);
 }
 
-// strict part 3: ND value columns per workgroup; p and the columns are staged
-// in LDS, then one lane per column adds in position order (first wave) and a
-// lane of the second wave forms expSum in position order.
-// grid (heads, hd / ND, rows), 128 threads.
-template <int ND>
-__global__ __launch_bounds__(128) void attn_chain_kernel(const float* __restrict__ cache_v,
-                                                        const int* __restrict__ pos0, int msl,
-                                                        int span, int heads, int kv_heads, int hd,
-                                                        int seq, DecodeScratch sc,
-                                                        double* __restrict__ out) {
-    extern __shared__ double lds[];  // p[span], then ND columns of span floats
-    const int h = blockIdx.x, d0 = blockIdx.y * ND, row = blockIdx.z;
+// strict part 3: one workgroup per (head, row).  Lane d < HD adds its value
+// column in position order; one lane of another wave forms expSum in position
+// order.  V rows and probabilities stream through two LDS buffers in chunks
+// of C = 4096 / HD positions (4096 floats), with kChainDepth chunks of loads
+// in flight in registers.  The loads are branch-free (indices clamped into
+// the ring and the score row; surplus values are never used), so each store
+// waits only for its own chunk.  grid (heads, rows), 256 threads.
+constexpr int kChainDepth = 4;
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_chain_kernel(const float* __restrict__ cache_v,
+                                                         const int* __restrict__ pos0, int msl,
+                                                         int span, int heads, int kv_heads,
+                                                         int seq, DecodeScratch sc,
+                                                         double* __restrict__ out) {
+    constexpr int C = 4096 / HD;
+    static_assert(C * HD == 4096 && C <= 256, "chunk geometry");
+    __shared__ float4 vbuf[2][1024];
+    __shared__ double pbuf[2][256];
+    __shared__ double es_sh;
+    const int h = blockIdx.x, row = blockIdx.y;
     const int b = row / seq, s = row % seq;
     const int kvh = h / (heads / kv_heads);
-    const int q_dim = heads * hd, kv_dim = kv_heads * hd;
+    const int q_dim = heads * HD, kv_dim = kv_heads * HD;
+    const int tid = threadIdx.x;
     const int L = *pos0 + s + 1;
-    double* orow = out + (size_t)row * q_dim + (size_t)h * hd;
+    double* orow = out + (size_t)row * q_dim + (size_t)h * HD;
     if (L > span) {
-        if (threadIdx.x < ND) orow[d0 + threadIdx.x] = __builtin_nan("");
+        if (tid < HD) orow[tid] = __builtin_nan("");
         return;
     }
-    double* p = lds;
-    float* vc = (float*)(lds + span);
+    const int nch = (L + C - 1) / C;
+    const float* vb = cache_v + (size_t)b * msl * kv_dim + (size_t)kvh * HD;
     const double* pr = sc.scores + ((size_t)row * heads + h) * span;
-    for (int k = threadIdx.x; k < L; k += 128) p[k] = pr[k];
-    const float* vb = cache_v + (size_t)b * msl * kv_dim + (size_t)kvh * hd + d0;
-    for (int i = threadIdx.x; i < L * ND; i += 128) {
-        const int k = i / ND, j = i % ND;
-        vc[j * span + k] = vb[(size_t)k * kv_dim + j];
+    constexpr int es_lane = HD <= 192 ? 192 : 0;
+
+    float4 r[kChainDepth][4];
+    double rp[kChainDepth];
+    auto issue = [&](int u, int c) {
+        const int cc = min(c, nch - 1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = (tid + i * 256) * 4;  // element of the 4096-float chunk
+            const int k = min(cc * C + e / HD, msl - 1);
+            r[u][i] = *(const float4*)(vb + (size_t)k * kv_dim + e % HD);
+        }
+        rp[u] = pr[min(cc * C + min(tid, C - 1), span - 1)];
+    };
+#pragma unroll
+    for (int u = 0; u < kChainDepth; ++u) issue(u, u);
+
+    double sum = 0.0, es = 0.0;
+    for (int c0 = 0; c0 < nch; c0 += kChainDepth) {
+#pragma unroll
+        for (int u = 0; u < kChainDepth; ++u) {
+            const int c = c0 + u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vbuf[u & 1][tid + i * 256] = r[u][i];
+            pbuf[u & 1][tid] = rp[u];
+            issue(u, c + kChainDepth);
+            __syncthreads();
+            if (c < nch) {  // uniform
+                const float* vbb = (const float*)vbuf[u & 1];
+                const double* pbb = pbuf[u & 1];
+                const int n = min(C, L - c * C);
+                if (tid < HD) {
+                    int j = 0;
+                    for (; j + 16 <= n; j += 16) {
+                        double a[16];
+                        float v[16];
+#pragma unroll
+                        for (int t = 0; t < 16; ++t) {
+                            a[t] = pbb[j + t];
+                            v[t] = vbb[(j + t) * HD + tid];
+                        }
+#pragma unroll
+                        for (int t = 0; t < 16; ++t) sum += a[t] * (double)v[t];
+                    }
+                    for (; j < n; ++j) sum += pbb[j] * (double)vbb[j * HD + tid];
+                }
+                if (tid == es_lane) es = ordered_sum(pbb, n, es);
+            }
+        }
     }
+    if (tid == es_lane) es_sh = es;
     __syncthreads();
-    __shared__ double es_sh;
-    double sum = 0.0;
-    if ((int)threadIdx.x < ND) {
-        sum = ordered_dot(p, vc + threadIdx.x * span, L, 0.0);
-    } else if ((int)threadIdx.x == 64) {
-        es_sh = ordered_sum(p, L, 0.0);
-    }
-    __syncthreads();
-    if ((int)threadIdx.x < ND) orow[d0 + threadIdx.x] = sum / es_sh;
+    if (tid < HD) orow[tid] = sum / es_sh;
 }
 
 // LDS bytes of one fused attention workgroup for `span` positions.
 size_t attention_lds_bytes(int hd, int span) {
     return ((size_t)((hd + 1) & ~1) + (size_t)span) * sizeof(double);
-}
-
-static size_t chain_lds(int span, int nd) { return (size_t)span * 8 + (size_t)span * nd * 4; }
-
-static int chain_nd(int span, int hd) {
-    if (hd % 2 == 0 && chain_lds(span, 2) <= kMaxAttnLds) return 2;
-    if (chain_lds(span, 1) <= kMaxAttnLds) return 1;
-    return 0;  // strict decode falls back to the fused kernel
 }
 
 size_t attention_scratch_bytes(int rows, int heads, int hd, int span) {
@@ -707,8 +746,8 @@ hipError_t launch_attention(const double* q, const float* cache_k, const float* 
     if (hd % 4 != 0 || hd > 256 || kv_heads <= 0 || heads % kv_heads != 0) return hipErrorInvalidValue;
     if (span > kMaxAttnSpan || span > msl) return hipErrorInvalidValue;
     const int rows = batch * seq;
-    const int nd = chain_nd(span, hd);
-    if (rows <= kSplitMaxRows && (!strict || nd > 0)) {
+    const bool chain_hd = hd == 32 || hd == 64 || hd == 128 || hd == 256;
+    if (rows <= kSplitMaxRows && (!strict || chain_hd)) {
         if (!scratch) return hipErrorInvalidValue;
         const DecodeScratch sc = decode_scratch(scratch, rows, heads, hd, span);
         const int nc = attn_nchunk(span);
@@ -723,13 +762,20 @@ hipError_t launch_attention(const double* q, const float* cache_k, const float* 
         } else {
             hipLaunchKernelGGL(attn_exp_kernel, dim3(heads, nc, rows), dim3(64), 0, s, pos0, span,
                                heads, seq, sc);
-            const size_t shm = chain_lds(span, nd);
-            if (nd == 2) {
-                hipLaunchKernelGGL(attn_chain_kernel<2>, dim3(heads, hd / 2, rows), dim3(128), shm, s,
-                                   cache_v, pos0, msl, span, heads, kv_heads, hd, seq, sc, out);
-            } else {
-                hipLaunchKernelGGL(attn_chain_kernel<1>, dim3(heads, hd, rows), dim3(128), shm, s,
-                                   cache_v, pos0, msl, span, heads, kv_heads, hd, seq, sc, out);
+            const dim3 g(heads, rows), t(256);
+            switch (hd) {
+                case 32:
+                    hipLaunchKernelGGL(attn_chain_kernel<32>, g, t, 0, s, cache_v, pos0, msl, span, heads, kv_heads, seq, sc, out);
+                    break;
+                case 64:
+                    hipLaunchKernelGGL(attn_chain_kernel<64>, g, t, 0, s, cache_v, pos0, msl, span, heads, kv_heads, seq, sc, out);
+                    break;
+                case 128:
+                    hipLaunchKernelGGL(attn_chain_kernel<128>, g, t, 0, s, cache_v, pos0, msl, span, heads, kv_heads, seq, sc, out);
+                    break;
+                default:
+                    hipLaunchKernelGGL(attn_chain_kernel<256>, g, t, 0, s, cache_v, pos0, msl, span, heads, kv_heads, seq, sc, out);
+                    break;
             }
         }
         return hipGetLastError();

@@ -528,18 +528,24 @@ bool norm_fused_ok(int m, int k, int strict, bool x16) {
     return norm_lds(m, k, strict) <= 60 * 1024;
 }
 
-template <int NMAT, int NORM, int STRICT, int FV>
+template <int NMAT, int NORM, int STRICT, int WAVES, int FV>
 static hipError_t launch_norm_t(const MatArgs& p, size_t shm, hipStream_t s) {
-    hipLaunchKernelGGL((skinny_kernel<NMAT, 1, kNormWaves, true, NORM, STRICT, FV>), dim3(p.ntiles),
-                       dim3(kNormThreads), shm, s, p);
+    hipLaunchKernelGGL((skinny_kernel<NMAT, 1, WAVES, true, NORM, STRICT, FV>), dim3(p.ntiles),
+                       dim3(WAVES * 64), shm, s, p);
     return hipGetLastError();
 }
 
+// More tiles than CUs: 4-wave workgroups, so two fit a CU and the grid runs in
+// one round (8-wave workgroups of the wide kernels fit only one per CU).
 template <int NMAT, int NORM, int STRICT>
 static hipError_t launch_norm_fv(const MatArgs& p, size_t shm, hipStream_t s) {
     const size_t groups = (size_t)p.e.m * (p.k / 4);
-    if (groups <= 2 * kNormThreads) return launch_norm_t<NMAT, NORM, STRICT, 2>(p, shm, s);
-    return launch_norm_t<NMAT, NORM, STRICT, 4>(p, shm, s);
+    if (p.ntiles > 256 && groups <= 4 * 256) {
+        if (groups <= 2 * 256) return launch_norm_t<NMAT, NORM, STRICT, 4, 2>(p, shm, s);
+        return launch_norm_t<NMAT, NORM, STRICT, 4, 4>(p, shm, s);
+    }
+    if (groups <= 2 * kNormThreads) return launch_norm_t<NMAT, NORM, STRICT, kNormWaves, 2>(p, shm, s);
+    return launch_norm_t<NMAT, NORM, STRICT, kNormWaves, 4>(p, shm, s);
 }
 
 template <int NMAT, int NORM>
