@@ -133,6 +133,73 @@ def ternary_ops_per_token(c) -> float:
     return 2.0 * per_layer * c["layers"]
 
 
+def decode_bytes_per_token(c, ctx: float) -> float:
+    """HBM bytes one decode step must read: packed ternary weights, the fp32
+    LM head, the K and V rows of `ctx` cached positions, the norm vectors."""
+    h, q, kv, f = c["hidden"], c["heads"] * c["head_dim"], c["kv_heads"] * c["head_dim"], c["inter"]
+    packed = (q + 2 * kv) * ((h + 15) // 16) * 4 + h * ((q + 15) // 16) * 4 \
+        + 2 * f * ((h + 15) // 16) * 4 + h * ((f + 15) // 16) * 4
+    norms = (2 * h + q + f) * 4
+    return c["layers"] * (packed + norms + 2 * kv * 4 * ctx) + c["vocab"] * h * 4
+
+
+def cpu_decode_sample(c, cores, log):
+    """Bounded CPU sample of config 3 on the oracle (loom's bitnet_simd path
+    restated): one decode step of one layer at context 2048 with a synthetic
+    KV cache (the step's cost does not depend on the cached values), times 30
+    layers, plus one fp32 LM head in DotTile order."""
+    import numpy as np
+
+    from oracle import oracle as orc
+    h, q_dim, kv_dim, inter = c["hidden"], c["heads"] * c["head_dim"], c["kv_heads"] * c["head_dim"], c["inter"]
+    ctx = 2048
+    mats = [orc.random_matrix(r, k, 0x900 + i) for i, (r, k) in
+            enumerate([(q_dim, h), (kv_dim, h), (kv_dim, h), (h, q_dim), (inter, h), (inter, h), (h, inter)])]
+    mha = orc.MHA(*mats[:4], c["heads"], c["kv_heads"], c["head_dim"], ctx + 64, theta=c["theta"],
+                  eps=1e-5, inner_norm=orc.uniform_f32(q_dim, 0.5, 1.5, 1))
+    mha.cache_k[:] = orc.normal_f32(mha.cache_k.size, 2)
+    mha.cache_v[:] = orc.normal_f32(mha.cache_v.size, 3)
+    blk = orc.Block(mha, orc.uniform_f32(h, 0.5, 1.5, 4), orc.uniform_f32(h, 0.5, 1.5, 5), *mats[4:],
+                    orc.uniform_f32(inter, 0.5, 1.5, 6), norm_eps=1e-5, ffn_eps=1e-5, ffn_activation=1)
+    x = orc.normal_f32(h, 7).reshape(1, h)
+    steps = 3
+    t0 = time.perf_counter()
+    for i in range(steps):
+        mha.c.kv_offset = ctx + i
+        blk.c.mha.kv_offset = ctx + i
+        blk.forward(x, workers=cores)
+    layer_s = (time.perf_counter() - t0) / steps
+    table = orc.normal_f32(c["vocab"] * h, 8)
+    t0 = time.perf_counter()
+    orc.lm_head(x[0], table, simd=True)
+    lm_s = time.perf_counter() - t0
+    step_s = layer_s * c["layers"] + lm_s
+    log(f"cpu decode sample: layer step {layer_s * 1e3:.1f} ms, LM head {lm_s * 1e3:.1f} ms")
+    return {"value": round(1.0 / step_s, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"one decode step of one BitNet-2B layer at context {ctx} (synthetic KV), "
+                      f"{steps} runs, x{c['layers']} layers, + one fp32 LM head "
+                      f"({layer_s * 1e3:.1f} ms/layer, {lm_s * 1e3:.1f} ms LM head)"}
+
+
+def cpu_block_sample(c, cores, seq, log):
+    """Config 2 on the oracle: one block forward over `seq` tokens."""
+    from oracle import oracle as orc
+    h, q_dim, kv_dim, inter = c["hidden"], c["heads"] * c["head_dim"], c["kv_heads"] * c["head_dim"], c["inter"]
+    mats = [orc.random_matrix(r, k, 0xA00 + i) for i, (r, k) in
+            enumerate([(q_dim, h), (kv_dim, h), (kv_dim, h), (h, q_dim), (inter, h), (inter, h), (h, inter)])]
+    mha = orc.MHA(*mats[:4], c["heads"], c["kv_heads"], c["head_dim"], 512, theta=c["theta"], eps=1e-5,
+                  inner_norm=orc.uniform_f32(q_dim, 0.5, 1.5, 1))
+    blk = orc.Block(mha, orc.uniform_f32(h, 0.5, 1.5, 4), orc.uniform_f32(h, 0.5, 1.5, 5), *mats[4:],
+                    orc.uniform_f32(inter, 0.5, 1.5, 6), norm_eps=1e-5, ffn_eps=1e-5, ffn_activation=1)
+    x = orc.normal_f32(seq * h, 9).reshape(seq, h)
+    t0 = time.perf_counter()
+    blk.forward(x, workers=cores)
+    s = time.perf_counter() - t0
+    log(f"cpu block seq{seq}: {s:.2f} s")
+    return {"value": round(seq / s, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"one config-2 block forward over {seq} tokens ({s:.2f} s)"}
+
+
 def bench_model(args, torch, timer, log):
     """Configs 2-4 on a random-init BitNet-2B-shape model."""
     import numpy as np
@@ -166,7 +233,7 @@ def bench_model(args, torch, timer, log):
     blocks = {}
     for norm in ("strict", "fast"):
         cfg = tf.BlockConfig(h, c["heads"], c["kv_heads"], c["head_dim"], inter, max_seq_len=512,
-                             rope_theta=c["theta"], norm_eps=1e-5, ffn_activation=6, norm=norm)
+                             rope_theta=c["theta"], norm_eps=1e-5, ffn_activation=1, norm=norm)
         blocks[norm] = tf.BitNetBlock(cfg, w0)
     x512 = torch.from_numpy(rng.standard_normal((512, h), dtype=np.float32)).cuda()
     xs = x512.clone()
@@ -182,20 +249,22 @@ def bench_model(args, torch, timer, log):
                         "int8_TOPS_projections": round(ops / (ms * 1e-3) / 1e12, 2)})
         log(f"config2 block seq512 {blk_res[-1]}")
         blk.release()
+    if args.cpu_seconds > 0:
+        out["cpu_block_seq512"] = cpu_block_sample(c, cpu_cores(), 512, log)
     out["block_seq512"] = {"config": "config2 BitNet-2B block (hidden 2560, 20/5 heads x 128, "
-                                     "FFN 6912 ReLU2-gated), seq 512, batch 1, fp32 norms, fp64 "
+                                     "FFN 6912 SiLU-gated), seq 512, batch 1, fp32 norms, fp64 "
                                      "attention", "runs": blk_res}
 
     # ---- configs 3 and 4: the full stack ---------------------------------------
     layers = [w0] + [layer() for _ in range(c["layers"] - 1)]
-    emb = rng.standard_normal((c["vocab"], h), dtype=np.float32)
+    emb = rng.standard_normal((c["vocab"], h), dtype=np.float32) * np.float32(0.02)
     fnorm = rng.uniform(0.5, 1.5, h).astype(np.float32)
     log(f"model weights generated in {time.perf_counter() - t0:.1f}s")
     res3, res4 = [], []
     for norm in args.model_norms.split(","):
         cfg = tf.BlockConfig(h, c["heads"], c["kv_heads"], c["head_dim"], inter, max_seq_len=msl,
                              max_batch=batch, rope_theta=c["theta"], norm_eps=1e-5,
-                             ffn_activation=6, norm=norm)
+                             ffn_activation=1, norm=norm)
         t1 = time.perf_counter()
         model = tf.Transformer(cfg, layers, emb, fnorm, vocab=c["vocab"], final_norm_eps=1e-5,
                                max_tokens=msl + 1, max_prefill=prompt)
@@ -217,7 +286,10 @@ def bench_model(args, torch, timer, log):
         torch.cuda.synchronize()
         t_dec = ev0.elapsed_time(ev1)
         toks = model.tokens()
-        res3.append({"norm": norm, "decode_tok_s": round(gen / (t_dec * 1e-3), 2),
+        tok_s = gen / (t_dec * 1e-3)
+        gbs = decode_bytes_per_token(c, prompt + gen / 2) * tok_s / 1e9
+        res3.append({"norm": norm, "decode_tok_s": round(tok_s, 2),
+                     "hbm_GBs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                      "ms_per_token": round(t_dec / gen, 4), "prefill_ms": round(t_pre1, 2),
                      "prefill_tok_s": round(prompt / (t_pre1 * 1e-3), 1),
                      "last_tokens": toks[0, -4:].tolist()})
@@ -238,6 +310,8 @@ def bench_model(args, torch, timer, log):
                      "int8_TOPS_projections": round(ternary_ops_per_token(c) * ntok / (t4 * 1e-3) / 1e12, 2)})
         log(f"config4 prefill {res4[-1]}")
         model.release()
+    if args.cpu_seconds > 0:
+        out["cpu_decode"] = cpu_decode_sample(c, cpu_cores(), log)
     out["decode"] = {"config": f"config3: {c['layers']} layers, vocab {c['vocab']}, tied fp32 "
                                f"LM head, greedy, {prompt}-token random prompt, {gen} tokens, "
                                "one HIP graph per token, positions on device",

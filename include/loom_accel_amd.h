@@ -62,6 +62,14 @@ int loom_amd_matrix_create(int device, const uint32_t* words, size_t n_words, in
 int loom_amd_matrix_from_entity_blob(int device, const void* blob, size_t len,
                                      loom_amd_matrix** out, size_t* consumed);
 
+/* Same, from Microsoft's offline BitNet U8 layout (HF checkpoints): packed is
+ * (rows/4) x cols bytes in host memory, byte (pr, c) holding the codes of
+ * rows lane*(rows/4) + pr for lane 0..3; scale is the checkpoint's
+ * weight_scale.  Replaces packMicrosoftOfflineBitNetRowsToU32FromBytes
+ * (poly/bitnet_cpu.go:1078-1098) followed by the repack.  Synchronous. */
+int loom_amd_matrix_from_ms_offline(int device, const uint8_t* packed, int rows, int cols,
+                                    float scale, loom_amd_matrix** out);
+
 void loom_amd_matrix_release(loom_amd_matrix* m);
 
 int loom_amd_matrix_shape(const loom_amd_matrix* m, int* rows, int* cols, float* scale,

@@ -99,6 +99,20 @@ class TernaryMatrix:
               "matrix_from_entity_blob")
         return cls(out.value, device)
 
+    @classmethod
+    def from_ms_offline(cls, packed: np.ndarray, rows: int, cols: int, scale: float,
+                        device: int = 0) -> "TernaryMatrix":
+        """Microsoft offline U8 layout ((rows/4) x cols bytes) with the
+        checkpoint's weight_scale (packMicrosoftOfflineBitNetRowsToU32FromBytes)."""
+        packed = np.ascontiguousarray(packed, np.uint8)
+        if packed.size < (rows // 4) * cols:
+            raise ValueError("packed holds fewer than (rows/4)*cols bytes")
+        out = C.c_void_p()
+        check(_lib.lib().loom_amd_matrix_from_ms_offline(device, packed.ctypes.data_as(C.c_void_p),
+                                                         rows, cols, scale, C.byref(out)),
+              "matrix_from_ms_offline")
+        return cls(out.value, device)
+
     @property
     def handle(self) -> C.c_void_p:
         if self._h is None:

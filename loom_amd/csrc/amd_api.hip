@@ -117,11 +117,58 @@ int create_matrix(int device, const uint32_t* words, size_t n_words, int rows, i
     return 0;
 }
 
+int create_matrix_ms_offline(int device, const uint8_t* packed, int rows, int cols, float scale,
+                             loom_amd_matrix** out) {
+    if (out == nullptr) return fail("out is null");
+    *out = nullptr;
+    if (packed == nullptr) return fail("packed bytes are null");
+    if (rows <= 0 || cols <= 0) return fail("rows and cols must be positive");
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev) {
+        return fail("device " + std::to_string(device) + " is not visible");
+    }
+    if (!is_gfx950(device)) return fail("device is not gfx950");
+    DeviceGuard guard(device);
+    auto* w = new loom_amd_matrix();
+    Matrix& m = w->m;
+    m.rows = rows;
+    m.cols = cols;
+    m.ntiles = ceil_div(rows, kTileRows);
+    m.ktiles = ceil_div(cols, kTileCols);
+    m.scale = scale;
+    m.device = device;
+    const int row_words = ceil_div(cols, 16);
+    const size_t packed_bytes = (size_t)(rows / 4) * cols;
+    uint8_t* dpacked = nullptr;
+    uint32_t* staging = nullptr;
+    hipError_t e = hipMalloc(&dpacked, packed_bytes ? packed_bytes : 1);
+    if (e == hipSuccess) e = hipMalloc(&staging, (size_t)rows * row_words * 4);
+    if (e == hipSuccess) e = hipMalloc(&m.tiles, m.bytes());
+    if (e == hipSuccess && packed_bytes) e = hipMemcpy(dpacked, packed, packed_bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = launch_ms_offline_to_words(dpacked, rows, cols, staging, nullptr);
+    if (e == hipSuccess) e = launch_repack(staging, rows, cols, row_words, &m, nullptr);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (staging) (void)hipFree(staging);
+    if (dpacked) (void)hipFree(dpacked);
+    if (e != hipSuccess) {
+        if (m.tiles) (void)hipFree(m.tiles);
+        delete w;
+        return fail_hip("offline matrix upload", e);
+    }
+    *out = w;
+    return 0;
+}
+
 }  // namespace lamd
 
 using namespace lamd;
 
 extern "C" {
+
+int loom_amd_matrix_from_ms_offline(int device, const uint8_t* packed, int rows, int cols,
+                                    float scale, loom_amd_matrix** out) {
+    return create_matrix_ms_offline(device, packed, rows, cols, scale, out);
+}
 
 const char* loom_amd_last_error(void) { return g_amd_error.c_str(); }
 

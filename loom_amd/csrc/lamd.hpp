@@ -83,6 +83,10 @@ struct Epilogue {
 // ---- launchers (quant_norm.hip, matmul_skinny.hip, matmul_gemm.hip) ----
 hipError_t launch_repack(const uint32_t* words, int rows, int cols, int row_words,
                          Matrix* m, hipStream_t s);
+// Microsoft offline U8 layout ((rows/4) x cols bytes) -> loom row-major words
+// (rows x ceil(cols/16)).
+hipError_t launch_ms_offline_to_words(const uint8_t* packed, int rows, int cols, uint32_t* words,
+                                      hipStream_t s);
 hipError_t launch_act_quant(const float* x, int ldx, int m, int k, int8_t* xq, int ldq,
                             float* amax, int32_t* xsum, hipStream_t s);
 hipError_t launch_act_quant_f64(const double* x, int ldx, int m, int k, int8_t* xq,

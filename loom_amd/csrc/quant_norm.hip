@@ -35,6 +35,43 @@ __global__ void repack_tiles_kernel(const uint32_t* __restrict__ words, int rows
     out[idx] = o;
 }
 
+// packMicrosoftOfflineBitNetRowsToU32FromBytes (poly/bitnet_cpu.go:1078-1098):
+// byte (pr, c) of the (rows/4) x cols offline matrix holds the 2-bit codes of
+// column c for rows lane*(rows/4) + pr, lane = 0..3 (bits 2*lane); code 3
+// becomes 1 (a zero weight).  Rows past 4*(rows/4) keep all-zero words.  One
+// thread per output word of loom's row-major layout (16 codes per word).
+__global__ void ms_offline_to_words_kernel(const uint8_t* __restrict__ packed, int rows, int cols,
+                                           int row_words, uint32_t* __restrict__ words) {
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long)rows * row_words) return;
+    const int row = (int)(idx / row_words);
+    const int w = (int)(idx % row_words);
+    const int prs = rows / 4;
+    uint32_t word = 0;
+    if (prs > 0 && row < 4 * prs) {
+        const int lane = row / prs, pr = row % prs;
+        const uint8_t* src = packed + (size_t)pr * cols;
+        for (int j = 0; j < 16; ++j) {
+            const int c = w * 16 + j;
+            if (c >= cols) break;
+            uint32_t code = (src[c] >> (2 * lane)) & 3u;
+            if (code > 2) code = 1;
+            word |= code << (2 * j);
+        }
+    }
+    words[idx] = word;
+}
+
+hipError_t launch_ms_offline_to_words(const uint8_t* packed, int rows, int cols, uint32_t* words,
+                                      hipStream_t s) {
+    const int row_words = ceil_div(cols, 16);
+    const long total = (long)rows * row_words;
+    if (total <= 0) return hipSuccess;
+    hipLaunchKernelGGL(ms_offline_to_words_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       s, packed, rows, cols, row_words, words);
+    return hipGetLastError();
+}
+
 hipError_t launch_repack(const uint32_t* words, int rows, int cols, int row_words, Matrix* m,
                          hipStream_t s) {
     const long total = (long)m->ntiles * m->ktiles * kTileWords;

@@ -443,3 +443,79 @@ def test_swiglu_large_tiles(orc, torch_dev, bn):
     # gate|up at M=4096 x inter=4096 runs the two-matrix large-tile kernel
     _swiglu_case(orc, torch_dev, bn, hidden=640, inter=4096, M=4096, seed=97, norm="fast",
                  with_norm_w=True)
+
+
+# ---------------------------------------------------------------- golden fixtures
+def _golden(name):
+    import os
+    return np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", name))
+
+
+@pytest.mark.parametrize("name", ["config0", "tail_3x17", "odd_33x65", "down_m4"])
+def test_golden_dense(orc, torch_dev, bn, name):
+    # GPU Dense forward against the committed fixtures (written from the
+    # oracle by tests/golden/make_golden.py), bit for bit.
+    import json
+    import os
+    from tests.golden import make_golden as mg
+    torch = torch_dev
+    w, x = mg.dense_inputs(name)
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "manifest.json")) as f:
+        m = json.load(f)["dense"][name]
+    assert mg.sha(w.words, np.float32(w.scale), x) == m["inputs_sha256"]
+    pre, _, taps = bn.dense_forward_packed_ternary(gpu_matrix(bn, w), to_dev(torch, x), taps=True)
+    torch.cuda.synchronize()
+    pre = pre.cpu().numpy()
+    acc = taps.acc.cpu().numpy()
+    assert mg.sha(pre) == m["pre_sha256"] and mg.sha(acc) == m["acc_sha256"]
+
+
+def test_golden_ms_offline_kat(orc, torch_dev, bn):
+    # TestMicrosoftOfflinePackedBitNetRowsDecode (poly/tests/bitnet_cpu_test.go:334-362)
+    # through the GPU offline import: xq {2,-3} with amax 127 (x = xq exactly).
+    import json
+    import os
+    torch = torch_dev
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "reference_kats.json")) as f:
+        k = json.load(f)["microsoft_offline_decode"]
+    w = bn.TernaryMatrix.from_ms_offline(np.array(k["packed"], np.uint8), k["rows"], k["cols"], k["scale"])
+    # the KAT fixes xq and amax: feed them to the quantized matvec directly
+    xq = np.zeros((1, bn.padded_cols(k["cols"])), np.int8)
+    xq[0, :k["cols"]] = k["xq"]
+    q = bn.QuantizedRows(to_dev(torch, xq), to_dev(torch, np.array([k["amax"]], np.float32)),
+                         to_dev(torch, np.array([sum(k["xq"])], np.int32)), k["cols"])
+    out = bn.ternary_matvec_quantized(w, q)
+    assert np.allclose(out.cpu().numpy()[0], k["out"], atol=1e-6, rtol=0)
+
+
+@pytest.mark.parametrize("rows,cols", [(8, 4), (64, 2560), (128, 6912), (7, 33), (2, 5)])
+def test_ms_offline_import_matches_oracle(orc, torch_dev, bn, rows, cols):
+    # packMicrosoftOfflineBitNetRowsToU32FromBytes (poly/bitnet_cpu.go:1078-1098)
+    # on the device == the oracle's packer, seen through a Dense forward.
+    torch = torch_dev
+    rng = np.random.default_rng(rows * 1000 + cols)
+    packed = rng.integers(0, 256, size=(rows // 4) * cols, dtype=np.uint8)
+    ref = orc.pack_ms_offline_bytes(packed, rows, cols, scale=0.5)
+    x = orc.normal_f32(3 * cols, rows + cols).reshape(3, cols)
+    want = orc.dense_forward(ref, x, simd=False)
+    w = bn.TernaryMatrix.from_ms_offline(packed, rows, cols, 0.5)
+    pre, _, taps = bn.dense_forward_packed_ternary(w, to_dev(torch, x), taps=True)
+    assert np.array_equal(taps.acc.cpu().numpy(), want.acc)
+    assert np.array_equal(pre.cpu().numpy(), want.pre)
+
+
+def test_golden_swiglu(orc, torch_dev, bn):
+    from tests.golden import make_golden as mg
+    torch = torch_dev
+    g, u, d, wn, x = mg.swiglu_inputs()
+    f = _golden("swiglu_small.npz")
+    for act in (mg.ACT_SILU, mg.ACT_RELU2):
+        h, out = bn.swiglu_forward_packed_ternary(gpu_matrix(bn, g), gpu_matrix(bn, u), gpu_matrix(bn, d),
+                                                  to_dev(torch, x), inner_norm=to_dev(torch, wn),
+                                                  eps=1e-5, activation=act)
+        h = h.cpu().numpy()
+        out = out.cpu().numpy()
+        if act == mg.ACT_RELU2:  # no exp(): every stage bit-exact
+            assert np.array_equal(h, f[f"h_{act}"]) and np.array_equal(out, f[f"out_{act}"])
+        else:  # exp() last bits: h within 1 fp32 ulp
+            assert ulp_diff_f32(h, f[f"h_{act}"]).max() <= 1
