@@ -432,6 +432,195 @@ __global__ __launch_bounds__(256) void attention_kernel(const double* __restrict
     softmax_pv<STRICT, 256>(p, L, vb, kv_dim, hd, red, orow);
 }
 
+// ---- prefill path: query tiles -------------------------------------------
+// One workgroup per (head, tile of kTileQ consecutive queries, sequence).  K
+// and V chunks of kChunkP positions are staged through LDS (the next chunk is
+// prefetched into registers while the current one is used), so each cached
+// row is read once per tile instead of once per query.  Pass 1 forms every
+// score of the tile and keeps each query's maximum; pass 2 forms the same
+// scores again (same chains, same values), takes p = exp(score - max), adds
+// expSum on one lane per query and sum(p * v) on one lane per (query, d), all
+// in position order.  Every sum therefore has the reference's order: the
+// tile kernel is exact in both norm modes.  Positions past a query's own
+// position are skipped (never added).
+constexpr int kTileQ = 32;
+constexpr int kChunkP = 32;
+
+template <int HD>
+struct TileLds {
+    double q[kTileQ][HD];
+    float kv[kChunkP][HD + 1];  // K chunk, then V chunk (+1: conflict-free row reads)
+    double p[kTileQ][kChunkP];
+    double mx[kTileQ];
+    double es[kTileQ];
+};
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict__ q,
+                                                        const float* __restrict__ cache_k,
+                                                        const float* __restrict__ cache_v,
+                                                        const int* __restrict__ pos0, int msl,
+                                                        int span, int heads, int kv_heads, int seq,
+                                                        double* __restrict__ out) {
+    constexpr int DB = HD / 32;                       // value columns per PV lane
+    constexpr int F4 = kChunkP * HD / 4 / 256;        // float4 per thread per chunk
+    static_assert(F4 >= 1 && kChunkP * HD == F4 * 4 * 256, "chunk geometry");
+    __shared__ TileLds<HD> sm;
+    const int tid = threadIdx.x;
+    const int h = blockIdx.x;
+    const int tile = gridDim.y - 1 - blockIdx.y;  // longest tiles first
+    const int b = blockIdx.z;
+    const int s0 = tile * kTileQ;
+    const int nq = min(kTileQ, seq - s0);
+    const int base = *pos0;
+    const int q_dim = heads * HD, kv_dim = kv_heads * HD;
+    const int kvh = h / (heads / kv_heads);
+    const size_t row0 = (size_t)b * seq + s0;
+    if (base + s0 + nq > span) {
+        for (int i = tid; i < nq * HD; i += 256)
+            out[(row0 + i / HD) * q_dim + (size_t)h * HD + i % HD] = __builtin_nan("");
+        return;
+    }
+    const int nch = (base + s0 + nq + kChunkP - 1) / kChunkP;
+    const float* kb = cache_k + (size_t)b * msl * kv_dim + (size_t)kvh * HD;
+    const float* vb = cache_v + (size_t)b * msl * kv_dim + (size_t)kvh * HD;
+    for (int i = tid; i < kTileQ * HD; i += 256) {
+        const int qi = i / HD;
+        sm.q[qi][i % HD] = qi < nq ? q[(row0 + qi) * q_dim + (size_t)h * HD + i % HD] : 0.0;
+    }
+    // chunk loads: branch-free (rows clamped into the ring)
+    float4 rk[F4];
+    auto load = [&](const float* src, int c) {
+#pragma unroll
+        for (int j = 0; j < F4; ++j) {
+            const int e = (tid + j * 256) * 4;
+            const int k = min(c * kChunkP + e / HD, msl - 1);
+            rk[j] = *(const float4*)(src + (size_t)k * kv_dim + e % HD);
+        }
+    };
+    auto store = [&]() {
+#pragma unroll
+        for (int j = 0; j < F4; ++j) {
+            const int e = (tid + j * 256) * 4;
+            float* d = &sm.kv[e / HD][e % HD];
+            d[0] = rk[j].x;
+            d[1] = rk[j].y;
+            d[2] = rk[j].z;
+            d[3] = rk[j].w;
+        }
+    };
+    // score lanes: queries 2*qp, 2*qp+1 x chunk positions 2*pp, 2*pp+1
+    const int qp = tid >> 4, pp = tid & 15;
+    const int qa = 2 * qp;
+    const int lim_a = base + s0 + qa;  // last position query qa sees
+    const double scale = 1.0 / sqrt((double)HD);
+    auto scores = [&](double (&sc)[2][2]) {
+        double d00 = 0.0, d01 = 0.0, d10 = 0.0, d11 = 0.0;
+        const float* k0 = sm.kv[2 * pp];
+        const float* k1 = sm.kv[2 * pp + 1];
+        const double* q0 = sm.q[qa];
+        const double* q1 = sm.q[qa + 1];
+#pragma unroll 8
+        for (int d = 0; d < HD; ++d) {
+            const double a0 = q0[d], a1 = q1[d];
+            const double b0 = (double)k0[d], b1 = (double)k1[d];
+            d00 += a0 * b0;
+            d01 += a0 * b1;
+            d10 += a1 * b0;
+            d11 += a1 * b1;
+        }
+        sc[0][0] = d00 * scale;
+        sc[0][1] = d01 * scale;
+        sc[1][0] = d10 * scale;
+        sc[1][1] = d11 * scale;
+    };
+
+    // ---- pass 1: maxima -------------------------------------------------
+    double m0 = -1e9, m1 = -1e9;
+    load(kb, 0);
+    for (int c = 0; c < nch; ++c) {
+        __syncthreads();  // previous chunk fully read
+        store();
+        load(kb, c + 1);  // prefetch (clamped past the last chunk)
+        __syncthreads();
+        double sc[2][2];
+        scores(sc);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int k = c * kChunkP + 2 * pp + j;
+            if (k <= lim_a && sc[0][j] > m0) m0 = sc[0][j];
+            if (k <= lim_a + 1 && sc[1][j] > m1) m1 = sc[1][j];
+        }
+    }
+    // maximum over the 16 lanes of each query pair (order-free)
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) {
+        const double o0 = __shfl_xor(m0, off, 16), o1 = __shfl_xor(m1, off, 16);
+        m0 = o0 > m0 ? o0 : m0;
+        m1 = o1 > m1 ? o1 : m1;
+    }
+    if (pp == 0) {
+        sm.mx[qa] = m0;
+        sm.mx[qa + 1] = m1;
+    }
+    // ---- pass 2: probabilities, expSum, PV --------------------------------
+    const int pq = tid >> 5, dl = tid & 31;  // PV lanes: queries 4*pq..+3, columns dl + 32*j
+    double acc[4][DB];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < DB; ++j) acc[i][j] = 0.0;
+    double es = 0.0;  // lane tid < kTileQ: query tid
+    load(kb, 0);
+    for (int c = 0; c < nch; ++c) {
+        __syncthreads();
+        store();      // K chunk c
+        load(vb, c);  // V chunk c, used after the scores
+        __syncthreads();
+        double sc[2][2];
+        scores(sc);
+        const double ma = sm.mx[qa], mb = sm.mx[qa + 1];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int k = c * kChunkP + 2 * pp + j;
+            sm.p[qa][2 * pp + j] = k <= lim_a ? exp(sc[0][j] - ma) : 0.0;
+            sm.p[qa + 1][2 * pp + j] = k <= lim_a + 1 ? exp(sc[1][j] - mb) : 0.0;
+        }
+        __syncthreads();  // probabilities written, K chunk read
+        store();          // V chunk c
+        load(kb, c + 1);  // next K chunk, used after the PV sums
+        __syncthreads();
+        const int kc = c * kChunkP;
+        if (tid < kTileQ) {
+            const int lim = base + s0 + tid;
+            for (int k = 0; k < kChunkP; ++k)
+                if (kc + k <= lim) es += sm.p[tid][k];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int qi = 4 * pq + i;
+            const int n = min(kChunkP, base + s0 + qi + 1 - kc);  // valid positions of this chunk
+            for (int k = 0; k < n; ++k) {
+                const double pk = sm.p[qi][k];
+#pragma unroll
+                for (int j = 0; j < DB; ++j) acc[i][j] += pk * (double)sm.kv[k][dl + 32 * j];
+            }
+        }
+    }
+    if (tid < kTileQ) sm.es[tid] = es;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int qi = 4 * pq + i;
+        if (qi < nq) {
+            const double e = sm.es[qi];
+#pragma unroll
+            for (int j = 0; j < DB; ++j)
+                out[(row0 + qi) * q_dim + (size_t)h * HD + dl + 32 * j] = acc[i][j] / e;
+        }
+    }
+}
+
 // ---- decode path (few query rows) ----------------------------------------
 // Scratch layout per (row, head): scores[span] (probabilities after the exp
 // step), chunk maxima cmax[nchunk] (64 positions per chunk), and for the
@@ -777,6 +966,17 @@ hipError_t launch_attention(const double* q, const float* cache_k, const float* 
                     hipLaunchKernelGGL(attn_chain_kernel<256>, g, t, 0, s, cache_v, pos0, msl, span, heads, kv_heads, seq, sc, out);
                     break;
             }
+        }
+        return hipGetLastError();
+    }
+    if (hd == 64 || hd == 128) {
+        const dim3 grid(heads, ceil_div(seq, kTileQ), batch);
+        if (hd == 128) {
+            hipLaunchKernelGGL(attn_tile_kernel<128>, grid, dim3(256), 0, s, q, cache_k, cache_v, pos0,
+                               msl, span, heads, kv_heads, seq, out);
+        } else {
+            hipLaunchKernelGGL(attn_tile_kernel<64>, grid, dim3(256), 0, s, q, cache_k, cache_v, pos0,
+                               msl, span, heads, kv_heads, seq, out);
         }
         return hipGetLastError();
     }
