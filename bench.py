@@ -40,6 +40,18 @@ UP = (6912, 2560)    # (N, K) of up/gate
 DOWN = (2560, 6912)  # (N, K) of down
 
 
+def pmc_traffic():
+    """HBM bytes per launch of the GEMV kernel from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE runs of this same workload (profiles/
+    gemv_m1_up_pmc.md: counters scaled by a copy kernel of known size)."""
+    path = os.path.join(ROOT, "profiles", "gemv_m1_up_pmc.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["traffic_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def gemv_bytes(m: int, n: int, k: int) -> int:
     return n * ((k + 15) // 16) * 4 + 4 * m * (k + n)
 
@@ -332,6 +344,8 @@ def main() -> int:
     ap.add_argument("--no-model", action="store_true", help="skip configs 2-4")
     ap.add_argument("--model-layers", type=int, default=30)
     ap.add_argument("--model-norms", default="fast,strict")
+    ap.add_argument("--calibrate-copy", type=int, default=0,
+                    help="also run 4 device copies of this many MiB (PMC byte-counter calibration)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -406,7 +420,8 @@ def main() -> int:
                    "M": 1, "K": k, "N": n, "rotating_copies": rot,
                    "kernel": _lib.lib().loom_amd_kernel_variant(1).decode()},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": pmc_traffic(),
                      "kernel": "skinny_matmul_kernel<1,1,8> (ternary GEMV)",
                      "us_per_launch": round(ms_kernel * 1e3, 3), "bytes_per_launch": b1},
     }
@@ -458,7 +473,22 @@ def main() -> int:
     if not args.no_model:
         result.update(bench_model(args, torch, timer, log))
 
+    # ---------------- copy kernel of known size (PMC calibration runs) ---------------
+    if args.calibrate_copy > 0:
+        nbytes = int(args.calibrate_copy) << 20
+        src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        result["calibration_copy_bytes"] = nbytes
+        log(f"calibration: 4 device copies of {nbytes} B")
+
     # ---------------- CPU baseline (oracle port of loom's bitnet_simd path) -------
+    if args.cpu_seconds <= 0:
+        print(json.dumps(result), flush=True)
+        return 0
     cores = cpu_cores()
     xs = orc.normal_f32(k, seed=1).reshape(1, k)
     host_up.ensure_codes()
