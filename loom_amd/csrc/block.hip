@@ -437,19 +437,20 @@ __global__ __launch_bounds__(256) void attention_kernel(const double* __restrict
 // and V chunks of kChunkP positions are staged through LDS (the next chunk is
 // prefetched into registers while the current one is used), so each cached
 // row is read once per tile instead of once per query.  Pass 1 forms every
-// score of the tile and keeps each query's maximum; pass 2 forms the same
-// scores again (same chains, same values), takes p = exp(score - max), adds
-// expSum on one lane per query and sum(p * v) on one lane per (query, d), all
-// in position order.  Every sum therefore has the reference's order: the
-// tile kernel is exact in both norm modes.  Positions past a query's own
-// position are skipped (never added).
+// score of the tile (each lane a 2 x 2 block of d-order chains), keeps each
+// query's maximum and stores the scores in `sc` (rows x heads x span);
+// pass 2 reads them back, takes p = exp(score - max), adds expSum on one lane
+// per query and sum(p * v) on one lane per (query, d), all in position order.
+// Every sum therefore has the reference's order: the tile kernel is exact in
+// both norm modes.  Positions past a query's own position are skipped (never
+// added).
 constexpr int kTileQ = 32;
 constexpr int kChunkP = 32;
 
 template <int HD>
 struct TileLds {
     double q[kTileQ][HD];
-    float kv[kChunkP][HD + 1];  // K chunk, then V chunk (+1: conflict-free row reads)
+    float kv[kChunkP][HD + 1];  // K chunk (pass 1) or V chunk (pass 2); +1: conflict-free rows
     double p[kTileQ][kChunkP];
     double mx[kTileQ];
     double es[kTileQ];
@@ -461,6 +462,7 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict
                                                         const float* __restrict__ cache_v,
                                                         const int* __restrict__ pos0, int msl,
                                                         int span, int heads, int kv_heads, int seq,
+                                                        double* __restrict__ sc_all,
                                                         double* __restrict__ out) {
     constexpr int DB = HD / 32;                       // value columns per PV lane
     constexpr int F4 = kChunkP * HD / 4 / 256;        // float4 per thread per chunk
@@ -509,12 +511,26 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict
             d[3] = rk[j].w;
         }
     };
-    // score lanes: queries 2*qp, 2*qp+1 x chunk positions 2*pp, 2*pp+1
+    // score lanes: queries qa = 2*qp, qa+1 x chunk positions 2*pp, 2*pp+1;
+    // their scores live at sca[k], sca[span + k] (rows qa, qa+1 of the tile)
     const int qp = tid >> 4, pp = tid & 15;
     const int qa = 2 * qp;
     const int lim_a = base + s0 + qa;  // last position query qa sees
     const double scale = 1.0 / sqrt((double)HD);
-    auto scores = [&](double (&sc)[2][2]) {
+    // rows past the tile's last query (a partial tile) neither store nor use
+    // scores; their reads are clamped onto the last query's row
+    const bool w0 = qa < nq, w1 = qa + 1 < nq;
+    double* sca = sc_all + ((row0 + min(qa, nq - 1)) * heads + h) * (size_t)span;
+    const size_t sc_next = w1 ? (size_t)heads * span : 0;  // row qa+1
+
+    // ---- pass 1: scores and maxima ---------------------------------------
+    double m0 = -1e9, m1 = -1e9;
+    load(kb, 0);
+    for (int c = 0; c < nch; ++c) {
+        __syncthreads();  // previous chunk fully read
+        store();
+        load(kb, c + 1);  // prefetch (clamped past the last chunk)
+        __syncthreads();
         double d00 = 0.0, d01 = 0.0, d10 = 0.0, d11 = 0.0;
         const float* k0 = sm.kv[2 * pp];
         const float* k1 = sm.kv[2 * pp + 1];
@@ -529,28 +545,16 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict
             d10 += a1 * b0;
             d11 += a1 * b1;
         }
-        sc[0][0] = d00 * scale;
-        sc[0][1] = d01 * scale;
-        sc[1][0] = d10 * scale;
-        sc[1][1] = d11 * scale;
-    };
-
-    // ---- pass 1: maxima -------------------------------------------------
-    double m0 = -1e9, m1 = -1e9;
-    load(kb, 0);
-    for (int c = 0; c < nch; ++c) {
-        __syncthreads();  // previous chunk fully read
-        store();
-        load(kb, c + 1);  // prefetch (clamped past the last chunk)
-        __syncthreads();
-        double sc[2][2];
-        scores(sc);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int k = c * kChunkP + 2 * pp + j;
-            if (k <= lim_a && sc[0][j] > m0) m0 = sc[0][j];
-            if (k <= lim_a + 1 && sc[1][j] > m1) m1 = sc[1][j];
+        const double s00 = d00 * scale, s01 = d01 * scale, s10 = d10 * scale, s11 = d11 * scale;
+        const int k = c * kChunkP + 2 * pp;
+        if (k + 1 < span) {
+            if (w0) *(double2*)(sca + k) = make_double2(s00, s01);
+            if (w1) *(double2*)(sca + sc_next + k) = make_double2(s10, s11);
         }
+        if (k <= lim_a && s00 > m0) m0 = s00;
+        if (k + 1 <= lim_a && s01 > m0) m0 = s01;
+        if (k <= lim_a + 1 && s10 > m1) m1 = s10;
+        if (k + 1 <= lim_a + 1 && s11 > m1) m1 = s11;
     }
     // maximum over the 16 lanes of each query pair (order-free)
 #pragma unroll
@@ -558,10 +562,6 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict
         const double o0 = __shfl_xor(m0, off, 16), o1 = __shfl_xor(m1, off, 16);
         m0 = o0 > m0 ? o0 : m0;
         m1 = o1 > m1 ? o1 : m1;
-    }
-    if (pp == 0) {
-        sm.mx[qa] = m0;
-        sm.mx[qa + 1] = m1;
     }
     // ---- pass 2: probabilities, expSum, PV --------------------------------
     const int pq = tid >> 5, dl = tid & 31;  // PV lanes: queries 4*pq..+3, columns dl + 32*j
@@ -571,39 +571,42 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict
 #pragma unroll
         for (int j = 0; j < DB; ++j) acc[i][j] = 0.0;
     double es = 0.0;  // lane tid < kTileQ: query tid
-    load(kb, 0);
+    // this lane's four scores of chunk c (clamped past the end; surplus unused)
+    double2 sv0, sv1;
+    auto load_scores = [&](int c) {
+        const int k = min(c, nch - 1) * kChunkP + 2 * pp;
+        const int kk = min(k, span - 2);
+        sv0 = *(const double2*)(sca + kk);
+        sv1 = *(const double2*)(sca + sc_next + kk);
+    };
+    __syncthreads();  // pass-1 reads of sm.kv done before V overwrites it
+    load(vb, 0);
+    load_scores(0);
     for (int c = 0; c < nch; ++c) {
-        __syncthreads();
-        store();      // K chunk c
-        load(vb, c);  // V chunk c, used after the scores
-        __syncthreads();
-        double sc[2][2];
-        scores(sc);
-        const double ma = sm.mx[qa], mb = sm.mx[qa + 1];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int k = c * kChunkP + 2 * pp + j;
-            sm.p[qa][2 * pp + j] = k <= lim_a ? exp(sc[0][j] - ma) : 0.0;
-            sm.p[qa + 1][2 * pp + j] = k <= lim_a + 1 ? exp(sc[1][j] - mb) : 0.0;
-        }
-        __syncthreads();  // probabilities written, K chunk read
+        __syncthreads();  // previous chunk's PV reads done
         store();          // V chunk c
-        load(kb, c + 1);  // next K chunk, used after the PV sums
+        const int k = c * kChunkP + 2 * pp;
+        sm.p[qa][2 * pp] = k <= lim_a ? exp(sv0.x - m0) : 0.0;
+        sm.p[qa][2 * pp + 1] = k + 1 <= lim_a ? exp(sv0.y - m0) : 0.0;
+        sm.p[qa + 1][2 * pp] = k <= lim_a + 1 ? exp(sv1.x - m1) : 0.0;
+        sm.p[qa + 1][2 * pp + 1] = k + 1 <= lim_a + 1 ? exp(sv1.y - m1) : 0.0;
+        load(vb, c + 1);   // next V chunk
+        load_scores(c + 1);
         __syncthreads();
         const int kc = c * kChunkP;
         if (tid < kTileQ) {
             const int lim = base + s0 + tid;
-            for (int k = 0; k < kChunkP; ++k)
-                if (kc + k <= lim) es += sm.p[tid][k];
+            for (int kk = 0; kk < kChunkP; ++kk)
+                if (kc + kk <= lim) es += sm.p[tid][kk];
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int qi = 4 * pq + i;
             const int n = min(kChunkP, base + s0 + qi + 1 - kc);  // valid positions of this chunk
-            for (int k = 0; k < n; ++k) {
-                const double pk = sm.p[qi][k];
+            for (int kk = 0; kk < n; ++kk) {
+                const double pk = sm.p[qi][kk];
 #pragma unroll
-                for (int j = 0; j < DB; ++j) acc[i][j] += pk * (double)sm.kv[k][dl + 32 * j];
+                for (int j = 0; j < DB; ++j) acc[i][j] += pk * (double)sm.kv[kk][dl + 32 * j];
             }
         }
     }
@@ -910,7 +913,8 @@ size_t attention_lds_bytes(int hd, int span) {
 }
 
 size_t attention_scratch_bytes(int rows, int heads, int hd, int span) {
-    if (rows > kSplitMaxRows) return 0;
+    // prefill tiles: every score of every row (rows x heads x span fp64)
+    if (rows > kSplitMaxRows) return (hd == 64 || hd == 128) ? (size_t)rows * heads * span * 8 : 0;
     const size_t rh = (size_t)rows * heads;
     const size_t nc = attn_nchunk(span);
     return rh * ((size_t)span + nc + nc * hd + nc) * sizeof(double);
@@ -970,13 +974,14 @@ hipError_t launch_attention(const double* q, const float* cache_k, const float* 
         return hipGetLastError();
     }
     if (hd == 64 || hd == 128) {
+        if (!scratch || span % 2 != 0) return hipErrorInvalidValue;
         const dim3 grid(heads, ceil_div(seq, kTileQ), batch);
         if (hd == 128) {
             hipLaunchKernelGGL(attn_tile_kernel<128>, grid, dim3(256), 0, s, q, cache_k, cache_v, pos0,
-                               msl, span, heads, kv_heads, seq, out);
+                               msl, span, heads, kv_heads, seq, scratch, out);
         } else {
             hipLaunchKernelGGL(attn_tile_kernel<64>, grid, dim3(256), 0, s, q, cache_k, cache_v, pos0,
-                               msl, span, heads, kv_heads, seq, out);
+                               msl, span, heads, kv_heads, seq, scratch, out);
         }
         return hipGetLastError();
     }

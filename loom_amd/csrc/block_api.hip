@@ -44,7 +44,7 @@ struct Workspace {
     int32_t* acc = nullptr;  // rows x (q_dim + 2 kv_dim)
     double* q = nullptr;     // rows x q_dim
     double* attn = nullptr;  // rows x q_dim
-    double* scores = nullptr;  // min(rows, kSplitMaxRows) x heads x span (decode attention)
+    double* scores = nullptr;  // attention scratch (decode: partial results; prefill: scores)
     int8_t* aq = nullptr;    // rows x pad(q_dim)
     float* amax2 = nullptr;
     int32_t* xsum2 = nullptr;
@@ -63,8 +63,10 @@ static size_t workspace_layout(const BlockDev& B, int rows, Workspace* W, char* 
     const size_t o_acc = L.take(r * (B.q_dim + 2 * B.kv_dim) * 4);
     const size_t o_q = L.take(r * B.q_dim * 8);
     const size_t o_at = L.take(r * B.q_dim * 8);
-    const size_t o_sc = L.take(attention_scratch_bytes(rows < kSplitMaxRows ? rows : kSplitMaxRows,
-                                                       B.heads, B.hd, B.span()));
+    const size_t sc_small = attention_scratch_bytes(rows < kSplitMaxRows ? rows : kSplitMaxRows,
+                                                    B.heads, B.hd, B.span());
+    const size_t sc_big = attention_scratch_bytes(rows, B.heads, B.hd, B.span());
+    const size_t o_sc = L.take(sc_small > sc_big ? sc_small : sc_big);
     const size_t o_aq = L.take(r * pad_cols(B.q_dim));
     const size_t o_am2 = L.take(r * 4);
     const size_t o_xs2 = L.take(r * 4);

@@ -191,7 +191,7 @@ def run_block_case(orc, torch, tf, w: Weights, seqs, seed, strict=True):
     blk.release()
 
 
-@pytest.mark.parametrize("seqs", [[1], [5], [9, 1, 1, 1], [64]])
+@pytest.mark.parametrize("seqs", [[1], [5], [9, 1, 1, 1], [64], [37, 1], [17]])
 def test_block_stages_small(orc, torch_dev, tf, seqs):
     w = Weights(orc, SMALL, seed=101)
     run_block_case(orc, torch_dev, tf, w, seqs, seed=900)
