@@ -441,9 +441,10 @@ __global__ __launch_bounds__(256) void attention_kernel(const double* __restrict
 // query's maximum and stores the scores in `sc` (rows x heads x span);
 // pass 2 reads them back, takes p = exp(score - max), adds expSum on one lane
 // per query and sum(p * v) on one lane per (query, d), all in position order.
-// Every sum therefore has the reference's order: the tile kernel is exact in
-// both norm modes.  Positions past a query's own position are skipped (never
-// added).
+// Every sum therefore has the reference's order and, with FMA false, the
+// reference's roundings: exact.  FMA true (fast mode) contracts each
+// multiply-add of the dot and value chains into one rounding.  Positions past
+// a query's own position are skipped (never added).
 constexpr int kTileQ = 32;
 constexpr int kChunkP = 32;
 
@@ -456,7 +457,7 @@ struct TileLds {
     double es[kTileQ];
 };
 
-template <int HD>
+template <int HD, bool FMA>
 __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict__ q,
                                                         const float* __restrict__ cache_k,
                                                         const float* __restrict__ cache_v,
@@ -540,10 +541,17 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict
         for (int d = 0; d < HD; ++d) {
             const double a0 = q0[d], a1 = q1[d];
             const double b0 = (double)k0[d], b1 = (double)k1[d];
-            d00 += a0 * b0;
-            d01 += a0 * b1;
-            d10 += a1 * b0;
-            d11 += a1 * b1;
+            if (FMA) {
+                d00 = fma(a0, b0, d00);
+                d01 = fma(a0, b1, d01);
+                d10 = fma(a1, b0, d10);
+                d11 = fma(a1, b1, d11);
+            } else {
+                d00 += a0 * b0;
+                d01 += a0 * b1;
+                d10 += a1 * b0;
+                d11 += a1 * b1;
+            }
         }
         const double s00 = d00 * scale, s01 = d01 * scale, s10 = d10 * scale, s11 = d11 * scale;
         const int k = c * kChunkP + 2 * pp;
@@ -606,7 +614,10 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict
             for (int kk = 0; kk < n; ++kk) {
                 const double pk = sm.p[qi][kk];
 #pragma unroll
-                for (int j = 0; j < DB; ++j) acc[i][j] += pk * (double)sm.kv[kk][dl + 32 * j];
+                for (int j = 0; j < DB; ++j) {
+                    const double v = (double)sm.kv[kk][dl + 32 * j];
+                    acc[i][j] = FMA ? fma(pk, v, acc[i][j]) : acc[i][j] + pk * v;
+                }
             }
         }
     }
@@ -976,13 +987,15 @@ hipError_t launch_attention(const double* q, const float* cache_k, const float* 
     if (hd == 64 || hd == 128) {
         if (!scratch || span % 2 != 0) return hipErrorInvalidValue;
         const dim3 grid(heads, ceil_div(seq, kTileQ), batch);
+#define LAMD_TILE(HDV, F)                                                                          \
+    hipLaunchKernelGGL((attn_tile_kernel<HDV, F>), grid, dim3(256), 0, s, q, cache_k, cache_v, pos0, \
+                       msl, span, heads, kv_heads, seq, scratch, out)
         if (hd == 128) {
-            hipLaunchKernelGGL(attn_tile_kernel<128>, grid, dim3(256), 0, s, q, cache_k, cache_v, pos0,
-                               msl, span, heads, kv_heads, seq, scratch, out);
+            if (strict) LAMD_TILE(128, false); else LAMD_TILE(128, true);
         } else {
-            hipLaunchKernelGGL(attn_tile_kernel<64>, grid, dim3(256), 0, s, q, cache_k, cache_v, pos0,
-                               msl, span, heads, kv_heads, seq, scratch, out);
+            if (strict) LAMD_TILE(64, false); else LAMD_TILE(64, true);
         }
+#undef LAMD_TILE
         return hipGetLastError();
     }
     const size_t shm = attention_lds_bytes(hd, span);

@@ -210,9 +210,17 @@ def test_block_stages_mha_no_gqa(orc, torch_dev, tf):
     run_block_case(orc, torch_dev, tf, w, [6, 1], seed=920)
 
 
-def test_block_stages_fast_norm(orc, torch_dev, tf):
+@pytest.mark.parametrize("seqs", [[12, 1], [40, 1]])
+def test_block_stages_fast_norm(orc, torch_dev, tf, seqs):
+    # fast mode: tree / chunked sums, fused multiply-adds in the prefill tiles
     w = Weights(orc, SMALL, seed=151)
-    run_block_case(orc, torch_dev, tf, w, [12, 1], seed=930, strict=False)
+    run_block_case(orc, torch_dev, tf, w, seqs, seed=930, strict=False)
+
+
+def test_block_fast_prefill_bitnet_2b(orc, torch_dev, tf):
+    # fast prefill tiles at the BitNet-2B head size (128)
+    w = Weights(orc, BITNET_2B, seed=155)
+    run_block_case(orc, torch_dev, tf, w, [70, 1], seed=935, strict=False)
 
 
 def test_block_stages_bitnet_2b_shape(orc, torch_dev, tf):
