@@ -635,6 +635,185 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict
     }
 }
 
+// ---- prefill path, fast mode: fp64 MFMA tiles -------------------------------
+// Same tiling and two passes as attn_tile_kernel, with the score and value
+// sums on v_mfma_f64_16x16x4f64 (lane l supplies A[l%16][l/16] and
+// B[l/16][l%16]; element v of lane l is D[4v + l/16][l%16]).  Each MFMA adds
+// four products at once, so the d-order and position-order chains become
+// 4-wide blocks: fast mode only.  Masked positions enter the value MFMAs with
+// p = 0 (the cached rows they meet are finite).  The Q fragments stay in
+// registers for the whole tile.  4 waves: for the scores, wave w owns query
+// tile w/2 and position tile w%2 of a 32 x 32 block; for the values, query
+// tile w/2 and HD/32 tiles of 16 value columns.
+typedef double v4d __attribute__((ext_vector_type(4)));
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_tile_mfma_kernel(const double* __restrict__ q,
+                                                             const float* __restrict__ cache_k,
+                                                             const float* __restrict__ cache_v,
+                                                             const int* __restrict__ pos0, int msl,
+                                                             int span, int heads, int kv_heads,
+                                                             int seq, double* __restrict__ sc_all,
+                                                             double* __restrict__ out) {
+    constexpr int NM = HD / 4;   // score MFMAs along d
+    constexpr int DT = HD / 32;  // value tiles (16 columns) per wave
+    constexpr int F4 = kChunkP * HD / 4 / 256;
+    static_assert(F4 >= 1 && kChunkP * HD == F4 * 4 * 256, "chunk geometry");
+    __shared__ float kv[kChunkP][HD + 1];
+    __shared__ double pt[kTileQ][kChunkP + 1];
+    __shared__ double mxs[2][kTileQ];
+    __shared__ double ess[kTileQ];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lr = lane & 15, lg = lane >> 4;
+    const int h = blockIdx.x;
+    const int tile = gridDim.y - 1 - blockIdx.y;
+    const int b = blockIdx.z;
+    const int s0 = tile * kTileQ;
+    const int nq = min(kTileQ, seq - s0);
+    const int base = *pos0;
+    const int q_dim = heads * HD, kv_dim = kv_heads * HD;
+    const int kvh = h / (heads / kv_heads);
+    const size_t row0 = (size_t)b * seq + s0;
+    if (base + s0 + nq > span) {
+        for (int i = tid; i < nq * HD; i += 256)
+            out[(row0 + i / HD) * q_dim + (size_t)h * HD + i % HD] = __builtin_nan("");
+        return;
+    }
+    const int nch = (base + s0 + nq + kChunkP - 1) / kChunkP;
+    const float* kb = cache_k + (size_t)b * msl * kv_dim + (size_t)kvh * HD;
+    const float* vb = cache_v + (size_t)b * msl * kv_dim + (size_t)kvh * HD;
+    float4 rk[F4];
+    auto load = [&](const float* src, int c) {
+#pragma unroll
+        for (int j = 0; j < F4; ++j) {
+            const int e = (tid + j * 256) * 4;
+            const int k = min(c * kChunkP + e / HD, msl - 1);
+            rk[j] = *(const float4*)(src + (size_t)k * kv_dim + e % HD);
+        }
+    };
+    auto store = [&]() {
+#pragma unroll
+        for (int j = 0; j < F4; ++j) {
+            const int e = (tid + j * 256) * 4;
+            float* d = &kv[e / HD][e % HD];
+            d[0] = rk[j].x;
+            d[1] = rk[j].y;
+            d[2] = rk[j].z;
+            d[3] = rk[j].w;
+        }
+    };
+    const int qt = wave >> 1, kt = wave & 1;
+    // Q fragment: Q[16 qt + lr][4 m + lg]
+    double qa[NM];
+    {
+        const int qr = 16 * qt + lr;
+        const double* src = q + (row0 + min(qr, nq - 1)) * q_dim + (size_t)h * HD + lg;
+#pragma unroll
+        for (int m = 0; m < NM; ++m) qa[m] = qr < nq ? src[4 * m] : 0.0;
+    }
+    const double scale = 1.0 / sqrt((double)HD);
+    // this lane's score slots: rows qi(v) = 16 qt + 4 v + lg, position 16 kt + lr
+    double* scr[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int qi = 16 * qt + 4 * v + lg;
+        scr[v] = sc_all + ((row0 + min(qi, nq - 1)) * heads + h) * (size_t)span;
+    }
+
+    // ---- pass 1 ---------------------------------------------------------------
+    double mv[4] = {-1e9, -1e9, -1e9, -1e9};
+    load(kb, 0);
+    for (int c = 0; c < nch; ++c) {
+        __syncthreads();
+        store();
+        load(kb, c + 1);
+        __syncthreads();
+        v4d acc = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            const double bk = (double)kv[16 * kt + lr][4 * m + lg];
+            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(qa[m], bk, acc, 0, 0, 0);
+        }
+        const int k = c * kChunkP + 16 * kt + lr;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int qi = 16 * qt + 4 * v + lg;
+            const double sv = acc[v] * scale;
+            if (qi < nq && k < span) scr[v][k] = sv;
+            if (k <= base + s0 + qi && sv > mv[v]) mv[v] = sv;
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+#pragma unroll
+        for (int off = 8; off > 0; off >>= 1) {
+            const double o = __shfl_xor(mv[v], off, 16);
+            mv[v] = o > mv[v] ? o : mv[v];
+        }
+        if (lr == 0) mxs[kt][16 * qt + 4 * v + lg] = mv[v];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int qi = 16 * qt + 4 * v + lg;
+        const double a = mxs[0][qi], c2 = mxs[1][qi];
+        mv[v] = c2 > a ? c2 : a;
+    }
+
+    // ---- pass 2 ---------------------------------------------------------------
+    v4d o[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) o[t] = v4d{0.0, 0.0, 0.0, 0.0};
+    double es = 0.0;  // lane tid < kTileQ: query tid
+    double sv[4];
+    auto load_scores = [&](int c) {
+        const int k = min(min(c, nch - 1) * kChunkP + 16 * kt + lr, span - 1);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) sv[v] = scr[v][k];
+    };
+    load(vb, 0);
+    load_scores(0);
+    const int dt0 = (wave & 1) * DT;
+    for (int c = 0; c < nch; ++c) {
+        __syncthreads();  // previous chunk's values and probabilities read
+        store();          // V chunk c
+        const int k = c * kChunkP + 16 * kt + lr;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int qi = 16 * qt + 4 * v + lg;
+            pt[qi][16 * kt + lr] = k <= base + s0 + qi ? exp(sv[v] - mv[v]) : 0.0;
+        }
+        load(vb, c + 1);
+        load_scores(c + 1);
+        __syncthreads();
+        if (tid < kTileQ) {
+#pragma unroll 8
+            for (int kk = 0; kk < kChunkP; ++kk) es += pt[tid][kk];
+        }
+#pragma unroll
+        for (int m = 0; m < kChunkP / 4; ++m) {
+            const double a = pt[16 * qt + lr][4 * m + lg];
+#pragma unroll
+            for (int t = 0; t < DT; ++t) {
+                const double bv = (double)kv[4 * m + lg][16 * (dt0 + t) + lr];
+                o[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, bv, o[t], 0, 0, 0);
+            }
+        }
+    }
+    if (tid < kTileQ) ess[tid] = es;
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int qi = 16 * qt + 4 * v + lg;
+        if (qi < nq) {
+            const double e = ess[qi];
+            double* orow = out + (row0 + qi) * q_dim + (size_t)h * HD;
+#pragma unroll
+            for (int t = 0; t < DT; ++t) orow[16 * (dt0 + t) + lr] = o[t][v] / e;
+        }
+    }
+}
+
 // ---- decode path (few query rows) ----------------------------------------
 // Scratch layout per (row, head): scores[span] (probabilities after the exp
 // step), chunk maxima cmax[nchunk] (64 positions per chunk), and for the
@@ -991,9 +1170,19 @@ hipError_t launch_attention(const double* q, const float* cache_k, const float* 
     hipLaunchKernelGGL((attn_tile_kernel<HDV, F>), grid, dim3(256), 0, s, q, cache_k, cache_v, pos0, \
                        msl, span, heads, kv_heads, seq, scratch, out)
         if (hd == 128) {
-            if (strict) LAMD_TILE(128, false); else LAMD_TILE(128, true);
+            if (strict) {
+                LAMD_TILE(128, false);
+            } else {
+                hipLaunchKernelGGL(attn_tile_mfma_kernel<128>, grid, dim3(256), 0, s, q, cache_k,
+                                   cache_v, pos0, msl, span, heads, kv_heads, seq, scratch, out);
+            }
         } else {
-            if (strict) LAMD_TILE(64, false); else LAMD_TILE(64, true);
+            if (strict) {
+                LAMD_TILE(64, false);
+            } else {
+                hipLaunchKernelGGL(attn_tile_mfma_kernel<64>, grid, dim3(256), 0, s, q, cache_k,
+                                   cache_v, pos0, msl, span, heads, kv_heads, seq, scratch, out);
+            }
         }
 #undef LAMD_TILE
         return hipGetLastError();
