@@ -815,9 +815,10 @@ __global__ __launch_bounds__(256) void attn_tile_mfma_kernel(const double* __res
 }
 
 // ---- decode path (few query rows) ----------------------------------------
-// Scratch layout per (row, head): scores[span] (probabilities after the exp
-// step), chunk maxima cmax[nchunk] (64 positions per chunk), and for the
-// fast path partial sums part[nsplit][hd] plus partial expSums pes[nsplit].
+// Scratch layout per (row, head): scores[span] (strict path: probabilities
+// after the exp step), chunk maxima cmax[nchunk] (64 positions per chunk), and
+// for the fast path the chunk-local partial sums part[nchunk][hd] and partial
+// expSums pes[nchunk].
 
 struct DecodeScratch {
     double* scores;  // rows x heads x span
@@ -897,68 +898,117 @@ __device__ __forceinline__ double global_max(const double* cm, int nc, double* r
     return m;
 }
 
-// fast part 2: probabilities, partial expSum and partial PV of one
-// 64-position chunk; grid (heads, nchunk, rows), 256 threads.
-__global__ __launch_bounds__(256) void attn_pv_partial_kernel(const float* __restrict__ cache_v,
-                                                              const int* __restrict__ pos0, int msl,
-                                                              int span, int heads, int kv_heads,
-                                                              int hd, int seq, DecodeScratch sc) {
-    extern __shared__ float vs[];  // V rows of the chunk: 64 x (hd + 4) floats
+// fast decode attention, part 1: one workgroup per (head, 64-position chunk,
+// row).  Scores: four lanes per position, each a d-order chain over a quarter
+// of the head, combined as (q0 + q1) + (q2 + q3).  Then the chunk maximum m_c,
+// p = exp(score - m_c), the chunk's expSum and its sum(p * v) per column.
+// The combine kernel rescales each chunk by exp(m_c - M) (M the overall
+// maximum, the same M the reference uses) and adds the chunks in order.
+// grid (heads, nchunk, rows), 256 threads.
+__global__ __launch_bounds__(256) void attn_chunk_kernel(const double* __restrict__ q,
+                                                         const float* __restrict__ cache_k,
+                                                         const float* __restrict__ cache_v,
+                                                         const int* __restrict__ pos0, int msl,
+                                                         int span, int heads, int kv_heads, int hd,
+                                                         int seq, DecodeScratch sc) {
+    extern __shared__ float vs[];  // V rows of the chunk: 64 x (hd + 4)
+    __shared__ double qs[256];
     __shared__ double ps[64];
     __shared__ double red[256];
+    __shared__ double wmx[4];
     const int h = blockIdx.x, chunk = blockIdx.y, row = blockIdx.z;
     const int b = row / seq, s = row % seq;
     const int kvh = h / (heads / kv_heads);
-    const int kv_dim = kv_heads * hd;
+    const int q_dim = heads * hd, kv_dim = kv_heads * hd;
     const int L = min(*pos0 + s + 1, span);
     const int k0 = chunk * 64;
     if (k0 >= L) return;
     const int n = min(64, L - k0);
     const int nchunk = attn_nchunk(span);
     const size_t rh = (size_t)row * heads + h;
-    // V rows of the chunk -> LDS (all loads in flight at once)
+    const int tid = threadIdx.x;
+    // V rows of the chunk -> LDS (loads in flight during the scores)
     const float* vb = cache_v + (size_t)b * msl * kv_dim + (size_t)kvh * hd;
     const int per_row4 = hd / 4;
-    for (int i = threadIdx.x; i < n * per_row4; i += 256) {
+    for (int i = tid; i < 64 * per_row4; i += 256) {
         const int r = i / per_row4, c4 = (i % per_row4) * 4;
-        *(float4*)&vs[r * (hd + 4) + c4] = *(const float4*)(vb + (size_t)(k0 + r) * kv_dim + c4);
+        *(float4*)&vs[r * (hd + 4) + c4] = *(const float4*)(vb + (size_t)min(k0 + r, msl - 1) * kv_dim + c4);
     }
-    if (threadIdx.x < 64) {
-        const int k = k0 + threadIdx.x;
-        const double sv = threadIdx.x < n ? sc.scores[rh * span + k] : 0.0;
-        const double m = global_max(sc.cmax + rh * nchunk, (L + 63) / 64, nullptr);
-        ps[threadIdx.x] = threadIdx.x < n ? exp(sv - m) : 0.0;
-    }
+    const double* qr = q + (size_t)row * q_dim + (size_t)h * hd;
+    for (int d = tid; d < hd; d += 256) qs[d] = qr[d];
     __syncthreads();
-    // partial expSum: fixed tree over the 64 probabilities
-    if (threadIdx.x < 64) {
-        double e = ps[threadIdx.x];
+    // scores
+    const int pl = tid >> 2, part = tid & 3;  // position in the chunk, quarter of d
+    const int kp = k0 + pl;
+    const int dq = hd / 4, d0 = part * dq;
+    double dot = 0.0;
+    {
+        const float* kr = cache_k + (size_t)b * msl * kv_dim + (size_t)min(kp, msl - 1) * kv_dim +
+                          (size_t)kvh * hd + d0;
+        if ((dq & 3) == 0) {
+            for (int d = 0; d < dq; d += 4) {
+                const float4 k4 = *(const float4*)(kr + d);
+                dot = fma(qs[d0 + d], (double)k4.x, dot);
+                dot = fma(qs[d0 + d + 1], (double)k4.y, dot);
+                dot = fma(qs[d0 + d + 2], (double)k4.z, dot);
+                dot = fma(qs[d0 + d + 3], (double)k4.w, dot);
+            }
+        } else {
+            for (int d = 0; d < dq; ++d) dot = fma(qs[d0 + d], (double)kr[d], dot);
+        }
+    }
+    const double o1 = __shfl_xor(dot, 1, 64);
+    const double pair = (part & 1) ? o1 + dot : dot + o1;  // q0+q1 (lanes 0,1), q2+q3 (lanes 2,3)
+    const double o2 = __shfl_xor(pair, 2, 64);
+    const double tot = (part & 2) ? o2 + pair : pair + o2;
+    const double sc_v = tot * (1.0 / sqrt((double)hd));
+    const bool valid = pl < n;
+    // chunk maximum (-1e9 start, NaN never wins)
+    double m = valid ? (sc_v > -1e9 ? sc_v : -1e9) : -1e9;
+    for (int off = 32; off > 0; off >>= 1) {
+        const double o = __shfl_xor(m, off, 64);
+        m = o > m ? o : m;
+    }
+    if ((tid & 63) == 0) wmx[tid >> 6] = m;
+    __syncthreads();
+    double mc = wmx[0];
+    for (int w = 1; w < 4; ++w) mc = wmx[w] > mc ? wmx[w] : mc;
+    if (part == 0) ps[pl] = valid ? exp(sc_v - mc) : 0.0;
+    __syncthreads();
+    if (tid < 64) {
+        double e = ps[tid];
         for (int off = 32; off > 0; off >>= 1) e = e + __shfl_down(e, off, 64);
-        if (threadIdx.x == 0) sc.pes[rh * nchunk + chunk] = e;
+        if (tid == 0) {
+            sc.pes[rh * nchunk + chunk] = e;
+            sc.cmax[rh * nchunk + chunk] = mc;
+        }
     }
     // partial PV: (256 / hd) slices of the chunk per column, combined in order
     const int slices = 256 / hd;
-    const int d = threadIdx.x % hd, sl = threadIdx.x / hd;
+    const int d = tid % hd, sl = tid / hd;
     const int per = (n + slices - 1) / slices;
     double sum = 0.0;
     if (sl < slices) {
         const int a0 = min(n, sl * per), a1 = min(n, a0 + per);
-        for (int k = a0; k < a1; ++k) sum += ps[k] * (double)vs[k * (hd + 4) + d];
+        for (int k = a0; k < a1; ++k) sum = fma(ps[k], (double)vs[k * (hd + 4) + d], sum);
     }
-    red[threadIdx.x] = sum;
+    red[tid] = sum;
     __syncthreads();
-    if ((int)threadIdx.x < hd) {
-        double t = red[threadIdx.x];
-        for (int k = 1; k < slices; ++k) t = t + red[k * hd + threadIdx.x];
-        sc.part[(rh * nchunk + chunk) * hd + threadIdx.x] = t;
+    if (tid < hd) {
+        double t = red[tid];
+        for (int k = 1; k < slices; ++k) t = t + red[k * hd + tid];
+        sc.part[(rh * nchunk + chunk) * hd + tid] = t;
     }
 }
 
-// fast part 3: combine the chunk partials in chunk order; grid (heads, rows)
+// fast part 2: combine the chunk partials in chunk order, each rescaled by
+// exp(m_c - M); grid (heads, rows)
 __global__ __launch_bounds__(256) void attn_combine_kernel(const int* __restrict__ pos0, int span,
                                                            int heads, int hd, int seq,
                                                            DecodeScratch sc,
                                                            double* __restrict__ out) {
+    __shared__ double fac[kMaxAttnSpan / 64 + 1];
+    __shared__ double es_sh;
     const int h = blockIdx.x, row = blockIdx.y;
     const int s = row % seq;
     const int L = *pos0 + s + 1;
@@ -970,16 +1020,25 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const int* __restrict
     }
     const int nc = (L + 63) / 64, nchunk = attn_nchunk(span);
     const size_t rh = (size_t)row * heads + h;
-    // sums in chunk order; eight loads are in flight ahead of each eight adds
-    double es = 0.0;
-    for (int c0 = 0; c0 < nc; c0 += 8) {
-        double v[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = c0 + i < nc ? sc.pes[rh * nchunk + c0 + i] : 0.0;
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            if (c0 + i < nc) es += v[i];
+    if (threadIdx.x < 64) {
+        double M = -1e9;
+        for (int c = threadIdx.x; c < nc; c += 64) {
+            const double v = sc.cmax[rh * nchunk + c];
+            M = v > M ? v : M;
+        }
+        for (int off = 32; off > 0; off >>= 1) {
+            const double o = __shfl_xor(M, off, 64);
+            M = o > M ? o : M;
+        }
+        for (int c = threadIdx.x; c < nc; c += 64) fac[c] = exp(sc.cmax[rh * nchunk + c] - M);
     }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double es = 0.0;
+        for (int c = 0; c < nc; ++c) es = fma(sc.pes[rh * nchunk + c], fac[c], es);
+        es_sh = es;
+    }
+    __syncthreads();
     for (int d = threadIdx.x; d < hd; d += 256) {
         double t = 0.0;
         for (int c0 = 0; c0 < nc; c0 += 8) {
@@ -988,9 +1047,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const int* __restrict
             for (int i = 0; i < 8; ++i) v[i] = c0 + i < nc ? sc.part[(rh * nchunk + c0 + i) * hd + d] : 0.0;
 #pragma unroll
             for (int i = 0; i < 8; ++i)
-                if (c0 + i < nc) t += v[i];
+                if (c0 + i < nc) t = fma(v[i], fac[c0 + i], t);
         }
-        orow[d] = t / es;
+        orow[d] = t / es_sh;
     }
 }
 
@@ -1134,15 +1193,15 @@ hipError_t launch_attention(const double* q, const float* cache_k, const float* 
         if (!scratch) return hipErrorInvalidValue;
         const DecodeScratch sc = decode_scratch(scratch, rows, heads, hd, span);
         const int nc = attn_nchunk(span);
-        hipLaunchKernelGGL(attn_scores_kernel, dim3(heads, nc, rows), dim3(64), 0, s, q, cache_k, pos0,
-                           msl, span, heads, kv_heads, hd, seq, sc);
         if (!strict) {
-            hipLaunchKernelGGL(attn_pv_partial_kernel, dim3(heads, nc, rows), dim3(256),
-                               (size_t)64 * (hd + 4) * sizeof(float), s,
-                               cache_v, pos0, msl, span, heads, kv_heads, hd, seq, sc);
+            hipLaunchKernelGGL(attn_chunk_kernel, dim3(heads, nc, rows), dim3(256),
+                               (size_t)64 * (hd + 4) * sizeof(float), s, q, cache_k, cache_v, pos0,
+                               msl, span, heads, kv_heads, hd, seq, sc);
             hipLaunchKernelGGL(attn_combine_kernel, dim3(heads, rows), dim3(256), 0, s, pos0, span,
                                heads, hd, seq, sc, out);
         } else {
+            hipLaunchKernelGGL(attn_scores_kernel, dim3(heads, nc, rows), dim3(64), 0, s, q, cache_k,
+                               pos0, msl, span, heads, kv_heads, hd, seq, sc);
             hipLaunchKernelGGL(attn_exp_kernel, dim3(heads, nc, rows), dim3(64), 0, s, pos0, span,
                                heads, seq, sc);
             const dim3 g(heads, rows), t(256);
