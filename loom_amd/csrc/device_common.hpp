@@ -37,6 +37,16 @@ __device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// D(32x32 i32) += A(32x32 i8) * B(32x32 i8), twice the int8 rate of the
+// 16x16x64 form on gfx950.  Lane l supplies A row l&31 and B column l&31 for
+// K half l>>5 (16 bytes each; byte j of A pairs with byte j of B); D element v
+// of lane l is row 8*(v>>2) + 4*(l>>5) + (v&3), column l&31.
+__device__ __forceinline__ v16i mfma32_i8(v4i a, v4i b, v16i c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
 // bitNetQuantizedActivation (poly/bitnet_cpu.go:73-84) with Go's int(float64)
 // on amd64 (CVTTSD2SQ): NaN and out-of-range values become INT64_MIN, which
 // loom then clamps to -128.
@@ -263,28 +273,42 @@ __device__ __forceinline__ RowScale row_scale(const EpiDev& e, float am, int xs)
 }
 
 // raw0/raw1: sum(code * xq) of matrix 0/1 for token row i, output n.  Codes
-// are weight+1, so acc = raw - sum(xq).
-__device__ __forceinline__ void epilogue_store(const EpiDev& e, int i, int n, int raw0, int raw1,
-                                               const RowScale& rs) {
-    const int acc0 = raw0 - rs.xs;
+// are weight+1, so acc = raw - sum(xq).  b0/b1 are bias0[n]/bias1[n] and res
+// is residual[i*ldo+n], loaded by the caller (read only when those pointers
+// are set); callers that batch their loads ahead of their stores use this.
+// KIND >= 0 fixes e.kind at compile time (callers that dispatch on it).
+template <int KIND = -1>
+__device__ __forceinline__ void epilogue_store_pre(const EpiDev& e, int i, int n, int raw0, int raw1,
+                                                   double os0, double os1, int xs, float b0, float b1,
+                                                   float res) {
+    const int kind = KIND >= 0 ? KIND : e.kind;
+    const int acc0 = raw0 - xs;
     const size_t o = (size_t)i * e.ldo + n;
     if (e.acc0) e.acc0[(size_t)i * e.n + n] = acc0;
-    if (e.kind == EPI_ACC) return;
-    if (e.kind == EPI_SWIGLU) {
-        const int acc1 = raw1 - rs.xs;
+    if (kind == EPI_ACC) return;
+    if (kind == EPI_SWIGLU) {
+        const int acc1 = raw1 - xs;
         if (e.acc1) e.acc1[(size_t)i * e.n + n] = acc1;
         // g := gate[o] + bias; u := up[o] + bias   (poly/swiglu.go:306-309)
-        const double g = (double)acc0 * rs.os0 + (e.bias0 ? (double)e.bias0[n] : 0.0);
-        const double u = (double)acc1 * rs.os1 + (e.bias1 ? (double)e.bias1[n] : 0.0);
+        const double g = (double)acc0 * os0 + (e.bias0 ? (double)b0 : 0.0);
+        const double u = (double)acc1 * os1 + (e.bias1 ? (double)b1 : 0.0);
         e.out[o] = (float)gate_product(g, u, e.activation);
         return;
     }
-    double d = (double)acc0 * rs.os0;
-    if (e.bias0) d = d + (double)e.bias0[n];
+    double d = (double)acc0 * os0;
+    if (e.bias0) d = d + (double)b0;
     float v = (float)d;
-    if (e.residual) v = v + e.residual[o];
+    if (e.residual) v = v + res;
     e.out[o] = v;
     if (e.post) e.post[o] = activate_f32(v, e.activation);
+}
+
+__device__ __forceinline__ void epilogue_store(const EpiDev& e, int i, int n, int raw0, int raw1,
+                                               const RowScale& rs) {
+    const float b0 = e.bias0 ? e.bias0[n] : 0.0f;
+    const float b1 = e.kind == EPI_SWIGLU && e.bias1 ? e.bias1[n] : 0.0f;
+    const float res = e.kind == EPI_DENSE && e.residual ? e.residual[(size_t)i * e.ldo + n] : 0.0f;
+    epilogue_store_pre(e, i, n, raw0, raw1, rs.os0, rs.os1, rs.xs, b0, b1, res);
 }
 
 // Arguments of the matmul kernels.

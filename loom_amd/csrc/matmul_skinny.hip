@@ -459,7 +459,7 @@ const char* kernel_variant(int m) {
     if (m <= 16) return "skinny_m16";
     if (m <= 32) return "skinny_m32";
     if (m <= 64) return "skinny_m64";
-    return "gemm";  // gemm512 (256x256 tiles) when they fill the chip, else gemm128
+    return "gemm";  // gemm32_kernel: 32x32x32 MFMA, 128-token x 256-row tiles
 }
 
 static MatArgs make_args(const Matrix* w0, const Matrix* w1, int m, const Epilogue& epi) {

@@ -421,17 +421,17 @@ def test_library_errors_are_loud(orc, torch_dev, bn):
     assert _lib.lib().loom_amd_ternary_matmul(None, None, 256, None, None, 1, None, None, None) == -1
 
 
-# ---------------------------------------------------------------- 256x256-tile GEMM paths
-def test_gemm512_ragged_rows_and_tiles(orc, torch_dev, bn):
-    # M and N not multiples of the 256-row / 16-row tiles: clamped loads must
-    # only ever feed outputs that are not stored.
+# ---------------------------------------------------------------- large-M GEMM (32x32x32 MFMA) paths
+def test_gemm_ragged_rows_and_tiles(orc, torch_dev, bn):
+    # M and N not multiples of the 128-token / 32-row blocks: clamped loads
+    # must only ever feed outputs that are not stored.
     m = orc.random_matrix(6900, 2560, seed=91)
     x = orc.normal_f32(4100 * 2560, seed=92).reshape(4100, 2560)
     _check_dense(orc, torch_dev, bn, m, x)
 
 
-def test_gemm512_general_epilogue(orc, torch_dev, bn):
-    # residual + activation force the general epilogue of the large-tile kernel
+def test_gemm_general_epilogue(orc, torch_dev, bn):
+    # residual + activation force the general epilogue of the large-M kernel
     m = orc.random_matrix(4096, 512, seed=93)
     x = orc.normal_f32(4096 * 512, seed=94).reshape(4096, 512)
     res = orc.normal_f32(4096 * 4096, seed=95).reshape(4096, 4096)
@@ -440,8 +440,15 @@ def test_gemm512_general_epilogue(orc, torch_dev, bn):
 
 
 def test_swiglu_large_tiles(orc, torch_dev, bn):
-    # gate|up at M=4096 x inter=4096 runs the two-matrix large-tile kernel
+    # gate|up at M=4096 x inter=4096 runs the two-matrix large-M kernel
     _swiglu_case(orc, torch_dev, bn, hidden=640, inter=4096, M=4096, seed=97, norm="fast",
+                 with_norm_w=True)
+
+
+def test_swiglu_large_ragged(orc, torch_dev, bn):
+    # 63 weight tiles (inter 1000) against 8-tile workgroups, 300 tokens against
+    # 128-token tiles: the partial blocks of both matrices
+    _swiglu_case(orc, torch_dev, bn, hidden=768, inter=1000, M=300, seed=98, norm="strict",
                  with_norm_w=True)
 
 
