@@ -74,6 +74,12 @@ static int check_matrix(const loom_amd_matrix* w, const char* name) {
     return 0;
 }
 
+// The matmul kernels address the tile buffer with 32-bit buffer offsets.
+static bool tiles_fit(int rows, int cols) {
+    const size_t bytes = (size_t)ceil_div(rows, kTileRows) * (size_t)ceil_div(cols, kTileCols) * kTileWords * 4;
+    return bytes <= 0x7fffffffu;
+}
+
 int create_matrix(int device, const uint32_t* words, size_t n_words, int rows, int cols,
                   int row_words, float scale, loom_amd_matrix** out) {
     if (out == nullptr) return fail("out is null");
@@ -91,6 +97,7 @@ int create_matrix(int device, const uint32_t* words, size_t n_words, int rows, i
         return fail("device " + std::to_string(device) + " is not visible");
     }
     if (!is_gfx950(device)) return fail("device is not gfx950");
+    if (!tiles_fit(rows, cols)) return fail("matrix tiles exceed 2 GiB (the kernels use 32-bit buffer offsets)");
     DeviceGuard guard(device);
     auto* w = new loom_amd_matrix();
     Matrix& m = w->m;
@@ -128,6 +135,7 @@ int create_matrix_ms_offline(int device, const uint8_t* packed, int rows, int co
         return fail("device " + std::to_string(device) + " is not visible");
     }
     if (!is_gfx950(device)) return fail("device is not gfx950");
+    if (!tiles_fit(rows, cols)) return fail("matrix tiles exceed 2 GiB (the kernels use 32-bit buffer offsets)");
     DeviceGuard guard(device);
     auto* w = new loom_amd_matrix();
     Matrix& m = w->m;

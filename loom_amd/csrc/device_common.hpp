@@ -39,6 +39,20 @@ __device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
 
 typedef int v16i __attribute__((ext_vector_type(16)));
 
+// dword 3 of a raw (untyped, unswizzled) gfx9 buffer resource
+constexpr int kBufferWord3 = 0x00020000;
+
+// Raw buffer resource over `bytes` bytes: loads at offsets past the end return
+// zero without touching memory, which lets a kernel issue a fixed number of
+// loads (so the wait counters see a fixed pattern) without branches.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, (int)bytes, kBufferWord3);
+}
+
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
 // D(32x32 i32) += A(32x32 i8) * B(32x32 i8), twice the int8 rate of the
 // 16x16x64 form on gfx950.  Lane l supplies A row l&31 and B column l&31 for
 // K half l>>5 (16 bytes each; byte j of A pairs with byte j of B); D element v

@@ -4,8 +4,6 @@
 namespace lamd {
 
 constexpr int kXcds = 8;
-// dword 3 of a raw (untyped, unswizzled) gfx9 buffer resource
-constexpr int kBufferWord3 = 0x00020000;
 
 // ------------------------------------------------------------------------
 // gemm32: v_mfma_i32_32x32x32_i8, which issues int8 at twice the rate of the

@@ -19,8 +19,10 @@ hipError_t launch_gemm(const MatArgs& p, bool two, hipStream_t s);
 constexpr int kFusedMaxRows = 4;
 constexpr int kFusedVec = 16;  // float4 per thread in the fused prologue (max)
 
-// Row of element group idx (4 elements) among M <= 4 rows of row4 groups.
+// Row of element group idx (4 elements) among M <= MR rows of row4 groups.
+template <int MR>
 __device__ __forceinline__ int row_of(int idx, int row4) {
+    if (MR == 1) return 0;
     return (idx >= row4) + (idx >= 2 * row4) + (idx >= 3 * row4);
 }
 
@@ -36,7 +38,7 @@ __device__ __forceinline__ double wave_sum_f64_lane0(double v) {
 // the squares of the (single) row in element order on one lane, from LDS.
 // FV: element groups (4 values) per thread.
 template <int NMAT, int MSUB, int WAVES, bool FUSEQ, int NORM = NORM_NONE, int STRICT = 0,
-          int FV = kFusedVec>
+          int FV = kFusedVec, int MR = kFusedMaxRows>
 __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
     constexpr int T = WAVES * 64;
     constexpr int U = 4 / MSUB;  // K tiles per batch per wave
@@ -66,37 +68,50 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
     float4 xv[FUSEQ && !F64 ? FV : 1];
     double xd[F64 ? FV : 1][4];
     float4 gv[NORM != NORM_NONE ? FV : 1];
+    // Every slot issues its load; slots past the data read past the end of a
+    // buffer resource (zero, no memory traffic).  With no branches around the
+    // loads the wait for the rows counts only the weight loads issued after
+    // them, which stay in flight through the prologue.
     if (FUSEQ) {
-        const float4* x4 = (const float4*)p.x;
-        const double2* x2 = (const double2*)p.x64;
-        const float4* w4 = (const float4*)p.nw;
+        const uint32_t xb = (uint32_t)n4 * (F64 ? 32u : 16u);
+        const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(F64 ? (const void*)p.x64 : (const void*)p.x, xb);
+        const __amdgpu_buffer_rsrc_t gr = buffer_rsrc(p.nw, p.nw ? (uint32_t)row4 * 16u : 0u);
 #pragma unroll
         for (int j = 0; j < FV; ++j) {
             const int idx = tid + j * T;
-            if (idx < n4) {
-                if (F64) {
-                    const double2 a = x2[2 * idx], b = x2[2 * idx + 1];
-                    xd[j][0] = a.x;
-                    xd[j][1] = a.y;
-                    xd[j][2] = b.x;
-                    xd[j][3] = b.y;
-                } else {
-                    xv[j] = x4[idx];
-                }
-                if (NORM != NORM_NONE) {
-                    const int c4 = idx - row_of(idx, row4) * row4;
-                    gv[j] = w4 ? w4[c4] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
-                }
+            const bool ok = idx < n4;
+            if (F64) {
+                const uint32_t o = ok ? (uint32_t)idx * 32u : xb;
+                const double2 a = __builtin_bit_cast(double2, buffer_load16(xr, o));
+                const double2 b = __builtin_bit_cast(double2, buffer_load16(xr, ok ? o + 16u : xb));
+                xd[j][0] = a.x;
+                xd[j][1] = a.y;
+                xd[j][2] = b.x;
+                xd[j][3] = b.y;
+            } else {
+                xv[j] = __builtin_bit_cast(float4, buffer_load16(xr, ok ? (uint32_t)idx * 16u : xb));
+            }
+            if (NORM != NORM_NONE) {
+                const int c4 = idx - row_of<MR>(idx, row4) * row4;
+                gv[j] = p.nw ? __builtin_bit_cast(float4, buffer_load16(gr, ok ? (uint32_t)c4 * 16u : (uint32_t)row4 * 16u))
+                             : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
             }
         }
     }
 
     // weights of the first batch
+    const uint32_t wbytes = (uint32_t)p.ntiles * (uint32_t)ktiles * 1024u;
+    const __amdgpu_buffer_rsrc_t wr0 = buffer_rsrc(p.w0, wbytes);
+    const __amdgpu_buffer_rsrc_t wr1 = buffer_rsrc(p.w1, wbytes);
     uint4 wv[NMAT][U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int kt = wave + u * WAVES;
-        if (kt < ktiles) {
+        if (FUSEQ) {  // (without a prologue to overlap, skipping the unused loads is cheaper)
+            const uint32_t o = kt < ktiles ? (uint32_t)(tile0 + (size_t)kt * 64) * 16u : wbytes;
+            wv[0][u] = buffer_load16(wr0, o);
+            if (NMAT == 2) wv[NMAT - 1][u] = buffer_load16(wr1, o);
+        } else if (kt < ktiles) {
             wv[0][u] = p.w0[tile0 + (size_t)kt * 64];
             if (NMAT == 2) wv[NMAT - 1][u] = p.w1[tile0 + (size_t)kt * 64];
         }
@@ -106,7 +121,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
     if (FUSEQ) {
         if (NORM != NORM_NONE) {
             // ---- sum of squares per row -----------------------------------
-            double tot[kFusedMaxRows];
+            double tot[MR];
             if (STRICT) {
                 // one row: squares to LDS, one lane adds them in element order
                 double* sq = (double*)xq_s;
@@ -131,14 +146,16 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
                 __syncthreads();
                 tot[0] = nsum[0][0];
 #pragma unroll
-                for (int rr = 1; rr < kFusedMaxRows; ++rr) tot[rr] = 0.0;
+                for (int rr = 1; rr < MR; ++rr) tot[rr] = 0.0;
             } else {
-                double ps[kFusedMaxRows] = {0.0, 0.0, 0.0, 0.0};
+                double ps[MR];
+#pragma unroll
+                for (int rr = 0; rr < MR; ++rr) ps[rr] = 0.0;
 #pragma unroll
                 for (int j = 0; j < FV; ++j) {
                     const int idx = tid + j * T;
                     if (idx < n4) {
-                        const int row = row_of(idx, row4);
+                        const int row = row_of<MR>(idx, row4);
                         double q = 0.0;
                         if (F64) {
 #pragma unroll
@@ -151,12 +168,12 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
                             q = q + d * d;
                         }
 #pragma unroll
-                        for (int rr = 0; rr < kFusedMaxRows; ++rr)
+                        for (int rr = 0; rr < MR; ++rr)
                             if (rr == row) ps[rr] = ps[rr] + q;
                     }
                 }
 #pragma unroll
-                for (int rr = 0; rr < kFusedMaxRows; ++rr) {
+                for (int rr = 0; rr < MR; ++rr) {
                     if (rr < M) {
                         const double w = wave_sum_f64_dpp(ps[rr]);
                         if (lane == 0) nsum[wave][rr] = w;
@@ -164,7 +181,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
                 }
                 __syncthreads();
 #pragma unroll
-                for (int rr = 0; rr < kFusedMaxRows; ++rr) {
+                for (int rr = 0; rr < MR; ++rr) {
                     double t = 0.0;
                     if (rr < M) {
                         t = nsum[0][rr];
@@ -174,9 +191,9 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
                 }
             }
             // ---- normalize in registers ------------------------------------
-            double f[kFusedMaxRows];
+            double f[MR];
 #pragma unroll
-            for (int rr = 0; rr < kFusedMaxRows; ++rr) {
+            for (int rr = 0; rr < MR; ++rr) {
                 const double ms = tot[rr] / (double)k + p.neps;
                 f[rr] = NORM == NORM_RMS ? sqrt(ms) : 1.0 / sqrt(ms);  // rms, or scale
             }
@@ -184,10 +201,10 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
             for (int j = 0; j < FV; ++j) {
                 const int idx = tid + j * T;
                 if (idx < n4) {
-                    const int row = row_of(idx, row4);
+                    const int row = row_of<MR>(idx, row4);
                     double fr = f[0];
 #pragma unroll
-                    for (int rr = 1; rr < kFusedMaxRows; ++rr)
+                    for (int rr = 1; rr < MR; ++rr)
                         if (rr == row) fr = f[rr];
                     const double g0 = gv[j].x, g1 = gv[j].y, g2 = gv[j].z, g3 = gv[j].w;
                     if (NORM == NORM_RMS) {
@@ -208,10 +225,12 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
                     }
                 }
             }
+            __syncthreads();
         }
-        __syncthreads();
         // bitNetActivationMaxAbs per row (poly/bitnet_cpu.go:45-71).
-        float lm[kFusedMaxRows] = {0.0f, 0.0f, 0.0f, 0.0f};
+        float lm[MR];
+#pragma unroll
+        for (int rr = 0; rr < MR; ++rr) lm[rr] = 0.0f;
 #pragma unroll
         for (int j = 0; j < FV; ++j) {
             const int idx = tid + j * T;
@@ -228,14 +247,14 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
                     a = max_nan_skip(a, fabsf(xv[j].z));
                     a = max_nan_skip(a, fabsf(xv[j].w));
                 }
-                const int row = row_of(idx, row4);
+                const int row = row_of<MR>(idx, row4);
 #pragma unroll
-                for (int rr = 0; rr < kFusedMaxRows; ++rr)
+                for (int rr = 0; rr < MR; ++rr)
                     if (rr == row) lm[rr] = max_nan_skip(lm[rr], a);
             }
         }
 #pragma unroll
-        for (int rr = 0; rr < kFusedMaxRows; ++rr) {
+        for (int rr = 0; rr < MR; ++rr) {
             if (rr < M) {
                 const float wm = wave_max_dpp(lm[rr]);
                 if (lane == 0) wmax[wave][rr] = wm;
@@ -243,9 +262,9 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
         }
         __syncthreads();
         // bitNetQuantizedActivation (poly/bitnet_cpu.go:73-95) into LDS.
-        double sc[kFusedMaxRows];
+        double sc[MR];
 #pragma unroll
-        for (int rr = 0; rr < kFusedMaxRows; ++rr) {
+        for (int rr = 0; rr < MR; ++rr) {
             float am = 0.0f;
             if (rr < M) {
                 for (int w = 0; w < WAVES; ++w) am = max_nan_skip(am, wmax[w][rr]);
@@ -254,15 +273,17 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
             if (am < 1e-5f) am = 1e-5f;
             sc[rr] = rr < M ? 127.0 / (double)am : 0.0;
         }
-        int ls[kFusedMaxRows] = {0, 0, 0, 0};
+        int ls[MR];
+#pragma unroll
+        for (int rr = 0; rr < MR; ++rr) ls[rr] = 0;
 #pragma unroll
         for (int j = 0; j < FV; ++j) {
             const int idx = tid + j * T;
             if (idx < n4) {
-                const int row = row_of(idx, row4);
+                const int row = row_of<MR>(idx, row4);
                 double s = sc[0];
 #pragma unroll
-                for (int rr = 1; rr < kFusedMaxRows; ++rr)
+                for (int rr = 1; rr < MR; ++rr)
                     if (rr == row) s = sc[rr];
                 int q0, q1, q2, q3;
                 if (F64) {
@@ -278,7 +299,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
                 }
                 *(uint32_t*)(xq_s + row * p.ldq + 4 * (idx - row * row4)) = pack4(q0, q1, q2, q3);
 #pragma unroll
-                for (int rr = 0; rr < kFusedMaxRows; ++rr)
+                for (int rr = 0; rr < MR; ++rr)
                     if (rr == row) ls[rr] += q0 + q1 + q2 + q3;
             }
         }
@@ -289,7 +310,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
             *(uint32_t*)(xq_s + row * p.ldq + k + 4 * (i - row * pad4)) = 0u;
         }
 #pragma unroll
-        for (int rr = 0; rr < kFusedMaxRows; ++rr) {
+        for (int rr = 0; rr < MR; ++rr) {
             if (rr < M) {
                 const int v = wave_sum_i_dpp(ls[rr]);
                 if (lane == 0) wsum[wave][rr] = v;
@@ -421,6 +442,21 @@ static int pick_waves(int ntiles, int ktiles, int cap) {
     return w;
 }
 
+// Fused-quantization launch: the fewest float4 slots per thread that hold the
+// rows (clamped loads fill the rest), and the one-row prologue for M = 1.
+template <int NMAT, int WAVES>
+static void launch_fused_w(const MatArgs& p, size_t shm, hipStream_t s) {
+    const size_t groups = (size_t)p.e.m * (p.k / 4);
+    const dim3 grid(p.ntiles), block(WAVES * 64);
+    if (p.e.m == 1 && groups <= (size_t)2 * WAVES * 64) {
+        hipLaunchKernelGGL((skinny_kernel<NMAT, 1, WAVES, true, NORM_NONE, 0, 2, 1>), grid, block, shm, s, p);
+    } else if (p.e.m == 1 && groups <= (size_t)4 * WAVES * 64) {
+        hipLaunchKernelGGL((skinny_kernel<NMAT, 1, WAVES, true, NORM_NONE, 0, 4, 1>), grid, block, shm, s, p);
+    } else {
+        hipLaunchKernelGGL((skinny_kernel<NMAT, 1, WAVES, true>), grid, block, shm, s, p);
+    }
+}
+
 template <int NMAT, int MSUB, bool FUSEQ>
 static hipError_t launch_skinny(const MatArgs& p, hipStream_t s) {
     // 1024-thread workgroups leave 128 VGPRs per lane: only the one-matrix kernels fit.
@@ -432,6 +468,19 @@ static hipError_t launch_skinny(const MatArgs& p, hipStream_t s) {
     }
     const size_t shm = FUSEQ ? (size_t)p.e.m * p.ldq : 0;
     const dim3 grid(p.ntiles);
+    if constexpr (FUSEQ) {
+        static_assert(MSUB == 1, "the fused prologue serves up to 4 rows");
+        switch (w) {
+            case 1: launch_fused_w<NMAT, 1>(p, shm, s); break;
+            case 2: launch_fused_w<NMAT, 2>(p, shm, s); break;
+            case 4: launch_fused_w<NMAT, 4>(p, shm, s); break;
+            case 8: launch_fused_w<NMAT, 8>(p, shm, s); break;
+            default:
+                if constexpr (kCap == 16) launch_fused_w<NMAT, 16>(p, shm, s);
+                break;
+        }
+        return hipGetLastError();
+    }
     switch (w) {
         case 1:
             hipLaunchKernelGGL((skinny_kernel<NMAT, MSUB, 1, FUSEQ>), grid, dim3(64), shm, s, p);
@@ -530,8 +579,13 @@ bool norm_fused_ok(int m, int k, int strict, bool x16) {
 
 template <int NMAT, int NORM, int STRICT, int WAVES, int FV>
 static hipError_t launch_norm_t(const MatArgs& p, size_t shm, hipStream_t s) {
-    hipLaunchKernelGGL((skinny_kernel<NMAT, 1, WAVES, true, NORM, STRICT, FV>), dim3(p.ntiles),
-                       dim3(WAVES * 64), shm, s, p);
+    if (p.e.m == 1) {  // one-row prologue (decode)
+        hipLaunchKernelGGL((skinny_kernel<NMAT, 1, WAVES, true, NORM, STRICT, FV, 1>), dim3(p.ntiles),
+                           dim3(WAVES * 64), shm, s, p);
+    } else {
+        hipLaunchKernelGGL((skinny_kernel<NMAT, 1, WAVES, true, NORM, STRICT, FV>), dim3(p.ntiles),
+                           dim3(WAVES * 64), shm, s, p);
+    }
     return hipGetLastError();
 }
 
