@@ -421,6 +421,26 @@ def test_library_errors_are_loud(orc, torch_dev, bn):
     assert _lib.lib().loom_amd_ternary_matmul(None, None, 256, None, None, 1, None, None, None) == -1
 
 
+def test_fused_quant_near_ties(orc, torch_dev, bn):
+    # The fused quantizer rounds in fp32 away from ties and defers to the fp64
+    # product within 1e-3 of one: rows built on and around exact ties (and
+    # across the 1e-3 band) must quantize exactly like loom's fp64 path.
+    rng = np.random.default_rng(7)
+    K = 4096
+    m = orc.random_matrix(32, K, seed=71)
+    for amax in (127.0, 63.5, 3.0, 1.0, 300.0, 0.001):
+        scale = 127.0 / float(np.float32(amax))
+        rows = []
+        for _ in range(4):
+            k = rng.integers(-127, 127, K).astype(np.float64)
+            eps = rng.choice([0.0, 1e-7, -1e-7, 3e-4, -3e-4, 9.9e-4, -9.9e-4, 1.1e-3, -1.1e-3,
+                              0.2, -0.3], K)
+            row = ((k + 0.5 + eps) / scale).astype(np.float32)
+            row[rng.integers(0, K)] = np.float32(amax) * rng.choice([1.0, -1.0])
+            rows.append(row)
+        _check_dense(orc, torch_dev, bn, m, np.stack(rows))
+
+
 # ---------------------------------------------------------------- large-M GEMM (32x32x32 MFMA) paths
 def test_gemm_ragged_rows_and_tiles(orc, torch_dev, bn):
     # M and N not multiples of the 128-token / 32-row blocks: clamped loads
