@@ -898,6 +898,187 @@ __device__ __forceinline__ double global_max(const double* cm, int nc, double* r
     return m;
 }
 
+// ---- fast decode attention for head_dim 64 / 128 ------------------------------
+// Part 1: one workgroup per (KV head, 32-position chunk, row) serves every
+// query head of the KV head's group (GQA), so each K/V row is read once.  Wave
+// w takes group member w (w+4, ...).  Scores: two lanes per position, four
+// interleaved chains over half the head each, (c0+c1)+(c2+c3), lo + hi.  Then
+// the chunk maximum m_c, p = exp(s - m_c), the chunk's expSum and sum(p * v)
+// (even and odd positions in two chains).
+constexpr int kGqaChunk = 32;
+__host__ __device__ inline int attn_nchunk32(int span) { return (span + kGqaChunk - 1) / kGqaChunk; }
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict__ q,
+                                                       const float* __restrict__ cache_k,
+                                                       const float* __restrict__ cache_v,
+                                                       const int* __restrict__ pos0, int msl,
+                                                       int span, int heads, int kv_heads, int seq,
+                                                       DecodeScratch sc) {
+    constexpr int CH = kGqaChunk;
+    constexpr int DH = HD / 2;   // score dims per lane
+    constexpr int DP = HD / 64;  // output dims per lane
+    constexpr int KP = HD + 4;   // padded LDS row (floats)
+    constexpr int PR4 = HD / 4;
+    __shared__ __align__(16) float ks[CH * KP];
+    __shared__ __align__(16) float vs[CH * KP];
+    __shared__ double qs[4][HD];
+    __shared__ double ps[4][CH];
+    const int kvh = blockIdx.x, chunk = blockIdx.y, row = blockIdx.z;
+    const int G = heads / kv_heads;
+    const int b = row / seq, s = row % seq;
+    const int L = min(*pos0 + s + 1, span);
+    const int k0 = chunk * CH;
+    if (k0 >= L) return;  // uniform
+    const int n = min(CH, L - k0);
+    const int nchunk = attn_nchunk32(span);
+    const int q_dim = heads * HD, kv_dim = kv_heads * HD;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // K and V rows of the chunk -> LDS (V rows past the length as zeros: their
+    // cache slots may hold anything, and 0 * NaN would poison the sums)
+    const size_t cb = (size_t)b * msl * kv_dim + (size_t)kvh * HD;
+#pragma unroll
+    for (int i = tid; i < CH * PR4; i += 256) {
+        const int r = i / PR4, c4 = (i % PR4) * 4;
+        const size_t o = cb + (size_t)min(k0 + r, msl - 1) * kv_dim + c4;
+        const float4 kv = *(const float4*)(cache_k + o);
+        float4 vv = *(const float4*)(cache_v + o);
+        if (r >= n) vv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        *(float4*)&ks[r * KP + c4] = kv;
+        *(float4*)&vs[r * KP + c4] = vv;
+    }
+    const int pl = lane >> 1, half = lane & 1;
+    const double inv_sqrt = 1.0 / sqrt((double)HD);
+    for (int g0 = 0; g0 < G; g0 += 4) {
+        const int g = g0 + wave;
+        const bool act = g < G;
+        const int h = kvh * G + g;
+        const size_t rh = (size_t)row * heads + h;
+        if (act)
+            for (int d = lane; d < HD; d += 64) qs[wave][d] = q[(size_t)row * q_dim + (size_t)h * HD + d];
+        __syncthreads();
+        double mc = -1e9, es = 0.0;
+        if (act) {
+            const float* kr = &ks[pl * KP + half * DH];
+            const double* qq = &qs[wave][half * DH];
+            double c0 = 0.0, c1 = 0.0, c2 = 0.0, c3 = 0.0;
+#pragma unroll 4
+            for (int d = 0; d < DH; d += 4) {
+                const float4 k4 = *(const float4*)(kr + d);
+                c0 = fma(qq[d], (double)k4.x, c0);
+                c1 = fma(qq[d + 1], (double)k4.y, c1);
+                c2 = fma(qq[d + 2], (double)k4.z, c2);
+                c3 = fma(qq[d + 3], (double)k4.w, c3);
+            }
+            const double part = (c0 + c1) + (c2 + c3);
+            const double oth = __shfl_xor(part, 1, 64);
+            const double dot = half ? oth + part : part + oth;
+            const double scv = dot * inv_sqrt;
+            const bool valid = pl < n;
+            double m = valid ? (scv > -1e9 ? scv : -1e9) : -1e9;  // NaN never wins
+            for (int off = 32; off > 0; off >>= 1) {
+                const double t = __shfl_xor(m, off, 64);
+                m = t > m ? t : m;
+            }
+            mc = m;
+            const double pr = valid ? exp(scv - mc) : 0.0;
+            if (half == 0) ps[wave][pl] = pr;
+            double e = half == 0 ? pr : 0.0;
+            for (int off = 32; off > 0; off >>= 1) e = e + __shfl_down(e, off, 64);
+            es = __shfl(e, 0, 64);
+        }
+        __syncthreads();
+        if (act) {
+            double a0[DP], a1[DP];
+#pragma unroll
+            for (int i = 0; i < DP; ++i) a0[i] = a1[i] = 0.0;
+#pragma unroll 4
+            for (int pp = 0; pp < CH; pp += 2) {
+                const double p0 = ps[wave][pp], p1 = ps[wave][pp + 1];
+#pragma unroll
+                for (int i = 0; i < DP; ++i) {
+                    a0[i] = fma(p0, (double)vs[pp * KP + lane * DP + i], a0[i]);
+                    a1[i] = fma(p1, (double)vs[(pp + 1) * KP + lane * DP + i], a1[i]);
+                }
+            }
+            double* dst = sc.part + (rh * nchunk + chunk) * HD + lane * DP;
+#pragma unroll
+            for (int i = 0; i < DP; ++i) dst[i] = a0[i] + a1[i];
+            if (lane == 0) {
+                sc.cmax[rh * nchunk + chunk] = mc;
+                sc.pes[rh * nchunk + chunk] = es;
+            }
+        }
+        __syncthreads();  // qs / ps are rewritten by the next group member
+    }
+}
+
+// Part 2: grid (heads, HD/32, rows), 256 threads: 8 threads per output dim,
+// thread j of a dim adds the chunks c = j (mod 8) rescaled by exp(m_c - M)
+// (M the overall maximum, the reference's M), then the 8 partial sums combine
+// as ((t0+t1)+(t2+t3))+((t4+t5)+(t6+t7)); expSum the same way over pes.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_combine32_kernel(const int* __restrict__ pos0, int span,
+                                                             int heads, int seq, DecodeScratch sc,
+                                                             double* __restrict__ out) {
+    constexpr int kMaxChunks = (kMaxAttnSpan + kGqaChunk - 1) / kGqaChunk;
+    __shared__ double facs[kMaxChunks];
+    __shared__ double wm[4];
+    const int h = blockIdx.x, dg = blockIdx.y, row = blockIdx.z;
+    const int s = row % seq;
+    const int Lt = *pos0 + s + 1;
+    const int L = min(Lt, span);
+    const int nca = (L + kGqaChunk - 1) / kGqaChunk;
+    const int nchunk = attn_nchunk32(span);
+    const size_t rh = (size_t)row * heads + h;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    double M = -1e9;
+    for (int c = tid; c < nca; c += 256) {
+        const double v = sc.cmax[rh * nchunk + c];
+        M = v > M ? v : M;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const double t = __shfl_xor(M, off, 64);
+        M = t > M ? t : M;
+    }
+    if (lane == 0) wm[wave] = M;
+    __syncthreads();
+    M = wm[0];
+    for (int w = 1; w < 4; ++w) M = wm[w] > M ? wm[w] : M;
+    for (int c = tid; c < nca; c += 256) facs[c] = exp(sc.cmax[rh * nchunk + c] - M);
+    __syncthreads();
+    const int j = tid & 7, d = dg * 32 + (tid >> 3);
+    const double* pb = sc.part + rh * nchunk * HD + d;
+    double t = 0.0, e = 0.0;
+    for (int c0 = 0; c0 < nca; c0 += 64) {
+        double v[8], pe[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int c = c0 + 8 * u + j;
+            v[u] = c < nca ? pb[(size_t)c * HD] : 0.0;
+            pe[u] = c < nca ? sc.pes[rh * nchunk + c] : 0.0;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int c = c0 + 8 * u + j;
+            if (c < nca) {
+                t = fma(v[u], facs[c], t);
+                e = fma(pe[u], facs[c], e);
+            }
+        }
+    }
+    // fixed tree over the 8 threads of the dim (consecutive lanes)
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) {
+        t = t + __shfl_down(t, off, 64);
+        e = e + __shfl_down(e, off, 64);
+    }
+    if (j == 0) {
+        double* orow = out + (size_t)row * heads * HD + (size_t)h * HD;
+        orow[d] = Lt > span ? __builtin_nan("") : t / e;
+    }
+}
+
 // fast decode attention, part 1: one workgroup per (head, 64-position chunk,
 // row).  Scores: four lanes per position, each a d-order chain over a quarter
 // of the head, combined as (q0 + q1) + (q2 + q3).  Then the chunk maximum m_c,
@@ -1164,14 +1345,15 @@ size_t attention_lds_bytes(int hd, int span) {
 size_t attention_scratch_bytes(int rows, int heads, int hd, int span) {
     // prefill tiles: every score of every row (rows x heads x span fp64)
     if (rows > kSplitMaxRows) return (hd == 64 || hd == 128) ? (size_t)rows * heads * span * 8 : 0;
+    // (room for 32-position chunks; the 64-position kernels use a prefix of each region)
     const size_t rh = (size_t)rows * heads;
-    const size_t nc = attn_nchunk(span);
+    const size_t nc = attn_nchunk32(span);
     return rh * ((size_t)span + nc + nc * hd + nc) * sizeof(double);
 }
 
 static DecodeScratch decode_scratch(double* base, int rows, int heads, int hd, int span) {
     const size_t rh = (size_t)rows * heads;
-    const size_t nc = attn_nchunk(span);
+    const size_t nc = attn_nchunk32(span);
     DecodeScratch sc;
     sc.scores = base;
     sc.cmax = sc.scores + rh * span;
@@ -1193,7 +1375,20 @@ hipError_t launch_attention(const double* q, const float* cache_k, const float* 
         if (!scratch) return hipErrorInvalidValue;
         const DecodeScratch sc = decode_scratch(scratch, rows, heads, hd, span);
         const int nc = attn_nchunk(span);
-        if (!strict) {
+        if (!strict && (hd == 64 || hd == 128)) {
+            const dim3 g(kv_heads, attn_nchunk32(span), rows), gc(heads, hd / 32, rows);
+            if (hd == 128) {
+                hipLaunchKernelGGL(attn_gqa_kernel<128>, g, dim3(256), 0, s, q, cache_k, cache_v, pos0,
+                                   msl, span, heads, kv_heads, seq, sc);
+                hipLaunchKernelGGL(attn_combine32_kernel<128>, gc, dim3(256), 0, s, pos0, span, heads,
+                                   seq, sc, out);
+            } else {
+                hipLaunchKernelGGL(attn_gqa_kernel<64>, g, dim3(256), 0, s, q, cache_k, cache_v, pos0,
+                                   msl, span, heads, kv_heads, seq, sc);
+                hipLaunchKernelGGL(attn_combine32_kernel<64>, gc, dim3(256), 0, s, pos0, span, heads,
+                                   seq, sc, out);
+            }
+        } else if (!strict) {
             hipLaunchKernelGGL(attn_chunk_kernel, dim3(heads, nc, rows), dim3(256),
                                (size_t)64 * (hd + 4) * sizeof(float), s, q, cache_k, cache_v, pos0,
                                msl, span, heads, kv_heads, hd, seq, sc);

@@ -96,6 +96,11 @@ static size_t workspace_layout(const BlockDev& B, int rows, Workspace* W, char* 
     return L.off;
 }
 
+static void free_workspace(Workspace* W) {
+    if (W->base) (void)hipFree(W->base);
+    *W = Workspace{};
+}
+
 static int alloc_workspace(const BlockDev& B, int rows, Workspace* W) {
     const size_t bytes = workspace_layout(B, rows, nullptr, nullptr);
     void* p = nullptr;
@@ -103,11 +108,6 @@ static int alloc_workspace(const BlockDev& B, int rows, Workspace* W) {
     if (e != hipSuccess) return fail_hip("block workspace", e);
     workspace_layout(B, rows, W, (char*)p);
     return 0;
-}
-
-static void free_workspace(Workspace* W) {
-    if (W->base) (void)hipFree(W->base);
-    *W = Workspace{};
 }
 
 static void free_block(BlockDev* B) {
