@@ -176,6 +176,30 @@ __device__ __forceinline__ void rope_angle(int pos, int d, int hd, double theta,
     *sn = sin(angle);
 }
 
+// The three per-element steps, shared with the fused decode attention kernel.
+__device__ __forceinline__ void q_pair(const int32_t* ar, double os, const float* bq, int j0, int j1,
+                                       double c, double sn, double* o0, double* o1) {
+    const double v0 = (double)ar[j0] * os + (bq ? (double)bq[j0] : 0.0);
+    const double v1 = (double)ar[j1] * os + (bq ? (double)bq[j1] : 0.0);
+    *o0 = v0 * c - v1 * sn;
+    *o1 = v0 * sn + v1 * c;
+}
+
+// ar points at the K part of the row's accumulators; j0/j1 index into K
+__device__ __forceinline__ void k_pair(const int32_t* ar, double os, const float* bk, int j0, int j1,
+                                       double c, double sn, float* o0, float* o1) {
+    const float k0 = (float)((double)ar[j0] * os + (bk ? (double)bk[j0] : 0.0));
+    const float k1 = (float)((double)ar[j1] * os + (bk ? (double)bk[j1] : 0.0));
+    const double v0 = (double)k0, v1 = (double)k1;
+    *o0 = (float)(v0 * c - v1 * sn);
+    *o1 = (float)(v0 * sn + v1 * c);
+}
+
+// ar points at the V part of the row's accumulators
+__device__ __forceinline__ float v_val(const int32_t* ar, double os, const float* bv, int j) {
+    return (float)((double)ar[j] * os + (bv ? (double)bv[j] : 0.0));
+}
+
 __global__ void qkv_rope_kernel(const int32_t* __restrict__ acc, const float* __restrict__ amax,
                                 float sq, float sk, float sv, const float* __restrict__ bq,
                                 const float* __restrict__ bk, const float* __restrict__ bv,
@@ -202,35 +226,24 @@ __global__ void qkv_rope_kernel(const int32_t* __restrict__ acc, const float* __
     if (r < qp) {
         const int h = r / half, d = r % half;
         const int j0 = h * hd + d, j1 = j0 + half;
-        const double os = output_scale(sq, am);
-        const double v0 = (double)ar[j0] * os + (bq ? (double)bq[j0] : 0.0);
-        const double v1 = (double)ar[j1] * os + (bq ? (double)bq[j1] : 0.0);
         double c, sn;
         rope_angle(pos, d, hd, theta, &c, &sn);
         double* qr = q + (size_t)row * q_dim;
-        qr[j0] = v0 * c - v1 * sn;
-        qr[j1] = v0 * sn + v1 * c;
+        q_pair(ar, output_scale(sq, am), bq, j0, j1, c, sn, &qr[j0], &qr[j1]);
     } else if (r < qp + kp) {
         const int t = r - qp;
         const int h = t / half, d = t % half;
         const int j0 = h * hd + d, j1 = j0 + half;
-        const double os = output_scale(sk, am);
-        const float k0 = (float)((double)ar[q_dim + j0] * os + (bk ? (double)bk[j0] : 0.0));
-        const float k1 = (float)((double)ar[q_dim + j1] * os + (bk ? (double)bk[j1] : 0.0));
         double c, sn;
         rope_angle(pos, d, hd, theta, &c, &sn);
-        const double v0 = (double)k0, v1 = (double)k1;
         if (latest) {
             float* kr = cache_k + (size_t)(pos % msl) * kv_dim;
-            kr[j0] = (float)(v0 * c - v1 * sn);
-            kr[j1] = (float)(v0 * sn + v1 * c);
+            k_pair(ar + q_dim, output_scale(sk, am), bk, j0, j1, c, sn, &kr[j0], &kr[j1]);
         }
     } else {
         const int j = r - qp - kp;
-        const double os = output_scale(sv, am);
         if (latest) {
-            cache_v[(size_t)(pos % msl) * kv_dim + j] =
-                (float)((double)ar[q_dim + kv_dim + j] * os + (bv ? (double)bv[j] : 0.0));
+            cache_v[(size_t)(pos % msl) * kv_dim + j] = v_val(ar + q_dim + kv_dim, output_scale(sv, am), bv, j);
         }
     }
 }
@@ -905,16 +918,29 @@ __device__ __forceinline__ double global_max(const double* cm, int nc, double* r
 // interleaved chains over half the head each, (c0+c1)+(c2+c3), lo + hi.  Then
 // the chunk maximum m_c, p = exp(s - m_c), the chunk's expSum and sum(p * v)
 // (even and odd positions in two chains).
+// ROPE (one token per sequence, seq == 1): the Q/K/V epilogue of the stacked
+// projection runs here instead of in qkv_rope_kernel, with the same steps
+// (q_pair / k_pair / v_val): each workgroup rotates the Q of its heads, and the
+// workgroup whose chunk holds the new position writes that position's K and V
+// to the cache (and uses them from LDS).  No other workgroup reads that row.
 constexpr int kGqaChunk = 32;
 __host__ __device__ inline int attn_nchunk32(int span) { return (span + kGqaChunk - 1) / kGqaChunk; }
 
-template <int HD>
-__global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict__ q,
-                                                       const float* __restrict__ cache_k,
-                                                       const float* __restrict__ cache_v,
-                                                       const int* __restrict__ pos0, int msl,
-                                                       int span, int heads, int kv_heads, int seq,
-                                                       DecodeScratch sc) {
+struct RopeArgs {
+    const int32_t* acc;  // stacked [Q; K; V] accumulators, row stride q_dim + 2 kv_dim
+    const float* amax;
+    float sq, sk, sv;
+    const float* bq;
+    const float* bk;
+    const float* bv;
+    double theta;
+};
+
+template <int HD, bool ROPE>
+__global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict__ q, float* cache_k,
+                                                       float* cache_v, const int* __restrict__ pos0,
+                                                       int msl, int span, int heads, int kv_heads,
+                                                       int seq, DecodeScratch sc, RopeArgs ra) {
     constexpr int CH = kGqaChunk;
     constexpr int DH = HD / 2;   // score dims per lane
     constexpr int DP = HD / 64;  // output dims per lane
@@ -924,10 +950,12 @@ __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict_
     __shared__ __align__(16) float vs[CH * KP];
     __shared__ double qs[4][HD];
     __shared__ double ps[4][CH];
+    __shared__ double rc[ROPE ? HD / 2 : 1], rsn[ROPE ? HD / 2 : 1];
     const int kvh = blockIdx.x, chunk = blockIdx.y, row = blockIdx.z;
     const int G = heads / kv_heads;
     const int b = row / seq, s = row % seq;
-    const int L = min(*pos0 + s + 1, span);
+    const int pos = *pos0 + s;
+    const int L = min(pos + 1, span);
     const int k0 = chunk * CH;
     if (k0 >= L) return;  // uniform
     const int n = min(CH, L - k0);
@@ -947,6 +975,32 @@ __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict_
         *(float4*)&ks[r * KP + c4] = kv;
         *(float4*)&vs[r * KP + c4] = vv;
     }
+    const int32_t* ar = ROPE ? ra.acc + (size_t)row * (q_dim + 2 * kv_dim) : nullptr;
+    if (ROPE) {
+        if (tid < HD / 2) rope_angle(pos, tid, HD, ra.theta, &rc[tid], &rsn[tid]);
+        __syncthreads();  // angles; the chunk's K/V rows in LDS
+        if (k0 <= pos && pos < k0 + CH) {
+            const int rr = pos - k0;
+            const float am = ra.amax[row];
+            float* krow = cache_k + (size_t)b * msl * kv_dim + (size_t)(pos % msl) * kv_dim;
+            float* vrow = cache_v + (size_t)b * msl * kv_dim + (size_t)(pos % msl) * kv_dim;
+            if (tid < HD / 2) {
+                const int j0 = kvh * HD + tid, j1 = j0 + HD / 2;
+                float o0, o1;
+                k_pair(ar + q_dim, output_scale(ra.sk, am), ra.bk, j0, j1, rc[tid], rsn[tid], &o0, &o1);
+                ks[rr * KP + tid] = o0;
+                ks[rr * KP + tid + HD / 2] = o1;
+                krow[j0] = o0;
+                krow[j1] = o1;
+            }
+            if (tid < HD) {
+                const int j = kvh * HD + tid;
+                const float v = v_val(ar + q_dim + kv_dim, output_scale(ra.sv, am), ra.bv, j);
+                vs[rr * KP + tid] = v;
+                vrow[j] = v;
+            }
+        }
+    }
     const int pl = lane >> 1, half = lane & 1;
     const double inv_sqrt = 1.0 / sqrt((double)HD);
     for (int g0 = 0; g0 < G; g0 += 4) {
@@ -954,8 +1008,20 @@ __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict_
         const bool act = g < G;
         const int h = kvh * G + g;
         const size_t rh = (size_t)row * heads + h;
-        if (act)
-            for (int d = lane; d < HD; d += 64) qs[wave][d] = q[(size_t)row * q_dim + (size_t)h * HD + d];
+        if (act) {
+            if (ROPE) {
+                const double os = output_scale(ra.sq, ra.amax[row]);
+                for (int d = lane; d < HD / 2; d += 64) {
+                    const int j0 = h * HD + d, j1 = j0 + HD / 2;
+                    double o0, o1;
+                    q_pair(ar, os, ra.bq, j0, j1, rc[d], rsn[d], &o0, &o1);
+                    qs[wave][d] = o0;
+                    qs[wave][d + HD / 2] = o1;
+                }
+            } else {
+                for (int d = lane; d < HD; d += 64) qs[wave][d] = q[(size_t)row * q_dim + (size_t)h * HD + d];
+            }
+        }
         __syncthreads();
         double mc = -1e9, es = 0.0;
         if (act) {
@@ -1362,6 +1428,34 @@ static DecodeScratch decode_scratch(double* base, int rows, int heads, int hd, i
     return sc;
 }
 
+bool attention_rope_ok(int seq, int hd, int strict, int span) {
+    return !strict && seq == 1 && (hd == 64 || hd == 128) && span <= kMaxAttnSpan;
+}
+
+hipError_t launch_attention_rope(const int32_t* acc, const float* amax, float sq, float sk, float sv,
+                                 const float* bq, const float* bk, const float* bv, double theta,
+                                 int batch, const int* pos0, int msl, int span, int heads,
+                                 int kv_heads, int hd, float* cache_k, float* cache_v,
+                                 double* scratch, double* out, hipStream_t s) {
+    if (batch <= 0) return hipSuccess;
+    if (!attention_rope_ok(1, hd, 0, span) || span > msl || !scratch) return hipErrorInvalidValue;
+    if (kv_heads <= 0 || heads % kv_heads != 0 || batch > kSplitMaxRows) return hipErrorInvalidValue;
+    if (theta <= 0.0) theta = 10000.0;
+    const DecodeScratch sc = decode_scratch(scratch, batch, heads, hd, span);
+    const RopeArgs ra{acc, amax, sq, sk, sv, bq, bk, bv, theta};
+    const dim3 g(kv_heads, attn_nchunk32(span), batch), gc(heads, hd / 32, batch);
+    if (hd == 128) {
+        hipLaunchKernelGGL((attn_gqa_kernel<128, true>), g, dim3(256), 0, s, nullptr, cache_k, cache_v,
+                           pos0, msl, span, heads, kv_heads, 1, sc, ra);
+        hipLaunchKernelGGL(attn_combine32_kernel<128>, gc, dim3(256), 0, s, pos0, span, heads, 1, sc, out);
+    } else {
+        hipLaunchKernelGGL((attn_gqa_kernel<64, true>), g, dim3(256), 0, s, nullptr, cache_k, cache_v,
+                           pos0, msl, span, heads, kv_heads, 1, sc, ra);
+        hipLaunchKernelGGL(attn_combine32_kernel<64>, gc, dim3(256), 0, s, pos0, span, heads, 1, sc, out);
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_attention(const double* q, const float* cache_k, const float* cache_v,
                             int batch, int seq, const int* pos0, int msl, int span, int heads,
                             int kv_heads, int hd, int strict, double* scratch, double* out,
@@ -1377,14 +1471,17 @@ hipError_t launch_attention(const double* q, const float* cache_k, const float* 
         const int nc = attn_nchunk(span);
         if (!strict && (hd == 64 || hd == 128)) {
             const dim3 g(kv_heads, attn_nchunk32(span), rows), gc(heads, hd / 32, rows);
+            const RopeArgs none{};
+            float* ck = const_cast<float*>(cache_k);  // read only without ROPE
+            float* cv = const_cast<float*>(cache_v);
             if (hd == 128) {
-                hipLaunchKernelGGL(attn_gqa_kernel<128>, g, dim3(256), 0, s, q, cache_k, cache_v, pos0,
-                                   msl, span, heads, kv_heads, seq, sc);
+                hipLaunchKernelGGL((attn_gqa_kernel<128, false>), g, dim3(256), 0, s, q, ck, cv, pos0,
+                                   msl, span, heads, kv_heads, seq, sc, none);
                 hipLaunchKernelGGL(attn_combine32_kernel<128>, gc, dim3(256), 0, s, pos0, span, heads,
                                    seq, sc, out);
             } else {
-                hipLaunchKernelGGL(attn_gqa_kernel<64>, g, dim3(256), 0, s, q, cache_k, cache_v, pos0,
-                                   msl, span, heads, kv_heads, seq, sc);
+                hipLaunchKernelGGL((attn_gqa_kernel<64, false>), g, dim3(256), 0, s, q, ck, cv, pos0,
+                                   msl, span, heads, kv_heads, seq, sc, none);
                 hipLaunchKernelGGL(attn_combine32_kernel<64>, gc, dim3(256), 0, s, pos0, span, heads,
                                    seq, sc, out);
             }

@@ -1,6 +1,7 @@
 // block_api.hip -- loom_amd_block_* and loom_amd_model_* entry points
 // (include/loom_accel_amd.h): one BitNet decoder block, and the greedy
 // decode loop of a stack of them, device-resident end to end.
+#include <stdlib.h>
 #include <string.h>
 
 #include <string>
@@ -20,6 +21,7 @@ struct BlockDev {
     int q_dim = 0, kv_dim = 0;
     double theta = 10000.0, norm_eps = 0.0, attn_eps = 0.0, ffn_eps = 0.0;
     int activation = 1, strict = 1;
+    bool fuse_rope = true;  // fast decode: Q/K/V epilogue inside the attention launch
     Matrix qkv, o, gate, up, down;  // tiles point into `weights`
     float sq = 1.0f, sk = 1.0f, sv = 1.0f;
     float *norm1 = nullptr, *norm2 = nullptr, *attn_norm = nullptr, *ffn_norm = nullptr;
@@ -182,6 +184,10 @@ static int build_block(int device, const loom_amd_block_desc* d, const loom_amd_
     B->ffn_eps = d->ffn_eps;
     B->activation = d->ffn_activation;
     B->strict = d->norm_mode == LOOM_AMD_NORM_STRICT;
+    // LOOM_AMD_UNFUSED_ROPE=1 keeps the separate Q/K/V epilogue launch in fast
+    // decode (the tests compare both paths)
+    const char* unfused = getenv("LOOM_AMD_UNFUSED_ROPE");
+    B->fuse_rope = !(unfused && unfused[0] == '1');
     const int H = B->hidden;
     if (expect_shape(w->q, "q", B->q_dim, H, device) || expect_shape(w->k, "k", B->kv_dim, H, device) ||
         expect_shape(w->v, "v", B->kv_dim, H, device) || expect_shape(w->o, "o", H, B->q_dim, device) ||
@@ -311,15 +317,23 @@ static int block_forward_dev(const BlockDev& B, const Workspace& W, float* x, in
             if (e != hipSuccess) return fail_hip("block qkv projection", e);
         }
     }
-    e = launch_qkv_rope(W.acc, W.amax, B.sq, B.sk, B.sv, B.bq, B.bk, B.bv, batch, seq, pos, B.msl,
-                        B.heads, B.kv_heads, B.hd, B.theta, W.q, B.cache_k, B.cache_v, s);
-    if (e != hipSuccess) return fail_hip("block qkv rope", e);
-    if (taps && (e = tap_copy(taps->q, W.q, (size_t)R * B.q_dim * 8, s)) != hipSuccess) {
-        return fail_hip("block taps", e);
+    if (!taps && B.fuse_rope && batch <= kSplitMaxRows && attention_rope_ok(seq, B.hd, B.strict, B.span())) {
+        // fast decode: the Q/K/V epilogue runs inside the attention launch
+        e = launch_attention_rope(W.acc, W.amax, B.sq, B.sk, B.sv, B.bq, B.bk, B.bv, B.theta, batch, pos,
+                                  B.msl, B.span(), B.heads, B.kv_heads, B.hd, B.cache_k, B.cache_v,
+                                  W.scores, W.attn, s);
+        if (e != hipSuccess) return fail_hip("block attention", e);
+    } else {
+        e = launch_qkv_rope(W.acc, W.amax, B.sq, B.sk, B.sv, B.bq, B.bk, B.bv, batch, seq, pos, B.msl,
+                            B.heads, B.kv_heads, B.hd, B.theta, W.q, B.cache_k, B.cache_v, s);
+        if (e != hipSuccess) return fail_hip("block qkv rope", e);
+        if (taps && (e = tap_copy(taps->q, W.q, (size_t)R * B.q_dim * 8, s)) != hipSuccess) {
+            return fail_hip("block taps", e);
+        }
+        e = launch_attention(W.q, B.cache_k, B.cache_v, batch, seq, pos, B.msl, B.span(), B.heads,
+                             B.kv_heads, B.hd, B.strict, W.scores, W.attn, s);
+        if (e != hipSuccess) return fail_hip("block attention", e);
     }
-    e = launch_attention(W.q, B.cache_k, B.cache_v, batch, seq, pos, B.msl, B.span(), B.heads,
-                         B.kv_heads, B.hd, B.strict, W.scores, W.attn, s);
-    if (e != hipSuccess) return fail_hip("block attention", e);
     if (taps && (e = tap_copy(taps->attn, W.attn, (size_t)R * B.q_dim * 8, s)) != hipSuccess) {
         return fail_hip("block taps", e);
     }

@@ -470,6 +470,35 @@ def test_greedy_sample_semantics(orc, torch_dev, tf):
         assert got == orc.argmax_first(row), m
 
 
+@pytest.mark.parametrize("shape", ["small", "bitnet2b"])
+def test_fast_decode_rope_fused_attention(orc, torch_dev, tf, shape, monkeypatch):
+    # Fast single-token decode runs the Q/K/V epilogue (RoPE, K/V cache write)
+    # inside the attention launch; with LOOM_AMD_UNFUSED_ROPE=1 a block keeps
+    # the separate epilogue kernel.  Same steps, so outputs and caches agree
+    # bit for bit, over batch 2 and several positions.
+    torch = torch_dev
+    sh = SMALL if shape == "small" else BITNET_2B
+    w = Weights(orc, sh, seed=1251, bias=True)
+    gw = w.gpu(tf)
+    fused = tf.BitNetBlock(w.cfg(tf, "fast", max_batch=2), gw)
+    monkeypatch.setenv("LOOM_AMD_UNFUSED_ROPE", "1")
+    plain = tf.BitNetBlock(w.cfg(tf, "fast", max_batch=2), gw)
+    monkeypatch.delenv("LOOM_AMD_UNFUSED_ROPE")
+    for i, seq in enumerate([33, 1, 1, 1, 1]):
+        x_in = orc.normal_f32(2 * seq * sh.hidden, 1400 + i).reshape(2, seq, sh.hidden)
+        a = to_dev(torch, x_in.reshape(2 * seq, sh.hidden)).reshape(2, seq, sh.hidden)
+        b = a.clone()
+        fused.forward(a)
+        plain.forward(b)
+        torch.cuda.synchronize()
+        assert a.cpu().numpy().tobytes() == b.cpu().numpy().tobytes(), f"call {i}"
+        for slot in (0, 1):
+            for t_a, t_b in zip(fused.kv_cache(slot), plain.kv_cache(slot)):
+                assert t_a.cpu().numpy().tobytes() == t_b.cpu().numpy().tobytes(), f"cache call {i}"
+    fused.release()
+    plain.release()
+
+
 @pytest.mark.parametrize("shape,norm", [("small", "strict"), ("small", "fast"),
                                         ("bitnet2b", "strict"), ("bitnet2b", "fast")])
 def test_block_decode_norm_fused_matches_staged(orc, torch_dev, tf, shape, norm):
