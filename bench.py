@@ -12,7 +12,8 @@ bytes = N*ceil(K/16)*4 + 4*M*(K+N) (packed weights + fp32 in + fp32 out).
 
 Also reported: the dominant kernel's roofline (per-launch time from HIP events
 on the launch stream), the config-1 sweep (M in {1,8,64,512,4096} on both FFN
-shapes: GB/s for M <= 8, int8 TOPS for M >= 64), the fused SwiGLU FFN, the
+shapes, plus M=16384, config 4's rows per GEMM: GB/s for M <= 8, int8 TOPS for
+M >= 64), the fused SwiGLU FFN, the
 config-2 decoder block (seq 512), the config-3 greedy decode (30 layers, vocab
 128256, 2048-token prompt, 256 tokens; tok/s) and the config-4 prefill (batch
 8 x 2048; tok/s and int8 TOPS of the ternary projections), and the CPU
@@ -430,7 +431,7 @@ def main() -> int:
     if not args.no_sweep:
         sweep = []
         for shape_name, (nn, kk), mats in (("up_gate", UP, ups), ("down", DOWN, dns)):
-            for M in (1, 8, 64, 512, 4096):
+            for M in (1, 8, 64, 512, 4096, 16384):  # 16384: config 4's rows per GEMM
                 x = torch.from_numpy(orc.normal_f32(M * kk, seed=M).reshape(M, kk)).cuda()
                 q = bn.quantize_activation(x)
                 o = torch.empty((M, nn), dtype=torch.float32, device="cuda")
