@@ -1314,41 +1314,44 @@ __global__ __launch_bounds__(64) void attn_exp_kernel(const int* __restrict__ po
     if (k < L) sc.scores[rh * span + k] = exp(sc.scores[rh * span + k] - m);
 }
 
-// strict part 3: one workgroup per (head, row).  Lane d < HD adds its value
-// column in position order; one lane of another wave forms expSum in position
-// order.  V rows and probabilities stream through two LDS buffers in chunks
-// of C = 4096 / HD positions (4096 floats), with kChainDepth chunks of loads
-// in flight in registers.  The loads are branch-free (indices clamped into
-// the ring and the score row; surplus values are never used), so each store
-// waits only for its own chunk.  grid (heads, rows), 256 threads.
+// strict part 3: one workgroup per (head, group of DG value columns, row).
+// Lane d < DG adds its value column in position order; one lane of another
+// wave forms expSum in position order (every group of the head forms the same
+// chain).  V columns and probabilities stream through two LDS buffers in
+// chunks of C = 4096 / DG positions (4096 floats), with kChainDepth chunks of
+// loads in flight in registers.  The loads are branch-free (indices clamped
+// into the ring and the score row; surplus values are never used), so each
+// store waits only for its own chunk.  grid (heads * HD / DG, rows), 256 threads.
 constexpr int kChainDepth = 4;
+constexpr int kChainCols = 16;
 
-template <int HD>
+template <int HD, int DG>
 __global__ __launch_bounds__(256) void attn_chain_kernel(const float* __restrict__ cache_v,
                                                          const int* __restrict__ pos0, int msl,
                                                          int span, int heads, int kv_heads,
                                                          int seq, DecodeScratch sc,
                                                          double* __restrict__ out) {
-    constexpr int C = 4096 / HD;
-    static_assert(C * HD == 4096 && C <= 256, "chunk geometry");
+    constexpr int C = 4096 / DG;
+    static_assert(C * DG == 4096 && C <= 256 && HD % DG == 0 && DG % 4 == 0 && DG <= 192,
+                  "chunk geometry");
     __shared__ float4 vbuf[2][1024];
     __shared__ double pbuf[2][256];
     __shared__ double es_sh;
-    const int h = blockIdx.x, row = blockIdx.y;
+    const int h = blockIdx.x / (HD / DG), dg = blockIdx.x % (HD / DG), row = blockIdx.y;
     const int b = row / seq, s = row % seq;
     const int kvh = h / (heads / kv_heads);
     const int q_dim = heads * HD, kv_dim = kv_heads * HD;
     const int tid = threadIdx.x;
     const int L = *pos0 + s + 1;
-    double* orow = out + (size_t)row * q_dim + (size_t)h * HD;
+    double* orow = out + (size_t)row * q_dim + (size_t)h * HD + dg * DG;
     if (L > span) {
-        if (tid < HD) orow[tid] = __builtin_nan("");
+        if (tid < DG) orow[tid] = __builtin_nan("");
         return;
     }
     const int nch = (L + C - 1) / C;
-    const float* vb = cache_v + (size_t)b * msl * kv_dim + (size_t)kvh * HD;
+    const float* vb = cache_v + (size_t)b * msl * kv_dim + (size_t)kvh * HD + dg * DG;
     const double* pr = sc.scores + ((size_t)row * heads + h) * span;
-    constexpr int es_lane = HD <= 192 ? 192 : 0;
+    constexpr int es_lane = 192;
 
     float4 r[kChainDepth][4];
     double rp[kChainDepth];
@@ -1357,8 +1360,8 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(const float* __restrict
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int e = (tid + i * 256) * 4;  // element of the 4096-float chunk
-            const int k = min(cc * C + e / HD, msl - 1);
-            r[u][i] = *(const float4*)(vb + (size_t)k * kv_dim + e % HD);
+            const int k = min(cc * C + e / DG, msl - 1);
+            r[u][i] = *(const float4*)(vb + (size_t)k * kv_dim + e % DG);
         }
         rp[u] = pr[min(cc * C + min(tid, C - 1), span - 1)];
     };
@@ -1379,7 +1382,7 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(const float* __restrict
                 const float* vbb = (const float*)vbuf[u & 1];
                 const double* pbb = pbuf[u & 1];
                 const int n = min(C, L - c * C);
-                if (tid < HD) {
+                if (tid < DG) {
                     int j = 0;
                     for (; j + 16 <= n; j += 16) {
                         double a[16];
@@ -1387,12 +1390,12 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(const float* __restrict
 #pragma unroll
                         for (int t = 0; t < 16; ++t) {
                             a[t] = pbb[j + t];
-                            v[t] = vbb[(j + t) * HD + tid];
+                            v[t] = vbb[(j + t) * DG + tid];
                         }
 #pragma unroll
                         for (int t = 0; t < 16; ++t) sum += a[t] * (double)v[t];
                     }
-                    for (; j < n; ++j) sum += pbb[j] * (double)vbb[j * HD + tid];
+                    for (; j < n; ++j) sum += pbb[j] * (double)vbb[j * DG + tid];
                 }
                 if (tid == es_lane) es = ordered_sum(pbb, n, es);
             }
@@ -1400,7 +1403,7 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(const float* __restrict
     }
     if (tid == es_lane) es_sh = es;
     __syncthreads();
-    if (tid < HD) orow[tid] = sum / es_sh;
+    if (tid < DG) orow[tid] = sum / es_sh;
 }
 
 // LDS bytes of one fused attention workgroup for `span` positions.
@@ -1496,21 +1499,18 @@ hipError_t launch_attention(const double* q, const float* cache_k, const float* 
                                pos0, msl, span, heads, kv_heads, hd, seq, sc);
             hipLaunchKernelGGL(attn_exp_kernel, dim3(heads, nc, rows), dim3(64), 0, s, pos0, span,
                                heads, seq, sc);
-            const dim3 g(heads, rows), t(256);
+            constexpr int DG = kChainCols;
+            const dim3 t(256);
+#define LAMD_CHAIN(HDV)                                                                              \
+    hipLaunchKernelGGL((attn_chain_kernel<HDV, DG>), dim3(heads * (HDV / DG), rows), t, 0, s, cache_v, pos0, \
+                       msl, span, heads, kv_heads, seq, sc, out)
             switch (hd) {
-                case 32:
-                    hipLaunchKernelGGL(attn_chain_kernel<32>, g, t, 0, s, cache_v, pos0, msl, span, heads, kv_heads, seq, sc, out);
-                    break;
-                case 64:
-                    hipLaunchKernelGGL(attn_chain_kernel<64>, g, t, 0, s, cache_v, pos0, msl, span, heads, kv_heads, seq, sc, out);
-                    break;
-                case 128:
-                    hipLaunchKernelGGL(attn_chain_kernel<128>, g, t, 0, s, cache_v, pos0, msl, span, heads, kv_heads, seq, sc, out);
-                    break;
-                default:
-                    hipLaunchKernelGGL(attn_chain_kernel<256>, g, t, 0, s, cache_v, pos0, msl, span, heads, kv_heads, seq, sc, out);
-                    break;
+                case 32: LAMD_CHAIN(32); break;
+                case 64: LAMD_CHAIN(64); break;
+                case 128: LAMD_CHAIN(128); break;
+                default: LAMD_CHAIN(256); break;
             }
+#undef LAMD_CHAIN
         }
         return hipGetLastError();
     }
