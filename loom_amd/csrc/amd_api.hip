@@ -110,6 +110,7 @@ int create_matrix(int device, const uint32_t* words, size_t n_words, int rows, i
     uint32_t* staging = nullptr;
     const size_t src_bytes = (size_t)rows * (size_t)row_words * 4;
     hipError_t e = hipMalloc(&staging, src_bytes);
+    if (e == hipSuccess) e = gemm_prepare(device);
     if (e == hipSuccess) e = hipMalloc(&m.tiles, m.bytes());
     if (e == hipSuccess) e = hipMemcpy(staging, words, src_bytes, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = launch_repack(staging, rows, cols, row_words, &m, nullptr);
@@ -151,6 +152,7 @@ int create_matrix_ms_offline(int device, const uint8_t* packed, int rows, int co
     uint32_t* staging = nullptr;
     hipError_t e = hipMalloc(&dpacked, packed_bytes ? packed_bytes : 1);
     if (e == hipSuccess) e = hipMalloc(&staging, (size_t)rows * row_words * 4);
+    if (e == hipSuccess) e = gemm_prepare(device);
     if (e == hipSuccess) e = hipMalloc(&m.tiles, m.bytes());
     if (e == hipSuccess && packed_bytes) e = hipMemcpy(dpacked, packed, packed_bytes, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = launch_ms_offline_to_words(dpacked, rows, cols, staging, nullptr);

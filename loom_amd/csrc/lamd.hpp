@@ -132,4 +132,8 @@ void* scratch(int device, size_t bytes, std::string* err);
 
 const char* kernel_variant(int m);  // name of the matmul path chosen for M rows
 
+// Allocates the GEMM's split-K workspace on a device (once; called when a
+// matrix is created there, never by a matmul call).
+hipError_t gemm_prepare(int device);
+
 }  // namespace lamd

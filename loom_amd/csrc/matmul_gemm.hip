@@ -1,9 +1,63 @@
 // matmul_gemm.hip -- ternary x int8 GEMM for many token rows (prefill, M > 64).
+#include <mutex>
+#include <vector>
+
 #include "device_common.hpp"
 
 namespace lamd {
 
 constexpr int kXcds = 8;
+
+// Split-K workspace of one device: int32 partial accumulators of up to
+// kSplitSlots workgroups (kSplitSlotInts each) and one arrival counter per
+// output tile.  The counters start at zero and the last workgroup of a tile
+// sets its counter back to zero, so no launch clears them.  Allocated when a
+// matrix is created on the device, never inside a matmul call (which may be
+// under stream capture); without it the GEMM does not split.  Split launches
+// that overlap on one device would share it: they are issued on one stream.
+constexpr int kSplitSlotInts = 64 * 256;  // 64-token tiles: 64 accumulators x 256 threads
+constexpr int kSplitSlots = 768;
+constexpr int kSplitTiles = 1024;
+struct SplitWs {
+    int32_t* part = nullptr;
+    unsigned* ctr = nullptr;
+};
+static std::mutex g_split_mu;
+static std::vector<SplitWs> g_split;
+
+hipError_t gemm_prepare(int device) {
+    std::lock_guard<std::mutex> lock(g_split_mu);
+    if ((int)g_split.size() <= device) g_split.resize(device + 1);
+    SplitWs& w = g_split[device];
+    if (w.part) return hipSuccess;
+    int32_t* part = nullptr;
+    unsigned* ctr = nullptr;
+    hipError_t e = hipMalloc(&part, (size_t)kSplitSlots * kSplitSlotInts * 4);
+    if (e == hipSuccess) e = hipMalloc(&ctr, (size_t)kSplitTiles * 4);
+    if (e == hipSuccess) e = hipMemset(ctr, 0, (size_t)kSplitTiles * 4);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        if (part) (void)hipFree(part);
+        if (ctr) (void)hipFree(ctr);
+        return e;
+    }
+    w.part = part;
+    w.ctr = ctr;
+    return hipSuccess;
+}
+
+static SplitWs split_ws(int device) {
+    std::lock_guard<std::mutex> lock(g_split_mu);
+    return device < (int)g_split.size() ? g_split[device] : SplitWs{};
+}
+
+// Grid of one GEMM launch: mtiles x ngroups output tiles, each split into
+// ksplit ranges of `sps` K stages (the last range may be shorter).
+struct GemmGrid {
+    int mtiles, ngroups, ksplit, sps;
+    int32_t* part;
+    unsigned* ctr;
+};
 
 // ------------------------------------------------------------------------
 // gemm32: v_mfma_i32_32x32x32_i8, which issues int8 at twice the rate of the
@@ -23,17 +77,27 @@ constexpr int kXcds = 8;
 // eight K steps.  Activations: padded LDS rows; lane l reads row l&31, chunk
 // c + h.  The loop runs two stages per trip so the two register sets of the
 // staged loads swap roles statically (no copies, no waits on fresh loads).
+// MI = 2 halves the tile to 64 tokens (more workgroups for mid-size M).
+// Split K (ksplit > 1, MI = 2 only): workgroup (tile, r) sums K stages
+// [r*sps, (r+1)*sps), stores its int32 accumulators to its workspace slot,
+// and the last of the tile's workgroups to arrive (a device-scope counter)
+// adds the other slots to its own -- integer adds, so the result is the same
+// in any order -- and runs the epilogue.
 // ------------------------------------------------------------------------
 constexpr int kRow32 = 144;
 
 // EPI: 0 = plain dense (fp32 out only), 1 + EPI_DENSE / EPI_SWIGLU / EPI_ACC =
 // that epilogue kind with its optional bias, residual, activation and taps.
-template <int NMAT, int EPI>
-__global__ __launch_bounds__(256, 2) void gemm32_kernel(MatArgs p, int mtiles, int ngroups) {
-    constexpr int MI = 4;
+template <int NMAT, int EPI, int MI>
+__global__ __launch_bounds__(256, 2) void gemm32_kernel(MatArgs p, GemmGrid gg) {
     constexpr int NJ = 2 / NMAT;
-    constexpr int BM = 128;
-    __shared__ __align__(16) int8_t As[2][BM * kRow32];
+    constexpr int BM = 32 * MI;
+    constexpr int VALS = NMAT * MI * NJ * 16;  // accumulators per thread
+    // activation stages; the epilogue parks 4 waves x 32 rows x 72 ints here
+    constexpr int kAsBytes = 2 * BM * kRow32 > 4 * 32 * 72 * 4 ? 2 * BM * kRow32 : 4 * 32 * 72 * 4;
+    __shared__ __align__(16) int8_t As_raw[kAsBytes];
+    int8_t (*As)[BM * kRow32] = (int8_t (*)[BM * kRow32])As_raw;
+    __shared__ int s_last;
     // per-token epilogue constants, loaded before the main loop so the
     // epilogue issues no loads between its stores (vmcnt counts both in order)
     __shared__ double s_os0[BM], s_os1[NMAT == 2 ? BM : 1];
@@ -46,13 +110,20 @@ __global__ __launch_bounds__(256, 2) void gemm32_kernel(MatArgs p, int mtiles, i
     const int M = p.e.m;
     const int ktiles = p.ktiles;
     const int nstages = 2 * ktiles;
+    const int S = gg.ksplit;
 
-    const int total = mtiles * ngroups;
+    // split index fastest: the workgroups of one tile run on one XCD and
+    // exchange their partial sums through its L2
+    const int total = gg.mtiles * gg.ngroups * S;
     const int per_xcd = (total + kXcds - 1) / kXcds;
     const int linear = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
     if (linear >= total) return;
-    const int mt = linear / ngroups;
-    const int ng = linear % ngroups;
+    const int tile = linear / S;
+    const int split = linear - tile * S;
+    const int mt = tile / gg.ngroups;
+    const int ng = tile % gg.ngroups;
+    const int st0 = split * gg.sps;
+    const int st1 = min(st0 + gg.sps, nstages);
     const int m_wg = mt * BM;
     const int nb0 = (ng * 4 + wn) * NJ;  // wave's first 32-row weight block
     for (int t = tid; t < BM; t += 256) {
@@ -75,22 +146,22 @@ __global__ __launch_bounds__(256, 2) void gemm32_kernel(MatArgs p, int mtiles, i
         const int nt = min(2 * (nb0 + j) + ((lane >> 4) & 1), p.ntiles - 1);
         woff[j] = (nt * ktiles * 64 + (lane & 15) + 16 * h) * 16;
     }
-    // chunk c (0..3) of thread tid -> row 32*c + (tid>>3), 16-byte column tid&7
-    int aoff_g[4];
+    // chunk c (0..MI-1) of thread tid -> row 32*c + (tid>>3), 16-byte column tid&7
+    int aoff_g[MI];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < MI; ++c) {
         const int row = min(m_wg + 32 * c + (tid >> 3), M - 1);
         aoff_g[c] = row * p.ldq + (tid & 7) * 16;
     }
     const int aoff0 = (tid >> 3) * kRow32 + (tid & 7) * 16;
-    auto load_a = [&](int stage, uint4 (&st)[4]) {
+    auto load_a = [&](int stage, uint4 (&st)[MI]) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
+        for (int c = 0; c < MI; ++c)
             st[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ares, aoff_g[c], stage * 128, 0));
     };
-    auto store_a = [&](int buf, const uint4 (&st)[4]) {
+    auto store_a = [&](int buf, const uint4 (&st)[MI]) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) *(uint4*)(&As[buf][aoff0 + c * 32 * kRow32]) = st[c];
+        for (int c = 0; c < MI; ++c) *(uint4*)(&As[buf][aoff0 + c * 32 * kRow32]) = st[c];
     };
     // stage s: words 2*(s&1) and 2*(s&1)+1 of both tile lanes, K tile s>>1
     auto load_b = [&](int stage, uint2 (&b)[NMAT][NJ][2]) {
@@ -139,21 +210,22 @@ __global__ __launch_bounds__(256, 2) void gemm32_kernel(MatArgs p, int mtiles, i
 
     // Loads are issued in the loop's order (a, b of one stage, then of the
     // next) so the wait counts at the loop head match on entry and back edge.
-    const int last = nstages - 1;
-    uint4 a0[4], a1[4];
+    const int last = st1 - 1;
+    uint4 a0[MI], a1[MI];
     uint2 b0[NMAT][NJ][2], b1[NMAT][NJ][2];
-    load_a(0, a0);
+    load_a(st0, a0);
     __builtin_amdgcn_sched_barrier(0);
-    load_b(0, b0);
+    load_b(st0, b0);
     __builtin_amdgcn_sched_barrier(0);
-    load_a(1, a1);
+    load_a(st0 + 1, a1);
     __builtin_amdgcn_sched_barrier(0);
-    load_b(1, b1);
+    load_b(st0 + 1, b1);
     __builtin_amdgcn_sched_barrier(0);
     store_a(0, a0);
     __syncthreads();
-    // nstages is even: two stages per trip; set 0 holds even stages, set 1 odd
-    for (int s = 0; s < nstages; s += 2) {
+    // the stage range has even length: two stages per trip; set 0 holds even
+    // stages, set 1 odd
+    for (int s = st0; s < st1; s += 2) {
         load_a(min(s + 2, last), a0);
         compute(0, b0);
         load_b(min(s + 2, last), b0);
@@ -165,6 +237,55 @@ __global__ __launch_bounds__(256, 2) void gemm32_kernel(MatArgs p, int mtiles, i
         store_a(0, a0);
         __syncthreads();
     }
+
+    if (MI == 2 && S > 1) {
+        // Partial sums of this K range -> slot `linear` (value-major: each
+        // instruction covers 256 contiguous bytes).  The exchange uses
+        // device-scope relaxed atomic stores and loads (sc1: coherent across the
+        // XCDs' L2s, without the whole-L2 write-back and invalidate a
+        // device-scope fence costs): every slot store has completed (s_waitcnt)
+        // before the workgroup's arrival is counted, and the last workgroup
+        // reads the other slots only after its own arrival returns.
+        int32_t* mine = gg.part + (size_t)linear * kSplitSlotInts;
+#pragma unroll
+        for (int a = 0; a < NMAT; ++a)
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v)
+                        __hip_atomic_store(&mine[(((a * MI + i) * NJ + j) * 16 + v) * 256 + tid], acc[a][i][j][v],
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) {
+            s_last = __hip_atomic_fetch_add(&gg.ctr[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                     (unsigned)(S - 1);
+        }
+        __syncthreads();
+        if (!s_last) return;
+        for (int o = 0; o < S; ++o) {
+            if (o == split) continue;
+            const int32_t* src = gg.part + (size_t)(tile * S + o) * kSplitSlotInts;
+#pragma unroll
+            for (int a = 0; a < NMAT; ++a)
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) {
+                        v16i t;
+#pragma unroll
+                        for (int v = 0; v < 16; ++v)
+                            t[v] = __hip_atomic_load(&src[(((a * MI + i) * NJ + j) * 16 + v) * 256 + tid],
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        acc[a][i][j] += t;
+                    }
+        }
+        // every workgroup of the tile has arrived: ready for the next launch
+        if (tid == 0) __hip_atomic_store(&gg.ctr[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    static_assert(MI != 2 || VALS * 256 == kSplitSlotInts, "a split slot holds one 64-token tile");
 
     // Epilogue, one 32-token block i at a time: each wave parks its int32
     // block (32 x 64 values) in its own 9 KB of the (now idle) activation
@@ -230,25 +351,84 @@ __global__ __launch_bounds__(256, 2) void gemm32_kernel(MatArgs p, int mtiles, i
     }
 }
 
-template <int NMAT, int EPI>
-static hipError_t launch_gemm32(const MatArgs& p, hipStream_t s) {
-    const int mtiles = ceil_div(p.e.m, 128);
-    const int ngroups = ceil_div(p.ntiles, 16 / NMAT);
-    const int total = mtiles * ngroups;
+// Tile height and split of a launch (measured on MI355X at both BitNet-2B FFN
+// shapes, M = 65 .. 16384): 64-token tiles beat 128-token tiles at every M
+// (three workgroups per CU instead of two hide more load latency).  Splitting
+// K pays only while few tiles exist and every range keeps a long K loop: with
+// at most kSplitMaxTiles tiles, about kSplitTarget workgroups in all, at least
+// kMinSplitStages stages per range, at most kMaxSplit ranges.
+constexpr int kSplitMaxTilesPlan = 96;
+constexpr int kSplitTarget = 240;
+constexpr int kMinSplitStages = 12;
+constexpr int kMaxSplit = 4;
+
+static int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return v && *v ? atoi(v) : dflt;
+}
+
+struct GemmPlan {
+    int mi, ksplit, sps;
+};
+
+static GemmPlan plan_gemm(int m, int ntiles, int ktiles, int nmat, int device) {
+    const int ngroups = ceil_div(ntiles, 16 / nmat);
+    const int nstages = 2 * ktiles;
+    // LOOM_AMD_GEMM_TILE=128|64 and LOOM_AMD_GEMM_SPLIT=n override the choice
+    // (tuning and tests)
+    const int force_tile = env_int("LOOM_AMD_GEMM_TILE", 0);
+    const int force_split = env_int("LOOM_AMD_GEMM_SPLIT", 0);
+    if (force_tile == 128) return GemmPlan{4, 1, nstages};
+    const int tiles = ceil_div(m, 64) * ngroups;
+    int want = 1;
+    if (force_split > 0) {
+        want = force_split;
+    } else if (tiles <= kSplitMaxTilesPlan) {
+        want = ceil_div(kSplitTarget, tiles);
+        if (want > nstages / kMinSplitStages) want = nstages / kMinSplitStages;
+        if (want > kMaxSplit) want = kMaxSplit;
+        if (want < 1) want = 1;
+    }
+    int sps = 2 * ceil_div(ktiles, want);  // even ranges of stages
+    if (sps > nstages) sps = nstages;
+    int ks = ceil_div(nstages, sps);
+    const SplitWs ws = split_ws(device);
+    if (ks > 1 && (!ws.part || tiles > kSplitTiles || tiles * ks > kSplitSlots)) ks = 1;
+    return GemmPlan{2, ks, ks > 1 ? sps : nstages};
+}
+
+template <int NMAT, int EPI, int MI>
+static hipError_t launch_gemm32(const MatArgs& p, const GemmPlan& pl, int device, hipStream_t s) {
+    GemmGrid gg;
+    gg.mtiles = ceil_div(p.e.m, 32 * MI);
+    gg.ngroups = ceil_div(p.ntiles, 16 / NMAT);
+    gg.ksplit = pl.ksplit;
+    gg.sps = pl.sps;
+    const SplitWs ws = pl.ksplit > 1 ? split_ws(device) : SplitWs{};
+    gg.part = ws.part;
+    gg.ctr = ws.ctr;
+    const int total = gg.mtiles * gg.ngroups * gg.ksplit;
     const int grid = ceil_div(total, kXcds) * kXcds;
-    hipLaunchKernelGGL((gemm32_kernel<NMAT, EPI>), dim3(grid), dim3(256), 0, s, p, mtiles, ngroups);
+    hipLaunchKernelGGL((gemm32_kernel<NMAT, EPI, MI>), dim3(grid), dim3(256), 0, s, p, gg);
     return hipGetLastError();
+}
+
+template <int NMAT, int EPI>
+static hipError_t launch_gemm_planned(const MatArgs& p, int device, hipStream_t s) {
+    const GemmPlan pl = plan_gemm(p.e.m, p.ntiles, p.ktiles, NMAT, device);
+    if (pl.mi == 4) return launch_gemm32<NMAT, EPI, 4>(p, pl, device, s);
+    return launch_gemm32<NMAT, EPI, 2>(p, pl, device, s);
 }
 
 static bool plain_dense(const EpiDev& e) {
     return e.kind == EPI_DENSE && !e.bias0 && !e.residual && !e.post && !e.acc0;
 }
 
-hipError_t launch_gemm(const MatArgs& p, bool two, hipStream_t s) {
-    if (two) return launch_gemm32<2, 1 + EPI_SWIGLU>(p, s);
-    if (plain_dense(p.e)) return launch_gemm32<1, 0>(p, s);
-    if (p.e.kind == EPI_ACC) return launch_gemm32<1, 1 + EPI_ACC>(p, s);
-    return launch_gemm32<1, 1 + EPI_DENSE>(p, s);
+hipError_t launch_gemm(const MatArgs& p, bool two, int device, hipStream_t s) {
+    if (two) return launch_gemm_planned<2, 1 + EPI_SWIGLU>(p, device, s);
+    if (plain_dense(p.e)) return launch_gemm_planned<1, 0>(p, device, s);
+    if (p.e.kind == EPI_ACC) return launch_gemm_planned<1, 1 + EPI_ACC>(p, device, s);
+    return launch_gemm_planned<1, 1 + EPI_DENSE>(p, device, s);
 }
 
 }  // namespace lamd

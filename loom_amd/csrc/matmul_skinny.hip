@@ -14,7 +14,7 @@
 
 namespace lamd {
 
-hipError_t launch_gemm(const MatArgs& p, bool two, hipStream_t s);
+hipError_t launch_gemm(const MatArgs& p, bool two, int device, hipStream_t s);
 
 constexpr int kFusedMaxRows = 4;
 constexpr int kFusedVec = 16;  // float4 per thread in the fused prologue (max)
@@ -508,7 +508,7 @@ const char* kernel_variant(int m) {
     if (m <= 16) return "skinny_m16";
     if (m <= 32) return "skinny_m32";
     if (m <= 64) return "skinny_m64";
-    return "gemm";  // gemm32_kernel: 32x32x32 MFMA, 128-token x 256-row tiles
+    return "gemm";  // gemm32_kernel: 32x32x32 MFMA, 128- or 64-token x 256-row tiles, split K
 }
 
 static MatArgs make_args(const Matrix* w0, const Matrix* w1, int m, const Epilogue& epi) {
@@ -548,7 +548,7 @@ hipError_t launch_matmul(const Matrix* w0, const Matrix* w1, const QuantAct& a, 
     if (m <= 16) return two ? launch_skinny<2, 1, false>(p, s) : launch_skinny<1, 1, false>(p, s);
     if (m <= 32) return two ? launch_skinny<2, 2, false>(p, s) : launch_skinny<1, 2, false>(p, s);
     if (m <= 64) return two ? launch_skinny<2, 4, false>(p, s) : launch_skinny<1, 4, false>(p, s);
-    return launch_gemm(p, two, s);
+    return launch_gemm(p, two, w0->device, s);
 }
 
 // The fused prologue holds the M x K rows in registers (kFusedVec float4 per

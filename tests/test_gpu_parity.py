@@ -472,6 +472,39 @@ def test_swiglu_large_ragged(orc, torch_dev, bn):
                  with_norm_w=True)
 
 
+@pytest.mark.parametrize("shape,M", [((2560, 6912), 300), ((6912, 2560), 200), ((2560, 6912), 65),
+                                     ((1000, 2000), 129), ((2560, 6912), 512)])
+def test_gemm_split_k(orc, torch_dev, bn, shape, M):
+    # 64-token tiles split over K (the last K range shorter than the others),
+    # with the general epilogue (taps, residual) and the plain one, back to back
+    # on the same arrival counters
+    n, k = shape
+    m = orc.random_matrix(n, k, seed=n + M)
+    x = orc.normal_f32(M * k, seed=M + 5).reshape(M, k)
+    _check_dense(orc, torch_dev, bn, m, x)
+    res = orc.normal_f32(M * n, seed=M + 6).reshape(M, n)
+    _check_dense(orc, torch_dev, bn, m, x, residual=res)
+
+
+@pytest.mark.parametrize("tile,split", [("64", "1"), ("64", "2"), ("64", "3"), ("64", "27"),
+                                        ("128", "0")])
+def test_gemm_forced_plans(orc, torch_dev, bn, monkeypatch, tile, split):
+    # every tile height and split width, including one K tile per workgroup
+    # (27 ranges of the down shape), against the oracle
+    monkeypatch.setenv("LOOM_AMD_GEMM_TILE", tile)
+    monkeypatch.setenv("LOOM_AMD_GEMM_SPLIT", split)
+    m = orc.random_matrix(2560, 6912, seed=3)
+    x = orc.normal_f32(70 * 6912, seed=4).reshape(70, 6912)
+    _check_dense(orc, torch_dev, bn, m, x)
+
+
+def test_swiglu_split_k(orc, torch_dev, bn):
+    # gate|up at the BitNet-2B shape with 100 tokens: two-matrix 64-token tiles
+    # split over K
+    _swiglu_case(orc, torch_dev, bn, hidden=2560, inter=6912, M=100, seed=99, norm="strict",
+                 with_norm_w=True)
+
+
 # ---------------------------------------------------------------- golden fixtures
 def _golden(name):
     import os
