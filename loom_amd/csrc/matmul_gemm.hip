@@ -55,6 +55,7 @@ static SplitWs split_ws(int device) {
 // ksplit ranges of `sps` K stages (the last range may be shorter).
 struct GemmGrid {
     int mtiles, ngroups, ksplit, sps;
+    int group;  // token tiles per group of the tile order (0: weight-row group fastest)
     int32_t* part;
     unsigned* ctr;
 };
@@ -84,7 +85,6 @@ struct GemmGrid {
 // adds the other slots to its own -- integer adds, so the result is the same
 // in any order -- and runs the epilogue.
 // ------------------------------------------------------------------------
-constexpr int kRow32 = 144;
 
 // EPI: 0 = plain dense (fp32 out only), 1 + EPI_DENSE / EPI_SWIGLU / EPI_ACC =
 // that epilogue kind with its optional bias, residual, activation and taps.
@@ -93,10 +93,18 @@ __global__ __launch_bounds__(256, 2) void gemm32_kernel(MatArgs p, GemmGrid gg) 
     constexpr int NJ = 2 / NMAT;
     constexpr int BM = 32 * MI;
     constexpr int VALS = NMAT * MI * NJ * 16;  // accumulators per thread
+    // K stage width in bytes: 64-token tiles take a whole 256-column K tile
+    // per stage (twice the bytes in flight per register set)
+    constexpr int SW = MI == 2 ? 256 : 128;
+    constexpr int KROW = SW + 16;    // padded LDS row: rows start 16 bytes apart mod 256
+    constexpr int CPR = SW / 16;     // 16-byte chunks per row
+    constexpr int RP = 256 / CPR;    // rows per load pass of 256 threads
+    constexpr int NA = BM / RP;      // activation loads per thread per stage
+    constexpr int WPS = SW / 64;     // B words per tile lane per stage
     // activation stages; the epilogue parks 4 waves x 32 rows x 72 ints here
-    constexpr int kAsBytes = 2 * BM * kRow32 > 4 * 32 * 72 * 4 ? 2 * BM * kRow32 : 4 * 32 * 72 * 4;
+    constexpr int kAsBytes = 2 * BM * KROW > 4 * 32 * 72 * 4 ? 2 * BM * KROW : 4 * 32 * 72 * 4;
     __shared__ __align__(16) int8_t As_raw[kAsBytes];
-    int8_t (*As)[BM * kRow32] = (int8_t (*)[BM * kRow32])As_raw;
+    int8_t (*As)[BM * KROW] = (int8_t (*)[BM * KROW])As_raw;
     __shared__ int s_last;
     // per-token epilogue constants, loaded before the main loop so the
     // epilogue issues no loads between its stores (vmcnt counts both in order)
@@ -109,7 +117,7 @@ __global__ __launch_bounds__(256, 2) void gemm32_kernel(MatArgs p, GemmGrid gg) 
     const int l32 = lane & 31, h = lane >> 5;
     const int M = p.e.m;
     const int ktiles = p.ktiles;
-    const int nstages = 2 * ktiles;
+    const int nstages = ktiles * (256 / SW);
     const int S = gg.ksplit;
 
     // split index fastest: the workgroups of one tile run on one XCD and
@@ -120,8 +128,22 @@ __global__ __launch_bounds__(256, 2) void gemm32_kernel(MatArgs p, GemmGrid gg) 
     if (linear >= total) return;
     const int tile = linear / S;
     const int split = linear - tile * S;
-    const int mt = tile / gg.ngroups;
-    const int ng = tile % gg.ngroups;
+    // Tile order: `group` token tiles vary fastest, then the weight-row
+    // group, so the workgroups resident on one XCD (a contiguous run) share a
+    // few activation tiles and a few weight tiles that fit its L2 together.
+    int mt, ng;
+    if (gg.group > 0) {
+        const int per_group = gg.group * gg.ngroups;
+        const int g0 = tile / per_group;
+        const int first = g0 * gg.group;
+        const int gsz = min(gg.mtiles - first, gg.group);
+        const int in = tile - g0 * per_group;
+        mt = first + in % gsz;
+        ng = in / gsz;
+    } else {
+        mt = tile / gg.ngroups;
+        ng = tile % gg.ngroups;
+    }
     const int st0 = split * gg.sps;
     const int st1 = min(st0 + gg.sps, nstages);
     const int m_wg = mt * BM;
@@ -146,35 +168,48 @@ __global__ __launch_bounds__(256, 2) void gemm32_kernel(MatArgs p, GemmGrid gg) 
         const int nt = min(2 * (nb0 + j) + ((lane >> 4) & 1), p.ntiles - 1);
         woff[j] = (nt * ktiles * 64 + (lane & 15) + 16 * h) * 16;
     }
-    // chunk c (0..MI-1) of thread tid -> row 32*c + (tid>>3), 16-byte column tid&7
-    int aoff_g[MI];
+    // A stage: BM token rows x SW bytes, NA 16-byte loads per thread; load c
+    // of thread tid -> row RP*c + tid/CPR, 16-byte column tid%CPR
+    int aoff_g[NA];
 #pragma unroll
-    for (int c = 0; c < MI; ++c) {
-        const int row = min(m_wg + 32 * c + (tid >> 3), M - 1);
-        aoff_g[c] = row * p.ldq + (tid & 7) * 16;
+    for (int c = 0; c < NA; ++c) {
+        const int row = min(m_wg + RP * c + tid / CPR, M - 1);
+        aoff_g[c] = row * p.ldq + (tid % CPR) * 16;
     }
-    const int aoff0 = (tid >> 3) * kRow32 + (tid & 7) * 16;
-    auto load_a = [&](int stage, uint4 (&st)[MI]) {
+    const int aoff0 = (tid / CPR) * KROW + (tid % CPR) * 16;
+    auto load_a = [&](int stage, uint4 (&st)[NA]) {
 #pragma unroll
-        for (int c = 0; c < MI; ++c)
-            st[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ares, aoff_g[c], stage * 128, 0));
+        for (int c = 0; c < NA; ++c)
+            st[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ares, aoff_g[c], stage * SW, 0));
     };
-    auto store_a = [&](int buf, const uint4 (&st)[MI]) {
+    auto store_a = [&](int buf, const uint4 (&st)[NA]) {
 #pragma unroll
-        for (int c = 0; c < MI; ++c) *(uint4*)(&As[buf][aoff0 + c * 32 * kRow32]) = st[c];
+        for (int c = 0; c < NA; ++c) *(uint4*)(&As[buf][aoff0 + c * RP * KROW]) = st[c];
     };
-    // stage s: words 2*(s&1) and 2*(s&1)+1 of both tile lanes, K tile s>>1
-    auto load_b = [&](int stage, uint2 (&b)[NMAT][NJ][2]) {
-        const int soff = (stage >> 1) * 1024 + (stage & 1) * 8;
+    // B stage: words of both tile lanes (u) covering the stage's columns: for
+    // SW = 128 words 2*(s&1), 2*(s&1)+1 of K tile s>>1; for SW = 256 all four
+    // words of K tile s
+    auto load_b = [&](int stage, uint32_t (&b)[NMAT][NJ][2][WPS]) {
+        const int soff = SW == 256 ? stage * 1024 : (stage >> 1) * 1024 + (stage & 1) * 8;
 #pragma unroll
-        for (int j = 0; j < NJ; ++j)
+        for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                b[0][j][u] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wres0, woff[j] + 512 * u, soff, 0));
-                if (NMAT == 2)
-                    b[NMAT - 1][j][u] =
-                        __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wres1, woff[j] + 512 * u, soff, 0));
-            }
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const __amdgpu_buffer_rsrc_t r = mat == 0 ? wres0 : wres1;
+                    if (SW == 256) {
+                        const uint4 w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, woff[j] + 512 * u, soff, 0));
+                        b[mat][j][u][0] = w.x;
+                        b[mat][j][u][1] = w.y;
+                        b[mat][j][u][WPS > 2 ? 2 : 0] = w.z;
+                        b[mat][j][u][WPS > 3 ? 3 : 1] = w.w;
+                    } else {
+                        const uint2 w = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, woff[j] + 512 * u, soff, 0));
+                        b[mat][j][u][0] = w.x;
+                        b[mat][j][u][1] = w.y;
+                    }
+                }
     };
 
     v16i acc[NMAT][MI][NJ];
@@ -185,47 +220,50 @@ __global__ __launch_bounds__(256, 2) void gemm32_kernel(MatArgs p, GemmGrid gg) 
 #pragma unroll
             for (int j = 0; j < NJ; ++j) acc[a][i][j] = v16i{};
 
-    const int a_row = l32 * kRow32 + 16 * h;
-    auto compute = [&](int buf, const uint2 (&bw)[NMAT][NJ][2]) {
+    const int a_row = l32 * KROW + 16 * h;
+    auto compute = [&](int buf, const uint32_t (&bw)[NMAT][NJ][2][WPS]) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int cq = (q & 1) * 4 + (q >> 1) * 2;  // first chunk of the step's pair
-            v4i b[NMAT][NJ];
+        for (int hh = 0; hh < SW / 128; ++hh)
 #pragma unroll
-            for (int mat = 0; mat < NMAT; ++mat)
-#pragma unroll
-                for (int j = 0; j < NJ; ++j)
-                    b[mat][j] = unpack_codes((q & 1) ? bw[mat][j][q >> 1].y : bw[mat][j][q >> 1].x);
-            v4i a[MI];
-#pragma unroll
-            for (int i = 0; i < MI; ++i) a[i] = *(const v4i*)(&As[buf][a_row + i * 32 * kRow32 + 16 * cq]);
-#pragma unroll
-            for (int i = 0; i < MI; ++i)
+            for (int q = 0; q < 4; ++q) {
+                const int cq = (q & 1) * 4 + (q >> 1) * 2;  // first chunk of the step's pair
+                v4i b[NMAT][NJ];
 #pragma unroll
                 for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
-                    for (int j = 0; j < NJ; ++j) acc[mat][i][j] = mfma32_i8(a[i], b[mat][j], acc[mat][i][j]);
-        }
+                    for (int j = 0; j < NJ; ++j) b[mat][j] = unpack_codes(bw[mat][j][q >> 1][2 * hh + (q & 1)]);
+                v4i a[MI];
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+                    a[i] = *(const v4i*)(&As[buf][a_row + i * 32 * KROW + hh * 128 + 16 * cq]);
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+                        for (int j = 0; j < NJ; ++j) acc[mat][i][j] = mfma32_i8(a[i], b[mat][j], acc[mat][i][j]);
+            }
     };
 
     // Loads are issued in the loop's order (a, b of one stage, then of the
     // next) so the wait counts at the loop head match on entry and back edge.
     const int last = st1 - 1;
-    uint4 a0[MI], a1[MI];
-    uint2 b0[NMAT][NJ][2], b1[NMAT][NJ][2];
+    uint4 a0[NA], a1[NA];
+    uint32_t b0[NMAT][NJ][2][WPS], b1[NMAT][NJ][2][WPS];
     load_a(st0, a0);
     __builtin_amdgcn_sched_barrier(0);
     load_b(st0, b0);
     __builtin_amdgcn_sched_barrier(0);
-    load_a(st0 + 1, a1);
+    load_a(min(st0 + 1, last), a1);
     __builtin_amdgcn_sched_barrier(0);
-    load_b(st0 + 1, b1);
+    load_b(min(st0 + 1, last), b1);
     __builtin_amdgcn_sched_barrier(0);
     store_a(0, a0);
     __syncthreads();
-    // the stage range has even length: two stages per trip; set 0 holds even
-    // stages, set 1 odd
-    for (int s = st0; s < st1; s += 2) {
+    // two stages per trip; set 0 holds the stages at even distance from st0,
+    // set 1 the others; an odd range ends with one stage in set 0
+    int s = st0;
+    for (; s + 1 < st1; s += 2) {
         load_a(min(s + 2, last), a0);
         compute(0, b0);
         load_b(min(s + 2, last), b0);
@@ -237,6 +275,7 @@ __global__ __launch_bounds__(256, 2) void gemm32_kernel(MatArgs p, GemmGrid gg) 
         store_a(0, a0);
         __syncthreads();
     }
+    if (s < st1) compute(0, b0);
 
     if (MI == 2 && S > 1) {
         // Partial sums of this K range -> slot `linear` (value-major: each
@@ -356,10 +395,10 @@ __global__ __launch_bounds__(256, 2) void gemm32_kernel(MatArgs p, GemmGrid gg) 
 // (three workgroups per CU instead of two hide more load latency).  Splitting
 // K pays only while few tiles exist and every range keeps a long K loop: with
 // at most kSplitMaxTiles tiles, about kSplitTarget workgroups in all, at least
-// kMinSplitStages stages per range, at most kMaxSplit ranges.
+// kMinSplitKtiles K tiles per range, at most kMaxSplit ranges.
 constexpr int kSplitMaxTilesPlan = 96;
 constexpr int kSplitTarget = 240;
-constexpr int kMinSplitStages = 12;
+constexpr int kMinSplitKtiles = 6;
 constexpr int kMaxSplit = 4;
 
 static int env_int(const char* name, int dflt) {
@@ -373,28 +412,28 @@ struct GemmPlan {
 
 static GemmPlan plan_gemm(int m, int ntiles, int ktiles, int nmat, int device) {
     const int ngroups = ceil_div(ntiles, 16 / nmat);
-    const int nstages = 2 * ktiles;
     // LOOM_AMD_GEMM_TILE=128|64 and LOOM_AMD_GEMM_SPLIT=n override the choice
     // (tuning and tests)
     const int force_tile = env_int("LOOM_AMD_GEMM_TILE", 0);
     const int force_split = env_int("LOOM_AMD_GEMM_SPLIT", 0);
-    if (force_tile == 128) return GemmPlan{4, 1, nstages};
+    if (force_tile == 128) return GemmPlan{4, 1, 2 * ktiles};  // 128-column stages
+    // 64-token tiles: one stage per 256-column K tile
     const int tiles = ceil_div(m, 64) * ngroups;
     int want = 1;
     if (force_split > 0) {
         want = force_split;
     } else if (tiles <= kSplitMaxTilesPlan) {
         want = ceil_div(kSplitTarget, tiles);
-        if (want > nstages / kMinSplitStages) want = nstages / kMinSplitStages;
+        if (want > ktiles / kMinSplitKtiles) want = ktiles / kMinSplitKtiles;
         if (want > kMaxSplit) want = kMaxSplit;
         if (want < 1) want = 1;
     }
-    int sps = 2 * ceil_div(ktiles, want);  // even ranges of stages
-    if (sps > nstages) sps = nstages;
-    int ks = ceil_div(nstages, sps);
+    int sps = ceil_div(ktiles, want);
+    if (sps > ktiles) sps = ktiles;
+    int ks = ceil_div(ktiles, sps);
     const SplitWs ws = split_ws(device);
     if (ks > 1 && (!ws.part || tiles > kSplitTiles || tiles * ks > kSplitSlots)) ks = 1;
-    return GemmPlan{2, ks, ks > 1 ? sps : nstages};
+    return GemmPlan{2, ks, ks > 1 ? sps : ktiles};
 }
 
 template <int NMAT, int EPI, int MI>
@@ -404,6 +443,7 @@ static hipError_t launch_gemm32(const MatArgs& p, const GemmPlan& pl, int device
     gg.ngroups = ceil_div(p.ntiles, 16 / NMAT);
     gg.ksplit = pl.ksplit;
     gg.sps = pl.sps;
+    gg.group = env_int("LOOM_AMD_GEMM_GROUP", 8);
     const SplitWs ws = pl.ksplit > 1 ? split_ws(device) : SplitWs{};
     gg.part = ws.part;
     gg.ctr = ws.ctr;
