@@ -1353,54 +1353,71 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(const float* __restrict
     const double* pr = sc.scores + ((size_t)row * heads + h) * span;
     constexpr int es_lane = 192;
 
-    float4 r[kChainDepth][4];
-    double rp[kChainDepth];
-    auto issue = [&](int u, int c) {
-        const int cc = min(c, nch - 1);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int e = (tid + i * 256) * 4;  // element of the 4096-float chunk
-            const int k = min(cc * C + e / DG, msl - 1);
-            r[u][i] = *(const float4*)(vb + (size_t)k * kv_dim + e % DG);
-        }
-        rp[u] = pr[min(cc * C + min(tid, C - 1), span - 1)];
-    };
-#pragma unroll
-    for (int u = 0; u < kChainDepth; ++u) issue(u, u);
+    // staging registers of the chunks in flight: named scalars filled by
+    // macros (arrays of them, indexed in loops, were kept in scratch memory)
+    float4 r0_0, r0_1, r0_2, r0_3, r1_0, r1_1, r1_2, r1_3;
+    float4 r2_0, r2_1, r2_2, r2_3, r3_0, r3_1, r3_2, r3_3;
+    double rp0, rp1, rp2, rp3;
+#define LAMD_CHAIN_LD(U, I, CC)                                                   \
+    {                                                                             \
+        const int e = (tid + (I) * 256) * 4; /* element of the 4096-float chunk */ \
+        const int k = min((CC) * C + e / DG, msl - 1);                            \
+        r##U##_##I = *(const float4*)(vb + (size_t)k * kv_dim + e % DG);          \
+    }
+#define LAMD_CHAIN_ISSUE(U, CH)                                                   \
+    {                                                                             \
+        const int cc = min((CH), nch - 1);                                        \
+        LAMD_CHAIN_LD(U, 0, cc) LAMD_CHAIN_LD(U, 1, cc)                           \
+        LAMD_CHAIN_LD(U, 2, cc) LAMD_CHAIN_LD(U, 3, cc)                           \
+        rp##U = pr[min(cc * C + min(tid, C - 1), span - 1)];                      \
+    }
+    LAMD_CHAIN_ISSUE(0, 0)
+    LAMD_CHAIN_ISSUE(1, 1)
+    LAMD_CHAIN_ISSUE(2, 2)
+    LAMD_CHAIN_ISSUE(3, 3)
 
     double sum = 0.0, es = 0.0;
-    for (int c0 = 0; c0 < nch; c0 += kChainDepth) {
-#pragma unroll
-        for (int u = 0; u < kChainDepth; ++u) {
-            const int c = c0 + u;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) vbuf[u & 1][tid + i * 256] = r[u][i];
-            pbuf[u & 1][tid] = rp[u];
-            issue(u, c + kChainDepth);
-            __syncthreads();
-            if (c < nch) {  // uniform
-                const float* vbb = (const float*)vbuf[u & 1];
-                const double* pbb = pbuf[u & 1];
-                const int n = min(C, L - c * C);
-                if (tid < DG) {
-                    int j = 0;
-                    for (; j + 16 <= n; j += 16) {
-                        double a[16];
-                        float v[16];
-#pragma unroll
-                        for (int t = 0; t < 16; ++t) {
-                            a[t] = pbb[j + t];
-                            v[t] = vbb[(j + t) * DG + tid];
-                        }
-#pragma unroll
-                        for (int t = 0; t < 16; ++t) sum += a[t] * (double)v[t];
-                    }
-                    for (; j < n; ++j) sum += pbb[j] * (double)vbb[j * DG + tid];
-                }
-                if (tid == es_lane) es = ordered_sum(pbb, n, es);
-            }
-        }
+    // one chunk step per staging set U (a macro expanded for each U)
+#define LAMD_CHAIN_STEP(U)                                                                   \
+    {                                                                                        \
+        const int c = c0 + (U);                                                              \
+        vbuf[(U) & 1][tid] = r##U##_0;                                                       \
+        vbuf[(U) & 1][tid + 256] = r##U##_1;                                                 \
+        vbuf[(U) & 1][tid + 512] = r##U##_2;                                                 \
+        vbuf[(U) & 1][tid + 768] = r##U##_3;                                                 \
+        pbuf[(U) & 1][tid] = rp##U;                                                          \
+        LAMD_CHAIN_ISSUE(U, c + kChainDepth)                                                 \
+        __syncthreads();                                                                     \
+        if (c < nch) { /* uniform */                                                         \
+            const float* vbb = (const float*)vbuf[(U) & 1];                                  \
+            const double* pbb = pbuf[(U) & 1];                                               \
+            const int n = min(C, L - c * C);                                                 \
+            if (tid < DG) {                                                                  \
+                int j = 0;                                                                   \
+                for (; j + 16 <= n; j += 16) {                                               \
+                    double a[16];                                                            \
+                    float v[16];                                                             \
+                    _Pragma("unroll") for (int t = 0; t < 16; ++t) {                        \
+                        a[t] = pbb[j + t];                                                   \
+                        v[t] = vbb[(j + t) * DG + tid];                                      \
+                    }                                                                        \
+                    _Pragma("unroll") for (int t = 0; t < 16; ++t) sum += a[t] * (double)v[t]; \
+                }                                                                            \
+                for (; j < n; ++j) sum += pbb[j] * (double)vbb[j * DG + tid];                \
+            }                                                                                \
+            if (tid == es_lane) es = ordered_sum(pbb, n, es);                                \
+        }                                                                                    \
     }
+    static_assert(kChainDepth == 4, "the loop below expands four chunk steps");
+    for (int c0 = 0; c0 < nch; c0 += kChainDepth) {
+        LAMD_CHAIN_STEP(0)
+        LAMD_CHAIN_STEP(1)
+        LAMD_CHAIN_STEP(2)
+        LAMD_CHAIN_STEP(3)
+    }
+#undef LAMD_CHAIN_STEP
+#undef LAMD_CHAIN_ISSUE
+#undef LAMD_CHAIN_LD
     if (tid == es_lane) es_sh = es;
     __syncthreads();
     if (tid < DG) orow[tid] = sum / es_sh;
@@ -1715,32 +1732,53 @@ __global__ __launch_bounds__(256) void lm_head_kernel(const float* __restrict__ 
     const int row = tid >> 3;   // logit within the workgroup
     const int lane = tid & 7;   // DotTile lane
     const int full = (hidden / 8) * 8;
-    double p = 0.0;
-    for (int c0 = 0; c0 < full; c0 += kLmSlab) {
-        const int width = min(kLmSlab, full - c0);
-        __syncthreads();
-        // coalesced slab load: kLmRows rows x width columns, 4 columns a thread
+    // Slab loads: kLmRows rows x kLmSlab columns, 4 columns a thread, issued
+    // one slab ahead of the slab being summed (columns past the row's full
+    // 8-column chunks are read clamped and never stored).  Every slab but the
+    // last issues the next slab's loads with no branch around them (a branch
+    // would make the compiler wait for them at once); the staging registers
+    // are a plain unrolled array (no lambda captures it, so it stays in VGPRs).
+    constexpr int NL = kLmRows * (kLmSlab / 4) / 256;
+    constexpr int C4N = kLmSlab / 4;
+    const float* srow[NL];
+    int lcol[NL];
 #pragma unroll
-        for (int it = 0; it < kLmRows * (kLmSlab / 4) / 256; ++it) {
-            const int i = tid + it * 256;
-            const int r = i / (kLmSlab / 4);
-            const int c4 = (i % (kLmSlab / 4)) * 4;
-            const int v = min(v0 + r, vocab - 1);
-            if (c4 < width) {
-                const float* src = table + (size_t)v * hidden + c0 + c4;
-                if (VEC) {
-                    *(float4*)&slab[r][c4] = *(const float4*)src;
-                } else {
-                    slab[r][c4] = src[0];
-                    slab[r][c4 + 1] = src[1];
-                    slab[r][c4 + 2] = src[2];
-                    slab[r][c4 + 3] = src[3];
-                }
-            }
+    for (int it = 0; it < NL; ++it) {
+        const int i = tid + it * 256;
+        srow[it] = table + (size_t)min(v0 + i / C4N, vocab - 1) * hidden;
+        lcol[it] = (i % C4N) * 4;
+    }
+#define LAMD_LM_LOAD(C0)                                                                 \
+    _Pragma("unroll") for (int it = 0; it < NL; ++it) {                                \
+        const float* src = srow[it] + min((C0) + lcol[it], full - 4);                  \
+        nx[it] = VEC ? *(const float4*)src : make_float4(src[0], src[1], src[2], src[3]); \
+    }
+#define LAMD_LM_STORE(W)                                                                 \
+    _Pragma("unroll") for (int it = 0; it < NL; ++it) {                                \
+        if (lcol[it] < (W)) *(float4*)&slab[(tid + it * 256) / C4N][lcol[it]] = nx[it]; \
+    }
+    float4 nx[NL];
+    double p = 0.0;
+    const int nsl = (full + kLmSlab - 1) / kLmSlab;
+    if (nsl > 0) {
+        LAMD_LM_LOAD(0)
+        for (int i = 0; i + 1 < nsl; ++i) {
+            const int c0 = i * kLmSlab;
+            __syncthreads();  // the previous slab is summed
+            LAMD_LM_STORE(kLmSlab)
+            LAMD_LM_LOAD(c0 + kLmSlab)
+            __syncthreads();
+            for (int c = lane; c < kLmSlab; c += 8) p += (double)xs[c0 + c] * (double)slab[row][c];
         }
+        const int c0 = (nsl - 1) * kLmSlab;
+        const int width = full - c0;
+        __syncthreads();
+        LAMD_LM_STORE(width)
         __syncthreads();
         for (int c = lane; c < width; c += 8) p += (double)xs[c0 + c] * (double)slab[row][c];
     }
+#undef LAMD_LM_LOAD
+#undef LAMD_LM_STORE
     // lanes 0..3: x_l = p_l + p_{l+4}; lanes 0,1: t0 = x0 + x2, t1 = x1 + x3
     const double p4 = __shfl_down(p, 4, 8);
     const double xl = p + p4;

@@ -437,7 +437,6 @@ struct loom_amd_model {
     int batch = 0;                // batch of the current sequences
     int shadow = 0;               // host copy of the position
     hipStream_t own = nullptr;
-    hipEvent_t ev_in = nullptr, ev_out = nullptr;
     hipGraphExec_t graph = nullptr;
     int graph_batch = 0;
 };
@@ -553,8 +552,6 @@ static void free_model(loom_amd_model* m) {
     free_workspace(&m->ws);
     if (m->misc) (void)hipFree(m->misc);
     if (m->own) (void)hipStreamDestroy(m->own);
-    if (m->ev_in) (void)hipEventDestroy(m->ev_in);
-    if (m->ev_out) (void)hipEventDestroy(m->ev_out);
     delete m;
 }
 
@@ -628,8 +625,6 @@ int loom_amd_model_create(int device, const loom_amd_model_desc* desc,
     if (e == hipSuccess) e = hipMemset(m->tokens, 0, (size_t)max_batch * max_tokens * 4);
     if (e == hipSuccess) e = hipMemset(m->pos, 0, sizeof(int));
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&m->own, hipStreamNonBlocking);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_in, hipEventDisableTiming);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_out, hipEventDisableTiming);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         free_model(m);
@@ -742,12 +737,9 @@ int loom_amd_model_decode(loom_amd_model* m, int steps, int use_graph, float* lo
     hipStream_t s = (hipStream_t)stream;
     hipError_t e = hipSuccess;
     if (use_graph) {
-        // replay on the model's own stream, ordered after the caller's work and
-        // before the caller's later work by the model's two events
+        // captured on the model's own (idle) stream, replayed on the caller's
+        // stream: the step graphs stay in one queue with the caller's work
         hipStream_t cs = m->own;
-        e = hipEventRecord(m->ev_in, s);
-        if (e == hipSuccess) e = hipStreamWaitEvent(cs, m->ev_in, 0);
-        if (e != hipSuccess) return fail_hip("model decode", e);
         if (!m->graph || m->graph_batch != m->batch) {
             if (m->graph) {
                 (void)hipGraphExecDestroy(m->graph);
@@ -770,9 +762,7 @@ int loom_amd_model_decode(loom_amd_model* m, int steps, int use_graph, float* lo
             }
             m->graph_batch = m->batch;
         }
-        for (int i = 0; i < steps && e == hipSuccess; ++i) e = hipGraphLaunch(m->graph, cs);
-        if (e == hipSuccess) e = hipEventRecord(m->ev_out, cs);
-        if (e == hipSuccess) e = hipStreamWaitEvent(s, m->ev_out, 0);
+        for (int i = 0; i < steps && e == hipSuccess; ++i) e = hipGraphLaunch(m->graph, s);
         if (e != hipSuccess) return fail_hip("model decode replay", e);
     } else {
         for (int i = 0; i < steps; ++i) {

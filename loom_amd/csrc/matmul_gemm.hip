@@ -275,7 +275,10 @@ __global__ __launch_bounds__(256, 2) void gemm32_kernel(MatArgs p, GemmGrid gg) 
         store_a(0, a0);
         __syncthreads();
     }
-    if (s < st1) compute(0, b0);
+    if (s < st1) {
+        compute(0, b0);
+        __syncthreads();  // every wave has read buffer 0 before the epilogue parks its sums there
+    }
 
     if (MI == 2 && S > 1) {
         // Partial sums of this K range -> slot `linear` (value-major: each

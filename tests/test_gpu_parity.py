@@ -498,6 +498,22 @@ def test_gemm_forced_plans(orc, torch_dev, bn, monkeypatch, tile, split):
     _check_dense(orc, torch_dev, bn, m, x)
 
 
+def test_gemm_odd_stage_count_repeatable(orc, torch_dev, bn):
+    # K = 6912 gives an odd number of K stages (a one-stage tail before the
+    # epilogue reuses the stage buffers): many back-to-back launches must all
+    # produce the oracle's bytes
+    torch = torch_dev
+    m = orc.random_matrix(2560, 6912, seed=41)
+    x = orc.normal_f32(1024 * 6912, seed=42).reshape(1024, 6912)
+    ref = orc.dense_forward(m, x, simd=True).pre
+    w = gpu_matrix(bn, m)
+    xd = to_dev(torch, x)
+    outs = [bn.dense_forward_packed_ternary(w, xd)[0] for _ in range(40)]
+    torch.cuda.synchronize()
+    for i, o in enumerate(outs):
+        assert o.cpu().numpy().tobytes() == ref.tobytes(), f"launch {i} differs"
+
+
 def test_swiglu_split_k(orc, torch_dev, bn):
     # gate|up at the BitNet-2B shape with 100 tokens: two-matrix 64-token tiles
     # split over K
