@@ -223,6 +223,35 @@ def test_block_fast_prefill_bitnet_2b(orc, torch_dev, tf):
     run_block_case(orc, torch_dev, tf, w, [70, 1], seed=935, strict=False)
 
 
+@pytest.mark.parametrize("norm", ["fast", "strict"])
+def test_block_repeatable(orc, torch_dev, tf, norm):
+    # The same prefill (every GEMM shape of the block, K-stage tails included)
+    # and decode step, many times back to back: every output byte and every
+    # cached K/V row must repeat.  A race between waves or launches shows up
+    # here as a rare difference.
+    torch = torch_dev
+    # 700 rows: the down projection (K = 6912, an odd number of K stages) runs
+    # unsplit, so its one-stage tail meets the epilogue
+    sh = Shape(2560, 20, 5, 128, 6912, 768)
+    w = Weights(orc, sh, seed=181, act=ACT_SILU)
+    blk = tf.BitNetBlock(w.cfg(tf, norm), w.gpu(tf))
+    xp = to_dev(torch, orc.normal_f32(700 * sh.hidden, 960).reshape(700, sh.hidden))
+    x1 = to_dev(torch, orc.normal_f32(sh.hidden, 961).reshape(1, sh.hidden))
+    ref = None
+    for rep in range(40 if norm == "fast" else 10):
+        a, b = xp.clone(), x1.clone()
+        blk.forward(a)
+        blk.forward(b)
+        ck, cv = blk.kv_cache(0)
+        got = (a.clone(), b.clone(), ck.clone(), cv.clone())
+        if ref is None:
+            ref = got
+            continue
+        for name, g, r in zip(("prefill", "decode", "K cache", "V cache"), got, ref):
+            assert torch.equal(g, r), f"repetition {rep}: {name} differs"
+    blk.release()
+
+
 def test_block_stages_bitnet_2b_shape(orc, torch_dev, tf):
     # config 2's block shape: hidden 2560, 20 heads / 5 KV heads x 128, FFN 6912
     w = Weights(orc, BITNET_2B, seed=161)
