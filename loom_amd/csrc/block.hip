@@ -177,27 +177,42 @@ __device__ __forceinline__ void rope_angle(int pos, int d, int hd, double theta,
 }
 
 // The three per-element steps, shared with the fused decode attention kernel.
-__device__ __forceinline__ void q_pair(const int32_t* ar, double os, const float* bq, int j0, int j1,
-                                       double c, double sn, double* o0, double* o1) {
-    const double v0 = (double)ar[j0] * os + (bq ? (double)bq[j0] : 0.0);
-    const double v1 = (double)ar[j1] * os + (bq ? (double)bq[j1] : 0.0);
+// The *_v forms take the loaded accumulators and biases (b_on: a bias exists).
+__device__ __forceinline__ void q_pair_v(int32_t a0, int32_t a1, double os, bool b_on, float b0, float b1,
+                                         double c, double sn, double* o0, double* o1) {
+    const double v0 = (double)a0 * os + (b_on ? (double)b0 : 0.0);
+    const double v1 = (double)a1 * os + (b_on ? (double)b1 : 0.0);
     *o0 = v0 * c - v1 * sn;
     *o1 = v0 * sn + v1 * c;
 }
 
-// ar points at the K part of the row's accumulators; j0/j1 index into K
-__device__ __forceinline__ void k_pair(const int32_t* ar, double os, const float* bk, int j0, int j1,
-                                       double c, double sn, float* o0, float* o1) {
-    const float k0 = (float)((double)ar[j0] * os + (bk ? (double)bk[j0] : 0.0));
-    const float k1 = (float)((double)ar[j1] * os + (bk ? (double)bk[j1] : 0.0));
+__device__ __forceinline__ void k_pair_v(int32_t a0, int32_t a1, double os, bool b_on, float b0, float b1,
+                                         double c, double sn, float* o0, float* o1) {
+    const float k0 = (float)((double)a0 * os + (b_on ? (double)b0 : 0.0));
+    const float k1 = (float)((double)a1 * os + (b_on ? (double)b1 : 0.0));
     const double v0 = (double)k0, v1 = (double)k1;
     *o0 = (float)(v0 * c - v1 * sn);
     *o1 = (float)(v0 * sn + v1 * c);
 }
 
+__device__ __forceinline__ float v_val_v(int32_t a, double os, bool b_on, float b) {
+    return (float)((double)a * os + (b_on ? (double)b : 0.0));
+}
+
+__device__ __forceinline__ void q_pair(const int32_t* ar, double os, const float* bq, int j0, int j1,
+                                       double c, double sn, double* o0, double* o1) {
+    q_pair_v(ar[j0], ar[j1], os, bq != nullptr, bq ? bq[j0] : 0.0f, bq ? bq[j1] : 0.0f, c, sn, o0, o1);
+}
+
+// ar points at the K part of the row's accumulators; j0/j1 index into K
+__device__ __forceinline__ void k_pair(const int32_t* ar, double os, const float* bk, int j0, int j1,
+                                       double c, double sn, float* o0, float* o1) {
+    k_pair_v(ar[j0], ar[j1], os, bk != nullptr, bk ? bk[j0] : 0.0f, bk ? bk[j1] : 0.0f, c, sn, o0, o1);
+}
+
 // ar points at the V part of the row's accumulators
 __device__ __forceinline__ float v_val(const int32_t* ar, double os, const float* bv, int j) {
-    return (float)((double)ar[j] * os + (bv ? (double)bv[j] : 0.0));
+    return v_val_v(ar[j], os, bv != nullptr, bv ? bv[j] : 0.0f);
 }
 
 __global__ void qkv_rope_kernel(const int32_t* __restrict__ acc, const float* __restrict__ amax,
@@ -962,32 +977,77 @@ __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict_
     const int nchunk = attn_nchunk32(span);
     const int q_dim = heads * HD, kv_dim = kv_heads * HD;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    // K and V rows of the chunk -> LDS (V rows past the length as zeros: their
-    // cache slots may hold anything, and 0 * NaN would poison the sums)
+    // K and V rows of the chunk -> registers (V rows past the length as zeros:
+    // their cache slots may hold anything, and 0 * NaN would poison the sums)
     const size_t cb = (size_t)b * msl * kv_dim + (size_t)kvh * HD;
+    constexpr int NKV = CH * PR4 / 256;
+    static_assert(NKV * 256 == CH * PR4, "chunk geometry");
+    float4 kreg[NKV], vreg[NKV];
 #pragma unroll
-    for (int i = tid; i < CH * PR4; i += 256) {
+    for (int j = 0; j < NKV; ++j) {
+        const int i = tid + j * 256;
         const int r = i / PR4, c4 = (i % PR4) * 4;
         const size_t o = cb + (size_t)min(k0 + r, msl - 1) * kv_dim + c4;
-        const float4 kv = *(const float4*)(cache_k + o);
-        float4 vv = *(const float4*)(cache_v + o);
-        if (r >= n) vv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        *(float4*)&ks[r * KP + c4] = kv;
-        *(float4*)&vs[r * KP + c4] = vv;
+        kreg[j] = *(const float4*)(cache_k + o);
+        vreg[j] = *(const float4*)(cache_v + o);
     }
+    // ROPE: the projection operands this workgroup needs are loaded with the
+    // K/V rows, and the angles computed while both are in flight: Q of the
+    // first group member per wave (lane d < HD/2: pair d, d + HD/2), and, in
+    // the workgroup whose chunk holds the new position, its K pair and V value
     const int32_t* ar = ROPE ? ra.acc + (size_t)row * (q_dim + 2 * kv_dim) : nullptr;
+    const bool newrow = ROPE && k0 <= pos && pos < k0 + CH;
+    int32_t qa0 = 0, qa1 = 0, ka0 = 0, ka1 = 0, va = 0;
+    float qb0 = 0.0f, qb1 = 0.0f, kb0 = 0.0f, kb1 = 0.0f, vbv = 0.0f;
+    float am = 0.0f;
     if (ROPE) {
+        am = ra.amax[row];
+        const int h0 = kvh * G + wave;
+        if (wave < G && lane < HD / 2) {
+            const int j0 = h0 * HD + lane, j1 = j0 + HD / 2;
+            qa0 = ar[j0];
+            qa1 = ar[j1];
+            if (ra.bq) {
+                qb0 = ra.bq[j0];
+                qb1 = ra.bq[j1];
+            }
+        }
+        if (newrow) {
+            if (tid < HD / 2) {
+                const int j0 = kvh * HD + tid, j1 = j0 + HD / 2;
+                ka0 = ar[q_dim + j0];
+                ka1 = ar[q_dim + j1];
+                if (ra.bk) {
+                    kb0 = ra.bk[j0];
+                    kb1 = ra.bk[j1];
+                }
+            }
+            if (tid < HD) {
+                const int j = kvh * HD + tid;
+                va = ar[q_dim + kv_dim + j];
+                if (ra.bv) vbv = ra.bv[j];
+            }
+        }
         if (tid < HD / 2) rope_angle(pos, tid, HD, ra.theta, &rc[tid], &rsn[tid]);
+    }
+#pragma unroll
+    for (int j = 0; j < NKV; ++j) {
+        const int i = tid + j * 256;
+        const int r = i / PR4, c4 = (i % PR4) * 4;
+        *(float4*)&ks[r * KP + c4] = kreg[j];
+        *(float4*)&vs[r * KP + c4] = r >= n ? make_float4(0.0f, 0.0f, 0.0f, 0.0f) : vreg[j];
+    }
+    if (ROPE) {
         __syncthreads();  // angles; the chunk's K/V rows in LDS
-        if (k0 <= pos && pos < k0 + CH) {
+        if (newrow) {
             const int rr = pos - k0;
-            const float am = ra.amax[row];
             float* krow = cache_k + (size_t)b * msl * kv_dim + (size_t)(pos % msl) * kv_dim;
             float* vrow = cache_v + (size_t)b * msl * kv_dim + (size_t)(pos % msl) * kv_dim;
             if (tid < HD / 2) {
                 const int j0 = kvh * HD + tid, j1 = j0 + HD / 2;
                 float o0, o1;
-                k_pair(ar + q_dim, output_scale(ra.sk, am), ra.bk, j0, j1, rc[tid], rsn[tid], &o0, &o1);
+                k_pair_v(ka0, ka1, output_scale(ra.sk, am), ra.bk != nullptr, kb0, kb1, rc[tid], rsn[tid],
+                         &o0, &o1);
                 ks[rr * KP + tid] = o0;
                 ks[rr * KP + tid + HD / 2] = o1;
                 krow[j0] = o0;
@@ -995,7 +1055,7 @@ __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict_
             }
             if (tid < HD) {
                 const int j = kvh * HD + tid;
-                const float v = v_val(ar + q_dim + kv_dim, output_scale(ra.sv, am), ra.bv, j);
+                const float v = v_val_v(va, output_scale(ra.sv, am), ra.bv != nullptr, vbv);
                 vs[rr * KP + tid] = v;
                 vrow[j] = v;
             }
@@ -1010,13 +1070,22 @@ __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict_
         const size_t rh = (size_t)row * heads + h;
         if (act) {
             if (ROPE) {
-                const double os = output_scale(ra.sq, ra.amax[row]);
-                for (int d = lane; d < HD / 2; d += 64) {
-                    const int j0 = h * HD + d, j1 = j0 + HD / 2;
-                    double o0, o1;
-                    q_pair(ar, os, ra.bq, j0, j1, rc[d], rsn[d], &o0, &o1);
-                    qs[wave][d] = o0;
-                    qs[wave][d + HD / 2] = o1;
+                const double os = output_scale(ra.sq, am);
+                if (g0 == 0) {  // operands loaded with the K/V rows
+                    if (lane < HD / 2) {
+                        double o0, o1;
+                        q_pair_v(qa0, qa1, os, ra.bq != nullptr, qb0, qb1, rc[lane], rsn[lane], &o0, &o1);
+                        qs[wave][lane] = o0;
+                        qs[wave][lane + HD / 2] = o1;
+                    }
+                } else {
+                    for (int d = lane; d < HD / 2; d += 64) {
+                        const int j0 = h * HD + d, j1 = j0 + HD / 2;
+                        double o0, o1;
+                        q_pair(ar, os, ra.bq, j0, j1, rc[d], rsn[d], &o0, &o1);
+                        qs[wave][d] = o0;
+                        qs[wave][d + HD / 2] = o1;
+                    }
                 }
             } else {
                 for (int d = lane; d < HD; d += 64) qs[wave][d] = q[(size_t)row * q_dim + (size_t)h * HD + d];
@@ -1098,6 +1167,19 @@ __global__ __launch_bounds__(256) void attn_combine32_kernel(const int* __restri
     const int nchunk = attn_nchunk32(span);
     const size_t rh = (size_t)row * heads + h;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int j = tid & 7, d = dg * 32 + (tid >> 3);
+    const double* pb = sc.part + rh * nchunk * HD + d;
+    // the partial sums of the first two groups of 64 chunks do not depend on
+    // the maximum: they load while it is formed
+    double pv[2][8], pe[2][8];
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int c = 64 * gi + 8 * u + j;
+            pv[gi][u] = c < nca ? pb[(size_t)c * HD] : 0.0;
+            pe[gi][u] = c < nca ? sc.pes[rh * nchunk + c] : 0.0;
+        }
     double M = -1e9;
     for (int c = tid; c < nca; c += 256) {
         const double v = sc.cmax[rh * nchunk + c];
@@ -1113,23 +1195,31 @@ __global__ __launch_bounds__(256) void attn_combine32_kernel(const int* __restri
     for (int w = 1; w < 4; ++w) M = wm[w] > M ? wm[w] : M;
     for (int c = tid; c < nca; c += 256) facs[c] = exp(sc.cmax[rh * nchunk + c] - M);
     __syncthreads();
-    const int j = tid & 7, d = dg * 32 + (tid >> 3);
-    const double* pb = sc.part + rh * nchunk * HD + d;
     double t = 0.0, e = 0.0;
-    for (int c0 = 0; c0 < nca; c0 += 64) {
-        double v[8], pe[8];
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int c = 64 * gi + 8 * u + j;
+            if (c < nca) {
+                t = fma(pv[gi][u], facs[c], t);
+                e = fma(pe[gi][u], facs[c], e);
+            }
+        }
+    for (int c0 = 128; c0 < nca; c0 += 64) {
+        double w[8], we[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int c = c0 + 8 * u + j;
-            v[u] = c < nca ? pb[(size_t)c * HD] : 0.0;
-            pe[u] = c < nca ? sc.pes[rh * nchunk + c] : 0.0;
+            w[u] = c < nca ? pb[(size_t)c * HD] : 0.0;
+            we[u] = c < nca ? sc.pes[rh * nchunk + c] : 0.0;
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int c = c0 + 8 * u + j;
             if (c < nca) {
-                t = fma(v[u], facs[c], t);
-                e = fma(pe[u], facs[c], e);
+                t = fma(w[u], facs[c], t);
+                e = fma(we[u], facs[c], e);
             }
         }
     }
