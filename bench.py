@@ -341,6 +341,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--sweep-m", default="1,8,64,512,4096,16384",
+                    help="token rows of the config-1 sweep (16384: config 4's rows per GEMM)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-model", action="store_true", help="skip configs 2-4")
     ap.add_argument("--model-layers", type=int, default=30)
@@ -402,6 +404,14 @@ def main() -> int:
     achieved = b1 / (ms_kernel * 1e-3) / 1e9
     log(f"gemv kernel M=1 up: {ms_kernel * 1e3:.2f} us/launch, {achieved:.0f} GB/s")
 
+    # latency floor of one launch that streams this many bytes: a device copy
+    # of the packed weights' size, rotating over as many buffers (HBM-resident)
+    srcs = [torch.empty(per // 4, dtype=torch.float32, device="cuda").fill_(1.0) for _ in range(rot)]
+    dst = torch.empty_like(srcs[0])
+    ms_copy = timer.run(lambda i: dst.copy_(srcs[i % rot]), args.steps, args.warmup, per_graph=rot)
+    del srcs, dst
+    log(f"device copy of {per} B: {ms_copy * 1e3:.2f} us/launch")
+
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -423,15 +433,18 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": pmc_traffic(),
-                     "kernel": "skinny_matmul_kernel<1,1,8> (ternary GEMV)",
-                     "us_per_launch": round(ms_kernel * 1e3, 3), "bytes_per_launch": b1},
+                     "kernel": "skinny_kernel<1,1,8,false> (ternary GEMV, pre-quantized row)",
+                     "us_per_launch": round(ms_kernel * 1e3, 3), "bytes_per_launch": b1,
+                     "copy_floor_us": round(ms_copy * 1e3, 3),
+                     "copy_floor_note": f"torch device copy of {per} B (read + write) per launch, "
+                                        f"same rotation: the per-launch latency floor at this size"},
     }
 
     # ---------------- config-1 sweep ----------------------------------------------
     if not args.no_sweep:
         sweep = []
         for shape_name, (nn, kk), mats in (("up_gate", UP, ups), ("down", DOWN, dns)):
-            for M in (1, 8, 64, 512, 4096, 16384):  # 16384: config 4's rows per GEMM
+            for M in (int(v) for v in args.sweep_m.split(",") if v):
                 x = torch.from_numpy(orc.normal_f32(M * kk, seed=M).reshape(M, kk)).cuda()
                 q = bn.quantize_activation(x)
                 o = torch.empty((M, nn), dtype=torch.float32, device="cuda")
