@@ -70,6 +70,16 @@ int loom_amd_matrix_from_entity_blob(int device, const void* blob, size_t len,
 int loom_amd_matrix_from_ms_offline(int device, const uint8_t* packed, int rows, int cols,
                                     float scale, loom_amd_matrix** out);
 
+/* Same, from an fp32 master (host, rows x cols, row-major), packed as loom's
+ * packFloat32AsBitNetTernaryMatrix does (poly/bitnet_cpu.go:934-962): scale =
+ * fp32(sequential fp64 sum of |w| / n) (0 -> 1), code = clamp(round(fp64(w /
+ * scale)), -1, 1) with the fp32 division of bitNetQuantValue
+ * (poly/bitnet_cpu.go:119-146); a master whose every weight is within 1e-6 of
+ * -1, 0 or 1 is packed at scale 1.  *scale_out (optional) receives the scale.
+ * Synchronous. */
+int loom_amd_matrix_from_float32(int device, const float* master, int rows, int cols,
+                                 loom_amd_matrix** out, float* scale_out);
+
 void loom_amd_matrix_release(loom_amd_matrix* m);
 
 int loom_amd_matrix_shape(const loom_amd_matrix* m, int* rows, int* cols, float* scale,
@@ -255,7 +265,13 @@ typedef struct loom_amd_model_desc {
 /* Build a model: layers[num_layers] as for loom_amd_block_create, fp32
  * embeddings (HOST, vocab x hidden), final RMSNorm gain (HOST, hidden, NULL =
  * no final norm) and fp32 LM head (HOST, vocab x hidden, NULL = tied to the
- * embeddings, BitNet's weight tying).  All layers share one device position. */
+ * embeddings, BitNet's weight tying).  A tied head runs in fp32 (DotTile
+ * order, poly/transformer.go:664-719).  An untied head of a model whose layers
+ * are ternary is what loom ternarizes (usePackedTernaryLMHead,
+ * poly/transformer.go:721-755): it is packed once here as
+ * loom_amd_matrix_from_float32 does and applied as the ternary matvec with
+ * per-token int8 activations, logits fp32(fp64 result).  All layers share one
+ * device position. */
 int loom_amd_model_create(int device, const loom_amd_model_desc* desc,
                           const loom_amd_block_weights* layers, const float* embeddings,
                           const float* final_norm, const float* lm_head, loom_amd_model** out);

@@ -89,6 +89,7 @@ SIGNATURES = {
     "loom_amd_matrix_create": (i32, [i32, P, sz, i32, i32, i32, f32, C.POINTER(P)]),
     "loom_amd_matrix_from_entity_blob": (i32, [i32, P, sz, C.POINTER(P), C.POINTER(sz)]),
     "loom_amd_matrix_from_ms_offline": (i32, [i32, P, i32, i32, f32, C.POINTER(P)]),
+    "loom_amd_matrix_from_float32": (i32, [i32, P, i32, i32, C.POINTER(P), C.POINTER(f32)]),
     "loom_amd_matrix_release": (None, [P]),
     "loom_amd_matrix_shape": (i32, [P, C.POINTER(i32), C.POINTER(i32), C.POINTER(f32),
                                     C.POINTER(sz)]),

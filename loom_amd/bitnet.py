@@ -113,6 +113,22 @@ class TernaryMatrix:
               "matrix_from_ms_offline")
         return cls(out.value, device)
 
+    @classmethod
+    def from_float32(cls, master: np.ndarray, rows: int, cols: int,
+                     device: int = 0) -> "TernaryMatrix":
+        """Pack an fp32 master as loom's packFloat32AsBitNetTernaryMatrix
+        (poly/bitnet_cpu.go:934-962): absmean scale, codes round(w/scale)
+        clamped to [-1, 1], scale 1 for an already-ternary master."""
+        master = np.ascontiguousarray(master, np.float32)
+        if master.size < rows * cols:
+            raise ValueError("master holds fewer than rows*cols weights")
+        out = C.c_void_p()
+        scale = C.c_float()
+        check(_lib.lib().loom_amd_matrix_from_float32(device, master.ctypes.data_as(C.c_void_p),
+                                                      rows, cols, C.byref(out), C.byref(scale)),
+              "matrix_from_float32")
+        return cls(out.value, device)
+
     @property
     def handle(self) -> C.c_void_p:
         if self._h is None:

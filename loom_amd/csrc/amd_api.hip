@@ -5,7 +5,11 @@
 
 #include <string.h>
 
+#include <math.h>
+
+#include <algorithm>
 #include <mutex>
+#include <thread>
 #include <string>
 #include <vector>
 
@@ -178,6 +182,80 @@ extern "C" {
 int loom_amd_matrix_from_ms_offline(int device, const uint8_t* packed, int rows, int cols,
                                     float scale, loom_amd_matrix** out) {
     return create_matrix_ms_offline(device, packed, rows, cols, scale, out);
+}
+
+// bitNetQuantValue (poly/bitnet_cpu.go:134-146): an fp32 division, rounded
+// half away from zero in fp64, clamped to [-1, 1]; Go's int(float64) on amd64
+// turns NaN and out-of-range values into INT64_MIN, hence -1.  Returns loom's
+// storage code (poly/bitnet_cpu.go:498-507): -1 -> 0, 0 -> 1, 1 -> 2.
+static uint32_t quant_code(float v, float scale) {
+    if (scale == 0.0f) scale = 1.0f;
+    const double r = round((double)(v / scale));
+    long long q;
+    if (!(r >= -9223372036854775808.0 && r < 9223372036854775808.0)) {
+        q = INT64_MIN;
+    } else {
+        q = (long long)r;
+    }
+    if (q > 1) q = 1;
+    if (q < -1) q = -1;
+    return (uint32_t)(q + 1);
+}
+
+// packFloat32AsBitNetTernaryMatrix (poly/bitnet_cpu.go:934-977) into loom's
+// row-major words (16 codes per u32, column c at bits 2*(c%16)).  The absmean
+// scale (poly/bitnet_cpu.go:119-132) is one sequential fp64 sum; the per-weight
+// codes are independent and are formed on several host threads.
+float pack_float32_words(const float* w, int rows, int cols, std::vector<uint32_t>* words) {
+    const size_t total = (size_t)rows * (size_t)cols;
+    double sum_abs = 0.0;
+    bool already = true;
+    for (size_t i = 0; i < total; ++i) {
+        const float v = w[i];
+        sum_abs += fabs((double)v);
+        if (!(fabs((double)v) < 1e-6 || fabs((double)(v - 1.0f)) < 1e-6 ||
+              fabs((double)(v + 1.0f)) < 1e-6)) {
+            already = false;
+        }
+    }
+    float scale = (float)(sum_abs / (double)total);
+    if (scale == 0.0f) scale = 1.0f;
+    if (already) scale = 1.0f;
+    const int rw = ceil_div(cols, 16);
+    words->assign((size_t)rows * rw, 0u);
+    uint32_t* out = words->data();
+    const unsigned hw = std::thread::hardware_concurrency();
+    const int nt = (int)std::max(1u, std::min(hw ? hw : 1u, 16u));
+    auto work = [&](int r0, int r1) {
+        for (int r = r0; r < r1; ++r) {
+            const float* src = w + (size_t)r * cols;
+            uint32_t* dst = out + (size_t)r * rw;
+            for (int c = 0; c < cols; ++c) dst[c / 16] |= quant_code(src[c], scale) << (2 * (c % 16));
+        }
+    };
+    if (nt <= 1 || total < ((size_t)1 << 20)) {
+        work(0, rows);
+    } else {
+        std::vector<std::thread> pool;
+        const int per = ceil_div(rows, nt);
+        for (int t = 0; t < nt; ++t) {
+            const int r0 = t * per, r1 = std::min(rows, r0 + per);
+            if (r0 < r1) pool.emplace_back(work, r0, r1);
+        }
+        for (auto& th : pool) th.join();
+    }
+    return scale;
+}
+
+int loom_amd_matrix_from_float32(int device, const float* master, int rows, int cols,
+                                 loom_amd_matrix** out, float* scale_out) {
+    if (out) *out = nullptr;
+    if (master == nullptr) return fail("master is null");
+    if (rows <= 0 || cols <= 0) return fail("rows and cols must be positive");
+    std::vector<uint32_t> words;
+    const float scale = pack_float32_words(master, rows, cols, &words);
+    if (scale_out) *scale_out = scale;
+    return create_matrix(device, words.data(), words.size(), rows, cols, ceil_div(cols, 16), scale, out);
 }
 
 const char* loom_amd_last_error(void) { return g_amd_error.c_str(); }

@@ -425,7 +425,8 @@ struct loom_amd_model {
     std::vector<BlockDev> layers;
     Workspace ws;
     float* embeddings = nullptr;
-    float* lm_head = nullptr;     // == embeddings when tied
+    float* lm_head = nullptr;     // fp32 head: == embeddings when tied
+    loom_amd_matrix* lm_ternary = nullptr;  // untied head of a ternary model (loom packs it)
     float* final_norm = nullptr;  // null: no final norm
     float* x = nullptr;           // max_batch*max_prefill x hidden
     float* fin = nullptr;         // max_batch x hidden
@@ -552,6 +553,7 @@ static void free_model(loom_amd_model* m) {
     free_workspace(&m->ws);
     if (m->misc) (void)hipFree(m->misc);
     if (m->own) (void)hipStreamDestroy(m->own);
+    if (m->lm_ternary) loom_amd_matrix_release(m->lm_ternary);
     delete m;
 }
 
@@ -592,7 +594,11 @@ int loom_amd_model_create(int device, const loom_amd_model_desc* desc,
     DeviceGuard guard(device);
     Layout L;
     const size_t o_emb = L.take((size_t)desc->vocab * H * 4);
-    const size_t o_lm = L.take(lm_head ? (size_t)desc->vocab * H * 4 : 0);
+    // usePackedTernaryLMHead (poly/transformer.go:721-734): an untied head of
+    // a model with ternary layers is packed and applied as a ternary matvec
+    const bool ternary_head = lm_head && desc->num_layers > 0;
+    const bool fp32_head = lm_head && !ternary_head;
+    const size_t o_lm = L.take(fp32_head ? (size_t)desc->vocab * H * 4 : 0);
     const size_t o_fn = L.take(final_norm ? (size_t)H * 4 : 0);
     const size_t o_x = L.take((size_t)max_batch * max_prefill * H * 4);
     const size_t o_fin = L.take((size_t)max_batch * H * 4);
@@ -607,7 +613,7 @@ int loom_amd_model_create(int device, const loom_amd_model_desc* desc,
     }
     char* base = (char*)m->misc;
     m->embeddings = (float*)(base + o_emb);
-    m->lm_head = lm_head ? (float*)(base + o_lm) : m->embeddings;
+    m->lm_head = fp32_head ? (float*)(base + o_lm) : m->embeddings;
     m->final_norm = final_norm ? (float*)(base + o_fn) : nullptr;
     m->x = (float*)(base + o_x);
     m->fin = (float*)(base + o_fin);
@@ -616,7 +622,7 @@ int loom_amd_model_create(int device, const loom_amd_model_desc* desc,
     m->argmax_part = (float2*)(base + o_part);
     m->pos = (int*)(base + o_pos);
     e = hipMemcpy(m->embeddings, embeddings, (size_t)desc->vocab * H * 4, hipMemcpyHostToDevice);
-    if (e == hipSuccess && lm_head) {
+    if (e == hipSuccess && fp32_head) {
         e = hipMemcpy(m->lm_head, lm_head, (size_t)desc->vocab * H * 4, hipMemcpyHostToDevice);
     }
     if (e == hipSuccess && final_norm) {
@@ -629,6 +635,12 @@ int loom_amd_model_create(int device, const loom_amd_model_desc* desc,
     if (e != hipSuccess) {
         free_model(m);
         return fail_hip("model upload", e);
+    }
+    if (ternary_head &&
+        loom_amd_matrix_from_float32(device, lm_head, desc->vocab, H, &m->lm_ternary, nullptr)) {
+        const std::string msg = "model LM head: " + g_amd_error;
+        free_model(m);
+        return fail(msg);
     }
     if (desc->num_layers > 0 && alloc_workspace(m->layers[0], max_batch * max_prefill, &m->ws)) {
         free_model(m);
@@ -661,8 +673,30 @@ static int model_head(loom_amd_model* m, const float* last, long ld, int batch, 
         if (e != hipSuccess) return fail_hip("model last rows", e);
     }
     h = m->fin;
-    e = launch_lm_head(m->lm_head, m->vocab, m->hidden, h, batch, m->logits, s);
-    if (e != hipSuccess) return fail_hip("model lm head", e);
+    if (m->lm_ternary) {
+        // applyPackedTernaryLMHead (poly/transformer.go:736-755): per-row int8
+        // quantization, ternary matvec, logits = fp32(fp64 result)
+        Epilogue epi;
+        epi.kind = EPI_DENSE;
+        epi.out = m->logits;
+        epi.ldo = m->vocab;
+        const Matrix& W = m->lm_ternary->m;
+        if (fused_quant_ok(batch, m->hidden, h)) {
+            e = launch_matmul_fused(&W, nullptr, h, batch, epi, nullptr, nullptr, s);
+        } else {
+            const Workspace& ws = m->ws;
+            const int ldq = pad_cols(m->hidden);
+            e = launch_act_quant(h, m->hidden, batch, m->hidden, ws.xq, ldq, ws.amax, ws.xsum, s);
+            if (e == hipSuccess) {
+                QuantAct a{ws.xq, ldq, ws.amax, ws.xsum};
+                e = launch_matmul(&W, nullptr, a, batch, epi, s);
+            }
+        }
+        if (e != hipSuccess) return fail_hip("model ternary lm head", e);
+    } else {
+        e = launch_lm_head(m->lm_head, m->vocab, m->hidden, h, batch, m->logits, s);
+        if (e != hipSuccess) return fail_hip("model lm head", e);
+    }
     e = launch_argmax(m->logits, m->vocab, batch, m->argmax_part, m->tokens, m->max_tokens, m->pos,
                       offset, s);
     if (e != hipSuccess) return fail_hip("model argmax", e);

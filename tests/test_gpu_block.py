@@ -553,3 +553,82 @@ def test_block_decode_norm_fused_matches_staged(orc, torch_dev, tf, shape, norm)
             assert np.array_equal(ga, gb), f"call {i}"
         else:
             assert np.mean(ga == gb) > 0.9 and np.abs(ga - gb).max() <= 0.02 * np.abs(ga).max()
+
+
+# ---------------------------------------------------------------- untied (ternary) LM head
+def _tiles(tf, bn_mat):
+    from loom_amd import _lib
+    import ctypes as C
+    rows, cols, scale, nbytes = C.c_int(), C.c_int(), C.c_float(), C.c_size_t()
+    _lib.lib().loom_amd_matrix_shape(bn_mat.handle, C.byref(rows), C.byref(cols), C.byref(scale),
+                                     C.byref(nbytes))
+    p = _lib.lib().loom_amd_matrix_tiles(bn_mat.handle)
+    t = tf._clone_device(p, (nbytes.value // 4,), 0, "<i4")
+    return t.cpu().numpy(), scale.value
+
+
+@pytest.mark.parametrize("case", ["kat", "normal", "ternary", "specials", "ragged"])
+def test_matrix_from_float32_matches_packer(orc, torch_dev, tf, case):
+    # loom_amd_matrix_from_float32 packs as packFloat32AsBitNetTernaryMatrix
+    # (poly/bitnet_cpu.go:934-962): the same words (hence the same device
+    # tiles) and the same scale as the oracle's packer.
+    from loom_amd import bitnet as bn
+    rng = np.random.default_rng(5)
+    if case == "kat":  # poly/tests/bitnet_cpu_test.go:134-153
+        rows, cols = 1, 4
+        w = np.array([-0.2, -0.8, 0.1, 0.8], np.float32)
+    elif case == "normal":
+        rows, cols = 96, 640
+        w = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
+    elif case == "ternary":  # every weight within 1e-6 of -1, 0, 1: scale 1
+        rows, cols = 32, 256
+        w = rng.integers(-1, 2, rows * cols).astype(np.float32)
+        w += (rng.standard_normal(rows * cols) * 1e-7).astype(np.float32)
+    elif case == "specials":  # NaN and out-of-range values become code -1
+        rows, cols = 16, 256
+        w = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
+        w[3], w[17], w[40], w[41] = np.nan, np.inf, -np.inf, np.float32(3e38)
+    else:
+        rows, cols = 33, 65
+        w = rng.standard_normal(rows * cols).astype(np.float32)
+    ref = orc.pack_float32(w, rows, cols)
+    got = bn.TernaryMatrix.from_float32(w, rows, cols)
+    want = bn.TernaryMatrix.from_words(ref.words, rows, cols, ref.scale)
+    tg, sg = _tiles(tf, got)
+    tw, sw = _tiles(tf, want)
+    assert np.float32(sg).tobytes() == np.float32(ref.scale).tobytes(), (sg, ref.scale)
+    assert np.array_equal(tg, tw)
+    if case == "kat":
+        assert np.float32(sg) == np.float32(0.475)
+    if case == "ternary":
+        assert sg == 1.0
+
+
+@pytest.mark.parametrize("batch", [1, 5])
+def test_model_untied_ternary_lm_head(orc, torch_dev, tf, batch):
+    # An untied head of a ternary model is what loom ternarizes
+    # (usePackedTernaryLMHead / applyPackedTernaryLMHead,
+    # poly/transformer.go:721-755): logits = fp32 of the ternary matvec of the
+    # final hidden with per-row int8 activations, bit for bit; 5 rows take the
+    # separate quantization launch, 1 row the fused one.
+    sh = SMALL
+    vocab = 700
+    M = Model(orc, sh, layers=2, vocab=vocab, seed=331)
+    head = orc.normal_f32(vocab * sh.hidden, 339) * np.float32(0.05)
+    cfg = M.layers[0].cfg(tf, norm="strict", max_batch=batch)
+    model = tf.Transformer(cfg, [w.gpu(tf) for w in M.layers], M.emb, M.fn, lm_head=head,
+                           vocab=vocab, final_norm_eps=1e-6, max_tokens=40)
+    ids = np.stack([(np.arange(10) * (31 + 2 * b) + 3 * b) % vocab for b in range(batch)])
+    logits = model.prefill(ids, logits=True).cpu().numpy()
+    hid = model.last_hidden().cpu().numpy()
+    packed = orc.pack_float32(head, vocab, sh.hidden)
+    ref = orc.dense_forward(packed, hid, simd=True)
+    assert logits.tobytes() == ref.pre.tobytes()
+    toks = model.tokens()
+    for b in range(batch):
+        assert toks[b, 10] == orc.argmax_first(logits[b])
+    # decode steps take the same head inside the captured step graph
+    step_logits = model.decode(3, use_graph=True, logits=True).cpu().numpy()
+    hid = model.last_hidden().cpu().numpy()
+    assert step_logits.tobytes() == orc.dense_forward(packed, hid, simd=True).pre.tobytes()
+    model.release()
