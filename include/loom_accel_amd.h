@@ -37,6 +37,10 @@ typedef struct loom_amd_matrix loom_amd_matrix;
 #define LOOM_AMD_NORM_STRICT 1 /* loom's sequential fp64 sum: bit-exact */
 #define LOOM_AMD_NORM_FAST 0   /* parallel fixed-order fp64 sum: <= 1 fp32 ulp */
 
+/* Summation order of the fp32 LM head (both bit-exact with loom). */
+#define LOOM_AMD_LM_DOTTILE 0    /* SIMD forward on: simd.DotTile's eight-lane order */
+#define LOOM_AMD_LM_SEQUENTIAL 1 /* SIMD forward off: one sequential fp64 sum per logit */
+
 /* Message of the last failing loom_amd_* call on the calling thread. */
 const char* loom_amd_last_error(void);
 
@@ -244,6 +248,12 @@ int loom_amd_block_kv_cache(const loom_amd_block* b, int slot, const float** k,
 int loom_amd_lm_head(const float* table, int vocab, int hidden, const float* x, int rows,
                      float* logits, void* stream);
 
+/* The same head with SIMD forward off (applyFP32LMHeadRows' scalar loop,
+ * poly/transformer.go:681-687, = dotTileGo, poly/simd/dot.go:14-21):
+ * logits[r][v] = fp32(sum over d in order of fp64(x[r][d]) * fp64(table[v][d])). */
+int loom_amd_lm_head_sequential(const float* table, int vocab, int hidden, const float* x,
+                                int rows, float* logits, void* stream);
+
 /* Greedy SampleTopK (k <= 1, poly/sampling.go:44-55) per row: the first
  * index of the largest logit, 0 when logits[r][0] is NaN.  ids (DEVICE) gets
  * one int32 per row. */
@@ -260,13 +270,15 @@ typedef struct loom_amd_model_desc {
     double final_norm_eps; /* <= 0: 1e-6 */
     int max_tokens;        /* tokens per sequence the model can hold (prompt + generated) */
     int max_prefill;       /* largest prompt length per call (0 = max_tokens) */
+    int lm_head_order;     /* fp32 head: LOOM_AMD_LM_DOTTILE (Network.UseSimdForward on
+                              amd64/arm64) or LOOM_AMD_LM_SEQUENTIAL (SIMD forward off) */
 } loom_amd_model_desc;
 
 /* Build a model: layers[num_layers] as for loom_amd_block_create, fp32
  * embeddings (HOST, vocab x hidden), final RMSNorm gain (HOST, hidden, NULL =
  * no final norm) and fp32 LM head (HOST, vocab x hidden, NULL = tied to the
- * embeddings, BitNet's weight tying).  A tied head runs in fp32 (DotTile
- * order, poly/transformer.go:664-719).  An untied head of a model whose layers
+ * embeddings, BitNet's weight tying).  A tied head runs in fp32, summed in
+ * desc->lm_head_order (poly/transformer.go:664-719).  An untied head of a model whose layers
  * are ternary is what loom ternarizes (usePackedTernaryLMHead,
  * poly/transformer.go:721-755): it is packed once here as
  * loom_amd_matrix_from_float32 does and applied as the ternary matvec with

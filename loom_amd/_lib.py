@@ -63,7 +63,8 @@ class BlockTaps(C.Structure):
 class ModelDesc(C.Structure):
     """loom_amd_model_desc."""
     _fields_ = [("block", BlockDesc), ("num_layers", i32), ("vocab", i32),
-                ("final_norm_eps", f64), ("max_tokens", i32), ("max_prefill", i32)]
+                ("final_norm_eps", f64), ("max_tokens", i32), ("max_prefill", i32),
+                ("lm_head_order", i32)]
 
 
 # name -> (restype, argtypes); every symbol declared in include/*.h.
@@ -108,6 +109,7 @@ SIGNATURES = {
     "loom_amd_block_kv_offset": (i32, [P]),
     "loom_amd_block_kv_cache": (i32, [P, i32, C.POINTER(P), C.POINTER(P)]),
     "loom_amd_lm_head": (i32, [P, i32, i32, P, i32, P, P]),
+    "loom_amd_lm_head_sequential": (i32, [P, i32, i32, P, i32, P, P]),
     "loom_amd_greedy_sample": (i32, [P, i32, i32, P, P]),
     "loom_amd_model_create": (i32, [i32, C.POINTER(ModelDesc), C.POINTER(BlockWeights), P, P, P,
                                     C.POINTER(P)]),

@@ -1796,105 +1796,141 @@ hipError_t launch_embed(const float* table, int vocab, int hidden, const int* to
 }
 
 // ------------------------------------------------------------------------
-// fp32 LM head in loom's amd64 DotTile order (poly/simd/avx2_amd64.s:14-79):
-// for each logit, eight fp64 lane partials p_l over the 8-column chunks in
-// chunk order, then ((p0+p4)+(p2+p6)) + ((p1+p5)+(p3+p7)) + 0, then the n%8
-// tail in order.  A workgroup owns 32 logits x 8 lanes; each 256-column slab
-// of its 32 table rows is staged through LDS with coalesced loads so every
-// lane still consumes its chunks in order.
+// fp32 LM head, logits[r][v] = fp32(sum_d fp64(x[r][d]) * fp64(table[v][d])),
+// in either of loom's two orders (applyFP32LMHeadRows,
+// poly/transformer.go:664-719):
+//  - DOTTILE (SIMD forward on; amd64 DotTile, poly/simd/avx2_amd64.s:14-79,
+//    which every architecture's DotTile matches): eight fp64 lane partials
+//    p_l over the 8-column chunks in chunk order, then
+//    ((p0+p4)+(p2+p6)) + ((p1+p5)+(p3+p7)) + 0, then the n%8 tail in order;
+//  - sequential (SIMD forward off, poly/transformer.go:681-687, = dotTileGo,
+//    poly/simd/dot.go:14-21): one fp64 chain, sum += x[d]*w[d] in order.
+// The product of two fp32 values is exact in fp64, so an FMA rounds exactly
+// as the separate multiply and add do.  Each thread owns one logit (the
+// eight DotTile partials are eight independent chains of that thread): a
+// workgroup covers 256 logits and stages 64-column slabs of its 256 table
+// rows through LDS (16 threads read one 256-byte row segment), the next
+// slab's loads in flight while the current one is summed.  The row pitch of
+// 65 floats keeps the per-thread column reads and the staging stores free of
+// bank conflicts.  A slab is a whole number of 8-column chunks, so the n%8
+// tail always lies in the last slab.
 // ------------------------------------------------------------------------
 
-constexpr int kLmRows = 32;
-constexpr int kLmSlab = 256;  // columns per LDS slab
+constexpr int kHeadLogits = 256;
+constexpr int kHeadSlab = 64;
 
-template <bool VEC>
+template <bool VEC, bool DOTTILE>
 __global__ __launch_bounds__(256) void lm_head_kernel(const float* __restrict__ table, int vocab,
                                                       int hidden, const float* __restrict__ x,
                                                       float* __restrict__ logits) {
-    __shared__ float slab[kLmRows][kLmSlab + 4];
+    __shared__ float slab[kHeadLogits][kHeadSlab + 1];
     extern __shared__ float xs[];  // hidden
     const int tid = threadIdx.x;
-    const int v0 = blockIdx.x * kLmRows;
+    const int v0 = blockIdx.x * kHeadLogits;
     x += (size_t)blockIdx.y * hidden;
     logits += (size_t)blockIdx.y * vocab;
     for (int i = tid; i < hidden; i += 256) xs[i] = x[i];
-    __syncthreads();
-    const int row = tid >> 3;   // logit within the workgroup
-    const int lane = tid & 7;   // DotTile lane
-    const int full = (hidden / 8) * 8;
-    // Slab loads: kLmRows rows x kLmSlab columns, 4 columns a thread, issued
-    // one slab ahead of the slab being summed (columns past the row's full
-    // 8-column chunks are read clamped and never stored).  Every slab but the
-    // last issues the next slab's loads with no branch around them (a branch
-    // would make the compiler wait for them at once); the staging registers
-    // are a plain unrolled array (no lambda captures it, so it stays in VGPRs).
-    constexpr int NL = kLmRows * (kLmSlab / 4) / 256;
-    constexpr int C4N = kLmSlab / 4;
+    constexpr int C4N = kHeadSlab / 4;           // threads per row segment
+    constexpr int NL = kHeadLogits * C4N / 256;  // float4 loads per thread per slab
+    const int lcol = (tid % C4N) * 4;
     const float* srow[NL];
-    int lcol[NL];
 #pragma unroll
     for (int it = 0; it < NL; ++it) {
-        const int i = tid + it * 256;
-        srow[it] = table + (size_t)min(v0 + i / C4N, vocab - 1) * hidden;
-        lcol[it] = (i % C4N) * 4;
+        srow[it] = table + (size_t)min(v0 + tid / C4N + it * (256 / C4N), vocab - 1) * hidden;
     }
-#define LAMD_LM_LOAD(C0)                                                                 \
-    _Pragma("unroll") for (int it = 0; it < NL; ++it) {                                \
-        const float* src = srow[it] + min((C0) + lcol[it], full - 4);                  \
-        nx[it] = VEC ? *(const float4*)src : make_float4(src[0], src[1], src[2], src[3]); \
+    // Loads past the last column are clamped and never stored.  Every slab
+    // but the last issues the next slab's loads with no branch around them (a
+    // branch would make the compiler wait for them at once); the staging
+    // registers are a plain unrolled array (no lambda captures it, so it stays
+    // in VGPRs).
+#define LAMD_HEAD_LOAD(C0)                                                             \
+    _Pragma("unroll") for (int it = 0; it < NL; ++it) {                              \
+        const int c = (C0) + lcol;                                                   \
+        if (VEC) {                                                                   \
+            nx[it] = *(const float4*)(srow[it] + min(c, hidden - 4));                \
+        } else {                                                                     \
+            nx[it] = make_float4(srow[it][min(c, hidden - 1)],                       \
+                                 srow[it][min(c + 1, hidden - 1)],                   \
+                                 srow[it][min(c + 2, hidden - 1)],                   \
+                                 srow[it][min(c + 3, hidden - 1)]);                  \
+        }                                                                            \
     }
-#define LAMD_LM_STORE(W)                                                                 \
-    _Pragma("unroll") for (int it = 0; it < NL; ++it) {                                \
-        if (lcol[it] < (W)) *(float4*)&slab[(tid + it * 256) / C4N][lcol[it]] = nx[it]; \
+#define LAMD_HEAD_STORE(W)                                                             \
+    _Pragma("unroll") for (int it = 0; it < NL; ++it) {                              \
+        float* d = &slab[tid / C4N + it * (256 / C4N)][lcol];                        \
+        if (lcol < (W)) d[0] = nx[it].x;                                             \
+        if (lcol + 1 < (W)) d[1] = nx[it].y;                                         \
+        if (lcol + 2 < (W)) d[2] = nx[it].z;                                         \
+        if (lcol + 3 < (W)) d[3] = nx[it].w;                                         \
+    }
+    // one 8-column chunk at slab column K into the lane partials (DOTTILE) or
+    // the single chain
+#define LAMD_HEAD_CHUNK(C0, K)                                                         \
+    _Pragma("unroll") for (int j = 0; j < 8; ++j) {                                  \
+        const double prod_x = (double)xs[(C0) + (K) + j];                            \
+        const double prod_w = (double)slab[tid][(K) + j];                            \
+        if (DOTTILE) {                                                               \
+            pl[j] = fma(prod_x, prod_w, pl[j]);                                      \
+        } else {                                                                     \
+            pl[0] = fma(prod_x, prod_w, pl[0]);                                      \
+        }                                                                            \
     }
     float4 nx[NL];
-    double p = 0.0;
-    const int nsl = (full + kLmSlab - 1) / kLmSlab;
-    if (nsl > 0) {
-        LAMD_LM_LOAD(0)
-        for (int i = 0; i + 1 < nsl; ++i) {
-            const int c0 = i * kLmSlab;
-            __syncthreads();  // the previous slab is summed
-            LAMD_LM_STORE(kLmSlab)
-            LAMD_LM_LOAD(c0 + kLmSlab)
-            __syncthreads();
-            for (int c = lane; c < kLmSlab; c += 8) p += (double)xs[c0 + c] * (double)slab[row][c];
-        }
-        const int c0 = (nsl - 1) * kLmSlab;
-        const int width = full - c0;
+    double pl[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pl[j] = 0.0;
+    const int nsl = (hidden + kHeadSlab - 1) / kHeadSlab;
+    LAMD_HEAD_LOAD(0)
+    for (int i = 0; i + 1 < nsl; ++i) {
+        const int c0 = i * kHeadSlab;
+        __syncthreads();  // the previous slab is summed (and xs is written)
+        LAMD_HEAD_STORE(kHeadSlab)
+        LAMD_HEAD_LOAD(c0 + kHeadSlab)
         __syncthreads();
-        LAMD_LM_STORE(width)
-        __syncthreads();
-        for (int c = lane; c < width; c += 8) p += (double)xs[c0 + c] * (double)slab[row][c];
+#pragma unroll
+        for (int k = 0; k < kHeadSlab; k += 8) LAMD_HEAD_CHUNK(c0, k)
     }
-#undef LAMD_LM_LOAD
-#undef LAMD_LM_STORE
-    // lanes 0..3: x_l = p_l + p_{l+4}; lanes 0,1: t0 = x0 + x2, t1 = x1 + x3
-    const double p4 = __shfl_down(p, 4, 8);
-    const double xl = p + p4;
-    const double x2 = __shfl_down(xl, 2, 8);
-    const double t = xl + x2;
-    const double t1 = __shfl_down(t, 1, 8);
-    if (lane == 0) {
-        double r = (t + t1) + 0.0;
-        const float* w = table + (size_t)min(v0 + row, vocab - 1) * hidden;
-        for (int i = full; i < hidden; ++i) r += (double)xs[i] * (double)w[i];
-        if (v0 + row < vocab) logits[v0 + row] = (float)r;
+    const int c0 = (nsl - 1) * kHeadSlab;
+    const int width = hidden - c0;
+    const int wfull = DOTTILE ? (width / 8) * 8 : 0;  // whole chunks of the last slab
+    __syncthreads();
+    LAMD_HEAD_STORE(width)
+    __syncthreads();
+    for (int k = 0; k < wfull; k += 8) LAMD_HEAD_CHUNK(c0, k)
+#undef LAMD_HEAD_LOAD
+#undef LAMD_HEAD_STORE
+#undef LAMD_HEAD_CHUNK
+    double r = pl[0];
+    if (DOTTILE) r = (((pl[0] + pl[4]) + (pl[2] + pl[6])) + ((pl[1] + pl[5]) + (pl[3] + pl[7]))) + 0.0;
+    for (int c = wfull; c < width; ++c) r = fma((double)xs[c0 + c], (double)slab[tid][c], r);
+    if (v0 + tid < vocab) logits[v0 + tid] = (float)r;
+}
+
+template <bool DOTTILE>
+static hipError_t launch_head(const float* table, int vocab, int hidden, const float* x, int rows,
+                              float* logits, hipStream_t s) {
+    if (vocab <= 0 || hidden <= 0 || rows <= 0) return hipSuccess;
+    const size_t shm = (size_t)hidden * sizeof(float);
+    if (shm > 64 * 1024) return hipErrorInvalidValue;
+    const dim3 g((unsigned)ceil_div(vocab, kHeadLogits), rows), b(256);
+    if (hidden % 4 == 0 && ((uintptr_t)table & 15) == 0) {
+        hipLaunchKernelGGL((lm_head_kernel<true, DOTTILE>), g, b, shm, s, table, vocab, hidden, x,
+                           logits);
+    } else {
+        hipLaunchKernelGGL((lm_head_kernel<false, DOTTILE>), g, b, shm, s, table, vocab, hidden, x,
+                           logits);
     }
+    return hipGetLastError();
 }
 
 hipError_t launch_lm_head(const float* table, int vocab, int hidden, const float* x, int rows,
                           float* logits, hipStream_t s) {
-    if (vocab <= 0 || hidden <= 0 || rows <= 0) return hipSuccess;
-    const size_t shm = (size_t)hidden * sizeof(float);
-    if (shm > 64 * 1024) return hipErrorInvalidValue;
-    const dim3 g((unsigned)ceil_div(vocab, kLmRows), rows), b(256);
-    if (hidden % 4 == 0 && ((uintptr_t)table & 15) == 0) {
-        hipLaunchKernelGGL(lm_head_kernel<true>, g, b, shm, s, table, vocab, hidden, x, logits);
-    } else {
-        hipLaunchKernelGGL(lm_head_kernel<false>, g, b, shm, s, table, vocab, hidden, x, logits);
-    }
-    return hipGetLastError();
+    return launch_head<true>(table, vocab, hidden, x, rows, logits, s);
+}
+
+hipError_t launch_lm_head_seq(const float* table, int vocab, int hidden, const float* x, int rows,
+                              float* logits, hipStream_t s) {
+    return launch_head<false>(table, vocab, hidden, x, rows, logits, s);
 }
 
 // ------------------------------------------------------------------------

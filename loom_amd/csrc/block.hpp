@@ -65,6 +65,9 @@ hipError_t launch_embed(const float* table, int vocab, int hidden, const int* to
 // DotTile order; logits rows are vocab apart.
 hipError_t launch_lm_head(const float* table, int vocab, int hidden, const float* x, int rows,
                           float* logits, hipStream_t s);
+// The same logits in loom's scalar order (one sequential fp64 sum per logit).
+hipError_t launch_lm_head_seq(const float* table, int vocab, int hidden, const float* x, int rows,
+                              float* logits, hipStream_t s);
 
 // Greedy sampling per logits row b: first strict maximum (index 0 when
 // logits[0] is NaN), written to tokens[b*cap + *pos0 + offset] when < cap.

@@ -422,6 +422,7 @@ struct loom_amd_model {
     int layers_n = 0, vocab = 0, hidden = 0, max_tokens = 0, max_prefill = 0;
     double final_eps = 0.0;
     int strict = 1;
+    int lm_sequential = 0;  // fp32 head in loom's scalar order (SIMD forward off)
     std::vector<BlockDev> layers;
     Workspace ws;
     float* embeddings = nullptr;
@@ -530,6 +531,16 @@ int loom_amd_lm_head(const float* table, int vocab, int hidden, const float* x, 
     return e == hipSuccess ? 0 : fail_hip("lm_head", e);
 }
 
+int loom_amd_lm_head_sequential(const float* table, int vocab, int hidden, const float* x,
+                                int rows, float* logits, void* stream) {
+    if (!table || !x || !logits) return fail("null buffer");
+    if (vocab <= 0 || hidden <= 0 || rows < 0) return fail("bad shape");
+    if ((size_t)hidden * 4 > 64 * 1024) return fail("hidden is limited to 16384");
+    if (rows == 0) return 0;
+    hipError_t e = launch_lm_head_seq(table, vocab, hidden, x, rows, logits, (hipStream_t)stream);
+    return e == hipSuccess ? 0 : fail_hip("lm_head_sequential", e);
+}
+
 int loom_amd_greedy_sample(const float* logits, int n, int rows, int32_t* ids, void* stream) {
     if (!logits || !ids) return fail("null buffer");
     if (n <= 0 || rows < 0) return fail("bad shape");
@@ -565,6 +576,8 @@ int loom_amd_model_create(int device, const loom_amd_model_desc* desc,
     if (!desc) return fail("model desc is null");
     if (desc->num_layers < 0 || desc->vocab <= 0) return fail("model desc: bad layer count or vocab");
     if (desc->num_layers > 0 && !layers) return fail("layers are null");
+    if (desc->lm_head_order != LOOM_AMD_LM_DOTTILE && desc->lm_head_order != LOOM_AMD_LM_SEQUENTIAL)
+        return fail("model desc: lm_head_order must be LOOM_AMD_LM_DOTTILE or LOOM_AMD_LM_SEQUENTIAL");
     if (!embeddings) return fail("embeddings are null");
     if (check_desc(&desc->block)) return -1;
     const loom_amd_block_desc& bd = desc->block;
@@ -583,6 +596,7 @@ int loom_amd_model_create(int device, const loom_amd_model_desc* desc,
     m->max_prefill = max_prefill;
     m->final_eps = desc->final_norm_eps;
     m->strict = bd.norm_mode == LOOM_AMD_NORM_STRICT;
+    m->lm_sequential = desc->lm_head_order == LOOM_AMD_LM_SEQUENTIAL;
     m->layers.resize(desc->num_layers);
     for (int i = 0; i < desc->num_layers; ++i) {
         if (build_block(device, &bd, &layers[i], &m->layers[i])) {
@@ -694,7 +708,9 @@ static int model_head(loom_amd_model* m, const float* last, long ld, int batch, 
         }
         if (e != hipSuccess) return fail_hip("model ternary lm head", e);
     } else {
-        e = launch_lm_head(m->lm_head, m->vocab, m->hidden, h, batch, m->logits, s);
+        e = m->lm_sequential
+                ? launch_lm_head_seq(m->lm_head, m->vocab, m->hidden, h, batch, m->logits, s)
+                : launch_lm_head(m->lm_head, m->vocab, m->hidden, h, batch, m->logits, s);
         if (e != hipSuccess) return fail_hip("model lm head", e);
     }
     e = launch_argmax(m->logits, m->vocab, batch, m->argmax_part, m->tokens, m->max_tokens, m->pos,

@@ -187,9 +187,10 @@ def _clone_device(ptr: int, shape: tuple, device: int, typestr: str = "<f4"):
     return torch.as_tensor(_DeviceView(ptr, shape, typestr), device=f"cuda:{device}").clone()
 
 
-def lm_head(table, x):
-    """applyFP32LMHeadRows (SIMD order) on device: table [vocab, hidden], x
-    [rows, hidden] float32 device tensors -> logits [rows, vocab]."""
+def lm_head(table, x, sequential: bool = False):
+    """applyFP32LMHeadRows on device: table [vocab, hidden], x [rows, hidden]
+    float32 device tensors -> logits [rows, vocab], in simd.DotTile's order
+    (SIMD forward on) or, with sequential, the scalar loop's."""
     torch = _torch()
     for t in (table, x):
         if t.dtype != torch.float32 or not t.is_cuda or not t.is_contiguous():
@@ -199,11 +200,16 @@ def lm_head(table, x):
     if x2.shape[1] != hidden:
         raise ValueError("hidden sizes differ")
     out = torch.empty(x2.shape[0], vocab, dtype=torch.float32, device=x.device)
-    check(_lib.lib().loom_amd_lm_head(C.c_void_p(table.data_ptr()), vocab, hidden,
-                                      C.c_void_p(x2.data_ptr()), x2.shape[0],
-                                      C.c_void_p(out.data_ptr()), _stream(x.device.index or 0)),
-          "lm_head")
+    fn = _lib.lib().loom_amd_lm_head_sequential if sequential else _lib.lib().loom_amd_lm_head
+    check(fn(C.c_void_p(table.data_ptr()), vocab, hidden, C.c_void_p(x2.data_ptr()), x2.shape[0],
+             C.c_void_p(out.data_ptr()), _stream(x.device.index or 0)), "lm_head")
     return out
+
+
+def lm_head_sequential(table, x):
+    """applyFP32LMHeadRows with SIMD forward off (one sequential fp64 sum per
+    logit) on device; arguments as for lm_head."""
+    return lm_head(table, x, sequential=True)
 
 
 def greedy_sample(logits):
@@ -220,13 +226,16 @@ def greedy_sample(logits):
 
 
 class Transformer:
-    """A stack of BitNet blocks with fp32 embeddings, final RMSNorm and fp32 LM
-    head (tied to the embeddings when lm_head is None), decoding greedily."""
+    """A stack of BitNet blocks with fp32 embeddings, final RMSNorm and LM head
+    (tied to the embeddings when lm_head is None), decoding greedily.  An fp32
+    head sums in simd.DotTile's order, or loom's scalar order when
+    simd_forward is False (Network.UseSimdForward)."""
 
     def __init__(self, cfg: BlockConfig, layers: list[BlockWeights], embeddings: np.ndarray,
                  final_norm: np.ndarray | None, lm_head: np.ndarray | None = None,
                  vocab: int | None = None, final_norm_eps: float = 1e-6,
-                 max_tokens: int | None = None, max_prefill: int = 0, device: int = 0):
+                 max_tokens: int | None = None, max_prefill: int = 0, device: int = 0,
+                 simd_forward: bool = True):
         self.cfg = cfg
         self.device = device
         emb = np.ascontiguousarray(embeddings, np.float32)
@@ -237,7 +246,7 @@ class Transformer:
             arr[i] = w.struct(keep)
         self.max_tokens = max_tokens or cfg.max_seq_len + 1
         desc = _lib.ModelDesc(cfg.desc(), len(layers), self.vocab, final_norm_eps,
-                              self.max_tokens, max_prefill)
+                              self.max_tokens, max_prefill, 0 if simd_forward else 1)
         fn = None if final_norm is None else np.ascontiguousarray(final_norm, np.float32)
         lm = None if lm_head is None else np.ascontiguousarray(lm_head, np.float32)
         out = C.c_void_p()
@@ -310,4 +319,4 @@ class Transformer:
 
 
 __all__ = ["BlockConfig", "BlockWeights", "BlockTaps", "BitNetBlock", "Transformer", "NORM_STRICT",
-           "lm_head", "greedy_sample"]
+           "lm_head", "lm_head_sequential", "greedy_sample"]

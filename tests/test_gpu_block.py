@@ -473,6 +473,31 @@ def test_lm_head_dottile_order(orc, torch_dev, tf, vocab, hidden):
         assert np.array_equal(got[r], orc.lm_head(x, table, simd=True)), (vocab, hidden, r)
 
 
+@pytest.mark.parametrize("vocab,hidden", [(1, 8), (33, 7), (100, 64), (257, 100), (1000, 2560),
+                                          (70, 2567), (5000, 320), (600, 65)])
+def test_lm_head_sequential_order(orc, torch_dev, tf, vocab, hidden):
+    # applyFP32LMHeadRows with SIMD forward off (poly/transformer.go:681-687):
+    # one sequential fp64 sum per logit, bit-exact; several rows, widths that
+    # end mid-slab, and a last row where the sequential and DotTile orders
+    # give 0 and 1 (products 2^60, 1, -2^60).
+    torch = torch_dev
+    table = orc.normal_f32(vocab * hidden, 19 + hidden) * np.float32(0.05)
+    rows = [orc.normal_f32(hidden, 31 + r) for r in range(3)]
+    if hidden >= 3:
+        t = table.reshape(vocab, hidden)
+        t[-1] = 0.0
+        t[-1, :3] = [2.0 ** 30, 2.0 ** -30, -(2.0 ** 30)]
+        rows.append(np.full(hidden, 2.0 ** 30, np.float32))
+    dt, dx = to_dev(torch, table.reshape(vocab, hidden)), to_dev(torch, np.stack(rows))
+    got = tf.lm_head_sequential(dt, dx).cpu().numpy()
+    for r, x in enumerate(rows):
+        assert np.array_equal(got[r], orc.lm_head(x, table, simd=False)), (vocab, hidden, r)
+    if hidden >= 3:
+        assert got[-1, -1] == 0.0
+    if hidden >= 8:  # narrower rows are all DotTile tail, summed in order
+        assert tf.lm_head(dt, dx).cpu().numpy()[-1, -1] == 1.0
+
+
 def test_greedy_sample_semantics(orc, torch_dev, tf):
     # SampleTopK greedy (poly/sampling.go:44-55): first strict maximum; NaN
     # never wins; a NaN at index 0 is never replaced.  Rows long enough to
@@ -631,4 +656,27 @@ def test_model_untied_ternary_lm_head(orc, torch_dev, tf, batch):
     step_logits = model.decode(3, use_graph=True, logits=True).cpu().numpy()
     hid = model.last_hidden().cpu().numpy()
     assert step_logits.tobytes() == orc.dense_forward(packed, hid, simd=True).pre.tobytes()
+    model.release()
+
+
+def test_model_sequential_lm_head(orc, torch_dev, tf):
+    # Network.UseSimdForward off: the tied fp32 head sums each logit in
+    # order (poly/transformer.go:681-687), in prefill and in the captured
+    # decode step.
+    sh = SMALL
+    vocab = 900
+    M = Model(orc, sh, layers=2, vocab=vocab, seed=351)
+    cfg = M.layers[0].cfg(tf, norm="strict", max_batch=2)
+    model = tf.Transformer(cfg, [w.gpu(tf) for w in M.layers], M.emb, M.fn, vocab=vocab,
+                           final_norm_eps=1e-6, max_tokens=40, simd_forward=False)
+    ids = np.stack([(np.arange(9) * 29 + 1) % vocab, (np.arange(9) * 41 + 7) % vocab])
+    logits = model.prefill(ids, logits=True).cpu().numpy()
+    hid = model.last_hidden().cpu().numpy()
+    for b in range(2):
+        assert logits[b].tobytes() == orc.lm_head(hid[b], M.emb, simd=False).tobytes()
+        assert model.tokens()[b, 9] == orc.argmax_first(logits[b])
+    step_logits = model.decode(3, use_graph=True, logits=True).cpu().numpy()
+    hid = model.last_hidden().cpu().numpy()
+    for b in range(2):
+        assert step_logits[b].tobytes() == orc.lm_head(hid[b], M.emb, simd=False).tobytes()
     model.release()

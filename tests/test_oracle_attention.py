@@ -221,3 +221,28 @@ def test_mha_stages_compose_to_forward(orc):
     assert np.array_equal(a, attn)
     p2, o2 = orc.attn_out(m.mats[3], attn, inner_norm=m.inner_norm, eps=1e-5)
     assert np.array_equal(p2, pre) and np.array_equal(o2, post)
+
+
+def test_lm_head_scalar_order_pinned(orc):
+    # The scalar head (poly/transformer.go:681-687, dotTileGo in
+    # poly/simd/dot.go:14-21) is one sequential fp64 sum per logit: equal bit
+    # for bit to the same loop in Python floats (fp64), ragged widths included.
+    for V, H in [(5, 1), (7, 13), (9, 37), (4, 300)]:
+        table = orc.normal_f32(V * H, 40 + H) * np.float32(0.3)
+        hidden = orc.normal_f32(H, 50 + H)
+        got = orc.lm_head(hidden, table, simd=False)
+        for v in range(V):
+            s = 0.0
+            for d in range(H):
+                s += float(hidden[d]) * float(table[v * H + d])
+            assert got[v] == np.float32(s), (V, H, v)
+    # A row whose two orders differ: x = 2^30 everywhere, w = (1, 1, -1, 0...)
+    # scaled so the products are 2^60, 1, -2^60.  In order the 1 is absorbed
+    # (2^60 + 1 rounds to 2^60) and the sum is 0; DotTile keeps the three in
+    # separate lanes and returns 1.
+    H = 16
+    hidden = np.full(H, 2.0 ** 30, np.float32)
+    row = np.zeros(H, np.float32)
+    row[0], row[1], row[2] = 2.0 ** 30, 2.0 ** -30, -(2.0 ** 30)
+    assert orc.lm_head(hidden, row, simd=False)[0] == 0.0
+    assert orc.lm_head(hidden, row, simd=True)[0] == 1.0
