@@ -393,6 +393,338 @@ __global__ __launch_bounds__(256, 2) void gemm32_kernel(MatArgs p, GemmGrid gg) 
     }
 }
 
+// ------------------------------------------------------------------------
+// gemm64: the 64-token tile with its activation stages copied global -> LDS
+// by the memory units (buffer_load ... lds, 16 bytes a lane), so no VGPRs
+// stage them and the A-operand reads can run ahead of the MFMAs at three
+// workgroups per CU.  Three stage buffers: stage s + 2 is copied (and its
+// weight words loaded into the third register set) while stage s is
+// computed, and one barrier per stage both publishes stage s + 1 and frees
+// the buffer of stage s.  Each wave waits for its own copies (vmcnt) before
+// that barrier; a bare s_barrier is used because __syncthreads' release
+// fence would wait for every outstanding copy.
+// Stage buffer layout: 64 rows x 16 chunks of 16 bytes, row R at R*256, its
+// logical chunk ch at physical chunk ch ^ (R & 15), so the 8 (or 16) rows a
+// group of lanes reads in one MFMA step fall in distinct banks; the copies
+// gather each row's chunks in that order (each copy instruction still reads
+// whole 256-byte row segments).
+// Weights, tile order, split K and per-token constants are as in gemm32.
+// The epilogue stores straight from the accumulators: per instruction the
+// two half-waves write 128 contiguous bytes of two rows.
+// ------------------------------------------------------------------------
+
+constexpr int kG64Stage = 64 * 256;  // bytes of one activation stage
+#ifndef LAMD_G64_AHEAD
+#define LAMD_G64_AHEAD 2
+#endif
+
+// The three stage buffers are distinct arrays and these helpers take
+// restrict pointers, so the compiler's wait before an LDS read covers only
+// the copies into the buffer being read.
+__device__ __forceinline__ void g64_copy(__amdgpu_buffer_rsrc_t r, int8_t* __restrict__ dst, int voff,
+                                         int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff,
+                                             soff, 0, 0);
+}
+__device__ __forceinline__ v4i g64_read(const int8_t* __restrict__ src, int off) {
+    return *(const v4i*)(src + off);
+}
+// s_waitcnt vmcnt(N) lgkmcnt(0): at most N vector-memory operations of this
+// wave outstanding (its older stage copies have landed in LDS) and none of
+// its LDS operations (its reads of the buffer that the barrier after this
+// wait hands to the next copy have returned).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
+template <int NMAT, int EPI>
+__global__ __launch_bounds__(256, 2) void gemm64_kernel(MatArgs p, GemmGrid gg) {
+    constexpr int NJ = 2 / NMAT;
+    constexpr int MI = 2;
+    constexpr int BM = 64;
+    constexpr int NA = 4;     // copies per thread per stage
+    constexpr int NSTEP = 8;  // MFMA K steps per 256-column stage
+    constexpr int NB = NMAT * NJ * 2;  // weight loads per thread per stage
+    __shared__ __align__(16) int8_t As0[kG64Stage];
+    __shared__ __align__(16) int8_t As1[kG64Stage];
+    __shared__ __align__(16) int8_t As2[kG64Stage];
+    __shared__ int s_last;
+    __shared__ double s_os0[BM], s_os1[NMAT == 2 ? BM : 1];
+    __shared__ int s_xs[BM];
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int wn = wave;
+    const int l32 = lane & 31, h = lane >> 5;
+    const int M = p.e.m;
+    const int ktiles = p.ktiles;
+    const int S = gg.ksplit;
+
+    const int total = gg.mtiles * gg.ngroups * S;
+    const int per_xcd = (total + kXcds - 1) / kXcds;
+    const int linear = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+    if (linear >= total) return;
+    const int tile = linear / S;
+    const int split = linear - tile * S;
+    int mt, ng;
+    if (gg.group > 0) {
+        const int per_group = gg.group * gg.ngroups;
+        const int g0 = tile / per_group;
+        const int first = g0 * gg.group;
+        const int gsz = min(gg.mtiles - first, gg.group);
+        const int in = tile - g0 * per_group;
+        mt = first + in % gsz;
+        ng = in / gsz;
+    } else {
+        mt = tile / gg.ngroups;
+        ng = tile % gg.ngroups;
+    }
+    const int st0 = split * gg.sps;
+    const int st1 = min(st0 + gg.sps, ktiles);
+    const int last = st1 - 1;
+    const int m_wg = mt * BM;
+    const int nb0 = (ng * 4 + wn) * NJ;  // wave's first 32-row weight block
+    for (int t = tid; t < BM; t += 256) {
+        const int tok = min(m_wg + t, M - 1);
+        const RowScale rs = row_scale(p.e, p.e.amax[tok], p.e.xsum[tok]);
+        s_os0[t] = rs.os0;
+        if (NMAT == 2) s_os1[t] = rs.os1;
+        s_xs[t] = rs.xs;
+    }
+
+    const __amdgpu_buffer_rsrc_t wres0 =
+        __builtin_amdgcn_make_buffer_rsrc((void*)p.w0, 0, 0x7fffffff, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t wres1 =
+        __builtin_amdgcn_make_buffer_rsrc((void*)p.w1, 0, 0x7fffffff, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t ares =
+        __builtin_amdgcn_make_buffer_rsrc((void*)p.xq, 0, 0x7fffffff, kBufferWord3);
+    int woff[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int nt = min(2 * (nb0 + j) + ((lane >> 4) & 1), p.ntiles - 1);
+        woff[j] = (nt * ktiles * 64 + (lane & 15) + 16 * h) * 16;
+    }
+    // copy c of this lane fills physical chunk P = 256c + 64*wave + lane of a
+    // stage buffer: row P/16, physical chunk P%16 = logical chunk
+    // (P%16) ^ (row%16) of that token row
+    int aoff_g[NA];
+#pragma unroll
+    for (int c = 0; c < NA; ++c) {
+        const int P = 256 * c + 64 * wave + lane;
+        const int r = P >> 4;
+        const int lc = (P & 15) ^ (r & 15);
+        aoff_g[c] = min(m_wg + r, M - 1) * p.ldq + lc * 16;
+    }
+    auto issue = [&](int8_t* buf, int stage, uint32_t (&b)[NMAT][NJ][2][4]) {
+#pragma unroll
+        for (int c = 0; c < NA; ++c) g64_copy(ares, buf + c * 4096 + wave * 1024, aoff_g[c], stage * 256);
+#pragma unroll
+        for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const __amdgpu_buffer_rsrc_t r = mat == 0 ? wres0 : wres1;
+                    const uint4 w = __builtin_bit_cast(
+                        uint4, __builtin_amdgcn_raw_buffer_load_b128(r, woff[j] + 512 * u, stage * 1024, 0));
+                    b[mat][j][u][0] = w.x;
+                    b[mat][j][u][1] = w.y;
+                    b[mat][j][u][2] = w.z;
+                    b[mat][j][u][3] = w.w;
+                }
+    };
+
+    v16i acc[NMAT][MI][NJ];
+#pragma unroll
+    for (int a = 0; a < NMAT; ++a)
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) acc[a][i][j] = v16i{};
+
+    // lane's A rows l32 and 32 + l32 (immediate +8192); step with chunk pair
+    // (c0, c0 + 1) reads logical chunk c0 + h = c0 ^ h at physical chunk
+    // c0 ^ h ^ (l32 & 15)
+    const int abase = l32 * 256 + ((h ^ (l32 & 15)) << 4);
+    auto compute = [&](const int8_t* buf, const uint32_t (&bw)[NMAT][NJ][2][4]) {
+#pragma unroll
+        for (int idx = 0; idx < NSTEP; ++idx) {
+            const int hh = idx >> 2, q = idx & 3;
+            const int c0 = hh * 8 + (q & 1) * 4 + (q >> 1) * 2;
+            const int off = abase ^ (c0 << 4);
+            v4i a[MI];
+#pragma unroll
+            for (int i = 0; i < MI; ++i) a[i] = g64_read(buf, off + i * 8192);
+            v4i b[NMAT][NJ];
+#pragma unroll
+            for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) b[mat][j] = unpack_codes(bw[mat][j][q >> 1][2 * hh + (q & 1)]);
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) acc[mat][i][j] = mfma32_i8(a[i], b[mat][j], acc[mat][i][j]);
+        }
+    };
+
+    // Instruction order of one region between barriers: stage s+2's copies
+    // and weight loads first, the A reads of a step LAMD_G64_AHEAD steps
+    // before its MFMAs, each MFMA followed by a share of the next step's
+    // unpack.
+    constexpr int NMF = MI * NJ * NMAT;         // MFMAs per step
+    constexpr int NUP = NMAT * NJ * 7;          // unpack VALU per step
+    constexpr int VPM = (NUP + NMF - 1) / NMF;  // VALU per MFMA slot
+    auto region_order = [&]() {
+        __builtin_amdgcn_sched_group_barrier(0x020, NA + NB, 0);
+#pragma unroll
+        for (int k = 0; k < LAMD_G64_AHEAD; ++k) __builtin_amdgcn_sched_group_barrier(0x100, MI, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, NUP, 0);
+#pragma unroll
+        for (int idx = 0; idx < NSTEP; ++idx) {
+#pragma unroll
+            for (int m = 0; m < NMF; ++m) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
+            }
+            if (idx + LAMD_G64_AHEAD < NSTEP) __builtin_amdgcn_sched_group_barrier(0x100, MI, 0);
+        }
+    };
+    // Vector-memory operations issued after stage s's copies when the wait
+    // for them is reached: stage s's weight loads and stage s+1's copies and
+    // weight loads.
+    constexpr int kAfter = NB + NA + NB;
+    uint32_t bw0[NMAT][NJ][2][4], bw1[NMAT][NJ][2][4], bw2[NMAT][NJ][2][4];
+    issue(As0, st0, bw0);
+    issue(As1, min(st0 + 1, last), bw1);
+    wait_vm_lgkm0<kAfter>();  // (lgkmcnt also covers the per-token constants)
+    __builtin_amdgcn_s_barrier();
+    int s = st0;
+    for (; s + 2 < st1; s += 3) {
+        issue(As2, min(s + 2, last), bw2);
+        compute(As0, bw0);
+        region_order();
+        wait_vm_lgkm0<kAfter>();
+        __builtin_amdgcn_s_barrier();
+        issue(As0, min(s + 3, last), bw0);
+        compute(As1, bw1);
+        region_order();
+        wait_vm_lgkm0<kAfter>();
+        __builtin_amdgcn_s_barrier();
+        issue(As1, min(s + 4, last), bw1);
+        compute(As2, bw2);
+        region_order();
+        wait_vm_lgkm0<kAfter>();
+        __builtin_amdgcn_s_barrier();
+    }
+    if (s < st1) {
+        compute(As0, bw0);
+        if (s + 1 < st1) {
+            wait_vm_lgkm0<NB>();  // stage s+1's copies (only its weight loads may remain)
+            __builtin_amdgcn_s_barrier();
+            compute(As1, bw1);
+        }
+    }
+    wait_vm_lgkm0<0>();  // no copy may still be writing LDS when the workgroup ends
+
+    if (S > 1) {
+        int32_t* mine = gg.part + (size_t)linear * kSplitSlotInts;
+#pragma unroll
+        for (int a = 0; a < NMAT; ++a)
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v)
+                        __hip_atomic_store(&mine[(((a * MI + i) * NJ + j) * 16 + v) * 256 + tid], acc[a][i][j][v],
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) {
+            s_last = __hip_atomic_fetch_add(&gg.ctr[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                     (unsigned)(S - 1);
+        }
+        __syncthreads();
+        if (!s_last) return;
+        for (int o = 0; o < S; ++o) {
+            if (o == split) continue;
+            const int32_t* src = gg.part + (size_t)(tile * S + o) * kSplitSlotInts;
+#pragma unroll
+            for (int a = 0; a < NMAT; ++a)
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) {
+                        v16i t;
+#pragma unroll
+                        for (int v = 0; v < 16; ++v)
+                            t[v] = __hip_atomic_load(&src[(((a * MI + i) * NJ + j) * 16 + v) * 256 + tid],
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        acc[a][i][j] += t;
+                    }
+        }
+        if (tid == 0) __hip_atomic_store(&gg.ctr[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    static_assert(NMAT * MI * NJ * 16 * 256 == kSplitSlotInts, "a split slot holds one 64-token tile");
+
+    // Epilogue from the accumulators: value v of block (i, j) is token row
+    // 32i + 8(v/4) + 4h + v%4, output column (nb0 + j)*32 + l32.  Residual
+    // loads of four rows are issued before their stores.
+    float bias0[NJ], bias1 = 0.0f;
+    bool ncol[NJ];
+    int ncl[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int n = (nb0 + j) * 32 + l32;
+        ncol[j] = n < p.e.n;
+        ncl[j] = min(n, p.e.n - 1);
+        bias0[j] = EPI && p.e.bias0 ? p.e.bias0[ncl[j]] : 0.0f;
+    }
+    if (EPI && NMAT == 2 && p.e.bias1) bias1 = p.e.bias1[ncl[0]];
+    const bool has_res = EPI == 1 + EPI_DENSE && p.e.residual;
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            float res[4][NJ];
+            if (has_res) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) {
+                        const int tok = min(m_wg + 32 * i + 8 * g + 4 * h + u, M - 1);
+                        res[u][j] = p.e.residual[(size_t)tok * p.e.ldo + ncl[j]];
+                    }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int t = 32 * i + 8 * g + 4 * h + u;
+                const int tok = m_wg + t;
+                if (tok >= M) continue;
+                const double os0 = s_os0[t];
+                const int xs = s_xs[t];
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    if (!ncol[j]) continue;
+                    const int n = (nb0 + j) * 32 + l32;
+                    const int raw0 = acc[0][i][j][4 * g + u];
+                    if (EPI == 0) {
+                        __builtin_nontemporal_store((float)((double)(raw0 - xs) * os0),
+                                                    &p.e.out[(size_t)tok * p.e.ldo + n]);
+                    } else {
+                        const int raw1 = NMAT == 2 ? acc[NMAT - 1][i][j][4 * g + u] : raw0;
+                        epilogue_store_pre<EPI - 1>(p.e, tok, n, raw0, raw1, os0, NMAT == 2 ? s_os1[t] : 0.0,
+                                                    xs, bias0[j], bias1, has_res ? res[u][j] : 0.0f);
+                    }
+                }
+            }
+        }
+}
+
 // Tile height and split of a launch (measured on MI355X at both BitNet-2B FFN
 // shapes, M = 65 .. 16384): 64-token tiles beat 128-token tiles at every M
 // (three workgroups per CU instead of two hide more load latency).  Splitting
@@ -452,7 +784,11 @@ static hipError_t launch_gemm32(const MatArgs& p, const GemmPlan& pl, int device
     gg.ctr = ws.ctr;
     const int total = gg.mtiles * gg.ngroups * gg.ksplit;
     const int grid = ceil_div(total, kXcds) * kXcds;
-    hipLaunchKernelGGL((gemm32_kernel<NMAT, EPI, MI>), dim3(grid), dim3(256), 0, s, p, gg);
+    if (MI == 2) {
+        hipLaunchKernelGGL((gemm64_kernel<NMAT, EPI>), dim3(grid), dim3(256), 0, s, p, gg);
+    } else {
+        hipLaunchKernelGGL((gemm32_kernel<NMAT, EPI, MI>), dim3(grid), dim3(256), 0, s, p, gg);
+    }
     return hipGetLastError();
 }
 
