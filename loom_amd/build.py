@@ -29,6 +29,10 @@ ARCH = "gfx950"
 # -ffp-contract=off: every fp64 rescale / norm expression rounds after each
 # operation, in the reference's order (no fused multiply-add).
 # -packed-fp32-ops: keep the compiler from emitting packed fp32 VALU ops.
+# -amdgpu-mfma-vgpr-form: MFMA sources and results in VGPRs.  Otherwise the
+# compiler places some accumulators in AGPRs and copies them to and from VGPRs
+# around every MFMA of a loop; the AGPRs also count against occupancy (the fp64
+# prefill attention runs 3 waves per SIMD instead of 2 with this option).
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -37,6 +41,7 @@ HIPCC_FLAGS = [
     "-ffp-contract=off",
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I", os.path.join(ROOT, "include"),
     "-I", CSRC,
 ]
