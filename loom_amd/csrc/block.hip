@@ -687,7 +687,12 @@ __global__ __launch_bounds__(256) void attn_tile_mfma_kernel(const double* __res
     constexpr int DT = HD / 32;  // value tiles (16 columns) per wave
     constexpr int F4 = kChunkP * HD / 4 / 256;
     static_assert(F4 >= 1 && kChunkP * HD == F4 * 4 * 256, "chunk geometry");
-    __shared__ float kv[kChunkP][HD + 1];
+    // The K or V chunk, converted to fp64 once as it is staged.  K rows are
+    // KP doubles apart (pass 1 reads 16 rows x 4 columns: 2*KP = 4 mod 64
+    // banks), V rows VP (pass 2 reads 4 rows x 16 columns: 2*VP = 32 mod 64),
+    // so both read patterns fill the banks without conflicts.
+    constexpr int KP = HD + 2, VP = HD + 16;
+    __shared__ double kvd[kChunkP * VP];
     __shared__ double pt[kTileQ][kChunkP + 1];
     __shared__ double mxs[2][kTileQ];
     __shared__ double ess[kTileQ];
@@ -719,15 +724,15 @@ __global__ __launch_bounds__(256) void attn_tile_mfma_kernel(const double* __res
             rk[j] = *(const float4*)(src + (size_t)k * kv_dim + e % HD);
         }
     };
-    auto store = [&]() {
+    auto store = [&](int pitch) {
 #pragma unroll
         for (int j = 0; j < F4; ++j) {
             const int e = (tid + j * 256) * 4;
-            float* d = &kv[e / HD][e % HD];
-            d[0] = rk[j].x;
-            d[1] = rk[j].y;
-            d[2] = rk[j].z;
-            d[3] = rk[j].w;
+            double* d = &kvd[(e / HD) * pitch + e % HD];
+            d[0] = (double)rk[j].x;
+            d[1] = (double)rk[j].y;
+            d[2] = (double)rk[j].z;
+            d[3] = (double)rk[j].w;
         }
     };
     const int qt = wave >> 1, kt = wave & 1;
@@ -753,13 +758,13 @@ __global__ __launch_bounds__(256) void attn_tile_mfma_kernel(const double* __res
     load(kb, 0);
     for (int c = 0; c < nch; ++c) {
         __syncthreads();
-        store();
+        store(KP);
         load(kb, c + 1);
         __syncthreads();
         v4d acc = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
-            const double bk = (double)kv[16 * kt + lr][4 * m + lg];
+            const double bk = kvd[(16 * kt + lr) * KP + 4 * m + lg];
             acc = __builtin_amdgcn_mfma_f64_16x16x4f64(qa[m], bk, acc, 0, 0, 0);
         }
         const int k = c * kChunkP + 16 * kt + lr;
@@ -804,7 +809,7 @@ __global__ __launch_bounds__(256) void attn_tile_mfma_kernel(const double* __res
     const int dt0 = (wave & 1) * DT;
     for (int c = 0; c < nch; ++c) {
         __syncthreads();  // previous chunk's values and probabilities read
-        store();          // V chunk c
+        store(VP);        // V chunk c
         const int k = c * kChunkP + 16 * kt + lr;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
@@ -823,7 +828,7 @@ __global__ __launch_bounds__(256) void attn_tile_mfma_kernel(const double* __res
             const double a = pt[16 * qt + lr][4 * m + lg];
 #pragma unroll
             for (int t = 0; t < DT; ++t) {
-                const double bv = (double)kv[4 * m + lg][16 * (dt0 + t) + lr];
+                const double bv = kvd[(4 * m + lg) * VP + 16 * (dt0 + t) + lr];
                 o[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, bv, o[t], 0, 0, 0);
             }
         }
