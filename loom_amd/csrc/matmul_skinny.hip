@@ -334,6 +334,16 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
         }
     }
 
+    // Pre-quantized rows: the epilogue's per-token amax and sum(xq) of the
+    // first output each thread finishes are loaded now, so the epilogue does
+    // not start with a memory round trip after the reduction.
+    float am_first = 0.0f;
+    int xs_first = 0;
+    if (!FUSEQ && tid < M * 16) {
+        am_first = p.e.amax[tid >> 4];
+        xs_first = p.e.xsum[tid >> 4];
+    }
+
     v4i acc[NMAT][MSUB];
 #pragma unroll
     for (int a = 0; a < NMAT; ++a)
@@ -421,6 +431,9 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
             am = __uint_as_float(amax_bits[tok]);
             if (am < 1e-5f) am = 1e-5f;
             xs = xsum_s[tok];
+        } else if (idx == tid) {
+            am = am_first;
+            xs = xs_first;
         } else {
             am = p.e.amax[tok];
             xs = p.e.xsum[tok];
