@@ -443,6 +443,151 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
 }
 
 // ------------------------------------------------------------------------
+// skinny_nt: 16 < M <= 64 on pre-quantized rows.  The same per-wave K split
+// and 16x16x64 MFMAs as skinny_kernel, but a workgroup owns NT adjacent
+// 16-row weight tiles, so the activation operands a wave loads for a K tile
+// serve NT tiles.  Every workgroup reads all M rows, and per 256-column K
+// tile those are M x 256 bytes against 1 KiB of one tile's weights, so at
+// these M the activation bytes pulled into the CUs dominate; they drop by NT.
+// ------------------------------------------------------------------------
+template <int NMAT, int MSUB, int WAVES, int NT>
+__global__ __launch_bounds__(WAVES * 64) void skinny_nt_kernel(MatArgs p) {
+    constexpr int T = WAVES * 64;
+    constexpr int U = 4 / MSUB;  // K tiles per batch per wave
+    __shared__ int red[NT][NMAT][MSUB * 16][16];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int r = lane & 15;
+    const int g = lane >> 4;
+    const int M = p.e.m;
+    const int ktiles = p.ktiles;
+    const int nt0 = blockIdx.x * NT;
+    // tiles past the last one read the last tile and store nothing
+    size_t tile0[NT];
+#pragma unroll
+    for (int q = 0; q < NT; ++q) tile0[q] = (size_t)min(nt0 + q, p.ntiles - 1) * ktiles * 64 + lane;
+
+    uint4 wv[NT][NMAT][U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int kt = wave + u * WAVES;
+        if (kt < ktiles) {
+#pragma unroll
+            for (int q = 0; q < NT; ++q) {
+                wv[q][0][u] = p.w0[tile0[q] + (size_t)kt * 64];
+                if (NMAT == 2) wv[q][NMAT - 1][u] = p.w1[tile0[q] + (size_t)kt * 64];
+            }
+        }
+    }
+    // the epilogue constants of the first output this thread finishes
+    const int first_tok = (tid % (M * 16)) >> 4;
+    float am_first = 0.0f;
+    int xs_first = 0;
+    if (tid < NT * M * 16) {
+        am_first = p.e.amax[first_tok];
+        xs_first = p.e.xsum[first_tok];
+    }
+    for (int i = tid; i < NT * NMAT * MSUB * 16 * 16; i += T) (&red[0][0][0][0])[i] = 0;
+
+    v4i acc[NT][NMAT][MSUB];
+#pragma unroll
+    for (int q = 0; q < NT; ++q)
+#pragma unroll
+        for (int a = 0; a < NMAT; ++a)
+#pragma unroll
+            for (int ms = 0; ms < MSUB; ++ms) acc[q][a][ms] = v4i{0, 0, 0, 0};
+
+    const int8_t* xbase[MSUB];
+    bool xval[MSUB];
+#pragma unroll
+    for (int ms = 0; ms < MSUB; ++ms) {
+        const int row = ms * 16 + r;
+        xval[ms] = row < M;
+        xbase[ms] = p.xq + (size_t)(xval[ms] ? row : 0) * p.ldq + g * 16;
+    }
+
+    for (int kb = wave; kb < ktiles; kb += WAVES * U) {
+        uint4 wn[NT][NMAT][U];
+        const int kn = kb + WAVES * U;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int kt = kn + u * WAVES;
+            if (kt < ktiles) {
+#pragma unroll
+                for (int q = 0; q < NT; ++q) {
+                    wn[q][0][u] = p.w0[tile0[q] + (size_t)kt * 64];
+                    if (NMAT == 2) wn[q][NMAT - 1][u] = p.w1[tile0[q] + (size_t)kt * 64];
+                }
+            }
+        }
+        v4i a[MSUB][U][4];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int kt = kb + u * WAVES;
+            if (kt < ktiles) {
+#pragma unroll
+                for (int ms = 0; ms < MSUB; ++ms) {
+                    const int8_t* xp = xbase[ms] + (size_t)kt * kTileCols;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        a[ms][u][t] = xval[ms] ? *(const v4i*)(xp + 64 * t) : v4i{0, 0, 0, 0};
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int kt = kb + u * WAVES;
+            if (kt < ktiles) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int q = 0; q < NT; ++q)
+#pragma unroll
+                        for (int mat = 0; mat < NMAT; ++mat) {
+                            const v4i b = unpack_codes(word_of(wv[q][mat][u], t));
+#pragma unroll
+                            for (int ms = 0; ms < MSUB; ++ms)
+                                acc[q][mat][ms] = mfma_i8(a[ms][u][t], b, acc[q][mat][ms]);
+                        }
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < NT; ++q)
+#pragma unroll
+            for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+                for (int u = 0; u < U; ++u) wv[q][mat][u] = wn[q][mat][u];
+    }
+
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < NT; ++q)
+#pragma unroll
+        for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+            for (int ms = 0; ms < MSUB; ++ms)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int tok = ms * 16 + 4 * g + v;
+                    if (tok < M) atomicAdd(&red[q][mat][tok][r], acc[q][mat][ms][v]);
+                }
+    __syncthreads();
+
+    for (int idx = tid; idx < NT * M * 16; idx += T) {
+        const int q = idx / (M * 16);
+        const int rem = idx - q * (M * 16);
+        const int tok = rem >> 4;
+        const int col = rem & 15;
+        const int n = (nt0 + q) * kTileRows + col;
+        if (nt0 + q >= p.ntiles || n >= p.e.n) continue;
+        const float am = idx == tid ? am_first : p.e.amax[tok];
+        const int xs = idx == tid ? xs_first : p.e.xsum[tok];
+        epilogue_store(p.e, tok, n, red[q][0][tok][col], red[q][NMAT - 1][tok][col], row_scale(p.e, am, xs));
+    }
+}
+
+// ------------------------------------------------------------------------
 // dispatch
 // ------------------------------------------------------------------------
 
@@ -516,6 +661,43 @@ static hipError_t launch_skinny(const MatArgs& p, hipStream_t s) {
     return hipGetLastError();
 }
 
+// 16 < M <= 64 on pre-quantized rows: tiles per workgroup.  Two tiles pay
+// for short K with many tiles (measured at M = 17..64: the up shape, K = 2560,
+// 13.4 -> 10.9 us at M = 64); with long K (the down shape, 27 K tiles) the
+// halved workgroup count lengthens each wave's serial K loop and one tile is
+// faster.  LOOM_AMD_SKINNY_NT = 1, 2 or 4 overrides (1 = skinny_kernel).
+static int skinny_nt(int ntiles, int ktiles) {
+    const char* v = getenv("LOOM_AMD_SKINNY_NT");
+    const int nt = v && *v ? atoi(v) : 0;
+    if (nt == 1 || nt == 2 || nt == 4) return nt;
+    return ktiles <= 16 && ntiles >= 256 ? 2 : 1;
+}
+
+// At most 8 waves: the NT-tile accumulators leave too few VGPRs for 1024
+// threads.
+template <int NMAT, int MSUB, int NT>
+static hipError_t launch_skinny_nt(const MatArgs& p, hipStream_t s) {
+    const int groups = ceil_div(p.ntiles, NT);
+    const int w = pick_waves(groups, p.ktiles, 8);
+    const dim3 grid(groups);
+    switch (w) {
+        case 1: hipLaunchKernelGGL((skinny_nt_kernel<NMAT, MSUB, 1, NT>), grid, dim3(64), 0, s, p); break;
+        case 2: hipLaunchKernelGGL((skinny_nt_kernel<NMAT, MSUB, 2, NT>), grid, dim3(128), 0, s, p); break;
+        case 4: hipLaunchKernelGGL((skinny_nt_kernel<NMAT, MSUB, 4, NT>), grid, dim3(256), 0, s, p); break;
+        default: hipLaunchKernelGGL((skinny_nt_kernel<NMAT, MSUB, 8, NT>), grid, dim3(512), 0, s, p); break;
+    }
+    return hipGetLastError();
+}
+
+// (four tiles of both SwiGLU matrices do not fit the register file)
+template <int NMAT, int MSUB>
+static hipError_t launch_small_m(const MatArgs& p, hipStream_t s) {
+    const int nt = skinny_nt(p.ntiles, p.ktiles);
+    if (nt == 4 && NMAT == 1) return launch_skinny_nt<NMAT, MSUB, 4>(p, s);
+    if (nt >= 2) return launch_skinny_nt<NMAT, MSUB, 2>(p, s);
+    return launch_skinny<NMAT, MSUB, false>(p, s);
+}
+
 const char* kernel_variant(int m) {
     if (m <= kFusedMaxRows) return "skinny_m16_fusedq";
     if (m <= 16) return "skinny_m16";
@@ -559,8 +741,8 @@ hipError_t launch_matmul(const Matrix* w0, const Matrix* w1, const QuantAct& a, 
     p.e.xsum = a.xsum;
     const bool two = epi.kind == EPI_SWIGLU;
     if (m <= 16) return two ? launch_skinny<2, 1, false>(p, s) : launch_skinny<1, 1, false>(p, s);
-    if (m <= 32) return two ? launch_skinny<2, 2, false>(p, s) : launch_skinny<1, 2, false>(p, s);
-    if (m <= 64) return two ? launch_skinny<2, 4, false>(p, s) : launch_skinny<1, 4, false>(p, s);
+    if (m <= 32) return two ? launch_small_m<2, 2>(p, s) : launch_small_m<1, 2>(p, s);
+    if (m <= 64) return two ? launch_small_m<2, 4>(p, s) : launch_small_m<1, 4>(p, s);
     return launch_gemm(p, two, w0->device, s);
 }
 

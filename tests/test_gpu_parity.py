@@ -498,6 +498,26 @@ def test_gemm_forced_plans(orc, torch_dev, bn, monkeypatch, tile, split):
     _check_dense(orc, torch_dev, bn, m, x)
 
 
+@pytest.mark.parametrize("nt", ["1", "2", "4"])
+@pytest.mark.parametrize("rows,cols,M", [(6912, 2560, 64), (2560, 6912, 40), (1000, 2570, 17),
+                                         (6900, 2560, 33)])
+def test_small_m_tiles_per_workgroup(orc, torch_dev, bn, monkeypatch, nt, rows, cols, M):
+    # 16 < M <= 64 with one, two or four 16-row tiles per workgroup (a ragged
+    # last group included): int32 accumulators and fp32 outputs bit-exact
+    monkeypatch.setenv("LOOM_AMD_SKINNY_NT", nt)
+    m = orc.random_matrix(rows, cols, seed=rows + M)
+    x = orc.normal_f32(M * cols, seed=M + 7).reshape(M, cols)
+    _check_dense(orc, torch_dev, bn, m, x)
+
+
+@pytest.mark.parametrize("nt", ["1", "2"])
+def test_small_m_swiglu_tiles_per_workgroup(orc, torch_dev, bn, monkeypatch, nt):
+    # gate|up with M = 48 and one or two tiles per workgroup
+    monkeypatch.setenv("LOOM_AMD_SKINNY_NT", nt)
+    _swiglu_case(orc, torch_dev, bn, hidden=2560, inter=6912, M=48, seed=131, norm="strict",
+                 with_norm_w=True)
+
+
 def test_gemm_odd_stage_count_repeatable(orc, torch_dev, bn):
     # K = 6912 gives an odd number of K stages (a one-stage tail before the
     # epilogue reuses the stage buffers): many back-to-back launches must all
