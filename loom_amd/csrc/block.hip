@@ -474,6 +474,7 @@ __global__ __launch_bounds__(256) void attention_kernel(const double* __restrict
 // multiply-add of the dot and value chains into one rounding.  Positions past
 // a query's own position are skipped (never added).
 constexpr int kTileQ = 32;
+constexpr int kAttnFastQt = 2;  // 16-query tiles per workgroup of the fast prefill kernel
 constexpr int kChunkP = 32;
 
 template <int HD>
@@ -675,7 +676,7 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict
 // tile w/2 and HD/32 tiles of 16 value columns.
 typedef double v4d __attribute__((ext_vector_type(4)));
 
-template <int HD>
+template <int HD, int QT>
 __global__ __launch_bounds__(256) void attn_tile_mfma_kernel(const double* __restrict__ q,
                                                              const float* __restrict__ cache_k,
                                                              const float* __restrict__ cache_v,
@@ -683,9 +684,16 @@ __global__ __launch_bounds__(256) void attn_tile_mfma_kernel(const double* __res
                                                              int span, int heads, int kv_heads,
                                                              int seq, double* __restrict__ sc_all,
                                                              double* __restrict__ out) {
-    constexpr int NM = HD / 4;   // score MFMAs along d
-    constexpr int DT = HD / 32;  // value tiles (16 columns) per wave
+    // QT 16-query tiles per workgroup; WPQ waves share one query tile: for
+    // the scores each takes KTW of the chunk's two 16-position tiles, for the
+    // values DT of the HD/16 value tiles.
+    constexpr int TQ = 16 * QT;
+    constexpr int WPQ = 4 / QT;
+    constexpr int KTW = 2 / WPQ;
+    constexpr int NM = HD / 4;         // score MFMAs along d
+    constexpr int DT = HD / 16 / WPQ;  // value tiles (16 columns) per wave
     constexpr int F4 = kChunkP * HD / 4 / 256;
+    static_assert(QT == 2 || QT == 4, "32 or 64 queries per workgroup");
     static_assert(F4 >= 1 && kChunkP * HD == F4 * 4 * 256, "chunk geometry");
     // The K or V chunk, converted to fp64 once as it is staged.  K rows are
     // KP doubles apart (pass 1 reads 16 rows x 4 columns: 2*KP = 4 mod 64
@@ -693,16 +701,15 @@ __global__ __launch_bounds__(256) void attn_tile_mfma_kernel(const double* __res
     // so both read patterns fill the banks without conflicts.
     constexpr int KP = HD + 2, VP = HD + 16;
     __shared__ double kvd[kChunkP * VP];
-    __shared__ double pt[kTileQ][kChunkP + 1];
-    __shared__ double mxs[2][kTileQ];
-    __shared__ double ess[kTileQ];
+    __shared__ double pt[TQ][kChunkP + 1];
+    __shared__ double red[WPQ * TQ];  // the waves' row maxima, later the expSums
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lr = lane & 15, lg = lane >> 4;
     const int h = blockIdx.x;
     const int tile = gridDim.y - 1 - blockIdx.y;
     const int b = blockIdx.z;
-    const int s0 = tile * kTileQ;
-    const int nq = min(kTileQ, seq - s0);
+    const int s0 = tile * TQ;
+    const int nq = min(TQ, seq - s0);
     const int base = *pos0;
     const int q_dim = heads * HD, kv_dim = kv_heads * HD;
     const int kvh = h / (heads / kv_heads);
@@ -735,7 +742,7 @@ __global__ __launch_bounds__(256) void attn_tile_mfma_kernel(const double* __res
             d[3] = (double)rk[j].w;
         }
     };
-    const int qt = wave >> 1, kt = wave & 1;
+    const int qt = wave / WPQ, slot = wave % WPQ, kt0 = slot * KTW;
     // Q fragment: Q[16 qt + lr][4 m + lg]
     double qa[NM];
     {
@@ -745,7 +752,7 @@ __global__ __launch_bounds__(256) void attn_tile_mfma_kernel(const double* __res
         for (int m = 0; m < NM; ++m) qa[m] = qr < nq ? src[4 * m] : 0.0;
     }
     const double scale = 1.0 / sqrt((double)HD);
-    // this lane's score slots: rows qi(v) = 16 qt + 4 v + lg, position 16 kt + lr
+    // this lane's score slots: rows qi(v) = 16 qt + 4 v + lg, positions 16 kt + lr
     double* scr[4];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -761,19 +768,26 @@ __global__ __launch_bounds__(256) void attn_tile_mfma_kernel(const double* __res
         store(KP);
         load(kb, c + 1);
         __syncthreads();
-        v4d acc = {0.0, 0.0, 0.0, 0.0};
+        v4d acc[KTW];
 #pragma unroll
-        for (int m = 0; m < NM; ++m) {
-            const double bk = kvd[(16 * kt + lr) * KP + 4 * m + lg];
-            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(qa[m], bk, acc, 0, 0, 0);
-        }
-        const int k = c * kChunkP + 16 * kt + lr;
+        for (int kk = 0; kk < KTW; ++kk) acc[kk] = v4d{0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int qi = 16 * qt + 4 * v + lg;
-            const double sv = acc[v] * scale;
-            if (qi < nq && k < span) scr[v][k] = sv;
-            if (k <= base + s0 + qi && sv > mv[v]) mv[v] = sv;
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int kk = 0; kk < KTW; ++kk) {
+                const double bk = kvd[(16 * (kt0 + kk) + lr) * KP + 4 * m + lg];
+                acc[kk] = __builtin_amdgcn_mfma_f64_16x16x4f64(qa[m], bk, acc[kk], 0, 0, 0);
+            }
+#pragma unroll
+        for (int kk = 0; kk < KTW; ++kk) {
+            const int k = c * kChunkP + 16 * (kt0 + kk) + lr;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int qi = 16 * qt + 4 * v + lg;
+                const double sv = acc[kk][v] * scale;
+                if (qi < nq && k < span) scr[v][k] = sv;
+                if (k <= base + s0 + qi && sv > mv[v]) mv[v] = sv;
+            }
         }
     }
 #pragma unroll
@@ -783,43 +797,51 @@ __global__ __launch_bounds__(256) void attn_tile_mfma_kernel(const double* __res
             const double o = __shfl_xor(mv[v], off, 16);
             mv[v] = o > mv[v] ? o : mv[v];
         }
-        if (lr == 0) mxs[kt][16 * qt + 4 * v + lg] = mv[v];
+        if (lr == 0) red[slot * TQ + 16 * qt + 4 * v + lg] = mv[v];
     }
     __syncthreads();
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
         const int qi = 16 * qt + 4 * v + lg;
-        const double a = mxs[0][qi], c2 = mxs[1][qi];
-        mv[v] = c2 > a ? c2 : a;
+        double mm = red[qi];
+#pragma unroll
+        for (int w = 1; w < WPQ; ++w) mm = red[w * TQ + qi] > mm ? red[w * TQ + qi] : mm;
+        mv[v] = mm;
     }
 
     // ---- pass 2 ---------------------------------------------------------------
     v4d o[DT];
 #pragma unroll
     for (int t = 0; t < DT; ++t) o[t] = v4d{0.0, 0.0, 0.0, 0.0};
-    double es = 0.0;  // lane tid < kTileQ: query tid
-    double sv[4];
+    double es = 0.0;  // lane tid < TQ: query tid
+    double sv[KTW][4];
     auto load_scores = [&](int c) {
-        const int k = min(min(c, nch - 1) * kChunkP + 16 * kt + lr, span - 1);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) sv[v] = scr[v][k];
+        for (int kk = 0; kk < KTW; ++kk) {
+            const int k = min(min(c, nch - 1) * kChunkP + 16 * (kt0 + kk) + lr, span - 1);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) sv[kk][v] = scr[v][k];
+        }
     };
     load(vb, 0);
     load_scores(0);
-    const int dt0 = (wave & 1) * DT;
+    const int dt0 = slot * DT;
     for (int c = 0; c < nch; ++c) {
-        __syncthreads();  // previous chunk's values and probabilities read
+        __syncthreads();  // previous chunk's values and probabilities read (and the maxima)
         store(VP);        // V chunk c
-        const int k = c * kChunkP + 16 * kt + lr;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int qi = 16 * qt + 4 * v + lg;
-            pt[qi][16 * kt + lr] = k <= base + s0 + qi ? exp(sv[v] - mv[v]) : 0.0;
+        for (int kk = 0; kk < KTW; ++kk) {
+            const int k = c * kChunkP + 16 * (kt0 + kk) + lr;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int qi = 16 * qt + 4 * v + lg;
+                pt[qi][16 * (kt0 + kk) + lr] = k <= base + s0 + qi ? exp(sv[kk][v] - mv[v]) : 0.0;
+            }
         }
         load(vb, c + 1);
         load_scores(c + 1);
         __syncthreads();
-        if (tid < kTileQ) {
+        if (tid < TQ) {
 #pragma unroll 8
             for (int kk = 0; kk < kChunkP; ++kk) es += pt[tid][kk];
         }
@@ -833,13 +855,13 @@ __global__ __launch_bounds__(256) void attn_tile_mfma_kernel(const double* __res
             }
         }
     }
-    if (tid < kTileQ) ess[tid] = es;
+    if (tid < TQ) red[tid] = es;
     __syncthreads();
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
         const int qi = 16 * qt + 4 * v + lg;
         if (qi < nq) {
-            const double e = ess[qi];
+            const double e = red[qi];
             double* orow = out + (row0 + qi) * q_dim + (size_t)h * HD;
 #pragma unroll
             for (int t = 0; t < DT; ++t) orow[16 * (dt0 + t) + lr] = o[t][v] / e;
@@ -1632,21 +1654,31 @@ hipError_t launch_attention(const double* q, const float* cache_k, const float* 
 #define LAMD_TILE(HDV, F)                                                                          \
     hipLaunchKernelGGL((attn_tile_kernel<HDV, F>), grid, dim3(256), 0, s, q, cache_k, cache_v, pos0, \
                        msl, span, heads, kv_heads, seq, scratch, out)
+        // fast mode: 16-query tiles per workgroup (LOOM_AMD_ATTN_QT = 2 or 4)
+        const char* qtv = getenv("LOOM_AMD_ATTN_QT");
+        const int qt = qtv && atoi(qtv) == 2 ? 2 : qtv && atoi(qtv) == 4 ? 4 : kAttnFastQt;
+        const dim3 gridf(heads, ceil_div(seq, 16 * qt), batch);
+#define LAMD_FAST(HDV, QTV)                                                                          \
+    hipLaunchKernelGGL((attn_tile_mfma_kernel<HDV, QTV>), gridf, dim3(256), 0, s, q, cache_k, cache_v, \
+                       pos0, msl, span, heads, kv_heads, seq, scratch, out)
         if (hd == 128) {
             if (strict) {
                 LAMD_TILE(128, false);
+            } else if (qt == 4) {
+                LAMD_FAST(128, 4);
             } else {
-                hipLaunchKernelGGL(attn_tile_mfma_kernel<128>, grid, dim3(256), 0, s, q, cache_k,
-                                   cache_v, pos0, msl, span, heads, kv_heads, seq, scratch, out);
+                LAMD_FAST(128, 2);
             }
         } else {
             if (strict) {
                 LAMD_TILE(64, false);
+            } else if (qt == 4) {
+                LAMD_FAST(64, 4);
             } else {
-                hipLaunchKernelGGL(attn_tile_mfma_kernel<64>, grid, dim3(256), 0, s, q, cache_k,
-                                   cache_v, pos0, msl, span, heads, kv_heads, seq, scratch, out);
+                LAMD_FAST(64, 2);
             }
         }
+#undef LAMD_FAST
 #undef LAMD_TILE
         return hipGetLastError();
     }

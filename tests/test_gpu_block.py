@@ -336,6 +336,27 @@ def test_block_refuses_positions_past_ring(orc, torch_dev, tf):
         blk.forward(to_dev(torch, np.zeros((2, 3, SMALL.hidden), np.float32)))
 
 
+@pytest.mark.parametrize("hd,seq", [(128, 300), (64, 200)])
+def test_fast_prefill_attention_query_tiles_agree(orc, torch_dev, tf, monkeypatch, hd, seq):
+    # the fast prefill kernel with 32 or 64 queries per workgroup sums in the
+    # same order: identical bytes for the block output and its K/V caches,
+    # ragged last query tile included
+    torch = torch_dev
+    sh = Shape(hd * 4, 4, 2, hd, 512, 512)
+    w = Weights(orc, sh, seed=451)
+    x = orc.normal_f32(seq * sh.hidden, seed=452).reshape(seq, sh.hidden)
+    outs = []
+    for qt in ("2", "4"):
+        monkeypatch.setenv("LOOM_AMD_ATTN_QT", qt)
+        blk = tf.BitNetBlock(w.cfg(tf, norm="fast"), w.gpu(tf))
+        xd = to_dev(torch, x)
+        blk.forward(xd)
+        torch.cuda.synchronize()
+        outs.append(xd.cpu().numpy().tobytes())
+        blk.release()
+    assert outs[0] == outs[1]
+
+
 # ---------------------------------------------------------------- model / decode loop
 class Model:
     def __init__(self, orc, sh: Shape, layers: int, vocab: int, seed: int):
