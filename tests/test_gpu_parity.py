@@ -498,6 +498,16 @@ def test_gemm_forced_plans(orc, torch_dev, bn, monkeypatch, tile, split):
     _check_dense(orc, torch_dev, bn, m, x)
 
 
+@pytest.mark.parametrize("group", ["0", "3", "8"])
+def test_gemm_tile_order_groups(orc, torch_dev, bn, monkeypatch, group):
+    # the GEMM's tile order: weight-row group fastest (0), or groups of 3
+    # token tiles (the last group partial: 5 token tiles) or 8
+    monkeypatch.setenv("LOOM_AMD_GEMM_GROUP", group)
+    m = orc.random_matrix(6900, 2560, seed=61)
+    x = orc.normal_f32(300 * 2560, seed=62).reshape(300, 2560)
+    _check_dense(orc, torch_dev, bn, m, x)
+
+
 @pytest.mark.parametrize("nt", ["1", "2", "4"])
 @pytest.mark.parametrize("rows,cols,M", [(6912, 2560, 64), (2560, 6912, 40), (1000, 2570, 17),
                                          (6900, 2560, 33)])
