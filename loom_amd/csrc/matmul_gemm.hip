@@ -61,7 +61,8 @@ struct GemmGrid {
 };
 
 // ------------------------------------------------------------------------
-// gemm32: v_mfma_i32_32x32x32_i8, which issues int8 at twice the rate of the
+// gemm32 (launched for the 128-token tile, MI = 4; the 64-token tile runs
+// gemm64_kernel below): v_mfma_i32_32x32x32_i8, which issues int8 at twice the rate of the
 // 16x16x64 form on gfx950 (measured: 4.5 vs 2.5 POPS sustained).  256 threads
 // as 4 waves along N, two workgroups per CU; workgroup tile 128 tokens x
 // 256/NMAT weight rows per matrix, wave tile 128 tokens x 64/NMAT weight rows
@@ -784,7 +785,7 @@ static hipError_t launch_gemm32(const MatArgs& p, const GemmPlan& pl, int device
     gg.ctr = ws.ctr;
     const int total = gg.mtiles * gg.ngroups * gg.ksplit;
     const int grid = ceil_div(total, kXcds) * kXcds;
-    if (MI == 2) {
+    if constexpr (MI == 2) {
         hipLaunchKernelGGL((gemm64_kernel<NMAT, EPI>), dim3(grid), dim3(256), 0, s, p, gg);
     } else {
         hipLaunchKernelGGL((gemm32_kernel<NMAT, EPI, MI>), dim3(grid), dim3(256), 0, s, p, gg);
