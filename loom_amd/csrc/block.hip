@@ -166,7 +166,7 @@ hipError_t launch_rmsnorm_quant(const float* x, long ldx, int m, int n, const fl
 // K and V go to ring row pos % msl of the row's sequence slot (batch index);
 // when one call holds more than msl tokens only the last token of each ring
 // row is written (the reference writes them in order, so the last one
-// stays).  One thread per Q pair, K pair or V element.
+// stays).
 // ------------------------------------------------------------------------
 
 __device__ __forceinline__ void rope_angle(int pos, int d, int hd, double theta, double* c,
@@ -215,50 +215,50 @@ __device__ __forceinline__ float v_val(const int32_t* ar, double os, const float
     return v_val_v(ar[j], os, bv != nullptr, bv ? bv[j] : 0.0f);
 }
 
-__global__ void qkv_rope_kernel(const int32_t* __restrict__ acc, const float* __restrict__ amax,
-                                float sq, float sk, float sv, const float* __restrict__ bq,
-                                const float* __restrict__ bk, const float* __restrict__ bv,
-                                int batch, int seq, const int* __restrict__ pos0, int msl,
-                                int heads, int kv_heads, int hd, double theta,
-                                double* __restrict__ q, float* __restrict__ cache_k,
-                                float* __restrict__ cache_v) {
+// One workgroup per token row: the row's hd/2 rotation angles are computed
+// once into LDS (pos / theta^(2d/hd), cos, sin in fp64: the same values for
+// every Q and K head), then the workgroup's threads stride over the row's Q
+// pairs, K pairs and V elements.
+constexpr int kRopeMaxHalf = 128;  // head_dim <= 256
+
+__global__ __launch_bounds__(256) void qkv_rope_kernel(
+    const int32_t* __restrict__ acc, const float* __restrict__ amax, float sq, float sk, float sv,
+    const float* __restrict__ bq, const float* __restrict__ bk, const float* __restrict__ bv, int batch,
+    int seq, const int* __restrict__ pos0, int msl, int heads, int kv_heads, int hd, double theta,
+    double* __restrict__ q, float* __restrict__ cache_k, float* __restrict__ cache_v) {
+    __shared__ double rc[kRopeMaxHalf], rs[kRopeMaxHalf];
     const int half = hd >> 1;
     const int q_dim = heads * hd, kv_dim = kv_heads * hd;
     const int qp = heads * half, kp = kv_heads * half;
     const int per_row = qp + kp + kv_dim;
-    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (long)batch * seq * per_row) return;
-    const int row = (int)(idx / per_row);  // token row b*seq + s
-    const int r = (int)(idx % per_row);
+    const int row = blockIdx.x;  // token row b*seq + s
     const int b = row / seq, s = row % seq;
     const int base = *pos0;
     const int pos = base + s;
+    for (int d = threadIdx.x; d < half; d += blockDim.x) rope_angle(pos, d, hd, theta, &rc[d], &rs[d]);
+    __syncthreads();
     const int32_t* ar = acc + (size_t)row * (q_dim + 2 * kv_dim);
     const float am = amax[row];
+    const double osq = output_scale(sq, am), osk = output_scale(sk, am), osv = output_scale(sv, am);
     cache_k += (size_t)b * msl * kv_dim;
     cache_v += (size_t)b * msl * kv_dim;
     const bool latest = pos + msl >= base + seq;
-    if (r < qp) {
-        const int h = r / half, d = r % half;
-        const int j0 = h * hd + d, j1 = j0 + half;
-        double c, sn;
-        rope_angle(pos, d, hd, theta, &c, &sn);
-        double* qr = q + (size_t)row * q_dim;
-        q_pair(ar, output_scale(sq, am), bq, j0, j1, c, sn, &qr[j0], &qr[j1]);
-    } else if (r < qp + kp) {
-        const int t = r - qp;
-        const int h = t / half, d = t % half;
-        const int j0 = h * hd + d, j1 = j0 + half;
-        double c, sn;
-        rope_angle(pos, d, hd, theta, &c, &sn);
-        if (latest) {
-            float* kr = cache_k + (size_t)(pos % msl) * kv_dim;
-            k_pair(ar + q_dim, output_scale(sk, am), bk, j0, j1, c, sn, &kr[j0], &kr[j1]);
-        }
-    } else {
-        const int j = r - qp - kp;
-        if (latest) {
-            cache_v[(size_t)(pos % msl) * kv_dim + j] = v_val(ar + q_dim + kv_dim, output_scale(sv, am), bv, j);
+    double* qr = q + (size_t)row * q_dim;
+    float* kr = cache_k + (size_t)(pos % msl) * kv_dim;
+    float* vr = cache_v + (size_t)(pos % msl) * kv_dim;
+    for (int r = threadIdx.x; r < per_row; r += blockDim.x) {
+        if (r < qp) {
+            const int h = r / half, d = r % half;
+            const int j0 = h * hd + d, j1 = j0 + half;
+            q_pair(ar, osq, bq, j0, j1, rc[d], rs[d], &qr[j0], &qr[j1]);
+        } else if (r < qp + kp) {
+            const int t = r - qp;
+            const int h = t / half, d = t % half;
+            const int j0 = h * hd + d, j1 = j0 + half;
+            if (latest) k_pair(ar + q_dim, osk, bk, j0, j1, rc[d], rs[d], &kr[j0], &kr[j1]);
+        } else {
+            const int j = r - qp - kp;
+            if (latest) vr[j] = v_val(ar + q_dim + kv_dim, osv, bv, j);
         }
     }
 }
@@ -267,15 +267,13 @@ hipError_t launch_qkv_rope(const int32_t* acc, const float* amax, float sq, floa
                            const float* bq, const float* bk, const float* bv, int batch, int seq,
                            const int* pos0, int msl, int heads, int kv_heads, int hd, double theta,
                            double* q, float* cache_k, float* cache_v, hipStream_t s) {
-    const long total =
-        (long)batch * seq * (heads * (hd / 2) + kv_heads * (hd / 2) + kv_heads * hd);
-    if (total <= 0) return hipSuccess;
-    if (hd % 2 != 0) return hipErrorInvalidValue;
+    const long rows = (long)batch * seq;
+    if (rows <= 0) return hipSuccess;
+    if (hd % 2 != 0 || hd / 2 > kRopeMaxHalf) return hipErrorInvalidValue;
     if (theta <= 0.0) theta = 10000.0;
-    const int threads = 256;
-    hipLaunchKernelGGL(qkv_rope_kernel, dim3((unsigned)((total + threads - 1) / threads)),
-                       dim3(threads), 0, s, acc, amax, sq, sk, sv, bq, bk, bv, batch, seq, pos0,
-                       msl, heads, kv_heads, hd, theta, q, cache_k, cache_v);
+    hipLaunchKernelGGL(qkv_rope_kernel, dim3((unsigned)rows), dim3(256), 0, s, acc, amax, sq, sk, sv,
+                       bq, bk, bv, batch, seq, pos0, msl, heads, kv_heads, hd, theta, q, cache_k,
+                       cache_v);
     return hipGetLastError();
 }
 
