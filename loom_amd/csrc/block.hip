@@ -1706,7 +1706,7 @@ __global__ __launch_bounds__(256) void norm_quant_f64_kernel(double* __restrict_
                                                              double eps, float* __restrict__ pre,
                                                              int8_t* __restrict__ xq, int ldq,
                                                              float* __restrict__ amax_out,
-                                                             int32_t* __restrict__ xsum_out) {
+                                                             int32_t* __restrict__ xsum_out, int keep) {
     extern __shared__ double sq[];
     __shared__ double red[256];
     __shared__ float shf[4];
@@ -1747,7 +1747,7 @@ __global__ __launch_bounds__(256) void norm_quant_f64_kernel(double* __restrict_
         if (i < n) {
             const double w = weight ? (double)weight[i] : 1.0;
             v[j] = v[j] * (scale * w);
-            ar[i] = v[j];
+            if (keep) ar[i] = v[j];
             if (pre) pre[(size_t)row * n + i] = (float)v[j];
             m = max_nan_skip(m, (float)fabs(v[j]));
         }
@@ -1776,17 +1776,18 @@ __global__ __launch_bounds__(256) void norm_quant_f64_kernel(double* __restrict_
 
 template <int STRICT>
 static hipError_t launch_norm_f64_t(double* a, int m, int n, const float* w, double eps, float* pre,
-                                    int8_t* xq, int ldq, float* amax, int32_t* xsum, hipStream_t s) {
+                                    int8_t* xq, int ldq, float* amax, int32_t* xsum, int keep,
+                                    hipStream_t s) {
     const size_t shm = STRICT ? (size_t)n * sizeof(double) : 0;
     const dim3 g(m), b(256);
     if (n <= 256 * 4) {
-        hipLaunchKernelGGL((norm_quant_f64_kernel<STRICT, 4>), g, b, shm, s, a, n, w, eps, pre, xq, ldq, amax, xsum);
+        hipLaunchKernelGGL((norm_quant_f64_kernel<STRICT, 4>), g, b, shm, s, a, n, w, eps, pre, xq, ldq, amax, xsum, keep);
     } else if (n <= 256 * 8) {
-        hipLaunchKernelGGL((norm_quant_f64_kernel<STRICT, 8>), g, b, shm, s, a, n, w, eps, pre, xq, ldq, amax, xsum);
+        hipLaunchKernelGGL((norm_quant_f64_kernel<STRICT, 8>), g, b, shm, s, a, n, w, eps, pre, xq, ldq, amax, xsum, keep);
     } else if (n <= 256 * 16) {
-        hipLaunchKernelGGL((norm_quant_f64_kernel<STRICT, 16>), g, b, shm, s, a, n, w, eps, pre, xq, ldq, amax, xsum);
+        hipLaunchKernelGGL((norm_quant_f64_kernel<STRICT, 16>), g, b, shm, s, a, n, w, eps, pre, xq, ldq, amax, xsum, keep);
     } else if (n <= 256 * 32) {
-        hipLaunchKernelGGL((norm_quant_f64_kernel<STRICT, 32>), g, b, shm, s, a, n, w, eps, pre, xq, ldq, amax, xsum);
+        hipLaunchKernelGGL((norm_quant_f64_kernel<STRICT, 32>), g, b, shm, s, a, n, w, eps, pre, xq, ldq, amax, xsum, keep);
     } else {
         return hipErrorInvalidValue;
     }
@@ -1795,12 +1796,13 @@ static hipError_t launch_norm_f64_t(double* a, int m, int n, const float* w, dou
 
 hipError_t launch_norm_quant_f64(double* a, int m, int n, const float* w, double eps, int strict,
                                  float* pre, int8_t* xq, int ldq, float* amax, int32_t* xsum,
-                                 hipStream_t s) {
+                                 hipStream_t s, bool keep_rows) {
     if (m <= 0) return hipSuccess;
     if (eps <= 0.0) eps = 1e-5;  // bitNetRMSNormFloat64Weighted default
     if (n > kMaxNormCols || (strict && n > kMaxStrictNormCols)) return hipErrorInvalidValue;
-    return strict ? launch_norm_f64_t<1>(a, m, n, w, eps, pre, xq, ldq, amax, xsum, s)
-                  : launch_norm_f64_t<0>(a, m, n, w, eps, pre, xq, ldq, amax, xsum, s);
+    const int keep = keep_rows ? 1 : 0;
+    return strict ? launch_norm_f64_t<1>(a, m, n, w, eps, pre, xq, ldq, amax, xsum, keep, s)
+                  : launch_norm_f64_t<0>(a, m, n, w, eps, pre, xq, ldq, amax, xsum, keep, s);
 }
 
 // ------------------------------------------------------------------------

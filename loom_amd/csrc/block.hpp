@@ -49,11 +49,12 @@ hipError_t launch_attention(const double* q, const float* cache_k, const float* 
                             int kv_heads, int hd, int strict, double* scratch, double* out,
                             hipStream_t s);
 
-// MHA inner norm on fp64 rows in place (data *= scale*w) + fp64 requantization.
-// pre (optional) receives fp32 of the normalized rows.  eps <= 0 selects 1e-5.
+// MHA inner norm on fp64 rows in place (data *= scale*w; skipped when
+// keep_rows is false) + fp64 requantization.  pre (optional) receives fp32 of
+// the normalized rows.  eps <= 0 selects 1e-5.
 hipError_t launch_norm_quant_f64(double* a, int m, int n, const float* w, double eps, int strict,
                                  float* pre, int8_t* xq, int ldq, float* amax, int32_t* xsum,
-                                 hipStream_t s);
+                                 hipStream_t s, bool keep_rows = true);
 
 // Embedding rows of batch x seq tokens: row (b, s) takes the id at
 // tokens[b*cap + *pos0 + s] (pos0 null = 0); ids outside the table give zero

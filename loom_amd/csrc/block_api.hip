@@ -349,8 +349,10 @@ static int block_forward_dev(const BlockDev& B, const Workspace& W, float* x, in
                                    B.attn_norm, attn_eps, ep, nullptr, s);
             if (e != hipSuccess) return fail_hip("block attention inner norm + o projection", e);
         } else {
+            // (only the int8 rows feed the O projection: the normalized fp64
+            // rows are not written back)
             e = launch_norm_quant_f64(W.attn, R, B.q_dim, B.attn_norm, attn_eps, B.strict, nullptr,
-                                      W.aq, ldqd, W.amax2, W.xsum2, s);
+                                      W.aq, ldqd, W.amax2, W.xsum2, s, false);
             if (e != hipSuccess) return fail_hip("block attention inner norm", e);
             QuantAct a{W.aq, ldqd, W.amax2, W.xsum2};
             e = launch_matmul(&B.o, nullptr, a, R, ep, s);
@@ -391,8 +393,9 @@ static int block_forward_dev(const BlockDev& B, const Workspace& W, float* x, in
                                    B.ffn_norm, ffn_eps, ep, nullptr, s);
             if (e != hipSuccess) return fail_hip("block ffn inner norm + down", e);
         } else {
+            // (only the int8 rows feed the down projection)
             e = launch_norm_quant(W.h, B.inter, R, B.inter, B.ffn_norm, ffn_eps, B.strict, W.hq, ldi,
-                                  W.amax3, W.xsum3, s);
+                                  W.amax3, W.xsum3, s, false);
             if (e != hipSuccess) return fail_hip("block ffn inner norm", e);
             QuantAct a{W.hq, ldi, W.amax3, W.xsum3};
             e = launch_matmul(&B.down, nullptr, a, R, ep, s);

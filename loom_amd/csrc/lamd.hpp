@@ -122,10 +122,12 @@ hipError_t launch_matmul_norm(const Matrix* w0, const Matrix* w1, const float* x
                               const Epilogue& epi, float* amax_tap, hipStream_t s);
 
 // Inner RMSNorm + requantization of SwiGLU rows (poly/bitnet_cpu.go:893-913 then
-// poly/bitnet_cpu.go:97-106).  In place on h (M x n fp32, row stride ldh).
+// poly/bitnet_cpu.go:97-106).  In place on h (M x n fp32, row stride ldh) unless
+// keep_rows is false (then only the int8 rows, amax and sum(xq) are written).
 hipError_t launch_norm_quant(float* h, int ldh, int m, int n, const float* weight, double eps,
                              int strict, int8_t* hq, int ldq, float* amax, int32_t* xsum,
-                             hipStream_t s);
+                             hipStream_t s,
+                             bool keep_rows = true);
 
 // Per-device scratch arena for the device-resident entry points.
 void* scratch(int device, size_t bytes, std::string* err);

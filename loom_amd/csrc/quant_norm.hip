@@ -192,7 +192,7 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(float* __restrict__ h, 
                                                          const float* __restrict__ weight,
                                                          double eps, int8_t* __restrict__ hq,
                                                          int ldq, float* __restrict__ amax_out,
-                                                         int32_t* __restrict__ xsum_out) {
+                                                         int32_t* __restrict__ xsum_out, int keep) {
     extern __shared__ double dsh[];  // STRICT: n squares; fast: 256 partial sums
     __shared__ float shf[4];
     __shared__ int shi[4];
@@ -224,13 +224,18 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(float* __restrict__ h, 
             const double f = (double)v[j];  // zero past n
             s += f * f;
         }
+        // fixed tree: element t adds element t + w for w = 128, 64, ..., 1;
+        // the levels below 64 run as lane moves inside wave 0 (same pairs)
         dsh[threadIdx.x] = s;
         __syncthreads();
-        for (int width = 128; width > 0; width >>= 1) {
-            if (threadIdx.x < width) dsh[threadIdx.x] = dsh[threadIdx.x] + dsh[threadIdx.x + width];
-            __syncthreads();
+        if (threadIdx.x < 128) dsh[threadIdx.x] = dsh[threadIdx.x] + dsh[threadIdx.x + 128];
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            double t = dsh[threadIdx.x] + dsh[threadIdx.x + 64];
+#pragma unroll
+            for (int width = 32; width > 0; width >>= 1) t = t + __shfl_down(t, width, 64);
+            if (threadIdx.x == 0) total = t;
         }
-        if (threadIdx.x == 0) total = dsh[0];
         __syncthreads();
     }
 
@@ -242,7 +247,7 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(float* __restrict__ h, 
         if (i < n) {
             const double w = weight ? (double)weight[i] : 1.0;
             v[j] = (float)((double)v[j] * scale * w);
-            hr[i] = v[j];
+            if (keep) hr[i] = v[j];
             m = max_nan_skip(m, fabsf(v[j]));
         }
     }
@@ -270,18 +275,19 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(float* __restrict__ h, 
 
 template <int STRICT>
 static hipError_t launch_norm_t(float* h, int ldh, int m, int n, const float* weight, double eps,
-                                int8_t* hq, int ldq, float* amax, int32_t* xsum, hipStream_t s) {
+                                int8_t* hq, int ldq, float* amax, int32_t* xsum, int keep,
+                                hipStream_t s) {
     const size_t shm = STRICT ? (size_t)n * sizeof(double) : 256 * sizeof(double);
     const dim3 g(m), b(256);
     if (n <= 256 * 8) {
         hipLaunchKernelGGL((norm_quant_kernel<STRICT, 8>), g, b, shm, s, h, ldh, n, weight, eps, hq,
-                           ldq, amax, xsum);
+                           ldq, amax, xsum, keep);
     } else if (n <= 256 * 16) {
         hipLaunchKernelGGL((norm_quant_kernel<STRICT, 16>), g, b, shm, s, h, ldh, n, weight, eps,
-                           hq, ldq, amax, xsum);
+                           hq, ldq, amax, xsum, keep);
     } else if (n <= 256 * 32) {
         hipLaunchKernelGGL((norm_quant_kernel<STRICT, 32>), g, b, shm, s, h, ldh, n, weight, eps,
-                           hq, ldq, amax, xsum);
+                           hq, ldq, amax, xsum, keep);
     } else {
         return hipErrorInvalidValue;
     }
@@ -290,12 +296,13 @@ static hipError_t launch_norm_t(float* h, int ldh, int m, int n, const float* we
 
 hipError_t launch_norm_quant(float* h, int ldh, int m, int n, const float* weight, double eps,
                              int strict, int8_t* hq, int ldq, float* amax, int32_t* xsum,
-                             hipStream_t s) {
+                             hipStream_t s, bool keep_rows) {
     if (m <= 0) return hipSuccess;
     if (eps <= 0.0) eps = 1e-5;
     if (n > kMaxNormCols) return hipErrorInvalidValue;
-    return strict ? launch_norm_t<1>(h, ldh, m, n, weight, eps, hq, ldq, amax, xsum, s)
-                  : launch_norm_t<0>(h, ldh, m, n, weight, eps, hq, ldq, amax, xsum, s);
+    const int keep = keep_rows ? 1 : 0;
+    return strict ? launch_norm_t<1>(h, ldh, m, n, weight, eps, hq, ldq, amax, xsum, keep, s)
+                  : launch_norm_t<0>(h, ldh, m, n, weight, eps, hq, ldq, amax, xsum, keep, s);
 }
 
 }  // namespace lamd
