@@ -215,10 +215,11 @@ __device__ __forceinline__ float v_val(const int32_t* ar, double os, const float
     return v_val_v(ar[j], os, bv != nullptr, bv ? bv[j] : 0.0f);
 }
 
-// One workgroup per token row: the row's hd/2 rotation angles are computed
-// once into LDS (pos / theta^(2d/hd), cos, sin in fp64: the same values for
-// every Q and K head), then the workgroup's threads stride over the row's Q
-// pairs, K pairs and V elements.
+// Workgroups (row, part): the row's hd/2 rotation angles are computed once
+// per workgroup into LDS (pos / theta^(2d/hd), cos, sin in fp64: the same
+// values for every Q and K head), then its threads stride over the row's Q
+// pairs, K pairs and V elements.  Many rows (prefill): one part per row; few
+// rows (decode): a row's items spread over several workgroups.
 constexpr int kRopeMaxHalf = 128;  // head_dim <= 256
 
 __global__ __launch_bounds__(256) void qkv_rope_kernel(
@@ -246,7 +247,7 @@ __global__ __launch_bounds__(256) void qkv_rope_kernel(
     double* qr = q + (size_t)row * q_dim;
     float* kr = cache_k + (size_t)(pos % msl) * kv_dim;
     float* vr = cache_v + (size_t)(pos % msl) * kv_dim;
-    for (int r = threadIdx.x; r < per_row; r += blockDim.x) {
+    for (int r = threadIdx.x + blockIdx.y * blockDim.x; r < per_row; r += blockDim.x * gridDim.y) {
         if (r < qp) {
             const int h = r / half, d = r % half;
             const int j0 = h * hd + d, j1 = j0 + half;
@@ -271,9 +272,11 @@ hipError_t launch_qkv_rope(const int32_t* acc, const float* amax, float sq, floa
     if (rows <= 0) return hipSuccess;
     if (hd % 2 != 0 || hd / 2 > kRopeMaxHalf) return hipErrorInvalidValue;
     if (theta <= 0.0) theta = 10000.0;
-    hipLaunchKernelGGL(qkv_rope_kernel, dim3((unsigned)rows), dim3(256), 0, s, acc, amax, sq, sk, sv,
-                       bq, bk, bv, batch, seq, pos0, msl, heads, kv_heads, hd, theta, q, cache_k,
-                       cache_v);
+    const int per_row = heads * (hd / 2) + kv_heads * (hd / 2) + kv_heads * hd;
+    const int parts = rows >= 256 ? 1 : ceil_div(per_row, 256);
+    hipLaunchKernelGGL(qkv_rope_kernel, dim3((unsigned)rows, parts), dim3(256), 0, s, acc, amax, sq,
+                       sk, sv, bq, bk, bv, batch, seq, pos0, msl, heads, kv_heads, hd, theta, q,
+                       cache_k, cache_v);
     return hipGetLastError();
 }
 
