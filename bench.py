@@ -37,6 +37,8 @@ INT8_PEAK_TOPS = 5000.0     # MI355X dense int8 MFMA, TOPS
 MALL_BYTES = 256 << 20
 METRIC = ("ternary GEMV GB/s (%HBM peak); decode tok/s + prefill int8 TOPS at BitNet-2B shape")
 
+SUSTAIN_COPIES = 128  # stacked up-shape matrices of the sustained figure (566 MB)
+
 UP = (6912, 2560)    # (N, K) of up/gate
 DOWN = (2560, 6912)  # (N, K) of down
 
@@ -62,21 +64,51 @@ def log(msg: str) -> None:
 
 
 def cpu_cores() -> int:
+    """Worker threads of the CPU baseline: every core the process may run on
+    (Go's GOMAXPROCS default), at most 16, the GPU box's host share."""
+    return max(1, min(cpu_nproc(), 16))
+
+
+def cpu_nproc() -> int:
     try:
-        c = len(os.sched_getaffinity(0))
+        return len(os.sched_getaffinity(0))
     except AttributeError:
-        c = os.cpu_count() or 1
-    return max(1, min(c, 16))  # the GPU box's host share is 16 cores
+        return os.cpu_count() or 1
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_host_fields(cores: int) -> dict:
+    return {"cores": cores, "nproc": cpu_nproc(), "os_cpu_count": os.cpu_count(),
+            "cpu_model": cpu_model()}
 
 
 class Timer:
     """HIP-event timing on the stream every loom_amd launch uses (torch's current
-    stream).  Steps are captured into a HIP graph of `per_graph` consecutive
-    calls and the graph is replayed, so the measurement is the device's
-    back-to-back throughput, not the Python launch rate."""
+    stream).  Steps are captured into HIP graphs and the graphs are replayed,
+    so the measurement is the device's back-to-back throughput, not the Python
+    launch rate.
+
+    Rotating runs (rotate=R > 1: call i uses weight copy i % R) capture one
+    graph of all R calls, whatever `steps` is, and replay it steps // R times,
+    then a graph of the first steps % R calls.  Before the timed region a
+    2 x MALL buffer is overwritten, so no copy is cache-resident when timing
+    starts; inside it a copy is read again only after the other R - 1 copies
+    (>= 2 x MALL of bytes), so every call streams its weights from HBM."""
 
     def __init__(self, torch):
         self.torch = torch
+        self._flush = None
+        self.last_working_set = 0  # distinct copies the last rotating timed region read
 
     def _capture(self, fn, first: int, count: int):
         graph = self.torch.cuda.CUDAGraph()
@@ -85,10 +117,17 @@ class Timer:
                 fn(i)
         return graph
 
-    def run(self, fn, steps: int, warmup: int, per_graph: int = 64) -> float:
+    def flush(self):
+        """Overwrite 2 x MALL of device memory (evicts the MALL and every L2)."""
+        torch = self.torch
+        if self._flush is None:
+            self._flush = torch.empty(2 * MALL_BYTES // 4, dtype=torch.float32, device="cuda")
+        self._flush.fill_(0.0)
+
+    def run(self, fn, steps: int, warmup: int, per_graph: int = 64, rotate: int = 0) -> float:
         """Mean ms per call over exactly `steps` calls (after `warmup` calls)."""
         torch = self.torch
-        per_graph = max(1, min(per_graph, steps))
+        steps = max(1, steps)
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
@@ -96,12 +135,19 @@ class Timer:
                 fn(i)
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
+        if rotate > 1:
+            per_graph = rotate  # never clamped: one graph visits every copy
+        else:
+            per_graph = max(1, min(per_graph, steps))
         full, rest = divmod(steps, per_graph)
         graph = self._capture(fn, 0, per_graph) if full else None
-        tail = self._capture(fn, full * per_graph, rest) if rest else None
+        tail = self._capture(fn, 0, rest) if rest else None
         for g in (graph, tail):
             if g is not None:
                 g.replay()  # untimed: first replay uploads the graph
+        if rotate > 1:
+            self.flush()
+            self.last_working_set = min(steps, rotate)
         torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
@@ -113,6 +159,24 @@ class Timer:
         end.record()
         torch.cuda.synchronize()
         return start.elapsed_time(end) / steps  # ms per call
+
+    def run_cold(self, fn, reps: int) -> float:
+        """Mean ms of one call timed alone, each after a 2 x MALL overwrite
+        (one untimed call first)."""
+        torch = self.torch
+        fn()
+        tot = 0.0
+        for _ in range(reps):
+            self.flush()
+            torch.cuda.synchronize()
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record()
+            fn()
+            end.record()
+            torch.cuda.synchronize()
+            tot += start.elapsed_time(end)
+        return tot / reps
 
 
 def make_matrix(orc, n, k, seed):
@@ -188,7 +252,7 @@ def cpu_decode_sample(c, cores, log):
     lm_s = time.perf_counter() - t0
     step_s = layer_s * c["layers"] + lm_s
     log(f"cpu decode sample: layer step {layer_s * 1e3:.1f} ms, LM head {lm_s * 1e3:.1f} ms")
-    return {"value": round(1.0 / step_s, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+    return {"value": round(1.0 / step_s, 3), "unit": "tok/s", **cpu_host_fields(cores), "kind": "port",
             "sample": f"one decode step of one BitNet-2B layer at context {ctx} (synthetic KV), "
                       f"{steps} runs, x{c['layers']} layers, + one fp32 LM head "
                       f"({layer_s * 1e3:.1f} ms/layer, {lm_s * 1e3:.1f} ms LM head)"}
@@ -209,8 +273,58 @@ def cpu_block_sample(c, cores, seq, log):
     blk.forward(x, workers=cores)
     s = time.perf_counter() - t0
     log(f"cpu block seq{seq}: {s:.2f} s")
-    return {"value": round(seq / s, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+    return {"value": round(seq / s, 1), "unit": "tokens/s", **cpu_host_fields(cores), "kind": "port",
             "sample": f"one config-2 block forward over {seq} tokens ({s:.2f} s)"}
+
+
+def cpu_sweep_sample(orc, cores, ms, log):
+    """Config 1 on the oracle: DenseForwardPackedTernaryCPU over M rows, each
+    row a full bitNetRunRows fan-out GEMV, rows one after another
+    (poly/dense.go:83-99), on both FFN shapes."""
+    import numpy as np
+    rows = []
+    for shape_name, (nn, kk), seed in (("up_gate", UP, 0xB17), ("down", DOWN, 0xD0)):
+        m = orc.random_matrix(nn, kk, seed)
+        m.ensure_codes()
+        for M in ms:
+            x = orc.normal_f32(M * kk, seed=M).reshape(M, kk)
+            orc.dense_forward(m, x[:1], simd=True, workers=cores)
+            t0 = time.perf_counter()
+            orc.dense_forward(m, x, simd=True, workers=cores)
+            dt = time.perf_counter() - t0
+            by = gemv_bytes(M, nn, kk)
+            rows.append({"shape": shape_name, "M": M, "ms": round(dt * 1e3, 3),
+                         "GBs": round(by / dt / 1e9, 3),
+                         "GOPS": round(2.0 * M * kk * nn / dt / 1e9, 2)})
+            log(f"cpu sweep {rows[-1]}")
+    del np
+    return {"runs": rows, "unit": "ms per DenseForward of M rows", **cpu_host_fields(cores),
+            "kind": "port",
+            "sample": "each (shape, M) once after one warm row; M rows serial, each fanned out "
+                      "over the cores as loom's bitNetRunRows does"}
+
+
+def cpu_prefill_slice(c, cores, log, seq=64):
+    """Config 4 on the oracle, bounded: one BitNet-2B layer's block forward
+    over a 64-token prefill slice (fresh cache), scaled to 30 layers."""
+    from oracle import oracle as orc
+    h, q_dim, kv_dim, inter = c["hidden"], c["heads"] * c["head_dim"], c["kv_heads"] * c["head_dim"], c["inter"]
+    mats = [orc.random_matrix(r, k, 0xB00 + i) for i, (r, k) in
+            enumerate([(q_dim, h), (kv_dim, h), (kv_dim, h), (h, q_dim), (inter, h), (inter, h), (h, inter)])]
+    mha = orc.MHA(*mats[:4], c["heads"], c["kv_heads"], c["head_dim"], 2048, theta=c["theta"],
+                  eps=1e-5, inner_norm=orc.uniform_f32(q_dim, 0.5, 1.5, 1))
+    blk = orc.Block(mha, orc.uniform_f32(h, 0.5, 1.5, 4), orc.uniform_f32(h, 0.5, 1.5, 5), *mats[4:],
+                    orc.uniform_f32(inter, 0.5, 1.5, 6), norm_eps=1e-5, ffn_eps=1e-5, ffn_activation=1)
+    x = orc.normal_f32(seq * h, 11).reshape(seq, h)
+    t0 = time.perf_counter()
+    blk.forward(x, workers=cores)
+    layer_s = time.perf_counter() - t0
+    tok_s = seq / (layer_s * c["layers"])
+    log(f"cpu prefill slice: {seq} tokens, one layer {layer_s:.2f} s")
+    return {"value": round(tok_s, 2), "unit": "tokens/s", **cpu_host_fields(cores), "kind": "port",
+            "sample": f"one BitNet-2B layer over a {seq}-token prefill slice ({layer_s:.2f} s), "
+                      f"x{c['layers']} layers (config 4's prefill is 8 x 2048 tokens; the "
+                      "slice's per-token cost is the rate)"}
 
 
 def bench_model(args, torch, timer, log):
@@ -325,6 +439,7 @@ def bench_model(args, torch, timer, log):
         model.release()
     if args.cpu_seconds > 0:
         out["cpu_decode"] = cpu_decode_sample(c, cpu_cores(), log)
+        out["cpu_prefill_slice"] = cpu_prefill_slice(c, cpu_cores(), log)
     out["decode"] = {"config": f"config3: {c['layers']} layers, vocab {c['vocab']}, tied fp32 "
                                f"LM head, greedy, {prompt}-token random prompt, {gen} tokens, "
                                "one HIP graph per token, positions on device",
@@ -347,6 +462,8 @@ def main() -> int:
     ap.add_argument("--no-model", action="store_true", help="skip configs 2-4")
     ap.add_argument("--model-layers", type=int, default=30)
     ap.add_argument("--model-norms", default="fast,strict")
+    ap.add_argument("--no-sustained", dest="sustained", action="store_false",
+                    help="skip the single-launch sustained-bandwidth figure")
     ap.add_argument("--calibrate-copy", type=int, default=0,
                     help="also run 4 device copies of this many MiB (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -385,33 +502,66 @@ def main() -> int:
     # ---------------- headline: dense forward M=1 on the up shape ---------------
     x1 = torch.from_numpy(orc.normal_f32(k, seed=1).reshape(1, k)).cuda()
     out1 = torch.empty((1, n), dtype=torch.float32, device="cuda")
+    b1 = gemv_bytes(1, n, k)
 
     def step_dense(i):
         bn.dense_forward_packed_ternary(ups[i % rot], x1, out=out1)
 
-    ms_step = timer.run(step_dense, args.steps, args.warmup, per_graph=rot)
-    b1 = gemv_bytes(1, n, k)
+    ms_step = timer.run(step_dense, args.steps, args.warmup, rotate=rot)
+    copies_read = timer.last_working_set
+    working_set = copies_read * per + 4 * (k + n)
     value = b1 / (ms_step * 1e-3) / 1e9
-    log(f"dense M=1 up: {ms_step * 1e3:.2f} us/step, {value:.0f} GB/s")
+    log(f"dense M=1 up: {ms_step * 1e3:.2f} us/step, {value:.0f} GB/s "
+        f"(timed region read {copies_read} copies, {working_set / 1e6:.0f} MB)")
 
-    # dominant kernel alone (pre-quantized activations): per-launch duration
+    # the GEMV alone on pre-quantized activations (the step's kernel without
+    # its quantization prologue)
     q1 = bn.quantize_activation(x1)
 
     def step_gemv(i):
         bn.ternary_matvec_quantized(ups[i % rot], q1)
 
-    ms_kernel = timer.run(step_gemv, args.steps, args.warmup, per_graph=rot)
-    achieved = b1 / (ms_kernel * 1e-3) / 1e9
-    log(f"gemv kernel M=1 up: {ms_kernel * 1e3:.2f} us/launch, {achieved:.0f} GB/s")
+    ms_kernel = timer.run(step_gemv, args.steps, args.warmup, rotate=rot)
+    log(f"gemv kernel M=1 up (pre-quantized): {ms_kernel * 1e3:.2f} us/launch, "
+        f"{b1 / (ms_kernel * 1e-3) / 1e9:.0f} GB/s")
 
     # latency floor of one launch that streams this many bytes: a device copy
     # of the packed weights' size, rotating over as many buffers (HBM-resident)
     srcs = [torch.empty(per // 4, dtype=torch.float32, device="cuda").fill_(1.0) for _ in range(rot)]
     dst = torch.empty_like(srcs[0])
-    ms_copy = timer.run(lambda i: dst.copy_(srcs[i % rot]), args.steps, args.warmup, per_graph=rot)
+    ms_copy = timer.run(lambda i: dst.copy_(srcs[i % rot]), args.steps, args.warmup, rotate=rot)
     del srcs, dst
     log(f"device copy of {per} B: {ms_copy * 1e3:.2f} us/launch")
 
+    # sustained rate of the same kernels without the per-launch floor: one
+    # launch over a stacked matrix of SUSTAIN_COPIES up-shape matrices (N =
+    # 6912 x copies rows, >= 2 x MALL), HBM-resident, the cache flushed first
+    sustained = None
+    if args.sustained:
+        big_n = n * SUSTAIN_COPIES
+        words = np.tile(host_up.words.reshape(n, -1), (SUSTAIN_COPIES, 1)).reshape(-1)
+        big = bn.TernaryMatrix.from_words(words, big_n, k, host_up.scale)
+        del words
+        big_bytes = gemv_bytes(1, big_n, k)
+        ob = torch.empty((1, big_n), dtype=torch.float32, device="cuda")
+        t_big_f = timer.run_cold(lambda: bn.dense_forward_packed_ternary(big, x1, out=ob), 5)
+        t_big_k = timer.run_cold(lambda: bn.ternary_matvec_quantized(big, q1), 5)
+        sustained = {
+            "bytes_per_launch": big_bytes, "rows": big_n, "K": k,
+            "us_fused": round(t_big_f * 1e3, 2), "us_kernel": round(t_big_k * 1e3, 2),
+            "GBs_fused": round(big_bytes / (t_big_f * 1e-3) / 1e9, 1),
+            "GBs_kernel": round(big_bytes / (t_big_k * 1e-3) / 1e9, 1),
+            "frac": round(big_bytes / (t_big_f * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "frac_kernel": round(big_bytes / (t_big_k * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "note": f"one launch of the step's kernels over {SUSTAIN_COPIES} stacked up-shape "
+                    f"matrices ({big_bytes / 1e6:.0f} MB, > 2 x MALL), 5 timed launches each "
+                    "after a 2 x MALL overwrite",
+        }
+        log(f"sustained: {sustained}")
+        big.release()
+        del ob
+
+    achieved = b1 / (ms_step * 1e-3) / 1e9
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -424,8 +574,10 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8xternary->int32, fp64 rescale, fp32 io",
-        "data": "synthetic: seeded ternary weights P(0)=.5, x~N(0,1); weights rotate over "
-                f"{rot} HBM-resident copies",
+        "data": "synthetic: seeded ternary weights P(0)=.5, x~N(0,1); step i reads weight copy "
+                f"i % {rot} ({rot} HBM-resident copies, {rot * per / 1e6:.0f} MB); a 2 x MALL "
+                "overwrite precedes the timed region",
+        "working_set_bytes": working_set,
         "config": {"workload": "config1 ternary GEMV M=1 K=2560 N=6912 (= config0 shape), "
                                "DenseForwardPackedTernary: act-quant + GEMV + epilogue",
                    "M": 1, "K": k, "N": n, "rotating_copies": rot,
@@ -433,11 +585,15 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": pmc_traffic(),
-                     "kernel": "skinny_kernel<1,1,8,false> (ternary GEMV, pre-quantized row)",
-                     "us_per_launch": round(ms_kernel * 1e3, 3), "bytes_per_launch": b1,
+                     "kernel": "skinny_kernel<1,1,8,true> (fused act-quant + ternary GEMV + "
+                               "epilogue: the step's only launch)",
+                     "us_per_launch": round(ms_step * 1e3, 3), "bytes_per_launch": b1,
+                     "us_prequantized_kernel": round(ms_kernel * 1e3, 3),
+                     "GBs_prequantized_kernel": round(b1 / (ms_kernel * 1e-3) / 1e9, 1),
                      "copy_floor_us": round(ms_copy * 1e3, 3),
                      "copy_floor_note": f"torch device copy of {per} B (read + write) per launch, "
-                                        f"same rotation: the per-launch latency floor at this size"},
+                                        f"same rotation: the per-launch latency floor at this size",
+                     "sustained": sustained},
     }
 
     # ---------------- config-1 sweep ----------------------------------------------
@@ -451,9 +607,9 @@ def main() -> int:
                 steps = max(20, min(args.steps, int(2e5 / M)))
                 nm = len(mats) if M <= 64 else 1
                 t_k = timer.run(lambda i: bn.ternary_matvec_quantized(mats[i % nm], q),
-                                steps, max(5, steps // 10), per_graph=min(nm, 64) if nm > 1 else 16)
+                                steps, max(5, steps // 10), per_graph=16, rotate=nm)
                 t_d = timer.run(lambda i: bn.dense_forward_packed_ternary(mats[i % nm], x, out=o),
-                                steps, max(5, steps // 10), per_graph=min(nm, 64) if nm > 1 else 16)
+                                steps, max(5, steps // 10), per_graph=16, rotate=nm)
                 ent = {"shape": shape_name, "M": M, "K": kk, "N": nn,
                        "kernel": _lib.lib().loom_amd_kernel_variant(M).decode(),
                        "us_kernel": round(t_k * 1e3, 3), "us_dense": round(t_d * 1e3, 3)}
@@ -514,12 +670,14 @@ def main() -> int:
         reps += 1
     cpu_s = (time.perf_counter() - t0) / reps
     result["cpu_baseline"] = {
-        "value": round(b1 / cpu_s / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+        "value": round(b1 / cpu_s / 1e9, 3), "unit": "GB/s", **cpu_host_fields(cores), "kind": "port",
         "sample": f"config0 GEMV M=1 K=2560 N=6912 repeated {reps}x over {args.cpu_seconds:.0f}s "
                   f"({cpu_s * 1e3:.3f} ms/GEMV; AVX2 byte-code path, bitNetRunRows fan-out)",
         "simd": "avx2" if orc.simd_available() else "scalar",
     }
     log(f"cpu baseline {result['cpu_baseline']}")
+    if not args.no_sweep:
+        result["cpu_sweep"] = cpu_sweep_sample(orc, cores, [1, 8, 64, 512, 4096], log)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -224,7 +224,8 @@ void loom_amd_block_release(loom_amd_block* b);
  * KV rule of mhaPrepareKVForForward (poly/mha_layout.go:62-70): a call with
  * seq == 1 on a warm cache continues at the current position; any other
  * call restarts at position 0.  Each of the batch sequences has its own KV
- * cache; all of them advance together.  Replaces the block loop body of
+ * cache; all of them advance together, so a single-token call on a warm
+ * cache must carry the batch that filled it (another batch is refused).  Replaces the block loop body of
  * forwardOnCPUNormal (poly/transformer_forward.go:228-245) for BitNet layers
  * (MHAForwardPackedTernaryCPU, poly/mha.go:204-371, and
  * SwiGLUForwardPackedTernaryCPU, poly/bitnet_cpu.go:915-1002).  May grow the

@@ -31,6 +31,21 @@ int visible_gfx950() {
     return c;
 }
 
+// ---- per-device serialization of the plugin's calls ----------------------
+
+// One lock per device (devices beyond kMaxLockedDevices share the last one).
+// The v2 plugin's infer calls hold it from the upload to the stream sync, so
+// two host threads running compiled layers on one device never share the
+// device's scratch arena and split-K workspace at the same time.
+constexpr int kMaxLockedDevices = 64;
+static std::mutex g_device_mu[kMaxLockedDevices];
+
+std::mutex& device_mutex(int device) {
+    if (device < 0) device = 0;
+    if (device >= kMaxLockedDevices) device = kMaxLockedDevices - 1;
+    return g_device_mu[device];
+}
+
 // ---- per-device scratch arena ------------------------------------------
 
 struct Arena {

@@ -1,6 +1,7 @@
 // api_util.hpp -- host helpers shared by the loom_amd_* entry points.
 #pragma once
 
+#include <mutex>
 #include <string>
 
 #include "lamd.hpp"
@@ -37,6 +38,9 @@ struct DeviceGuard {
 
 bool is_gfx950(int dev);
 int visible_gfx950();
+
+// Lock serializing the v2 plugin's calls on one device (amd_api.hip).
+std::mutex& device_mutex(int device);
 
 // Bump layout of one allocation's sub-buffers, 256-byte aligned.
 struct Layout {

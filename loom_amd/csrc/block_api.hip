@@ -418,6 +418,7 @@ struct loom_amd_block {
     Workspace ws;
     int* pos = nullptr;  // device
     int shadow = 0;      // host copy of the KV position
+    int warm_batch = 0;  // sequences the warm cache holds (batch of the calls that filled it)
 };
 
 struct loom_amd_model {
@@ -491,6 +492,13 @@ int loom_amd_block_forward(loom_amd_block* b, float* x, int batch, int seq,
         return fail("batch " + std::to_string(batch) + " > max_batch " + std::to_string(B.max_batch));
     }
     const int base = next_base(b->shadow, seq);
+    if (base > 0 && batch != b->warm_batch) {
+        // each sequence owns a ring: a single-token call with another batch
+        // would read slots the warm cache never filled
+        return fail("single-token call of batch " + std::to_string(batch) +
+                    " on a warm cache of batch " + std::to_string(b->warm_batch) +
+                    ": continue with the same batch or restart with a longer call");
+    }
     if (base + seq > B.span()) {
         return fail("positions " + std::to_string(base) + ".." + std::to_string(base + seq - 1) +
                     " pass max_seq_len " + std::to_string(B.msl));
@@ -511,6 +519,7 @@ int loom_amd_block_forward(loom_amd_block* b, float* x, int batch, int seq,
     e = launch_add_int(b->pos, seq, s);
     if (e != hipSuccess) return fail_hip("block position", e);
     b->shadow = base + seq;
+    b->warm_batch = batch;
     return 0;
 }
 

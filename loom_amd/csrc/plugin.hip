@@ -8,6 +8,7 @@
 //                   then optionally n fp32 inner-norm weights.
 // dtype "TERNARY"; size_label "m=..,k=..,n=..[,act=..][,eps=..][,norm=strict|fast]".
 // Only device "GPU" exists: loom's own CPU path is the CPU implementation.
+#include "api_util.hpp"
 #include "lamd.hpp"
 #include "loom_accel.h"
 #include "loom_accel_amd.h"
@@ -18,10 +19,6 @@
 #include <chrono>
 #include <mutex>
 #include <string>
-
-namespace lamd {
-int visible_gfx950();
-}
 
 struct loom_accel_plugin {
     int device = 0;
@@ -186,7 +183,10 @@ void release(loom_accel_compiled_layer* l) {
     delete l;
 }
 
-// Runs the layer on l->d_in -> l->d_out and waits for it.
+// Runs the layer on l->d_in -> l->d_out and waits for it.  The caller holds
+// the device's lock: every layer on a device shares its scratch arena and
+// split-K workspace (loom's Go glue has no lock of its own, and goroutines
+// may call infer on two compiled layers at once).
 int run(loom_accel_compiled_layer* l, std::string* why) {
     int rc;
     if (l->kind == 0) {
@@ -366,6 +366,7 @@ int loom_accel_first_infer(loom_accel_compiled_layer* layer, double* first_infer
         return -1;
     }
     const auto t0 = Clock::now();
+    std::lock_guard<std::mutex> lock(lamd::device_mutex(layer->device));
     hipError_t e = hipMemsetAsync(layer->d_in, 0, layer->in_bytes, layer->stream);
     if (e != hipSuccess) {
         set_err(err, err_len, std::string("first_infer: ") + hipGetErrorString(e));
@@ -399,6 +400,7 @@ int loom_accel_infer(loom_accel_compiled_layer* layer, const void* in, size_t in
         return -1;
     }
     const auto t0 = Clock::now();
+    std::lock_guard<std::mutex> lock(lamd::device_mutex(layer->device));
     hipError_t e = hipMemcpyAsync(layer->d_in, in, in_bytes, hipMemcpyHostToDevice, layer->stream);
     if (e != hipSuccess) {
         set_err(err, err_len, std::string("infer upload: ") + hipGetErrorString(e));

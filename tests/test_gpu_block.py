@@ -336,6 +336,30 @@ def test_block_refuses_positions_past_ring(orc, torch_dev, tf):
         blk.forward(to_dev(torch, np.zeros((2, 3, SMALL.hidden), np.float32)))
 
 
+def test_block_refuses_decode_batch_other_than_warm_cache(orc, torch_dev, tf):
+    # each sequence owns a KV ring: a single-token call continuing a warm
+    # cache must have the batch that filled it (a wider batch would read slots
+    # no call wrote); a longer call restarts every sequence at position 0
+    from loom_amd._lib import AMDError
+    torch = torch_dev
+    w = Weights(orc, SMALL, seed=213)
+    blk = tf.BitNetBlock(w.cfg(tf, max_batch=2), w.gpu(tf))
+    x4 = orc.normal_f32(4 * SMALL.hidden, 1110).reshape(1, 4, SMALL.hidden)
+    blk.forward(to_dev(torch, x4))
+    with pytest.raises(AMDError, match="warm cache of batch 1"):
+        blk.forward(to_dev(torch, np.zeros((2, 1, SMALL.hidden), np.float32)))
+    assert blk.kv_offset == 4
+    blk.forward(to_dev(torch, x4[:, :1]))  # same batch continues
+    assert blk.kv_offset == 5
+    blk.forward(to_dev(torch, np.concatenate([x4, x4])))  # batch 2 restarts
+    assert blk.kv_offset == 4
+    blk.forward(to_dev(torch, np.zeros((2, 1, SMALL.hidden), np.float32)))
+    assert blk.kv_offset == 5
+    with pytest.raises(AMDError, match="warm cache of batch 2"):
+        blk.forward(to_dev(torch, np.zeros((1, 1, SMALL.hidden), np.float32)))
+    blk.release()
+
+
 @pytest.mark.parametrize("hd,seq", [(128, 300), (64, 200)])
 def test_fast_prefill_attention_query_tiles_agree(orc, torch_dev, tf, monkeypatch, hd, seq):
     # the fast prefill kernel with 32 or 64 queries per workgroup sums in the

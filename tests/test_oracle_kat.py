@@ -250,6 +250,110 @@ def test_inner_norm_closed_form(orc):
     assert np.all(h3 == want)
 
 
+def _seq_sum_sq(v64):
+    # loom's sequential fp64 sum of squares (np.add.accumulate adds in order)
+    return float(np.add.accumulate(v64 * v64)[-1])
+
+
+def _differs(a, b):
+    return not np.array_equal(np.asarray(a).view(np.uint8), np.asarray(b).view(np.uint8))
+
+
+def _association_probes():
+    # probe elements found by tests/golden/find_association_probes.py: tiny
+    # values appended to a seeded row, each with a weight for which the two
+    # fp64 associations round to different fp32 values
+    import json
+    import os
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                           "association_probes.json")) as f:
+        return json.load(f)
+
+
+def test_inner_norm_f32_association(orc):
+    # bitNetRMSNormTensorRowWeighted (poly/bitnet_cpu.go:893-913) writes
+    # T(float64(v) * scale * w): Go evaluates left to right, (v*scale)*w.
+    # On the probe elements the other association gives another fp32 value;
+    # the oracle must give the reference's on every element.
+    P = _association_probes()
+    probes = P["inner_norm_f32"]
+    base = orc.normal_f32(P["base_n"], P["base_seed"])
+    x = np.concatenate([base, np.array([p["x"] for p in probes], np.float32)])
+    w = np.concatenate([orc.uniform_f32(P["base_n"], 0.5, 1.5, 602),
+                        np.array([p["w"] for p in probes], np.float32)])
+    n, eps = x.size, P["eps"]
+    x64, w64 = x.astype(np.float64), w.astype(np.float64)
+    scale = 1.0 / math.sqrt(_seq_sum_sq(x64) / n + eps)
+    ref = ((x64 * scale) * w64).astype(np.float32)
+    alt = (x64 * (scale * w64)).astype(np.float32)
+    tail = slice(P["base_n"], None)
+    assert np.all(ref[tail].view(np.uint32) != alt[tail].view(np.uint32)), \
+        "a probe no longer separates the associations"
+    got = orc.bitnet_rmsnorm_row(x, w, eps)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_inner_norm_f64_association(orc):
+    # bitNetRMSNormFloat64Weighted (poly/bitnet_cpu.go:868-887) writes
+    # data[i] *= scale * w: the product scale*w is formed first, the opposite
+    # association of the fp32-row helper above.
+    import ctypes as C
+    n, eps = 2560, 1e-5
+    d = orc.normal_f32(n, 603).astype(np.float64) * (1.0 + 2.0 ** -30)
+    w = orc.uniform_f32(n, 0.5, 1.5, 604)
+    w64 = w.astype(np.float64)
+    scale = 1.0 / math.sqrt(_seq_sum_sq(d) / n + eps)
+    ref = d * (scale * w64)
+    alt = (d * scale) * w64
+    assert _differs(ref, alt), "inputs do not separate the associations"
+    got = d.copy()
+    orc.lib().orc_bitnet_rmsnorm_f64(got.ctypes.data_as(C.c_void_p), n,
+                                     w.ctypes.data_as(C.c_void_p), eps)
+    assert np.array_equal(got.view(np.uint64), ref.view(np.uint64))
+
+
+def test_rmsnorm_divides_by_rms(orc):
+    # RMSNormForwardPolymorphic (poly/norm.go:102-138): normed = x / rms, a
+    # division, then T(normed * g); multiplying by 1/rms rounds the probe
+    # elements to other fp32 values.
+    P = _association_probes()
+    probes = P["rmsnorm"]
+    base = orc.normal_f32(P["base_n"], P["base_seed"])
+    x = np.concatenate([base, np.array([p["x"] for p in probes], np.float32)])
+    g = np.concatenate([orc.uniform_f32(P["base_n"], 0.5, 1.5, 606),
+                        np.array([p["g"] for p in probes], np.float32)])
+    n, eps = x.size, P["eps"]
+    got = orc.rmsnorm_forward(np.stack([x, x[::-1].copy()]), g, eps)
+    g64 = g.astype(np.float64)
+    x64 = x.astype(np.float64)
+    rms = math.sqrt(_seq_sum_sq(x64) / n + eps)
+    ref = ((x64 / rms) * g64).astype(np.float32)
+    alt = ((x64 * (1.0 / rms)) * g64).astype(np.float32)
+    tail = slice(P["base_n"], None)
+    assert np.all(ref[tail].view(np.uint32) != alt[tail].view(np.uint32)), \
+        "a probe no longer separates division from the reciprocal"
+    assert np.array_equal(got[0].view(np.uint32), ref.view(np.uint32))
+    # second row (reversed: another sum order) still follows the formula
+    xr = x64[::-1]
+    rr = math.sqrt(_seq_sum_sq(xr) / n + eps)
+    assert np.array_equal(got[1].view(np.uint32), ((xr / rr) * g64).astype(np.float32).view(np.uint32))
+
+
+def test_norm_sums_are_sequential(orc):
+    # every norm sums its squares in element order: a row whose pairwise and
+    # sequential sums differ must follow the sequential one
+    n = 4096
+    x = orc.normal_f32(n, 607) * np.float32(1e3)
+    x[::97] = np.float32(3e-4)
+    x64 = x.astype(np.float64)
+    seq = _seq_sum_sq(x64)
+    assert seq != float(np.sum(x64 * x64)) or seq != math.fsum(x64 * x64)
+    scale = 1.0 / math.sqrt(seq / n + 1e-5)
+    want = (x64 * scale).astype(np.float32)
+    got = orc.bitnet_rmsnorm_row(x, None, 1e-5)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 def test_rmsnorm_layer_closed_form(orc):
     x = np.full((2, 8), 3.0, np.float32)
     y = orc.rmsnorm_forward(x, np.ones(8, np.float32), eps=1e-6)
