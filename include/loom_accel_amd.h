@@ -205,12 +205,26 @@ typedef struct loom_amd_block_weights {
     const float* bias_o;          /* hidden, optional */
 } loom_amd_block_weights;
 
-/* Optional device copies of block intermediates (rows = batch*seq). */
+/* Optional device copies of block intermediates (rows = batch*seq), every
+ * field optional.  Requesting taps does not change which kernels run: each
+ * stage writes its tap from the kernel that computes it. */
 typedef struct loom_amd_block_taps {
-    float* y1;    /* rows x hidden: RMSNorm1 output */
-    double* q;    /* rows x q_dim: Q after bias and RoPE */
-    double* attn; /* rows x q_dim: attention output before the inner norm */
-    float* mid;   /* rows x hidden: x after the attention residual */
+    float* y1;         /* rows x hidden: RMSNorm1 output */
+    double* q;         /* rows x q_dim: Q after bias and RoPE */
+    double* attn;      /* rows x q_dim: attention output before the inner norm */
+    float* mid;        /* rows x hidden: x after the attention residual */
+    int8_t* xq1;       /* rows x hidden: int8 RMSNorm1 rows (Q/K/V input) */
+    float* amax1;      /* rows: their activation absmax (floored at 1e-5) */
+    double* attn_norm; /* rows x q_dim: attention after the MHA inner norm */
+    int8_t* aq;        /* rows x q_dim: its int8 rows (O projection input) */
+    float* aamax;      /* rows */
+    float* y2;         /* rows x hidden: RMSNorm2 output */
+    int8_t* xq2;       /* rows x hidden: its int8 rows (gate/up input) */
+    float* amax2;      /* rows */
+    float* h;          /* rows x intermediate: gate product before the inner norm */
+    float* hn;         /* rows x intermediate: after the SwiGLU inner norm (loom's preAct) */
+    int8_t* hq;        /* rows x intermediate: its int8 rows (down input) */
+    float* hamax;      /* rows */
 } loom_amd_block_taps;
 
 /* Build a block on device: stacks Q|K|V into one projection, allocates the

@@ -57,7 +57,10 @@ class BlockWeights(C.Structure):
 
 
 class BlockTaps(C.Structure):
-    _fields_ = [("y1", P), ("q", P), ("attn", P), ("mid", P)]
+    """loom_amd_block_taps."""
+    _fields_ = [("y1", P), ("q", P), ("attn", P), ("mid", P), ("xq1", P), ("amax1", P),
+                ("attn_norm", P), ("aq", P), ("aamax", P), ("y2", P), ("xq2", P), ("amax2", P),
+                ("h", P), ("hn", P), ("hq", P), ("hamax", P)]
 
 
 class ModelDesc(C.Structure):

@@ -977,6 +977,7 @@ struct RopeArgs {
     const float* bk;
     const float* bv;
     double theta;
+    double* q_tap;  // debug tap: Q rows after bias and RoPE (rows x q_dim), written by chunk 0
 };
 
 template <int HD, bool ROPE>
@@ -1099,12 +1100,17 @@ __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict_
         if (act) {
             if (ROPE) {
                 const double os = output_scale(ra.sq, am);
+                double* qt = ra.q_tap && chunk == 0 ? ra.q_tap + (size_t)row * q_dim + (size_t)h * HD : nullptr;
                 if (g0 == 0) {  // operands loaded with the K/V rows
                     if (lane < HD / 2) {
                         double o0, o1;
                         q_pair_v(qa0, qa1, os, ra.bq != nullptr, qb0, qb1, rc[lane], rsn[lane], &o0, &o1);
                         qs[wave][lane] = o0;
                         qs[wave][lane + HD / 2] = o1;
+                        if (qt) {
+                            qt[lane] = o0;
+                            qt[lane + HD / 2] = o1;
+                        }
                     }
                 } else {
                     for (int d = lane; d < HD / 2; d += 64) {
@@ -1113,6 +1119,10 @@ __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict_
                         q_pair(ar, os, ra.bq, j0, j1, rc[d], rsn[d], &o0, &o1);
                         qs[wave][d] = o0;
                         qs[wave][d + HD / 2] = o1;
+                        if (qt) {
+                            qt[d] = o0;
+                            qt[d + HD / 2] = o1;
+                        }
                     }
                 }
             } else {
@@ -1574,13 +1584,13 @@ hipError_t launch_attention_rope(const int32_t* acc, const float* amax, float sq
                                  const float* bq, const float* bk, const float* bv, double theta,
                                  int batch, const int* pos0, int msl, int span, int heads,
                                  int kv_heads, int hd, float* cache_k, float* cache_v,
-                                 double* scratch, double* out, hipStream_t s) {
+                                 double* scratch, double* out, hipStream_t s, double* q_tap) {
     if (batch <= 0) return hipSuccess;
     if (!attention_rope_ok(1, hd, 0, span) || span > msl || !scratch) return hipErrorInvalidValue;
     if (kv_heads <= 0 || heads % kv_heads != 0 || batch > kSplitMaxRows) return hipErrorInvalidValue;
     if (theta <= 0.0) theta = 10000.0;
     const DecodeScratch sc = decode_scratch(scratch, batch, heads, hd, span);
-    const RopeArgs ra{acc, amax, sq, sk, sv, bq, bk, bv, theta};
+    const RopeArgs ra{acc, amax, sq, sk, sv, bq, bk, bv, theta, q_tap};
     const dim3 g(kv_heads, attn_nchunk32(span), batch), gc(heads, hd / 32, batch);
     if (hd == 128) {
         hipLaunchKernelGGL((attn_gqa_kernel<128, true>), g, dim3(256), 0, s, nullptr, cache_k, cache_v,

@@ -43,7 +43,8 @@ hipError_t launch_attention_rope(const int32_t* acc, const float* amax, float sq
                                  const float* bq, const float* bk, const float* bv, double theta,
                                  int batch, const int* pos0, int msl, int span, int heads,
                                  int kv_heads, int hd, float* cache_k, float* cache_v,
-                                 double* scratch, double* out, hipStream_t s);
+                                 double* scratch, double* out, hipStream_t s,
+                                 double* q_tap = nullptr);
 hipError_t launch_attention(const double* q, const float* cache_k, const float* cache_v,
                             int batch, int seq, const int* pos0, int msl, int span, int heads,
                             int kv_heads, int hd, int strict, double* scratch, double* out,

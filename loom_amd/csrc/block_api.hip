@@ -22,6 +22,7 @@ struct BlockDev {
     double theta = 10000.0, norm_eps = 0.0, attn_eps = 0.0, ffn_eps = 0.0;
     int activation = 1, strict = 1;
     bool fuse_rope = true;  // fast decode: Q/K/V epilogue inside the attention launch
+    bool fuse_norm = true;  // decode: row norms inside the consuming matmul
     Matrix qkv, o, gate, up, down;  // tiles point into `weights`
     float sq = 1.0f, sk = 1.0f, sv = 1.0f;
     float *norm1 = nullptr, *norm2 = nullptr, *attn_norm = nullptr, *ffn_norm = nullptr;
@@ -188,6 +189,9 @@ static int build_block(int device, const loom_amd_block_desc* d, const loom_amd_
     // decode (the tests compare both paths)
     const char* unfused = getenv("LOOM_AMD_UNFUSED_ROPE");
     B->fuse_rope = !(unfused && unfused[0] == '1');
+    // LOOM_AMD_UNFUSED_NORM=1 keeps the separate norm launches in decode
+    const char* unfused_norm = getenv("LOOM_AMD_UNFUSED_NORM");
+    B->fuse_norm = !(unfused_norm && unfused_norm[0] == '1');
     const int H = B->hidden;
     if (expect_shape(w->q, "q", B->q_dim, H, device) || expect_shape(w->k, "k", B->kv_dim, H, device) ||
         expect_shape(w->v, "v", B->kv_dim, H, device) || expect_shape(w->o, "o", H, B->q_dim, device) ||
@@ -285,11 +289,20 @@ static hipError_t tap_copy(void* dst, const void* src, size_t bytes, hipStream_t
     return hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s);
 }
 
+// int8 rows of a padded workspace (ld bytes apart) into a dense tap (n bytes apart).
+static hipError_t tap_rows(int8_t* dst, const int8_t* src, int ld, int n, int rows, hipStream_t s) {
+    if (!dst) return hipSuccess;
+    return hipMemcpy2DAsync(dst, (size_t)n, src, (size_t)ld, (size_t)n, rows, hipMemcpyDeviceToDevice, s);
+}
+
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // Enqueues one block forward on x (rows = batch*seq) at device position *pos.
-// Without taps, few rows take the decode path: each row norm runs inside the
-// matmul that consumes it (launch_matmul_norm).
+// Few rows take the decode path: each row norm runs inside the matmul that
+// consumes it (launch_matmul_norm).  Taps never change the path: every stage
+// writes its tap from the kernel that computes it (workgroup 0 of a
+// norm-fused matmul, the chunk-0 workgroups of the fused decode attention) or
+// by a copy of the workspace it leaves behind.
 static int block_forward_dev(const BlockDev& B, const Workspace& W, float* x, int batch, int seq,
                              const int* pos, const loom_amd_block_taps* taps, hipStream_t s) {
     const int R = batch * seq;
@@ -297,46 +310,53 @@ static int block_forward_dev(const BlockDev& B, const Workspace& W, float* x, in
     const double rms_eps = B.norm_eps > 0 ? B.norm_eps : 1e-6;   // RMSNormForwardPolymorphic
     const double attn_eps = B.attn_eps > 0 ? B.attn_eps : 1e-5;  // bitNetRMSNormFloat64Weighted
     const double ffn_eps = B.ffn_eps > 0 ? B.ffn_eps : 1e-5;     // bitNetRMSNormTensorRowWeighted
-    const bool fuse = taps == nullptr && aligned16(x);
+    const loom_amd_block_taps none{};
+    const loom_amd_block_taps& T = taps ? *taps : none;
+    const bool fuse = B.fuse_norm && aligned16(x);
     hipError_t e;
+#define TAP(call)                                                  \
+    do {                                                           \
+        if ((e = (call)) != hipSuccess) return fail_hip("block taps", e); \
+    } while (0)
     // x := x + MHA(RMSNorm1(x))
     {
         Epilogue ep;
         ep.kind = EPI_ACC;
         ep.acc0 = W.acc;
         if (fuse && norm_fused_ok(R, B.hidden, B.strict, true)) {
+            NormTaps nt;
+            nt.rows = T.y1;
+            nt.xq = T.xq1;
             e = launch_matmul_norm(&B.qkv, nullptr, x, nullptr, R, NORM_RMS, B.strict, B.norm1,
-                                   rms_eps, ep, W.amax, s);
+                                   rms_eps, ep, W.amax, s, &nt);
             if (e != hipSuccess) return fail_hip("block rmsnorm1 + qkv projection", e);
         } else {
-            e = launch_rmsnorm_quant(x, B.hidden, R, B.hidden, B.norm1, rms_eps, B.strict,
-                                     taps ? taps->y1 : nullptr, W.xq, ldh, W.amax, W.xsum, s);
+            e = launch_rmsnorm_quant(x, B.hidden, R, B.hidden, B.norm1, rms_eps, B.strict, T.y1,
+                                     W.xq, ldh, W.amax, W.xsum, s);
             if (e != hipSuccess) return fail_hip("block rmsnorm1", e);
+            TAP(tap_rows(T.xq1, W.xq, ldh, B.hidden, R, s));
             QuantAct a{W.xq, ldh, W.amax, W.xsum};
             e = launch_matmul(&B.qkv, nullptr, a, R, ep, s);
             if (e != hipSuccess) return fail_hip("block qkv projection", e);
         }
+        TAP(tap_copy(T.amax1, W.amax, (size_t)R * 4, s));
     }
-    if (!taps && B.fuse_rope && batch <= kSplitMaxRows && attention_rope_ok(seq, B.hd, B.strict, B.span())) {
+    if (B.fuse_rope && batch <= kSplitMaxRows && attention_rope_ok(seq, B.hd, B.strict, B.span())) {
         // fast decode: the Q/K/V epilogue runs inside the attention launch
         e = launch_attention_rope(W.acc, W.amax, B.sq, B.sk, B.sv, B.bq, B.bk, B.bv, B.theta, batch, pos,
                                   B.msl, B.span(), B.heads, B.kv_heads, B.hd, B.cache_k, B.cache_v,
-                                  W.scores, W.attn, s);
+                                  W.scores, W.attn, s, T.q);
         if (e != hipSuccess) return fail_hip("block attention", e);
     } else {
         e = launch_qkv_rope(W.acc, W.amax, B.sq, B.sk, B.sv, B.bq, B.bk, B.bv, batch, seq, pos, B.msl,
                             B.heads, B.kv_heads, B.hd, B.theta, W.q, B.cache_k, B.cache_v, s);
         if (e != hipSuccess) return fail_hip("block qkv rope", e);
-        if (taps && (e = tap_copy(taps->q, W.q, (size_t)R * B.q_dim * 8, s)) != hipSuccess) {
-            return fail_hip("block taps", e);
-        }
+        TAP(tap_copy(T.q, W.q, (size_t)R * B.q_dim * 8, s));
         e = launch_attention(W.q, B.cache_k, B.cache_v, batch, seq, pos, B.msl, B.span(), B.heads,
                              B.kv_heads, B.hd, B.strict, W.scores, W.attn, s);
         if (e != hipSuccess) return fail_hip("block attention", e);
     }
-    if (taps && (e = tap_copy(taps->attn, W.attn, (size_t)R * B.q_dim * 8, s)) != hipSuccess) {
-        return fail_hip("block taps", e);
-    }
+    TAP(tap_copy(T.attn, W.attn, (size_t)R * B.q_dim * 8, s));
     {
         Epilogue ep;
         ep.kind = EPI_DENSE;
@@ -345,23 +365,28 @@ static int block_forward_dev(const BlockDev& B, const Workspace& W, float* x, in
         ep.out = x;
         ep.ldo = B.hidden;
         if (fuse && norm_fused_ok(R, B.q_dim, B.strict, true)) {
+            NormTaps nt;
+            nt.rows = T.attn_norm;
+            nt.xq = T.aq;
+            nt.amax = T.aamax;
             e = launch_matmul_norm(&B.o, nullptr, nullptr, W.attn, R, NORM_INNER_F64, B.strict,
-                                   B.attn_norm, attn_eps, ep, nullptr, s);
+                                   B.attn_norm, attn_eps, ep, nullptr, s, &nt);
             if (e != hipSuccess) return fail_hip("block attention inner norm + o projection", e);
         } else {
             // (only the int8 rows feed the O projection: the normalized fp64
-            // rows are not written back)
+            // rows are written back only for the tap)
             e = launch_norm_quant_f64(W.attn, R, B.q_dim, B.attn_norm, attn_eps, B.strict, nullptr,
-                                      W.aq, ldqd, W.amax2, W.xsum2, s, false);
+                                      W.aq, ldqd, W.amax2, W.xsum2, s, T.attn_norm != nullptr);
             if (e != hipSuccess) return fail_hip("block attention inner norm", e);
+            TAP(tap_copy(T.attn_norm, W.attn, (size_t)R * B.q_dim * 8, s));
+            TAP(tap_rows(T.aq, W.aq, ldqd, B.q_dim, R, s));
+            TAP(tap_copy(T.aamax, W.amax2, (size_t)R * 4, s));
             QuantAct a{W.aq, ldqd, W.amax2, W.xsum2};
             e = launch_matmul(&B.o, nullptr, a, R, ep, s);
             if (e != hipSuccess) return fail_hip("block o projection", e);
         }
     }
-    if (taps && (e = tap_copy(taps->mid, x, (size_t)R * B.hidden * 4, s)) != hipSuccess) {
-        return fail_hip("block taps", e);
-    }
+    TAP(tap_copy(T.mid, x, (size_t)R * B.hidden * 4, s));
     // x := x + SwiGLU(RMSNorm2(x))
     {
         Epilogue ep;
@@ -370,18 +395,25 @@ static int block_forward_dev(const BlockDev& B, const Workspace& W, float* x, in
         ep.out = W.h;
         ep.ldo = B.inter;
         if (fuse && norm_fused_ok(R, B.hidden, B.strict, true)) {
+            NormTaps nt;
+            nt.rows = T.y2;
+            nt.xq = T.xq2;
+            nt.amax = T.amax2;
             e = launch_matmul_norm(&B.gate, &B.up, x, nullptr, R, NORM_RMS, B.strict, B.norm2,
-                                   rms_eps, ep, nullptr, s);
+                                   rms_eps, ep, nullptr, s, &nt);
             if (e != hipSuccess) return fail_hip("block rmsnorm2 + gate/up", e);
         } else {
-            e = launch_rmsnorm_quant(x, B.hidden, R, B.hidden, B.norm2, rms_eps, B.strict, nullptr,
+            e = launch_rmsnorm_quant(x, B.hidden, R, B.hidden, B.norm2, rms_eps, B.strict, T.y2,
                                      W.xq, ldh, W.amax, W.xsum, s);
             if (e != hipSuccess) return fail_hip("block rmsnorm2", e);
+            TAP(tap_rows(T.xq2, W.xq, ldh, B.hidden, R, s));
+            TAP(tap_copy(T.amax2, W.amax, (size_t)R * 4, s));
             QuantAct a{W.xq, ldh, W.amax, W.xsum};
             e = launch_matmul(&B.gate, &B.up, a, R, ep, s);
             if (e != hipSuccess) return fail_hip("block gate/up", e);
         }
     }
+    TAP(tap_copy(T.h, W.h, (size_t)R * B.inter * 4, s));
     {
         Epilogue ep;
         ep.kind = EPI_DENSE;
@@ -389,19 +421,28 @@ static int block_forward_dev(const BlockDev& B, const Workspace& W, float* x, in
         ep.out = x;
         ep.ldo = B.hidden;
         if (fuse && norm_fused_ok(R, B.inter, B.strict, true)) {
+            NormTaps nt;
+            nt.rows = T.hn;
+            nt.xq = T.hq;
+            nt.amax = T.hamax;
             e = launch_matmul_norm(&B.down, nullptr, W.h, nullptr, R, NORM_INNER_F32, B.strict,
-                                   B.ffn_norm, ffn_eps, ep, nullptr, s);
+                                   B.ffn_norm, ffn_eps, ep, nullptr, s, &nt);
             if (e != hipSuccess) return fail_hip("block ffn inner norm + down", e);
         } else {
-            // (only the int8 rows feed the down projection)
+            // (only the int8 rows feed the down projection; the normalized
+            // rows are written back only for the tap)
             e = launch_norm_quant(W.h, B.inter, R, B.inter, B.ffn_norm, ffn_eps, B.strict, W.hq, ldi,
-                                  W.amax3, W.xsum3, s, false);
+                                  W.amax3, W.xsum3, s, T.hn != nullptr);
             if (e != hipSuccess) return fail_hip("block ffn inner norm", e);
+            TAP(tap_copy(T.hn, W.h, (size_t)R * B.inter * 4, s));
+            TAP(tap_rows(T.hq, W.hq, ldi, B.inter, R, s));
+            TAP(tap_copy(T.hamax, W.amax3, (size_t)R * 4, s));
             QuantAct a{W.hq, ldi, W.amax3, W.xsum3};
             e = launch_matmul(&B.down, nullptr, a, R, ep, s);
             if (e != hipSuccess) return fail_hip("block down", e);
         }
     }
+#undef TAP
     return 0;
 }
 

@@ -341,6 +341,7 @@ struct MatArgs {
     const double* x64;  // fp64 rows (NORM_INNER_F64), ldx = K
     const float* nw;    // gain / inner-norm weight (length K), null = ones
     double neps;        // eps of the norm
+    void* norm_tap;     // normalized rows (M x K; fp32, fp64 for NORM_INNER_F64), workgroup 0 (optional)
     EpiDev e;
 };
 

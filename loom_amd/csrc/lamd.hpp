@@ -113,13 +113,22 @@ enum RowNorm : int {
 // Whether launch_matmul_norm takes m rows of width k (x16 is the row pointer's
 // 16-byte alignment).
 bool norm_fused_ok(int m, int k, int strict, bool x16);
+// Debug taps of a norm-fused matmul, written by workgroup 0 (all optional):
+// the normalized rows (M x K, fp32, or fp64 for NORM_INNER_F64), their int8
+// quantization (M x K) and activation absmax (M, floored at 1e-5).
+struct NormTaps {
+    void* rows = nullptr;
+    int8_t* xq = nullptr;
+    float* amax = nullptr;
+};
 // Matmul whose workgroups normalize (mode, strict summation order, gain nw,
 // eps) and quantize the rows x (fp32) or x64 (fp64, NORM_INNER_F64)
 // themselves.  eps is used as given.  amax_tap (optional, M floats) receives
 // the rows' activation absmax.
 hipError_t launch_matmul_norm(const Matrix* w0, const Matrix* w1, const float* x, const double* x64,
                               int m, int mode, int strict, const float* nw, double eps,
-                              const Epilogue& epi, float* amax_tap, hipStream_t s);
+                              const Epilogue& epi, float* amax_tap, hipStream_t s,
+                              const NormTaps* taps = nullptr);
 
 // Inner RMSNorm + requantization of SwiGLU rows (poly/bitnet_cpu.go:893-913 then
 // poly/bitnet_cpu.go:97-106).  In place on h (M x n fp32, row stride ldh) unless

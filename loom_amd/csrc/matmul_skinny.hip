@@ -225,6 +225,26 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
                     }
                 }
             }
+            if (p.norm_tap && blockIdx.x == 0) {
+                // debug tap: the normalized rows as this workgroup quantizes them
+#pragma unroll
+                for (int j = 0; j < FV; ++j) {
+                    const int idx = tid + j * T;
+                    if (idx < n4) {
+                        const int row = row_of<MR>(idx, row4);
+                        const size_t at = (size_t)row * k + 4 * (size_t)(idx - row * row4);
+                        if (F64) {
+                            double* t = (double*)p.norm_tap + at;
+                            t[0] = xd[j][0];
+                            t[1] = xd[j][1];
+                            t[2] = xd[j][2];
+                            t[3] = xd[j][3];
+                        } else {
+                            *(float4*)((float*)p.norm_tap + at) = xv[j];
+                        }
+                    }
+                }
+            }
             __syncthreads();
         }
         // bitNetActivationMaxAbs per row (poly/bitnet_cpu.go:45-71).
@@ -804,7 +824,8 @@ static hipError_t launch_norm_st(const MatArgs& p, int strict, size_t shm, hipSt
 
 hipError_t launch_matmul_norm(const Matrix* w0, const Matrix* w1, const float* x, const double* x64,
                               int m, int mode, int strict, const float* nw, double eps,
-                              const Epilogue& epi, float* amax_tap, hipStream_t s) {
+                              const Epilogue& epi, float* amax_tap, hipStream_t s,
+                              const NormTaps* taps) {
     if (m <= 0) return hipSuccess;
     const void* rows = mode == NORM_INNER_F64 ? (const void*)x64 : (const void*)x;
     if (!rows || !norm_fused_ok(m, w0->cols, strict, ((uintptr_t)rows & 15) == 0)) {
@@ -817,6 +838,11 @@ hipError_t launch_matmul_norm(const Matrix* w0, const Matrix* w1, const float* x
     p.nw = nw;
     p.neps = eps;
     p.amax_tap = amax_tap;
+    if (taps) {
+        p.norm_tap = taps->rows;
+        p.xq_tap = taps->xq;
+        if (taps->amax && !amax_tap) p.amax_tap = taps->amax;
+    }
     p.ldq = pad_cols(w0->cols);
     const size_t shm = norm_lds(m, w0->cols, strict);
     const bool two = epi.kind == EPI_SWIGLU;

@@ -98,10 +98,30 @@ class BlockWeights:
 
 @dataclass
 class BlockTaps:
-    y1: object = None    # rows x hidden fp32: RMSNorm1 output
-    q: object = None     # rows x q_dim fp64: Q after bias and RoPE
-    attn: object = None  # rows x q_dim fp64: attention before the inner norm
-    mid: object = None   # rows x hidden fp32: x after the attention residual
+    """Device copies of one block call's intermediates (loom_amd_block_taps).
+    Requesting them does not change which kernels run."""
+    y1: object = None         # rows x hidden fp32: RMSNorm1 output
+    q: object = None          # rows x q_dim fp64: Q after bias and RoPE
+    attn: object = None       # rows x q_dim fp64: attention before the inner norm
+    mid: object = None        # rows x hidden fp32: x after the attention residual
+    xq1: object = None        # rows x hidden int8: quantized RMSNorm1 rows
+    amax1: object = None      # rows fp32
+    attn_norm: object = None  # rows x q_dim fp64: attention after the inner norm
+    aq: object = None         # rows x q_dim int8
+    aamax: object = None      # rows fp32
+    y2: object = None         # rows x hidden fp32: RMSNorm2 output
+    xq2: object = None        # rows x hidden int8
+    amax2: object = None      # rows fp32
+    h: object = None          # rows x inter fp32: gate product before the inner norm
+    hn: object = None         # rows x inter fp32: after the inner norm
+    hq: object = None         # rows x inter int8
+    hamax: object = None      # rows fp32
+
+    FIELDS = ("y1", "q", "attn", "mid", "xq1", "amax1", "attn_norm", "aq", "aamax", "y2", "xq2",
+              "amax2", "h", "hn", "hq", "hamax")
+
+    def numpy(self) -> dict:
+        return {f: getattr(self, f).cpu().numpy() for f in self.FIELDS}
 
 
 class BitNetBlock:
@@ -141,13 +161,18 @@ class BitNetBlock:
         tp = None
         if taps:
             dev = x.device
-            t = BlockTaps(
-                y1=torch.empty(rows, self.cfg.hidden, dtype=torch.float32, device=dev),
-                q=torch.empty(rows, self.cfg.q_dim, dtype=torch.float64, device=dev),
-                attn=torch.empty(rows, self.cfg.q_dim, dtype=torch.float64, device=dev),
-                mid=torch.empty(rows, self.cfg.hidden, dtype=torch.float32, device=dev))
-            tp = C.byref(_lib.BlockTaps(t.y1.data_ptr(), t.q.data_ptr(), t.attn.data_ptr(),
-                                        t.mid.data_ptr()))
+            H, Q, I = self.cfg.hidden, self.cfg.q_dim, self.cfg.intermediate
+
+            def e(*shape, dt=torch.float32):
+                return torch.empty(*shape, dtype=dt, device=dev)
+
+            f64, i8 = torch.float64, torch.int8
+            t = BlockTaps(y1=e(rows, H), q=e(rows, Q, dt=f64), attn=e(rows, Q, dt=f64),
+                          mid=e(rows, H), xq1=e(rows, H, dt=i8), amax1=e(rows),
+                          attn_norm=e(rows, Q, dt=f64), aq=e(rows, Q, dt=i8), aamax=e(rows),
+                          y2=e(rows, H), xq2=e(rows, H, dt=i8), amax2=e(rows),
+                          h=e(rows, I), hn=e(rows, I), hq=e(rows, I, dt=i8), hamax=e(rows))
+            tp = C.byref(_lib.BlockTaps(*(getattr(t, f).data_ptr() for f in BlockTaps.FIELDS)))
         check(_lib.lib().loom_amd_block_forward(self._h, C.c_void_p(x.data_ptr()), batch, seq, tp,
                                                 _stream(self.device)), "block_forward")
         return x, t

@@ -534,6 +534,45 @@ void orc_bitnet_rmsnorm_f64(double* data, int n, const float* weight, double eps
     }
 }
 
+/* Stage of the MHA output projection (poly/mha.go:362-368) and the SwiGLU
+ * down projection (poly/swiglu.go:316-320) from given int8 rows: per row s,
+ * out = fp32(bitNetTernaryMatVecQuantized(xq[s], amax[s]) + bias), the bias
+ * (0 when NULL) added in fp64 as both sites add it. */
+void orc_dense_quantized(const orc_matrix* w, const int8_t* xq, const float* amax, int m,
+                         const float* bias, int simd, int workers, float* out) {
+    double* t = (double*)malloc((size_t)w->rows * sizeof(double));
+    for (int s = 0; s < m; s++) {
+        matvec_quantized(w, xq + (size_t)s * w->cols, amax[s], simd, workers, t, NULL);
+        for (int i = 0; i < w->rows; i++) {
+            out[(size_t)s * w->rows + i] = (float)(t[i] + (bias ? (double)bias[i] : 0.0));
+        }
+    }
+    free(t);
+}
+
+/* Gate/up stage of SwiGLUForwardPackedTernaryCPU (poly/swiglu.go:303-312)
+ * from given int8 rows: h = fp32(swigluGateProduct(g + bias_g, u + bias_u)),
+ * bias = [gate inter | up inter] or NULL. */
+void orc_swiglu_gate_rows(const orc_matrix* gate, const orc_matrix* up, const float* bias,
+                          int activation, const int8_t* xq, const float* amax, int m, int simd,
+                          int workers, float* h) {
+    const int inter = gate->rows;
+    double* g = (double*)malloc((size_t)inter * sizeof(double));
+    double* u = (double*)malloc((size_t)inter * sizeof(double));
+    for (int s = 0; s < m; s++) {
+        const int8_t* row = xq + (size_t)s * gate->cols;
+        matvec_quantized(gate, row, amax[s], simd, workers, g, NULL);
+        matvec_quantized(up, row, amax[s], simd, workers, u, NULL);
+        for (int o = 0; o < inter; o++) {
+            double gv = g[o] + (bias ? (double)bias[o] : 0.0);
+            double uv = u[o] + (bias ? (double)bias[inter + o] : 0.0);
+            h[(size_t)s * inter + o] = (float)orc_swiglu_gate_product(gv, uv, activation);
+        }
+    }
+    free(u);
+    free(g);
+}
+
 /* SwiGLUForwardPackedTernaryCPU (poly/swiglu.go:270-322). */
 void orc_swiglu_forward(const orc_matrix* gate, const orc_matrix* up,
                         const orc_matrix* down, const float* bias,
@@ -768,10 +807,16 @@ void orc_attention(const double* Q, const float* cache_k, const float* cache_v, 
     const int q_dim = heads * hd, kv_dim = kv_heads * hd;
     const int per_kv = heads / kv_heads;
     const double scale = 1.0 / sqrt((double)hd);
-    double* scores = (double*)malloc((size_t)(seq_base + seq) * sizeof(double));
-    for (int s = 0; s < seq; s++) {
-        const int total = seq_base + s;
-        for (int h = 0; h < heads; h++) {
+    /* (query, head) pairs are independent: threads split the pairs, and each
+     * pair runs the reference's loops unchanged, so the results do not depend
+     * on the thread count */
+#pragma omp parallel
+    {
+        double* scores = (double*)malloc((size_t)(seq_base + seq) * sizeof(double));
+#pragma omp for schedule(dynamic, 1)
+        for (long sh = 0; sh < (long)seq * heads; sh++) {
+            const int s = (int)(sh / heads), h = (int)(sh % heads);
+            const int total = seq_base + s;
             const int kvh = h / per_kv;
             double max_score = -1e9;
             for (int kp = 0; kp <= total; kp++) {
@@ -796,8 +841,8 @@ void orc_attention(const double* Q, const float* cache_k, const float* cache_v, 
                 attn[(size_t)s * q_dim + (size_t)h * hd + d] = sum / exp_sum;
             }
         }
+        free(scores);
     }
-    free(scores);
 }
 
 /* Output stage of MHAForwardPackedTernaryCPU (poly/mha.go:356-368): per row,
@@ -828,8 +873,8 @@ void orc_attn_out(const orc_matrix* o, const float* bias_o, const float* inner_n
  * The KV cache is a ring of msl rows (pos % msl), prepared as
  * mhaPrepareKVForForward does (poly/mha_layout.go:62-70): a pass that is not
  * a warm single-token step resets kv_offset to 0. */
-void orc_mha_forward(orc_mha* L, const float* in, int seq, int simd, int workers,
-                     float* pre, float* post, double* q_out, double* attn_out) {
+void orc_mha_project(orc_mha* L, const float* in, int seq, int seq_base, int simd, int workers,
+                     double* Q) {
     const int d_model = L->d_model;
     const int heads = L->num_heads;
     const int kv_heads = L->num_kv_heads > 0 ? L->num_kv_heads : heads;
@@ -837,14 +882,6 @@ void orc_mha_forward(orc_mha* L, const float* in, int seq, int simd, int workers
     const int q_dim = heads * hd;
     const int kv_dim = kv_heads * hd;
     const int msl = L->msl > 0 ? L->msl : 512;
-    const int incremental = (seq == 1 && L->kv_offset > 0);
-    if (!incremental) {
-        memset(L->cache_k, 0, (size_t)msl * kv_dim * sizeof(float));
-        memset(L->cache_v, 0, (size_t)msl * kv_dim * sizeof(float));
-        L->kv_offset = 0;
-    }
-    const int seq_base = L->kv_offset;
-    double* Q = (double*)malloc((size_t)seq * q_dim * sizeof(double));
     double* tq = (double*)malloc((size_t)q_dim * sizeof(double));
     double* tk = (double*)malloc((size_t)kv_dim * sizeof(double));
     double* tv = (double*)malloc((size_t)kv_dim * sizeof(double));
@@ -888,6 +925,29 @@ void orc_mha_forward(orc_mha* L, const float* in, int seq, int simd, int workers
             }
         }
     }
+    free(xq);
+    free(tv);
+    free(tk);
+    free(tq);
+}
+
+void orc_mha_forward(orc_mha* L, const float* in, int seq, int simd, int workers,
+                     float* pre, float* post, double* q_out, double* attn_out) {
+    const int heads = L->num_heads;
+    const int kv_heads = L->num_kv_heads > 0 ? L->num_kv_heads : heads;
+    const int hd = L->head_dim;
+    const int q_dim = heads * hd;
+    const int kv_dim = kv_heads * hd;
+    const int msl = L->msl > 0 ? L->msl : 512;
+    const int incremental = (seq == 1 && L->kv_offset > 0);
+    if (!incremental) {
+        memset(L->cache_k, 0, (size_t)msl * kv_dim * sizeof(float));
+        memset(L->cache_v, 0, (size_t)msl * kv_dim * sizeof(float));
+        L->kv_offset = 0;
+    }
+    const int seq_base = L->kv_offset;
+    double* Q = (double*)malloc((size_t)seq * q_dim * sizeof(double));
+    orc_mha_project(L, in, seq, seq_base, simd, workers, Q);
     if (q_out) memcpy(q_out, Q, (size_t)seq * q_dim * sizeof(double));
     double* attn = (double*)malloc((size_t)seq * q_dim * sizeof(double));
     orc_attention(Q, L->cache_k, L->cache_v, seq, seq_base, msl, heads, kv_heads, hd, attn);
@@ -896,10 +956,6 @@ void orc_mha_forward(orc_mha* L, const float* in, int seq, int simd, int workers
                  post);
     L->kv_offset = seq_base + seq;
     free(attn);
-    free(xq);
-    free(tv);
-    free(tk);
-    free(tq);
     free(Q);
 }
 

@@ -146,8 +146,22 @@ void orc_attention(const double* Q, const float* cache_k, const float* cache_v, 
 void orc_attn_out(const orc_matrix* o, const float* bias_o, const float* inner_norm, double eps,
                   double* attn, int seq, int q_dim, int simd, int workers, float* pre,
                   float* post);
+/* Projection stage of MHAForwardPackedTernaryCPU (poly/mha.go:262-314) for
+ * `seq` rows at positions seq_base + s: shared quantization, Q (fp64 + bias),
+ * K/V rows (fp32 + bias) into the ring caches, RoPE on Q and the cached K.
+ * Q receives seq x q_dim; kv_offset is not changed. */
+void orc_mha_project(orc_mha* L, const float* in, int seq, int seq_base, int simd, int workers,
+                     double* Q);
 void orc_mha_forward(orc_mha* L, const float* in, int seq, int simd, int workers,
                      float* pre, float* post, double* q_out, double* attn_out);
+
+/* Stages from given int8 rows (for stage-wise checks): the output / down
+ * projection with its fp64 bias add, and the SwiGLU gate product rows. */
+void orc_dense_quantized(const orc_matrix* w, const int8_t* xq, const float* amax, int m,
+                         const float* bias, int simd, int workers, float* out);
+void orc_swiglu_gate_rows(const orc_matrix* gate, const orc_matrix* up, const float* bias,
+                          int activation, const int8_t* xq, const float* amax, int m, int simd,
+                          int workers, float* h);
 
 typedef struct orc_block {
     int hidden;

@@ -79,6 +79,9 @@ def _declare(L: C.CDLL) -> None:
         "orc_attention": (None, [P, P, P, i, i, i, i, i, i, P]),
         "orc_attn_out": (None, [P, P, P, d, P, i, i, i, i, P, P]),
         "orc_mha_forward": (None, [P, P, i, i, i, P, P, P, P]),
+        "orc_mha_project": (None, [P, P, i, i, i, i, P]),
+        "orc_dense_quantized": (None, [P, P, P, i, P, i, i, P]),
+        "orc_swiglu_gate_rows": (None, [P, P, P, i, P, P, i, i, i, P]),
         "orc_block_forward": (None, [P, P, i, i, i]),
         "orc_lm_head_seq": (None, [P, P, i, i, P]),
         "orc_dot_tile": (d, [P, P, i, d]),
@@ -339,6 +342,45 @@ def swiglu_forward(gate: Matrix, up: Matrix, down: Matrix, x: np.ndarray,
     return SwiGLUResult(out, h, xq, amax, hq, hamax, ag, au, ad)
 
 
+def dense_quantized(m: Matrix, xq: np.ndarray, amax: np.ndarray, bias: np.ndarray | None = None,
+                    simd: bool = True, workers: int = 0) -> np.ndarray:
+    """Output / down projection stage from given int8 rows (poly/mha.go:362-368,
+    poly/swiglu.go:316-320): fp32(matvec + bias) per row."""
+    xq = np.ascontiguousarray(xq, np.int8).reshape(-1, m.cols)
+    amax = np.ascontiguousarray(amax, np.float32).reshape(-1)
+    out = np.empty((xq.shape[0], m.rows), np.float32)
+    cm = m._c(simd)
+    bs = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    lib().orc_dense_quantized(C.byref(cm), _p(xq), _p(amax), xq.shape[0], _p(bs), int(simd),
+                              workers or (os.cpu_count() or 1), _p(out))
+    return out
+
+
+def swiglu_gate_rows(gate: Matrix, up: Matrix, xq: np.ndarray, amax: np.ndarray,
+                     activation: int = ACT_SILU, bias: np.ndarray | None = None,
+                     simd: bool = True, workers: int = 0) -> np.ndarray:
+    """Gate/up stage of SwiGLUForwardPackedTernaryCPU (poly/swiglu.go:303-312)
+    from given int8 rows: h = fp32(gate product), before the inner norm."""
+    xq = np.ascontiguousarray(xq, np.int8).reshape(-1, gate.cols)
+    amax = np.ascontiguousarray(amax, np.float32).reshape(-1)
+    h = np.empty((xq.shape[0], gate.rows), np.float32)
+    cg, cu = gate._c(simd), up._c(simd)
+    bs = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    lib().orc_swiglu_gate_rows(C.byref(cg), C.byref(cu), _p(bs), activation, _p(xq), _p(amax),
+                               xq.shape[0], int(simd), workers or (os.cpu_count() or 1), _p(h))
+    return h
+
+
+def quant_rows(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """bitNetQuantizeActivationNumeric / ...Float64 per row (fp32 or fp64 rows)."""
+    x = np.ascontiguousarray(x)
+    q = np.empty(x.shape, np.int8)
+    amax = np.empty(x.shape[0], np.float32)
+    for r in range(x.shape[0]):
+        q[r], amax[r] = quant_act(x[r])
+    return q, amax
+
+
 def swiglu_gate_product(g: float, u: float, activation: int = ACT_SILU) -> float:
     return float(lib().orc_swiglu_gate_product(g, u, activation))
 
@@ -468,6 +510,16 @@ class MHA:
     @property
     def kv_offset(self) -> int:
         return self.c.kv_offset
+
+    def project(self, x: np.ndarray, base: int, workers: int = 0) -> np.ndarray:
+        """Projection stage only (poly/mha.go:262-314): Q/K/V of the rows at
+        positions base.., the K/V rows written into this MHA's caches; returns
+        Q after bias and RoPE (fp64).  kv_offset is left unchanged."""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, self.d_model)
+        q = np.empty((x.shape[0], self.num_heads * self.head_dim), np.float64)
+        lib().orc_mha_project(C.byref(self.c), _p(x), x.shape[0], base, int(self.simd),
+                              workers or (os.cpu_count() or 1), _p(q))
+        return q
 
     def forward(self, x: np.ndarray, workers: int = 0):
         """Returns (pre, post, q_after_rope, attn_before_norm)."""

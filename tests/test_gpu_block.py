@@ -1,20 +1,13 @@
 """Parity of the gfx950 decoder block and decode loop against the CPU oracle
 (loom's MHAForwardPackedTernaryCPU / forwardOnCPUNormal / Generate restated).
 
-Bar, stage by stage (strict norm mode):
-  * RMSNorm outputs, int8 quantization, int32 accumulators, the O projection
-    with its residual and the whole FFN half (ReLU2 gate): bit-exact, each
-    stage fed the GPU's own input to it;
-  * RoPE uses pow/cos/sin and softmax uses exp, whose last fp64 bit differs
-    between libm implementations (Go, glibc, ROCm ocml): Q is checked within
-    1e-12 relative to its row scale (bit-exact at position 0, where the
-    rotation is the identity), cached K within 1 fp32 ulp (V bit-exact), and
-    attention within 1e-12 relative against the oracle fed the GPU's Q and
-    caches;
-  * the LM head is bit-exact (loom's amd64 DotTile order) and the greedy token
-    is the oracle's argmax of the GPU logits.
-End to end, the last-bit libm differences can move an int8 code across a
-rounding boundary, so the whole block is compared with a stated tolerance.
+Every block call is checked stage by stage, each stage fed the GPU's own
+input to it (tests/stages.py states the bar of each stage).  Taps do not
+change which kernels run, so the decode rows are checked on the norm-fused
+matmuls and the fused decode attention that production runs; the staged
+kernels are checked by forcing them (LOOM_AMD_UNFUSED_NORM /
+LOOM_AMD_UNFUSED_ROPE).  The LM head is bit-exact in both of loom's orders
+and the greedy token is the oracle's argmax of the GPU logits.
 Citations are relative to the loom v0.83.0 tree.
 """
 import numpy as np
@@ -22,7 +15,8 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-ACT_SILU, ACT_RELU2 = 1, 6
+from tests.stages import (ACT_RELU2, ACT_SILU, BITNET_2B, SMALL, Shape, Weights, check_stages,  # noqa: F401
+                          run_block_case, to_dev, ulp_diff_f32)
 
 
 @pytest.fixture(scope="module")
@@ -38,157 +32,6 @@ def torch_dev():
 def tf(torch_dev):
     from loom_amd import transformer
     return transformer
-
-
-class Shape:
-    def __init__(self, hidden, heads, kv, hd, inter, msl, theta=500000.0):
-        self.hidden, self.heads, self.kv, self.hd, self.inter, self.msl = hidden, heads, kv, hd, inter, msl
-        self.theta = theta
-        self.q_dim, self.kv_dim = heads * hd, kv * hd
-
-
-SMALL = Shape(256, 4, 2, 64, 512, 64)
-BITNET_2B = Shape(2560, 20, 5, 128, 6912, 640)  # BitNet-b1.58-2B block (config 2)
-
-
-class Weights:
-    """Oracle matrices + fp32 vectors of one block (seeded)."""
-
-    def __init__(self, orc, sh: Shape, seed: int, act: int = ACT_RELU2, bias: bool = False):
-        self.sh, self.act = sh, act
-        self.q = orc.random_matrix(sh.q_dim, sh.hidden, seed)
-        self.k = orc.random_matrix(sh.kv_dim, sh.hidden, seed + 1)
-        self.v = orc.random_matrix(sh.kv_dim, sh.hidden, seed + 2)
-        self.o = orc.random_matrix(sh.hidden, sh.q_dim, seed + 3)
-        self.g = orc.random_matrix(sh.inter, sh.hidden, seed + 4)
-        self.u = orc.random_matrix(sh.inter, sh.hidden, seed + 5)
-        self.d = orc.random_matrix(sh.hidden, sh.inter, seed + 6)
-        self.n1 = orc.uniform_f32(sh.hidden, 0.5, 1.5, seed + 7)
-        self.n2 = orc.uniform_f32(sh.hidden, 0.5, 1.5, seed + 8)
-        self.an = orc.uniform_f32(sh.q_dim, 0.5, 1.5, seed + 9)
-        self.fn = orc.uniform_f32(sh.inter, 0.5, 1.5, seed + 10)
-        self.bias = None
-        if bias:
-            self.bias = [orc.normal_f32(n, seed + 11 + i) * np.float32(0.1)
-                         for i, n in enumerate([sh.q_dim, sh.kv_dim, sh.kv_dim, sh.hidden])]
-
-    def gpu(self, tf):
-        from loom_amd.bitnet import TernaryMatrix
-
-        def m(x):
-            return TernaryMatrix.from_words(x.words, x.rows, x.cols, x.scale)
-
-        b = self.bias or [None] * 4
-        return tf.BlockWeights(m(self.q), m(self.k), m(self.v), m(self.o), m(self.g), m(self.u),
-                               m(self.d), self.n1, self.n2, self.an, self.fn, *b)
-
-    def cfg(self, tf, norm="strict", max_batch=1):
-        sh = self.sh
-        return tf.BlockConfig(sh.hidden, sh.heads, sh.kv, sh.hd, sh.inter, max_seq_len=sh.msl,
-                              max_batch=max_batch, rope_theta=sh.theta, norm_eps=1e-5,
-                              attn_eps=1e-5, ffn_eps=1e-5, ffn_activation=self.act, norm=norm)
-
-    def oracle_mha(self, orc):
-        sh = self.sh
-        m = orc.MHA(self.q, self.k, self.v, self.o, sh.heads, sh.kv, sh.hd, sh.msl,
-                    theta=sh.theta, eps=1e-5, inner_norm=self.an)
-        if self.bias:
-            # the oracle MHA wrapper has no bias arguments: set them on its C struct
-            self._bias_keep = [np.ascontiguousarray(b, np.float32) for b in self.bias]
-            from oracle.oracle import _p
-            m.c.bias_q, m.c.bias_k, m.c.bias_v, m.c.bias_o = (_p(b) for b in self._bias_keep)
-        return m
-
-    def oracle_block(self, orc):
-        return orc.Block(self.oracle_mha(orc), self.n1, self.n2, self.g, self.u, self.d, self.fn,
-                         norm_eps=1e-5, ffn_eps=1e-5, ffn_activation=self.act)
-
-
-def ulp_diff_f32(a, b):
-    a = np.ascontiguousarray(a, np.float32).view(np.int32).astype(np.int64)
-    b = np.ascontiguousarray(b, np.float32).view(np.int32).astype(np.int64)
-    a = np.where(a < 0, np.int64(-2**31) - a, a)
-    b = np.where(b < 0, np.int64(-2**31) - b, b)
-    return np.abs(a - b)
-
-
-def to_dev(torch, a):
-    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
-
-
-def check_stages(orc, w: Weights, mha_ref, x_in, taps, out, cache_k, cache_v, base, strict=True):
-    """Stage-wise parity of one GPU block call (rows = seq tokens at positions
-    base..base+seq-1 of one sequence).  mha_ref is an oracle MHA whose
-    kv_offset equals base; it is advanced by this call."""
-    sh = w.sh
-    seq = x_in.shape[0]
-    y1 = taps.y1.cpu().numpy()
-    q = taps.q.cpu().numpy()
-    attn = taps.attn.cpu().numpy()
-    mid = taps.mid.cpu().numpy()
-    # RMSNorm1 (poly/norm.go:102-138)
-    y1_ref = orc.rmsnorm_forward(x_in, w.n1, 1e-5)
-    if strict:
-        assert np.array_equal(y1, y1_ref), "rmsnorm1 not bit-exact"
-    else:
-        assert ulp_diff_f32(y1, y1_ref).max() <= 1
-    # Q/K/V + RoPE: the oracle fed the GPU's y1
-    _, _, q_ref, _ = mha_ref.forward(y1)
-    assert mha_ref.kv_offset == base + seq
-    scale = np.abs(q_ref).max(axis=1, keepdims=True)
-    assert np.all(np.abs(q - q_ref) <= 1e-12 * scale), "Q after RoPE off by more than 1e-12"
-    if base == 0:
-        # position 0: cos = 1, sin = 0 exactly -> the rotation is the identity
-        assert np.array_equal(q[0], q_ref[0])
-    kd = sh.kv_dim
-    ck_ref = mha_ref.cache_k.reshape(sh.msl, kd)
-    cv_ref = mha_ref.cache_v.reshape(sh.msl, kd)
-    rows = slice(base, base + seq)
-    assert np.array_equal(cache_v[rows], cv_ref[rows]), "V cache not bit-exact"
-    assert ulp_diff_f32(cache_k[rows], ck_ref[rows]).max() <= 1, "K cache beyond 1 ulp"
-    if base == 0:
-        assert np.array_equal(cache_k[0], ck_ref[0])
-    # attention (poly/mha.go:316-354), the oracle fed the GPU's Q and caches
-    attn_ref = orc.attention(q, cache_k, cache_v, base, sh.msl, sh.heads, sh.kv, sh.hd)
-    ascale = np.abs(attn_ref).max(axis=1, keepdims=True)
-    assert np.all(np.abs(attn - attn_ref) <= 1e-12 * ascale), "attention off by more than 1e-12"
-    # inner norm + requant + O + residual (poly/mha.go:356-368, transformer_forward.go:236)
-    bo = w.bias[3] if w.bias else None
-    _, post = orc.attn_out(w.o, attn, inner_norm=w.an, eps=1e-5, bias_o=bo)
-    mid_ref = (post + x_in).astype(np.float32)
-    if strict:
-        assert np.array_equal(mid, mid_ref), "O projection + residual not bit-exact"
-    else:
-        assert np.mean(mid == mid_ref) > 0.9
-    # RMSNorm2 + SwiGLU + residual (transformer_forward.go:238-245)
-    y2 = orc.rmsnorm_forward(mid, w.n2, 1e-5)
-    f = orc.swiglu_forward(w.g, w.u, w.d, y2, inner_norm=w.fn, eps=1e-5, activation=w.act).out
-    out_ref = (f + mid).astype(np.float32)
-    if strict and w.act == ACT_RELU2:
-        assert np.array_equal(out, out_ref), "FFN half not bit-exact"
-    else:
-        # SiLU gate: exp() last bits (h within 1 ulp), which can move an int8 code
-        assert np.mean(out == out_ref) > 0.9
-        assert np.abs(out - out_ref).max() <= 0.05 * np.abs(out_ref).max()
-
-
-def run_block_case(orc, torch, tf, w: Weights, seqs, seed, strict=True):
-    """Prefill seqs[0] tokens then single-token steps for the rest."""
-    sh = w.sh
-    blk = tf.BitNetBlock(w.cfg(tf, "strict" if strict else "fast"), w.gpu(tf))
-    mha_ref = w.oracle_mha(orc)
-    base = 0
-    for i, seq in enumerate(seqs):
-        x_in = orc.normal_f32(seq * sh.hidden, seed + i).reshape(seq, sh.hidden)
-        x = to_dev(torch, x_in)
-        print(f"  block call {i}: seq={seq} base={base}", flush=True)
-        _, taps = blk.forward(x, taps=True)
-        torch.cuda.synchronize()
-        assert blk.kv_offset == base + seq
-        ck, cv = (t.cpu().numpy() for t in blk.kv_cache(0))
-        check_stages(orc, w, mha_ref, x_in, taps, x.cpu().numpy(), ck, cv, base, strict)
-        base += seq
-    blk.release()
 
 
 @pytest.mark.parametrize("seqs", [[1], [5], [9, 1, 1, 1], [64], [37, 1], [17]])
@@ -265,9 +108,11 @@ def test_block_bitnet_2b_seq512(orc, torch_dev, tf):
 
 
 def test_block_end_to_end_tolerance(orc, torch_dev, tf):
-    # Whole block vs the oracle's own chain.  Only libm last bits differ, so
-    # almost every element is identical; a moved int8 code changes a row by
-    # about one quantization step.
+    # Whole block vs the oracle's own chain, each fed only the block input
+    # (not a parity bar: the stage-wise tests are).  Only libm last bits
+    # (pow/cos/sin in RoPE, exp in the softmax) differ, so almost every element
+    # is identical; a moved int8 code changes a row by about one quantization
+    # step.
     torch = torch_dev
     w = Weights(orc, SMALL, seed=181)
     blk = tf.BitNetBlock(w.cfg(tf), w.gpu(tf))
@@ -600,29 +445,49 @@ def test_fast_decode_rope_fused_attention(orc, torch_dev, tf, shape, monkeypatch
 
 @pytest.mark.parametrize("shape,norm", [("small", "strict"), ("small", "fast"),
                                         ("bitnet2b", "strict"), ("bitnet2b", "fast")])
-def test_block_decode_norm_fused_matches_staged(orc, torch_dev, tf, shape, norm):
-    # Without taps a decode row is normalized inside each matmul that consumes
-    # it (RMSNorm1 -> QKV, attention inner norm -> O, RMSNorm2 -> gate/up, FFN
-    # inner norm -> down).  Strict sums are the same ordered chains, so the
-    # result equals the staged path bit for bit; fast sums use another fixed
-    # order (last-bit differences, which can move an int8 code).
+def test_block_decode_norm_fused_and_staged(orc, torch_dev, tf, shape, norm, monkeypatch):
+    # A decode row is normalized inside each matmul that consumes it (RMSNorm1
+    # -> QKV, attention inner norm -> O, RMSNorm2 -> gate/up, FFN inner norm
+    # -> down); LOOM_AMD_UNFUSED_NORM=1 keeps the separate norm launches.  Both
+    # paths are checked stage by stage against the oracle; strict sums are
+    # the same ordered chains in both, so their outputs are also equal byte
+    # for byte.
     torch = torch_dev
     sh = SMALL if shape == "small" else BITNET_2B
-    w = Weights(orc, sh, seed=1201)
+    w = Weights(orc, sh, seed=1201, act=ACT_SILU)
     gw = w.gpu(tf)
-    staged = tf.BitNetBlock(w.cfg(tf, norm), gw)
     fused = tf.BitNetBlock(w.cfg(tf, norm), gw)
+    monkeypatch.setenv("LOOM_AMD_UNFUSED_NORM", "1")
+    staged = tf.BitNetBlock(w.cfg(tf, norm), gw)
+    monkeypatch.delenv("LOOM_AMD_UNFUSED_NORM")
+    refs = {"fused": w.oracle_mha(orc), "staged": w.oracle_mha(orc)}
+    base = 0
     for i, seq in enumerate([6, 1, 1, 1]):
         x_in = orc.normal_f32(seq * sh.hidden, 1300 + i).reshape(seq, sh.hidden)
-        a = to_dev(torch, x_in)
-        b = to_dev(torch, x_in)
-        staged.forward(a, taps=True)
-        fused.forward(b)
-        ga, gb = a.cpu().numpy(), b.cpu().numpy()
+        outs = {}
+        for name, blk in (("fused", fused), ("staged", staged)):
+            x = to_dev(torch, x_in)
+            _, t = blk.forward(x, taps=True)
+            torch.cuda.synchronize()
+            ck, cv = (a.cpu().numpy() for a in blk.kv_cache(0))
+            outs[name] = x.cpu().numpy()
+            print(f"  call {i} ({name}): seq={seq} base={base}", flush=True)
+            check_stages(orc, w, refs[name], x_in, t.numpy(), outs[name], ck, cv, base,
+                         strict=norm == "strict")
         if norm == "strict":
-            assert np.array_equal(ga, gb), f"call {i}"
-        else:
-            assert np.mean(ga == gb) > 0.9 and np.abs(ga - gb).max() <= 0.02 * np.abs(ga).max()
+            assert outs["fused"].tobytes() == outs["staged"].tobytes(), f"call {i}"
+        base += seq
+    fused.release()
+    staged.release()
+
+
+@pytest.mark.parametrize("norm", ["strict", "fast"])
+def test_block_decode_many_positions(orc, torch_dev, tf, norm):
+    # single-token steps after a prefill, across decode-attention chunk
+    # borders (32-position chunks in fast mode), checked stage by stage
+    w = Weights(orc, BITNET_2B, seed=1211, act=ACT_SILU, bias=True)
+    run_block_case(orc, torch_dev, tf, w, [31] + [1] * 5 + [1] * 30, seed=1220,
+                   strict=norm == "strict")
 
 
 # ---------------------------------------------------------------- untied (ternary) LM head

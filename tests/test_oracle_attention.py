@@ -223,6 +223,78 @@ def test_mha_stages_compose_to_forward(orc):
     assert np.array_equal(p2, pre) and np.array_equal(o2, post)
 
 
+def test_mha_project_and_row_stages_compose(orc):
+    # The finer stages of the GPU stage checks reproduce MHA.forward bit for
+    # bit: project (Q and the K/V cache rows), attention of single rows at
+    # their own positions, the fp64 inner norm + requantization, and the O
+    # projection from the int8 rows (dense_quantized) with a bias.
+    import ctypes as C
+    m = make_mha(orc, seed=63)
+    bo = orc.normal_f32(HID, 64) * np.float32(0.1)
+    m._bo = bo
+    m.c.bias_o = bo.ctypes.data_as(C.c_void_p)
+    S = 7
+    x = orc.normal_f32(S * HID, 65).reshape(S, HID)
+    pre, post, q, attn = m.forward(x)
+    m2 = make_mha(orc, seed=63)
+    q2 = m2.project(x, 0)
+    assert np.array_equal(q2, q)
+    assert np.array_equal(m2.cache_k, m.cache_k) and np.array_equal(m2.cache_v, m.cache_v)
+    ck, cv = m2.cache_k.reshape(MSL, KV * HD), m2.cache_v.reshape(MSL, KV * HD)
+    for r in (0, 3, S - 1):
+        a = orc.attention(q2[r:r + 1], ck, cv, r, MSL, HEADS, KV, HD)
+        assert np.array_equal(a[0], attn[r])
+    normed = attn.copy()
+    for r in range(S):
+        orc.lib().orc_bitnet_rmsnorm_f64(normed[r].ctypes.data_as(C.c_void_p), normed.shape[1],
+                                         m.inner_norm.ctypes.data_as(C.c_void_p), 1e-5)
+    assert np.array_equal(normed.astype(np.float32), pre)
+    aq, aam = orc.quant_rows(normed)
+    assert np.array_equal(orc.dense_quantized(m.mats[3], aq, aam, bias=bo), post)
+
+
+def test_swiglu_row_stages_compose(orc):
+    # swiglu_gate_rows + inner norm + requantization + dense_quantized (down)
+    # reproduce swiglu_forward bit for bit, with biases, for both gates.
+    H, I = 64, 96
+    g = orc.random_matrix(I, H, 71)
+    u = orc.random_matrix(I, H, 72)
+    d = orc.random_matrix(H, I, 73)
+    nw = orc.uniform_f32(I, 0.5, 1.5, 74)
+    bias = orc.normal_f32(2 * I + H, 75) * np.float32(0.1)
+    x = orc.normal_f32(4 * H, 76).reshape(4, H)
+    for act in (orc.ACT_SILU, orc.ACT_RELU2):
+        r = orc.swiglu_forward(g, u, d, x, inner_norm=nw, bias=bias, eps=1e-5, activation=act)
+        xq, am = orc.quant_rows(x)
+        assert np.array_equal(xq, r.xq) and np.array_equal(am, r.amax)
+        h = orc.swiglu_gate_rows(g, u, xq, am, activation=act, bias=bias[:2 * I])
+        hn = np.stack([orc.bitnet_rmsnorm_row(h[i], nw, 1e-5) for i in range(4)])
+        assert np.array_equal(hn.view(np.uint32), r.h.view(np.uint32))
+        hq, ham = orc.quant_rows(hn)
+        assert np.array_equal(hq, r.hq) and np.array_equal(ham, r.hamax)
+        out = orc.dense_quantized(d, hq, ham, bias=bias[2 * I:])
+        assert np.array_equal(out.view(np.uint32), r.out.view(np.uint32))
+
+
+def test_attention_threads_do_not_change_bits(orc):
+    # the oracle splits (query, head) pairs over threads; each pair runs the
+    # reference's loops, so 1 thread and many give the same bytes
+    import os
+    import subprocess
+    import sys
+    code = ("import numpy as np, sys; sys.path.insert(0, %r); from oracle import oracle as orc; "
+            "q = orc.normal_f32(5*4*32, 1).astype(np.float64).reshape(5, 128); "
+            "k = orc.normal_f32(40*64, 2).reshape(40, 64); v = orc.normal_f32(40*64, 3).reshape(40, 64); "
+            "a = orc.attention(q, k, v, 30, 40, 4, 2, 32); sys.stdout.write(a.tobytes().hex())")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    outs = []
+    for th in ("1", "6"):
+        env = dict(os.environ, OMP_NUM_THREADS=th)
+        outs.append(subprocess.run([sys.executable, "-c", code % root], env=env, check=True,
+                                   capture_output=True, text=True).stdout)
+    assert outs[0] == outs[1] and len(outs[0]) > 0
+
+
 def test_lm_head_scalar_order_pinned(orc):
     # The scalar head (poly/transformer.go:681-687, dotTileGo in
     # poly/simd/dot.go:14-21) is one sequential fp64 sum per logit: equal bit
