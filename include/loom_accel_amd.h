@@ -133,6 +133,19 @@ int loom_amd_dense_forward(const loom_amd_matrix* w, const float* x, int m, int 
                            float* pre, float* post, const float* residual,
                            const loom_amd_dense_taps* taps, void* stream);
 
+/* loom_amd_dense_forward that allocates nothing.  No counterpart in loom: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Quantized
+ * rows are staged in a fixed 8 MiB device array per GPU instead of the
+ * growable scratch arena: m * (256*ceil(k/256) + 8) plus alignment must fit
+ * 8 MiB (larger calls fail with a message; four rows or fewer need no staging).
+ * Every call on one GPU shares that array: calls overlapping on one GPU race
+ * and must be serialized by the caller.  Same outputs as
+ * loom_amd_dense_forward, without taps. */
+int loom_amd_dense_forward_noalloc(const loom_amd_matrix* w, const float* x, int m,
+                                   int activation, float* pre, float* post,
+                                   const float* residual, void* stream);
+
 typedef struct loom_amd_swiglu_taps {
     int8_t* xq;        /* m*hidden */
     float* amax;       /* m */
