@@ -7,7 +7,14 @@
  * NULL, last_error(NULL).  Also checks the size contract of weight_bytes and
  * the error convention of compile_layer on bad descriptors.
  *
- * usage: abi_conformance <path-to-so> <expect_gpu:0|1>
+ * With a case file (third argument, GPU boxes), it then replays the sequence
+ * of the AMD Go glue's CompileLayer / Infer:
+ * weight_bytes(desc) == blob length, compile_layer, layer_io_bytes,
+ * first_infer (error ignored), infer, output == the expected bytes,
+ * release_layer, plugin_close.  Case file: little-endian u32 length + bytes
+ * for each of layer name, size label, weight blob, input, expected output.
+ *
+ * usage: abi_conformance <path-to-so> <expect_gpu:0|1> [case-file]
  * Prints one line per check; exit status 0 when every check passed.
  */
 #include <dlfcn.h>
@@ -43,6 +50,69 @@ typedef int (*fn_first)(loom_accel_compiled_layer*, double*, char*, size_t);
 typedef int (*fn_infer)(loom_accel_compiled_layer*, const void*, size_t, void*, size_t, double*,
                         char*, size_t);
 typedef const char* (*fn_lasterr)(loom_accel_plugin*);
+
+/* One length-prefixed field of the case file (malloc'd, NUL-terminated). */
+static unsigned char* read_field(FILE* f, size_t* len) {
+    unsigned char b[4];
+    if (fread(b, 1, 4, f) != 4) return NULL;
+    *len = (size_t)b[0] | (size_t)b[1] << 8 | (size_t)b[2] << 16 | (size_t)b[3] << 24;
+    unsigned char* p = (unsigned char*)malloc(*len + 1);
+    if (!p) return NULL;
+    if (*len && fread(p, 1, *len, f) != *len) {
+        free(p);
+        return NULL;
+    }
+    p[*len] = 0;
+    return p;
+}
+
+/* The glue's CompileLayer + Infer sequence on one layer. */
+static void replay_case(void** sym, loom_accel_plugin* gpu, const char* path) {
+    FILE* f = fopen(path, "rb");
+    CHECK(f != NULL, "case file opens");
+    if (!f) return;
+    size_t ln, ll, lb, li, lo;
+    unsigned char* name = read_field(f, &ln);
+    unsigned char* label = read_field(f, &ll);
+    unsigned char* blob = read_field(f, &lb);
+    unsigned char* in = read_field(f, &li);
+    unsigned char* want = read_field(f, &lo);
+    fclose(f);
+    CHECK(name && label && blob && in && want, "case file parses");
+    if (!(name && label && blob && in && want)) return;
+    loom_accel_layer_desc d = {(const char*)name, "TERNARY", (const char*)label};
+    printf("     case %s %s\n", name, label);
+    CHECK(((fn_wbytes)sym[5])(&d) == lb, "weight_bytes(desc) == blob length");
+    char err[512] = {0};
+    loom_accel_compiled_layer* layer = NULL;
+    double cms = -1.0;
+    int rc = ((fn_compile)sym[6])(gpu, &d, blob, lb, &layer, &cms, err, sizeof err);
+    CHECK(rc == 0 && layer != NULL && cms >= 0.0, "compile_layer succeeds");
+    if (rc != 0) {
+        printf("     compile error: %s\n", err);
+        return;
+    }
+    size_t ib = 0, ob = 0;
+    CHECK(((fn_io)sym[8])(layer, &ib, &ob, NULL, 0) == 0 && ib == li && ob == lo,
+          "layer_io_bytes matches the case");
+    double fms = 0.0;
+    (void)((fn_first)sym[9])(layer, &fms, NULL, 0); /* error ignored, as the glue does */
+    unsigned char* got = (unsigned char*)malloc(lo);
+    double ims = -1.0;
+    for (int rep = 0; rep < 3; rep++) {
+        memset(got, 0xff, lo);
+        rc = ((fn_infer)sym[10])(layer, in, li, got, lo, &ims, err, sizeof err);
+        CHECK(rc == 0 && ims >= 0.0, "infer succeeds");
+        CHECK(rc == 0 && memcmp(got, want, lo) == 0, "infer output == oracle bytes");
+    }
+    free(got);
+    ((fn_release)sym[7])(layer);
+    free(name);
+    free(label);
+    free(blob);
+    free(in);
+    free(want);
+}
 
 int main(int argc, char** argv) {
     if (argc < 3) {
@@ -137,6 +207,7 @@ int main(int argc, char** argv) {
                   "infer with a wrong size -> -1");
             release_layer(out);
             release_layer(NULL);
+            for (int c = 3; c < argc; c++) replay_case(sym, gpu, argv[c]);
             plugin_close(gpu);
         }
     }

@@ -394,6 +394,37 @@ def test_plugin_bitnet_swiglu(orc, torch_dev):
         p.close()
 
 
+def test_c_loader_replays_glue_on_gpu(orc, torch_dev, tmp_path):
+    # tests/abi_conformance.c replays the AMD Go glue's sequence (INTEGRATION.md
+    # section 1: dlopen + 12 dlsyms + version + open GPU, weight_bytes, compile,
+    # io_bytes, first_infer, infer x3, release, close) on the GPU box; the
+    # outputs must equal the oracle's Dense forward bytes (linear and ReLU).
+    import os
+    import struct
+    import subprocess
+    from loom_amd import _lib
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    exe = tmp_path / "abi_conformance"
+    subprocess.run(["gcc", "-O1", "-Wall", "-I", os.path.join(root, "include"),
+                    os.path.join(root, "tests", "abi_conformance.c"), "-o", str(exe), "-ldl"],
+                   check=True)
+    cases = []
+    for i, (n, k, M, act) in enumerate([(384, 640, 3, -1), (2560, 6912, 1, 0), (6912, 2560, 70, -1)]):
+        m = orc.random_matrix(n, k, seed=800 + i)
+        x = orc.normal_f32(M * k, seed=810 + i).reshape(M, k)
+        ref = orc.dense_forward(m, x, activation=act, simd=True)
+        want = (ref.pre if act == -1 else ref.post).tobytes()
+        label = f"m={M},k={k},n={n},act={act}"
+        fields = [b"BitNetLinear", label.encode(), m.entity_blob(), x.tobytes(), want]
+        path = tmp_path / f"case{i}.bin"
+        path.write_bytes(b"".join(struct.pack("<I", len(f)) + f for f in fields))
+        cases.append(str(path))
+    proc = subprocess.run([str(exe), _lib.LIB_PATH, "1", *cases], capture_output=True, text=True)
+    print(proc.stdout)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
+    assert proc.stdout.count("ok   infer output == oracle bytes") == 3 * len(cases)
+
+
 def test_plugin_concurrent_infer_two_threads(orc, torch_dev):
     # loom's Go glue takes no lock around infer, and two goroutines may run
     # two compiled layers at once.  Every layer on a device shares the
