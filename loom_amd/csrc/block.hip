@@ -106,13 +106,14 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float* __restr
     m = block_max(m, shf);
     if (m < 1e-5f) m = 1e-5f;
     const double qs = 127.0 / (double)m;
+    const float qs32 = (float)qs;
     int s = 0;
     int8_t* qr = xq + (size_t)row * ldq;
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
         const int i = threadIdx.x + j * 256;
         if (i < n) {
-            const int q = quant_one((double)v[j], qs);
+            const int q = quant_f32(v[j], qs32, qs);
             s += q;
             qr[i] = (int8_t)q;
         }

@@ -72,6 +72,24 @@ __device__ __forceinline__ int quant_one(double v, double scale) {
     return (int)r;
 }
 
+// quant_one for an fp32 value v with |v| <= amax (s = fp64 127/amax, s32 =
+// fp32(s)), decided in fp32 where that is exact.  |v*s| <= 127, and the fp32
+// product p32 = fp32(v * s32) is within 2^-23 * 127 < 1.52e-5 of loom's fp64
+// product; so when p32 lies farther than 3.1e-5 from every rounding boundary
+// k + 1/2, both round to the same integer, the nearest one to p32 (rintf).
+// Near a boundary, and for NaN (every comparison fails), the fp64 path
+// decides.  (p32 - rintf(p32) and 0.5 - d are exact: Sterbenz.)
+__device__ __forceinline__ int quant_f32(float v, float s32, double s) {
+    const float p = v * s32;
+    const float r = rintf(p);
+    const float d = fabsf(p - r);
+    if (0.5f - d > 3.1e-5f) {
+        const int q = (int)r;
+        return q < -128 ? -128 : (q > 127 ? 127 : q);
+    }
+    return quant_one((double)v, s);
+}
+
 __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
     return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
            ((uint32_t)(d & 0xff) << 24);

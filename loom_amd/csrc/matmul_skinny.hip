@@ -15,6 +15,8 @@
 namespace lamd {
 
 hipError_t launch_gemm(const MatArgs& p, bool two, int device, hipStream_t s);
+bool stream_ok(int m, int k, int n_tiles, bool fused, const Epilogue& epi);
+hipError_t launch_stream(const MatArgs& p, bool fuseq, hipStream_t s);
 
 constexpr int kFusedMaxRows = 4;
 constexpr int kFusedVec = 16;  // float4 per thread in the fused prologue (max)
@@ -283,6 +285,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
         __syncthreads();
         // bitNetQuantizedActivation (poly/bitnet_cpu.go:73-95) into LDS.
         double sc[MR];
+        float sc32[MR];
 #pragma unroll
         for (int rr = 0; rr < MR; ++rr) {
             float am = 0.0f;
@@ -292,6 +295,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
             if (tid == rr) amax_bits[rr] = __float_as_uint(am);  // read after the main loop
             if (am < 1e-5f) am = 1e-5f;
             sc[rr] = rr < M ? 127.0 / (double)am : 0.0;
+            sc32[rr] = (float)sc[rr];
         }
         int ls[MR];
 #pragma unroll
@@ -302,9 +306,13 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
             if (idx < n4) {
                 const int row = row_of<MR>(idx, row4);
                 double s = sc[0];
+                float s32 = sc32[0];
 #pragma unroll
                 for (int rr = 1; rr < MR; ++rr)
-                    if (rr == row) s = sc[rr];
+                    if (rr == row) {
+                        s = sc[rr];
+                        s32 = sc32[rr];
+                    }
                 int q0, q1, q2, q3;
                 if (F64) {
                     q0 = quant_one(xd[j][0], s);
@@ -312,10 +320,10 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
                     q2 = quant_one(xd[j][2], s);
                     q3 = quant_one(xd[j][3], s);
                 } else {
-                    q0 = quant_one((double)xv[j].x, s);
-                    q1 = quant_one((double)xv[j].y, s);
-                    q2 = quant_one((double)xv[j].z, s);
-                    q3 = quant_one((double)xv[j].w, s);
+                    q0 = quant_f32(xv[j].x, s32, s);
+                    q1 = quant_f32(xv[j].y, s32, s);
+                    q2 = quant_f32(xv[j].z, s32, s);
+                    q3 = quant_f32(xv[j].w, s32, s);
                 }
                 *(uint32_t*)(xq_s + row * p.ldq + 4 * (idx - row * row4)) = pack4(q0, q1, q2, q3);
 #pragma unroll
@@ -760,6 +768,7 @@ hipError_t launch_matmul(const Matrix* w0, const Matrix* w1, const QuantAct& a, 
     p.e.amax = a.amax;
     p.e.xsum = a.xsum;
     const bool two = epi.kind == EPI_SWIGLU;
+    if (!two && stream_ok(m, w0->cols, w0->ntiles, false, epi)) return launch_stream(p, false, s);
     if (m <= 16) return two ? launch_skinny<2, 1, false>(p, s) : launch_skinny<1, 1, false>(p, s);
     if (m <= 32) return two ? launch_small_m<2, 2>(p, s) : launch_small_m<1, 2>(p, s);
     if (m <= 64) return two ? launch_small_m<2, 4>(p, s) : launch_small_m<1, 4>(p, s);
@@ -871,6 +880,7 @@ hipError_t launch_matmul_fused(const Matrix* w0, const Matrix* w1, const float* 
     p.ldq = pad_cols(w0->cols);
     p.xq_tap = xq_tap;
     p.amax_tap = amax_tap;
+    if (epi.kind != EPI_SWIGLU && stream_ok(m, w0->cols, w0->ntiles, true, epi)) return launch_stream(p, true, s);
     return epi.kind == EPI_SWIGLU ? launch_skinny<2, 1, true>(p, s) : launch_skinny<1, 1, true>(p, s);
 }
 

@@ -116,11 +116,13 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const T* __restrict__ x,
         m = block_max(m, shf);
         if (m < 1e-5f) m = 1e-5f;
         const double scale = 127.0 / (double)m;
+        const float scale32 = (float)scale;
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
             const int i = threadIdx.x + j * 256;
             if (i < k) {
-                const int q = quant_one((double)v[j], scale);
+                const int q = sizeof(T) == 4 ? quant_f32((float)v[j], scale32, scale)
+                                             : quant_one((double)v[j], scale);
                 s += q;
                 qr[i] = (int8_t)q;
             }
@@ -254,13 +256,14 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(float* __restrict__ h, 
     m = block_max(m, shf);
     if (m < 1e-5f) m = 1e-5f;
     const double qs = 127.0 / (double)m;
+    const float qs32 = (float)qs;
     int s = 0;
     int8_t* qr = hq + (size_t)row * ldq;
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
         const int i = threadIdx.x + j * 256;
         if (i < n) {
-            const int q = quant_one((double)v[j], qs);
+            const int q = quant_f32(v[j], qs32, qs);
             s += q;
             qr[i] = (int8_t)q;
         }

@@ -394,6 +394,33 @@ def test_plugin_bitnet_swiglu(orc, torch_dev):
         p.close()
 
 
+@pytest.mark.parametrize("force", ["1", ""])
+@pytest.mark.parametrize("n,k", [(6912, 2560), (2560, 6912), (6900, 2570), (1000, 1792),
+                                 (70000, 2560)])
+def test_stream_gemv_matches_oracle(orc, torch_dev, bn, monkeypatch, force, n, k):
+    # The streaming GEMV (fixed grid of waves, each walking its 16-row tiles'
+    # K tiles through a ring of in-flight loads): forced on every shape
+    # (LOOM_AMD_GEMV_STREAM=1) and by default (large N only).  Fused
+    # quantization (Dense forward) and pre-quantized rows, M = 1..4: int8 rows,
+    # amax and fp32 outputs bit-exact against the oracle.
+    torch = torch_dev
+    if force:
+        monkeypatch.setenv("LOOM_AMD_GEMV_STREAM", force)
+    m = orc.random_matrix(n, k, seed=n + 3 * k)
+    w = gpu_matrix(bn, m)
+    for M in (1, 2, 3, 4):
+        x = orc.normal_f32(M * k, seed=900 + M).reshape(M, k)
+        ref = orc.dense_forward(m, x, simd=True)
+        xd = to_dev(torch, x)
+        pre, _ = bn.dense_forward_packed_ternary(w, xd)
+        q = bn.quantize_activation(xd)
+        out = bn.ternary_matvec_quantized(w, q)
+        torch.cuda.synchronize()
+        assert pre.cpu().numpy().tobytes() == ref.pre.tobytes(), (n, k, M, "fused")
+        assert out.cpu().numpy().tobytes() == ref.pre.tobytes(), (n, k, M, "pre-quantized")
+    w.release()
+
+
 def test_c_loader_replays_glue_on_gpu(orc, torch_dev, tmp_path):
     # tests/abi_conformance.c replays the AMD Go glue's sequence (INTEGRATION.md
     # section 1: dlopen + 12 dlsyms + version + open GPU, weight_bytes, compile,
@@ -504,24 +531,37 @@ def test_library_errors_are_loud(orc, torch_dev, bn):
     assert _lib.lib().loom_amd_ternary_matmul(None, None, 256, None, None, 1, None, None, None) == -1
 
 
-def test_fused_quant_near_ties(orc, torch_dev, bn):
-    # The fused quantizer rounds in fp32 away from ties and defers to the fp64
-    # product within 1e-3 of one: rows built on and around exact ties (and
-    # across the 1e-3 band) must quantize exactly like loom's fp64 path.
+@pytest.mark.parametrize("path", ["skinny", "stream"])
+def test_fused_quant_near_ties(orc, torch_dev, bn, monkeypatch, path):
+    # The quantizers decide in fp32 when the fp32 product lies farther than
+    # 3.1e-5 from a rounding boundary k + 1/2 (it is within 1.52e-5 of loom's
+    # fp64 product) and take loom's fp64 path otherwise: rows built on exact
+    # ties, inside the band, at its edge and just outside it must quantize
+    # exactly like loom's fp64 path -- through the fused matmul prologue
+    # (skinny or streaming kernel) and the stand-alone quantization kernel.
+    torch = torch_dev
+    if path == "stream":
+        monkeypatch.setenv("LOOM_AMD_GEMV_STREAM", "1")
     rng = np.random.default_rng(7)
     K = 4096
     m = orc.random_matrix(32, K, seed=71)
-    for amax in (127.0, 63.5, 3.0, 1.0, 300.0, 0.001):
+    bands = [0.0, 1e-7, -1e-7, 1.5e-5, -1.5e-5, 2.5e-5, -2.5e-5, 3.1e-5, -3.1e-5, 3.5e-5,
+             -3.5e-5, 5e-5, -5e-5, 3e-4, -3e-4, 9.9e-4, -9.9e-4, 0.2, -0.3]
+    for amax in (127.0, 63.5, 3.0, 1.0, 300.0, 0.001, 7.3):
         scale = 127.0 / float(np.float32(amax))
         rows = []
         for _ in range(4):
             k = rng.integers(-127, 127, K).astype(np.float64)
-            eps = rng.choice([0.0, 1e-7, -1e-7, 3e-4, -3e-4, 9.9e-4, -9.9e-4, 1.1e-3, -1.1e-3,
-                              0.2, -0.3], K)
+            eps = rng.choice(bands, K)
             row = ((k + 0.5 + eps) / scale).astype(np.float32)
             row[rng.integers(0, K)] = np.float32(amax) * rng.choice([1.0, -1.0])
             rows.append(row)
-        _check_dense(orc, torch_dev, bn, m, np.stack(rows))
+        x = np.stack(rows)
+        _check_dense(orc, torch, bn, m, x)
+        q = bn.quantize_activation(to_dev(torch, x))
+        torch.cuda.synchronize()
+        xq_ref, am_ref = orc.quant_rows(x)
+        assert np.array_equal(q.unpadded().cpu().numpy(), xq_ref), amax
 
 
 # ---------------------------------------------------------------- large-M GEMM (32x32x32 MFMA) paths
