@@ -678,6 +678,167 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict
 // tile w/2 and HD/32 tiles of 16 value columns.
 typedef double v4d __attribute__((ext_vector_type(4)));
 
+// One-pass fast prefill attention (fast mode).  The two-pass kernel below
+// keeps every score in a workspace between its passes (rows x heads x span
+// fp64: 2.7 GB per layer at 8 x 2048 tokens); this one keeps a running row
+// maximum instead (online softmax).  Each wave owns 16 queries of one head and
+// computes, per 32-position chunk, the transposed scores S^T = K Q^T on the
+// fp64 matrix cores: lane (lr, lg) then holds query lr's scores at positions
+// 16 kt + 4 v + lg, which is exactly the B operand layout of O^T = V^T P^T.
+// So the probabilities never leave registers, a query's running maximum and
+// sum live in the four lanes that share lr (two shuffles per chunk), and the
+// output rows are rescaled lane-locally by exp(old max - new max) when the
+// maximum grows.  The HPW heads of a workgroup share one KV head: every chunk
+// of K and V is staged once (converted to fp64) for all four waves.  The sums
+// differ in order from loom's sequential ones (a fixed order: deterministic),
+// within 1e-12 of the row scale.
+template <int HD, int HPW>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attn_flash_mfma_kernel(
+    const double* __restrict__ q, const float* __restrict__ cache_k,
+    const float* __restrict__ cache_v, const int* __restrict__ pos0, int msl, int span, int heads,
+    int kv_heads, int seq, double* __restrict__ out) {
+    constexpr int TQ = 16 * (4 / HPW);  // queries per workgroup
+    constexpr int NM = HD / 4;          // k-steps of a score tile
+    constexpr int NT = HD / 16;         // output tiles of 16 head columns
+    constexpr int F2 = kChunkP * HD / 2 / 256;  // float2 loads per thread and operand
+    static_assert(HPW == 1 || HPW == 2 || HPW == 4, "heads per workgroup");
+    static_assert(F2 >= 1 && kChunkP * HD == F2 * 2 * 256, "chunk geometry");
+    // K rows KP doubles apart (16 rows x 4 columns per read: 2*KP = 4 mod 64
+    // banks), V rows VP (4 rows x 16 columns: 2*VP = 32 mod 64): both reads
+    // are conflict-free per half wave.
+    constexpr int KP = HD + 2, VP = HD + 16;
+    __shared__ double kd[kChunkP * KP];
+    __shared__ double vd[kChunkP * VP];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lr = lane & 15, lg = lane >> 4;
+    const int h = blockIdx.x * HPW + wave % HPW;
+    const int tile = gridDim.y - 1 - blockIdx.y;  // long rows first
+    const int b = blockIdx.z;
+    const int s0 = tile * TQ;
+    const int nq = min(TQ, seq - s0);
+    const int base = *pos0;
+    const int q_dim = heads * HD, kv_dim = kv_heads * HD;
+    const int kvh = blockIdx.x * HPW / (heads / kv_heads);
+    const size_t row0 = (size_t)b * seq + s0;
+    if (base + s0 + nq > span) {
+        for (int i = tid; i < nq * HD * HPW; i += 256)
+            out[(row0 + i / (HD * HPW)) * q_dim + (size_t)blockIdx.x * HPW * HD + i % (HD * HPW)] =
+                __builtin_nan("");
+        return;
+    }
+    const int nch = (base + s0 + nq + kChunkP - 1) / kChunkP;
+    const float* kb = cache_k + (size_t)b * msl * kv_dim + (size_t)kvh * HD;
+    const float* vb = cache_v + (size_t)b * msl * kv_dim + (size_t)kvh * HD;
+    // staging: consecutive lanes take consecutive column pairs of a row, so
+    // the fp64 pairs they write to LDS are consecutive 16-byte words
+    float2 rk[F2], rv[F2];
+    auto load = [&](int c) {
+#pragma unroll
+        for (int j = 0; j < F2; ++j) {
+            const int e = (tid + j * 256) * 2;
+            const size_t off = (size_t)min(c * kChunkP + e / HD, msl - 1) * kv_dim + e % HD;
+            rk[j] = *(const float2*)(kb + off);
+            rv[j] = *(const float2*)(vb + off);
+        }
+    };
+    auto store = [&]() {
+#pragma unroll
+        for (int j = 0; j < F2; ++j) {
+            const int e = (tid + j * 256) * 2;
+            double* dk = &kd[(e / HD) * KP + e % HD];
+            double* dv = &vd[(e / HD) * VP + e % HD];
+            dk[0] = (double)rk[j].x;
+            dk[1] = (double)rk[j].y;
+            dv[0] = (double)rv[j].x;
+            dv[1] = (double)rv[j].y;
+        }
+    };
+    const int qi = 16 * (wave / HPW) + lr;  // this lane's query in the tile
+    const int qpos = base + s0 + qi;
+    // B operand of S^T: Q^T[4 m + lg][lr] = Q[query lr][4 m + lg]
+    double qa[NM];
+    {
+        const double* src = q + (row0 + min(qi, nq - 1)) * q_dim + (size_t)h * HD + lg;
+#pragma unroll
+        for (int m = 0; m < NM; ++m) qa[m] = qi < nq ? src[4 * m] : 0.0;
+    }
+    const double scale = 1.0 / sqrt((double)HD);
+    double mrun = -1e9;  // running maximum of query qi's scores
+    double lsum = 0.0;   // this lane's share of their exponential sum
+    v4d o[NT];           // o[t][v] = O[query qi][16 t + 4 v + lg]
+#pragma unroll
+    for (int t = 0; t < NT; ++t) o[t] = v4d{0.0, 0.0, 0.0, 0.0};
+    load(0);
+    for (int c = 0; c < nch; ++c) {
+        __syncthreads();  // the previous chunk's reads of kd and vd are done
+        store();
+        load(c + 1);  // in flight during this chunk's products
+        __syncthreads();
+        v4d sa[2] = {v4d{0.0, 0.0, 0.0, 0.0}, v4d{0.0, 0.0, 0.0, 0.0}};
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                const double ak = kd[(16 * kt + lr) * KP + 4 * m + lg];
+                sa[kt] = __builtin_amdgcn_mfma_f64_16x16x4f64(ak, qa[m], sa[kt], 0, 0, 0);
+            }
+        // sa[kt][v] = S[query qi][position c*32 + 16 kt + 4 v + lg]
+        double sv[2][4];
+        bool ok[2][4];
+        double cm = -1e9;  // NaN never wins
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                ok[kt][v] = c * kChunkP + 16 * kt + 4 * v + lg <= qpos;
+                sv[kt][v] = sa[kt][v] * scale;
+                if (ok[kt][v] && sv[kt][v] > cm) cm = sv[kt][v];
+            }
+        {
+            double t = __shfl_xor(cm, 16);
+            cm = t > cm ? t : cm;
+            t = __shfl_xor(cm, 32);
+            cm = t > cm ? t : cm;
+        }
+        if (cm > mrun) {
+            const double alpha = exp(mrun - cm);
+            lsum *= alpha;
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) o[t][v] *= alpha;
+            mrun = cm;
+        }
+        double p[2][4];  // exp(-inf) = 0 at masked positions: no branch
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                p[kt][v] = exp(ok[kt][v] ? sv[kt][v] - mrun : -__builtin_inf());
+                lsum += p[kt][v];
+            }
+        // O^T += V^T P^T: A = V[position 16 kt + 4 m + lg][16 t + lr], B = p[kt][m]
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const double av = vd[(16 * kt + 4 * m + lg) * VP + 16 * t + lr];
+                    o[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(av, p[kt][m], o[t], 0, 0, 0);
+                }
+    }
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+    if (qi < nq) {
+        double* orow = out + (row0 + qi) * q_dim + (size_t)h * HD;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) orow[16 * t + 4 * v + lg] = o[t][v] / lsum;
+    }
+}
+
 template <int HD, int QT>
 __global__ __launch_bounds__(256) void attn_tile_mfma_kernel(const double* __restrict__ q,
                                                              const float* __restrict__ cache_k,
@@ -1557,9 +1718,20 @@ size_t attention_lds_bytes(int hd, int span) {
     return ((size_t)((hd + 1) & ~1) + (size_t)span) * sizeof(double);
 }
 
-size_t attention_scratch_bytes(int rows, int heads, int hd, int span) {
-    // prefill tiles: every score of every row (rows x heads x span fp64)
-    if (rows > kSplitMaxRows) return (hd == 64 || hd == 128) ? (size_t)rows * heads * span * 8 : 0;
+int attention_fast_two_pass_qt() {
+    const char* v = getenv("LOOM_AMD_ATTN_QT");
+    const int qt = v ? atoi(v) : 0;
+    return qt == 2 || qt == 4 ? qt : 0;
+}
+
+size_t attention_scratch_bytes(int rows, int heads, int hd, int span, int strict, int fast_qt) {
+    // prefill tiles of the strict and two-pass fast kernels: every score of
+    // every row (rows x heads x span fp64); the one-pass kernel needs none
+    if (rows > kSplitMaxRows) {
+        if (hd != 64 && hd != 128) return 0;
+        if (!strict && fast_qt == 0) return 0;
+        return (size_t)rows * heads * span * 8;
+    }
     // (room for 32-position chunks; the 64-position kernels use a prefix of each region)
     const size_t rh = (size_t)rows * heads;
     const size_t nc = attn_nchunk32(span);
@@ -1607,8 +1779,8 @@ hipError_t launch_attention_rope(const int32_t* acc, const float* amax, float sq
 
 hipError_t launch_attention(const double* q, const float* cache_k, const float* cache_v,
                             int batch, int seq, const int* pos0, int msl, int span, int heads,
-                            int kv_heads, int hd, int strict, double* scratch, double* out,
-                            hipStream_t s) {
+                            int kv_heads, int hd, int strict, int fast_qt, double* scratch,
+                            double* out, hipStream_t s) {
     if (seq <= 0 || batch <= 0) return hipSuccess;
     if (hd % 4 != 0 || hd > 256 || kv_heads <= 0 || heads % kv_heads != 0) return hipErrorInvalidValue;
     if (span > kMaxAttnSpan || span > msl) return hipErrorInvalidValue;
@@ -1661,15 +1833,33 @@ hipError_t launch_attention(const double* q, const float* cache_k, const float* 
         return hipGetLastError();
     }
     if (hd == 64 || hd == 128) {
+        const int qt = fast_qt == 2 || fast_qt == 4 ? fast_qt : 0;
+        if (!strict && qt == 0) {
+            // heads sharing one KV head go to one workgroup, up to four
+            const int group = heads / kv_heads;
+            const int hpw = group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
+            const dim3 gridh(heads / hpw, ceil_div(seq, 64 / hpw), batch);
+#define LAMD_FLASH(HDV, HPWV)                                                                    \
+    hipLaunchKernelGGL((attn_flash_mfma_kernel<HDV, HPWV>), gridh, dim3(256), 0, s, q, cache_k, \
+                       cache_v, pos0, msl, span, heads, kv_heads, seq, out)
+            if (hd == 128) {
+                if (hpw == 4) LAMD_FLASH(128, 4);
+                else if (hpw == 2) LAMD_FLASH(128, 2);
+                else LAMD_FLASH(128, 1);
+            } else {
+                if (hpw == 4) LAMD_FLASH(64, 4);
+                else if (hpw == 2) LAMD_FLASH(64, 2);
+                else LAMD_FLASH(64, 1);
+            }
+#undef LAMD_FLASH
+            return hipGetLastError();
+        }
         if (!scratch || span % 2 != 0) return hipErrorInvalidValue;
         const dim3 grid(heads, ceil_div(seq, kTileQ), batch);
 #define LAMD_TILE(HDV, F)                                                                          \
     hipLaunchKernelGGL((attn_tile_kernel<HDV, F>), grid, dim3(256), 0, s, q, cache_k, cache_v, pos0, \
                        msl, span, heads, kv_heads, seq, scratch, out)
-        // fast mode: 16-query tiles per workgroup (LOOM_AMD_ATTN_QT = 2 or 4)
-        const char* qtv = getenv("LOOM_AMD_ATTN_QT");
-        const int qt = qtv && atoi(qtv) == 2 ? 2 : qtv && atoi(qtv) == 4 ? 4 : kAttnFastQt;
-        const dim3 gridf(heads, ceil_div(seq, 16 * qt), batch);
+        const dim3 gridf(heads, ceil_div(seq, 16 * (qt ? qt : 2)), batch);
 #define LAMD_FAST(HDV, QTV)                                                                          \
     hipLaunchKernelGGL((attn_tile_mfma_kernel<HDV, QTV>), gridf, dim3(256), 0, s, q, cache_k, cache_v, \
                        pos0, msl, span, heads, kv_heads, seq, scratch, out)

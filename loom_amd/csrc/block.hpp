@@ -34,7 +34,11 @@ hipError_t launch_qkv_rope(const int32_t* acc, const float* amax, float sq, floa
 // decode path, which needs `scratch` (attention_scratch_bytes).
 constexpr int kSplitMaxRows = 16;
 size_t attention_lds_bytes(int hd, int span);
-size_t attention_scratch_bytes(int rows, int heads, int hd, int span);
+// fast_qt: 0 selects the one-pass fast prefill kernel (no score workspace),
+// 2 or 4 the two-pass kernel with that many 16-query tiles per workgroup.
+size_t attention_scratch_bytes(int rows, int heads, int hd, int span, int strict, int fast_qt);
+// LOOM_AMD_ATTN_QT = 2 or 4 asks for the two-pass fast prefill kernel; 0 otherwise.
+int attention_fast_two_pass_qt();
 // Fast decode (one token per sequence, head_dim 64/128): the Q/K/V epilogue
 // of qkv_rope fused into the attention launch (writes the new K/V to the
 // caches, never materializes Q).
@@ -47,7 +51,7 @@ hipError_t launch_attention_rope(const int32_t* acc, const float* amax, float sq
                                  double* q_tap = nullptr);
 hipError_t launch_attention(const double* q, const float* cache_k, const float* cache_v,
                             int batch, int seq, const int* pos0, int msl, int span, int heads,
-                            int kv_heads, int hd, int strict, double* scratch, double* out,
+                            int kv_heads, int hd, int strict, int fast_qt, double* scratch, double* out,
                             hipStream_t s);
 
 // MHA inner norm on fp64 rows in place (data *= scale*w; skipped when

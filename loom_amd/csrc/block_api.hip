@@ -21,6 +21,7 @@ struct BlockDev {
     int q_dim = 0, kv_dim = 0;
     double theta = 10000.0, norm_eps = 0.0, attn_eps = 0.0, ffn_eps = 0.0;
     int activation = 1, strict = 1;
+    int attn_qt = 0;  // fast prefill attention kernel (attention_fast_two_pass_qt at creation)
     bool fuse_rope = true;  // fast decode: Q/K/V epilogue inside the attention launch
     bool fuse_norm = true;  // decode: row norms inside the consuming matmul
     Matrix qkv, o, gate, up, down;  // tiles point into `weights`
@@ -67,8 +68,8 @@ static size_t workspace_layout(const BlockDev& B, int rows, Workspace* W, char* 
     const size_t o_q = L.take(r * B.q_dim * 8);
     const size_t o_at = L.take(r * B.q_dim * 8);
     const size_t sc_small = attention_scratch_bytes(rows < kSplitMaxRows ? rows : kSplitMaxRows,
-                                                    B.heads, B.hd, B.span());
-    const size_t sc_big = attention_scratch_bytes(rows, B.heads, B.hd, B.span());
+                                                    B.heads, B.hd, B.span(), B.strict, B.attn_qt);
+    const size_t sc_big = attention_scratch_bytes(rows, B.heads, B.hd, B.span(), B.strict, B.attn_qt);
     const size_t o_sc = L.take(sc_small > sc_big ? sc_small : sc_big);
     const size_t o_aq = L.take(r * pad_cols(B.q_dim));
     const size_t o_am2 = L.take(r * 4);
@@ -185,6 +186,7 @@ static int build_block(int device, const loom_amd_block_desc* d, const loom_amd_
     B->ffn_eps = d->ffn_eps;
     B->activation = d->ffn_activation;
     B->strict = d->norm_mode == LOOM_AMD_NORM_STRICT;
+    B->attn_qt = attention_fast_two_pass_qt();
     // LOOM_AMD_UNFUSED_ROPE=1 keeps the separate Q/K/V epilogue launch in fast
     // decode (the tests compare both paths)
     const char* unfused = getenv("LOOM_AMD_UNFUSED_ROPE");
@@ -353,7 +355,7 @@ static int block_forward_dev(const BlockDev& B, const Workspace& W, float* x, in
         if (e != hipSuccess) return fail_hip("block qkv rope", e);
         TAP(tap_copy(T.q, W.q, (size_t)R * B.q_dim * 8, s));
         e = launch_attention(W.q, B.cache_k, B.cache_v, batch, seq, pos, B.msl, B.span(), B.heads,
-                             B.kv_heads, B.hd, B.strict, W.scores, W.attn, s);
+                             B.kv_heads, B.hd, B.strict, B.attn_qt, W.scores, W.attn, s);
         if (e != hipSuccess) return fail_hip("block attention", e);
     }
     TAP(tap_copy(T.attn, W.attn, (size_t)R * B.q_dim * 8, s));

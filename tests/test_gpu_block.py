@@ -206,24 +206,33 @@ def test_block_refuses_decode_batch_other_than_warm_cache(orc, torch_dev, tf):
 
 
 @pytest.mark.parametrize("hd,seq", [(128, 300), (64, 200)])
-def test_fast_prefill_attention_query_tiles_agree(orc, torch_dev, tf, monkeypatch, hd, seq):
-    # the fast prefill kernel with 32 or 64 queries per workgroup sums in the
-    # same order: identical bytes for the block output and its K/V caches,
-    # ragged last query tile included
+def test_fast_prefill_attention_kernels_agree(orc, torch_dev, tf, monkeypatch, hd, seq):
+    # the two-pass fast prefill kernel with 32 or 64 queries per workgroup
+    # sums in the same order: identical bytes for the block output and its K/V
+    # caches, ragged last query tile included.  The default one-pass kernel
+    # (running maximum) sums in another fixed order: its attention rows are
+    # within the fast bar (1e-12 of the row scale) of the two-pass rows, and
+    # its K/V caches are the same bytes.
     torch = torch_dev
     sh = Shape(hd * 4, 4, 2, hd, 512, 512)
     w = Weights(orc, sh, seed=451)
     x = orc.normal_f32(seq * sh.hidden, seed=452).reshape(seq, sh.hidden)
-    outs = []
-    for qt in ("2", "4"):
+    outs, attn, kv = [], [], []
+    for qt in ("2", "4", ""):
         monkeypatch.setenv("LOOM_AMD_ATTN_QT", qt)
         blk = tf.BitNetBlock(w.cfg(tf, norm="fast"), w.gpu(tf))
         xd = to_dev(torch, x)
-        blk.forward(xd)
+        _, T = blk.forward(xd, taps=True)
         torch.cuda.synchronize()
         outs.append(xd.cpu().numpy().tobytes())
+        attn.append(T.numpy()["attn"])
+        kv.append(b"".join(c.cpu().numpy().tobytes() for c in blk.kv_cache()))
         blk.release()
-    assert outs[0] == outs[1]
+    assert outs[0] == outs[1] and kv[0] == kv[1] == kv[2]
+    assert np.array_equal(attn[0], attn[1])
+    scale = np.abs(attn[0]).max(axis=-1, keepdims=True)
+    assert np.all(np.abs(attn[2] - attn[0]) <= 1e-12 * scale)
+    assert not np.array_equal(attn[2], np.zeros_like(attn[2]))
 
 
 # ---------------------------------------------------------------- model / decode loop
