@@ -344,6 +344,17 @@ __device__ __forceinline__ void epilogue_store(const EpiDev& e, int i, int n, in
 }
 
 // Arguments of the matmul kernels.
+// Workspace of the small-M split kernel (matmul_skinny.hip): int32 output
+// accumulators of the row groups and one arrival counter per group, both
+// zero between launches (the last workgroup of a group clears them).
+constexpr int kSmallSplitInts = 1 << 21;  // 8 MiB
+constexpr int kSmallSplitGroups = 2048;
+struct SmallSplitWs {
+    int32_t* acc = nullptr;
+    unsigned* ctr = nullptr;
+};
+SmallSplitWs small_split_ws(int device);
+
 struct MatArgs {
     const uint4* w0;
     const uint4* w1;

@@ -21,6 +21,8 @@ constexpr int kSplitTiles = 1024;
 struct SplitWs {
     int32_t* part = nullptr;
     unsigned* ctr = nullptr;
+    int32_t* sacc = nullptr;  // small-M split: accumulators, zero between launches
+    unsigned* sctr = nullptr;  // small-M split: arrival counters, zero between launches
 };
 static std::mutex g_split_mu;
 static std::vector<SplitWs> g_split;
@@ -32,18 +34,34 @@ hipError_t gemm_prepare(int device) {
     if (w.part) return hipSuccess;
     int32_t* part = nullptr;
     unsigned* ctr = nullptr;
+    int32_t* sacc = nullptr;
+    unsigned* sctr = nullptr;
     hipError_t e = hipMalloc(&part, (size_t)kSplitSlots * kSplitSlotInts * 4);
     if (e == hipSuccess) e = hipMalloc(&ctr, (size_t)kSplitTiles * 4);
     if (e == hipSuccess) e = hipMemset(ctr, 0, (size_t)kSplitTiles * 4);
+    if (e == hipSuccess) e = hipMalloc(&sacc, (size_t)kSmallSplitInts * 4);
+    if (e == hipSuccess) e = hipMemset(sacc, 0, (size_t)kSmallSplitInts * 4);
+    if (e == hipSuccess) e = hipMalloc(&sctr, (size_t)kSmallSplitGroups * 4);
+    if (e == hipSuccess) e = hipMemset(sctr, 0, (size_t)kSmallSplitGroups * 4);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         if (part) (void)hipFree(part);
         if (ctr) (void)hipFree(ctr);
+        if (sacc) (void)hipFree(sacc);
+        if (sctr) (void)hipFree(sctr);
         return e;
     }
     w.part = part;
     w.ctr = ctr;
+    w.sacc = sacc;
+    w.sctr = sctr;
     return hipSuccess;
+}
+
+SmallSplitWs small_split_ws(int device) {
+    std::lock_guard<std::mutex> lock(g_split_mu);
+    if (device >= (int)g_split.size()) return SmallSplitWs{};
+    return SmallSplitWs{g_split[device].sacc, g_split[device].sctr};
 }
 
 static SplitWs split_ws(int device) {

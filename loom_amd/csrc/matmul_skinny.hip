@@ -616,6 +616,187 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_nt_kernel(MatArgs p) {
 }
 
 // ------------------------------------------------------------------------
+// small_split: 16 < M <= 64 on pre-quantized rows, one matrix.  What bounds
+// these M is not HBM but the activation bytes every workgroup pulls from L2:
+// with full K per workgroup each CU reads all M x K int8 rows (442 KB at
+// M = 64, K = 6912), and a CU draws only a few tens of GB/s from L2 under
+// that load.  So a workgroup owns NT = 4 adjacent 16-row weight tiles and a
+// slice of KPS = 4 K tiles: it stages its M x 1 KiB activation slice in LDS
+// with row-contiguous 16-byte loads (whole cache lines), its 8 waves take
+// one K tile and two row tiles each, and the waves' partial sums meet in
+// LDS in a fixed order.  The K slices of a row group then meet through
+// device-scope integer atomic adds into the group's accumulators (integer
+// sums: exact in any order); the last workgroup to arrive (arrival counter)
+// reads the totals, runs the epilogue and sets accumulators and counter back
+// to zero for the next launch.  Every partial add has completed (s_waitcnt)
+// before its workgroup's arrival is counted, and the last workgroup reads
+// only after its own arrival returns: the exchange of the split GEMM.
+// ------------------------------------------------------------------------
+constexpr int kSmallNT = 4;
+constexpr int kSmallKps = 4;
+constexpr int kSmallWaves = 8;
+
+struct SmallSplit {
+    int S;          // K slices (workgroups per row group)
+    int32_t* acc;   // row-group accumulators (S > 1)
+    unsigned* ctr;  // arrival counters (S > 1)
+};
+
+template <int MSUB>
+__global__ __launch_bounds__(kSmallWaves * 64) void small_split_kernel(MatArgs p, SmallSplit ss) {
+    constexpr int WAVES = kSmallWaves, T = WAVES * 64, NT = kSmallNT, KPS = kSmallKps;
+    constexpr int R = MSUB * 16;          // staged rows (tokens)
+    constexpr int PITCH = KPS * 256 + 16;  // bytes per staged row (16-row reads: no bank conflicts)
+    constexpr int CH = R * KPS * 16;       // 16-byte chunks staged
+    constexpr int CPT = CH / T;
+    constexpr int QPW = NT * KPS / WAVES;  // row tiles per wave
+    constexpr int EPT = NT * R * 16 / T;   // outputs per thread
+    static_assert(CH % T == 0 && (NT * KPS) % WAVES == 0 && (NT * R * 16) % T == 0, "geometry");
+    static_assert(NT * KPS * R * 16 * 4 <= R * PITCH, "partial sums fit the staging buffer");
+    __shared__ __align__(16) int8_t lds[R * PITCH];  // activation slice, then the waves' partial sums
+    __shared__ int s_last;
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int r = lane & 15;
+    const int g = lane >> 4;
+    const int M = p.e.m;
+    const int ktiles = p.ktiles;
+    const int group = blockIdx.x / ss.S;
+    const int slice = blockIdx.x - group * ss.S;
+    const int nt0 = group * NT;
+    const int kt0 = slice * KPS;
+
+    // activation slice: chunk c is 16 bytes of row c / (16 KPS); a wave reads
+    // 1 KiB of one row.  Rows past M and K tiles past the last read zero.
+    const uint32_t xbytes = (uint32_t)M * (uint32_t)p.ldq;
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(p.xq, xbytes);
+    uint4 st[CPT];
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        const int c = tid + j * T;
+        const int row = c / (KPS * 16), c16 = c % (KPS * 16);
+        const bool ok = row < M && kt0 + c16 / 16 < ktiles;
+        st[j] = buffer_load16(xr, ok ? (uint32_t)row * (uint32_t)p.ldq + (uint32_t)kt0 * 256u + c16 * 16u : xbytes);
+    }
+    // weights: wave w takes K tile kt0 + w % KPS of row tiles w / KPS + 2j
+    const int ktl = wave % KPS;
+    const uint32_t wbytes = (uint32_t)p.ntiles * (uint32_t)ktiles * 1024u;
+    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(p.w0, wbytes);
+    uint4 wv[QPW];
+#pragma unroll
+    for (int j = 0; j < QPW; ++j) {
+        const int nt = nt0 + wave / KPS + j * (WAVES / KPS);
+        const int kt = kt0 + ktl;
+        const bool ok = nt < p.ntiles && kt < ktiles;
+        wv[j] = buffer_load16(wr, ok ? (((uint32_t)nt * (uint32_t)ktiles + (uint32_t)kt) * 64u + lane) * 16u : wbytes);
+    }
+    // the epilogue's per-token amax and sum(xq), loaded while the rest is in
+    // flight (clamped, unconditional loads: a branch around a load would make
+    // the compiler wait for every load issued before it)
+    float am[EPT];
+    int xs[EPT];
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+        const int tok = min(((tid + i * T) % (R * 16)) >> 4, M - 1);
+        am[i] = p.e.amax[tok];
+        xs[i] = p.e.xsum[tok];
+    }
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        const int c = tid + j * T;
+        *(uint4*)&lds[(c / (KPS * 16)) * PITCH + (c % (KPS * 16)) * 16] = st[j];
+    }
+    __syncthreads();
+
+    v4i acc[QPW][MSUB];
+#pragma unroll
+    for (int j = 0; j < QPW; ++j)
+#pragma unroll
+        for (int ms = 0; ms < MSUB; ++ms) acc[j][ms] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        v4i a[MSUB];
+#pragma unroll
+        for (int ms = 0; ms < MSUB; ++ms)
+            a[ms] = *(const v4i*)&lds[(ms * 16 + r) * PITCH + ktl * 256 + 64 * t + 16 * g];
+#pragma unroll
+        for (int j = 0; j < QPW; ++j) {
+            const v4i b = unpack_codes(word_of(wv[j], t));
+#pragma unroll
+            for (int ms = 0; ms < MSUB; ++ms) acc[j][ms] = mfma_i8(a[ms], b, acc[j][ms]);
+        }
+    }
+    __syncthreads();  // every wave has read its activations
+    // partial sums: part[q][k][tok][col], q = row tile, k = K tile of the slice
+    int* part = (int*)lds;
+#pragma unroll
+    for (int j = 0; j < QPW; ++j) {
+        const int q = wave / KPS + j * (WAVES / KPS);
+#pragma unroll
+        for (int ms = 0; ms < MSUB; ++ms)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                part[((q * KPS + ktl) * R + ms * 16 + 4 * g + v) * 16 + r] = acc[j][ms][v];
+    }
+    __syncthreads();
+    int tot[EPT];
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+        const int e = tid + i * T;
+        const int q = e / (R * 16), rem = e % (R * 16);
+        int s = 0;
+#pragma unroll
+        for (int k = 0; k < KPS; ++k) s += part[(q * KPS + k) * R * 16 + rem];
+        tot[i] = s;
+    }
+    if (ss.S > 1) {
+        int32_t* gacc = ss.acc + (size_t)group * NT * 64 * 16;
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) {
+            const int e = tid + i * T;
+            const int q = e / (R * 16), rem = e % (R * 16);
+            if ((rem >> 4) < M)
+                __hip_atomic_fetch_add(&gacc[q * 64 * 16 + rem], tot[i], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) {
+            s_last = __hip_atomic_fetch_add(&ss.ctr[group], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                     (unsigned)(ss.S - 1);
+        }
+        __syncthreads();
+        if (!s_last) return;
+        // (rows past M were never added to: zero, read and cleared unconditionally
+        // so that no branch serializes the loads)
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) {
+            const int e = tid + i * T;
+            const int q = e / (R * 16), rem = e % (R * 16);
+            tot[i] = __hip_atomic_load(&gacc[q * 64 * 16 + rem], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) {
+            const int e = tid + i * T;
+            const int q = e / (R * 16), rem = e % (R * 16);
+            __hip_atomic_store(&gacc[q * 64 * 16 + rem], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        // every workgroup of the group has arrived: ready for the next launch
+        if (tid == 0) __hip_atomic_store(&ss.ctr[group], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+        const int e = tid + i * T;
+        const int q = e / (R * 16), rem = e % (R * 16);
+        const int tok = rem >> 4, col = rem & 15;
+        const int n = (nt0 + q) * kTileRows + col;
+        if (tok < M && nt0 + q < p.ntiles && n < p.e.n)
+            epilogue_store(p.e, tok, n, tot[i], tot[i], row_scale(p.e, am[i], xs[i]));
+    }
+}
+
+// ------------------------------------------------------------------------
 // dispatch
 // ------------------------------------------------------------------------
 
@@ -717,9 +898,41 @@ static hipError_t launch_skinny_nt(const MatArgs& p, hipStream_t s) {
     return hipGetLastError();
 }
 
+static int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return v && *v ? atoi(v) : dflt;
+}
+
+// small_split_kernel for one matrix when its workspace holds the row groups.
+// Its K-slice exchange costs a few microseconds (three device-scope round
+// trips), so it pays only where full-K workgroups pull the most activation
+// bytes: long K (more than 16 K tiles) and M > 24 (measured at M = 17..64:
+// K = 6912 13.8 vs 16.2 us at M = 64, 9.4 vs 9.7 at M = 32; K = 2560 slower
+// at every M).  LOOM_AMD_SMALLM = 1 always takes it, 0 never.
+template <int MSUB>
+static bool launch_small_split(const MatArgs& p, int device, hipStream_t s, hipError_t* e) {
+    const int mode = env_int("LOOM_AMD_SMALLM", -1);
+    if (mode == 0 || (mode != 1 && (p.ktiles <= 16 || p.e.m <= 24))) return false;
+    const int groups = ceil_div(p.ntiles, kSmallNT);
+    const int S = ceil_div(p.ktiles, kSmallKps);
+    SmallSplit ss{S, nullptr, nullptr};
+    if (S > 1) {
+        const SmallSplitWs ws = small_split_ws(device);
+        if (!ws.acc || groups > kSmallSplitGroups || (size_t)groups * kSmallNT * 64 * 16 > (size_t)kSmallSplitInts)
+            return false;
+        ss.acc = ws.acc;
+        ss.ctr = ws.ctr;
+    }
+    hipLaunchKernelGGL((small_split_kernel<MSUB>), dim3(groups * S), dim3(kSmallWaves * 64), 0, s, p, ss);
+    *e = hipGetLastError();
+    return true;
+}
+
 // (four tiles of both SwiGLU matrices do not fit the register file)
 template <int NMAT, int MSUB>
-static hipError_t launch_small_m(const MatArgs& p, hipStream_t s) {
+static hipError_t launch_small_m(const MatArgs& p, int device, hipStream_t s) {
+    hipError_t e = hipSuccess;
+    if (NMAT == 1 && launch_small_split<MSUB>(p, device, s, &e)) return e;
     const int nt = skinny_nt(p.ntiles, p.ktiles);
     if (nt == 4 && NMAT == 1) return launch_skinny_nt<NMAT, MSUB, 4>(p, s);
     if (nt >= 2) return launch_skinny_nt<NMAT, MSUB, 2>(p, s);
@@ -770,8 +983,8 @@ hipError_t launch_matmul(const Matrix* w0, const Matrix* w1, const QuantAct& a, 
     const bool two = epi.kind == EPI_SWIGLU;
     if (!two && stream_ok(m, w0->cols, w0->ntiles, false, epi)) return launch_stream(p, false, s);
     if (m <= 16) return two ? launch_skinny<2, 1, false>(p, s) : launch_skinny<1, 1, false>(p, s);
-    if (m <= 32) return two ? launch_small_m<2, 2>(p, s) : launch_small_m<1, 2>(p, s);
-    if (m <= 64) return two ? launch_small_m<2, 4>(p, s) : launch_small_m<1, 4>(p, s);
+    if (m <= 32) return two ? launch_small_m<2, 2>(p, w0->device, s) : launch_small_m<1, 2>(p, w0->device, s);
+    if (m <= 64) return two ? launch_small_m<2, 4>(p, w0->device, s) : launch_small_m<1, 4>(p, w0->device, s);
     return launch_gemm(p, two, w0->device, s);
 }
 

@@ -631,16 +631,44 @@ def test_gemm_tile_order_groups(orc, torch_dev, bn, monkeypatch, group):
     _check_dense(orc, torch_dev, bn, m, x)
 
 
-@pytest.mark.parametrize("nt", ["1", "2", "4"])
+@pytest.mark.parametrize("nt", ["split", "1", "2", "4"])
 @pytest.mark.parametrize("rows,cols,M", [(6912, 2560, 64), (2560, 6912, 40), (1000, 2570, 17),
-                                         (6900, 2560, 33)])
+                                         (6900, 2560, 33), (40000, 512, 20)])
 def test_small_m_tiles_per_workgroup(orc, torch_dev, bn, monkeypatch, nt, rows, cols, M):
-    # 16 < M <= 64 with one, two or four 16-row tiles per workgroup (a ragged
-    # last group included): int32 accumulators and fp32 outputs bit-exact
-    monkeypatch.setenv("LOOM_AMD_SKINNY_NT", nt)
+    # 16 < M <= 64: the K-split kernel (default; 40000 rows exceed its
+    # workspace and take the single-workgroup kernels), and the skinny kernels
+    # with one, two or four 16-row tiles per workgroup (ragged last group and
+    # K slice included): int32 accumulators and fp32 outputs bit-exact
+    if nt == "split":
+        monkeypatch.setenv("LOOM_AMD_SMALLM", "1")
+    else:
+        monkeypatch.setenv("LOOM_AMD_SMALLM", "0")
+        monkeypatch.setenv("LOOM_AMD_SKINNY_NT", nt)
     m = orc.random_matrix(rows, cols, seed=rows + M)
     x = orc.normal_f32(M * cols, seed=M + 7).reshape(M, cols)
     _check_dense(orc, torch_dev, bn, m, x)
+
+
+def test_small_m_split_repeatable(orc, torch_dev, bn, monkeypatch):
+    # the K-split kernel leaves its accumulators and arrival counters at zero:
+    # back-to-back launches of two shapes (different row groups and slices),
+    # residual epilogue included, all give the oracle's bytes
+    monkeypatch.setenv("LOOM_AMD_SMALLM", "1")
+    torch = torch_dev
+    cases = []
+    for rows, cols, M in ((2560, 6912, 64), (6912, 2560, 29)):
+        m = orc.random_matrix(rows, cols, seed=rows + 3)
+        x = orc.normal_f32(M * cols, seed=cols + M).reshape(M, cols)
+        res = orc.normal_f32(M * rows, seed=M).reshape(M, rows)
+        ref = (orc.dense_forward(m, x, simd=True).pre + res).astype(np.float32)
+        cases.append((gpu_matrix(bn, m), to_dev(torch, x), to_dev(torch, res), ref))
+    outs = []
+    for rep in range(20):
+        for w, xd, rd, ref in cases:
+            outs.append((bn.dense_forward_packed_ternary(w, xd, residual=rd)[0], ref))
+    torch.cuda.synchronize()
+    for o, ref in outs:
+        assert o.cpu().numpy().tobytes() == ref.tobytes()
 
 
 @pytest.mark.parametrize("nt", ["1", "2"])
