@@ -79,365 +79,55 @@ struct GemmGrid {
 };
 
 // ------------------------------------------------------------------------
-// gemm32 (launched for the 128-token tile, MI = 4; the 64-token tile runs
-// gemm64_kernel below): v_mfma_i32_32x32x32_i8, which issues int8 at twice the rate of the
-// 16x16x64 form on gfx950 (measured: 4.5 vs 2.5 POPS sustained).  256 threads
-// as 4 waves along N, two workgroups per CU; workgroup tile 128 tokens x
-// 256/NMAT weight rows per matrix, wave tile 128 tokens x 64/NMAT weight rows
-// (4 x NJ blocks of 32 x 32); K stages of 128 columns.  Workgroups are mapped
-// so that each XCD (blockIdx % 8) walks a contiguous run of tiles with the
-// weight-row index fastest: consecutive tiles on one XCD share the activation
-// tile, which then stays in that XCD's L2.
+// gemm_lds_kernel: v_mfma_i32_32x32x32_i8, which issues int8 at twice the
+// rate of the 16x16x64 form on gfx950 (measured: 4.5 vs 2.5 POPS sustained).
+// 256 threads as 4 waves along N; workgroup tile 32*MI tokens x 256/NMAT
+// weight rows per matrix, wave tile 32*MI tokens x 64/NMAT weight rows (MI x
+// NJ blocks of 32 x 32); K stages of 256 columns (one K tile).  MI = 2
+// (64-token tiles, three workgroups per CU) serves mid-size M and split K;
+// MI = 4 (128-token tiles, two per CU) feeds each unpacked weight word to
+// four MFMAs instead of two, which pays once the grid is large.
+// Tile order: workgroups are mapped so that each XCD (blockIdx % 8) walks a
+// contiguous run of tiles, in groups of `group` token tiles with the
+// weight-row group fastest inside a group: consecutive tiles on one XCD share
+// activation and weight tiles, which then stay in that XCD's L2.
 // Weights come straight from the 16-row tile layout: lane l takes weight row
 // l&31 of its 32-row block (tile (l>>4)&1, row l&15) and loads the words of
 // tile lanes (l&15) + 16h and (l&15) + 16h + 32 (h = l>>5), which hold the K
 // chunks 4t + h and 4t + 2 + h of every 256-column tile.  MFMA step q of a
 // stage pairs chunk c and c + 1 (c = 0, 4, 2, 6 within the stage) across the
 // two K halves, so the eight words a lane holds per tile are exactly its
-// eight K steps.  Activations: padded LDS rows; lane l reads row l&31, chunk
-// c + h.  The loop runs two stages per trip so the two register sets of the
-// staged loads swap roles statically (no copies, no waits on fresh loads).
-// MI = 2 halves the tile to 64 tokens (more workgroups for mid-size M).
+// eight K steps.
+// Activations: the stages are copied global -> LDS by the memory units
+// (buffer_load ... lds, 16 bytes a lane), so no VGPRs stage them and the
+// A-operand reads run ahead of the MFMAs.  MI = 2 keeps three stage buffers
+// (stage s + 2 copied, with its weight words loaded into the third register
+// set, while stage s is computed); MI = 4 keeps two (stage s + 1).  One
+// barrier per stage both publishes the next stage and frees the buffer just
+// read.  Each wave waits for its own copies (vmcnt) before that barrier; a
+// bare s_barrier is used because __syncthreads' release fence would wait for
+// every outstanding copy.
+// Stage buffer layout: 32*MI rows x 16 chunks of 16 bytes, row R at R*256,
+// its logical chunk ch at physical chunk ch ^ (R & 15), so the 8 (or 16) rows
+// a group of lanes reads in one MFMA step fall in distinct banks; the copies
+// gather each row's chunks in that order (each copy instruction still reads
+// whole 256-byte row segments).
 // Split K (ksplit > 1, MI = 2 only): workgroup (tile, r) sums K stages
 // [r*sps, (r+1)*sps), stores its int32 accumulators to its workspace slot,
 // and the last of the tile's workgroups to arrive (a device-scope counter)
 // adds the other slots to its own -- integer adds, so the result is the same
 // in any order -- and runs the epilogue.
-// ------------------------------------------------------------------------
-
-// EPI: 0 = plain dense (fp32 out only), 1 + EPI_DENSE / EPI_SWIGLU / EPI_ACC =
-// that epilogue kind with its optional bias, residual, activation and taps.
-template <int NMAT, int EPI, int MI>
-__global__ __launch_bounds__(256, 2) void gemm32_kernel(MatArgs p, GemmGrid gg) {
-    constexpr int NJ = 2 / NMAT;
-    constexpr int BM = 32 * MI;
-    constexpr int VALS = NMAT * MI * NJ * 16;  // accumulators per thread
-    // K stage width in bytes: 64-token tiles take a whole 256-column K tile
-    // per stage (twice the bytes in flight per register set)
-    constexpr int SW = MI == 2 ? 256 : 128;
-    constexpr int KROW = SW + 16;    // padded LDS row: rows start 16 bytes apart mod 256
-    constexpr int CPR = SW / 16;     // 16-byte chunks per row
-    constexpr int RP = 256 / CPR;    // rows per load pass of 256 threads
-    constexpr int NA = BM / RP;      // activation loads per thread per stage
-    constexpr int WPS = SW / 64;     // B words per tile lane per stage
-    // activation stages; the epilogue parks 4 waves x 32 rows x 72 ints here
-    constexpr int kAsBytes = 2 * BM * KROW > 4 * 32 * 72 * 4 ? 2 * BM * KROW : 4 * 32 * 72 * 4;
-    __shared__ __align__(16) int8_t As_raw[kAsBytes];
-    int8_t (*As)[BM * KROW] = (int8_t (*)[BM * KROW])As_raw;
-    __shared__ int s_last;
-    // per-token epilogue constants, loaded before the main loop so the
-    // epilogue issues no loads between its stores (vmcnt counts both in order)
-    __shared__ double s_os0[BM], s_os1[NMAT == 2 ? BM : 1];
-    __shared__ int s_xs[BM];
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6;
-    const int lane = tid & 63;
-    const int wn = wave;
-    const int l32 = lane & 31, h = lane >> 5;
-    const int M = p.e.m;
-    const int ktiles = p.ktiles;
-    const int nstages = ktiles * (256 / SW);
-    const int S = gg.ksplit;
-
-    // split index fastest: the workgroups of one tile run on one XCD and
-    // exchange their partial sums through its L2
-    const int total = gg.mtiles * gg.ngroups * S;
-    const int per_xcd = (total + kXcds - 1) / kXcds;
-    const int linear = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
-    if (linear >= total) return;
-    const int tile = linear / S;
-    const int split = linear - tile * S;
-    // Tile order: `group` token tiles vary fastest, then the weight-row
-    // group, so the workgroups resident on one XCD (a contiguous run) share a
-    // few activation tiles and a few weight tiles that fit its L2 together.
-    int mt, ng;
-    if (gg.group > 0) {
-        const int per_group = gg.group * gg.ngroups;
-        const int g0 = tile / per_group;
-        const int first = g0 * gg.group;
-        const int gsz = min(gg.mtiles - first, gg.group);
-        const int in = tile - g0 * per_group;
-        mt = first + in % gsz;
-        ng = in / gsz;
-    } else {
-        mt = tile / gg.ngroups;
-        ng = tile % gg.ngroups;
-    }
-    const int st0 = split * gg.sps;
-    const int st1 = min(st0 + gg.sps, nstages);
-    const int m_wg = mt * BM;
-    const int nb0 = (ng * 4 + wn) * NJ;  // wave's first 32-row weight block
-    for (int t = tid; t < BM; t += 256) {
-        const int tok = min(m_wg + t, M - 1);
-        const RowScale rs = row_scale(p.e, p.e.amax[tok], p.e.xsum[tok]);
-        s_os0[t] = rs.os0;
-        if (NMAT == 2) s_os1[t] = rs.os1;
-        s_xs[t] = rs.xs;
-    }
-
-    const __amdgpu_buffer_rsrc_t wres0 =
-        __builtin_amdgcn_make_buffer_rsrc((void*)p.w0, 0, 0x7fffffff, kBufferWord3);
-    const __amdgpu_buffer_rsrc_t wres1 =
-        __builtin_amdgcn_make_buffer_rsrc((void*)p.w1, 0, 0x7fffffff, kBufferWord3);
-    const __amdgpu_buffer_rsrc_t ares =
-        __builtin_amdgcn_make_buffer_rsrc((void*)p.xq, 0, 0x7fffffff, kBufferWord3);
-    int woff[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        const int nt = min(2 * (nb0 + j) + ((lane >> 4) & 1), p.ntiles - 1);
-        woff[j] = (nt * ktiles * 64 + (lane & 15) + 16 * h) * 16;
-    }
-    // A stage: BM token rows x SW bytes, NA 16-byte loads per thread; load c
-    // of thread tid -> row RP*c + tid/CPR, 16-byte column tid%CPR
-    int aoff_g[NA];
-#pragma unroll
-    for (int c = 0; c < NA; ++c) {
-        const int row = min(m_wg + RP * c + tid / CPR, M - 1);
-        aoff_g[c] = row * p.ldq + (tid % CPR) * 16;
-    }
-    const int aoff0 = (tid / CPR) * KROW + (tid % CPR) * 16;
-    auto load_a = [&](int stage, uint4 (&st)[NA]) {
-#pragma unroll
-        for (int c = 0; c < NA; ++c)
-            st[c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ares, aoff_g[c], stage * SW, 0));
-    };
-    auto store_a = [&](int buf, const uint4 (&st)[NA]) {
-#pragma unroll
-        for (int c = 0; c < NA; ++c) *(uint4*)(&As[buf][aoff0 + c * RP * KROW]) = st[c];
-    };
-    // B stage: words of both tile lanes (u) covering the stage's columns: for
-    // SW = 128 words 2*(s&1), 2*(s&1)+1 of K tile s>>1; for SW = 256 all four
-    // words of K tile s
-    auto load_b = [&](int stage, uint32_t (&b)[NMAT][NJ][2][WPS]) {
-        const int soff = SW == 256 ? stage * 1024 : (stage >> 1) * 1024 + (stage & 1) * 8;
-#pragma unroll
-        for (int mat = 0; mat < NMAT; ++mat)
-#pragma unroll
-            for (int j = 0; j < NJ; ++j)
-#pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    const __amdgpu_buffer_rsrc_t r = mat == 0 ? wres0 : wres1;
-                    if (SW == 256) {
-                        const uint4 w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, woff[j] + 512 * u, soff, 0));
-                        b[mat][j][u][0] = w.x;
-                        b[mat][j][u][1] = w.y;
-                        b[mat][j][u][WPS > 2 ? 2 : 0] = w.z;
-                        b[mat][j][u][WPS > 3 ? 3 : 1] = w.w;
-                    } else {
-                        const uint2 w = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, woff[j] + 512 * u, soff, 0));
-                        b[mat][j][u][0] = w.x;
-                        b[mat][j][u][1] = w.y;
-                    }
-                }
-    };
-
-    v16i acc[NMAT][MI][NJ];
-#pragma unroll
-    for (int a = 0; a < NMAT; ++a)
-#pragma unroll
-        for (int i = 0; i < MI; ++i)
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) acc[a][i][j] = v16i{};
-
-    const int a_row = l32 * KROW + 16 * h;
-    auto compute = [&](int buf, const uint32_t (&bw)[NMAT][NJ][2][WPS]) {
-#pragma unroll
-        for (int hh = 0; hh < SW / 128; ++hh)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int cq = (q & 1) * 4 + (q >> 1) * 2;  // first chunk of the step's pair
-                v4i b[NMAT][NJ];
-#pragma unroll
-                for (int mat = 0; mat < NMAT; ++mat)
-#pragma unroll
-                    for (int j = 0; j < NJ; ++j) b[mat][j] = unpack_codes(bw[mat][j][q >> 1][2 * hh + (q & 1)]);
-                v4i a[MI];
-#pragma unroll
-                for (int i = 0; i < MI; ++i)
-                    a[i] = *(const v4i*)(&As[buf][a_row + i * 32 * KROW + hh * 128 + 16 * cq]);
-#pragma unroll
-                for (int i = 0; i < MI; ++i)
-#pragma unroll
-                    for (int mat = 0; mat < NMAT; ++mat)
-#pragma unroll
-                        for (int j = 0; j < NJ; ++j) acc[mat][i][j] = mfma32_i8(a[i], b[mat][j], acc[mat][i][j]);
-            }
-    };
-
-    // Loads are issued in the loop's order (a, b of one stage, then of the
-    // next) so the wait counts at the loop head match on entry and back edge.
-    const int last = st1 - 1;
-    uint4 a0[NA], a1[NA];
-    uint32_t b0[NMAT][NJ][2][WPS], b1[NMAT][NJ][2][WPS];
-    load_a(st0, a0);
-    __builtin_amdgcn_sched_barrier(0);
-    load_b(st0, b0);
-    __builtin_amdgcn_sched_barrier(0);
-    load_a(min(st0 + 1, last), a1);
-    __builtin_amdgcn_sched_barrier(0);
-    load_b(min(st0 + 1, last), b1);
-    __builtin_amdgcn_sched_barrier(0);
-    store_a(0, a0);
-    __syncthreads();
-    // two stages per trip; set 0 holds the stages at even distance from st0,
-    // set 1 the others; an odd range ends with one stage in set 0
-    int s = st0;
-    for (; s + 1 < st1; s += 2) {
-        load_a(min(s + 2, last), a0);
-        compute(0, b0);
-        load_b(min(s + 2, last), b0);
-        store_a(1, a1);
-        __syncthreads();
-        load_a(min(s + 3, last), a1);
-        compute(1, b1);
-        load_b(min(s + 3, last), b1);
-        store_a(0, a0);
-        __syncthreads();
-    }
-    if (s < st1) {
-        compute(0, b0);
-        __syncthreads();  // every wave has read buffer 0 before the epilogue parks its sums there
-    }
-
-    if (MI == 2 && S > 1) {
-        // Partial sums of this K range -> slot `linear` (value-major: each
-        // instruction covers 256 contiguous bytes).  The exchange uses
-        // device-scope relaxed atomic stores and loads (sc1: coherent across the
-        // XCDs' L2s, without the whole-L2 write-back and invalidate a
-        // device-scope fence costs): every slot store has completed (s_waitcnt)
-        // before the workgroup's arrival is counted, and the last workgroup
-        // reads the other slots only after its own arrival returns.
-        int32_t* mine = gg.part + (size_t)linear * kSplitSlotInts;
-#pragma unroll
-        for (int a = 0; a < NMAT; ++a)
-#pragma unroll
-            for (int i = 0; i < MI; ++i)
-#pragma unroll
-                for (int j = 0; j < NJ; ++j)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v)
-                        __hip_atomic_store(&mine[(((a * MI + i) * NJ + j) * 16 + v) * 256 + tid], acc[a][i][j][v],
-                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (tid == 0) {
-            s_last = __hip_atomic_fetch_add(&gg.ctr[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                     (unsigned)(S - 1);
-        }
-        __syncthreads();
-        if (!s_last) return;
-        for (int o = 0; o < S; ++o) {
-            if (o == split) continue;
-            const int32_t* src = gg.part + (size_t)(tile * S + o) * kSplitSlotInts;
-#pragma unroll
-            for (int a = 0; a < NMAT; ++a)
-#pragma unroll
-                for (int i = 0; i < MI; ++i)
-#pragma unroll
-                    for (int j = 0; j < NJ; ++j) {
-                        v16i t;
-#pragma unroll
-                        for (int v = 0; v < 16; ++v)
-                            t[v] = __hip_atomic_load(&src[(((a * MI + i) * NJ + j) * 16 + v) * 256 + tid],
-                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        acc[a][i][j] += t;
-                    }
-        }
-        // every workgroup of the tile has arrived: ready for the next launch
-        if (tid == 0) __hip_atomic_store(&gg.ctr[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    static_assert(MI != 2 || VALS * 256 == kSplitSlotInts, "a split slot holds one 64-token tile");
-
-    // Epilogue, one 32-token block i at a time: each wave parks its int32
-    // block (32 x 64 values) in its own 9 KB of the (now idle) activation
-    // buffers, then lane c finishes column c of every row, so each store
-    // instruction writes 256 contiguous bytes and the loop stays small.
-    // Residual loads are issued 8 rows ahead of their stores (vmcnt counts
-    // loads and stores in one order).
-    constexpr int kPitch = 72;  // ints per parked row: the two half-waves' rows land 32 banks apart
-    int* park = (int*)&As[0][0] + wave * 32 * kPitch;
-    const int col = lane & (NMAT == 2 ? 31 : 63);
-    const int n = nb0 * 32 + col;
-    const bool ncol = n < p.e.n;
-    const int nc = min(n, p.e.n - 1);
-    const float bias0 = EPI && p.e.bias0 ? p.e.bias0[nc] : 0.0f;
-    const float bias1 = EPI && NMAT == 2 && p.e.bias1 ? p.e.bias1[nc] : 0.0f;
-    const bool has_res = EPI == 1 + EPI_DENSE && p.e.residual;
-    constexpr int RPI = NMAT == 2 ? 2 : 1;  // rows per wave instruction
-#pragma unroll 1
-    for (int i = 0; i < MI; ++i) {
-        // (a uniform branch per block keeps acc in registers: no dynamic index)
-#pragma unroll
-        for (int ib = 0; ib < MI; ++ib) {
-            if (ib != i) continue;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int row = 8 * (v >> 2) + 4 * h + (v & 3);
-#pragma unroll
-                for (int mat = 0; mat < NMAT; ++mat)
-#pragma unroll
-                    for (int j = 0; j < NJ; ++j) park[row * kPitch + (mat + j) * 32 + l32] = acc[mat][ib][j][v];
-            }
-        }
-        __syncthreads();
-        const int t0 = 32 * i + (NMAT == 2 ? (lane >> 5) : 0);
-#pragma unroll 1
-        for (int r0 = 0; r0 < 32; r0 += 8 * RPI) {
-            float res[8];
-            if (has_res) {
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const int tok = min(m_wg + t0 + r0 + u * RPI, M - 1);
-                    res[u] = p.e.residual[(size_t)tok * p.e.ldo + nc];
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int rl = r0 + u * RPI + (NMAT == 2 ? (lane >> 5) : 0);  // row within the block
-                const int t = 32 * i + rl;
-                const int tok = m_wg + t;
-                if (tok >= M || !ncol) continue;
-                const int raw0 = park[rl * kPitch + col];
-                const int raw1 = NMAT == 2 ? park[rl * kPitch + 32 + col] : raw0;
-                if (EPI == 0) {
-                    __builtin_nontemporal_store((float)((double)(raw0 - s_xs[t]) * s_os0[t]),
-                                                &p.e.out[(size_t)tok * p.e.ldo + n]);
-                } else {
-                    epilogue_store_pre<EPI - 1>(p.e, tok, n, raw0, raw1, s_os0[t], NMAT == 2 ? s_os1[t] : 0.0,
-                                                s_xs[t], bias0, bias1, has_res ? res[u] : 0.0f);
-                }
-            }
-        }
-        __syncthreads();
-    }
-}
-
-// ------------------------------------------------------------------------
-// gemm64: the 64-token tile with its activation stages copied global -> LDS
-// by the memory units (buffer_load ... lds, 16 bytes a lane), so no VGPRs
-// stage them and the A-operand reads can run ahead of the MFMAs at three
-// workgroups per CU.  Three stage buffers: stage s + 2 is copied (and its
-// weight words loaded into the third register set) while stage s is
-// computed, and one barrier per stage both publishes stage s + 1 and frees
-// the buffer of stage s.  Each wave waits for its own copies (vmcnt) before
-// that barrier; a bare s_barrier is used because __syncthreads' release
-// fence would wait for every outstanding copy.
-// Stage buffer layout: 64 rows x 16 chunks of 16 bytes, row R at R*256, its
-// logical chunk ch at physical chunk ch ^ (R & 15), so the 8 (or 16) rows a
-// group of lanes reads in one MFMA step fall in distinct banks; the copies
-// gather each row's chunks in that order (each copy instruction still reads
-// whole 256-byte row segments).
-// Weights, tile order, split K and per-token constants are as in gemm32.
 // The epilogue stores straight from the accumulators: per instruction the
 // two half-waves write 128 contiguous bytes of two rows.
+// EPI: 0 = plain dense (fp32 out only), 1 + EPI_DENSE / EPI_SWIGLU / EPI_ACC =
+// that epilogue kind with its optional bias, residual, activation and taps.
 // ------------------------------------------------------------------------
 
-constexpr int kG64Stage = 64 * 256;  // bytes of one activation stage
 #ifndef LAMD_G64_AHEAD
 #define LAMD_G64_AHEAD 2
 #endif
 
-// The three stage buffers are distinct arrays and these helpers take
+// The stage buffers are distinct arrays and these helpers take
 // restrict pointers, so the compiler's wait before an LDS read covers only
 // the copies into the buffer being read.
 __device__ __forceinline__ void g64_copy(__amdgpu_buffer_rsrc_t r, int8_t* __restrict__ dst, int voff,
@@ -458,17 +148,17 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
 }
 
-template <int NMAT, int EPI>
-__global__ __launch_bounds__(256, 2) void gemm64_kernel(MatArgs p, GemmGrid gg) {
+template <int NMAT, int EPI, int MI>
+__global__ __launch_bounds__(256, 2) void gemm_lds_kernel(MatArgs p, GemmGrid gg) {
     constexpr int NJ = 2 / NMAT;
-    constexpr int MI = 2;
-    constexpr int BM = 64;
-    constexpr int NA = 4;     // copies per thread per stage
-    constexpr int NSTEP = 8;  // MFMA K steps per 256-column stage
+    constexpr int BM = 32 * MI;
+    constexpr int NA = BM / 16;  // copies per thread per stage
+    constexpr int NSTEP = 8;     // MFMA K steps per 256-column stage
     constexpr int NB = NMAT * NJ * 2;  // weight loads per thread per stage
-    __shared__ __align__(16) int8_t As0[kG64Stage];
-    __shared__ __align__(16) int8_t As1[kG64Stage];
-    __shared__ __align__(16) int8_t As2[kG64Stage];
+    static_assert(MI == 2 || MI == 4, "64- or 128-token tiles");
+    __shared__ __align__(16) int8_t As0[BM * 256];
+    __shared__ __align__(16) int8_t As1[BM * 256];
+    __shared__ __align__(16) int8_t As2[MI == 2 ? BM * 256 : 16];  // (128-token tiles: two buffers)
     __shared__ int s_last;
     __shared__ double s_os0[BM], s_os1[NMAT == 2 ? BM : 1];
     __shared__ int s_xs[BM];
@@ -612,11 +302,36 @@ __global__ __launch_bounds__(256, 2) void gemm64_kernel(MatArgs p, GemmGrid gg) 
             if (idx + LAMD_G64_AHEAD < NSTEP) __builtin_amdgcn_sched_group_barrier(0x100, MI, 0);
         }
     };
-    // Vector-memory operations issued after stage s's copies when the wait
-    // for them is reached: stage s's weight loads and stage s+1's copies and
-    // weight loads.
-    constexpr int kAfter = NB + NA + NB;
+    // Vector-memory operations that may still be outstanding when a stage's
+    // copies must have landed: the whole issue of the stage after it.  (The
+    // scheduler may place an issue's weight loads before or after its
+    // copies, so a count that relied on the order inside one issue could let
+    // copies of the stage about to be read through.)
+    constexpr int kAfter = NA + NB;
     uint32_t bw0[NMAT][NJ][2][4], bw1[NMAT][NJ][2][4], bw2[NMAT][NJ][2][4];
+    if constexpr (MI == 4) {
+        // 128-token tiles: two 32 KB stage buffers (two workgroups per CU),
+        // stage s+1 copied while stage s is computed
+        // (every wait counts all of the next stage's loads: the scheduler may
+        // place its weight loads before or after its copies)
+        issue(As0, st0, bw0);
+        wait_vm_lgkm0<0>();  // (lgkmcnt also covers the per-token constants)
+        __builtin_amdgcn_s_barrier();
+        int s = st0;
+        for (; s + 1 < st1; s += 2) {
+            issue(As1, s + 1, bw1);
+            compute(As0, bw0);
+            region_order();
+            wait_vm_lgkm0<0>();  // stage s+1's copies have landed; As0's reads returned
+            __builtin_amdgcn_s_barrier();
+            issue(As0, min(s + 2, last), bw0);
+            compute(As1, bw1);
+            region_order();
+            wait_vm_lgkm0<0>();
+            __builtin_amdgcn_s_barrier();
+        }
+        if (s < st1) compute(As0, bw0);
+    } else {
     issue(As0, st0, bw0);
     issue(As1, min(st0 + 1, last), bw1);
     wait_vm_lgkm0<kAfter>();  // (lgkmcnt also covers the per-token constants)
@@ -642,14 +357,15 @@ __global__ __launch_bounds__(256, 2) void gemm64_kernel(MatArgs p, GemmGrid gg) 
     if (s < st1) {
         compute(As0, bw0);
         if (s + 1 < st1) {
-            wait_vm_lgkm0<NB>();  // stage s+1's copies (only its weight loads may remain)
+            wait_vm_lgkm0<0>();  // stage s+1's copies and weights (the last issued)
             __builtin_amdgcn_s_barrier();
             compute(As1, bw1);
         }
     }
+    }
     wait_vm_lgkm0<0>();  // no copy may still be writing LDS when the workgroup ends
 
-    if (S > 1) {
+    if (MI == 2 && S > 1) {
         int32_t* mine = gg.part + (size_t)linear * kSplitSlotInts;
 #pragma unroll
         for (int a = 0; a < NMAT; ++a)
@@ -688,7 +404,7 @@ __global__ __launch_bounds__(256, 2) void gemm64_kernel(MatArgs p, GemmGrid gg) 
         }
         if (tid == 0) __hip_atomic_store(&gg.ctr[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    static_assert(NMAT * MI * NJ * 16 * 256 == kSplitSlotInts, "a split slot holds one 64-token tile");
+    static_assert(MI != 2 || NMAT * MI * NJ * 16 * 256 == kSplitSlotInts, "a split slot holds one 64-token tile");
 
     // Epilogue from the accumulators: value v of block (i, j) is token row
     // 32i + 8(v/4) + 4h + v%4, output column (nb0 + j)*32 + l32.  Residual
@@ -745,11 +461,13 @@ __global__ __launch_bounds__(256, 2) void gemm64_kernel(MatArgs p, GemmGrid gg) 
 }
 
 // Tile height and split of a launch (measured on MI355X at both BitNet-2B FFN
-// shapes, M = 65 .. 16384): 64-token tiles beat 128-token tiles at every M
-// (three workgroups per CU instead of two hide more load latency).  Splitting
+// shapes, M = 65 .. 16384): 128-token tiles win once the grid has at least
+// kTile128MinTiles of them (M = 16384: 2.1 vs 1.8 POPS at K = 2560, 2.5 vs
+// 2.1 at K = 6912; M = 4096: 64-token tiles by up to 15 %).  Splitting
 // K pays only while few tiles exist and every range keeps a long K loop: with
 // at most kSplitMaxTiles tiles, about kSplitTarget workgroups in all, at least
 // kMinSplitKtiles K tiles per range, at most kMaxSplit ranges.
+constexpr int kTile128MinTiles = 1024;
 constexpr int kSplitMaxTilesPlan = 96;
 constexpr int kSplitTarget = 240;
 constexpr int kMinSplitKtiles = 6;
@@ -770,8 +488,10 @@ static GemmPlan plan_gemm(int m, int ntiles, int ktiles, int nmat, int device) {
     // (tuning and tests)
     const int force_tile = env_int("LOOM_AMD_GEMM_TILE", 0);
     const int force_split = env_int("LOOM_AMD_GEMM_SPLIT", 0);
-    if (force_tile == 128) return GemmPlan{4, 1, 2 * ktiles};  // 128-column stages
-    // 64-token tiles: one stage per 256-column K tile
+    if (force_tile == 128) return GemmPlan{4, 1, ktiles};
+    // large grids take 128-token tiles (never split)
+    if (force_tile != 64 && force_split == 0 && ceil_div(m, 128) * ngroups >= kTile128MinTiles)
+        return GemmPlan{4, 1, ktiles};
     const int tiles = ceil_div(m, 64) * ngroups;
     int want = 1;
     if (force_split > 0) {
@@ -791,7 +511,7 @@ static GemmPlan plan_gemm(int m, int ntiles, int ktiles, int nmat, int device) {
 }
 
 template <int NMAT, int EPI, int MI>
-static hipError_t launch_gemm32(const MatArgs& p, const GemmPlan& pl, int device, hipStream_t s) {
+static hipError_t launch_gemm_tile(const MatArgs& p, const GemmPlan& pl, int device, hipStream_t s) {
     GemmGrid gg;
     gg.mtiles = ceil_div(p.e.m, 32 * MI);
     gg.ngroups = ceil_div(p.ntiles, 16 / NMAT);
@@ -803,19 +523,15 @@ static hipError_t launch_gemm32(const MatArgs& p, const GemmPlan& pl, int device
     gg.ctr = ws.ctr;
     const int total = gg.mtiles * gg.ngroups * gg.ksplit;
     const int grid = ceil_div(total, kXcds) * kXcds;
-    if constexpr (MI == 2) {
-        hipLaunchKernelGGL((gemm64_kernel<NMAT, EPI>), dim3(grid), dim3(256), 0, s, p, gg);
-    } else {
-        hipLaunchKernelGGL((gemm32_kernel<NMAT, EPI, MI>), dim3(grid), dim3(256), 0, s, p, gg);
-    }
+    hipLaunchKernelGGL((gemm_lds_kernel<NMAT, EPI, MI>), dim3(grid), dim3(256), 0, s, p, gg);
     return hipGetLastError();
 }
 
 template <int NMAT, int EPI>
 static hipError_t launch_gemm_planned(const MatArgs& p, int device, hipStream_t s) {
     const GemmPlan pl = plan_gemm(p.e.m, p.ntiles, p.ktiles, NMAT, device);
-    if (pl.mi == 4) return launch_gemm32<NMAT, EPI, 4>(p, pl, device, s);
-    return launch_gemm32<NMAT, EPI, 2>(p, pl, device, s);
+    if (pl.mi == 4) return launch_gemm_tile<NMAT, EPI, 4>(p, pl, device, s);
+    return launch_gemm_tile<NMAT, EPI, 2>(p, pl, device, s);
 }
 
 static bool plain_dense(const EpiDev& e) {

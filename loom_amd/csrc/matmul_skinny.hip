@@ -944,7 +944,7 @@ const char* kernel_variant(int m) {
     if (m <= 16) return "skinny_m16";
     if (m <= 32) return "skinny_m32";
     if (m <= 64) return "skinny_m64";
-    return "gemm";  // gemm64_kernel (gemm32_kernel for 128-token tiles): 32x32x32 MFMA, split K
+    return "gemm";  // gemm_lds_kernel (64- or 128-token tiles): 32x32x32 MFMA, split K
 }
 
 static MatArgs make_args(const Matrix* w0, const Matrix* w1, int m, const Epilogue& epi) {
