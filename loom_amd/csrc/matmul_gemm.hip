@@ -407,8 +407,33 @@ __global__ __launch_bounds__(256, 2) void gemm_lds_kernel(MatArgs p, GemmGrid gg
     static_assert(MI != 2 || NMAT * MI * NJ * 16 * 256 == kSplitSlotInts, "a split slot holds one 64-token tile");
 
     // Epilogue from the accumulators: value v of block (i, j) is token row
-    // 32i + 8(v/4) + 4h + v%4, output column (nb0 + j)*32 + l32.  Residual
-    // loads of four rows are issued before their stores.
+    // 32i + 8(v/4) + 4h + v%4, output column (nb0 + j)*32 + l32.
+    if (EPI == 0 && m_wg + BM <= M && (nb0 + NJ) * 32 <= p.e.n) {
+        // plain Dense on a full tile: no row or column tests; each store
+        // takes a wave-uniform row pointer plus this lane's 32-bit offset,
+        // and the per-token constants come from LDS at immediate offsets
+        const int ldo = p.e.ldo;
+        const int loff = 4 * h * ldo + nb0 * 32 + l32;
+        const double* os_l = s_os0 + 4 * h;
+        const int* xs_l = s_xs + 4 * h;
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int t = 32 * i + 8 * g + u;  // this lane's row: t + 4h
+                    float* rowp = p.e.out + (size_t)(m_wg + t) * ldo;
+                    const double os0 = os_l[t];
+                    const int xs = xs_l[t];
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j)
+                        __builtin_nontemporal_store((float)((double)(acc[0][i][j][4 * g + u] - xs) * os0),
+                                                    &rowp[loff + 32 * j]);
+                }
+        return;
+    }
+    // (general case) Residual loads of four rows are issued before their stores.
     float bias0[NJ], bias1 = 0.0f;
     bool ncol[NJ];
     int ncl[NJ];
