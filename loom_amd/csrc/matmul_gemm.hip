@@ -433,6 +433,70 @@ __global__ __launch_bounds__(256, 2) void gemm_lds_kernel(MatArgs p, GemmGrid gg
                 }
         return;
     }
+    if (EPI != 0 && m_wg + BM <= M && (nb0 + NJ) * 32 <= p.e.n) {
+        // every other epilogue on a full tile: the same branch-free row walk
+        // (wave-uniform row offsets, this lane's column), residual loads of a
+        // row group issued before its stores
+        const int ldo = p.e.ldo, ldn = p.e.n;
+        const int col = nb0 * 32 + l32;
+        float bias0[NJ], bias1[NJ];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            bias0[j] = p.e.bias0 ? p.e.bias0[col + 32 * j] : 0.0f;
+            bias1[j] = NMAT == 2 && p.e.bias1 ? p.e.bias1[col + 32 * j] : 0.0f;
+        }
+        const bool has_res = EPI == 1 + EPI_DENSE && p.e.residual;
+        const double* os0_l = s_os0 + 4 * h;
+        const double* os1_l = NMAT == 2 ? s_os1 + 4 * h : s_os0;
+        const int* xs_l = s_xs + 4 * h;
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                float res[4][NJ];
+                if (has_res) {
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const float* rrow = p.e.residual + (size_t)(m_wg + 32 * i + 8 * g + u) * ldo;
+#pragma unroll
+                        for (int j = 0; j < NJ; ++j) res[u][j] = rrow[4 * h * ldo + col + 32 * j];
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int t = 32 * i + 8 * g + u;  // this lane's row: t + 4h
+                    const size_t row = (size_t)(m_wg + t);
+                    const double os0 = os0_l[t];
+                    const double os1 = NMAT == 2 ? os1_l[t] : 0.0;
+                    const int xs = xs_l[t];
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) {
+                        const int raw0 = acc[0][i][j][4 * g + u];
+                        const int raw1 = NMAT == 2 ? acc[NMAT - 1][i][j][4 * g + u] : raw0;
+                        const int a0 = raw0 - xs;
+                        const int c = 4 * h * ldn + col + 32 * j;  // (acc taps: row pitch N)
+                        const int co = 4 * h * ldo + col + 32 * j;
+                        if (p.e.acc0) p.e.acc0[row * ldn + c] = a0;
+                        if (EPI == 1 + EPI_ACC) continue;
+                        if (EPI == 1 + EPI_SWIGLU) {
+                            const int a1 = raw1 - xs;
+                            if (p.e.acc1) p.e.acc1[row * ldn + c] = a1;
+                            const double gg0 = (double)a0 * os0 + (p.e.bias0 ? (double)bias0[j] : 0.0);
+                            const double uu = (double)a1 * os1 + (p.e.bias1 ? (double)bias1[j] : 0.0);
+                            p.e.out[row * ldo + co] = (float)gate_product(gg0, uu, p.e.activation);
+                        } else {
+                            double d = (double)a0 * os0;
+                            if (p.e.bias0) d = d + (double)bias0[j];
+                            float v = (float)d;
+                            if (has_res) v = v + res[u][j];
+                            p.e.out[row * ldo + co] = v;
+                            if (p.e.post) p.e.post[row * ldo + co] = activate_f32(v, p.e.activation);
+                        }
+                    }
+                }
+            }
+        return;
+    }
     // (general case) Residual loads of four rows are issued before their stores.
     float bias0[NJ], bias1 = 0.0f;
     bool ncol[NJ];
