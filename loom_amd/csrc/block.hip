@@ -1682,19 +1682,7 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(const float* __restrict
             const float* vbb = (const float*)vbuf[(U) & 1];                                  \
             const double* pbb = pbuf[(U) & 1];                                               \
             const int n = min(C, L - c * C);                                                 \
-            if (tid < DG) {                                                                  \
-                int j = 0;                                                                   \
-                for (; j + 16 <= n; j += 16) {                                               \
-                    double a[16];                                                            \
-                    float v[16];                                                             \
-                    _Pragma("unroll") for (int t = 0; t < 16; ++t) {                        \
-                        a[t] = pbb[j + t];                                                   \
-                        v[t] = vbb[(j + t) * DG + tid];                                      \
-                    }                                                                        \
-                    _Pragma("unroll") for (int t = 0; t < 16; ++t) sum += a[t] * (double)v[t]; \
-                }                                                                            \
-                for (; j < n; ++j) sum += pbb[j] * (double)vbb[j * DG + tid];                \
-            }                                                                                \
+            if (tid < DG) sum = ordered_dot(pbb, vbb + tid, DG, n, sum);                   \
             if (tid == es_lane) es = ordered_sum(pbb, n, es);                                \
         }                                                                                    \
     }

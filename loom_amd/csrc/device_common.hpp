@@ -175,7 +175,8 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
 }
 
 // Sum of n fp64 terms in index order (one lane): terms are read from LDS
-// sixteen at a time ahead of the dependent additions.
+// sixteen at a time ahead of the dependent additions (each addition waits
+// only for its own read: LDS reads return in order).
 __device__ __forceinline__ double ordered_sum(const double* t, int n, double s) {
     int i = 0;
     for (; i + 16 <= n; i += 16) {
@@ -189,21 +190,46 @@ __device__ __forceinline__ double ordered_sum(const double* t, int n, double s) 
     return s;
 }
 
-// sum over k in index order of p[k] * (double)v[k] (LDS operands), same read-ahead.
-__device__ __forceinline__ double ordered_dot(const double* p, const float* v, int n, double s) {
-    int i = 0;
-    for (; i + 16 <= n; i += 16) {
-        double a[16];
-        float b[16];
+// sum over k in index order of p[k] * (double)v[k * vs] (LDS operands; a
+// product, then a sum, each rounded).  Blocks of 16 terms, double-buffered:
+// the reads of block b + 1 are issued before the additions of block b (the
+// block read after the last full one is clamped to an existing block rather
+// than guarded by a branch).
+__device__ __forceinline__ double ordered_dot(const double* p, const float* v, int vs, int n, double s) {
+    constexpr int B = 16;
+    const int nb = n / B;
+    if (nb > 0) {
+        double a[B], c[B];
+        float b[B], d[B];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            a[j] = p[i + j];
-            b[j] = v[i + j];
+        for (int j = 0; j < B; ++j) {
+            a[j] = p[j];
+            b[j] = v[j * vs];
         }
+        int blk = 0;
+        for (; blk + 2 <= nb; blk += 2) {
+            const int o1 = (blk + 1) * B, o2 = min(blk + 2, nb - 1) * B;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) s += a[j] * (double)b[j];
+            for (int j = 0; j < B; ++j) {
+                c[j] = p[o1 + j];
+                d[j] = v[(o1 + j) * vs];
+            }
+#pragma unroll
+            for (int j = 0; j < B; ++j) s += a[j] * (double)b[j];
+#pragma unroll
+            for (int j = 0; j < B; ++j) {
+                a[j] = p[o2 + j];
+                b[j] = v[(o2 + j) * vs];
+            }
+#pragma unroll
+            for (int j = 0; j < B; ++j) s += c[j] * (double)d[j];
+        }
+        if (blk < nb) {
+#pragma unroll
+            for (int j = 0; j < B; ++j) s += a[j] * (double)b[j];
+        }
     }
-    for (; i < n; ++i) s += p[i] * (double)v[i];
+    for (int i = nb * B; i < n; ++i) s += p[i] * (double)v[i * vs];
     return s;
 }
 

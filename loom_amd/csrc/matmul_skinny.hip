@@ -934,7 +934,9 @@ static hipError_t launch_small_m(const MatArgs& p, int device, hipStream_t s) {
     hipError_t e = hipSuccess;
     if (NMAT == 1 && launch_small_split<MSUB>(p, device, s, &e)) return e;
     const int nt = skinny_nt(p.ntiles, p.ktiles);
-    if (nt == 4 && NMAT == 1) return launch_skinny_nt<NMAT, MSUB, 4>(p, s);
+    if constexpr (NMAT == 1) {
+        if (nt == 4) return launch_skinny_nt<NMAT, MSUB, 4>(p, s);
+    }
     if (nt >= 2) return launch_skinny_nt<NMAT, MSUB, 2>(p, s);
     return launch_skinny<NMAT, MSUB, false>(p, s);
 }
