@@ -39,6 +39,88 @@ __device__ double lds_sum(const double* terms, int n, double* scratch256) {
 }
 
 // ------------------------------------------------------------------------
+// Strict sums of squares of many rows (prefill): one lane per row.  Lane r
+// of a wave adds row r's squares in element order -- the reference's
+// sequential chain -- so a wave runs 64 chains at the latency of one, where
+// the per-row kernels below run one chain per workgroup.  Each lane reads its
+// row in 16-byte loads, eight loads a block, the next block in flight while
+// the current one is added (the block read after the last full one is
+// clamped to an existing block instead of guarded by a branch).  For fp32
+// rows the fp64 squares are exact; for fp64 rows each square is rounded
+// before its addition, as the reference computes it.
+// ------------------------------------------------------------------------
+constexpr int kRowChainMinRows = 256;  // below this the per-row kernels keep their own chain
+
+template <typename T>
+__global__ __launch_bounds__(64) void row_sumsq_kernel(const T* __restrict__ x, long ldx, int n, int m,
+                                                       double* __restrict__ totals) {
+    constexpr int V = 16 / sizeof(T);  // elements per load
+    constexpr int G = 8;               // loads per block
+    constexpr int E = V * G;           // elements per block
+    const int row = blockIdx.x * 64 + threadIdx.x;
+    const T* xr = x + (size_t)min(row, m - 1) * ldx;  // lanes past m repeat the last row, store nothing
+    double s = 0.0;
+    const int nb = n / E;
+    auto add = [&](const uint4 (&blk)[G]) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            if constexpr (sizeof(T) == 4) {
+                const float4 f = __builtin_bit_cast(float4, blk[g]);
+                const double a = f.x, b = f.y, c = f.z, d = f.w;
+                s = s + a * a;
+                s = s + b * b;
+                s = s + c * c;
+                s = s + d * d;
+            } else {
+                const double2 f = __builtin_bit_cast(double2, blk[g]);
+                s = s + f.x * f.x;
+                s = s + f.y * f.y;
+            }
+        }
+    };
+    if (nb > 0) {
+        const uint4* xv = (const uint4*)xr;
+        uint4 a[G], b[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) a[g] = xv[g];
+        int blk = 0;
+        for (; blk + 2 <= nb; blk += 2) {  // a holds block blk
+            const uint4* pb = xv + (size_t)(blk + 1) * G;
+            const uint4* pa = xv + (size_t)min(blk + 2, nb - 1) * G;
+#pragma unroll
+            for (int g = 0; g < G; ++g) b[g] = pb[g];
+            add(a);
+#pragma unroll
+            for (int g = 0; g < G; ++g) a[g] = pa[g];
+            add(b);
+        }
+        if (blk < nb) add(a);
+    }
+    for (int i = nb * E; i < n; ++i) {
+        const double f = (double)xr[i];
+        s = s + f * f;
+    }
+    if (row < m) totals[row] = s;
+}
+
+// Strict row totals for m rows when the row-chain kernel applies (many rows,
+// 16-byte aligned rows); returns false when the caller keeps its own chain.
+template <typename T>
+static bool launch_row_sumsq(const T* x, long ldx, int m, int n, double* totals, hipStream_t s,
+                             hipError_t* e) {
+    if (!totals || m < kRowChainMinRows) return false;
+    if (((uintptr_t)x & 15) != 0 || ((size_t)ldx * sizeof(T)) % 16 != 0) return false;
+    hipLaunchKernelGGL((row_sumsq_kernel<T>), dim3(ceil_div(m, 64)), dim3(64), 0, s, x, ldx, n, m, totals);
+    *e = hipGetLastError();
+    return true;
+}
+
+bool launch_row_sumsq_f32(const float* x, long ldx, int m, int n, double* totals, hipStream_t s,
+                          hipError_t* e) {
+    return launch_row_sumsq<float>(x, ldx, m, n, totals, s, e);
+}
+
+// ------------------------------------------------------------------------
 // RMSNorm layer (poly/norm.go:102-138) fused with the following projection's
 // int8 quantization (poly/bitnet_cpu.go:45-106): one workgroup per row.
 // y = fp32((x / rms) * g), rms = sqrt(sum(x^2)/n + eps).  xq may be null
@@ -51,7 +133,8 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float* __restr
                                                             double eps, float* __restrict__ y,
                                                             int8_t* __restrict__ xq, int ldq,
                                                             float* __restrict__ amax_out,
-                                                            int32_t* __restrict__ xsum_out) {
+                                                            int32_t* __restrict__ xsum_out,
+                                                            const double* __restrict__ totals) {
     extern __shared__ double sq[];  // STRICT: n squares; fast: 256 partials
     __shared__ double red[256];
     __shared__ float shf[4];
@@ -65,7 +148,9 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float* __restr
         v[j] = i < n ? xr[i] : 0.0f;
     }
     double total;
-    if (STRICT) {
+    if (STRICT && totals) {
+        total = totals[row];  // the row-chain kernel's ordered sum
+    } else if (STRICT) {
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
             const int i = threadIdx.x + j * 256;
@@ -129,31 +214,38 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float* __restr
 template <int STRICT>
 static hipError_t launch_rmsnorm_t(const float* x, long ldx, int m, int n, const float* gain,
                                    double eps, float* y, int8_t* xq, int ldq, float* amax,
-                                   int32_t* xsum, hipStream_t s) {
-    const size_t shm = STRICT ? (size_t)n * sizeof(double) : 0;
+                                   int32_t* xsum, const double* totals, hipStream_t s) {
+    const size_t shm = STRICT && !totals ? (size_t)n * sizeof(double) : 0;
     const dim3 g(m), b(256);
+#define LAMD_RMS(VPT)                                                                          \
+    hipLaunchKernelGGL((rmsnorm_quant_kernel<STRICT, VPT>), g, b, shm, s, x, ldx, n, gain, eps, y, xq, \
+                       ldq, amax, xsum, totals)
     if (n <= 256 * 4) {
-        hipLaunchKernelGGL((rmsnorm_quant_kernel<STRICT, 4>), g, b, shm, s, x, ldx, n, gain, eps, y, xq, ldq, amax, xsum);
+        LAMD_RMS(4);
     } else if (n <= 256 * 8) {
-        hipLaunchKernelGGL((rmsnorm_quant_kernel<STRICT, 8>), g, b, shm, s, x, ldx, n, gain, eps, y, xq, ldq, amax, xsum);
+        LAMD_RMS(8);
     } else if (n <= 256 * 16) {
-        hipLaunchKernelGGL((rmsnorm_quant_kernel<STRICT, 16>), g, b, shm, s, x, ldx, n, gain, eps, y, xq, ldq, amax, xsum);
+        LAMD_RMS(16);
     } else if (n <= 256 * 32) {
-        hipLaunchKernelGGL((rmsnorm_quant_kernel<STRICT, 32>), g, b, shm, s, x, ldx, n, gain, eps, y, xq, ldq, amax, xsum);
+        LAMD_RMS(32);
     } else {
         return hipErrorInvalidValue;
     }
+#undef LAMD_RMS
     return hipGetLastError();
 }
 
 hipError_t launch_rmsnorm_quant(const float* x, long ldx, int m, int n, const float* gain,
                                 double eps, int strict, float* y, int8_t* xq, int ldq, float* amax,
-                                int32_t* xsum, hipStream_t s) {
+                                int32_t* xsum, hipStream_t s, double* totals) {
     if (m <= 0) return hipSuccess;
     if (eps <= 0.0) eps = 1e-6;  // RMSNormForwardPolymorphic default
     if (n > kMaxNormCols || (strict && n > kMaxStrictNormCols)) return hipErrorInvalidValue;
-    return strict ? launch_rmsnorm_t<1>(x, ldx, m, n, gain, eps, y, xq, ldq, amax, xsum, s)
-                  : launch_rmsnorm_t<0>(x, ldx, m, n, gain, eps, y, xq, ldq, amax, xsum, s);
+    if (!strict) return launch_rmsnorm_t<0>(x, ldx, m, n, gain, eps, y, xq, ldq, amax, xsum, nullptr, s);
+    hipError_t e = hipSuccess;
+    const bool rows = launch_row_sumsq<float>(x, ldx, m, n, totals, s, &e);
+    if (e != hipSuccess) return e;
+    return launch_rmsnorm_t<1>(x, ldx, m, n, gain, eps, y, xq, ldq, amax, xsum, rows ? totals : nullptr, s);
 }
 
 // ------------------------------------------------------------------------
@@ -1898,7 +1990,8 @@ __global__ __launch_bounds__(256) void norm_quant_f64_kernel(double* __restrict_
                                                              double eps, float* __restrict__ pre,
                                                              int8_t* __restrict__ xq, int ldq,
                                                              float* __restrict__ amax_out,
-                                                             int32_t* __restrict__ xsum_out, int keep) {
+                                                             int32_t* __restrict__ xsum_out, int keep,
+                                                             const double* __restrict__ totals) {
     extern __shared__ double sq[];
     __shared__ double red[256];
     __shared__ float shf[4];
@@ -1912,7 +2005,9 @@ __global__ __launch_bounds__(256) void norm_quant_f64_kernel(double* __restrict_
         v[j] = i < n ? ar[i] : 0.0;
     }
     double total;
-    if (STRICT) {
+    if (STRICT && totals) {
+        total = totals[row];  // the row-chain kernel's ordered sum
+    } else if (STRICT) {
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
             const int i = threadIdx.x + j * 256;
@@ -1969,32 +2064,39 @@ __global__ __launch_bounds__(256) void norm_quant_f64_kernel(double* __restrict_
 template <int STRICT>
 static hipError_t launch_norm_f64_t(double* a, int m, int n, const float* w, double eps, float* pre,
                                     int8_t* xq, int ldq, float* amax, int32_t* xsum, int keep,
-                                    hipStream_t s) {
-    const size_t shm = STRICT ? (size_t)n * sizeof(double) : 0;
+                                    const double* totals, hipStream_t s) {
+    const size_t shm = STRICT && !totals ? (size_t)n * sizeof(double) : 0;
     const dim3 g(m), b(256);
+#define LAMD_NF64(VPT)                                                                          \
+    hipLaunchKernelGGL((norm_quant_f64_kernel<STRICT, VPT>), g, b, shm, s, a, n, w, eps, pre, xq, ldq, \
+                       amax, xsum, keep, totals)
     if (n <= 256 * 4) {
-        hipLaunchKernelGGL((norm_quant_f64_kernel<STRICT, 4>), g, b, shm, s, a, n, w, eps, pre, xq, ldq, amax, xsum, keep);
+        LAMD_NF64(4);
     } else if (n <= 256 * 8) {
-        hipLaunchKernelGGL((norm_quant_f64_kernel<STRICT, 8>), g, b, shm, s, a, n, w, eps, pre, xq, ldq, amax, xsum, keep);
+        LAMD_NF64(8);
     } else if (n <= 256 * 16) {
-        hipLaunchKernelGGL((norm_quant_f64_kernel<STRICT, 16>), g, b, shm, s, a, n, w, eps, pre, xq, ldq, amax, xsum, keep);
+        LAMD_NF64(16);
     } else if (n <= 256 * 32) {
-        hipLaunchKernelGGL((norm_quant_f64_kernel<STRICT, 32>), g, b, shm, s, a, n, w, eps, pre, xq, ldq, amax, xsum, keep);
+        LAMD_NF64(32);
     } else {
         return hipErrorInvalidValue;
     }
+#undef LAMD_NF64
     return hipGetLastError();
 }
 
 hipError_t launch_norm_quant_f64(double* a, int m, int n, const float* w, double eps, int strict,
                                  float* pre, int8_t* xq, int ldq, float* amax, int32_t* xsum,
-                                 hipStream_t s, bool keep_rows) {
+                                 hipStream_t s, bool keep_rows, double* totals) {
     if (m <= 0) return hipSuccess;
     if (eps <= 0.0) eps = 1e-5;  // bitNetRMSNormFloat64Weighted default
     if (n > kMaxNormCols || (strict && n > kMaxStrictNormCols)) return hipErrorInvalidValue;
     const int keep = keep_rows ? 1 : 0;
-    return strict ? launch_norm_f64_t<1>(a, m, n, w, eps, pre, xq, ldq, amax, xsum, keep, s)
-                  : launch_norm_f64_t<0>(a, m, n, w, eps, pre, xq, ldq, amax, xsum, keep, s);
+    if (!strict) return launch_norm_f64_t<0>(a, m, n, w, eps, pre, xq, ldq, amax, xsum, keep, nullptr, s);
+    hipError_t e = hipSuccess;
+    const bool rows = launch_row_sumsq<double>(a, n, m, n, totals, s, &e);
+    if (e != hipSuccess) return e;
+    return launch_norm_f64_t<1>(a, m, n, w, eps, pre, xq, ldq, amax, xsum, keep, rows ? totals : nullptr, s);
 }
 
 // ------------------------------------------------------------------------

@@ -15,10 +15,12 @@ constexpr int kMaxAttnSpan = 7424;         // positions: (60 KiB / 8) - 256
 // RMSNormForwardPolymorphic (poly/norm.go:102-138) on m rows of n, optionally
 // followed by the int8 quantization of the normalized row.  y and xq may each
 // be null.  eps <= 0 selects the reference default 1e-6.
-// x rows are ldx floats apart; y rows are dense (n).
+// x rows are ldx floats apart; y rows are dense (n).  totals (optional, m
+// doubles of workspace): in strict mode with many rows, the rows' ordered sums
+// of squares are formed one lane per row first (row_sumsq_kernel).
 hipError_t launch_rmsnorm_quant(const float* x, long ldx, int m, int n, const float* gain,
                                 double eps, int strict, float* y, int8_t* xq, int ldq, float* amax,
-                                int32_t* xsum, hipStream_t s);
+                                int32_t* xsum, hipStream_t s, double* totals = nullptr);
 
 // Rescale + bias + RoPE of the stacked Q/K/V accumulators (batch*seq rows of
 // q_dim + 2*kv_dim int32): Q rows to q (fp64, rows x q_dim), K/V rows into
@@ -56,10 +58,11 @@ hipError_t launch_attention(const double* q, const float* cache_k, const float* 
 
 // MHA inner norm on fp64 rows in place (data *= scale*w; skipped when
 // keep_rows is false) + fp64 requantization.  pre (optional) receives fp32 of
-// the normalized rows.  eps <= 0 selects 1e-5.
+// the normalized rows.  eps <= 0 selects 1e-5.  totals: as for
+// launch_rmsnorm_quant.
 hipError_t launch_norm_quant_f64(double* a, int m, int n, const float* w, double eps, int strict,
                                  float* pre, int8_t* xq, int ldq, float* amax, int32_t* xsum,
-                                 hipStream_t s, bool keep_rows = true);
+                                 hipStream_t s, bool keep_rows = true, double* totals = nullptr);
 
 // Embedding rows of batch x seq tokens: row (b, s) takes the id at
 // tokens[b*cap + *pos0 + s] (pos0 null = 0); ids outside the table give zero

@@ -56,6 +56,7 @@ struct Workspace {
     int8_t* hq = nullptr;    // rows x pad(inter)
     float* amax3 = nullptr;
     int32_t* xsum3 = nullptr;
+    double* totals = nullptr;  // rows x fp64: strict ordered sums of squares (many rows)
 };
 
 static size_t workspace_layout(const BlockDev& B, int rows, Workspace* W, char* base) {
@@ -78,6 +79,7 @@ static size_t workspace_layout(const BlockDev& B, int rows, Workspace* W, char* 
     const size_t o_hq = L.take(r * pad_cols(B.inter));
     const size_t o_am3 = L.take(r * 4);
     const size_t o_xs3 = L.take(r * 4);
+    const size_t o_tot = L.take(r * 8);
     if (W && base) {
         W->base = base;
         W->bytes = L.off;
@@ -96,6 +98,7 @@ static size_t workspace_layout(const BlockDev& B, int rows, Workspace* W, char* 
         W->hq = (int8_t*)(base + o_hq);
         W->amax3 = (float*)(base + o_am3);
         W->xsum3 = (int32_t*)(base + o_xs3);
+        W->totals = (double*)(base + o_tot);
     }
     return L.off;
 }
@@ -334,7 +337,7 @@ static int block_forward_dev(const BlockDev& B, const Workspace& W, float* x, in
             if (e != hipSuccess) return fail_hip("block rmsnorm1 + qkv projection", e);
         } else {
             e = launch_rmsnorm_quant(x, B.hidden, R, B.hidden, B.norm1, rms_eps, B.strict, T.y1,
-                                     W.xq, ldh, W.amax, W.xsum, s);
+                                     W.xq, ldh, W.amax, W.xsum, s, W.totals);
             if (e != hipSuccess) return fail_hip("block rmsnorm1", e);
             TAP(tap_rows(T.xq1, W.xq, ldh, B.hidden, R, s));
             QuantAct a{W.xq, ldh, W.amax, W.xsum};
@@ -378,7 +381,8 @@ static int block_forward_dev(const BlockDev& B, const Workspace& W, float* x, in
             // (only the int8 rows feed the O projection: the normalized fp64
             // rows are written back only for the tap)
             e = launch_norm_quant_f64(W.attn, R, B.q_dim, B.attn_norm, attn_eps, B.strict, nullptr,
-                                      W.aq, ldqd, W.amax2, W.xsum2, s, T.attn_norm != nullptr);
+                                      W.aq, ldqd, W.amax2, W.xsum2, s, T.attn_norm != nullptr,
+                                      W.totals);
             if (e != hipSuccess) return fail_hip("block attention inner norm", e);
             TAP(tap_copy(T.attn_norm, W.attn, (size_t)R * B.q_dim * 8, s));
             TAP(tap_rows(T.aq, W.aq, ldqd, B.q_dim, R, s));
@@ -406,7 +410,7 @@ static int block_forward_dev(const BlockDev& B, const Workspace& W, float* x, in
             if (e != hipSuccess) return fail_hip("block rmsnorm2 + gate/up", e);
         } else {
             e = launch_rmsnorm_quant(x, B.hidden, R, B.hidden, B.norm2, rms_eps, B.strict, T.y2,
-                                     W.xq, ldh, W.amax, W.xsum, s);
+                                     W.xq, ldh, W.amax, W.xsum, s, W.totals);
             if (e != hipSuccess) return fail_hip("block rmsnorm2", e);
             TAP(tap_rows(T.xq2, W.xq, ldh, B.hidden, R, s));
             TAP(tap_copy(T.amax2, W.amax, (size_t)R * 4, s));
@@ -434,7 +438,7 @@ static int block_forward_dev(const BlockDev& B, const Workspace& W, float* x, in
             // (only the int8 rows feed the down projection; the normalized
             // rows are written back only for the tap)
             e = launch_norm_quant(W.h, B.inter, R, B.inter, B.ffn_norm, ffn_eps, B.strict, W.hq, ldi,
-                                  W.amax3, W.xsum3, s, T.hn != nullptr);
+                                  W.amax3, W.xsum3, s, T.hn != nullptr, W.totals);
             if (e != hipSuccess) return fail_hip("block ffn inner norm", e);
             TAP(tap_copy(T.hn, W.h, (size_t)R * B.inter * 4, s));
             TAP(tap_rows(T.hq, W.hq, ldi, B.inter, R, s));

@@ -133,10 +133,16 @@ hipError_t launch_matmul_norm(const Matrix* w0, const Matrix* w1, const float* x
 // Inner RMSNorm + requantization of SwiGLU rows (poly/bitnet_cpu.go:893-913 then
 // poly/bitnet_cpu.go:97-106).  In place on h (M x n fp32, row stride ldh) unless
 // keep_rows is false (then only the int8 rows, amax and sum(xq) are written).
+// totals (optional, m doubles of workspace): in strict mode with many rows the
+// rows' ordered sums of squares are formed one lane per row first.
 hipError_t launch_norm_quant(float* h, int ldh, int m, int n, const float* weight, double eps,
                              int strict, int8_t* hq, int ldq, float* amax, int32_t* xsum,
-                             hipStream_t s,
-                             bool keep_rows = true);
+                             hipStream_t s, bool keep_rows = true, double* totals = nullptr);
+// Strict ordered sums of squares of m fp32 rows (one lane per row, in element
+// order) into totals when m is large enough and the rows are 16-byte aligned;
+// returns false (nothing launched) otherwise.
+bool launch_row_sumsq_f32(const float* x, long ldx, int m, int n, double* totals, hipStream_t s,
+                          hipError_t* e);
 
 // Per-device scratch arena for the device-resident entry points.
 void* scratch(int device, size_t bytes, std::string* err);

@@ -194,7 +194,8 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(float* __restrict__ h, 
                                                          const float* __restrict__ weight,
                                                          double eps, int8_t* __restrict__ hq,
                                                          int ldq, float* __restrict__ amax_out,
-                                                         int32_t* __restrict__ xsum_out, int keep) {
+                                                         int32_t* __restrict__ xsum_out, int keep,
+                                                         const double* __restrict__ totals) {
     extern __shared__ double dsh[];  // STRICT: n squares; fast: 256 partial sums
     __shared__ float shf[4];
     __shared__ int shi[4];
@@ -207,7 +208,10 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(float* __restrict__ h, 
         const int i = threadIdx.x + j * 256;
         v[j] = i < n ? hr[i] : 0.0f;
     }
-    if (STRICT) {
+    if (STRICT && totals) {
+        if (threadIdx.x == 0) total = totals[row];  // the row-chain kernel's ordered sum
+        __syncthreads();
+    } else if (STRICT) {
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
             const int i = threadIdx.x + j * 256;
@@ -279,33 +283,37 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(float* __restrict__ h, 
 template <int STRICT>
 static hipError_t launch_norm_t(float* h, int ldh, int m, int n, const float* weight, double eps,
                                 int8_t* hq, int ldq, float* amax, int32_t* xsum, int keep,
-                                hipStream_t s) {
-    const size_t shm = STRICT ? (size_t)n * sizeof(double) : 256 * sizeof(double);
+                                const double* totals, hipStream_t s) {
+    const size_t shm = STRICT && !totals ? (size_t)n * sizeof(double) : 256 * sizeof(double);
     const dim3 g(m), b(256);
+#define LAMD_NQ(VPT)                                                                            \
+    hipLaunchKernelGGL((norm_quant_kernel<STRICT, VPT>), g, b, shm, s, h, ldh, n, weight, eps, hq, ldq, \
+                       amax, xsum, keep, totals)
     if (n <= 256 * 8) {
-        hipLaunchKernelGGL((norm_quant_kernel<STRICT, 8>), g, b, shm, s, h, ldh, n, weight, eps, hq,
-                           ldq, amax, xsum, keep);
+        LAMD_NQ(8);
     } else if (n <= 256 * 16) {
-        hipLaunchKernelGGL((norm_quant_kernel<STRICT, 16>), g, b, shm, s, h, ldh, n, weight, eps,
-                           hq, ldq, amax, xsum, keep);
+        LAMD_NQ(16);
     } else if (n <= 256 * 32) {
-        hipLaunchKernelGGL((norm_quant_kernel<STRICT, 32>), g, b, shm, s, h, ldh, n, weight, eps,
-                           hq, ldq, amax, xsum, keep);
+        LAMD_NQ(32);
     } else {
         return hipErrorInvalidValue;
     }
+#undef LAMD_NQ
     return hipGetLastError();
 }
 
 hipError_t launch_norm_quant(float* h, int ldh, int m, int n, const float* weight, double eps,
                              int strict, int8_t* hq, int ldq, float* amax, int32_t* xsum,
-                             hipStream_t s, bool keep_rows) {
+                             hipStream_t s, bool keep_rows, double* totals) {
     if (m <= 0) return hipSuccess;
     if (eps <= 0.0) eps = 1e-5;
     if (n > kMaxNormCols) return hipErrorInvalidValue;
     const int keep = keep_rows ? 1 : 0;
-    return strict ? launch_norm_t<1>(h, ldh, m, n, weight, eps, hq, ldq, amax, xsum, keep, s)
-                  : launch_norm_t<0>(h, ldh, m, n, weight, eps, hq, ldq, amax, xsum, keep, s);
+    if (!strict) return launch_norm_t<0>(h, ldh, m, n, weight, eps, hq, ldq, amax, xsum, keep, nullptr, s);
+    hipError_t e = hipSuccess;
+    const bool rows = launch_row_sumsq_f32(h, ldh, m, n, totals, s, &e);
+    if (e != hipSuccess) return e;
+    return launch_norm_t<1>(h, ldh, m, n, weight, eps, hq, ldq, amax, xsum, keep, rows ? totals : nullptr, s);
 }
 
 }  // namespace lamd
