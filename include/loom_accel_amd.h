@@ -117,6 +117,18 @@ int loom_amd_norm_quant_rows(float* h, int m, int n, const float* weight, double
                              int norm_mode, int8_t* hq, int ldq, float* amax, int32_t* xsum,
                              void* stream);
 
+/* The reference's sequential fp64 sum, out[i] = s0 + t[i][0] + t[i][1] + ...
+ * in index order with one rounding per addition, for m rows of n terms
+ * (n <= 8064; device pointers), one workgroup of `threads` (64, 256 or 512:
+ * the widths the strict norm kernels use) per row.  Every strict-mode sum of
+ * squares is this chain (e.g. the sum of squares of
+ * bitNetRMSNormTensorRowWeighted, poly/bitnet_cpu.go:901-905); the entry
+ * point has no counterpart of its own in the reference: it exposes the
+ * library's exact parallel forms of the chain so that callers and tests can
+ * check them against a plain sequential sum. */
+int loom_amd_ordered_sum_rows(const double* terms, int m, int n, double s0, double* out,
+                              int threads, void* stream);
+
 /* ---- layers ---------------------------------------------------------- */
 
 typedef struct loom_amd_dense_taps {

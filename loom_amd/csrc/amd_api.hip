@@ -403,6 +403,17 @@ int loom_amd_norm_quant_rows(float* h, int m, int n, const float* weight, double
     return e == hipSuccess ? 0 : fail_hip("norm_quant_rows", e);
 }
 
+int loom_amd_ordered_sum_rows(const double* terms, int m, int n, double s0, double* out,
+                              int threads, void* stream) {
+    if (m < 0 || n <= 0) return fail("bad shape");
+    if (m == 0) return 0;
+    if (!terms || !out) return fail("null buffer");
+    if (n > kMaxStrictNormCols) return fail("ordered sums are limited to 8064 terms per row");
+    if (threads != 64 && threads != 256 && threads != 512) return fail("threads must be 64, 256 or 512");
+    hipError_t e = launch_ordered_sum_rows(terms, m, n, s0, out, threads, (hipStream_t)stream);
+    return e == hipSuccess ? 0 : fail_hip("ordered_sum_rows", e);
+}
+
 int loom_amd_dense_forward(const loom_amd_matrix* w, const float* x, int m, int activation,
                            float* pre, float* post, const float* residual,
                            const loom_amd_dense_taps* taps, void* stream) {

@@ -17,13 +17,12 @@ namespace lamd {
 // ------------------------------------------------------------------------
 
 template <int STRICT>
-__device__ double lds_sum(const double* terms, int n, double* scratch256) {
+__device__ __forceinline__ double lds_sum(double* terms, int n, double* scratch256) {
     __shared__ double result;
     __syncthreads();
     if (STRICT) {
-        if (threadIdx.x == 0) result = ordered_sum(terms, n, 0.0);
-        __syncthreads();
-        return result;
+        __shared__ OrderedSumLds<4> osum;
+        return ordered_sum_block<4>(terms, n, 0.0, osum);
     }
     double s = 0.0;
     for (int i = threadIdx.x; i < n; i += blockDim.x) s += terms[i];
@@ -215,7 +214,7 @@ template <int STRICT>
 static hipError_t launch_rmsnorm_t(const float* x, long ldx, int m, int n, const float* gain,
                                    double eps, float* y, int8_t* xq, int ldq, float* amax,
                                    int32_t* xsum, const double* totals, hipStream_t s) {
-    const size_t shm = STRICT && !totals ? (size_t)n * sizeof(double) : 0;
+    const size_t shm = STRICT && !totals ? (size_t)ordered_sum_slots(n, 4) * sizeof(double) : 0;
     const dim3 g(m), b(256);
 #define LAMD_RMS(VPT)                                                                          \
     hipLaunchKernelGGL((rmsnorm_quant_kernel<STRICT, VPT>), g, b, shm, s, x, ldx, n, gain, eps, y, xq, \
@@ -2065,7 +2064,7 @@ template <int STRICT>
 static hipError_t launch_norm_f64_t(double* a, int m, int n, const float* w, double eps, float* pre,
                                     int8_t* xq, int ldq, float* amax, int32_t* xsum, int keep,
                                     const double* totals, hipStream_t s) {
-    const size_t shm = STRICT && !totals ? (size_t)n * sizeof(double) : 0;
+    const size_t shm = STRICT && !totals ? (size_t)ordered_sum_slots(n, 4) * sizeof(double) : 0;
     const dim3 g(m), b(256);
 #define LAMD_NF64(VPT)                                                                          \
     hipLaunchKernelGGL((norm_quant_f64_kernel<STRICT, VPT>), g, b, shm, s, a, n, w, eps, pre, xq, ldq, \

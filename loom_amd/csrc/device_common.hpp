@@ -233,6 +233,431 @@ __device__ __forceinline__ double ordered_dot(const double* p, const float* v, i
     return s;
 }
 
+// Inclusive prefix sum over the 64 lanes in fp64 (DPP lane moves): row_shr 1,
+// 2, 4, 8 scan each 16-lane row, then row_bcast 15 adds row 0's total to row 1
+// and row 2's to row 3 (row mask 0xa), and row_bcast 31 adds the first two
+// rows' total to rows 2 and 3 (row mask 0xc).  Exact when every partial sum is
+// (integers below 2^53).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ double dpp_rows_d(double v) {
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)b, CTRL, ROWS, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), CTRL, ROWS, 0xf, false);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
+__device__ __forceinline__ double wave_scan_f64_dpp(double v) {
+    v = v + dpp_rows_d<kDppShr1, 0xf>(v);
+    v = v + dpp_rows_d<kDppShr2, 0xf>(v);
+    v = v + dpp_rows_d<kDppShr4, 0xf>(v);
+    v = v + dpp_rows_d<kDppShr8, 0xf>(v);
+    v = v + dpp_rows_d<kDppBcast15, 0xa>(v);
+    v = v + dpp_rows_d<kDppBcast31, 0xc>(v);
+    return v;
+}
+
+// a wave-uniform 64-bit value (e.g. read from LDS) into scalar registers
+__device__ __forceinline__ unsigned long long uniform_u64(unsigned long long v) {
+    return ((unsigned long long)(unsigned)__builtin_amdgcn_readfirstlane((int)(v >> 32)) << 32) |
+           (unsigned)__builtin_amdgcn_readfirstlane((int)v);
+}
+
+__device__ __forceinline__ double readlane_d(double v, int lane) {
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int)b, lane);
+    const int hi = __builtin_amdgcn_readlane((int)(b >> 32), lane);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
+
+// The one-lane chain `for (i = 0; i < n; ++i) s = s + t[i];` (t in LDS),
+// bit for bit, run by all 64 lanes of a wavefront (uniform control flow; every
+// lane returns the result).
+//
+// While the running sum s stays in one binade [2^E, 2^(E+1)), every rounded
+// sum is a multiple of q = 2^(E-52), and for a term 0 <= t < 2^E the rounded
+// s + t is s + q * r with r the integer nearest t/q -- unless t/q is a
+// half-integer k + 1/2, where round-half-even picks whichever of s + q*k and
+// s + q*(k+1) has an even s/q.  A wave therefore takes 64 x C terms per step:
+// lane l rounds its C consecutive terms to integers in units of q (scaling by
+// a power of two is exact); a tie depends only on the parity of the running
+// sum before it, and a tie leaves that sum even, so each lane's block is
+// summed for an incoming parity of 0 and the parity each lane actually sees is
+// read off three wave ballots (the last lane below with a tie, and the
+// parities of the blocks since).  An inclusive prefix sum of the block sums
+// (integers below 2^53: exact in fp64) then gives the running sum after each
+// block.  The first block whose running sum leaves the binade, or that holds a
+// negative, non-finite or too large term, ends the accepted prefix; its terms
+// are added one by one with fp64 additions, and the next step starts after it
+// in the binade reached.  A running sum of +0 skips to the first non-zero term
+// (+0 + t = t); a running sum that is negative, -0, below 2^-967, above 2^977
+// or not finite is advanced one term at a time.  Non-negative finite terms
+// (squares, exponentials) take the parallel step.
+constexpr int kChainC = 4;  // terms per lane and step of ordered_sum_wave
+
+template <int C>
+__device__ __forceinline__ double ordered_sum_wave(const double* t, int n, double s) {
+    const int lane = threadIdx.x & 63;
+    const unsigned long long lt = (1ull << lane) - 1ull;  // lanes below this one
+    int base = 0;
+    while (base < n) {
+        const unsigned long long sb = (unsigned long long)__double_as_longlong(s);
+        const int ex = (int)(sb >> 52);  // sign and biased exponent
+        if (sb == 0ull) {
+            int first = C;
+#pragma unroll
+            for (int i = C - 1; i >= 0; --i) {
+                const int idx = base + lane * C + i;
+                if (idx < n && t[idx] != 0.0) first = i;  // (NaN compares unequal)
+            }
+            const unsigned long long nz = __builtin_amdgcn_ballot_w64(first < C);
+            if (nz == 0ull) {
+                base += 64 * C;
+                continue;
+            }
+            const int j = __builtin_ctzll(nz);
+            const int idx = base + j * C + __builtin_amdgcn_readlane(first, j);
+            s = s + t[idx];
+            base = idx + 1;
+            continue;
+        }
+        if (ex < 56 || ex > 2000) {
+            const int end = min(n, base + 64 * C);
+            for (; base < end; ++base) s = s + t[base];
+            continue;
+        }
+        const double scale = __longlong_as_double((long long)(2098 - ex) << 52);  // 1/q
+        const double q = __longlong_as_double((long long)(ex - 52) << 52);
+        const double su = s * scale;   // s/q: an integer in [2^52, 2^53)
+        const double room = 0x1p53 - su;
+        double d0 = 0.0, sgn = 0.0;
+        int par = 0;  // parity of the running sum: relative until the block's first tie
+        bool tied = false, bad = false;
+#pragma unroll
+        for (int i = 0; i < C; ++i) {
+            const int idx = base + lane * C + i;
+            const double u = (idx < n ? t[idx] : 0.0) * scale;
+            bad |= !(u >= 0.0 && u < 0x1p52);
+            const double fl = floor(u);
+            const bool tie = u - fl == 0.5;
+            const double rn = rint(u);
+            const int pf = (int)__double_as_longlong(fl + 0x1p52) & 1;
+            const int pr = (int)__double_as_longlong(rn + 0x1p52) & 1;
+            const int up = par ^ pf;  // the tie's round-up that leaves the sum even
+            if (tie && !tied) sgn = up ? -1.0 : 1.0;  // change for an odd incoming parity
+            d0 += tie ? fl + (double)up : rn;
+            par = tie ? 0 : (par ^ pr);
+            tied |= tie;
+        }
+        const unsigned long long ht = __builtin_amdgcn_ballot_w64(tied);
+        const unsigned long long po = __builtin_amdgcn_ballot_w64(tied && par);
+        const unsigned long long fp = __builtin_amdgcn_ballot_w64(!tied && par);
+        const unsigned long long below = ht & lt;
+        const int b = below ? 63 - __builtin_clzll(below) : -1;
+        const unsigned long long since = b >= 0 ? lt & ~((2ull << b) - 1ull) : lt;
+        const int p0 = b >= 0 ? (int)(po >> b) & 1 : (int)(sb & 1ull);
+        const int pin = p0 ^ (__builtin_popcountll(fp & since) & 1);
+        const double psum = wave_scan_f64_dpp(tied && pin ? d0 + sgn : d0);
+        const unsigned long long stop = __builtin_amdgcn_ballot_w64(bad || !(psum < room));
+        if (stop == 0ull) {
+            s = (su + readlane63_d(psum)) * q;
+            base += 64 * C;
+        } else {
+            const int j = __builtin_ctzll(stop);
+            s = (su + (j > 0 ? readlane_d(psum, j - 1) : 0.0)) * q;
+            const int b0 = base + j * C;
+#pragma unroll
+            for (int i = 0; i < C; ++i)
+                if (b0 + i < n) s = s + t[b0 + i];
+            base = b0 + C;
+        }
+    }
+    return s;
+}
+
+// Inclusive prefix sum over the lanes of one segment: lane l adds only the
+// partial sums of lanes at or above ss (its segment's first lane), so each
+// segment is summed on its own (the DPP steps of wave_scan_f64_dpp).
+__device__ __forceinline__ double wave_seg_scan_f64(double v, int ss, int lane) {
+#define LAMD_SEG_STEP(CTRL, K)                                                    \
+    {                                                                             \
+        const double o = dpp_rows_d<CTRL, 0xf>(v);                                \
+        v = v + (((lane & 15) >= (K) && lane - (K) >= ss) ? o : 0.0);             \
+    }
+    LAMD_SEG_STEP(kDppShr1, 1)
+    LAMD_SEG_STEP(kDppShr2, 2)
+    LAMD_SEG_STEP(kDppShr4, 4)
+    LAMD_SEG_STEP(kDppShr8, 8)
+#undef LAMD_SEG_STEP
+    {
+        const double o = dpp_rows_d<kDppBcast15, 0xa>(v);  // rows 1 and 3 take lane 15 / 47
+        v = v + ((((lane >> 4) & 1) && (lane & ~15) - 1 >= ss) ? o : 0.0);
+    }
+    {
+        const double o = dpp_rows_d<kDppBcast31, 0xc>(v);  // rows 2 and 3 take lane 31
+        v = v + ((lane >= 32 && 31 >= ss) ? o : 0.0);
+    }
+    return v;
+}
+
+// LDS of ordered_sum_block for W waves: each wave's records, in order, at
+// [64w, 64w + count[w]).
+template <int W>
+struct OrderedSumLds {
+    double wtot[W];      // plain sum of each wave's terms
+    int count[W];        // records of each wave
+    double d0[W * 64];   // segment: its sum for an even incoming parity (units of q)
+    double d1[W * 64];   // segment: for an odd incoming parity
+    double sc[W * 64];   // segment: 1/q; sequential run: first term
+    double q[W * 64];    // segment: q; sequential run: number of terms
+    int meta[W * 64];    // segment: binade | first term << 11; sequential run: -1
+    double result;
+};
+
+// Terms per lane of ordered_sum_block for n terms over 64W threads: the
+// smallest of 1, 3, 5, 11, 15, 17, 27, 33, 63 that covers n (odd, so the lanes'
+// blocks start in different LDS banks).  The term array must hold
+// 64 * W * ordered_sum_lane_terms(n, W) doubles; ordered_sum_block writes -0
+// past the n terms.
+__host__ __device__ constexpr int ordered_sum_lane_terms(int n, int w) {
+    const int need = (n + 64 * w - 1) / (64 * w);
+    return need <= 1 ? 1 : need <= 3 ? 3 : need <= 5 ? 5 : need <= 11 ? 11 : need <= 15 ? 15
+         : need <= 17 ? 17 : need <= 27 ? 27 : need <= 33 ? 33 : 63;
+}
+__host__ __device__ constexpr int ordered_sum_slots(int n, int w) {
+    return 64 * w * ordered_sum_lane_terms(n, w);
+}
+
+template <int W, int G>
+__device__ __forceinline__ double ordered_sum_block_g(double* t, int n, double s0,
+                                                     OrderedSumLds<W>& sh) {
+    constexpr int T = W * 64;
+    constexpr int U = G < 8 ? G : 8;  // reads in flight per lane
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const double* tb = t + tid * G;  // this lane's block
+
+    // estimated running sums before and after each lane; an Inf or NaN term
+    // shows in the largest exponent field, a negative one in the smallest term
+    // (-0 padding is neither)
+    double a = 0.0, mn = 0.0;
+    unsigned hw = 0;
+#pragma unroll
+    for (int i0 = 0; i0 < G; i0 += U) {
+        double v[U];
+#pragma unroll
+        for (int j = 0; j < U; ++j) v[j] = i0 + j < G ? tb[i0 + j] : 0.0;
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            if (i0 + j < G) {
+                a = a + v[j];
+                mn = fmin(mn, v[j]);
+                hw = max(hw, (unsigned)((unsigned long long)__double_as_longlong(v[j]) >> 32) & 0x7fffffffu);
+            }
+        }
+    }
+    const double inc = wave_scan_f64_dpp(a);
+    double exc = __shfl_up(inc, 1, 64);
+    if (lane == 0) exc = 0.0;
+    if (lane == 63) sh.wtot[wave] = inc;
+    __syncthreads();
+    double off = s0;
+#pragma unroll
+    for (int v = 0; v < W - 1; ++v) off = v < wave ? off + sh.wtot[v] : off;
+    const double lo = (off + exc) * (1.0 - 0x1p-30);
+    const double hi = ((off + exc) + a) * (1.0 + 0x1p-30);
+    int e = (int)((unsigned long long)__double_as_longlong(lo) >> 52);  // biased exponent
+    const bool sq = !(lo >= 0x1p-960 && hi < 0x1p1000 &&
+                      e == (int)((unsigned long long)__double_as_longlong(hi) >> 52) &&
+                      hw < 0x7ff00000u && mn >= 0.0);  // non-negative finite terms, one binade
+    if (sq) e = 1023;
+    const double scale = __longlong_as_double((long long)(2098 - e) << 52);  // 1/q
+
+    // this lane's terms in units of q, for an even incoming parity.  u + 2^52
+    // rounds u (0 <= u < 2^52 in a lane that keeps its binade) to the nearest
+    // integer, half even; at a half-integer an odd running sum takes the other
+    // neighbour u + (u - rn) instead.  The first tie changes the lane's sum by
+    // +-1 when the incoming parity is odd (flip).
+    double d0 = 0.0;
+    unsigned par = 0, tied = 0, flip = 0;
+#pragma unroll
+    for (int i0 = 0; i0 < G; i0 += U) {
+        double v[U];
+#pragma unroll
+        for (int j = 0; j < U; ++j) v[j] = i0 + j < G ? tb[i0 + j] : 0.0;
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            if (i0 + j < G) {
+                const double u = v[j] * scale;
+                const double w = u + 0x1p52;
+                const double rn = w - 0x1p52;
+                const double df = u - rn;  // exact
+                const unsigned odd = (unsigned)__double_as_longlong(w) & 1u;
+                const unsigned tie = fabs(df) == 0.5 ? 1u : 0u;
+                d0 = d0 + ((tie & par) ? u + df : rn);
+                const unsigned up = df > 0.0 ? 1u : 0u;
+                flip = (tie & ~tied) ? (up ^ par ^ 1u) : flip;  // 1: -1, 0: +1
+                tied |= tie;
+                par = tie ? 0u : (par ^ odd);
+            }
+        }
+    }
+    const double sgn = flip ? -1.0 : 1.0;
+
+    // segments and each lane's incoming parity
+    const unsigned long long lt = (1ull << lane) - 1ull, le = lt | (1ull << lane);
+    const unsigned long long SQ = __builtin_amdgcn_ballot_w64(sq);
+    const int eprev = __shfl_up(e, 1, 64);
+    const bool start = !sq && (lane == 0 || ((SQ >> ((lane - 1) & 63)) & 1ull) || eprev != e);
+    const unsigned long long SS = __builtin_amdgcn_ballot_w64(start);
+    const unsigned long long ht = __builtin_amdgcn_ballot_w64(!sq && tied);
+    const unsigned long long po = __builtin_amdgcn_ballot_w64(!sq && tied && par);
+    const unsigned long long fp = __builtin_amdgcn_ballot_w64(!sq && !tied && par);
+    const int ss = sq ? lane + 1 : 63 - __builtin_clzll((SS & le) | 1ull);
+    const int ssc = sq ? lane : ss;
+    const unsigned long long inseg = lt & ~((1ull << ssc) - 1ull);  // segment lanes below
+    const unsigned long long below = ht & inseg;
+    const int b = below ? 63 - __builtin_clzll(below) : -1;       // last tie below
+    const unsigned long long since = b >= 0 ? (lt & ~((2ull << b) - 1ull)) : inseg;
+    const int p0 = b >= 0 ? (int)((po >> b) & 1ull) : 0;
+    const int pin = p0 ^ (__builtin_popcountll(fp & since) & 1);
+    const double d = sq ? 0.0 : ((tied && pin) ? d0 + sgn : d0);
+    const double dl = (!sq && tied && b < 0) ? (pin ? -sgn : sgn) : 0.0;
+    const double psum = wave_seg_scan_f64(d, ss, lane);
+    const bool end = !sq && (lane == 63 || (((SS | SQ) >> ((lane + 1) & 63)) & 1ull));
+    const unsigned long long SE = __builtin_amdgcn_ballot_w64(end);
+    const unsigned long long ft = ht & ~((1ull << ssc) - 1ull) & le;  // ties from the segment start
+    const double fl = __shfl(dl, ft ? __builtin_ctzll(ft) : lane, 64);
+    // records: segment ends, and the first lanes of runs of sequential lanes
+    const unsigned long long SR = SQ & ~(SQ << 1);
+    const unsigned long long IT = SE | SR;
+    const int slot = wave * 64 + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(IT >> 32),
+                                                               __builtin_amdgcn_mbcnt_lo((unsigned)IT, 0u));
+    if (end) {
+        sh.d0[slot] = psum;
+        sh.d1[slot] = ft ? psum + fl : psum;
+        sh.sc[slot] = scale;
+        sh.q[slot] = __longlong_as_double((long long)(e - 52) << 52);
+        sh.meta[slot] = e | ((wave * 64 + ss) * G << 11);
+    } else if ((SR >> lane) & 1ull) {
+        const unsigned long long rest_lanes = ~(SQ >> lane);  // zero only if all 64 lanes are sequential
+        const int run = rest_lanes ? __builtin_ctzll(rest_lanes) : 64;  // sequential lanes from this one
+        sh.sc[slot] = (double)(tid * G);
+        sh.q[slot] = (double)(run * G);
+        sh.meta[slot] = -1;
+    }
+    if (lane == 0) sh.count[wave] = __builtin_popcountll(IT);
+    __syncthreads();
+
+    // wave 0 walks the records in order, reading each one while the previous
+    // one is applied (a failed check ends the walk and the remaining terms go
+    // through ordered_sum_wave)
+    if (wave == 0) {
+        double s = s0;
+        int rest = -1;
+        for (int w = 0; w < W && rest < 0; ++w) {
+            const int cnt = __builtin_amdgcn_readfirstlane(sh.count[w]);
+            const int r0 = w * 64;
+            double nd0 = sh.d0[r0], nd1 = sh.d1[r0], nsc = sh.sc[r0], nq = sh.q[r0];
+            int nmeta = sh.meta[r0];
+            for (int k = 0; k < cnt; ++k) {
+                const double cd0 = nd0, cd1 = nd1, csc = nsc, cq = nq;
+                const int meta = __builtin_amdgcn_readfirstlane(nmeta);
+                const int rn = r0 + min(k + 1, 63);
+                nd0 = sh.d0[rn];
+                nd1 = sh.d1[rn];
+                nsc = sh.sc[rn];
+                nq = sh.q[rn];
+                nmeta = sh.meta[rn];
+                if (meta < 0) {
+                    // a run of sequential lanes: its terms, U read ahead of the
+                    // additions (the padding past n is -0: s + -0 = s for every s)
+                    const int b0 = __builtin_amdgcn_readfirstlane((int)csc);
+                    const int len = __builtin_amdgcn_readfirstlane((int)cq);
+                    for (int g = 0; g < len; g += G) {
+                        const double* sb = t + b0 + g;
+#pragma unroll
+                        for (int i0 = 0; i0 < G; i0 += U) {
+                            double v[U];
+#pragma unroll
+                            for (int j = 0; j < U; ++j) v[j] = i0 + j < G ? sb[i0 + j] : 0.0;
+#pragma unroll
+                            for (int j = 0; j < U; ++j)
+                                if (i0 + j < G) s = s + v[j];
+                        }
+                    }
+                    continue;
+                }
+                const double su = s * csc;
+                const double D = (__double_as_longlong(su) & 1ll) ? cd1 : cd0;
+                const bool ok = (int)((unsigned long long)__double_as_longlong(s) >> 52) == (meta & 0x7ff) &&
+                                D < 0x1p53 - su;
+                if (__builtin_expect(!ok, 0)) {
+                    rest = meta >> 11;
+                    break;
+                }
+                s = (su + D) * cq;
+            }
+        }
+        if (rest >= 0) s = ordered_sum_wave<kChainC>(t + rest, n - rest, s);
+        if (lane == 0) sh.result = s;
+    }
+    __syncthreads();
+    return sh.result;
+}
+
+// The one-lane chain `for (i = 0; i < n; ++i) s = s + t[i];` (t in LDS), bit
+// for bit, formed by all W x 64 threads of the workgroup (every thread calls
+// it; it returns the result to every thread and holds four barriers).  t must
+// hold ordered_sum_slots(n, W) doubles: the slots past n are set to -0, which
+// leaves every sum unchanged.
+//
+// Thread g takes the G = ordered_sum_lane_terms(n, W) consecutive terms
+// [gG, gG + G).  A plain fp64 prefix sum of the lanes' totals estimates the
+// running sum before and after each lane (within a relative 1e-12 for
+// non-negative terms), which places each lane in the binade [2^E, 2^(E+1))
+// its running sum keeps throughout -- with a margin of 2^-30 either side --
+// or marks it sequential (a crossing of a power of two, a zero or tiny start,
+// a huge end, a negative or non-finite term).  In a binade every rounded sum
+// is a multiple of q = 2^(E-52) and s + t rounds to s + q * r with r = t/q
+// rounded to the nearest integer, except at a half-integer t/q, whose
+// round-half-even result is the candidate that leaves s/q even (see
+// ordered_sum_wave).  So a lane sums its r in units of q exactly, taking its
+// segment's incoming parity as even; a run of lanes with one binade forms a
+// segment whose sum is a segmented prefix sum over the lanes (exact: integers
+// below 2^53), where each lane's parity comes from wave ballots, and whose sum
+// for an odd incoming parity differs only at its first tie.  Wave 0 then walks
+// the records in order: a segment checks that the exact running sum lies in
+// its binade with room for the segment's sum and adds it (its parity picks the
+// variant); a sequential lane adds its terms with fp64 additions.  A failed
+// check (a running sum the estimate misplaced: possible only with negative
+// terms) hands the rest of the row, from that segment's first term, to
+// ordered_sum_wave.
+template <int W>
+__device__ __forceinline__ double ordered_sum_block(double* t, int n, double s0,
+                                                   OrderedSumLds<W>& sh) {
+    static_assert(W >= 2 && W <= 16, "64 x W threads, at most 63 terms per lane for n <= 8064");
+    if (n <= 0) return s0;
+    const int G = ordered_sum_lane_terms(n, W);
+    for (int i = n + (int)threadIdx.x; i < 64 * W * G; i += 64 * W) t[i] = -0.0;
+    __syncthreads();
+    switch (G) {
+        case 1: return ordered_sum_block_g<W, 1>(t, n, s0, sh);
+        case 3: return ordered_sum_block_g<W, 3>(t, n, s0, sh);
+        case 5: return ordered_sum_block_g<W, 5>(t, n, s0, sh);
+        case 11: return ordered_sum_block_g<W, 11>(t, n, s0, sh);
+        case 15: return ordered_sum_block_g<W, 15>(t, n, s0, sh);
+        case 17: return ordered_sum_block_g<W, 17>(t, n, s0, sh);
+        default: break;
+    }
+    if constexpr (W <= 4) {  // more than 17 terms per lane for n <= 8064 only below 512 threads
+        switch (G) {
+            case 27: return ordered_sum_block_g<W, 27>(t, n, s0, sh);
+            case 33: return ordered_sum_block_g<W, 33>(t, n, s0, sh);
+            default: break;
+        }
+    }
+    if constexpr (W <= 2) return ordered_sum_block_g<W, 63>(t, n, s0, sh);
+    return ordered_sum_wave<kChainC>(t, n, s0);  // (not reached for n <= 8064)
+}
+
 // Block reductions over blockDim.x threads (a multiple of 64, at most 1024).
 __device__ inline float block_max(float v, float* sh) {
     v = wave_max(v);

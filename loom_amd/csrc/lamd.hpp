@@ -144,6 +144,12 @@ hipError_t launch_norm_quant(float* h, int ldh, int m, int n, const float* weigh
 bool launch_row_sumsq_f32(const float* x, long ldx, int m, int n, double* totals, hipStream_t s,
                           hipError_t* e);
 
+// out[i] = s0 + t[i][0] + t[i][1] + ... + t[i][n-1] in index order (one fp64
+// rounding per addition) for m rows of n terms (n <= kMaxStrictNormCols), one
+// workgroup of `threads` (64, 256 or 512) per row.
+hipError_t launch_ordered_sum_rows(const double* terms, int m, int n, double s0, double* out,
+                                   int threads, hipStream_t s);
+
 // Per-device scratch arena for the device-resident entry points.
 void* scratch(int device, size_t bytes, std::string* err);
 

@@ -125,7 +125,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
             // ---- sum of squares per row -----------------------------------
             double tot[MR];
             if (STRICT) {
-                // one row: squares to LDS, one lane adds them in element order
+                // one row: squares to LDS, then their element-order chain
                 double* sq = (double*)xq_s;
 #pragma unroll
                 for (int j = 0; j < FV; ++j) {
@@ -144,9 +144,12 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
                     }
                 }
                 __syncthreads();
-                if (tid == 0) nsum[0][0] = ordered_sum(sq, k, 0.0);
-                __syncthreads();
-                tot[0] = nsum[0][0];
+                if constexpr (WAVES >= 2) {
+                    __shared__ OrderedSumLds<WAVES> osum;
+                    tot[0] = ordered_sum_block<WAVES>(sq, k, 0.0, osum);
+                } else {
+                    tot[0] = ordered_sum_wave<kChainC>(sq, k, 0.0);
+                }
 #pragma unroll
                 for (int rr = 1; rr < MR; ++rr) tot[rr] = 0.0;
             } else {
@@ -1002,9 +1005,11 @@ bool fused_quant_ok(int m, int k, const float* x) {
 constexpr int kNormWaves = 8;
 constexpr int kNormThreads = kNormWaves * 64;
 
+// Dynamic LDS of a norm-fused launch: the quantized rows, or in strict mode
+// the row's squares padded for ordered_sum_block (either workgroup width).
 static size_t norm_lds(int m, int k, int strict) {
     const size_t q = (size_t)m * pad_cols(k);
-    const size_t sq = strict ? (size_t)k * 8 : 0;
+    const size_t sq = strict ? (size_t)max(ordered_sum_slots(k, 4), ordered_sum_slots(k, kNormWaves)) * 8 : 0;
     return q > sq ? q : sq;
 }
 
@@ -1013,7 +1018,7 @@ bool norm_fused_ok(int m, int k, int strict, bool x16) {
     // rows held in registers: up to 4 element groups per thread (more spills)
     if ((size_t)m * (k / 4) > (size_t)4 * kNormThreads) return false;
     if (strict && m != 1) return false;  // one row of squares in LDS
-    return norm_lds(m, k, strict) <= 60 * 1024;
+    return norm_lds(m, k, strict) <= 96 * 1024;
 }
 
 template <int NMAT, int NORM, int STRICT, int WAVES, int FV>

@@ -221,7 +221,9 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(float* __restrict__ h, 
             }
         }
         __syncthreads();
-        if (threadIdx.x == 0) total = ordered_sum(dsh, n, 0.0);
+        __shared__ OrderedSumLds<4> osum;
+        const double r = ordered_sum_block<4>(dsh, n, 0.0, osum);
+        if (threadIdx.x == 0) total = r;
         __syncthreads();
     } else {
         double s = 0.0;
@@ -284,7 +286,8 @@ template <int STRICT>
 static hipError_t launch_norm_t(float* h, int ldh, int m, int n, const float* weight, double eps,
                                 int8_t* hq, int ldq, float* amax, int32_t* xsum, int keep,
                                 const double* totals, hipStream_t s) {
-    const size_t shm = STRICT && !totals ? (size_t)n * sizeof(double) : 256 * sizeof(double);
+    const size_t shm = STRICT && !totals ? (size_t)ordered_sum_slots(n, 4) * sizeof(double)
+                                         : 256 * sizeof(double);
     const dim3 g(m), b(256);
 #define LAMD_NQ(VPT)                                                                            \
     hipLaunchKernelGGL((norm_quant_kernel<STRICT, VPT>), g, b, shm, s, h, ldh, n, weight, eps, hq, ldq, \
@@ -314,6 +317,43 @@ hipError_t launch_norm_quant(float* h, int ldh, int m, int n, const float* weigh
     const bool rows = launch_row_sumsq_f32(h, ldh, m, n, totals, s, &e);
     if (e != hipSuccess) return e;
     return launch_norm_t<1>(h, ldh, m, n, weight, eps, hq, ldq, amax, xsum, keep, rows ? totals : nullptr, s);
+}
+
+// One workgroup per row: the row's n terms into LDS, then the index-order
+// chain s0 + t[0] + t[1] + ... formed by ordered_sum_wave (64 threads) or
+// ordered_sum_block (256 or 512 threads: the strict norm kernels' widths).
+template <int W>
+__global__ __launch_bounds__(W * 64) void ordered_sum_rows_kernel(const double* __restrict__ terms, int n,
+                                                                  double s0, double* __restrict__ out) {
+    extern __shared__ double tsh[];
+    const double* tr = terms + (size_t)blockIdx.x * n;
+    for (int i = threadIdx.x; i < n; i += W * 64) tsh[i] = tr[i];
+    __syncthreads();
+    double r;
+    if constexpr (W == 1) {
+        r = ordered_sum_wave<kChainC>(tsh, n, s0);
+    } else {
+        __shared__ OrderedSumLds<W> osum;
+        r = ordered_sum_block<W>(tsh, n, s0, osum);
+    }
+    if (threadIdx.x == 0) out[blockIdx.x] = r;
+}
+
+hipError_t launch_ordered_sum_rows(const double* terms, int m, int n, double s0, double* out,
+                                   int threads, hipStream_t s) {
+    if (m <= 0) return hipSuccess;
+    if (n <= 0 || n > kMaxStrictNormCols) return hipErrorInvalidValue;
+    const size_t shm = (size_t)max(n, ordered_sum_slots(n, threads / 64)) * sizeof(double);
+    if (threads == 64) {
+        hipLaunchKernelGGL(ordered_sum_rows_kernel<1>, dim3(m), dim3(64), shm, s, terms, n, s0, out);
+    } else if (threads == 256) {
+        hipLaunchKernelGGL(ordered_sum_rows_kernel<4>, dim3(m), dim3(256), shm, s, terms, n, s0, out);
+    } else if (threads == 512) {
+        hipLaunchKernelGGL(ordered_sum_rows_kernel<8>, dim3(m), dim3(512), shm, s, terms, n, s0, out);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 }  // namespace lamd
