@@ -398,17 +398,16 @@ __device__ __forceinline__ double wave_seg_scan_f64(double v, int ss, int lane) 
     return v;
 }
 
-// LDS of ordered_sum_block for W waves: each wave's records, in order, at
-// [64w, 64w + count[w]).
+// LDS of ordered_sum_block for W waves (records at the lane that ends a
+// segment).
 template <int W>
 struct OrderedSumLds {
-    double wtot[W];      // plain sum of each wave's terms
-    int count[W];        // records of each wave
-    double d0[W * 64];   // segment: its sum for an even incoming parity (units of q)
-    double d1[W * 64];   // segment: for an odd incoming parity
-    double sc[W * 64];   // segment: 1/q; sequential run: first term
-    double q[W * 64];    // segment: q; sequential run: number of terms
-    int meta[W * 64];    // segment: binade | first term << 11; sequential run: -1
+    double wtot[W];               // plain sum of each wave's terms
+    unsigned long long items[W];  // lanes with a record: segment ends and sequential lanes
+    unsigned long long seql[W];   // the sequential lanes
+    double seg[W * 64];           // a segment's sum (incoming parity even), at its last lane
+    double flip[W * 64];          // its change for an odd incoming parity
+    int meta[W * 64];             // binade | first lane << 16
     double result;
 };
 
@@ -429,17 +428,18 @@ __host__ __device__ constexpr int ordered_sum_slots(int n, int w) {
 template <int W, int G>
 __device__ __forceinline__ double ordered_sum_block_g(double* t, int n, double s0,
                                                      OrderedSumLds<W>& sh) {
-    constexpr int T = W * 64;
-    constexpr int U = G < 8 ? G : 8;  // reads in flight per lane
+    constexpr int U = G < 8 ? G : (G <= 17 ? 8 : 4);  // reads in flight per lane
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const double* tb = t + tid * G;  // this lane's block
+    const bool active = wave < W;    // waves past W only meet the barriers
+    const double* tb = t + tid * G;  // this lane's block (active waves)
 
     // estimated running sums before and after each lane; an Inf or NaN term
     // shows in the largest exponent field, a negative one in the smallest term
     // (-0 padding is neither)
-    double a = 0.0, mn = 0.0;
+    double a = 0.0, mn = 0.0, exc = 0.0;
     unsigned hw = 0;
-#pragma unroll
+    if (active) {
+#pragma unroll(G <= 17 ? 8 : 1)
     for (int i0 = 0; i0 < G; i0 += U) {
         double v[U];
 #pragma unroll
@@ -454,10 +454,12 @@ __device__ __forceinline__ double ordered_sum_block_g(double* t, int n, double s
         }
     }
     const double inc = wave_scan_f64_dpp(a);
-    double exc = __shfl_up(inc, 1, 64);
+    exc = __shfl_up(inc, 1, 64);
     if (lane == 0) exc = 0.0;
     if (lane == 63) sh.wtot[wave] = inc;
+    }
     __syncthreads();
+    if (active) {
     double off = s0;
 #pragma unroll
     for (int v = 0; v < W - 1; ++v) off = v < wave ? off + sh.wtot[v] : off;
@@ -477,7 +479,7 @@ __device__ __forceinline__ double ordered_sum_block_g(double* t, int n, double s
     // +-1 when the incoming parity is odd (flip).
     double d0 = 0.0;
     unsigned par = 0, tied = 0, flip = 0;
-#pragma unroll
+#pragma unroll(G <= 17 ? 8 : 1)
     for (int i0 = 0; i0 < G; i0 += U) {
         double v[U];
 #pragma unroll
@@ -525,75 +527,71 @@ __device__ __forceinline__ double ordered_sum_block_g(double* t, int n, double s
     const unsigned long long SE = __builtin_amdgcn_ballot_w64(end);
     const unsigned long long ft = ht & ~((1ull << ssc) - 1ull) & le;  // ties from the segment start
     const double fl = __shfl(dl, ft ? __builtin_ctzll(ft) : lane, 64);
-    // records: segment ends, and the first lanes of runs of sequential lanes
-    const unsigned long long SR = SQ & ~(SQ << 1);
-    const unsigned long long IT = SE | SR;
-    const int slot = wave * 64 + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(IT >> 32),
-                                                               __builtin_amdgcn_mbcnt_lo((unsigned)IT, 0u));
     if (end) {
-        sh.d0[slot] = psum;
-        sh.d1[slot] = ft ? psum + fl : psum;
-        sh.sc[slot] = scale;
-        sh.q[slot] = __longlong_as_double((long long)(e - 52) << 52);
-        sh.meta[slot] = e | ((wave * 64 + ss) * G << 11);
-    } else if ((SR >> lane) & 1ull) {
-        const unsigned long long rest_lanes = ~(SQ >> lane);  // zero only if all 64 lanes are sequential
-        const int run = rest_lanes ? __builtin_ctzll(rest_lanes) : 64;  // sequential lanes from this one
-        sh.sc[slot] = (double)(tid * G);
-        sh.q[slot] = (double)(run * G);
-        sh.meta[slot] = -1;
+        sh.seg[tid] = psum;
+        sh.flip[tid] = ft ? fl : 0.0;
+        sh.meta[tid] = e | (ss << 16);
     }
-    if (lane == 0) sh.count[wave] = __builtin_popcountll(IT);
+    if (lane == 0) {
+        sh.items[wave] = SE | SQ;
+        sh.seql[wave] = SQ;
+    }
+    }
     __syncthreads();
 
-    // wave 0 walks the records in order, reading each one while the previous
-    // one is applied (a failed check ends the walk and the remaining terms go
-    // through ordered_sum_wave)
+    // wave 0 walks the records in order (a failed check ends the walk and
+    // the remaining terms go through ordered_sum_wave); the next wave's records
+    // are read while the current wave's are walked
     if (wave == 0) {
         double s = s0;
         int rest = -1;
+        double segv = sh.seg[lane], flipv = sh.flip[lane];
+        int metav = sh.meta[lane];
+        unsigned long long itv = sh.items[0], sqv = sh.seql[0];
         for (int w = 0; w < W && rest < 0; ++w) {
-            const int cnt = __builtin_amdgcn_readfirstlane(sh.count[w]);
-            const int r0 = w * 64;
-            double nd0 = sh.d0[r0], nd1 = sh.d1[r0], nsc = sh.sc[r0], nq = sh.q[r0];
-            int nmeta = sh.meta[r0];
-            for (int k = 0; k < cnt; ++k) {
-                const double cd0 = nd0, cd1 = nd1, csc = nsc, cq = nq;
-                const int meta = __builtin_amdgcn_readfirstlane(nmeta);
-                const int rn = r0 + min(k + 1, 63);
-                nd0 = sh.d0[rn];
-                nd1 = sh.d1[rn];
-                nsc = sh.sc[rn];
-                nq = sh.q[rn];
-                nmeta = sh.meta[rn];
-                if (meta < 0) {
-                    // a run of sequential lanes: its terms, U read ahead of the
-                    // additions (the padding past n is -0: s + -0 = s for every s)
-                    const int b0 = __builtin_amdgcn_readfirstlane((int)csc);
-                    const int len = __builtin_amdgcn_readfirstlane((int)cq);
-                    for (int g = 0; g < len; g += G) {
-                        const double* sb = t + b0 + g;
+            unsigned long long items = uniform_u64(itv);
+            const unsigned long long seqm = uniform_u64(sqv);
+            const double cseg = segv, cflip = flipv;
+            const int cmeta = metav;
+            if (w + 1 < W) {
+                segv = sh.seg[(w + 1) * 64 + lane];
+                flipv = sh.flip[(w + 1) * 64 + lane];
+                metav = sh.meta[(w + 1) * 64 + lane];
+                itv = sh.items[w + 1];
+                sqv = sh.seql[w + 1];
+            }
+            while (items) {
+                const int l = __builtin_ctzll(items);
+                items &= items - 1ull;
+                const int b0 = (w * 64 + l) * G;
+                if ((seqm >> l) & 1ull) {
+                    // a sequential lane: its G terms, read U ahead of the additions
+                    // (the padding past n is -0, and s + -0 = s for every s)
+                    const double* sb = t + b0;
+#pragma unroll(G <= 17 ? 8 : 1)
+                    for (int i0 = 0; i0 < G; i0 += U) {
+                        double v[U];
 #pragma unroll
-                        for (int i0 = 0; i0 < G; i0 += U) {
-                            double v[U];
+                        for (int j = 0; j < U; ++j) v[j] = i0 + j < G ? sb[i0 + j] : 0.0;
 #pragma unroll
-                            for (int j = 0; j < U; ++j) v[j] = i0 + j < G ? sb[i0 + j] : 0.0;
-#pragma unroll
-                            for (int j = 0; j < U; ++j)
-                                if (i0 + j < G) s = s + v[j];
-                        }
+                        for (int j = 0; j < U; ++j)
+                            if (i0 + j < G) s = s + v[j];
                     }
                     continue;
                 }
-                const double su = s * csc;
-                const double D = (__double_as_longlong(su) & 1ll) ? cd1 : cd0;
-                const bool ok = (int)((unsigned long long)__double_as_longlong(s) >> 52) == (meta & 0x7ff) &&
-                                D < 0x1p53 - su;
+                const int meta = __builtin_amdgcn_readlane(cmeta, l);
+                const int E = meta & 0x7ff;
+                const double sc = __longlong_as_double((long long)(2098 - E) << 52);
+                const double q = __longlong_as_double((long long)(E - 52) << 52);
+                const double seg = readlane_d(cseg, l), fv = readlane_d(cflip, l);
+                const double su = s * sc;
+                const double D = seg + ((__double_as_longlong(su) & 1ll) ? fv : 0.0);
+                const bool ok = (int)((unsigned long long)__double_as_longlong(s) >> 52) == E && D < 0x1p53 - su;
                 if (__builtin_expect(!ok, 0)) {
-                    rest = meta >> 11;
+                    rest = (w * 64 + (meta >> 16)) * G;
                     break;
                 }
-                s = (su + D) * cq;
+                s = (su + D) * q;
             }
         }
         if (rest >= 0) s = ordered_sum_wave<kChainC>(t + rest, n - rest, s);
@@ -604,8 +602,9 @@ __device__ __forceinline__ double ordered_sum_block_g(double* t, int n, double s
 }
 
 // The one-lane chain `for (i = 0; i < n; ++i) s = s + t[i];` (t in LDS), bit
-// for bit, formed by all W x 64 threads of the workgroup (every thread calls
-// it; it returns the result to every thread and holds four barriers).  t must
+// for bit, formed by the first W waves of the workgroup (every thread of the
+// workgroup calls it -- waves past W only meet its four barriers -- and every
+// thread gets the result).  t must
 // hold ordered_sum_slots(n, W) doubles: the slots past n are set to -0, which
 // leaves every sum unchanged.
 //
@@ -633,10 +632,10 @@ __device__ __forceinline__ double ordered_sum_block_g(double* t, int n, double s
 template <int W>
 __device__ __forceinline__ double ordered_sum_block(double* t, int n, double s0,
                                                    OrderedSumLds<W>& sh) {
-    static_assert(W >= 2 && W <= 16, "64 x W threads, at most 63 terms per lane for n <= 8064");
+    static_assert(W >= 2 && W <= 8, "the sum runs on 2 to 8 waves");
     if (n <= 0) return s0;
     const int G = ordered_sum_lane_terms(n, W);
-    for (int i = n + (int)threadIdx.x; i < 64 * W * G; i += 64 * W) t[i] = -0.0;
+    for (int i = n + (int)threadIdx.x; i < 64 * W * G; i += (int)blockDim.x) t[i] = -0.0;
     __syncthreads();
     switch (G) {
         case 1: return ordered_sum_block_g<W, 1>(t, n, s0, sh);
@@ -647,7 +646,7 @@ __device__ __forceinline__ double ordered_sum_block(double* t, int n, double s0,
         case 17: return ordered_sum_block_g<W, 17>(t, n, s0, sh);
         default: break;
     }
-    if constexpr (W <= 4) {  // more than 17 terms per lane for n <= 8064 only below 512 threads
+    if constexpr (W <= 4) {  // more than 17 terms per lane (n <= 8064) only below 8 waves
         switch (G) {
             case 27: return ordered_sum_block_g<W, 27>(t, n, s0, sh);
             case 33: return ordered_sum_block_g<W, 33>(t, n, s0, sh);

@@ -19,6 +19,8 @@ bool stream_ok(int m, int k, int n_tiles, bool fused, const Epilogue& epi);
 hipError_t launch_stream(const MatArgs& p, bool fuseq, hipStream_t s);
 
 constexpr int kFusedMaxRows = 4;
+// strict norm rows this long form their sum on eight waves (fewer terms per lane)
+constexpr int kSumWideCols = 4096;
 constexpr int kFusedVec = 16;  // float4 per thread in the fused prologue (max)
 
 // Row of element group idx (4 elements) among M <= MR rows of row4 groups.
@@ -144,9 +146,19 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
                     }
                 }
                 __syncthreads();
-                if constexpr (WAVES >= 2) {
-                    __shared__ OrderedSumLds<WAVES> osum;
-                    tot[0] = ordered_sum_block<WAVES>(sq, k, 0.0, osum);
+                if constexpr (WAVES >= 8 && NMAT == 1) {  // long rows on eight waves, others on four
+                    __shared__ union {
+                        OrderedSumLds<8> w8;
+                        OrderedSumLds<4> w4;
+                    } osum;
+                    if (k >= kSumWideCols) {
+                        tot[0] = ordered_sum_block<8>(sq, k, 0.0, osum.w8);
+                    } else {
+                        tot[0] = ordered_sum_block<4>(sq, k, 0.0, osum.w4);
+                    }
+                } else if constexpr (WAVES >= 4) {
+                    __shared__ OrderedSumLds<4> osum;
+                    tot[0] = ordered_sum_block<4>(sq, k, 0.0, osum);
                 } else {
                     tot[0] = ordered_sum_wave<kChainC>(sq, k, 0.0);
                 }
@@ -1006,10 +1018,12 @@ constexpr int kNormWaves = 8;
 constexpr int kNormThreads = kNormWaves * 64;
 
 // Dynamic LDS of a norm-fused launch: the quantized rows, or in strict mode
-// the row's squares padded for ordered_sum_block (either workgroup width).
+// the row's squares padded for ordered_sum_block (four waves, or eight for
+// rows of kSumWideCols and more).
 static size_t norm_lds(int m, int k, int strict) {
     const size_t q = (size_t)m * pad_cols(k);
-    const size_t sq = strict ? (size_t)max(ordered_sum_slots(k, 4), ordered_sum_slots(k, kNormWaves)) * 8 : 0;
+    const int slots = max(ordered_sum_slots(k, 4), k >= kSumWideCols ? ordered_sum_slots(k, 8) : 0);
+    const size_t sq = strict ? (size_t)slots * 8 : 0;
     return q > sq ? q : sq;
 }
 

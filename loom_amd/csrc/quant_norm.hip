@@ -321,7 +321,8 @@ hipError_t launch_norm_quant(float* h, int ldh, int m, int n, const float* weigh
 
 // One workgroup per row: the row's n terms into LDS, then the index-order
 // chain s0 + t[0] + t[1] + ... formed by ordered_sum_wave (64 threads) or
-// ordered_sum_block (256 or 512 threads: the strict norm kernels' widths).
+// ordered_sum_block on four waves (256 or 512 threads: the strict norm
+// kernels' widths).
 template <int W>
 __global__ __launch_bounds__(W * 64) void ordered_sum_rows_kernel(const double* __restrict__ terms, int n,
                                                                   double s0, double* __restrict__ out) {
@@ -332,9 +333,9 @@ __global__ __launch_bounds__(W * 64) void ordered_sum_rows_kernel(const double* 
     double r;
     if constexpr (W == 1) {
         r = ordered_sum_wave<kChainC>(tsh, n, s0);
-    } else {
-        __shared__ OrderedSumLds<W> osum;
-        r = ordered_sum_block<W>(tsh, n, s0, osum);
+    } else {  // the first four waves form the sum
+        __shared__ OrderedSumLds<4> osum;
+        r = ordered_sum_block<4>(tsh, n, s0, osum);
     }
     if (threadIdx.x == 0) out[blockIdx.x] = r;
 }
@@ -343,7 +344,7 @@ hipError_t launch_ordered_sum_rows(const double* terms, int m, int n, double s0,
                                    int threads, hipStream_t s) {
     if (m <= 0) return hipSuccess;
     if (n <= 0 || n > kMaxStrictNormCols) return hipErrorInvalidValue;
-    const size_t shm = (size_t)max(n, ordered_sum_slots(n, threads / 64)) * sizeof(double);
+    const size_t shm = (size_t)max(n, ordered_sum_slots(n, threads < 256 ? 1 : 4)) * sizeof(double);
     if (threads == 64) {
         hipLaunchKernelGGL(ordered_sum_rows_kernel<1>, dim3(m), dim3(64), shm, s, terms, n, s0, out);
     } else if (threads == 256) {
