@@ -1696,13 +1696,17 @@ __global__ __launch_bounds__(64) void attn_exp_kernel(const int* __restrict__ po
 }
 
 // strict part 3: one workgroup per (head, group of DG value columns, row).
-// Lane d < DG adds its value column in position order; one lane of another
-// wave forms expSum in position order (every group of the head forms the same
-// chain).  V columns and probabilities stream through two LDS buffers in
-// chunks of C = 4096 / DG positions (4096 floats), with kChainDepth chunks of
-// loads in flight in registers.  The loads are branch-free (indices clamped
-// into the ring and the score row; surplus values are never used), so each
-// store waits only for its own chunk.  grid (heads * HD / DG, rows), 256 threads.
+// Lane d <= DG of wave 0 adds column d of the products p[k] * v[k][d] in
+// position order (the reference's `sum += p * v`, a product then a sum, each
+// rounded); column DG holds p itself, whose chain is expSum.  Chunks of
+// C = 4096 / DG positions: every thread loads its 16 values of a chunk (and
+// the probabilities they need: C / 256 more for column DG) kChainDepth chunks
+// ahead, forms its products
+// in registers and writes them to one of two LDS product buffers, transposed
+// so that a chain lane reads two positions per 16-byte load; wave 0 adds chunk
+// c while the products of chunk c + 1 are written.  The loads are branch-free
+// (indices clamped into the ring and the score row; surplus values are never
+// added).  grid (heads * HD / DG, rows), 256 threads.
 constexpr int kChainDepth = 4;
 constexpr int kChainCols = 16;
 
@@ -1712,12 +1716,12 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(const float* __restrict
                                                          int span, int heads, int kv_heads,
                                                          int seq, DecodeScratch sc,
                                                          double* __restrict__ out) {
-    constexpr int C = 4096 / DG;
-    static_assert(C * DG == 4096 && C <= 256 && HD % DG == 0 && DG % 4 == 0 && DG <= 192,
+    constexpr int C = 4096 / DG;  // positions per chunk
+    constexpr int CP = C + 2;     // row pitch (16-byte aligned rows, lanes' reads in different banks)
+    static_assert(C * DG == 4096 && C % 256 == 0 && C <= 512 && HD % DG == 0 && DG % 4 == 0,
                   "chunk geometry");
-    __shared__ float4 vbuf[2][1024];
-    __shared__ double pbuf[2][256];
-    __shared__ double es_sh;
+    constexpr int PT = C / 256;   // probabilities of column DG per thread
+    __shared__ __align__(16) double prod[2][DG + 1][CP];
     const int h = blockIdx.x / (HD / DG), dg = blockIdx.x % (HD / DG), row = blockIdx.y;
     const int b = row / seq, s = row % seq;
     const int kvh = h / (heads / kv_heads);
@@ -1732,62 +1736,90 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(const float* __restrict
     const int nch = (L + C - 1) / C;
     const float* vb = cache_v + (size_t)b * msl * kv_dim + (size_t)kvh * HD + dg * DG;
     const double* pr = sc.scores + ((size_t)row * heads + h) * span;
-    constexpr int es_lane = 192;
 
-    // staging registers of the chunks in flight: named scalars filled by
-    // macros (arrays of them, indexed in loops, were kept in scratch memory)
+    // staging registers of the chunks in flight (named scalars filled by
+    // macros: arrays of them, indexed in loops, were kept in scratch memory).
+    // Thread tid holds the float4s at elements 4(tid + 256 I) of the chunk's
+    // C x DG values (position e / DG, column e % DG), the probabilities of
+    // those positions, and the probability of position tid (column DG).
     float4 r0_0, r0_1, r0_2, r0_3, r1_0, r1_1, r1_2, r1_3;
     float4 r2_0, r2_1, r2_2, r2_3, r3_0, r3_1, r3_2, r3_3;
-    double rp0, rp1, rp2, rp3;
+    double p0_0, p0_1, p0_2, p0_3, p1_0, p1_1, p1_2, p1_3;
+    double p2_0, p2_1, p2_2, p2_3, p3_0, p3_1, p3_2, p3_3;
+    double pt0[PT], pt1[PT], pt2[PT], pt3[PT];
 #define LAMD_CHAIN_LD(U, I, CC)                                                   \
     {                                                                             \
-        const int e = (tid + (I) * 256) * 4; /* element of the 4096-float chunk */ \
-        const int k = min((CC) * C + e / DG, msl - 1);                            \
-        r##U##_##I = *(const float4*)(vb + (size_t)k * kv_dim + e % DG);          \
+        const int e = (tid + (I) * 256) * 4; /* element of the C x DG chunk */     \
+        const int k = (CC) * C + e / DG;                                          \
+        r##U##_##I = *(const float4*)(vb + (size_t)min(k, msl - 1) * kv_dim + e % DG); \
+        p##U##_##I = pr[min(k, span - 1)];                                        \
     }
 #define LAMD_CHAIN_ISSUE(U, CH)                                                   \
     {                                                                             \
         const int cc = min((CH), nch - 1);                                        \
         LAMD_CHAIN_LD(U, 0, cc) LAMD_CHAIN_LD(U, 1, cc)                           \
         LAMD_CHAIN_LD(U, 2, cc) LAMD_CHAIN_LD(U, 3, cc)                           \
-        rp##U = pr[min(cc * C + min(tid, C - 1), span - 1)];                      \
+        _Pragma("unroll") for (int q = 0; q < PT; ++q)                            \
+            pt##U[q] = pr[min(cc * C + tid + 256 * q, span - 1)];                 \
+    }
+#define LAMD_CHAIN_PR(U, I, BUF)                                                  \
+    {                                                                             \
+        const int e = (tid + (I) * 256) * 4;                                      \
+        const int k = e / DG, d = e % DG;                                         \
+        prod[BUF][d][k] = p##U##_##I * (double)r##U##_##I.x;                      \
+        prod[BUF][d + 1][k] = p##U##_##I * (double)r##U##_##I.y;                  \
+        prod[BUF][d + 2][k] = p##U##_##I * (double)r##U##_##I.z;                  \
+        prod[BUF][d + 3][k] = p##U##_##I * (double)r##U##_##I.w;                  \
+    }
+#define LAMD_CHAIN_PRODUCTS(U, BUF)                                               \
+    {                                                                             \
+        LAMD_CHAIN_PR(U, 0, BUF) LAMD_CHAIN_PR(U, 1, BUF)                         \
+        LAMD_CHAIN_PR(U, 2, BUF) LAMD_CHAIN_PR(U, 3, BUF)                         \
+        _Pragma("unroll") for (int q = 0; q < PT; ++q)                            \
+            prod[BUF][DG][tid + 256 * q] = pt##U[q];                              \
     }
     LAMD_CHAIN_ISSUE(0, 0)
     LAMD_CHAIN_ISSUE(1, 1)
     LAMD_CHAIN_ISSUE(2, 2)
     LAMD_CHAIN_ISSUE(3, 3)
+    LAMD_CHAIN_PRODUCTS(0, 0)
+    LAMD_CHAIN_ISSUE(0, kChainDepth)
+    __syncthreads();
 
-    double sum = 0.0, es = 0.0;
-    // one chunk step per staging set U (a macro expanded for each U)
-#define LAMD_CHAIN_STEP(U)                                                                   \
-    {                                                                                        \
-        const int c = c0 + (U);                                                              \
-        vbuf[(U) & 1][tid] = r##U##_0;                                                       \
-        vbuf[(U) & 1][tid + 256] = r##U##_1;                                                 \
-        vbuf[(U) & 1][tid + 512] = r##U##_2;                                                 \
-        vbuf[(U) & 1][tid + 768] = r##U##_3;                                                 \
-        pbuf[(U) & 1][tid] = rp##U;                                                          \
-        LAMD_CHAIN_ISSUE(U, c + kChainDepth)                                                 \
-        __syncthreads();                                                                     \
-        if (c < nch) { /* uniform */                                                         \
-            const float* vbb = (const float*)vbuf[(U) & 1];                                  \
-            const double* pbb = pbuf[(U) & 1];                                               \
-            const int n = min(C, L - c * C);                                                 \
-            if (tid < DG) sum = ordered_dot(pbb, vbb + tid, DG, n, sum);                   \
-            if (tid == es_lane) es = ordered_sum(pbb, n, es);                                \
-        }                                                                                    \
+    double sum = 0.0;  // column tid's chain (tid <= DG)
+    // step for chunk c = c0 + U: the products of chunk c + 1 (staging set
+    // U + 1) go to buffer (c + 1) & 1 and that set is refilled, then wave 0
+    // adds chunk c from buffer c & 1 (both parities are compile-time: c0 is a
+    // multiple of four).  Products and loads run for every chunk's step, for
+    // chunks past the last one too (clamped indices; no chain reads them), so
+    // the loads of the next three chunks stay in flight across each wait.
+#define LAMD_CHAIN_STEP(U, UN)                                                    \
+    {                                                                             \
+        const int c = c0 + (U);                                                   \
+        if (c >= nch) break;                                                      \
+        LAMD_CHAIN_PRODUCTS(UN, ((U) + 1) & 1)                                    \
+        LAMD_CHAIN_ISSUE(UN, c + 1 + kChainDepth)                                 \
+        if (c < nch && tid <= DG) {                                               \
+            const double* pc = prod[(U) & 1][tid];                                \
+            const int n = min(C, L - c * C);                                      \
+            sum = chain_add_pairs<C>(pc, n, sum);                                 \
+        }                                                                         \
+        __syncthreads();                                                          \
     }
     static_assert(kChainDepth == 4, "the loop below expands four chunk steps");
     for (int c0 = 0; c0 < nch; c0 += kChainDepth) {
-        LAMD_CHAIN_STEP(0)
-        LAMD_CHAIN_STEP(1)
-        LAMD_CHAIN_STEP(2)
-        LAMD_CHAIN_STEP(3)
+        LAMD_CHAIN_STEP(0, 1)
+        LAMD_CHAIN_STEP(1, 2)
+        LAMD_CHAIN_STEP(2, 3)
+        LAMD_CHAIN_STEP(3, 0)
     }
 #undef LAMD_CHAIN_STEP
+#undef LAMD_CHAIN_PRODUCTS
+#undef LAMD_CHAIN_PR
 #undef LAMD_CHAIN_ISSUE
 #undef LAMD_CHAIN_LD
-    if (tid == es_lane) es_sh = es;
+    __shared__ double es_sh;
+    if (tid == DG) es_sh = sum;
     __syncthreads();
     if (tid < DG) orow[tid] = sum / es_sh;
 }

@@ -174,62 +174,47 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(b, 63));
 }
 
-// Sum of n fp64 terms in index order (one lane): terms are read from LDS
-// sixteen at a time ahead of the dependent additions (each addition waits
-// only for its own read: LDS reads return in order).
-__device__ __forceinline__ double ordered_sum(const double* t, int n, double s) {
-    int i = 0;
-    for (; i + 16 <= n; i += 16) {
-        double v[16];
+// s + p[base] + ... + p[base + 15] in index order, the terms past n replaced
+// by -0 (s + -0 = s for every s).
+__device__ __forceinline__ double add_block16(const double2 (&v)[8], int base, int n, double s) {
+    if (base + 16 <= n) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) v[j] = t[i + j];
+        for (int j = 0; j < 8; ++j) {
+            s = s + v[j].x;
+            s = s + v[j].y;
+        }
+    } else {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) s += v[j];
+        for (int j = 0; j < 8; ++j) {
+            s = s + (base + 2 * j < n ? v[j].x : -0.0);
+            s = s + (base + 2 * j + 1 < n ? v[j].y : -0.0);
+        }
     }
-    for (; i < n; ++i) s += t[i];
     return s;
 }
 
-// sum over k in index order of p[k] * (double)v[k * vs] (LDS operands; a
-// product, then a sum, each rounded).  Blocks of 16 terms, double-buffered:
-// the reads of block b + 1 are issued before the additions of block b (the
-// block read after the last full one is clamped to an existing block rather
-// than guarded by a branch).
-__device__ __forceinline__ double ordered_dot(const double* p, const float* v, int vs, int n, double s) {
-    constexpr int B = 16;
-    const int nb = n / B;
-    if (nb > 0) {
-        double a[B], c[B];
-        float b[B], d[B];
+// s + p[0] + p[1] + ... + p[n-1] in index order (one lane; p in LDS, 16-byte
+// aligned, C doubles readable, n <= C), two terms per 16-byte read, with the
+// reads of four blocks of sixteen terms in flight ahead of the additions
+// (reads past n are never added).
+template <int C>
+__device__ __forceinline__ double chain_add_pairs(const double* p, int n, double s) {
+    static_assert(C % 16 == 0, "blocks of sixteen terms");
+    const double2* p2 = (const double2*)p;
+    constexpr int NB = C / 16, D = NB < 4 ? NB : 4;
+    double2 v[D][8];
 #pragma unroll
-        for (int j = 0; j < B; ++j) {
-            a[j] = p[j];
-            b[j] = v[j * vs];
-        }
-        int blk = 0;
-        for (; blk + 2 <= nb; blk += 2) {
-            const int o1 = (blk + 1) * B, o2 = min(blk + 2, nb - 1) * B;
+    for (int b = 0; b < D; ++b)
 #pragma unroll
-            for (int j = 0; j < B; ++j) {
-                c[j] = p[o1 + j];
-                d[j] = v[(o1 + j) * vs];
-            }
+        for (int j = 0; j < 8; ++j) v[b][j] = p2[b * 8 + j];
 #pragma unroll
-            for (int j = 0; j < B; ++j) s += a[j] * (double)b[j];
+    for (int b = 0; b < NB; ++b) {
+        if (b * 16 < n) s = add_block16(v[b % D], b * 16, n, s);
+        if (b + D < NB) {
 #pragma unroll
-            for (int j = 0; j < B; ++j) {
-                a[j] = p[o2 + j];
-                b[j] = v[(o2 + j) * vs];
-            }
-#pragma unroll
-            for (int j = 0; j < B; ++j) s += c[j] * (double)d[j];
-        }
-        if (blk < nb) {
-#pragma unroll
-            for (int j = 0; j < B; ++j) s += a[j] * (double)b[j];
+            for (int j = 0; j < 8; ++j) v[b % D][j] = p2[(b + D) * 8 + j];
         }
     }
-    for (int i = nb * B; i < n; ++i) s += p[i] * (double)v[i * vs];
     return s;
 }
 
