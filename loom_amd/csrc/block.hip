@@ -48,7 +48,7 @@ __device__ __forceinline__ double lds_sum(double* terms, int n, double* scratch2
 // rows the fp64 squares are exact; for fp64 rows each square is rounded
 // before its addition, as the reference computes it.
 // ------------------------------------------------------------------------
-constexpr int kRowChainMinRows = 256;  // below this the per-row kernels keep their own chain
+constexpr int kRowChainMinRows = 1024;  // below this the per-row kernels form each row's sum themselves
 
 template <typename T>
 __global__ __launch_bounds__(64) void row_sumsq_kernel(const T* __restrict__ x, long ldx, int n, int m,

@@ -272,6 +272,26 @@ def test_norm_quant_strict_bit_exact(orc, torch_dev, bn, n):
             assert np.float32(q.amax[i].item()) == np.float32(eamax)
 
 
+@pytest.mark.parametrize("M", [300, 1100])
+def test_norm_quant_strict_many_rows(orc, torch_dev, bn, M):
+    # below 1024 rows each workgroup forms its row's ordered sum of squares
+    # (the workgroup-parallel exact form); from 1024 rows one lane per row
+    # adds the row in order.  Sampled rows, bit-exact against the oracle.
+    torch = torch_dev
+    n = 2560
+    h = orc.normal_f32(M * n, seed=M + 7).reshape(M, n) * np.float32(2.0)
+    h[:, ::97] *= np.float32(40.0)  # a few large values per row
+    hd = to_dev(torch, h.copy())
+    q = bn.norm_quant_rows(hd, None, eps=1e-5, norm="strict")
+    torch.cuda.synchronize()
+    got = hd.cpu().numpy()
+    qn = q.unpadded().cpu().numpy()
+    for i in sorted({0, 1, M // 2, M - 2, M - 1} | set(range(3, M, 61))):
+        want = orc.bitnet_rmsnorm_row(h[i], None, 1e-5)
+        assert got[i].tobytes() == want.tobytes(), f"row {i} normalized values"
+        assert np.array_equal(qn[i], orc.quant_act(want)[0]), f"row {i} codes"
+
+
 def test_norm_quant_fast_within_one_ulp(orc, torch_dev, bn):
     torch = torch_dev
     n, M = 6912, 16
