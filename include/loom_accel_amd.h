@@ -332,6 +332,7 @@ void loom_amd_model_release(loom_amd_model* m);
 /* Prefill: restart every sequence with batch x n prompt ids (HOST), run the
  * stack, the final norm and the LM head on each sequence's last row, and
  * pick the next token greedily (SampleTopK with k<=1, poly/sampling.go:44-55).
+ * The ids are copied out of the caller's memory before the call returns.
  * logits (DEVICE, batch x vocab) is optional. */
 int loom_amd_model_prefill(loom_amd_model* m, const int32_t* ids, int batch, int n,
                            float* logits, void* stream);
@@ -345,7 +346,8 @@ int loom_amd_model_decode(loom_amd_model* m, int steps, int use_graph, float* lo
                           void* stream);
 
 /* Copy the tokens of every sequence (HOST, batch x count: prompt then
- * generated ids).  Synchronous on stream.  count = current position + 1. */
+ * generated ids).  Waits for stream; `out` holds the ids when the call
+ * returns.  count = current position + 1. */
 int loom_amd_model_tokens(const loom_amd_model* m, int32_t* out, int count, void* stream);
 
 /* Current position (tokens fed through the stack per sequence). */

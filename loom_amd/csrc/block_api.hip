@@ -487,6 +487,12 @@ struct loom_amd_model {
     float2* argmax_part = nullptr;  // max_batch x kArgmaxMaxParts
     int* pos = nullptr;           // device position shared by every layer
     void* misc = nullptr;
+    // Pinned staging for the ids that cross the boundary (prompt upload,
+    // token read-back): copies from pageable memory need not have finished
+    // when the call that queued them returns.  ids_sent marks the last upload
+    // out of it, so neither the next upload nor a read-back overwrites it early.
+    int32_t* host_ids = nullptr;  // max_batch x max_tokens
+    hipEvent_t ids_sent = nullptr;
     int batch = 0;                // batch of the current sequences
     int shadow = 0;               // host copy of the position
     hipStream_t own = nullptr;
@@ -622,6 +628,8 @@ static void free_model(loom_amd_model* m) {
     for (auto& L : m->layers) free_block(&L);
     free_workspace(&m->ws);
     if (m->misc) (void)hipFree(m->misc);
+    if (m->host_ids) (void)hipHostFree(m->host_ids);
+    if (m->ids_sent) (void)hipEventDestroy(m->ids_sent);
     if (m->own) (void)hipStreamDestroy(m->own);
     if (m->lm_ternary) loom_amd_matrix_release(m->lm_ternary);
     delete m;
@@ -704,6 +712,11 @@ int loom_amd_model_create(int device, const loom_amd_model_desc* desc,
     if (e == hipSuccess) e = hipMemset(m->tokens, 0, (size_t)max_batch * max_tokens * 4);
     if (e == hipSuccess) e = hipMemset(m->pos, 0, sizeof(int));
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&m->own, hipStreamNonBlocking);
+    if (e == hipSuccess) {
+        e = hipHostMalloc((void**)&m->host_ids, (size_t)max_batch * max_tokens * 4,
+                          hipHostMallocDefault);
+    }
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ids_sent, hipEventDisableTiming);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         free_model(m);
@@ -789,11 +802,17 @@ int loom_amd_model_prefill(loom_amd_model* m, const int32_t* ids, int batch, int
     if (m->layers_n > 0 && n > m->layers[0].span()) return fail("prompt longer than max_seq_len");
     DeviceGuard guard(m->device);
     hipStream_t s = (hipStream_t)stream;
-    hipError_t e = launch_set_int(m->pos, 0, s);
+    // the previous upload out of host_ids must have left it before it is refilled
+    hipError_t e = hipEventSynchronize(m->ids_sent);
     if (e == hipSuccess) {
-        e = hipMemcpy2DAsync(m->tokens, (size_t)m->max_tokens * 4, ids, (size_t)n * 4, (size_t)n * 4,
-                             batch, hipMemcpyHostToDevice, s);
+        memcpy(m->host_ids, ids, (size_t)batch * n * 4);
+        e = launch_set_int(m->pos, 0, s);
     }
+    if (e == hipSuccess) {
+        e = hipMemcpy2DAsync(m->tokens, (size_t)m->max_tokens * 4, m->host_ids, (size_t)n * 4,
+                             (size_t)n * 4, batch, hipMemcpyHostToDevice, s);
+    }
+    if (e == hipSuccess) e = hipEventRecord(m->ids_sent, s);
     if (e == hipSuccess) {
         e = launch_embed(m->embeddings, m->vocab, m->hidden, m->tokens, m->max_tokens, m->pos, batch,
                          n, m->x, s);
@@ -892,11 +911,17 @@ int loom_amd_model_tokens(const loom_amd_model* m, int32_t* out, int count, void
     if (count <= 0 || count > m->max_tokens) return fail("count out of range");
     DeviceGuard guard(m->device);
     hipStream_t s = (hipStream_t)stream;
-    hipError_t e = hipMemcpy2DAsync(out, (size_t)count * 4, m->tokens, (size_t)m->max_tokens * 4,
-                                    (size_t)count * 4, m->batch > 0 ? m->batch : 1,
-                                    hipMemcpyDeviceToHost, s);
+    const int rows = m->batch > 0 ? m->batch : 1;
+    // through the pinned buffer: the copy has landed once the stream is idle
+    hipError_t e = hipEventSynchronize(m->ids_sent);
+    if (e == hipSuccess) {
+        e = hipMemcpy2DAsync(m->host_ids, (size_t)count * 4, m->tokens, (size_t)m->max_tokens * 4,
+                             (size_t)count * 4, rows, hipMemcpyDeviceToHost, s);
+    }
     if (e == hipSuccess) e = hipStreamSynchronize(s);
-    return e == hipSuccess ? 0 : fail_hip("model tokens", e);
+    if (e != hipSuccess) return fail_hip("model tokens", e);
+    memcpy(out, m->host_ids, (size_t)rows * count * 4);
+    return 0;
 }
 
 int loom_amd_model_position(const loom_amd_model* m) { return m ? m->shadow : -1; }

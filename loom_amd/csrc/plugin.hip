@@ -37,6 +37,10 @@ struct loom_accel_compiled_layer {
     float* d_norm = nullptr;
     float* d_in = nullptr;
     float* d_out = nullptr;
+    // pinned staging of the caller's host buffers: copies between pageable
+    // memory and the device need not have finished when they are queued
+    void* h_in = nullptr;
+    void* h_out = nullptr;
     hipStream_t stream = nullptr;
     size_t in_bytes = 0, out_bytes = 0;
 };
@@ -178,6 +182,8 @@ void release(loom_accel_compiled_layer* l) {
     if (l->d_norm) (void)hipFree(l->d_norm);
     if (l->d_in) (void)hipFree(l->d_in);
     if (l->d_out) (void)hipFree(l->d_out);
+    if (l->h_in) (void)hipHostFree(l->h_in);
+    if (l->h_out) (void)hipHostFree(l->h_out);
     if (l->stream) (void)hipStreamDestroy(l->stream);
     if (prev >= 0) (void)hipSetDevice(prev);
     delete l;
@@ -332,6 +338,8 @@ int loom_accel_compile_layer(loom_accel_plugin* plugin, const loom_accel_layer_d
     hipError_t e = hipStreamCreateWithFlags(&l->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipMalloc(&l->d_in, l->in_bytes);
     if (e == hipSuccess) e = hipMalloc(&l->d_out, l->out_bytes);
+    if (e == hipSuccess) e = hipHostMalloc(&l->h_in, l->in_bytes, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipHostMalloc(&l->h_out, l->out_bytes, hipHostMallocDefault);
     if (e == hipSuccess && s.kind == 1 && left == (size_t)s.n * 4) {
         e = hipMalloc(&l->d_norm, left);
         if (e == hipSuccess) e = hipMemcpy(l->d_norm, p, left, hipMemcpyHostToDevice);
@@ -401,7 +409,10 @@ int loom_accel_infer(loom_accel_compiled_layer* layer, const void* in, size_t in
     }
     const auto t0 = Clock::now();
     std::lock_guard<std::mutex> lock(lamd::device_mutex(layer->device));
-    hipError_t e = hipMemcpyAsync(layer->d_in, in, in_bytes, hipMemcpyHostToDevice, layer->stream);
+    // run() leaves the stream idle, so the previous call's copies are done
+    memcpy(layer->h_in, in, in_bytes);
+    hipError_t e = hipMemcpyAsync(layer->d_in, layer->h_in, in_bytes, hipMemcpyHostToDevice,
+                                  layer->stream);
     if (e != hipSuccess) {
         set_err(err, err_len, std::string("infer upload: ") + hipGetErrorString(e));
         return -1;
@@ -411,12 +422,13 @@ int loom_accel_infer(loom_accel_compiled_layer* layer, const void* in, size_t in
         set_err(err, err_len, why);
         return -1;
     }
-    e = hipMemcpyAsync(out, layer->d_out, out_bytes, hipMemcpyDeviceToHost, layer->stream);
+    e = hipMemcpyAsync(layer->h_out, layer->d_out, out_bytes, hipMemcpyDeviceToHost, layer->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(layer->stream);
     if (e != hipSuccess) {
         set_err(err, err_len, std::string("infer download: ") + hipGetErrorString(e));
         return -1;
     }
+    memcpy(out, layer->h_out, out_bytes);
     if (infer_ms) *infer_ms = ms_since(t0);
     return 0;
 }
