@@ -1124,8 +1124,8 @@ __global__ __launch_bounds__(256) void attn_tile_mfma_kernel(const double* __res
 }
 
 // ---- decode path (few query rows) ----------------------------------------
-// Scratch layout per (row, head): scores[span] (strict path: probabilities
-// after the exp step), chunk maxima cmax[nchunk] (64 positions per chunk), and
+// Scratch layout per (row, head): scores[span], chunk maxima cmax[nchunk]
+// (64 positions per chunk on the strict path, 32 on the fast GQA path), and
 // for the fast path the chunk-local partial sums part[nchunk][hd] and partial
 // expSums pes[nchunk].
 
@@ -1137,75 +1137,6 @@ struct DecodeScratch {
 };
 
 __host__ __device__ inline int attn_nchunk(int span) { return (span + 63) / 64; }
-
-// part 1: scores for 64 positions per wave of one head, and the maximum of
-// each 64-position chunk.  q is wave-uniform, so it is read through the
-// scalar cache; each lane reads its K row (128 floats at a time, all loads
-// issued before the chain).  grid (heads, nchunk, rows)
-__global__ __launch_bounds__(64) void attn_scores_kernel(const double* __restrict__ q,
-                                                         const float* __restrict__ cache_k,
-                                                         const int* __restrict__ pos0, int msl,
-                                                         int span, int heads, int kv_heads, int hd,
-                                                         int seq, DecodeScratch sc) {
-    const int h = blockIdx.x, row = blockIdx.z;
-    const int kvh = h / (heads / kv_heads);
-    const int b = row / seq, s = row % seq;
-    const int q_dim = heads * hd, kv_dim = kv_heads * hd;
-    const int L = min(*pos0 + s + 1, span);
-    const int chunk = blockIdx.y;
-    if (chunk * 64 >= L) return;  // uniform over the workgroup
-    const double* qr = q + (size_t)row * q_dim + (size_t)h * hd;
-    const int kp = chunk * 64 + threadIdx.x;
-    const int nchunk = attn_nchunk(span);
-    double dot = 0.0;
-    if (kp < L) {
-        const float* kr = cache_k + (size_t)b * msl * kv_dim + (size_t)kp * kv_dim + (size_t)kvh * hd;
-        for (int d0 = 0; d0 < hd; d0 += 128) {
-            const int n4 = min(32, (hd - d0) >> 2);
-            float4 kk[32];
-#pragma unroll
-            for (int i = 0; i < 32; ++i)
-                if (i < n4) kk[i] = *(const float4*)(kr + d0 + 4 * i);
-#pragma unroll
-            for (int i = 0; i < 32; ++i) {
-                if (i < n4) {
-                    const int d = d0 + 4 * i;
-                    dot += qr[d] * (double)kk[i].x;
-                    dot += qr[d + 1] * (double)kk[i].y;
-                    dot += qr[d + 2] * (double)kk[i].z;
-                    dot += qr[d + 3] * (double)kk[i].w;
-                }
-            }
-        }
-    }
-    const size_t rh = (size_t)row * heads + h;
-    double m = -1e9;
-    if (kp < L) {
-        const double v = dot * (1.0 / sqrt((double)hd));
-        sc.scores[rh * span + kp] = v;
-        m = v;
-    }
-    // chunk maximum (exact in any order; NaN never wins)
-    for (int off = 32; off > 0; off >>= 1) {
-        const double o = __shfl_xor(m, off, 64);
-        m = o > m ? o : m;
-    }
-    if (threadIdx.x == 0) sc.cmax[rh * nchunk + chunk] = m;
-}
-
-// maximum over the chunk maxima of (row, head): -1e9 start, NaN never wins
-__device__ __forceinline__ double global_max(const double* cm, int nc, double* red64) {
-    double m = -1e9;
-    for (int c = threadIdx.x; c < nc; c += 64) {
-        const double v = cm[c];
-        m = v > m ? v : m;
-    }
-    for (int off = 32; off > 0; off >>= 1) {
-        const double o = __shfl_xor(m, off, 64);
-        m = o > m ? o : m;
-    }
-    return m;
-}
 
 // ---- fast decode attention for head_dim 64 / 128 ------------------------------
 // Part 1: one workgroup per (KV head, 32-position chunk, row) serves every
@@ -1232,6 +1163,153 @@ struct RopeArgs {
     double theta;
     double* q_tap;  // debug tap: Q rows after bias and RoPE (rows x q_dim), written by chunk 0
 };
+
+// strict part 1: the scores of one 64-position chunk for every query head of
+// one KV head, and each head's chunk maximum.  The chunk's K rows are copied
+// to LDS with coalesced loads (pitch HD + 2 floats: the lanes' row reads fall
+// in different banks); wave w serves group members w, w + 4, ...; lane i owns
+// position k0 + i and forms q . k in dimension order, one rounded product and
+// one rounded sum per dimension (the reference's `dot += q[d] * k[d]`), then
+// scales it by 1 / sqrt(hd).  ROPE (one token per sequence): Q comes from the
+// stacked projection accumulators by the Q/K/V epilogue steps of
+// qkv_rope_kernel (each lane computes the rotation angle of its own pair), and
+// the workgroup whose chunk holds the new position writes that position's K
+// and V rows to the cache and takes the K row into LDS itself.  No other
+// workgroup reads that row.  grid (kv_heads, nchunk, rows), 256 threads.
+template <int HD, bool ROPE>
+__global__ __launch_bounds__(256) void attn_scores_gqa_kernel(const double* __restrict__ q,
+                                                              float* cache_k, float* cache_v,
+                                                              const int* __restrict__ pos0, int msl,
+                                                              int span, int heads, int kv_heads,
+                                                              int seq, DecodeScratch sc, RopeArgs ra) {
+    constexpr int CH = 64;
+    constexpr int KP = HD + 2;       // LDS row pitch (floats)
+    constexpr int PR4 = HD / 4;      // float4 per K row
+    constexpr int NK = CH * PR4 / 256;
+    constexpr int HALF = HD / 2;
+    constexpr int NA = (HALF + 63) / 64;  // rotation pairs per lane
+    static_assert(NK * 256 == CH * PR4, "chunk geometry");
+    __shared__ __align__(16) float ks[CH * KP];
+    __shared__ double qs[4][HD];
+    const int kvh = blockIdx.x, chunk = blockIdx.y, row = blockIdx.z;
+    const int G = heads / kv_heads;
+    const int b = row / seq, s = row % seq;
+    const int pos = *pos0 + s;
+    const int L = min(pos + 1, span);
+    const int k0 = chunk * CH;
+    if (k0 >= L) return;  // uniform over the workgroup
+    const int nchunk = attn_nchunk(span);
+    const int q_dim = heads * HD, kv_dim = kv_heads * HD;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const size_t cb = (size_t)b * msl * kv_dim + (size_t)kvh * HD;
+    // the chunk's K rows (rows past the length are read but never scored)
+    float4 kreg[NK];
+#pragma unroll
+    for (int j = 0; j < NK; ++j) {
+        const int i = tid + j * 256;
+        const int r = i / PR4, c4 = (i % PR4) * 4;
+        kreg[j] = *(const float4*)(cache_k + cb + (size_t)min(k0 + r, msl - 1) * kv_dim + c4);
+    }
+    const int32_t* ar = ROPE ? ra.acc + (size_t)row * (q_dim + 2 * kv_dim) : nullptr;
+    const bool newrow = ROPE && k0 <= pos && pos < k0 + CH;
+    double rcos[NA], rsin[NA];
+    double osq = 0.0;
+    if (ROPE) {
+        const float am = ra.amax[row];
+        osq = output_scale(ra.sq, am);
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+            const int d = lane + 64 * a;
+            rcos[a] = rsin[a] = 0.0;
+            if (d < HALF) rope_angle(pos, d, HD, ra.theta, &rcos[a], &rsin[a]);
+        }
+        if (newrow && wave == 0) {
+            // the new position's K pairs (lane d: d, d + HD/2) and V values
+            const double osk = output_scale(ra.sk, am), osv = output_scale(ra.sv, am);
+            float* krow = cache_k + (size_t)b * msl * kv_dim + (size_t)(pos % msl) * kv_dim + kvh * HD;
+            float* vrow = cache_v + (size_t)b * msl * kv_dim + (size_t)(pos % msl) * kv_dim + kvh * HD;
+            float* kl = ks + (pos - k0) * KP;
+#pragma unroll
+            for (int a = 0; a < NA; ++a) {
+                const int d = lane + 64 * a;
+                if (d < HALF) {
+                    float o0, o1;
+                    k_pair(ar + q_dim, osk, ra.bk, kvh * HD + d, kvh * HD + d + HALF, rcos[a], rsin[a],
+                           &o0, &o1);
+                    krow[d] = o0;
+                    krow[d + HALF] = o1;
+                    kl[d] = o0;
+                    kl[d + HALF] = o1;
+                }
+            }
+            for (int d = lane; d < HD; d += 64) vrow[d] = v_val(ar + q_dim + kv_dim, osv, ra.bv, kvh * HD + d);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NK; ++j) {
+        const int i = tid + j * 256;
+        const int r = i / PR4, c4 = (i % PR4) * 4;
+        if (!(newrow && k0 + r == pos)) {
+            float* kl = ks + r * KP + c4;
+            *(float2*)kl = make_float2(kreg[j].x, kreg[j].y);
+            *(float2*)(kl + 2) = make_float2(kreg[j].z, kreg[j].w);
+        }
+    }
+    const size_t rh0 = (size_t)row * heads;
+    const float* kr = ks + lane * KP;
+    const int kp = k0 + lane;
+    // rounds of four group members (uniform: every wave meets each barrier)
+    for (int m0 = 0; m0 < G; m0 += 4) {
+        const int member = m0 + wave;
+        const int h = kvh * G + member;
+        if (member < G) {
+            if (ROPE) {
+#pragma unroll
+                for (int a = 0; a < NA; ++a) {
+                    const int d = lane + 64 * a;
+                    if (d < HALF) {
+                        double o0, o1;
+                        q_pair(ar, osq, ra.bq, h * HD + d, h * HD + d + HALF, rcos[a], rsin[a], &o0, &o1);
+                        qs[wave][d] = o0;
+                        qs[wave][d + HALF] = o1;
+                        if (ra.q_tap && chunk == 0) {
+                            double* qt = ra.q_tap + (size_t)row * q_dim + (size_t)h * HD;
+                            qt[d] = o0;
+                            qt[d + HALF] = o1;
+                        }
+                    }
+                }
+            } else {
+                const double* qr = q + (size_t)row * q_dim + (size_t)h * HD;
+                for (int d = lane; d < HD; d += 64) qs[wave][d] = qr[d];
+            }
+        }
+        __syncthreads();  // K rows (first round) and this round's Q in LDS
+        if (member < G) {
+            double dot = 0.0;
+#pragma unroll 8
+            for (int d = 0; d < HD; d += 2) {
+                const float2 kk = *(const float2*)(kr + d);
+                dot += qs[wave][d] * (double)kk.x;
+                dot += qs[wave][d + 1] * (double)kk.y;
+            }
+            const size_t rh = rh0 + h;
+            double m = -1e9;
+            if (kp < L) {
+                const double v = dot * (1.0 / sqrt((double)HD));
+                sc.scores[rh * span + kp] = v;
+                m = v;
+            }
+            // chunk maximum (exact in any order; NaN never wins)
+            for (int off = 32; off > 0; off >>= 1) {
+                const double o = __shfl_xor(m, off, 64);
+                m = o > m ? o : m;
+            }
+            if (lane == 0) sc.cmax[rh * nchunk + chunk] = m;
+        }
+        __syncthreads();  // this round's Q reads are done before the next round's writes
+    }
+}
 
 template <int HD, bool ROPE>
 __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict__ q, float* cache_k,
@@ -1681,32 +1759,21 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const int* __restrict
     }
 }
 
-// strict part 2: probabilities in place of the scores; grid (heads, nchunk, rows), 64 threads
-__global__ __launch_bounds__(64) void attn_exp_kernel(const int* __restrict__ pos0, int span,
-                                                      int heads, int seq, DecodeScratch sc) {
-    const int h = blockIdx.x, chunk = blockIdx.y, row = blockIdx.z;
-    const int s = row % seq;
-    const int L = min(*pos0 + s + 1, span);
-    const int k = chunk * 64 + threadIdx.x;
-    if (chunk * 64 >= L) return;
-    const int nchunk = attn_nchunk(span);
-    const size_t rh = (size_t)row * heads + h;
-    const double m = global_max(sc.cmax + rh * nchunk, (L + 63) / 64, nullptr);
-    if (k < L) sc.scores[rh * span + k] = exp(sc.scores[rh * span + k] - m);
-}
-
-// strict part 3: one workgroup per (head, group of DG value columns, row).
-// Lane d <= DG of wave 0 adds column d of the products p[k] * v[k][d] in
-// position order (the reference's `sum += p * v`, a product then a sum, each
-// rounded); column DG holds p itself, whose chain is expSum.  Chunks of
-// C = 4096 / DG positions: every thread loads its 16 values of a chunk (and
-// the probabilities they need: C / 256 more for column DG) kChainDepth chunks
-// ahead, forms its products
-// in registers and writes them to one of two LDS product buffers, transposed
-// so that a chain lane reads two positions per 16-byte load; wave 0 adds chunk
-// c while the products of chunk c + 1 are written.  The loads are branch-free
-// (indices clamped into the ring and the score row; surplus values are never
-// added).  grid (heads * HD / DG, rows), 256 threads.
+// strict part 2: one workgroup per (head, group of DG value columns, row).
+// The probabilities p[k] = exp(score[k] - max) are formed here: the maximum
+// over the chunk maxima (every wave forms it), then one probability per thread
+// and 256-position chunk into an LDS ring two chunks deep.  Lane d <= DG of
+// wave 0 adds column d of the products p[k] * v[k][d] in position order (the
+// reference's `sum += p * v`, a product then a sum, each rounded); column DG
+// holds p itself, whose chain is expSum.  Chunks of C = 4096 / DG positions:
+// every thread loads its 16 values of a chunk (and the scores it turns into
+// probabilities: C / 256) kChainDepth chunks ahead, forms its products in
+// registers and writes them to one of two LDS product buffers, transposed so
+// that a chain lane reads two positions per 16-byte load; wave 0 adds chunk c
+// while the products of chunk c + 1 and the probabilities of chunk c + 2 are
+// written.  The loads are branch-free (indices clamped into the ring and the
+// score row; surplus values are never added).  grid (heads * HD / DG, rows),
+// 256 threads.
 constexpr int kChainDepth = 4;
 constexpr int kChainCols = 16;
 
@@ -1720,13 +1787,14 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(const float* __restrict
     constexpr int CP = C + 2;     // row pitch (16-byte aligned rows, lanes' reads in different banks)
     static_assert(C * DG == 4096 && C % 256 == 0 && C <= 512 && HD % DG == 0 && DG % 4 == 0,
                   "chunk geometry");
-    constexpr int PT = C / 256;   // probabilities of column DG per thread
+    constexpr int PT = C / 256;   // probabilities per thread and chunk
     __shared__ __align__(16) double prod[2][DG + 1][CP];
+    __shared__ double pr_sh[2][C];
     const int h = blockIdx.x / (HD / DG), dg = blockIdx.x % (HD / DG), row = blockIdx.y;
     const int b = row / seq, s = row % seq;
     const int kvh = h / (heads / kv_heads);
     const int q_dim = heads * HD, kv_dim = kv_heads * HD;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
     const int L = *pos0 + s + 1;
     double* orow = out + (size_t)row * q_dim + (size_t)h * HD + dg * DG;
     if (L > span) {
@@ -1735,24 +1803,22 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(const float* __restrict
     }
     const int nch = (L + C - 1) / C;
     const float* vb = cache_v + (size_t)b * msl * kv_dim + (size_t)kvh * HD + dg * DG;
-    const double* pr = sc.scores + ((size_t)row * heads + h) * span;
+    const size_t rh = (size_t)row * heads + h;
+    const double* sr = sc.scores + rh * span;
 
     // staging registers of the chunks in flight (named scalars filled by
     // macros: arrays of them, indexed in loops, were kept in scratch memory).
     // Thread tid holds the float4s at elements 4(tid + 256 I) of the chunk's
-    // C x DG values (position e / DG, column e % DG), the probabilities of
-    // those positions, and the probability of position tid (column DG).
+    // C x DG values (position e / DG, column e % DG) and the scores of
+    // positions tid + 256 q.
     float4 r0_0, r0_1, r0_2, r0_3, r1_0, r1_1, r1_2, r1_3;
     float4 r2_0, r2_1, r2_2, r2_3, r3_0, r3_1, r3_2, r3_3;
-    double p0_0, p0_1, p0_2, p0_3, p1_0, p1_1, p1_2, p1_3;
-    double p2_0, p2_1, p2_2, p2_3, p3_0, p3_1, p3_2, p3_3;
     double pt0[PT], pt1[PT], pt2[PT], pt3[PT];
 #define LAMD_CHAIN_LD(U, I, CC)                                                   \
     {                                                                             \
         const int e = (tid + (I) * 256) * 4; /* element of the C x DG chunk */     \
         const int k = (CC) * C + e / DG;                                          \
         r##U##_##I = *(const float4*)(vb + (size_t)min(k, msl - 1) * kv_dim + e % DG); \
-        p##U##_##I = pr[min(k, span - 1)];                                        \
     }
 #define LAMD_CHAIN_ISSUE(U, CH)                                                   \
     {                                                                             \
@@ -1760,44 +1826,71 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(const float* __restrict
         LAMD_CHAIN_LD(U, 0, cc) LAMD_CHAIN_LD(U, 1, cc)                           \
         LAMD_CHAIN_LD(U, 2, cc) LAMD_CHAIN_LD(U, 3, cc)                           \
         _Pragma("unroll") for (int q = 0; q < PT; ++q)                            \
-            pt##U[q] = pr[min(cc * C + tid + 256 * q, span - 1)];                 \
+            pt##U[q] = sr[min(cc * C + tid + 256 * q, span - 1)];                 \
+    }
+#define LAMD_CHAIN_EXP(U, BUF)                                                    \
+    {                                                                             \
+        _Pragma("unroll") for (int q = 0; q < PT; ++q)                            \
+            pr_sh[BUF][tid + 256 * q] = exp(pt##U[q] - mx);                       \
     }
 #define LAMD_CHAIN_PR(U, I, BUF)                                                  \
     {                                                                             \
         const int e = (tid + (I) * 256) * 4;                                      \
         const int k = e / DG, d = e % DG;                                         \
-        prod[BUF][d][k] = p##U##_##I * (double)r##U##_##I.x;                      \
-        prod[BUF][d + 1][k] = p##U##_##I * (double)r##U##_##I.y;                  \
-        prod[BUF][d + 2][k] = p##U##_##I * (double)r##U##_##I.z;                  \
-        prod[BUF][d + 3][k] = p##U##_##I * (double)r##U##_##I.w;                  \
+        const double p = pr_sh[BUF][k];                                           \
+        prod[BUF][d][k] = p * (double)r##U##_##I.x;                               \
+        prod[BUF][d + 1][k] = p * (double)r##U##_##I.y;                           \
+        prod[BUF][d + 2][k] = p * (double)r##U##_##I.z;                           \
+        prod[BUF][d + 3][k] = p * (double)r##U##_##I.w;                           \
     }
 #define LAMD_CHAIN_PRODUCTS(U, BUF)                                               \
     {                                                                             \
         LAMD_CHAIN_PR(U, 0, BUF) LAMD_CHAIN_PR(U, 1, BUF)                         \
         LAMD_CHAIN_PR(U, 2, BUF) LAMD_CHAIN_PR(U, 3, BUF)                         \
         _Pragma("unroll") for (int q = 0; q < PT; ++q)                            \
-            prod[BUF][DG][tid + 256 * q] = pt##U[q];                              \
+            prod[BUF][DG][tid + 256 * q] = pr_sh[BUF][tid + 256 * q];             \
     }
     LAMD_CHAIN_ISSUE(0, 0)
     LAMD_CHAIN_ISSUE(1, 1)
     LAMD_CHAIN_ISSUE(2, 2)
     LAMD_CHAIN_ISSUE(3, 3)
+    // maximum over the chunk maxima of the 64-position score chunks with
+    // data: -1e9 start, NaN never wins (each wave forms the same value)
+    double mx = -1e9;
+    {
+        const double* cm = sc.cmax + rh * attn_nchunk(span);
+        const int nc = (L + 63) / 64;
+        for (int c = lane; c < nc; c += 64) {
+            const double v = cm[c];
+            mx = v > mx ? v : mx;
+        }
+        for (int off = 32; off > 0; off >>= 1) {
+            const double o = __shfl_xor(mx, off, 64);
+            mx = o > mx ? o : mx;
+        }
+    }
+    LAMD_CHAIN_EXP(0, 0)
+    LAMD_CHAIN_EXP(1, 1)
+    __syncthreads();
     LAMD_CHAIN_PRODUCTS(0, 0)
     LAMD_CHAIN_ISSUE(0, kChainDepth)
     __syncthreads();
 
     double sum = 0.0;  // column tid's chain (tid <= DG)
     // step for chunk c = c0 + U: the products of chunk c + 1 (staging set
-    // U + 1) go to buffer (c + 1) & 1 and that set is refilled, then wave 0
-    // adds chunk c from buffer c & 1 (both parities are compile-time: c0 is a
-    // multiple of four).  Products and loads run for every chunk's step, for
-    // chunks past the last one too (clamped indices; no chain reads them), so
-    // the loads of the next three chunks stay in flight across each wait.
-#define LAMD_CHAIN_STEP(U, UN)                                                    \
+    // U + 1) go to buffer (c + 1) & 1 and that set is refilled, the
+    // probabilities of chunk c + 2 (set UE) go to ring slot c & 1, then wave 0
+    // adds chunk c from buffer c & 1 (all parities are compile-time: c0 is a
+    // multiple of four).  Products, probabilities and loads run for every
+    // chunk's step, for chunks past the last one too (clamped indices; no
+    // chain reads them), so the loads of the next three chunks stay in flight
+    // across each wait.
+#define LAMD_CHAIN_STEP(U, UN, UE)                                                \
     {                                                                             \
         const int c = c0 + (U);                                                   \
         if (c >= nch) break;                                                      \
         LAMD_CHAIN_PRODUCTS(UN, ((U) + 1) & 1)                                    \
+        LAMD_CHAIN_EXP(UE, (U) & 1)                                               \
         LAMD_CHAIN_ISSUE(UN, c + 1 + kChainDepth)                                 \
         if (c < nch && tid <= DG) {                                               \
             const double* pc = prod[(U) & 1][tid];                                \
@@ -1808,14 +1901,15 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(const float* __restrict
     }
     static_assert(kChainDepth == 4, "the loop below expands four chunk steps");
     for (int c0 = 0; c0 < nch; c0 += kChainDepth) {
-        LAMD_CHAIN_STEP(0, 1)
-        LAMD_CHAIN_STEP(1, 2)
-        LAMD_CHAIN_STEP(2, 3)
-        LAMD_CHAIN_STEP(3, 0)
+        LAMD_CHAIN_STEP(0, 1, 2)
+        LAMD_CHAIN_STEP(1, 2, 3)
+        LAMD_CHAIN_STEP(2, 3, 0)
+        LAMD_CHAIN_STEP(3, 0, 1)
     }
 #undef LAMD_CHAIN_STEP
 #undef LAMD_CHAIN_PRODUCTS
 #undef LAMD_CHAIN_PR
+#undef LAMD_CHAIN_EXP
 #undef LAMD_CHAIN_ISSUE
 #undef LAMD_CHAIN_LD
     __shared__ double es_sh;
@@ -1860,21 +1954,65 @@ static DecodeScratch decode_scratch(double* base, int rows, int heads, int hd, i
     return sc;
 }
 
+// Strict decode attention: scores (with the Q/K/V epilogue when ra.acc is
+// set), then probabilities with the value and expSum chains.
+static hipError_t launch_strict_decode(const double* q, float* cache_k, float* cache_v,
+                                       const int* pos0, int msl, int span, int heads, int kv_heads,
+                                       int hd, int seq, int rows, const DecodeScratch& sc,
+                                       const RopeArgs& ra, double* out, hipStream_t s) {
+    const int nc = attn_nchunk(span);
+    const dim3 gs(kv_heads, nc, rows), t(256);
+    constexpr int DG = kChainCols;
+#define LAMD_SCORES(HDV)                                                                          \
+    {                                                                                             \
+        if (ra.acc)                                                                               \
+            hipLaunchKernelGGL((attn_scores_gqa_kernel<HDV, true>), gs, t, 0, s, q, cache_k, cache_v, \
+                               pos0, msl, span, heads, kv_heads, seq, sc, ra);                    \
+        else                                                                                      \
+            hipLaunchKernelGGL((attn_scores_gqa_kernel<HDV, false>), gs, t, 0, s, q, cache_k,       \
+                               cache_v, pos0, msl, span, heads, kv_heads, seq, sc, ra);           \
+    }
+#define LAMD_CHAIN(HDV)                                                                              \
+    hipLaunchKernelGGL((attn_chain_kernel<HDV, DG>), dim3(heads * (HDV / DG), rows), t, 0, s, cache_v, pos0, \
+                       msl, span, heads, kv_heads, seq, sc, out)
+    switch (hd) {
+        case 32: LAMD_SCORES(32); break;
+        case 64: LAMD_SCORES(64); break;
+        case 128: LAMD_SCORES(128); break;
+        default: LAMD_SCORES(256); break;
+    }
+    switch (hd) {
+        case 32: LAMD_CHAIN(32); break;
+        case 64: LAMD_CHAIN(64); break;
+        case 128: LAMD_CHAIN(128); break;
+        default: LAMD_CHAIN(256); break;
+    }
+#undef LAMD_CHAIN
+#undef LAMD_SCORES
+    return hipGetLastError();
+}
+
 bool attention_rope_ok(int seq, int hd, int strict, int span) {
-    return !strict && seq == 1 && (hd == 64 || hd == 128) && span <= kMaxAttnSpan;
+    if (seq != 1 || span > kMaxAttnSpan) return false;
+    return strict ? (hd == 32 || hd == 64 || hd == 128 || hd == 256) : (hd == 64 || hd == 128);
 }
 
 hipError_t launch_attention_rope(const int32_t* acc, const float* amax, float sq, float sk, float sv,
                                  const float* bq, const float* bk, const float* bv, double theta,
                                  int batch, const int* pos0, int msl, int span, int heads,
-                                 int kv_heads, int hd, float* cache_k, float* cache_v,
+                                 int kv_heads, int hd, int strict, float* cache_k, float* cache_v,
                                  double* scratch, double* out, hipStream_t s, double* q_tap) {
     if (batch <= 0) return hipSuccess;
-    if (!attention_rope_ok(1, hd, 0, span) || span > msl || !scratch) return hipErrorInvalidValue;
+    if (!attention_rope_ok(1, hd, strict, span) || span > msl || !scratch || !acc)
+        return hipErrorInvalidValue;
     if (kv_heads <= 0 || heads % kv_heads != 0 || batch > kSplitMaxRows) return hipErrorInvalidValue;
     if (theta <= 0.0) theta = 10000.0;
     const DecodeScratch sc = decode_scratch(scratch, batch, heads, hd, span);
     const RopeArgs ra{acc, amax, sq, sk, sv, bq, bk, bv, theta, q_tap};
+    if (strict) {
+        return launch_strict_decode(nullptr, cache_k, cache_v, pos0, msl, span, heads, kv_heads, hd, 1,
+                                    batch, sc, ra, out, s);
+    }
     const dim3 g(kv_heads, attn_nchunk32(span), batch), gc(heads, hd / 32, batch);
     if (hd == 128) {
         hipLaunchKernelGGL((attn_gqa_kernel<128, true>), g, dim3(256), 0, s, nullptr, cache_k, cache_v,
@@ -1924,22 +2062,10 @@ hipError_t launch_attention(const double* q, const float* cache_k, const float* 
             hipLaunchKernelGGL(attn_combine_kernel, dim3(heads, rows), dim3(256), 0, s, pos0, span,
                                heads, hd, seq, sc, out);
         } else {
-            hipLaunchKernelGGL(attn_scores_kernel, dim3(heads, nc, rows), dim3(64), 0, s, q, cache_k,
-                               pos0, msl, span, heads, kv_heads, hd, seq, sc);
-            hipLaunchKernelGGL(attn_exp_kernel, dim3(heads, nc, rows), dim3(64), 0, s, pos0, span,
-                               heads, seq, sc);
-            constexpr int DG = kChainCols;
-            const dim3 t(256);
-#define LAMD_CHAIN(HDV)                                                                              \
-    hipLaunchKernelGGL((attn_chain_kernel<HDV, DG>), dim3(heads * (HDV / DG), rows), t, 0, s, cache_v, pos0, \
-                       msl, span, heads, kv_heads, seq, sc, out)
-            switch (hd) {
-                case 32: LAMD_CHAIN(32); break;
-                case 64: LAMD_CHAIN(64); break;
-                case 128: LAMD_CHAIN(128); break;
-                default: LAMD_CHAIN(256); break;
-            }
-#undef LAMD_CHAIN
+            const RopeArgs none{};
+            return launch_strict_decode(q, const_cast<float*>(cache_k), const_cast<float*>(cache_v),
+                                        pos0, msl, span, heads, kv_heads, hd, seq, rows, sc, none, out,
+                                        s);
         }
         return hipGetLastError();
     }

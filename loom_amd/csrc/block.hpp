@@ -41,14 +41,14 @@ size_t attention_lds_bytes(int hd, int span);
 size_t attention_scratch_bytes(int rows, int heads, int hd, int span, int strict, int fast_qt);
 // LOOM_AMD_ATTN_QT = 2 or 4 asks for the two-pass fast prefill kernel; 0 otherwise.
 int attention_fast_two_pass_qt();
-// Fast decode (one token per sequence, head_dim 64/128): the Q/K/V epilogue
-// of qkv_rope fused into the attention launch (writes the new K/V to the
-// caches, never materializes Q).
+// Decode (one token per sequence; head_dim 64/128 fast, 32/64/128/256
+// strict): the Q/K/V epilogue of qkv_rope fused into the attention launch
+// (writes the new K/V to the caches, never materializes Q).
 bool attention_rope_ok(int seq, int hd, int strict, int span);
 hipError_t launch_attention_rope(const int32_t* acc, const float* amax, float sq, float sk, float sv,
                                  const float* bq, const float* bk, const float* bv, double theta,
                                  int batch, const int* pos0, int msl, int span, int heads,
-                                 int kv_heads, int hd, float* cache_k, float* cache_v,
+                                 int kv_heads, int hd, int strict, float* cache_k, float* cache_v,
                                  double* scratch, double* out, hipStream_t s,
                                  double* q_tap = nullptr);
 hipError_t launch_attention(const double* q, const float* cache_k, const float* cache_v,

@@ -22,7 +22,7 @@ struct BlockDev {
     double theta = 10000.0, norm_eps = 0.0, attn_eps = 0.0, ffn_eps = 0.0;
     int activation = 1, strict = 1;
     int attn_qt = 0;  // fast prefill attention kernel (attention_fast_two_pass_qt at creation)
-    bool fuse_rope = true;  // fast decode: Q/K/V epilogue inside the attention launch
+    bool fuse_rope = true;  // decode: Q/K/V epilogue inside the attention launch
     bool fuse_norm = true;  // decode: row norms inside the consuming matmul
     Matrix qkv, o, gate, up, down;  // tiles point into `weights`
     float sq = 1.0f, sk = 1.0f, sv = 1.0f;
@@ -190,7 +190,7 @@ static int build_block(int device, const loom_amd_block_desc* d, const loom_amd_
     B->activation = d->ffn_activation;
     B->strict = d->norm_mode == LOOM_AMD_NORM_STRICT;
     B->attn_qt = attention_fast_two_pass_qt();
-    // LOOM_AMD_UNFUSED_ROPE=1 keeps the separate Q/K/V epilogue launch in fast
+    // LOOM_AMD_UNFUSED_ROPE=1 keeps the separate Q/K/V epilogue launch in
     // decode (the tests compare both paths)
     const char* unfused = getenv("LOOM_AMD_UNFUSED_ROPE");
     B->fuse_rope = !(unfused && unfused[0] == '1');
@@ -347,9 +347,10 @@ static int block_forward_dev(const BlockDev& B, const Workspace& W, float* x, in
         TAP(tap_copy(T.amax1, W.amax, (size_t)R * 4, s));
     }
     if (B.fuse_rope && batch <= kSplitMaxRows && attention_rope_ok(seq, B.hd, B.strict, B.span())) {
-        // fast decode: the Q/K/V epilogue runs inside the attention launch
+        // decode: the Q/K/V epilogue runs inside the attention launch
         e = launch_attention_rope(W.acc, W.amax, B.sq, B.sk, B.sv, B.bq, B.bk, B.bv, B.theta, batch, pos,
-                                  B.msl, B.span(), B.heads, B.kv_heads, B.hd, B.cache_k, B.cache_v,
+                                  B.msl, B.span(), B.heads, B.kv_heads, B.hd, B.strict, B.cache_k,
+                                  B.cache_v,
                                   W.scores, W.attn, s, T.q);
         if (e != hipSuccess) return fail_hip("block attention", e);
     } else {

@@ -43,7 +43,7 @@ __device__ __forceinline__ double wave_sum_f64_lane0(double v) {
 // FV: element groups (4 values) per thread.
 template <int NMAT, int MSUB, int WAVES, bool FUSEQ, int NORM = NORM_NONE, int STRICT = 0,
           int FV = kFusedVec, int MR = kFusedMaxRows>
-__global__ __launch_bounds__(WAVES * 64) void skinny_kernel(MatArgs p) {
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2))) void skinny_kernel(MatArgs p) {
     constexpr int T = WAVES * 64;
     constexpr int U = 4 / MSUB;  // K tiles per batch per wave
     extern __shared__ __align__(16) int8_t xq_s[];  // FUSEQ: M rows x ldq (STRICT: k squares first)

@@ -423,21 +423,24 @@ def test_greedy_sample_semantics(orc, torch_dev, tf):
         assert got == orc.argmax_first(row), m
 
 
-@pytest.mark.parametrize("shape", ["small", "bitnet2b"])
-def test_fast_decode_rope_fused_attention(orc, torch_dev, tf, shape, monkeypatch):
-    # Fast single-token decode runs the Q/K/V epilogue (RoPE, K/V cache write)
-    # inside the attention launch; with LOOM_AMD_UNFUSED_ROPE=1 a block keeps
-    # the separate epilogue kernel.  Same steps, so outputs and caches agree
-    # bit for bit, over batch 2 and several positions.
+@pytest.mark.parametrize("shape,norm", [("small", "fast"), ("bitnet2b", "fast"),
+                                        ("small", "strict"), ("bitnet2b", "strict"),
+                                        ("mha32", "strict")])
+def test_decode_rope_fused_attention(orc, torch_dev, tf, shape, norm, monkeypatch):
+    # Single-token decode runs the Q/K/V epilogue (RoPE, K/V cache write)
+    # inside the attention launch (fast: the GQA chunk kernel; strict: the
+    # scores kernel); with LOOM_AMD_UNFUSED_ROPE=1 a block keeps the separate
+    # epilogue kernel.  Same steps, so outputs and caches agree bit for bit,
+    # over batch 2 and several positions (past one 64-position chunk).
     torch = torch_dev
-    sh = SMALL if shape == "small" else BITNET_2B
+    sh = {"small": SMALL, "bitnet2b": BITNET_2B, "mha32": Shape(128, 4, 4, 32, 256, 128)}[shape]
     w = Weights(orc, sh, seed=1251, bias=True)
     gw = w.gpu(tf)
-    fused = tf.BitNetBlock(w.cfg(tf, "fast", max_batch=2), gw)
+    fused = tf.BitNetBlock(w.cfg(tf, norm, max_batch=2), gw)
     monkeypatch.setenv("LOOM_AMD_UNFUSED_ROPE", "1")
-    plain = tf.BitNetBlock(w.cfg(tf, "fast", max_batch=2), gw)
+    plain = tf.BitNetBlock(w.cfg(tf, norm, max_batch=2), gw)
     monkeypatch.delenv("LOOM_AMD_UNFUSED_ROPE")
-    for i, seq in enumerate([33, 1, 1, 1, 1]):
+    for i, seq in enumerate([min(62, sh.msl - 8), 1, 1, 1, 1]):
         x_in = orc.normal_f32(2 * seq * sh.hidden, 1400 + i).reshape(2, seq, sh.hidden)
         a = to_dev(torch, x_in.reshape(2 * seq, sh.hidden)).reshape(2, seq, sh.hidden)
         b = a.clone()
