@@ -1208,7 +1208,7 @@ __global__ __launch_bounds__(256) void attn_scores_gqa_kernel(const double* __re
     for (int j = 0; j < NK; ++j) {
         const int i = tid + j * 256;
         const int r = i / PR4, c4 = (i % PR4) * 4;
-        kreg[j] = *(const float4*)(cache_k + cb + (size_t)min(k0 + r, msl - 1) * kv_dim + c4);
+        kreg[j] = load16_nt((const float4*)(cache_k + cb + (size_t)min(k0 + r, msl - 1) * kv_dim + c4));
     }
     const int32_t* ar = ROPE ? ra.acc + (size_t)row * (q_dim + 2 * kv_dim) : nullptr;
     const bool newrow = ROPE && k0 <= pos && pos < k0 + CH;
@@ -1348,8 +1348,8 @@ __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict_
         const int i = tid + j * 256;
         const int r = i / PR4, c4 = (i % PR4) * 4;
         const size_t o = cb + (size_t)min(k0 + r, msl - 1) * kv_dim + c4;
-        kreg[j] = *(const float4*)(cache_k + o);
-        vreg[j] = *(const float4*)(cache_v + o);
+        kreg[j] = load16_nt((const float4*)(cache_k + o));
+        vreg[j] = load16_nt((const float4*)(cache_v + o));
     }
     // ROPE: the projection operands this workgroup needs are loaded with the
     // K/V rows, and the angles computed while both are in flight: Q of the
@@ -2335,7 +2335,7 @@ __global__ __launch_bounds__(256) void lm_head_kernel(const float* __restrict__ 
     _Pragma("unroll") for (int it = 0; it < NL; ++it) {                              \
         const int c = (C0) + lcol;                                                   \
         if (VEC) {                                                                   \
-            nx[it] = *(const float4*)(srow[it] + min(c, hidden - 4));                \
+            nx[it] = load16_nt((const float4*)(srow[it] + min(c, hidden - 4)));      \
         } else {                                                                     \
             nx[it] = make_float4(srow[it][min(c, hidden - 1)],                       \
                                  srow[it][min(c + 1, hidden - 1)],                   \

@@ -113,11 +113,11 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
         const int kt = wave + u * WAVES;
         if (FUSEQ) {  // (without a prologue to overlap, skipping the unused loads is cheaper)
             const uint32_t o = kt < ktiles ? (uint32_t)(tile0 + (size_t)kt * 64) * 16u : wbytes;
-            wv[0][u] = buffer_load16(wr0, o);
-            if (NMAT == 2) wv[NMAT - 1][u] = buffer_load16(wr1, o);
+            wv[0][u] = buffer_load16_nt(wr0, o);
+            if (NMAT == 2) wv[NMAT - 1][u] = buffer_load16_nt(wr1, o);
         } else if (kt < ktiles) {
-            wv[0][u] = p.w0[tile0 + (size_t)kt * 64];
-            if (NMAT == 2) wv[NMAT - 1][u] = p.w1[tile0 + (size_t)kt * 64];
+            wv[0][u] = load16_nt(p.w0 + tile0 + (size_t)kt * 64);
+            if (NMAT == 2) wv[NMAT - 1][u] = load16_nt(p.w1 + tile0 + (size_t)kt * 64);
         }
     }
 
@@ -411,8 +411,8 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
         for (int u = 0; u < U; ++u) {
             const int kt = kn + u * WAVES;
             if (kt < ktiles) {
-                wn[0][u] = p.w0[tile0 + (size_t)kt * 64];
-                if (NMAT == 2) wn[NMAT - 1][u] = p.w1[tile0 + (size_t)kt * 64];
+                wn[0][u] = load16_nt(p.w0 + tile0 + (size_t)kt * 64);
+                if (NMAT == 2) wn[NMAT - 1][u] = load16_nt(p.w1 + tile0 + (size_t)kt * 64);
             }
         }
         v4i a[MSUB][U][4];
@@ -518,8 +518,8 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_nt_kernel(MatArgs p) {
         if (kt < ktiles) {
 #pragma unroll
             for (int q = 0; q < NT; ++q) {
-                wv[q][0][u] = p.w0[tile0[q] + (size_t)kt * 64];
-                if (NMAT == 2) wv[q][NMAT - 1][u] = p.w1[tile0[q] + (size_t)kt * 64];
+                wv[q][0][u] = load16_nt(p.w0 + tile0[q] + (size_t)kt * 64);
+                if (NMAT == 2) wv[q][NMAT - 1][u] = load16_nt(p.w1 + tile0[q] + (size_t)kt * 64);
             }
         }
     }
@@ -559,8 +559,8 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_nt_kernel(MatArgs p) {
             if (kt < ktiles) {
 #pragma unroll
                 for (int q = 0; q < NT; ++q) {
-                    wn[q][0][u] = p.w0[tile0[q] + (size_t)kt * 64];
-                    if (NMAT == 2) wn[q][NMAT - 1][u] = p.w1[tile0[q] + (size_t)kt * 64];
+                    wn[q][0][u] = load16_nt(p.w0 + tile0[q] + (size_t)kt * 64);
+                    if (NMAT == 2) wn[q][NMAT - 1][u] = load16_nt(p.w1 + tile0[q] + (size_t)kt * 64);
                 }
             }
         }
@@ -704,7 +704,7 @@ __global__ __launch_bounds__(kSmallWaves * 64) void small_split_kernel(MatArgs p
         const int nt = nt0 + wave / KPS + j * (WAVES / KPS);
         const int kt = kt0 + ktl;
         const bool ok = nt < p.ntiles && kt < ktiles;
-        wv[j] = buffer_load16(wr, ok ? (((uint32_t)nt * (uint32_t)ktiles + (uint32_t)kt) * 64u + lane) * 16u : wbytes);
+        wv[j] = buffer_load16_nt(wr, ok ? (((uint32_t)nt * (uint32_t)ktiles + (uint32_t)kt) * 64u + lane) * 16u : wbytes);
     }
     // the epilogue's per-token amax and sum(xq), loaded while the rest is in
     // flight (clamped, unconditional loads: a branch around a load would make

@@ -90,7 +90,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_kernel(MatArgs p) {
     };
     uint4 buf[D];
 #pragma unroll
-    for (int j = 0; j < D; ++j) buf[j] = buffer_load16(wr, next_off());
+    for (int j = 0; j < D; ++j) buf[j] = buffer_load16_nt(wr, next_off());
 
     // ---- quantized rows into LDS (+ 256 zero bytes read by the rows past M)
     if (FUSEQ) {
@@ -252,7 +252,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_kernel(MatArgs p) {
                 const v4i a = *(const v4i*)(ap + 64 * t);
                 acc = mfma_i8(a, unpack_codes(word_of(buf[j], t)), acc);
             }
-            buf[j] = buffer_load16(wr, next_off());
+            buf[j] = buffer_load16_nt(wr, next_off());
             if (++ckt == ktiles) {
                 if (npend == 0) {
                     pend0 = acc;
