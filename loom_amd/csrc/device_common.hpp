@@ -6,6 +6,8 @@
 
 #include <math.h>
 
+#include <utility>
+
 #include "lamd.hpp"
 
 #pragma clang fp contract(off)
@@ -71,6 +73,27 @@ __device__ __forceinline__ uint4 load16_nt(const uint4* p) {
 
 __device__ __forceinline__ float4 load16_nt(const float4* p) {
     return __builtin_bit_cast(float4, __builtin_nontemporal_load((const u32x4*)p));
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// f(std::integral_constant<int, 0>{}) ... f(...<N - 1>{}): a loop whose index
+// is a compile-time constant in every iteration, for bodies the unroller may
+// leave rolled (a rolled loop over accumulator blocks indexes them
+// dynamically and moves them to scratch memory).
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// 16-byte non-temporal store of four adjacent floats (p 16-byte aligned)
+__device__ __forceinline__ void store16_nt(float* p, float a, float b, float c, float d) {
+    const f32x4 v = {a, b, c, d};
+    __builtin_nontemporal_store(v, (f32x4*)p);
 }
 
 // D(32x32 i32) += A(32x32 i8) * B(32x32 i8), twice the int8 rate of the

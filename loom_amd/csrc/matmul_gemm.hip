@@ -147,6 +147,8 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
 }
+// s_waitcnt lgkmcnt(0) only (vmcnt and expcnt at their maxima)
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
 
 template <int NMAT, int EPI, int MI>
 __global__ __launch_bounds__(256, 2) void gemm_lds_kernel(MatArgs p, GemmGrid gg) {
@@ -408,6 +410,50 @@ __global__ __launch_bounds__(256, 2) void gemm_lds_kernel(MatArgs p, GemmGrid gg
 
     // Epilogue from the accumulators: value v of block (i, j) is token row
     // 32i + 8(v/4) + 4h + v%4, output column (nb0 + j)*32 + l32.
+    // (the test covers the workgroup's whole tile, not this wave's columns:
+    // every wave of the workgroup takes this path and meets its barrier.
+    // 128-token tiles only: on the 64-token tiles of mid-size M it measured
+    // slower than storing from the accumulators.)
+    if (EPI == 0 && MI == 4 && m_wg + BM <= M && (ng * 4 + 4) * NJ * 32 <= p.e.n && p.e.ldo % 4 == 0 &&
+        ((uintptr_t)p.e.out & 15) == 0) {
+        // plain Dense on a full tile with 16-byte aligned rows: each 32 x 32
+        // block of a wave is written to a wave-private LDS tile in the
+        // accumulator layout and read back as four adjacent columns per lane,
+        // so one store instruction writes 8 whole 128-byte row segments with
+        // 16 bytes a lane (a quarter of the store instructions of storing
+        // from the accumulators).  The stage buffers hold the tiles: every
+        // wave has finished its MFMA operand reads at the barrier.
+        constexpr int TP = 40;  // tile pitch (floats): 16-byte rows; the two half-waves' rows in disjoint banks
+        static_assert(MI != 4 || 4 * 32 * TP * 4 <= BM * 256, "epilogue tiles");
+        __builtin_amdgcn_s_barrier();
+        float* tl = (float*)As0 + wave * 32 * TP;
+        const int ldo = p.e.ldo;
+        const double* os_l = s_os0 + 4 * h;
+        const int* xs_l = s_xs + 4 * h;
+        const int rr = lane >> 3, cc = (lane & 7) * 4;  // read-back: row rr + 8k, columns cc .. cc + 3
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int t = 32 * i + 8 * g + u;  // this lane's row: t + 4h
+                        tl[(8 * g + 4 * h + u) * TP + l32] =
+                            (float)((double)(acc[0][i][j][4 * g + u] - xs_l[t]) * os_l[t]);
+                    }
+                wait_lgkm0();  // the wave's tile writes have landed
+                float* orow = p.e.out + (size_t)(m_wg + 32 * i + rr) * ldo + (nb0 + j) * 32 + cc;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float4 v = *(const float4*)&tl[(rr + 8 * k) * TP + cc];
+                    store16_nt(orow + (size_t)(8 * k) * ldo, v.x, v.y, v.z, v.w);
+                }
+                wait_lgkm0();  // read back before the next block's writes
+            }
+        return;
+    }
     if (EPI == 0 && m_wg + BM <= M && (nb0 + NJ) * 32 <= p.e.n) {
         // plain Dense on a full tile: no row or column tests; each store
         // takes a wave-uniform row pointer plus this lane's 32-bit offset,
@@ -431,6 +477,85 @@ __global__ __launch_bounds__(256, 2) void gemm_lds_kernel(MatArgs p, GemmGrid gg
                         __builtin_nontemporal_store((float)((double)(acc[0][i][j][4 * g + u] - xs) * os0),
                                                     &rowp[loff + 32 * j]);
                 }
+        return;
+    }
+    if (EPI != 0 && MI == 4 && m_wg + BM <= M && (ng * 4 + 4) * NJ * 32 <= p.e.n &&
+        (EPI == 1 + EPI_ACC ? p.e.n % 4 == 0 && ((uintptr_t)p.e.acc0 & 15) == 0
+                            : !p.e.acc0 && !p.e.acc1 && !p.e.post && p.e.ldo % 4 == 0 &&
+                                  ((uintptr_t)p.e.out & 15) == 0 &&
+                                  (!p.e.residual || ((uintptr_t)p.e.residual & 15) == 0))) {
+        // the other epilogues on a full 128-token tile, through the same
+        // wave-private LDS tiles as the plain Dense one (workgroup-uniform
+        // test, one barrier): in the accumulator layout each value is
+        // rescaled (+ bias) to its fp32 pre-residual value (SwiGLU: the gate
+        // product; EPI_ACC: the int32 accumulator's bits); read back as four
+        // adjacent columns of a row, the residual (one 16-byte load) and the
+        // stores follow in the reference's order.  (With an activation copy
+        // or accumulator taps the accumulators would stay live across their
+        // code and spill: those take the path below.)
+        constexpr int TP = 40;
+        static_assert(MI != 4 || 4 * 32 * TP * 4 <= BM * 256, "epilogue tiles");
+        __builtin_amdgcn_s_barrier();
+        float* tl = (float*)As0 + wave * 32 * TP;
+        const int ldo = p.e.ldo, ldn = p.e.n;
+        const double* os0_l = s_os0 + 4 * h;
+        const double* os1_l = NMAT == 2 ? s_os1 + 4 * h : s_os0;
+        const int* xs_l = s_xs + 4 * h;
+        const bool has_res = EPI == 1 + EPI_DENSE && p.e.residual;
+        const int rr = lane >> 3, cc = (lane & 7) * 4;
+        static_for<NJ>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            const int col = (nb0 + j) * 32 + l32;
+            const float bias0 = EPI != 1 + EPI_ACC && p.e.bias0 ? p.e.bias0[col] : 0.0f;
+            const float bias1 = NMAT == 2 && p.e.bias1 ? p.e.bias1[col] : 0.0f;
+            static_for<MI>([&](auto ic) {
+                constexpr int i = decltype(ic)::value;
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int t = 32 * i + 8 * g + u;  // this lane's row: t + 4h
+                        const int xs = xs_l[t];
+                        const int a0 = acc[0][i][j][4 * g + u] - xs;
+                        float v;
+                        if (EPI == 1 + EPI_ACC) {
+                            v = __int_as_float(a0);
+                        } else if (EPI == 1 + EPI_SWIGLU) {
+                            const int a1 = acc[NMAT - 1][i][j][4 * g + u] - xs;
+                            const double gg0 = (double)a0 * os0_l[t] + (p.e.bias0 ? (double)bias0 : 0.0);
+                            const double uu = (double)a1 * os1_l[t] + (p.e.bias1 ? (double)bias1 : 0.0);
+                            v = (float)gate_product(gg0, uu, p.e.activation);
+                        } else {
+                            double d = (double)a0 * os0_l[t];
+                            if (p.e.bias0) d = d + (double)bias0;
+                            v = (float)d;
+                        }
+                        tl[(8 * g + 4 * h + u) * TP + l32] = v;
+                    }
+                wait_lgkm0();  // the wave's tile writes have landed
+                const size_t row0 = (size_t)(m_wg + 32 * i + rr);
+                const int c0 = (nb0 + j) * 32 + cc;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float4 v = *(const float4*)&tl[(rr + 8 * k) * TP + cc];
+                    const size_t row = row0 + 8 * k;
+                    if (EPI == 1 + EPI_ACC) {
+                        *(int4*)(p.e.acc0 + row * ldn + c0) =
+                            make_int4(__float_as_int(v.x), __float_as_int(v.y), __float_as_int(v.z), __float_as_int(v.w));
+                    } else if (EPI == 1 + EPI_SWIGLU) {
+                        *(float4*)(p.e.out + row * ldo + c0) = v;
+                    } else {
+                        float4 o = v;
+                        if (has_res) {
+                            const float4 r4 = *(const float4*)(p.e.residual + row * ldo + c0);
+                            o = make_float4(o.x + r4.x, o.y + r4.y, o.z + r4.z, o.w + r4.w);
+                        }
+                        *(float4*)(p.e.out + row * ldo + c0) = o;
+                    }
+                }
+                wait_lgkm0();  // read back before the next block's writes
+            });
+        });
         return;
     }
     if (EPI != 0 && m_wg + BM <= M && (nb0 + NJ) * 32 <= p.e.n) {
