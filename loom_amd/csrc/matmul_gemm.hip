@@ -430,7 +430,9 @@ __global__ __launch_bounds__(256, 2) void gemm_lds_kernel(MatArgs p, GemmGrid gg
         const int ldo = p.e.ldo;
         const double* os_l = s_os0 + 4 * h;
         const int* xs_l = s_xs + 4 * h;
-        const int rr = lane >> 3, cc = (lane & 7) * 4;  // read-back: row rr + 8k, columns cc .. cc + 3
+        // read-back: row rr + 8k, columns cc .. cc + 3; each 16-lane group reads
+        // rows r and r + 4, whose segments lie 32 banks apart at pitch 40
+        const int rr = (lane >> 4) + 4 * ((lane >> 3) & 1), cc = (lane & 7) * 4;
 #pragma unroll
         for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -502,7 +504,7 @@ __global__ __launch_bounds__(256, 2) void gemm_lds_kernel(MatArgs p, GemmGrid gg
         const double* os1_l = NMAT == 2 ? s_os1 + 4 * h : s_os0;
         const int* xs_l = s_xs + 4 * h;
         const bool has_res = EPI == 1 + EPI_DENSE && p.e.residual;
-        const int rr = lane >> 3, cc = (lane & 7) * 4;
+        const int rr = (lane >> 4) + 4 * ((lane >> 3) & 1), cc = (lane & 7) * 4;
         static_for<NJ>([&](auto jc) {
             constexpr int j = decltype(jc)::value;
             const int col = (nb0 + j) * 32 + l32;
