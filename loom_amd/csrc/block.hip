@@ -1766,19 +1766,20 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const int* __restrict
 // wave 0 adds column d of the products p[k] * v[k][d] in position order (the
 // reference's `sum += p * v`, a product then a sum, each rounded); column DG
 // holds p itself, whose chain is expSum.  Chunks of C = 4096 / DG positions:
-// every thread loads its 16 values of a chunk (and the scores it turns into
-// probabilities: C / 256) kChainDepth chunks ahead, forms its products in
-// registers and writes them to one of two LDS product buffers, transposed so
-// that a chain lane reads two positions per 16-byte load; wave 0 adds chunk c
-// while the products of chunk c + 1 and the probabilities of chunk c + 2 are
-// written.  The loads are branch-free (indices clamped into the ring and the
-// score row; surplus values are never added).  grid (heads * HD / DG, rows),
-// 256 threads.
+// each of the 256 threads of waves 1-4 loads its 16 values of a chunk (and
+// the scores it turns into probabilities: C / 256) kChainDepth chunks ahead,
+// forms its products in registers and writes them to one of two LDS product
+// buffers, transposed so that a chain lane reads two positions per 16-byte
+// load; wave 0 only adds: chunk c while the other waves write the products of
+// chunk c + 1 and the probabilities of chunk c + 2.  The loads are
+// branch-free (indices clamped into the ring and the score row; surplus
+// values are never added).  grid (heads * HD / DG, rows), 320 threads.
 constexpr int kChainDepth = 4;
 constexpr int kChainCols = 16;
+constexpr int kChainThreads = 320;  // wave 0: the chains; waves 1-4: loads, probabilities, products
 
 template <int HD, int DG>
-__global__ __launch_bounds__(256) void attn_chain_kernel(const float* __restrict__ cache_v,
+__global__ __launch_bounds__(kChainThreads) void attn_chain_kernel(const float* __restrict__ cache_v,
                                                          const int* __restrict__ pos0, int msl,
                                                          int span, int heads, int kv_heads,
                                                          int seq, DecodeScratch sc,
@@ -1795,6 +1796,8 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(const float* __restrict
     const int kvh = h / (heads / kv_heads);
     const int q_dim = heads * HD, kv_dim = kv_heads * HD;
     const int tid = threadIdx.x, lane = tid & 63;
+    const int pt = tid - 64;        // product thread index (waves 1-4)
+    const bool maker = tid >= 64;   // waves 1-4 (wave-uniform)
     const int L = *pos0 + s + 1;
     double* orow = out + (size_t)row * q_dim + (size_t)h * HD + dg * DG;
     if (L > span) {
@@ -1816,7 +1819,7 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(const float* __restrict
     double pt0[PT], pt1[PT], pt2[PT], pt3[PT];
 #define LAMD_CHAIN_LD(U, I, CC)                                                   \
     {                                                                             \
-        const int e = (tid + (I) * 256) * 4; /* element of the C x DG chunk */     \
+        const int e = (pt + (I) * 256) * 4; /* element of the C x DG chunk */     \
         const int k = (CC) * C + e / DG;                                          \
         r##U##_##I = *(const float4*)(vb + (size_t)min(k, msl - 1) * kv_dim + e % DG); \
     }
@@ -1826,16 +1829,16 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(const float* __restrict
         LAMD_CHAIN_LD(U, 0, cc) LAMD_CHAIN_LD(U, 1, cc)                           \
         LAMD_CHAIN_LD(U, 2, cc) LAMD_CHAIN_LD(U, 3, cc)                           \
         _Pragma("unroll") for (int q = 0; q < PT; ++q)                            \
-            pt##U[q] = sr[min(cc * C + tid + 256 * q, span - 1)];                 \
+            pt##U[q] = sr[min(cc * C + pt + 256 * q, span - 1)];                 \
     }
 #define LAMD_CHAIN_EXP(U, BUF)                                                    \
     {                                                                             \
         _Pragma("unroll") for (int q = 0; q < PT; ++q)                            \
-            pr_sh[BUF][tid + 256 * q] = exp(pt##U[q] - mx);                       \
+            pr_sh[BUF][pt + 256 * q] = exp(pt##U[q] - mx);                       \
     }
 #define LAMD_CHAIN_PR(U, I, BUF)                                                  \
     {                                                                             \
-        const int e = (tid + (I) * 256) * 4;                                      \
+        const int e = (pt + (I) * 256) * 4;                                      \
         const int k = e / DG, d = e % DG;                                         \
         const double p = pr_sh[BUF][k];                                           \
         prod[BUF][d][k] = p * (double)r##U##_##I.x;                               \
@@ -1848,12 +1851,14 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(const float* __restrict
         LAMD_CHAIN_PR(U, 0, BUF) LAMD_CHAIN_PR(U, 1, BUF)                         \
         LAMD_CHAIN_PR(U, 2, BUF) LAMD_CHAIN_PR(U, 3, BUF)                         \
         _Pragma("unroll") for (int q = 0; q < PT; ++q)                            \
-            prod[BUF][DG][tid + 256 * q] = pr_sh[BUF][tid + 256 * q];             \
+            prod[BUF][DG][pt + 256 * q] = pr_sh[BUF][pt + 256 * q];             \
     }
-    LAMD_CHAIN_ISSUE(0, 0)
-    LAMD_CHAIN_ISSUE(1, 1)
-    LAMD_CHAIN_ISSUE(2, 2)
-    LAMD_CHAIN_ISSUE(3, 3)
+    if (maker) {
+        LAMD_CHAIN_ISSUE(0, 0)
+        LAMD_CHAIN_ISSUE(1, 1)
+        LAMD_CHAIN_ISSUE(2, 2)
+        LAMD_CHAIN_ISSUE(3, 3)
+    }
     // maximum over the chunk maxima of the 64-position score chunks with
     // data: -1e9 start, NaN never wins (each wave forms the same value)
     double mx = -1e9;
@@ -1869,17 +1874,21 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(const float* __restrict
             mx = o > mx ? o : mx;
         }
     }
-    LAMD_CHAIN_EXP(0, 0)
-    LAMD_CHAIN_EXP(1, 1)
+    if (maker) {
+        LAMD_CHAIN_EXP(0, 0)
+        LAMD_CHAIN_EXP(1, 1)
+    }
     __syncthreads();
-    LAMD_CHAIN_PRODUCTS(0, 0)
-    LAMD_CHAIN_ISSUE(0, kChainDepth)
+    if (maker) {
+        LAMD_CHAIN_PRODUCTS(0, 0)
+        LAMD_CHAIN_ISSUE(0, kChainDepth)
+    }
     __syncthreads();
 
     double sum = 0.0;  // column tid's chain (tid <= DG)
-    // step for chunk c = c0 + U: the products of chunk c + 1 (staging set
-    // U + 1) go to buffer (c + 1) & 1 and that set is refilled, the
-    // probabilities of chunk c + 2 (set UE) go to ring slot c & 1, then wave 0
+    // step for chunk c = c0 + U: waves 1-4 write the products of chunk c + 1
+    // (staging set U + 1) to buffer (c + 1) & 1 and refill that set, and the
+    // probabilities of chunk c + 2 (set UE) to ring slot c & 1, while wave 0
     // adds chunk c from buffer c & 1 (all parities are compile-time: c0 is a
     // multiple of four).  Products, probabilities and loads run for every
     // chunk's step, for chunks past the last one too (clamped indices; no
@@ -1889,9 +1898,11 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(const float* __restrict
     {                                                                             \
         const int c = c0 + (U);                                                   \
         if (c >= nch) break;                                                      \
-        LAMD_CHAIN_PRODUCTS(UN, ((U) + 1) & 1)                                    \
-        LAMD_CHAIN_EXP(UE, (U) & 1)                                               \
-        LAMD_CHAIN_ISSUE(UN, c + 1 + kChainDepth)                                 \
+        if (maker) {                                                               \
+            LAMD_CHAIN_PRODUCTS(UN, ((U) + 1) & 1)                                \
+            LAMD_CHAIN_EXP(UE, (U) & 1)                                           \
+            LAMD_CHAIN_ISSUE(UN, c + 1 + kChainDepth)                             \
+        }                                                                         \
         if (c < nch && tid <= DG) {                                               \
             const double* pc = prod[(U) & 1][tid];                                \
             const int n = min(C, L - c * C);                                      \
@@ -1973,8 +1984,8 @@ static hipError_t launch_strict_decode(const double* q, float* cache_k, float* c
                                cache_v, pos0, msl, span, heads, kv_heads, seq, sc, ra);           \
     }
 #define LAMD_CHAIN(HDV)                                                                              \
-    hipLaunchKernelGGL((attn_chain_kernel<HDV, DG>), dim3(heads * (HDV / DG), rows), t, 0, s, cache_v, pos0, \
-                       msl, span, heads, kv_heads, seq, sc, out)
+    hipLaunchKernelGGL((attn_chain_kernel<HDV, DG>), dim3(heads * (HDV / DG), rows), dim3(kChainThreads), 0, \
+                       s, cache_v, pos0, msl, span, heads, kv_heads, seq, sc, out)
     switch (hd) {
         case 32: LAMD_SCORES(32); break;
         case 64: LAMD_SCORES(64); break;
