@@ -67,6 +67,21 @@ __device__ __forceinline__ uint4 buffer_load16_nt(__amdgpu_buffer_rsrc_t r, uint
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
+// 16-byte loads and stores with the device-scope coherence bit (sc1): the
+// cache policy the compiler gives agent-scope relaxed atomic loads and stores
+// on gfx950, here on four words at once.  A store goes through to the level
+// that every XCD sees; a load reads from that level, not from a line its own
+// XCD's L2 may still hold.
+constexpr int kCoherentSC1 = 16;
+
+__device__ __forceinline__ u32x4 buffer_load16_sc1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kCoherentSC1));
+}
+
+__device__ __forceinline__ void buffer_store16_sc1(u32x4 v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, 0, kCoherentSC1);
+}
+
 __device__ __forceinline__ uint4 load16_nt(const uint4* p) {
     return __builtin_bit_cast(uint4, __builtin_nontemporal_load((const u32x4*)p));
 }

@@ -368,7 +368,11 @@ __global__ __launch_bounds__(256, 2) void gemm_lds_kernel(MatArgs p, GemmGrid gg
     wait_vm_lgkm0<0>();  // no copy may still be writing LDS when the workgroup ends
 
     if (MI == 2 && S > 1) {
-        int32_t* mine = gg.part + (size_t)linear * kSplitSlotInts;
+        // Slot layout: 16-byte group q (values 4q .. 4q+3) of accumulator
+        // block b of thread t at int offset ((b*4 + q)*256 + t)*4, so each
+        // store or load instruction of the workgroup covers 4 KB in one run.
+        const __amdgpu_buffer_rsrc_t mine =
+            buffer_rsrc(gg.part + (size_t)linear * kSplitSlotInts, kSplitSlotInts * 4);
 #pragma unroll
         for (int a = 0; a < NMAT; ++a)
 #pragma unroll
@@ -376,9 +380,12 @@ __global__ __launch_bounds__(256, 2) void gemm_lds_kernel(MatArgs p, GemmGrid gg
 #pragma unroll
                 for (int j = 0; j < NJ; ++j)
 #pragma unroll
-                    for (int v = 0; v < 16; ++v)
-                        __hip_atomic_store(&mine[(((a * MI + i) * NJ + j) * 16 + v) * 256 + tid], acc[a][i][j][v],
-                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    for (int q = 0; q < 4; ++q) {
+                        const v16i& c = acc[a][i][j];
+                        const u32x4 w = {(unsigned)c[4 * q], (unsigned)c[4 * q + 1], (unsigned)c[4 * q + 2],
+                                         (unsigned)c[4 * q + 3]};
+                        buffer_store16_sc1(w, mine, (uint32_t)(((((a * MI + i) * NJ + j) * 4 + q) * 256 + tid) * 16));
+                    }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (tid == 0) {
@@ -387,22 +394,32 @@ __global__ __launch_bounds__(256, 2) void gemm_lds_kernel(MatArgs p, GemmGrid gg
         }
         __syncthreads();
         if (!s_last) return;
+        // one slot at a time, its 16 loads issued before any add
         for (int o = 0; o < S; ++o) {
             if (o == split) continue;
-            const int32_t* src = gg.part + (size_t)(tile * S + o) * kSplitSlotInts;
+            const __amdgpu_buffer_rsrc_t src =
+                buffer_rsrc(gg.part + (size_t)(tile * S + o) * kSplitSlotInts, kSplitSlotInts * 4);
+            u32x4 t[NMAT][MI][NJ][4];
 #pragma unroll
             for (int a = 0; a < NMAT; ++a)
 #pragma unroll
                 for (int i = 0; i < MI; ++i)
 #pragma unroll
-                    for (int j = 0; j < NJ; ++j) {
-                        v16i t;
+                    for (int j = 0; j < NJ; ++j)
 #pragma unroll
-                        for (int v = 0; v < 16; ++v)
-                            t[v] = __hip_atomic_load(&src[(((a * MI + i) * NJ + j) * 16 + v) * 256 + tid],
-                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        acc[a][i][j] += t;
-                    }
+                        for (int q = 0; q < 4; ++q)
+                            t[a][i][j][q] =
+                                buffer_load16_sc1(src, (uint32_t)(((((a * MI + i) * NJ + j) * 4 + q) * 256 + tid) * 16));
+#pragma unroll
+            for (int a = 0; a < NMAT; ++a)
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) acc[a][i][j][4 * q + r] += (int)t[a][i][j][q][r];
         }
         if (tid == 0) __hip_atomic_store(&gg.ctr[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
