@@ -99,8 +99,10 @@ class Timer:
     launch rate.
 
     Rotating runs (rotate=R > 1: call i uses weight copy i % R) capture one
-    graph of all R calls, whatever `steps` is, and replay it steps // R times,
-    then a graph of the first steps % R calls.  Before the timed region the
+    graph of all R calls, whatever `steps` is, and time ceil(steps / R) replays
+    of it: the timed region always covers whole rotations (at least `steps`
+    calls, every copy read), and the mean is over the calls actually run
+    (`last_launches`).  Before the timed region the
     full graph runs once untimed, so copy i was last read R - i calls earlier:
     the copies read after it (>= 2 x MALL of bytes for the first R - 58) have
     evicted it from the MALL and the L2s, while the address translations stay
@@ -111,6 +113,7 @@ class Timer:
     def __init__(self, torch):
         self.torch = torch
         self.last_working_set = 0  # distinct copies the last rotating timed region read
+        self.last_launches = 0  # calls the last timed region ran
 
     def _capture(self, fn, first: int, count: int):
         graph = self.torch.cuda.CUDAGraph()
@@ -120,7 +123,8 @@ class Timer:
         return graph
 
     def run(self, fn, steps: int, warmup: int, per_graph: int = 64, rotate: int = 0) -> float:
-        """Mean ms per call over exactly `steps` calls (after `warmup` calls)."""
+        """Mean ms per call over `steps` calls (after `warmup` calls); rotating
+        runs round `steps` up to whole rotations."""
         torch = self.torch
         steps = max(1, steps)
         side = torch.cuda.Stream()
@@ -131,17 +135,22 @@ class Timer:
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
         if rotate > 1:
-            per_graph = rotate  # never clamped: one graph visits every copy
+            # whole rotations only: the timed region reads every copy, so its
+            # working set is all R copies whatever `steps` is
+            per_graph = rotate
+            full, rest = -(-steps // rotate), 0
         else:
             per_graph = max(1, min(per_graph, steps))
-        full, rest = divmod(steps, per_graph)
-        graph = self._capture(fn, 0, per_graph) if (full or rotate > 1) else None
+            full, rest = divmod(steps, per_graph)
+        graph = self._capture(fn, 0, per_graph) if full else None
         tail = self._capture(fn, 0, rest) if rest else None
         for g in (tail, graph):
             if g is not None:
                 g.replay()  # untimed: uploads the graphs; the full rotation runs last
+        launches = full * per_graph + rest
+        self.last_launches = launches
         if rotate > 1:
-            self.last_working_set = min(steps, rotate)
+            self.last_working_set = rotate
         torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
@@ -152,7 +161,7 @@ class Timer:
             tail.replay()
         end.record()
         torch.cuda.synchronize()
-        return start.elapsed_time(end) / steps  # ms per call
+        return start.elapsed_time(end) / launches  # ms per call
 
     def run_big(self, fn, reps: int) -> float:
         """Mean ms per call of `reps` back-to-back calls that each stream more
@@ -501,6 +510,7 @@ def main() -> int:
 
     ms_step = timer.run(step_dense, args.steps, args.warmup, rotate=rot)
     copies_read = timer.last_working_set
+    launches_timed = timer.last_launches
     working_set = copies_read * per + 4 * (k + n)
     value = b1 / (ms_step * 1e-3) / 1e9
     log(f"dense M=1 up: {ms_step * 1e3:.2f} us/step, {value:.0f} GB/s "
@@ -573,10 +583,12 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "int8xternary->int32, fp64 rescale, fp32 io",
         "data": "synthetic: seeded ternary weights P(0)=.5, x~N(0,1); step i reads weight copy "
-                f"i % {rot} ({rot} HBM-resident copies, {rot * per / 1e6:.0f} MB); an untimed "
-                "pass over every copy precedes the timed region, so each timed step's weights "
-                "come from HBM",
+                f"i % {rot} ({rot} HBM-resident copies, {rot * per / 1e6:.0f} MB); the timed "
+                f"region runs whole rotations ({launches_timed} launches for --steps "
+                f"{args.steps}, every copy read) after an untimed one, so each timed step's "
+                "weights come from HBM; ms_per_step is the mean over the launches run",
         "working_set_bytes": working_set,
+        "launches_timed": launches_timed,
         "config": {"workload": "config1 ternary GEMV M=1 K=2560 N=6912 (= config0 shape), "
                                "DenseForwardPackedTernary: act-quant + GEMV + epilogue",
                    "M": 1, "K": k, "N": n, "rotating_copies": rot,

@@ -828,13 +828,31 @@ __device__ __forceinline__ void epilogue_store_pre(const EpiDev& e, int i, int n
     if (e.post) e.post[o] = activate_f32(v, e.activation);
 }
 
+// The epilogue's per-output inputs that come from memory: bias0[n],
+// bias1[n] and residual[i*ldo+n] (zero where the pointer is null or the kind
+// does not read them).  Kernels load them for all of a round's outputs
+// before the round's first store: the vector memory counter is in order, so a
+// load issued after a store also waits for that store to complete.
+struct EpiIn {
+    float b0, b1, res;
+};
+
+__device__ __forceinline__ EpiIn epilogue_inputs(const EpiDev& e, int i, int n) {
+    EpiIn v;
+    v.b0 = e.bias0 ? e.bias0[n] : 0.0f;
+    v.b1 = e.kind == EPI_SWIGLU && e.bias1 ? e.bias1[n] : 0.0f;
+    v.res = e.kind == EPI_DENSE && e.residual ? e.residual[(size_t)i * e.ldo + n] : 0.0f;
+    return v;
+}
+
 __device__ __forceinline__ void epilogue_store(const EpiDev& e, int i, int n, int raw0, int raw1,
                                                const RowScale& rs) {
-    const float b0 = e.bias0 ? e.bias0[n] : 0.0f;
-    const float b1 = e.kind == EPI_SWIGLU && e.bias1 ? e.bias1[n] : 0.0f;
-    const float res = e.kind == EPI_DENSE && e.residual ? e.residual[(size_t)i * e.ldo + n] : 0.0f;
-    epilogue_store_pre(e, i, n, raw0, raw1, rs.os0, rs.os1, rs.xs, b0, b1, res);
+    const EpiIn v = epilogue_inputs(e, i, n);
+    epilogue_store_pre(e, i, n, raw0, raw1, rs.os0, rs.os1, rs.xs, v.b0, v.b1, v.res);
 }
+
+// Outputs per thread per epilogue round of the small-M kernels.
+constexpr int kEpiBatch = 4;
 
 // Arguments of the matmul kernels.
 // Workspace of the small-M split kernel (matmul_skinny.hip): int32 output

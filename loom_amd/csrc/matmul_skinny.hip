@@ -121,6 +121,24 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
         }
     }
 
+    // The epilogue inputs of the first output this thread finishes (bias and
+    // residual, and for pre-quantized rows the row's amax and sum(xq)) are
+    // loaded now, so the epilogue does not start with a memory round trip
+    // after the reduction (clamped indices: no branch per lane).  The
+    // fused-quantization kernels load them in the epilogue instead: an early
+    // residual load measured slower in the norm-fused decode GEMVs (decode
+    // 694 -> 678 tokens/s).
+    constexpr bool kEarlyIn = !FUSEQ;
+    const int tc0 = min(tid >> 4, M - 1), nc0 = min(nt * kTileRows + (tid & 15), p.e.n - 1);
+    EpiIn in_first{0.0f, 0.0f, 0.0f};
+    if (kEarlyIn) in_first = epilogue_inputs(p.e, tc0, nc0);
+    float am_first = 0.0f;
+    int xs_first = 0;
+    if (!FUSEQ) {
+        am_first = p.e.amax[tc0];
+        xs_first = p.e.xsum[tc0];
+    }
+
     for (int i = tid; i < NMAT * MSUB * 16 * 16; i += T) (&red[0][0][0])[i] = 0;
     if (FUSEQ) {
         if (NORM != NORM_NONE) {
@@ -377,15 +395,6 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
         }
     }
 
-    // Pre-quantized rows: the epilogue's per-token amax and sum(xq) of the
-    // first output each thread finishes are loaded now, so the epilogue does
-    // not start with a memory round trip after the reduction.
-    float am_first = 0.0f;
-    int xs_first = 0;
-    if (!FUSEQ && tid < M * 16) {
-        am_first = p.e.amax[tid >> 4];
-        xs_first = p.e.xsum[tid >> 4];
-    }
 
     v4i acc[NMAT][MSUB];
 #pragma unroll
@@ -463,25 +472,45 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
             }
     __syncthreads();
 
-    for (int idx = tid; idx < M * 16; idx += T) {
-        const int tok = idx >> 4;
-        const int col = idx & 15;
-        const int n = nt * kTileRows + col;
-        if (n >= p.e.n) continue;
-        float am;
-        int xs;
-        if (FUSEQ) {
-            am = __uint_as_float(amax_bits[tok]);
-            if (am < 1e-5f) am = 1e-5f;
-            xs = xsum_s[tok];
-        } else if (idx == tid) {
-            am = am_first;
-            xs = xs_first;
-        } else {
-            am = p.e.amax[tok];
-            xs = p.e.xsum[tok];
+    // Rounds of EB (at most two) outputs per thread; a round loads the inputs
+    // of all its outputs before its first store (the first round's first
+    // output's were loaded at the start).
+    constexpr int EB = (MSUB * 256 + T - 1) / T < 2 ? (MSUB * 256 + T - 1) / T : 2;
+    const int total = M * 16;
+    for (int base = 0; base < total; base += EB * T) {
+        int tk[EB], nn[EB], xs[EB];
+        float am[EB];
+        EpiIn in[EB];
+#pragma unroll
+        for (int j = 0; j < EB; ++j) {
+            const int idx = base + tid + j * T;
+            tk[j] = idx >> 4;
+            nn[j] = nt * kTileRows + (idx & 15);
+            const int tc = min(tk[j], M - 1), nc = min(nn[j], p.e.n - 1);
+            const bool first = j == 0 && base == 0;
+            if (FUSEQ) {
+                const float a = __uint_as_float(amax_bits[tc]);
+                am[j] = a < 1e-5f ? 1e-5f : a;
+                xs[j] = xsum_s[tc];
+            } else if (first) {
+                am[j] = am_first;
+                xs[j] = xs_first;
+            } else {
+                am[j] = p.e.amax[tc];
+                xs[j] = p.e.xsum[tc];
+            }
+            in[j] = first && kEarlyIn ? in_first : epilogue_inputs(p.e, tc, nc);
         }
-        epilogue_store(p.e, tok, n, red[0][tok][col], red[NMAT - 1][tok][col], row_scale(p.e, am, xs));
+#pragma unroll
+        for (int j = 0; j < EB; ++j) {
+            const int idx = base + tid + j * T;
+            if (idx < total && nn[j] < p.e.n) {
+                const int col = idx & 15;
+                const RowScale rs = row_scale(p.e, am[j], xs[j]);
+                epilogue_store_pre(p.e, tk[j], nn[j], red[0][tk[j]][col], red[NMAT - 1][tk[j]][col], rs.os0,
+                                   rs.os1, rs.xs, in[j].b0, in[j].b1, in[j].res);
+            }
+        }
     }
 }
 
@@ -522,14 +551,6 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_nt_kernel(MatArgs p) {
                 if (NMAT == 2) wv[q][NMAT - 1][u] = load16_nt(p.w1 + tile0[q] + (size_t)kt * 64);
             }
         }
-    }
-    // the epilogue constants of the first output this thread finishes
-    const int first_tok = (tid % (M * 16)) >> 4;
-    float am_first = 0.0f;
-    int xs_first = 0;
-    if (tid < NT * M * 16) {
-        am_first = p.e.amax[first_tok];
-        xs_first = p.e.xsum[first_tok];
     }
     for (int i = tid; i < NT * NMAT * MSUB * 16 * 16; i += T) (&red[0][0][0][0])[i] = 0;
 
@@ -617,16 +638,38 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_nt_kernel(MatArgs p) {
                 }
     __syncthreads();
 
-    for (int idx = tid; idx < NT * M * 16; idx += T) {
-        const int q = idx / (M * 16);
-        const int rem = idx - q * (M * 16);
-        const int tok = rem >> 4;
-        const int col = rem & 15;
-        const int n = (nt0 + q) * kTileRows + col;
-        if (nt0 + q >= p.ntiles || n >= p.e.n) continue;
-        const float am = idx == tid ? am_first : p.e.amax[tok];
-        const int xs = idx == tid ? xs_first : p.e.xsum[tok];
-        epilogue_store(p.e, tok, n, red[q][0][tok][col], red[q][NMAT - 1][tok][col], row_scale(p.e, am, xs));
+    // Rounds of kEpiBatch outputs per thread: a round loads the amax, sum(xq),
+    // bias and residual of all its outputs (clamped indices, no branch per
+    // lane) before its first store.
+    constexpr int EB = (NT * MSUB * 256 + T - 1) / T < kEpiBatch ? (NT * MSUB * 256 + T - 1) / T : kEpiBatch;
+    const int total = NT * M * 16;
+    for (int base = 0; base < total; base += EB * T) {
+        int tk[EB], nn[EB], qq[EB], xs[EB];
+        float am[EB];
+        EpiIn in[EB];
+#pragma unroll
+        for (int j = 0; j < EB; ++j) {
+            const int idx = base + tid + j * T;
+            const int q = idx / (M * 16);
+            const int rem = idx - q * (M * 16);
+            qq[j] = q;
+            tk[j] = rem >> 4;
+            nn[j] = (nt0 + q) * kTileRows + (rem & 15);
+            const int tc = min(tk[j], M - 1), nc = min(nn[j], p.e.n - 1);
+            am[j] = p.e.amax[tc];
+            xs[j] = p.e.xsum[tc];
+            in[j] = epilogue_inputs(p.e, tc, nc);
+        }
+#pragma unroll
+        for (int j = 0; j < EB; ++j) {
+            const int idx = base + tid + j * T;
+            if (idx < total && nt0 + qq[j] < p.ntiles && nn[j] < p.e.n) {
+                const int col = nn[j] - (nt0 + qq[j]) * kTileRows;
+                const RowScale rs = row_scale(p.e, am[j], xs[j]);
+                epilogue_store_pre(p.e, tk[j], nn[j], red[qq[j]][0][tk[j]][col], red[qq[j]][NMAT - 1][tk[j]][col],
+                                   rs.os0, rs.os1, rs.xs, in[j].b0, in[j].b1, in[j].res);
+            }
+        }
     }
 }
 
@@ -800,14 +843,25 @@ __global__ __launch_bounds__(kSmallWaves * 64) void small_split_kernel(MatArgs p
         // every workgroup of the group has arrived: ready for the next launch
         if (tid == 0) __hip_atomic_store(&ss.ctr[group], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    // bias and residual of every output first, then the stores
+    EpiIn in[EPT];
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+        const int e = tid + i * T;
+        const int q = e / (R * 16), rem = e % (R * 16);
+        const int n = (nt0 + q) * kTileRows + (rem & 15);
+        in[i] = epilogue_inputs(p.e, min(rem >> 4, M - 1), min(n, p.e.n - 1));
+    }
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
         const int e = tid + i * T;
         const int q = e / (R * 16), rem = e % (R * 16);
         const int tok = rem >> 4, col = rem & 15;
         const int n = (nt0 + q) * kTileRows + col;
-        if (tok < M && nt0 + q < p.ntiles && n < p.e.n)
-            epilogue_store(p.e, tok, n, tot[i], tot[i], row_scale(p.e, am[i], xs[i]));
+        if (tok < M && nt0 + q < p.ntiles && n < p.e.n) {
+            const RowScale rs = row_scale(p.e, am[i], xs[i]);
+            epilogue_store_pre(p.e, tok, n, tot[i], tot[i], rs.os0, rs.os1, rs.xs, in[i].b0, in[i].b1, in[i].res);
+        }
     }
 }
 
