@@ -40,20 +40,23 @@ __device__ __forceinline__ double wave_sum_f64_lane0(double v) {
 
 // NORM: RowNorm applied before the quantization (FUSEQ only).  STRICT sums
 // the squares of the (single) row in element order on one lane, from LDS.
-// FV: element groups (4 values) per thread.
+// FV: element groups (4 values) per thread.  NTR: adjacent 16-row weight
+// tiles per workgroup (the fused prologue's row loads and quantization are
+// then shared by NTR tiles; tiles past the last read the last tile and store
+// nothing).
 template <int NMAT, int MSUB, int WAVES, bool FUSEQ, int NORM = NORM_NONE, int STRICT = 0,
-          int FV = kFusedVec, int MR = kFusedMaxRows>
+          int FV = kFusedVec, int MR = kFusedMaxRows, int NTR = 1>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2))) void skinny_kernel(MatArgs p) {
     constexpr int T = WAVES * 64;
     constexpr int U = 4 / MSUB;  // K tiles per batch per wave
     extern __shared__ __align__(16) int8_t xq_s[];  // FUSEQ: M rows x ldq (STRICT: k squares first)
-    __shared__ int red[NMAT][MSUB * 16][16];
+    __shared__ int red[NTR][NMAT][MSUB * 16][16];
     __shared__ unsigned amax_bits[kFusedMaxRows];
     __shared__ int xsum_s[kFusedMaxRows];
     __shared__ double nsum[NORM != NORM_NONE ? WAVES : 1][kFusedMaxRows];
     __shared__ float wmax[FUSEQ ? WAVES : 1][kFusedMaxRows];
     __shared__ int wsum[FUSEQ ? WAVES : 1][kFusedMaxRows];
-    const int nt = blockIdx.x;
+    const int nt = blockIdx.x * NTR;  // first weight tile of the workgroup
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
@@ -61,7 +64,9 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
     const int g = lane >> 4;
     const int M = p.e.m;
     const int ktiles = p.ktiles;
-    const size_t tile0 = (size_t)nt * ktiles * 64 + lane;
+    size_t tile0[NTR];
+#pragma unroll
+    for (int q = 0; q < NTR; ++q) tile0[q] = (size_t)min(nt + q, p.ntiles - 1) * ktiles * 64 + lane;
 
     // FUSEQ: the rows (and norm weights) are loaded first, so waiting for them
     // does not also wait for the weight loads queued behind them.
@@ -107,17 +112,20 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
     const uint32_t wbytes = (uint32_t)p.ntiles * (uint32_t)ktiles * 1024u;
     const __amdgpu_buffer_rsrc_t wr0 = buffer_rsrc(p.w0, wbytes);
     const __amdgpu_buffer_rsrc_t wr1 = buffer_rsrc(p.w1, wbytes);
-    uint4 wv[NMAT][U];
+    uint4 wv[NTR][NMAT][U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int kt = wave + u * WAVES;
-        if (FUSEQ) {  // (without a prologue to overlap, skipping the unused loads is cheaper)
-            const uint32_t o = kt < ktiles ? (uint32_t)(tile0 + (size_t)kt * 64) * 16u : wbytes;
-            wv[0][u] = buffer_load16_nt(wr0, o);
-            if (NMAT == 2) wv[NMAT - 1][u] = buffer_load16_nt(wr1, o);
-        } else if (kt < ktiles) {
-            wv[0][u] = load16_nt(p.w0 + tile0 + (size_t)kt * 64);
-            if (NMAT == 2) wv[NMAT - 1][u] = load16_nt(p.w1 + tile0 + (size_t)kt * 64);
+#pragma unroll
+        for (int q = 0; q < NTR; ++q) {
+            if (FUSEQ) {  // (without a prologue to overlap, skipping the unused loads is cheaper)
+                const uint32_t o = kt < ktiles ? (uint32_t)(tile0[q] + (size_t)kt * 64) * 16u : wbytes;
+                wv[q][0][u] = buffer_load16_nt(wr0, o);
+                if (NMAT == 2) wv[q][NMAT - 1][u] = buffer_load16_nt(wr1, o);
+            } else if (kt < ktiles) {
+                wv[q][0][u] = load16_nt(p.w0 + tile0[q] + (size_t)kt * 64);
+                if (NMAT == 2) wv[q][NMAT - 1][u] = load16_nt(p.w1 + tile0[q] + (size_t)kt * 64);
+            }
         }
     }
 
@@ -129,7 +137,8 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
     // residual load measured slower in the norm-fused decode GEMVs (decode
     // 694 -> 678 tokens/s).
     constexpr bool kEarlyIn = !FUSEQ;
-    const int tc0 = min(tid >> 4, M - 1), nc0 = min(nt * kTileRows + (tid & 15), p.e.n - 1);
+    const int tc0 = min((tid % (M * 16)) >> 4, M - 1);
+    const int nc0 = min((nt + min(tid / (M * 16), NTR - 1)) * kTileRows + (tid & 15), p.e.n - 1);
     EpiIn in_first{0.0f, 0.0f, 0.0f};
     if (kEarlyIn) in_first = epilogue_inputs(p.e, tc0, nc0);
     float am_first = 0.0f;
@@ -139,7 +148,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
         xs_first = p.e.xsum[tc0];
     }
 
-    for (int i = tid; i < NMAT * MSUB * 16 * 16; i += T) (&red[0][0][0])[i] = 0;
+    for (int i = tid; i < NTR * NMAT * MSUB * 16 * 16; i += T) (&red[0][0][0][0])[i] = 0;
     if (FUSEQ) {
         if (NORM != NORM_NONE) {
             // ---- sum of squares per row -----------------------------------
@@ -396,11 +405,13 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
     }
 
 
-    v4i acc[NMAT][MSUB];
+    v4i acc[NTR][NMAT][MSUB];
 #pragma unroll
-    for (int a = 0; a < NMAT; ++a)
+    for (int q = 0; q < NTR; ++q)
 #pragma unroll
-        for (int ms = 0; ms < MSUB; ++ms) acc[a][ms] = v4i{0, 0, 0, 0};
+        for (int a = 0; a < NMAT; ++a)
+#pragma unroll
+            for (int ms = 0; ms < MSUB; ++ms) acc[q][a][ms] = v4i{0, 0, 0, 0};
 
     const int8_t* xbase[MSUB];
     bool xval[MSUB];
@@ -414,14 +425,17 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
 
     for (int kb = wave; kb < ktiles; kb += WAVES * U) {
         // next batch's weights, issued before this batch's MFMAs
-        uint4 wn[NMAT][U];
+        uint4 wn[NTR][NMAT][U];
         const int kn = kb + WAVES * U;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int kt = kn + u * WAVES;
             if (kt < ktiles) {
-                wn[0][u] = load16_nt(p.w0 + tile0 + (size_t)kt * 64);
-                if (NMAT == 2) wn[NMAT - 1][u] = load16_nt(p.w1 + tile0 + (size_t)kt * 64);
+#pragma unroll
+                for (int q = 0; q < NTR; ++q) {
+                    wn[q][0][u] = load16_nt(p.w0 + tile0[q] + (size_t)kt * 64);
+                    if (NMAT == 2) wn[q][NMAT - 1][u] = load16_nt(p.w1 + tile0[q] + (size_t)kt * 64);
+                }
             }
         }
         v4i a[MSUB][U][4];
@@ -445,47 +459,58 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
 #pragma unroll
-                    for (int mat = 0; mat < NMAT; ++mat) {
-                        const v4i b = unpack_codes(word_of(wv[mat][u], t));
+                    for (int q = 0; q < NTR; ++q)
 #pragma unroll
-                        for (int ms = 0; ms < MSUB; ++ms)
-                            acc[mat][ms] = mfma_i8(a[ms][u][t], b, acc[mat][ms]);
-                    }
+                        for (int mat = 0; mat < NMAT; ++mat) {
+                            const v4i b = unpack_codes(word_of(wv[q][mat][u], t));
+#pragma unroll
+                            for (int ms = 0; ms < MSUB; ++ms)
+                                acc[q][mat][ms] = mfma_i8(a[ms][u][t], b, acc[q][mat][ms]);
+                        }
                 }
             }
         }
 #pragma unroll
-        for (int mat = 0; mat < NMAT; ++mat)
+        for (int q = 0; q < NTR; ++q)
 #pragma unroll
-            for (int u = 0; u < U; ++u) wv[mat][u] = wn[mat][u];
+            for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+                for (int u = 0; u < U; ++u) wv[q][mat][u] = wn[q][mat][u];
     }
 
     __syncthreads();
 #pragma unroll
-    for (int mat = 0; mat < NMAT; ++mat)
+    for (int q = 0; q < NTR; ++q)
 #pragma unroll
-        for (int ms = 0; ms < MSUB; ++ms)
+        for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int tok = ms * 16 + 4 * g + v;
-                if (tok < M) atomicAdd(&red[mat][tok][r], acc[mat][ms][v]);
-            }
+            for (int ms = 0; ms < MSUB; ++ms)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int tok = ms * 16 + 4 * g + v;
+                    if (tok < M) atomicAdd(&red[q][mat][tok][r], acc[q][mat][ms][v]);
+                }
     __syncthreads();
 
     // Rounds of EB (at most two) outputs per thread; a round loads the inputs
     // of all its outputs before its first store (the first round's first
-    // output's were loaded at the start).
-    constexpr int EB = (MSUB * 256 + T - 1) / T < 2 ? (MSUB * 256 + T - 1) / T : 2;
-    const int total = M * 16;
+    // output's were loaded at the start).  Output idx: tile idx / (16 M),
+    // token (idx mod 16 M) / 16, column idx mod 16.
+    constexpr int EPT = (NTR * MSUB * 256 + T - 1) / T;
+    constexpr int EB = EPT < 2 ? EPT : 2;
+    const int total = NTR * M * 16;
     for (int base = 0; base < total; base += EB * T) {
-        int tk[EB], nn[EB], xs[EB];
+        int tk[EB], nn[EB], xs[EB], qq[EB];
         float am[EB];
         EpiIn in[EB];
 #pragma unroll
         for (int j = 0; j < EB; ++j) {
             const int idx = base + tid + j * T;
-            tk[j] = idx >> 4;
-            nn[j] = nt * kTileRows + (idx & 15);
+            const int q = NTR == 1 ? 0 : idx / (M * 16);
+            const int rem = idx - q * (M * 16);
+            qq[j] = q;
+            tk[j] = rem >> 4;
+            nn[j] = (nt + q) * kTileRows + (rem & 15);
             const int tc = min(tk[j], M - 1), nc = min(nn[j], p.e.n - 1);
             const bool first = j == 0 && base == 0;
             if (FUSEQ) {
@@ -504,11 +529,11 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
 #pragma unroll
         for (int j = 0; j < EB; ++j) {
             const int idx = base + tid + j * T;
-            if (idx < total && nn[j] < p.e.n) {
+            if (idx < total && nt + qq[j] < p.ntiles && nn[j] < p.e.n) {
                 const int col = idx & 15;
                 const RowScale rs = row_scale(p.e, am[j], xs[j]);
-                epilogue_store_pre(p.e, tk[j], nn[j], red[0][tk[j]][col], red[NMAT - 1][tk[j]][col], rs.os0,
-                                   rs.os1, rs.xs, in[j].b0, in[j].b1, in[j].res);
+                epilogue_store_pre(p.e, tk[j], nn[j], red[qq[j]][0][tk[j]][col], red[qq[j]][NMAT - 1][tk[j]][col],
+                                   rs.os0, rs.os1, rs.xs, in[j].b0, in[j].b1, in[j].res);
             }
         }
     }
@@ -884,6 +909,24 @@ template <int NMAT, int WAVES>
 static void launch_fused_w(const MatArgs& p, size_t shm, hipStream_t s) {
     const size_t groups = (size_t)p.e.m * (p.k / 4);
     const dim3 grid(p.ntiles), block(WAVES * 64);
+    // One row, one matrix: a workgroup takes two adjacent weight tiles, so
+    // the row's loads and quantization serve both (the Dense step at the
+    // BitNet-2B up shape: 5.58 -> 5.24 us).  LOOM_AMD_FUSED_NTR = 1, 2 or 4
+    // overrides (tests and tuning).
+    if constexpr (NMAT == 1 && WAVES <= 8) {
+        const char* env = getenv("LOOM_AMD_FUSED_NTR");
+        const int ntr = env && *env ? atoi(env) : 2;
+        if (p.e.m == 1 && groups <= (size_t)2 * WAVES * 64 && ntr == 2) {
+            hipLaunchKernelGGL((skinny_kernel<NMAT, 1, WAVES, true, NORM_NONE, 0, 2, 1, 2>),
+                               dim3(ceil_div(p.ntiles, 2)), block, shm, s, p);
+            return;
+        }
+        if (p.e.m == 1 && groups <= (size_t)2 * WAVES * 64 && ntr == 4) {
+            hipLaunchKernelGGL((skinny_kernel<NMAT, 1, WAVES, true, NORM_NONE, 0, 2, 1, 4>),
+                               dim3(ceil_div(p.ntiles, 4)), block, shm, s, p);
+            return;
+        }
+    }
     if (p.e.m == 1 && groups <= (size_t)2 * WAVES * 64) {
         hipLaunchKernelGGL((skinny_kernel<NMAT, 1, WAVES, true, NORM_NONE, 0, 2, 1>), grid, block, shm, s, p);
     } else if (p.e.m == 1 && groups <= (size_t)4 * WAVES * 64) {

@@ -651,6 +651,20 @@ def test_gemm_tile_order_groups(orc, torch_dev, bn, monkeypatch, group):
     _check_dense(orc, torch_dev, bn, m, x)
 
 
+@pytest.mark.parametrize("ntr", ["1", "2", "4"])
+@pytest.mark.parametrize("rows,cols", [(6912, 2560), (2560, 6912), (1000, 2560), (40, 1000), (33, 260)])
+def test_fused_row_tiles_per_workgroup(orc, torch_dev, bn, monkeypatch, ntr, rows, cols):
+    # M = 1 with the quantization fused: one, two or four 16-row weight tiles
+    # per workgroup (ragged last groups: 63 and 3 tiles, a partial last tile
+    # of 33 rows), plain and with residual + ReLU: bit-exact
+    monkeypatch.setenv("LOOM_AMD_FUSED_NTR", ntr)
+    m = orc.random_matrix(rows, cols, seed=rows + cols)
+    x = orc.normal_f32(cols, seed=cols + 1).reshape(1, cols)
+    res = orc.normal_f32(rows, seed=rows + 2).reshape(1, rows)
+    _check_dense(orc, torch_dev, bn, m, x)
+    _check_dense(orc, torch_dev, bn, m, x, activation=0, residual=res)
+
+
 @pytest.mark.parametrize("nt", ["split", "1", "2", "4"])
 @pytest.mark.parametrize("rows,cols,M", [(6912, 2560, 64), (2560, 6912, 40), (1000, 2570, 17),
                                          (6900, 2560, 33), (40000, 512, 20)])
