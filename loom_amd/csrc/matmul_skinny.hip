@@ -415,13 +415,16 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
 
     const int8_t* xbase[MSUB];
     bool xval[MSUB];
+    uint32_t xoff[MSUB];  // pre-quantized rows: byte offsets (rows past M read zero)
 #pragma unroll
     for (int ms = 0; ms < MSUB; ++ms) {
         const int row = ms * 16 + r;
         xval[ms] = row < M;
         const int rr = xval[ms] ? row : 0;
         xbase[ms] = (FUSEQ ? (const int8_t*)xq_s : p.xq) + (size_t)rr * p.ldq + g * 16;
+        xoff[ms] = (uint32_t)row * (uint32_t)p.ldq + (uint32_t)g * 16u;
     }
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(p.xq, FUSEQ ? 0u : (uint32_t)M * (uint32_t)p.ldq);
 
     for (int kb = wave; kb < ktiles; kb += WAVES * U) {
         // next batch's weights, issued before this batch's MFMAs
@@ -445,10 +448,18 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
             if (kt < ktiles) {
 #pragma unroll
                 for (int ms = 0; ms < MSUB; ++ms) {
-                    const int8_t* xp = xbase[ms] + (size_t)kt * kTileCols;
+                    if (FUSEQ) {
+                        const int8_t* xp = xbase[ms] + (size_t)kt * kTileCols;
 #pragma unroll
-                    for (int t = 0; t < 4; ++t)
-                        a[ms][u][t] = xval[ms] ? *(const v4i*)(xp + 64 * t) : v4i{0, 0, 0, 0};
+                        for (int t = 0; t < 4; ++t)
+                            a[ms][u][t] = xval[ms] ? *(const v4i*)(xp + 64 * t) : v4i{0, 0, 0, 0};
+                    } else {
+                        // rows past M fall past the buffer's end: zero, no branch
+#pragma unroll
+                        for (int t = 0; t < 4; ++t)
+                            a[ms][u][t] = __builtin_bit_cast(
+                                v4i, buffer_load16(xr, xoff[ms] + (uint32_t)kt * kTileCols + 64u * t));
+                    }
                 }
             }
         }
@@ -488,7 +499,9 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     const int tok = ms * 16 + 4 * g + v;
-                    if (tok < M) atomicAdd(&red[q][mat][tok][r], acc[q][mat][ms][v]);
+                    // (rows past M multiplied zero activations: their zero sums go
+                    // to rows the epilogue never reads, with no branch)
+                    if (!FUSEQ || tok < M) atomicAdd(&red[q][mat][tok][r], acc[q][mat][ms][v]);
                 }
     __syncthreads();
 
@@ -587,14 +600,10 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_nt_kernel(MatArgs p) {
 #pragma unroll
             for (int ms = 0; ms < MSUB; ++ms) acc[q][a][ms] = v4i{0, 0, 0, 0};
 
-    const int8_t* xbase[MSUB];
-    bool xval[MSUB];
+    uint32_t xoff[MSUB];  // byte offsets of this lane's rows (rows past M read zero)
 #pragma unroll
-    for (int ms = 0; ms < MSUB; ++ms) {
-        const int row = ms * 16 + r;
-        xval[ms] = row < M;
-        xbase[ms] = p.xq + (size_t)(xval[ms] ? row : 0) * p.ldq + g * 16;
-    }
+    for (int ms = 0; ms < MSUB; ++ms) xoff[ms] = (uint32_t)(ms * 16 + r) * (uint32_t)p.ldq + (uint32_t)g * 16u;
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(p.xq, (uint32_t)M * (uint32_t)p.ldq);
 
     for (int kb = wave; kb < ktiles; kb += WAVES * U) {
         uint4 wn[NT][NMAT][U];
@@ -616,12 +625,11 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_nt_kernel(MatArgs p) {
             const int kt = kb + u * WAVES;
             if (kt < ktiles) {
 #pragma unroll
-                for (int ms = 0; ms < MSUB; ++ms) {
-                    const int8_t* xp = xbase[ms] + (size_t)kt * kTileCols;
+                for (int ms = 0; ms < MSUB; ++ms)
 #pragma unroll
-                    for (int t = 0; t < 4; ++t)
-                        a[ms][u][t] = xval[ms] ? *(const v4i*)(xp + 64 * t) : v4i{0, 0, 0, 0};
-                }
+                    for (int t = 0; t < 4; ++t)  // rows past M fall past the buffer's end: zero, no branch
+                        a[ms][u][t] = __builtin_bit_cast(
+                            v4i, buffer_load16(xr, xoff[ms] + (uint32_t)kt * kTileCols + 64u * t));
             }
         }
 #pragma unroll
@@ -659,7 +667,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_nt_kernel(MatArgs p) {
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     const int tok = ms * 16 + 4 * g + v;
-                    if (tok < M) atomicAdd(&red[q][mat][tok][r], acc[q][mat][ms][v]);
+                    atomicAdd(&red[q][mat][tok][r], acc[q][mat][ms][v]);  // rows past M add zero
                 }
     __syncthreads();
 
@@ -959,6 +967,18 @@ static hipError_t launch_skinny(const MatArgs& p, hipStream_t s) {
                 break;
         }
         return hipGetLastError();
+    }
+    if constexpr (!FUSEQ && NMAT == 1 && MSUB == 1) {
+        // Up to 16 pre-quantized rows, one matrix, eight waves: two weight tiles
+        // per workgroup share the rows' loads (BitNet-2B up shape: M = 1
+        // 4.10 -> 3.91 us, M = 8 4.77 -> 4.43, M = 16 5.59 -> 4.89).
+        // LOOM_AMD_SKINNY_NTR = 1 takes one tile (tests and tuning).
+        const char* env = getenv("LOOM_AMD_SKINNY_NTR");
+        if (w == 8 && !(env && atoi(env) == 1)) {
+            hipLaunchKernelGGL((skinny_kernel<NMAT, MSUB, 8, FUSEQ, NORM_NONE, 0, kFusedVec, kFusedMaxRows, 2>),
+                               dim3(ceil_div(p.ntiles, 2)), dim3(512), shm, s, p);
+            return hipGetLastError();
+        }
     }
     switch (w) {
         case 1:

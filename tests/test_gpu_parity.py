@@ -535,6 +535,11 @@ def test_entity_blob_upload_matches_words(orc, torch_dev, bn):
     ob = bn.ternary_matvec_quantized(b, q)
     torch.cuda.synchronize()
     assert torch.equal(oa, ob)
+    # and the blob-built matrix's Dense forward equals the oracle bit for bit
+    x = orc.normal_f32(3 * 300, 5).reshape(3, 300)
+    pre, _ = bn.dense_forward_packed_ternary(a, to_dev(torch, x))
+    torch.cuda.synchronize()
+    assert pre.cpu().numpy().tobytes() == orc.dense_forward(m, x, simd=True).pre.tobytes()
 
 
 def test_library_errors_are_loud(orc, torch_dev, bn):
