@@ -670,6 +670,21 @@ def test_fused_row_tiles_per_workgroup(orc, torch_dev, bn, monkeypatch, ntr, row
     _check_dense(orc, torch_dev, bn, m, x, activation=0, residual=res)
 
 
+@pytest.mark.parametrize("ntr", ["1", "2"])
+@pytest.mark.parametrize("rows,cols,M", [(6912, 2560, 5), (6912, 2560, 16), (1000, 2560, 8), (40, 1000, 13)])
+def test_prequantized_row_tiles_per_workgroup(orc, torch_dev, bn, monkeypatch, ntr, rows, cols, M):
+    # 4 < M <= 16 (quantized by its own kernel, then the skinny GEMV on the
+    # int8 rows, read branch-free: rows past M fall past the buffer's end):
+    # one or two 16-row weight tiles per workgroup (ragged last groups of 63
+    # and 3 tiles), plain and with residual + ReLU: bit-exact
+    monkeypatch.setenv("LOOM_AMD_SKINNY_NTR", ntr)
+    m = orc.random_matrix(rows, cols, seed=rows + M)
+    x = orc.normal_f32(M * cols, seed=M + 3).reshape(M, cols)
+    res = orc.normal_f32(M * rows, seed=M + 4).reshape(M, rows)
+    _check_dense(orc, torch_dev, bn, m, x)
+    _check_dense(orc, torch_dev, bn, m, x, activation=0, residual=res)
+
+
 @pytest.mark.parametrize("nt", ["split", "1", "2", "4"])
 @pytest.mark.parametrize("rows,cols,M", [(6912, 2560, 64), (2560, 6912, 40), (1000, 2570, 17),
                                          (6900, 2560, 33), (40000, 512, 20)])
