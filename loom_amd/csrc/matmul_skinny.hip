@@ -449,10 +449,11 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
 #pragma unroll
                 for (int ms = 0; ms < MSUB; ++ms) {
                     if (FUSEQ) {
+                        // rows past M read row 0 of the LDS copy (xbase clamps
+                        // them); their sums are never added to the reduction
                         const int8_t* xp = xbase[ms] + (size_t)kt * kTileCols;
 #pragma unroll
-                        for (int t = 0; t < 4; ++t)
-                            a[ms][u][t] = xval[ms] ? *(const v4i*)(xp + 64 * t) : v4i{0, 0, 0, 0};
+                        for (int t = 0; t < 4; ++t) a[ms][u][t] = *(const v4i*)(xp + 64 * t);
                     } else {
                         // rows past M fall past the buffer's end: zero, no branch
 #pragma unroll
