@@ -596,9 +596,9 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": pmc_traffic(),
-                     "kernel": "skinny_kernel<1,1,8,true,...,NTR=2> (fused act-quant + ternary "
-                               "GEMV + epilogue, two 16-row weight tiles per workgroup: the step's "
-                               "only launch)",
+                     "kernel": "skinny_kernel<1,1,4,true,0,0,4,1,2> (fused act-quant + ternary "
+                               "GEMV + epilogue; four waves, two 16-row weight tiles per workgroup: "
+                               "the step's only launch)",
                      "us_per_launch": round(ms_step * 1e3, 3), "bytes_per_launch": b1,
                      "us_prequantized_kernel": round(ms_kernel * 1e3, 3),
                      "GBs_prequantized_kernel": round(b1 / (ms_kernel * 1e-3) / 1e9, 1),

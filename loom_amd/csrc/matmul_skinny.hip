@@ -920,8 +920,9 @@ static void launch_fused_w(const MatArgs& p, size_t shm, hipStream_t s) {
     const dim3 grid(p.ntiles), block(WAVES * 64);
     // One row, one matrix: a workgroup takes two adjacent weight tiles, so
     // the row's loads and quantization serve both (the Dense step at the
-    // BitNet-2B up shape: 5.58 -> 5.24 us).  LOOM_AMD_FUSED_NTR = 1, 2 or 4
-    // overrides (tests and tuning).
+    // BitNet-2B up shape, eight waves: 5.58 -> 5.24 us).  LOOM_AMD_FUSED_NTR =
+    // 1, 2 or 4 overrides (tests and tuning; four tiles only with two float4
+    // slots a thread).
     if constexpr (NMAT == 1 && WAVES <= 8) {
         const char* env = getenv("LOOM_AMD_FUSED_NTR");
         const int ntr = env && *env ? atoi(env) : 2;
@@ -933,6 +934,11 @@ static void launch_fused_w(const MatArgs& p, size_t shm, hipStream_t s) {
         if (p.e.m == 1 && groups <= (size_t)2 * WAVES * 64 && ntr == 4) {
             hipLaunchKernelGGL((skinny_kernel<NMAT, 1, WAVES, true, NORM_NONE, 0, 2, 1, 4>),
                                dim3(ceil_div(p.ntiles, 4)), block, shm, s, p);
+            return;
+        }
+        if (p.e.m == 1 && groups <= (size_t)4 * WAVES * 64 && ntr == 2) {
+            hipLaunchKernelGGL((skinny_kernel<NMAT, 1, WAVES, true, NORM_NONE, 0, 4, 1, 2>),
+                               dim3(ceil_div(p.ntiles, 2)), block, shm, s, p);
             return;
         }
     }
@@ -956,7 +962,19 @@ static hipError_t launch_skinny(const MatArgs& p, hipStream_t s) {
     }
     const size_t shm = FUSEQ ? (size_t)p.e.m * p.ldq : 0;
     const dim3 grid(p.ntiles);
+    if constexpr (FUSEQ && NMAT == 1) {
+        // One row that four waves hold in four float4 slots a thread: four-wave
+        // workgroups with two weight tiles each instead of eight-wave ones
+        // (BitNet-2B up shape: 5.15 -> 4.81 us per Dense step; two waves 7.40)
+        if (w == 8 && p.e.m == 1 && (size_t)p.k / 4 <= (size_t)4 * 4 * 64) w = 4;
+    }
     if constexpr (FUSEQ) {
+        const char* fw = getenv("LOOM_AMD_FUSED_WAVES");  // tuning override (1..16)
+        if (fw && *fw) {
+            const int v = atoi(fw);
+            if (v == 1 || v == 2 || v == 4 || v == 8 || (v == 16 && kCap == 16)) w = v;
+            while (w < kCap && (size_t)p.e.m * p.k > (size_t)4 * kFusedVec * 64 * w) w <<= 1;
+        }
         static_assert(MSUB == 1, "the fused prologue serves up to 4 rows");
         switch (w) {
             case 1: launch_fused_w<NMAT, 1>(p, shm, s); break;

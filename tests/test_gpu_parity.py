@@ -663,6 +663,8 @@ def test_fused_row_tiles_per_workgroup(orc, torch_dev, bn, monkeypatch, ntr, row
     # per workgroup (ragged last groups: 63 and 3 tiles, a partial last tile
     # of 33 rows), plain and with residual + ReLU: bit-exact
     monkeypatch.setenv("LOOM_AMD_FUSED_NTR", ntr)
+    if ntr == "4":
+        monkeypatch.setenv("LOOM_AMD_FUSED_WAVES", "8")  # four tiles: eight-wave workgroups
     m = orc.random_matrix(rows, cols, seed=rows + cols)
     x = orc.normal_f32(cols, seed=cols + 1).reshape(1, cols)
     res = orc.normal_f32(rows, seed=rows + 2).reshape(1, rows)
