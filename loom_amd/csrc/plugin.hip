@@ -5,8 +5,11 @@
 //                   (poly/dense.go:66-101); weights: one BITNET_TERNARY blob.
 //   "BitNetSwiGLU"  one ternary SwiGLU FFN, SwiGLUForwardPackedTernaryCPU
 //                   (poly/swiglu.go:270-322); weights: gate, up, down blobs,
-//                   then optionally n fp32 inner-norm weights.
-// dtype "TERNARY"; size_label "m=..,k=..,n=..[,act=..][,eps=..][,norm=strict|fast]".
+//                   then optionally n fp32 inner-norm weights, then (with
+//                   bias=1) the 2n + k fp32 biases [gate | up | down] of the
+//                   layer's Master tail (poly/swiglu.go:276-281).
+// dtype "TERNARY"; size_label
+// "m=..,k=..,n=..[,act=..][,eps=..][,norm=strict|fast][,bias=0|1]".
 // Only device "GPU" exists: loom's own CPU path is the CPU implementation.
 #include "api_util.hpp"
 #include "lamd.hpp"
@@ -35,6 +38,7 @@ struct loom_accel_compiled_layer {
     int device = 0;
     loom_amd_matrix* w[3] = {nullptr, nullptr, nullptr};
     float* d_norm = nullptr;
+    float* d_bias = nullptr;
     float* d_in = nullptr;
     float* d_out = nullptr;
     // pinned staging of the caller's host buffers: copies between pageable
@@ -68,6 +72,7 @@ struct Spec {
     int activation = -1;
     double eps = 1e-5;
     int norm_mode = LOOM_AMD_NORM_STRICT;
+    int bias = 0;
 };
 
 bool parse_int(const std::string& v, int* out) {
@@ -127,6 +132,9 @@ bool parse_desc(const loom_accel_layer_desc* desc, Spec* s, std::string* why) {
             have_n = true;
         } else if (key == "act") {
             ok = parse_int(val, &s->activation) && s->activation >= -1 && s->activation <= 6;
+        } else if (key == "bias") {
+            ok = s->kind == 1 && (val == "0" || val == "1");
+            s->bias = val == "1";
         } else if (key == "eps") {
             char* end = nullptr;
             s->eps = strtod(val.c_str(), &end);
@@ -158,9 +166,13 @@ size_t blob_bytes(int rows, int cols) {
     return 24 + (size_t)rows * (size_t)((cols + 15) / 16) * 4;
 }
 
+size_t spec_bias_bytes(const Spec& s) {
+    return s.kind == 1 && s.bias ? (size_t)(2 * s.n + s.k) * 4 : 0;
+}
+
 size_t spec_weight_bytes(const Spec& s) {
     if (s.kind == 0) return blob_bytes(s.n, s.k);
-    return 2 * blob_bytes(s.n, s.k) + blob_bytes(s.k, s.n) + (size_t)s.n * 4;
+    return 2 * blob_bytes(s.n, s.k) + blob_bytes(s.k, s.n) + (size_t)s.n * 4 + spec_bias_bytes(s);
 }
 
 int read_blob_shape(const uint8_t* p, size_t len, int* rows, int* cols) {
@@ -180,6 +192,7 @@ void release(loom_accel_compiled_layer* l) {
         w = nullptr;
     }
     if (l->d_norm) (void)hipFree(l->d_norm);
+    if (l->d_bias) (void)hipFree(l->d_bias);
     if (l->d_in) (void)hipFree(l->d_in);
     if (l->d_out) (void)hipFree(l->d_out);
     if (l->h_in) (void)hipHostFree(l->h_in);
@@ -204,7 +217,7 @@ int run(loom_accel_compiled_layer* l, std::string* why) {
                                     l->activation != -1 ? l->d_out : nullptr, nullptr, nullptr,
                                     l->stream);
     } else {
-        rc = loom_amd_swiglu_forward(l->w[0], l->w[1], l->w[2], nullptr, l->d_norm, l->eps,
+        rc = loom_amd_swiglu_forward(l->w[0], l->w[1], l->w[2], l->d_bias, l->d_norm, l->eps,
                                      l->activation, l->norm_mode, l->d_in, l->m, l->d_out,
                                      nullptr, nullptr, nullptr, l->stream);
     }
@@ -340,9 +353,16 @@ int loom_accel_compile_layer(loom_accel_plugin* plugin, const loom_accel_layer_d
     if (e == hipSuccess) e = hipMalloc(&l->d_out, l->out_bytes);
     if (e == hipSuccess) e = hipHostMalloc(&l->h_in, l->in_bytes, hipHostMallocDefault);
     if (e == hipSuccess) e = hipHostMalloc(&l->h_out, l->out_bytes, hipHostMallocDefault);
-    if (e == hipSuccess && s.kind == 1 && left == (size_t)s.n * 4) {
-        e = hipMalloc(&l->d_norm, left);
-        if (e == hipSuccess) e = hipMemcpy(l->d_norm, p, left, hipMemcpyHostToDevice);
+    const size_t bias_bytes = spec_bias_bytes(s);
+    if (e == hipSuccess && s.kind == 1 && left == (size_t)s.n * 4 + bias_bytes) {
+        e = hipMalloc(&l->d_norm, (size_t)s.n * 4);
+        if (e == hipSuccess) e = hipMemcpy(l->d_norm, p, (size_t)s.n * 4, hipMemcpyHostToDevice);
+        p += (size_t)s.n * 4;
+        left -= (size_t)s.n * 4;
+    }
+    if (e == hipSuccess && bias_bytes) {
+        e = hipMalloc(&l->d_bias, bias_bytes);
+        if (e == hipSuccess) e = hipMemcpy(l->d_bias, p, bias_bytes, hipMemcpyHostToDevice);
     }
     if (prev >= 0) (void)hipSetDevice(prev);
     if (e != hipSuccess) {

@@ -66,10 +66,17 @@ def test_weight_bytes_contract(amd_lib):
     assert wb("BitNetLinear", "TERNARY", "m=3,k=17,n=3") == 24 + 3 * 2 * 4
     assert wb("BitNetSwiGLU", "TERNARY", "m=1,k=2560,n=6912") == (
         2 * (24 + 6912 * 160 * 4) + 24 + 2560 * 432 * 4 + 6912 * 4)
+    # bias=1: the Master-tail biases [gate | up | down] follow the norm weights
+    assert wb("BitNetSwiGLU", "TERNARY", "m=1,k=2560,n=6912,bias=1") == (
+        2 * (24 + 6912 * 160 * 4) + 24 + 2560 * 432 * 4 + 6912 * 4 + (2 * 6912 + 2560) * 4)
+    assert wb("BitNetSwiGLU", "TERNARY", "m=1,k=2560,n=6912,bias=0") == wb(
+        "BitNetSwiGLU", "TERNARY", "m=1,k=2560,n=6912")
     for bad in [("Dense", "TERNARY", "m=1,k=4,n=4"), ("BitNetLinear", "INT8", "m=1,k=4,n=4"),
                 ("BitNetLinear", "TERNARY", "medium"), ("BitNetLinear", "TERNARY", "m=1,k=4"),
                 ("BitNetLinear", "TERNARY", "m=0,k=4,n=4"), ("BitNetLinear", "TERNARY",
-                                                             "m=1,k=4,n=4,norm=loose")]:
+                                                             "m=1,k=4,n=4,norm=loose"),
+                ("BitNetLinear", "TERNARY", "m=1,k=4,n=4,bias=1"),  # loom's Dense has no bias
+                ("BitNetSwiGLU", "TERNARY", "m=1,k=4,n=4,bias=2")]:
         assert wb(*bad) == 0, bad
     assert amd_lib.loom_accel_weight_bytes(None) == 0
 
@@ -106,3 +113,25 @@ def test_c_loader_conformance(amd_lib, tmp_path):
     proc = subprocess.run([str(exe), _lib.LIB_PATH, "1" if gpu_visible() else "0"],
                           capture_output=True, text=True)
     assert proc.returncode == 0, proc.stdout + proc.stderr
+
+
+def test_drift_spectrum_classifier():
+    # classifyDrift's buckets (lucy/examples/apple/spectrum.go:37-58) at and
+    # either side of each edge; maxAbsDiffTensor's NaN rule and size mismatch
+    # (lucy/examples/apple/dispatch.go:205-238)
+    import numpy as np
+    from tests import spectrum as sp
+    tol = 1e-7
+    cases = [(0.0, sp.EXACT), (5e-8, sp.INDUS), (1e-7, sp.INDUS), (1.0000001e-7, sp.LOWBIT),
+             (1e-6, sp.LOWBIT), (1.01e-6, sp.DRIFT), (0.1, sp.DRIFT), (0.10001, sp.H_DRIFT),
+             (1.0, sp.H_DRIFT), (1.5, sp.BROKE), (float("nan"), sp.FATAL),
+             (float("inf"), sp.FATAL)]
+    for diff, want in cases:
+        assert sp.classify(diff, tol) == want, (diff, sp.LABELS[want])
+    assert sp.infer_tolerance("FP32") == 1e-7 and sp.infer_tolerance("TERNARY") == 1e-7
+    assert sp.gpu_parity_tolerance("FP32") == 0.1
+    a = np.array([1.0, np.nan, 3.0], np.float32)
+    b = np.array([1.0, 2.0, 3.5], np.float32)
+    assert sp.max_abs_diff(a, b) == 0.5          # NaN difference skipped
+    assert sp.max_abs_diff(a, b[:2]) == np.finfo(np.float64).max
+    assert sp.histogram(a, b, tol) == [1, 0, 0, 0, 1, 0, 1]

@@ -162,12 +162,33 @@ def _check_dense(orc, torch, bn, m, x, activation=-1, residual=None):
     assert pre2.cpu().numpy().tobytes() == want_pre.tobytes(), "fp32 output without taps"
     if activation != -1:
         if residual is None:
-            got = post.cpu().numpy()
-            if activation in (0, 6):
-                assert got.tobytes() == ref.post.tobytes()
-            else:  # exp/tanh last-bit freedom: <= 1 ulp
-                assert ulp_diff_f32(got, ref.post).max() <= 1
+            check_activation(activation, ref.pre, post.cpu().numpy(), ref.post)
     return M
+
+
+def check_activation(act, pre, got, want):
+    """loom's Activate (poly/poly.go:167-200) on the device against the oracle.
+
+    ReLU (0), LeakyReLU (5), ReLU2 (6) and linear use IEEE basic operations
+    only: bit-exact.  SiLU (1), Tanh (3) and Sigmoid (4) round an exp/tanh
+    value to fp32, whose last fp64 bit differs between libraries: <= 1 fp32 ulp.
+    GELU (2) also forms 1 + tanh(z), which cancels for pre < 0: <= 1 fp32 ulp,
+    or, where the cancellation leaves fewer than 24 correct bits in loom's own
+    fp64 arithmetic, within 0.5*|pre|*4*2^-53 (tanh's last bits times the
+    factor 0.5*pre) plus one fp32 rounding."""
+    got = np.asarray(got, np.float32)
+    want = np.asarray(want, np.float32)
+    if act in (-1, 0, 5, 6) or act > 6 or act < -1:
+        assert got.tobytes() == want.tobytes(), f"activation {act}: bit-exact"
+        return
+    d = ulp_diff_f32(got, want)
+    if act != 2:
+        assert d.max() <= 1, f"activation {act}: {int(d.max())} ulps"
+        return
+    p64 = np.asarray(pre, np.float64)
+    bound = 0.5 * np.abs(p64) * 4 * 2.0**-53 + np.abs(want.astype(np.float64)) * 2.0**-23
+    far = np.abs(got.astype(np.float64) - want.astype(np.float64)) > bound
+    assert not np.any((d > 1) & far), f"GELU: {int(np.count_nonzero((d > 1) & far))} outside the bar"
 
 
 @pytest.mark.parametrize("rows,cols", LOOM_SHAPES)
@@ -225,13 +246,27 @@ def test_dense_fused_quant_edge_rows(orc, torch_dev, bn, M):
         assert pre.cpu().numpy().tobytes() == ref.pre.tobytes()
 
 
-@pytest.mark.parametrize("act", [0, 1, 6])
+@pytest.mark.parametrize("act", [0, 1, 2, 3, 4, 5, 6])
 def test_dense_activation_and_residual(orc, torch_dev, bn, act):
     m = orc.random_matrix(96, 160, seed=5)
     x = orc.normal_f32(9 * 160, seed=6).reshape(9, 160)
     _check_dense(orc, torch_dev, bn, m, x, activation=act)
     res = orc.normal_f32(9 * 96, seed=8).reshape(9, 96)
     _check_dense(orc, torch_dev, bn, m, x, residual=res)
+
+
+@pytest.mark.parametrize("act", [-1, 0, 1, 2, 3, 4, 5, 6, 9])
+@pytest.mark.parametrize("M", [1, 9, 40, 256, 300])
+def test_dense_every_activation_on_every_kernel(orc, torch_dev, bn, act, M):
+    # Activate(pre) for every id of poly/poly.go:90-97 (and an unknown id,
+    # which loom treats as linear) through each matmul family: the fused
+    # M = 1 GEMV, the small-M kernels, the GEMM's full-tile epilogue (M = 256
+    # of 128-token tiles, N = 512 of 256-row tiles) and its ragged edge
+    # (M = 300).  Inputs scaled by 30 put pre in about [-8, 8], across the
+    # curved parts of every activation.
+    m = orc.random_matrix(512, 640, seed=40 + M)
+    x = orc.normal_f32(M * 640, seed=41 + M).reshape(M, 640) * np.float32(30.0)
+    _check_dense(orc, torch_dev, bn, m, x, activation=act)
 
 
 def test_config0_gemv_bit_exact(orc, torch_dev, bn):
@@ -309,18 +344,24 @@ def test_norm_quant_fast_within_one_ulp(orc, torch_dev, bn):
 
 
 # ---------------------------------------------------------------- SwiGLU
-def _swiglu_case(orc, torch, bn, hidden, inter, M, seed, norm, with_norm_w, act=1):
+def _swiglu_case(orc, torch, bn, hidden, inter, M, seed, norm, with_norm_w, act=1,
+                 with_bias=False):
     g = orc.random_matrix(inter, hidden, seed=seed)
     u = orc.random_matrix(inter, hidden, seed=seed + 1)
     d = orc.random_matrix(hidden, inter, seed=seed + 2)
     wn = orc.uniform_f32(inter, 0.5, 1.5, seed=seed + 3) if with_norm_w else None
     x = orc.normal_f32(M * hidden, seed=seed + 4).reshape(M, hidden)
+    # loom's Master-tail biases [gate inter | up inter | down hidden]
+    # (poly/swiglu.go:276-281, poly/bitnet_cpu.go:521-526)
+    bias = orc.normal_f32(2 * inter + hidden, seed=seed + 5) * np.float32(0.25) if with_bias else None
     G, U, D = gpu_matrix(bn, g), gpu_matrix(bn, u), gpu_matrix(bn, d)
     h, out, t = bn.swiglu_forward_packed_ternary(
         G, U, D, to_dev(torch, x), inner_norm=None if wn is None else to_dev(torch, wn),
-        eps=1e-5, activation=act, norm=norm, taps=True)
+        eps=1e-5, activation=act, norm=norm, taps=True,
+        bias=None if bias is None else to_dev(torch, bias))
     torch.cuda.synchronize()
-    ref = orc.swiglu_forward(g, u, d, x, inner_norm=wn, eps=1e-5, activation=act, simd=True)
+    ref = orc.swiglu_forward(g, u, d, x, inner_norm=wn, bias=bias, eps=1e-5, activation=act,
+                             simd=True)
     # integer stages before the gate: bit-exact
     assert np.array_equal(t.xq.cpu().numpy(), ref.xq)
     assert t.amax.cpu().numpy().tobytes() == ref.amax.tobytes()
@@ -336,8 +377,9 @@ def _swiglu_case(orc, torch, bn, hidden, inter, M, seed, norm, with_norm_w, act=
     acc_down_ref = np.stack([orc.matvec_scalar(d, hq_ref[i], orc.output_scale(d.scale, hamax_ref[i]))[1]
                              for i in range(M)])
     assert np.array_equal(t.acc_down.cpu().numpy(), acc_down_ref)
-    out_ref = np.stack([(acc_down_ref[i].astype(np.float64) * orc.output_scale(d.scale, hamax_ref[i]))
-                        .astype(np.float32) for i in range(M)])
+    bias_d = 0.0 if bias is None else bias[2 * inter:].astype(np.float64)
+    out_ref = np.stack([(acc_down_ref[i].astype(np.float64) * orc.output_scale(d.scale, hamax_ref[i])
+                         + bias_d).astype(np.float32) for i in range(M)])
     assert out.cpu().numpy().tobytes() == out_ref.tobytes()
     return hg, ref
 
@@ -353,6 +395,23 @@ def test_swiglu_small(orc, torch_dev, bn, norm, M):
 def test_swiglu_relu2_and_silu(orc, torch_dev, bn, act):
     _swiglu_case(orc, torch_dev, bn, hidden=128, inter=320, M=3, seed=21, norm="strict",
                  with_norm_w=False, act=act)
+
+
+@pytest.mark.parametrize("norm", ["strict", "fast"])
+@pytest.mark.parametrize("act", [1, 6])
+@pytest.mark.parametrize("M", [1, 3, 40, 100])
+def test_swiglu_biases(orc, torch_dev, bn, norm, act, M):
+    # gate/up biases enter in fp64 before the gate product, the down bias
+    # after the down matvec (poly/swiglu.go:303-320): through the fused M = 1
+    # GEMV, the small-M kernels and the GEMM epilogue
+    _swiglu_case(orc, torch_dev, bn, hidden=256, inter=640, M=M, seed=70 + M, norm=norm,
+                 with_norm_w=True, act=act, with_bias=True)
+
+
+@pytest.mark.parametrize("M", [1, 256])
+def test_swiglu_biases_bitnet_2b_shape(orc, torch_dev, bn, M):
+    _swiglu_case(orc, torch_dev, bn, hidden=2560, inter=6912, M=M, seed=90 + M, norm="strict",
+                 with_norm_w=True, with_bias=True)
 
 
 @pytest.mark.parametrize("M", [1, 64, 256])
@@ -390,6 +449,28 @@ def test_plugin_bitnet_linear(orc, torch_dev):
         p.close()
 
 
+@pytest.mark.parametrize("act", [1, 2, 3, 4, 5])
+def test_plugin_bitnet_linear_activations(orc, torch_dev, act):
+    # the size label's act=<id> reaches Activate (poly/dense.go:94-98): the
+    # plugin hands back postAct, as DispatchAccelForward does
+    # (poly/accel_intel.go:223-225)
+    from loom_amd import accel
+    n, k, M = 384, 512, 5
+    m = orc.random_matrix(n, k, seed=60 + act)
+    x = orc.normal_f32(M * k, seed=61 + act).reshape(M, k) * np.float32(30.0)
+    p = accel.open_amd(device="GPU")
+    try:
+        res = p.compile_layer(accel.LayerDesc("BitNetLinear", "TERNARY", f"m={M},k={k},n={n},act={act}"),
+                              m.entity_blob())
+        out = bytearray(res.out_bytes)
+        res.layer.infer(x.tobytes(), out)
+        ref = orc.dense_forward(m, x, activation=act, simd=True)
+        check_activation(act, ref.pre, np.frombuffer(bytes(out), np.float32).reshape(M, n), ref.post)
+        res.layer.release()
+    finally:
+        p.close()
+
+
 def test_plugin_bitnet_swiglu(orc, torch_dev):
     from loom_amd import accel
     hidden, inter, M = 128, 320, 3
@@ -409,6 +490,37 @@ def test_plugin_bitnet_swiglu(orc, torch_dev):
         ref = orc.swiglu_forward(g, u, d, x, inner_norm=wn, eps=1e-5, simd=True)
         got = np.frombuffer(bytes(out), np.float32).reshape(M, hidden)
         assert ulp_diff_f32(got, ref.out).max() <= 1 or np.array_equal(got, ref.out)
+        res.layer.release()
+    finally:
+        p.close()
+
+
+@pytest.mark.parametrize("with_norm", [True, False])
+def test_plugin_bitnet_swiglu_biases(orc, torch_dev, with_norm):
+    # bias=1: the blob ends with loom's Master-tail biases [gate | up | down]
+    # (poly/swiglu.go:276-281), after the optional inner-norm weights
+    from loom_amd import accel
+    hidden, inter, M = 128, 320, 2
+    g = orc.random_matrix(inter, hidden, seed=41)
+    u = orc.random_matrix(inter, hidden, seed=42)
+    d = orc.random_matrix(hidden, inter, seed=43)
+    wn = orc.uniform_f32(inter, 0.5, 1.5, seed=44) if with_norm else None
+    bias = orc.normal_f32(2 * inter + hidden, seed=45) * np.float32(0.25)
+    x = orc.normal_f32(M * hidden, seed=46).reshape(M, hidden)
+    p = accel.open_amd(device="GPU")
+    try:
+        desc = accel.LayerDesc("BitNetSwiGLU", "TERNARY", f"m={M},k={hidden},n={inter},bias=1")
+        blob = g.entity_blob() + u.entity_blob() + d.entity_blob()
+        blob += (wn.tobytes() if with_norm else b"") + bias.tobytes()
+        res = p.compile_layer(desc, blob)
+        out = bytearray(res.out_bytes)
+        res.layer.infer(x.tobytes(), out)
+        ref = orc.swiglu_forward(g, u, d, x, inner_norm=wn, bias=bias, eps=1e-5, simd=True)
+        got = np.frombuffer(bytes(out), np.float32).reshape(M, hidden)
+        assert ulp_diff_f32(got, ref.out).max() <= 1
+        # the biases are not ignored: without them the output differs
+        ref0 = orc.swiglu_forward(g, u, d, x, inner_norm=wn, eps=1e-5, simd=True)
+        assert ulp_diff_f32(got, ref0.out).max() > 1
         res.layer.release()
     finally:
         p.close()

@@ -224,6 +224,213 @@ def test_dense_activations(orc):
     assert np.array_equal(lin.post, lin.pre)
 
 
+# ---------------------------------------------------------------- Activate, id by id
+# loom's Activate for float32 (poly/poly.go:167-200; ids poly/poly.go:90-97).
+# Each branch is pinned by IEEE closed forms at special points and, for the
+# branches that call exp/tanh/pow, by an independent fp64 formulation
+# (scipy's expit, tanh from expm1, x*x*x for the cube): where that value lies
+# safely inside one fp32 rounding interval the fp32 result is fixed whatever
+# the last fp64 bit of the library routine, so it is checked bit for bit;
+# elsewhere within 1 fp32 ulp.
+
+def _act(orc, v, act):
+    return np.float32(orc.activate(float(np.float32(v)), act))
+
+
+def _bits(v):
+    return np.asarray(v, np.float32).view(np.uint32).item()
+
+
+def _ulps(a, b):
+    ia = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    ib = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    ia = np.where(ia < 0, np.int64(-2**31) - ia, ia)
+    ib = np.where(ib < 0, np.int64(-2**31) - ib, ib)
+    return int(np.abs(ia - ib))
+
+
+def _fp32_fixed(y, rel):
+    """fp32(y) if every value within rel of y rounds to the same fp32, else None."""
+    if rel > 1e-6:
+        return None
+    lo, hi = np.float32(y * (1.0 - rel)), np.float32(y * (1.0 + rel))
+    return lo if _bits(lo) == _bits(hi) else None
+
+
+def _act_samples():
+    rng = np.random.default_rng(20240501)
+    v = (rng.standard_normal(3000) * 3.0).astype(np.float32)
+    return np.concatenate([v, np.linspace(-6, 6, 241, dtype=np.float32)])
+
+
+def _tanh64(z):
+    # tanh(z) = -expm1(-2z) / (2 + expm1(-2z)); sign-symmetric form
+    a = abs(z)
+    e = math.expm1(-2.0 * a)
+    t = -e / (2.0 + e)
+    return math.copysign(t, z)
+
+
+def _check_libm_branch(orc, act, value64, rel, min_exact, abs_err=None):
+    # abs_err(v): an absolute error bound that replaces the 1-ulp fallback
+    # where the reference's own fp64 arithmetic leaves fewer correct bits
+    # than fp32 holds
+    exact = 0
+    for v in _act_samples():
+        got = _act(orc, v, act)
+        r = value64(float(v))
+        y, post = r[0], r[1]
+        want = _fp32_fixed(y, r[2] if len(r) > 2 else rel)
+        if want is not None:
+            want = post(want)
+            assert _bits(got) == _bits(want), (act, float(v), float(got), float(want))
+            exact += 1
+        elif abs_err is not None and abs_err(float(v)) > 0:
+            assert abs(float(got) - y) <= abs_err(float(v)), (act, float(v))
+        else:
+            assert _ulps(got, post(np.float32(y))) <= 1, (act, float(v))
+    assert exact >= min_exact, (act, exact)
+
+
+def test_activate_relu_and_relu2_closed_forms(orc):
+    # ReLU (0): v < 0 -> 0, else v (so -0 and NaN pass through); ReLU2 (6): v*v in fp32.
+    for v in _act_samples():
+        assert _bits(_act(orc, v, orc.ACT_RELU)) == _bits(np.float32(0) if v < 0 else v)
+        want = np.float32(0) if v < 0 else np.float32(v) * np.float32(v)
+        assert _bits(_act(orc, v, orc.ACT_RELU2)) == _bits(want)
+    assert _bits(_act(orc, -0.0, orc.ACT_RELU)) == 0x80000000
+    assert _bits(_act(orc, -0.0, orc.ACT_RELU2)) == 0x00000000  # (-0)*(-0) = +0
+    assert np.isnan(_act(orc, np.nan, orc.ACT_RELU))
+    assert np.isnan(_act(orc, np.nan, orc.ACT_RELU2))
+    assert _act(orc, -np.inf, orc.ACT_RELU) == 0 and _act(orc, np.inf, orc.ACT_RELU) == np.inf
+    assert _act(orc, 3e19, orc.ACT_RELU2) == np.inf  # fp32 product overflows
+
+
+def test_activate_linear_and_unknown_ids_are_identity(orc):
+    # ActivationLinear (-1) and any id outside the enum take the default branch.
+    for act in (orc.ACT_LINEAR, 7, 99, -5):
+        for v in (-2.5, 0.0, -0.0, 1e-40, 3.0e38, np.inf, -np.inf):
+            assert _bits(_act(orc, v, act)) == _bits(np.float32(v))
+        assert np.isnan(_act(orc, np.nan, act))
+
+
+def test_activate_leaky_relu_multiplies_in_fp64(orc):
+    # LeakyReLU (5): T(float64(v) * 0.01) for v < 0 -- an fp64 product with the
+    # fp64 constant 0.01, then one rounding to fp32.  The exact product is
+    # formed with fractions and rounded to fp64 (float() of a Fraction is
+    # correctly rounded), then to fp32.
+    from fractions import Fraction
+    c = Fraction(0.01)
+    fp32_form_differs = 0
+    for v in _act_samples():
+        got = _act(orc, v, orc.ACT_LEAKY_RELU)
+        if not v < 0:
+            assert _bits(got) == _bits(v)
+            continue
+        want = np.float32(float(Fraction(float(v)) * c))
+        assert _bits(got) == _bits(want), float(v)
+        if _bits(np.float32(v) * np.float32(0.01)) != _bits(want):
+            fp32_form_differs += 1
+    # the samples separate loom's fp64 product from an fp32 one (v * 0.01f)
+    assert fp32_form_differs > 10
+    assert _bits(_act(orc, -0.0, orc.ACT_LEAKY_RELU)) == 0x80000000
+    assert _act(orc, -np.inf, orc.ACT_LEAKY_RELU) == -np.inf
+    assert np.isnan(_act(orc, np.nan, orc.ACT_LEAKY_RELU))
+    # subnormal result: -1e-40 * 0.01 = -1e-42 (fp32 subnormal), not flushed
+    assert _act(orc, -1e-40, orc.ACT_LEAKY_RELU) == np.float32(float(Fraction(float(np.float32(-1e-40))) * c))
+
+
+def test_activate_sigmoid(orc):
+    # Sigmoid (4): T(1 / (1 + exp(-v))), fp64 then one rounding.
+    from scipy.special import expit
+    _check_libm_branch(orc, orc.ACT_SIGMOID, lambda v: (float(expit(v)), lambda f: f),
+                       rel=1e-12, min_exact=3000)
+    assert _act(orc, 0.0, orc.ACT_SIGMOID) == np.float32(0.5)
+    assert _act(orc, 30.0, orc.ACT_SIGMOID) == np.float32(1.0)  # 1 - 9.4e-14 rounds to 1
+    assert _act(orc, -30.0, orc.ACT_SIGMOID) == np.float32(1.0 / (1.0 + math.exp(30.0)))
+    assert _act(orc, np.inf, orc.ACT_SIGMOID) == 1.0
+    assert _bits(_act(orc, -np.inf, orc.ACT_SIGMOID)) == 0  # 1/(1+inf) = +0
+    assert np.isnan(_act(orc, np.nan, orc.ACT_SIGMOID))
+
+
+def test_activate_silu_multiplies_in_fp32(orc):
+    # SiLU (1): v * T(1/(1+exp(-v))) -- the sigmoid is rounded to fp32 first
+    # and the product is an fp32 multiply (Go's T * T), not fp32(v64 * sig64).
+    from scipy.special import expit
+    _check_libm_branch(orc, orc.ACT_SILU,
+                       lambda v: (float(expit(v)), lambda f, v=v: np.float32(v) * f),
+                       rel=1e-12, min_exact=3000)
+    fp64_form_differs = 0
+    for v in _act_samples():
+        sig = _fp32_fixed(float(expit(float(v))), 1e-12)
+        if sig is None:
+            continue
+        if _bits(np.float32(float(v) * float(expit(float(v))))) != _bits(np.float32(v) * sig):
+            fp64_form_differs += 1
+    assert fp64_form_differs > 10  # the samples separate the two multiplications
+    assert _bits(_act(orc, 0.0, orc.ACT_SILU)) == 0
+    assert _act(orc, 30.0, orc.ACT_SILU) == np.float32(30.0)
+    assert _act(orc, np.inf, orc.ACT_SILU) == np.inf
+    assert np.isnan(_act(orc, -np.inf, orc.ACT_SILU))  # -inf * 0
+    assert np.isnan(_act(orc, np.nan, orc.ACT_SILU))
+
+
+def test_activate_tanh(orc):
+    # Tanh (3): T(math.Tanh(float64(v))) -- tanh in fp64, then one rounding.
+    _check_libm_branch(orc, orc.ACT_TANH, lambda v: (_tanh64(v), lambda f: f),
+                       rel=1e-12, min_exact=3000)
+    assert _bits(_act(orc, -0.0, orc.ACT_TANH)) == 0x80000000
+    assert _act(orc, 30.0, orc.ACT_TANH) == 1.0 and _act(orc, -30.0, orc.ACT_TANH) == -1.0
+    assert _act(orc, np.inf, orc.ACT_TANH) == 1.0 and _act(orc, -np.inf, orc.ACT_TANH) == -1.0
+    assert np.isnan(_act(orc, np.nan, orc.ACT_TANH))
+    # tiny v: tanh(v) = v to fp64 precision
+    assert _act(orc, 1e-20, orc.ACT_TANH) == np.float32(1e-20)
+
+
+def _gelu64(v):
+    # tanh-form GELU with the cube as x*x*x and tanh from expm1; the margin
+    # grows as 1 + tanh cancels (v < 0): a few fp64 ulps of tanh, relative
+    # to 1 + tanh
+    inner = math.sqrt(2.0 / math.pi) * (v + 0.044715 * (v * v * v))
+    t = _tanh64(inner)
+    one_t = 1.0 + t
+    rel = 1e-13 / one_t if one_t > 0 else 1.0
+    return 0.5 * v * one_t, (lambda f: f), min(rel, 1.0)
+
+
+def test_activate_gelu_tanh_form(orc):
+    # GELU (2): T(0.5*v64*(1 + tanh(sqrt(2/pi)*(v64 + 0.044715*pow(v64, 3))))).
+    # (1 + tanh) cancels for v < 0, so the exact check asks for a margin that
+    # grows with the cancellation.
+    def cancelled(v):
+        # 1 + tanh(z) for z < -17: fp64 tanh is within a few ulps of -1
+        # (ulp 1.1e-16), so the reference keeps only its absolute error,
+        # 0.5*|v|*(4 * 2^-53), plus the fp32 rounding of the result
+        y = _gelu64(v)[0]
+        return 0.5 * abs(v) * 4 * 2.0**-53 + abs(y) * 2.0**-23 if _gelu64(v)[2] > 1e-9 else 0.0
+    _check_libm_branch(orc, orc.ACT_GELU, _gelu64, rel=None, min_exact=2500, abs_err=cancelled)
+    # the tanh form, not the erf form: at v = 1 they are ~1.5e-4 apart (> 1000 ulps)
+    erf_form = np.float32(0.5 * (1.0 + math.erf(1.0 / math.sqrt(2.0))))
+    assert _ulps(_act(orc, 1.0, orc.ACT_GELU), erf_form) > 1000
+    assert _bits(_act(orc, 0.0, orc.ACT_GELU)) == 0
+    assert _act(orc, 30.0, orc.ACT_GELU) == np.float32(30.0)
+    assert _bits(_act(orc, -30.0, orc.ACT_GELU)) == 0x80000000  # (0.5*-30)*(1 + -1) = -0
+    assert _act(orc, np.inf, orc.ACT_GELU) == np.inf
+    assert np.isnan(_act(orc, -np.inf, orc.ACT_GELU))  # -inf * 0
+    assert np.isnan(_act(orc, np.nan, orc.ACT_GELU))
+
+
+def test_dense_post_applies_activate_per_element(orc):
+    # DenseForwardPackedTernaryCPU (poly/dense.go:94-98): post = Activate(pre) elementwise,
+    # for every id, on the fp32 pre-activation.
+    m = orc.random_matrix(48, 96, seed=19)
+    x = orc.normal_f32(3 * 96, 2).reshape(3, 96) * np.float32(40.0)
+    for act in (orc.ACT_LINEAR, 0, 1, 2, 3, 4, 5, 6):
+        out = orc.dense_forward(m, x, activation=act)
+        want = np.array([_act(orc, v, act) for v in out.pre.ravel()], np.float32).reshape(out.pre.shape)
+        assert out.post.tobytes() == want.tobytes(), act
+
+
 # ---------------------------------------------------------------- swiglu pieces
 def test_gate_product_closed_forms(orc):
     assert orc.swiglu_gate_product(0.0, 5.0) == 0.0

@@ -70,7 +70,7 @@ def test_noalloc_activation_and_residual(orc, torch_dev):
     w = bn.TernaryMatrix.from_words(m.words, n, k, m.scale)
     x = torch.from_numpy(orc.normal_f32(M * k, seed=8).reshape(M, k)).cuda()
     r = torch.from_numpy(orc.normal_f32(M * n, seed=9).reshape(M, n)).cuda()
-    for act in (0, 6):  # ReLU, ReLU2: exact activations
+    for act in (0, 1, 2, 3, 4, 5, 6):  # every Activate id (poly/poly.go:90-97): same kernels, same bytes
         got_pre, got_post = _noalloc(torch, w, x, activation=act, residual=r)
         want_pre, want_post = bn.dense_forward_packed_ternary(w, x, activation=act, residual=r)
         torch.cuda.synchronize()
