@@ -129,6 +129,16 @@ int loom_amd_norm_quant_rows(float* h, int m, int n, const float* weight, double
 int loom_amd_ordered_sum_rows(const double* terms, int m, int n, double s0, double* out,
                               int threads, void* stream);
 
+/* y[i] = exp(x[i]) for n fp64 values (device pointers), with the device exp
+ * that every kernel of the library calls: the attention probabilities
+ * exp(score - max) of MHAForwardPackedTernaryCPU (poly/mha.go:339-342), the
+ * SwiGLU gate's sigmoid (poly/swiglu.go:37-46) and Activate
+ * (poly/poly.go:167-200), all math.Exp in the reference.  No counterpart of
+ * its own in the reference: it lets callers and tests evaluate the
+ * reference's exp-free chains around the device's exp, e.g. strict
+ * attention bit for bit. */
+int loom_amd_exp_rows(const double* x, long n, double* y, void* stream);
+
 /* ---- layers ---------------------------------------------------------- */
 
 typedef struct loom_amd_dense_taps {

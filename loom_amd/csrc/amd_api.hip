@@ -414,6 +414,14 @@ int loom_amd_ordered_sum_rows(const double* terms, int m, int n, double s0, doub
     return e == hipSuccess ? 0 : fail_hip("ordered_sum_rows", e);
 }
 
+int loom_amd_exp_rows(const double* x, long n, double* y, void* stream) {
+    if (n < 0) return fail("bad size");
+    if (n == 0) return 0;
+    if (!x || !y) return fail("null buffer");
+    hipError_t e = launch_exp_rows(x, n, y, (hipStream_t)stream);
+    return e == hipSuccess ? 0 : fail_hip("exp_rows", e);
+}
+
 int loom_amd_dense_forward(const loom_amd_matrix* w, const float* x, int m, int activation,
                            float* pre, float* post, const float* residual,
                            const loom_amd_dense_taps* taps, void* stream) {

@@ -149,6 +149,7 @@ bool launch_row_sumsq_f32(const float* x, long ldx, int m, int n, double* totals
 // workgroup of `threads` (64, 256 or 512) per row.
 hipError_t launch_ordered_sum_rows(const double* terms, int m, int n, double s0, double* out,
                                    int threads, hipStream_t s);
+hipError_t launch_exp_rows(const double* x, long n, double* y, hipStream_t s);
 
 // Per-device scratch arena for the device-resident entry points.
 void* scratch(int device, size_t bytes, std::string* err);

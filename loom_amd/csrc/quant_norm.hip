@@ -357,4 +357,19 @@ hipError_t launch_ordered_sum_rows(const double* terms, int m, int n, double s0,
     return hipGetLastError();
 }
 
+// y[i] = exp(x[i]) in fp64 with the device exp every kernel of the library
+// calls (the attention probabilities, the SwiGLU gate's sigmoid, Activate).
+__global__ __launch_bounds__(256) void exp_rows_kernel(const double* __restrict__ x, long n,
+                                                       double* __restrict__ y) {
+    const long stride = (long)gridDim.x * blockDim.x;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) y[i] = exp(x[i]);
+}
+
+hipError_t launch_exp_rows(const double* x, long n, double* y, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    const long blocks = std::min<long>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(exp_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, n, y);
+    return hipGetLastError();
+}
+
 }  // namespace lamd

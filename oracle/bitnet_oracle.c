@@ -845,6 +845,81 @@ void orc_attention(const double* Q, const float* cache_k, const float* cache_v, 
     }
 }
 
+/* The attention of MHAForwardPackedTernaryCPU (poly/mha.go:316-354) in two
+ * stages on either side of math.Exp, so that a device's chains can be
+ * checked bit for bit given the device's own exp.  Only the listed rows
+ * rows[0..nrows) of Q are evaluated (row s sits at position seq_base + s).
+ * Layout of args / probs: for each listed row i, for each head h, the
+ * positions 0..seq_base+rows[i]; orc_attention_span gives the length.
+ *
+ * Stage 1 (poly/mha.go:324-337): every score is the dimension-order chain
+ * dot += Q*K, then dot*scale; the maximum runs from -1e9 over positions in
+ * order; args = score - max.
+ * Stage 2 (poly/mha.go:339-352): p = probs (the caller's exp of args);
+ * expSum += p in position order; each column's sum += p*V in position
+ * order; out = sum / expSum. */
+long orc_attention_span(const int* rows, int nrows, int seq_base, int heads) {
+    long n = 0;
+    for (int i = 0; i < nrows; i++) n += (long)heads * (seq_base + rows[i] + 1);
+    return n;
+}
+
+static long attn_span_offset(const int* rows, int i, int seq_base, int heads) {
+    return orc_attention_span(rows, i, seq_base, heads);
+}
+
+void orc_attention_args(const double* Q, const float* cache_k, const int* rows, int nrows,
+                        int seq_base, int msl, int heads, int kv_heads, int hd, double* args) {
+    const int q_dim = heads * hd, kv_dim = kv_heads * hd;
+    const int per_kv = heads / kv_heads;
+    const double scale = 1.0 / sqrt((double)hd);
+#pragma omp parallel for schedule(dynamic, 1)
+    for (long ih = 0; ih < (long)nrows * heads; ih++) {
+        const int i = (int)(ih / heads), h = (int)(ih % heads);
+        const int s = rows[i], total = seq_base + s;
+        const int kvh = h / per_kv;
+        double* a = args + attn_span_offset(rows, i, seq_base, heads) + (long)h * (total + 1);
+        const double* qr = Q + (size_t)s * q_dim + (size_t)h * hd;
+        double max_score = -1e9;
+        for (int kp = 0; kp <= total; kp++) {
+            const float* kr = cache_k + (size_t)(kp % msl) * kv_dim + (size_t)kvh * hd;
+            double dot = 0.0;
+            for (int d = 0; d < hd; d++) dot += qr[d] * (double)kr[d];
+            const double score = dot * scale;
+            a[kp] = score;
+            if (score > max_score) max_score = score;
+        }
+        for (int kp = 0; kp <= total; kp++) a[kp] = a[kp] - max_score;
+    }
+}
+
+void orc_attention_chains(const double* probs, const float* cache_v, const int* rows, int nrows,
+                          int seq_base, int msl, int heads, int kv_heads, int hd, double* attn) {
+    const int q_dim = heads * hd, kv_dim = kv_heads * hd;
+    const int per_kv = heads / kv_heads;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (long ih = 0; ih < (long)nrows * heads; ih++) {
+        const int i = (int)(ih / heads), h = (int)(ih % heads);
+        const int total = seq_base + rows[i];
+        const int kvh = h / per_kv;
+        const double* p = probs + attn_span_offset(rows, i, seq_base, heads) + (long)h * (total + 1);
+        double exp_sum = 0.0;
+        for (int kp = 0; kp <= total; kp++) exp_sum += p[kp];
+        for (int d = 0; d < hd; d++) {
+            double sum = 0.0;
+            for (int kp = 0; kp <= total; kp++) {
+                sum += p[kp] * (double)cache_v[(size_t)(kp % msl) * kv_dim + (size_t)kvh * hd + d];
+            }
+            attn[(size_t)i * q_dim + (size_t)h * hd + d] = sum / exp_sum;
+        }
+    }
+}
+
+/* The host C library's exp, elementwise (the exp that orc_attention calls). */
+void orc_exp_rows(const double* x, long n, double* y) {
+    for (long i = 0; i < n; i++) y[i] = exp(x[i]);
+}
+
 /* Output stage of MHAForwardPackedTernaryCPU (poly/mha.go:356-368): per row,
  * bitNetRMSNormFloat64Weighted in place, fp64 requantization, O matvec,
  * pre = fp32(normalized row), post = fp32(O + bias).  attn is modified. */

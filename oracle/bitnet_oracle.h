@@ -143,6 +143,12 @@ typedef struct orc_mha {
 
 void orc_attention(const double* Q, const float* cache_k, const float* cache_v, int seq,
                    int seq_base, int msl, int heads, int kv_heads, int hd, double* attn);
+long orc_attention_span(const int* rows, int nrows, int seq_base, int heads);
+void orc_attention_args(const double* Q, const float* cache_k, const int* rows, int nrows,
+                        int seq_base, int msl, int heads, int kv_heads, int hd, double* args);
+void orc_attention_chains(const double* probs, const float* cache_v, const int* rows, int nrows,
+                          int seq_base, int msl, int heads, int kv_heads, int hd, double* attn);
+void orc_exp_rows(const double* x, long n, double* y);
 void orc_attn_out(const orc_matrix* o, const float* bias_o, const float* inner_norm, double eps,
                   double* attn, int seq, int q_dim, int simd, int workers, float* pre,
                   float* post);

@@ -77,6 +77,10 @@ def _declare(L: C.CDLL) -> None:
                                       P, P, P, P, P, P, P, P, P]),
         "orc_rmsnorm_forward": (None, [P, i, i, P, d, P, P]),
         "orc_attention": (None, [P, P, P, i, i, i, i, i, i, P]),
+        "orc_attention_span": (C.c_long, [P, i, i, i]),
+        "orc_attention_args": (None, [P, P, P, i, i, i, i, i, i, P]),
+        "orc_attention_chains": (None, [P, P, P, i, i, i, i, i, i, P]),
+        "orc_exp_rows": (None, [P, C.c_long, P]),
         "orc_attn_out": (None, [P, P, P, d, P, i, i, i, i, P, P]),
         "orc_mha_forward": (None, [P, P, i, i, i, P, P, P, P]),
         "orc_mha_project": (None, [P, P, i, i, i, i, P]),
@@ -468,6 +472,46 @@ def attention(q: np.ndarray, cache_k: np.ndarray, cache_v: np.ndarray, seq_base:
     lib().orc_attention(_p(q), _p(ck), _p(cv), q.shape[0], seq_base, msl, num_heads,
                         num_kv_heads, head_dim, _p(out))
     return out
+
+
+def _attn_rows(q, rows):
+    rows = np.arange(q.shape[0]) if rows is None else np.asarray(rows)
+    return np.ascontiguousarray(rows, np.int32)
+
+
+def attention_args(q: np.ndarray, cache_k: np.ndarray, seq_base: int, msl: int, num_heads: int,
+                   num_kv_heads: int, head_dim: int, rows=None) -> np.ndarray:
+    """Stage 1 of the attention (poly/mha.go:324-337) for rows `rows` of q
+    (all by default): the exp arguments score - max, flat, per row, per head,
+    positions 0..seq_base+row."""
+    q = np.ascontiguousarray(q, np.float64).reshape(-1, num_heads * head_dim)
+    r = _attn_rows(q, rows)
+    n = lib().orc_attention_span(_p(r), r.size, seq_base, num_heads)
+    out = np.empty(n, np.float64)
+    lib().orc_attention_args(_p(q), _p(np.ascontiguousarray(cache_k, np.float32)), _p(r), r.size,
+                             seq_base, msl, num_heads, num_kv_heads, head_dim, _p(out))
+    return out
+
+
+def attention_chains(probs: np.ndarray, cache_v: np.ndarray, seq_base: int, msl: int,
+                     num_heads: int, num_kv_heads: int, head_dim: int, rows) -> np.ndarray:
+    """Stage 2 of the attention (poly/mha.go:339-352) from probabilities in
+    attention_args' layout: [len(rows), q_dim] fp64."""
+    r = np.ascontiguousarray(rows, np.int32)
+    p = np.ascontiguousarray(probs, np.float64)
+    assert p.size == lib().orc_attention_span(_p(r), r.size, seq_base, num_heads)
+    out = np.empty((r.size, num_heads * head_dim), np.float64)
+    lib().orc_attention_chains(_p(p), _p(np.ascontiguousarray(cache_v, np.float32)), _p(r), r.size,
+                               seq_base, msl, num_heads, num_kv_heads, head_dim, _p(out))
+    return out
+
+
+def exp_rows(x: np.ndarray) -> np.ndarray:
+    """The C library's exp elementwise (the exp orc_attention uses)."""
+    x = np.ascontiguousarray(x, np.float64)
+    y = np.empty_like(x)
+    lib().orc_exp_rows(_p(x), x.size, _p(y))
+    return y
 
 
 def attn_out(o: Matrix, attn: np.ndarray, inner_norm: np.ndarray | None = None,

@@ -15,7 +15,11 @@ so a difference is pinned to the stage that made it.  Bars:
   * Q after RoPE within 1e-12 of the row scale (pow/cos/sin last bits;
     bit-exact at position 0, where the rotation is the identity), the K cache
     within 1 fp32 ulp (V bit-exact), attention within 1e-12 of the row scale
-    (exp last bits; fast mode also sums in another fixed order);
+    of the oracle (exp last bits; fast mode also sums in another fixed
+    order); in strict mode the attention is also bit-exact against the
+    oracle's exp-free chains (dimension-order scores, maximum, position-order
+    expSum and value sums, division) evaluated around the device's own exp,
+    which pins every summation order of poly/mha.go:316-354;
   * the SiLU gate product (exp) within 1 fp32 ulp; ReLU2 bit-exact.
 Citations are relative to the loom v0.83.0 tree.
 """
@@ -127,6 +131,32 @@ def _rel_rows(got, want, tol, what):
     assert err <= tol, f"{what}: off by {err:.3e} of the row scale (bar {tol:g})"
 
 
+def device_exp(a):
+    """exp of fp64 values with the device exp the library's kernels call
+    (loom_amd_exp_rows)."""
+    import torch
+    from loom_amd import _lib
+    x = torch.from_numpy(np.ascontiguousarray(a, np.float64)).cuda()
+    y = torch.empty_like(x)
+    rc = _lib.lib().loom_amd_exp_rows(C.c_void_p(x.data_ptr()), x.numel(), C.c_void_p(y.data_ptr()),
+                                      C.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0, _lib.lib().loom_amd_last_error()
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+def strict_attention_bit_exact(orc, sh, q, cache_k, cache_v, base, R, attn):
+    """Strict attention rows R against the reference's chains around the
+    device's exp (poly/mha.go:324-352): the exp arguments score - max from the
+    GPU's Q and K cache (dimension-order dots, maximum from -1e9), the
+    device's exp of them, then expSum and the value sums in position order
+    and the division -- every value bit for bit."""
+    args = orc.attention_args(q, cache_k, base, sh.msl, sh.heads, sh.kv, sh.hd, rows=R)
+    ref = orc.attention_chains(device_exp(args), cache_v, base, sh.msl, sh.heads, sh.kv, sh.hd, R)
+    bad = np.count_nonzero(attn.view(np.uint64) != ref.view(np.uint64))
+    assert bad == 0, f"strict attention: {bad} of {attn.size} values differ from the reference chains"
+
+
 def f64_inner_norm(orc, rows, w, eps=1e-5):
     """bitNetRMSNormFloat64Weighted (poly/bitnet_cpu.go:868-887) per row."""
     out = np.array(rows, np.float64, copy=True)
@@ -177,6 +207,8 @@ def check_stages(orc, w: Weights, mha_ref, x_in, T, out, cache_k, cache_v, base,
                                            sh.heads, sh.kv, sh.hd)[0] for r in R])
     attn = T["attn"][R]
     _rel_rows(attn, attn_ref, 1e-12, "attention")
+    if strict:
+        strict_attention_bit_exact(orc, sh, q, cache_k, cache_v, base, R, attn)
     # MHA inner norm of the GPU's attention rows (poly/mha.go:356-360) and the
     # fp64 requantization
     an = T["attn_norm"][R]

@@ -318,3 +318,70 @@ def test_lm_head_scalar_order_pinned(orc):
     row[0], row[1], row[2] = 2.0 ** 30, 2.0 ** -30, -(2.0 ** 30)
     assert orc.lm_head(hidden, row, simd=False)[0] == 0.0
     assert orc.lm_head(hidden, row, simd=True)[0] == 1.0
+
+
+def test_attention_two_stages_compose_to_attention(orc):
+    # orc_attention_args -> exp -> orc_attention_chains (the split used to
+    # check a device's chains given the device's own exp) reproduces the
+    # attention of poly/mha.go:316-354 bit for bit: GQA, a nonzero base,
+    # listed rows in any subset, a ring shorter than the positions.
+    rng = np.random.default_rng(81)
+    for heads, kv, hd, S, base, msl in [(4, 2, 32, 5, 0, 40), (6, 3, 16, 4, 9, 20),
+                                        (8, 1, 64, 3, 30, 33), (2, 2, 8, 6, 12, 10)]:
+        q = rng.standard_normal((S, heads * hd)) * 2.0
+        ck = rng.standard_normal((msl, kv * hd)).astype(np.float32)
+        cv = rng.standard_normal((msl, kv * hd)).astype(np.float32)
+        want = orc.attention(q, ck, cv, base, msl, heads, kv, hd)
+        for rows in (None, [S - 1], [0, S - 1], list(range(0, S, 2))):
+            r = np.arange(S) if rows is None else np.asarray(rows)
+            args = orc.attention_args(q, ck, base, msl, heads, kv, hd, rows=r)
+            assert args.size == sum(heads * (base + int(i) + 1) for i in r)
+            assert np.all(args <= 0.0)  # score - max
+            got = orc.attention_chains(orc.exp_rows(args), cv, base, msl, heads, kv, hd, r)
+            assert got.tobytes() == want[r].tobytes(), (heads, kv, hd, base, rows)
+
+
+def test_attention_args_are_dimension_order_chains(orc):
+    # Each exp argument is (sum_d Q*K in dimension order) * scale - max: on a
+    # row whose terms cancel, the dimension-order chain and a pairwise sum
+    # give different scores, and the oracle takes the chain's.
+    hd, heads, kv = 4, 1, 1
+    q = np.array([[1e16, 1.0, -1e16, 1.0]])
+    ck = np.array([[1, 1, 1, 1], [0, 0, 0, 0]], np.float32)
+    args = orc.attention_args(q, ck, 1, 2, heads, kv, hd, rows=[0])
+    chain = ((1e16 + 1.0) - 1e16) + 1.0          # = 1.0 in fp64 (1e16 + 1 rounds to 1e16)
+    assert chain == 1.0 and (1e16 - 1e16) + (1.0 + 1.0) == 2.0
+    score0 = chain * (1.0 / math.sqrt(hd))
+    mx = max(score0, 0.0)
+    assert args.tolist() == [score0 - mx, 0.0 - mx]
+    # probabilities then expSum and the position-order value chain
+    cv = np.array([[1e16, 0, 0, 0], [1.0, 0, 0, 0]], np.float32)
+    p = np.array([1.0, 0.5])
+    out = orc.attention_chains(p, cv, 1, 2, heads, kv, hd, [0])
+    assert out[0, 0] == (1.0 * float(np.float32(1e16)) + 0.5 * 1.0) / 1.5
+
+
+def test_attention_chains_detect_another_order(orc):
+    # The bit-exact check of a device's strict attention against
+    # attention_chains would catch a device that summed in another order:
+    # the same probabilities summed in reverse position order (or by a
+    # pairwise tree) give different bits for most outputs at these sizes.
+    rng = np.random.default_rng(83)
+    heads, kv, hd, base, msl = 4, 1, 64, 300, 301
+    q = rng.standard_normal((1, heads * hd))
+    ck = rng.standard_normal((msl, kv * hd)).astype(np.float32)
+    cv = rng.standard_normal((msl, kv * hd)).astype(np.float32)
+    args = orc.attention_args(q, ck, base, msl, heads, kv, hd, rows=[0])
+    p = orc.exp_rows(args).reshape(heads, base + 1)
+    got = orc.attention_chains(p.ravel(), cv, base, msl, heads, kv, hd, [0])[0].reshape(heads, hd)
+    v = cv[:base + 1].astype(np.float64)
+    rev = np.zeros((heads, hd))
+    es = np.zeros(heads)
+    for kp in range(base, -1, -1):
+        rev += p[:, kp:kp + 1] * v[kp][None, :]
+        es += p[:, kp]
+    rev /= es[:, None]
+    tree = (p @ v) / p.sum(axis=1, keepdims=True)   # BLAS / pairwise orders
+    assert np.count_nonzero(rev != got) > got.size // 4
+    assert np.count_nonzero(tree != got) > got.size // 4
+    assert np.max(np.abs(rev - got)) < 1e-13  # same values, other roundings
