@@ -213,7 +213,8 @@ typedef struct loom_amd_block_desc {
     int max_batch;      /* independent sequences per call (0 = 1) */
     double rope_theta;  /* 0 = 10000 */
     double norm_eps;    /* RMSNorm1/2 eps (<= 0: 1e-6, poly/norm.go:104) */
-    double attn_eps;    /* MHA inner norm eps (<= 0: 1e-5) */
+    double attn_eps;    /* the MHA layer's RMSNormEps: inner norm eps (<= 0: 1e-5);
+                           per-head Q/K norm eps (<= 0: 1e-6, mhaQKNormEpsilon) */
     double ffn_eps;     /* SwiGLU inner norm eps (<= 0: 1e-5) */
     int ffn_activation; /* gate activation: 1 SiLU, 6 ReLU2 */
     int norm_mode;      /* LOOM_AMD_NORM_STRICT or LOOM_AMD_NORM_FAST */
@@ -238,6 +239,14 @@ typedef struct loom_amd_block_weights {
     const float* bias_k;          /* kv_dim, optional */
     const float* bias_v;          /* kv_dim, optional */
     const float* bias_o;          /* hidden, optional */
+    /* per-head Q / K RMSNorm weights, loom's QNormWeight / KNormWeight
+     * (poly/mha.go:285-290, 584-646), applied before RoPE when the length
+     * is > 0: head_dim (shared by every head), heads*head_dim (one block per
+     * head) or any other length (unit weights, as loom) */
+    const float* q_norm;
+    int q_norm_len;
+    const float* k_norm;
+    int k_norm_len;
 } loom_amd_block_weights;
 
 /* Optional device copies of block intermediates (rows = batch*seq), every

@@ -53,7 +53,8 @@ class BlockWeights(C.Structure):
     """loom_amd_block_weights (matrix handles + host fp32 arrays)."""
     _fields_ = [("q", P), ("k", P), ("v", P), ("o", P), ("gate", P), ("up", P), ("down", P),
                 ("norm1", P), ("norm2", P), ("attn_inner_norm", P), ("ffn_inner_norm", P),
-                ("bias_q", P), ("bias_k", P), ("bias_v", P), ("bias_o", P)]
+                ("bias_q", P), ("bias_k", P), ("bias_v", P), ("bias_o", P),
+                ("q_norm", P), ("q_norm_len", i32), ("k_norm", P), ("k_norm_len", i32)]
 
 
 class BlockTaps(C.Structure):

@@ -29,8 +29,12 @@ payloads; memory-mapped), with loom's dtype decodes (poly/safetensors.go:
 624-781): BF16 is the 16 high bits of an fp32, F16 widens exactly, F64 and the
 integer types round to the nearest fp32.  Nothing in a file is executed.
 
-Per-head Q/K RMSNorm weights (``q_norm`` / ``k_norm``, poly/mha.go:285-290) are
-refused: the block does not apply them.
+Per-head Q/K RMSNorm weights (``q_norm`` / ``k_norm``) become the block's
+QNormWeight / KNormWeight as loom stores them (any length,
+poly/prefix_safetensor.go:425-434); the block applies them before RoPE
+(poly/mha.go:285-290) with eps 1e-6, since the import leaves the MHA layer's
+RMSNormEps unset (mhaQKNormEpsilon, poly/mha.go:19-24; InitHFDecoderBlocks,
+poly/hf_decoder.go:43-51).
 """
 from __future__ import annotations
 
@@ -271,8 +275,6 @@ def load_blocks(tensors: dict[str, StoredTensor], dims: DecoderDims, device: int
         li, slot, role = r
         if li >= dims.layers:
             continue
-        if role in ("qn", "kn"):
-            raise NotImplementedError(f"{name}: per-head Q/K RMSNorm is not supported by this block")
         per[li][(slot, role)] = t
     h, q, kv, inter = dims.hidden, dims.q_dim, dims.kv_dim, dims.inter
     shapes = {(1, "q"): (q, h), (1, "k"): (kv, h), (1, "v"): (kv, h), (1, "o"): (h, q),
@@ -302,18 +304,25 @@ def load_blocks(tensors: dict[str, StoredTensor], dims: DecoderDims, device: int
         norm1, norm2 = vec((0, ""), h), vec((2, ""), h)
         if norm1 is None or norm2 is None:
             raise ValueError(f"layer {li}: missing input_layernorm / post_attention_layernorm")
+        def raw(key):  # QNormWeight / KNormWeight keep whatever length the tensor has
+            t = d.get(key)
+            return None if t is None else t.to_float32().reshape(-1)
+
         out.append(tf.BlockWeights(mats["q"], mats["k"], mats["v"], mats["o"], mats["g"], mats["u"],
                                    mats["d"], norm1, norm2, vec((1, "inner_norm"), q),
-                                   vec((3, "inner_norm"), inter)))
+                                   vec((3, "inner_norm"), inter),
+                                   q_norm=raw((1, "qn")), k_norm=raw((1, "kn"))))
     return out
 
 
 def block_config(dims: DecoderDims, norm: str = "strict", max_seq_len: int = 2048,
                  max_batch: int = 1) -> tf.BlockConfig:
-    # inner norms: loom's default eps (the HF import leaves it unset)
+    # the import leaves the MHA and SwiGLU layers' RMSNormEps unset
+    # (poly/hf_decoder.go:43-66): their inner norms take loom's default 1e-5,
+    # the per-head Q/K norms 1e-6 (attn_eps 0 selects both defaults)
     return tf.BlockConfig(dims.hidden, dims.heads, dims.kv_heads, dims.head_dim, dims.inter,
                           max_seq_len=max_seq_len, max_batch=max_batch, rope_theta=dims.theta,
-                          norm_eps=dims.rms_eps, attn_eps=1e-5, ffn_eps=1e-5,
+                          norm_eps=dims.rms_eps, attn_eps=0.0, ffn_eps=1e-5,
                           ffn_activation=dims.activation, norm=norm)
 
 

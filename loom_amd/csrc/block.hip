@@ -254,6 +254,12 @@ hipError_t launch_rmsnorm_quant(const float* x, long ldx, int m, int n, const fl
 //   Q = fp64(acc)*os_q + bias_q (fp64, kept), rotated in fp64;
 //   K = fp32(fp64(acc)*os_k + bias_k), rotated from fp64 back to fp32;
 //   V = fp32(fp64(acc)*os_v + bias_v);
+// With per-head Q/K norm weights (poly/mha.go:285-290), Q and the fp32 K row
+// are normalized per head before the rotation (applyPerHeadRMSNormFloat64 /
+// ...Tensor, poly/mha.go:584-646): the head's sum of squares as the
+// dimension-order fp64 chain, inv = 1/sqrt(sumSq/hd + eps), x = x*inv*gamma
+// (left to right; K rounded back to fp32); a head with rms == 0 is left
+// unchanged.
 // RoPE rotates the half-split pairs (d, d + hd/2) by pos / theta^(2d/hd).
 // K and V go to ring row pos % msl of the row's sequence slot (batch index);
 // when one call holds more than msl tokens only the last token of each ring
@@ -268,20 +274,78 @@ __device__ __forceinline__ void rope_angle(int pos, int d, int hd, double theta,
     *sn = sin(angle);
 }
 
+// Per-head norm of one head (see above).  inv < 0 marks a head the
+// reference leaves unchanged (rms == 0); a NaN inv is applied, as there.
+struct HeadNorm {
+    bool on = false;   // weights present for this projection
+    double inv = 0.0;
+    double g0 = 1.0, g1 = 1.0;  // gamma of the pair's two dimensions
+};
+
+// gamma element of dimension d of head h: gamma[d] when the weights hold one
+// head, gamma[h*hd + d] when they hold every head, else 1
+__device__ __forceinline__ double qk_gamma(const float* g, int len, int heads, int hd, int h, int d) {
+    if (len == hd) return (double)g[d];
+    if (len == heads * hd) return (double)g[(size_t)h * hd + d];
+    return 1.0;
+}
+
+__device__ __forceinline__ double qk_inv_rms(double sum_sq, int hd, double eps) {
+    const double rms = sqrt(sum_sq / (double)hd + eps);
+    return rms == 0.0 ? -1.0 : 1.0 / rms;
+}
+
+__device__ __forceinline__ HeadNorm head_norm(bool on, double inv, const float* g, int len, int heads,
+                                              int hd, int h, int d0, int d1) {
+    HeadNorm n;
+    n.on = on && !(inv < 0.0);
+    n.inv = inv;
+    if (n.on) {
+        n.g0 = qk_gamma(g, len, heads, hd, h, d0);
+        n.g1 = qk_gamma(g, len, heads, hd, h, d1);
+    }
+    return n;
+}
+
+// The sequential fp64 sum of squares of one head's Q (fp64 after bias) or K
+// (rounded to fp32 first) values, formed by one thread from the accumulators
+// (j0: the head's first accumulator index within the projection).
+template <bool KROUND>
+__device__ __forceinline__ double head_sum_sq(const int32_t* ar, double os, const float* b, int j0, int hd) {
+    double s = 0.0;
+#pragma unroll 8
+    for (int d = 0; d < hd; ++d) {
+        double v = (double)ar[j0 + d] * os + (b ? (double)b[j0 + d] : 0.0);
+        if (KROUND) v = (double)(float)v;
+        s = s + v * v;
+    }
+    return s;
+}
+
 // The three per-element steps, shared with the fused decode attention kernel.
 // The *_v forms take the loaded accumulators and biases (b_on: a bias exists).
 __device__ __forceinline__ void q_pair_v(int32_t a0, int32_t a1, double os, bool b_on, float b0, float b1,
-                                         double c, double sn, double* o0, double* o1) {
-    const double v0 = (double)a0 * os + (b_on ? (double)b0 : 0.0);
-    const double v1 = (double)a1 * os + (b_on ? (double)b1 : 0.0);
+                                         double c, double sn, double* o0, double* o1,
+                                         const HeadNorm& hn = HeadNorm{}) {
+    double v0 = (double)a0 * os + (b_on ? (double)b0 : 0.0);
+    double v1 = (double)a1 * os + (b_on ? (double)b1 : 0.0);
+    if (hn.on) {
+        v0 = v0 * hn.inv * hn.g0;
+        v1 = v1 * hn.inv * hn.g1;
+    }
     *o0 = v0 * c - v1 * sn;
     *o1 = v0 * sn + v1 * c;
 }
 
 __device__ __forceinline__ void k_pair_v(int32_t a0, int32_t a1, double os, bool b_on, float b0, float b1,
-                                         double c, double sn, float* o0, float* o1) {
-    const float k0 = (float)((double)a0 * os + (b_on ? (double)b0 : 0.0));
-    const float k1 = (float)((double)a1 * os + (b_on ? (double)b1 : 0.0));
+                                         double c, double sn, float* o0, float* o1,
+                                         const HeadNorm& hn = HeadNorm{}) {
+    float k0 = (float)((double)a0 * os + (b_on ? (double)b0 : 0.0));
+    float k1 = (float)((double)a1 * os + (b_on ? (double)b1 : 0.0));
+    if (hn.on) {
+        k0 = (float)((double)k0 * hn.inv * hn.g0);
+        k1 = (float)((double)k1 * hn.inv * hn.g1);
+    }
     const double v0 = (double)k0, v1 = (double)k1;
     *o0 = (float)(v0 * c - v1 * sn);
     *o1 = (float)(v0 * sn + v1 * c);
@@ -292,14 +356,18 @@ __device__ __forceinline__ float v_val_v(int32_t a, double os, bool b_on, float 
 }
 
 __device__ __forceinline__ void q_pair(const int32_t* ar, double os, const float* bq, int j0, int j1,
-                                       double c, double sn, double* o0, double* o1) {
-    q_pair_v(ar[j0], ar[j1], os, bq != nullptr, bq ? bq[j0] : 0.0f, bq ? bq[j1] : 0.0f, c, sn, o0, o1);
+                                       double c, double sn, double* o0, double* o1,
+                                       const HeadNorm& hn = HeadNorm{}) {
+    q_pair_v(ar[j0], ar[j1], os, bq != nullptr, bq ? bq[j0] : 0.0f, bq ? bq[j1] : 0.0f, c, sn, o0, o1,
+             hn);
 }
 
 // ar points at the K part of the row's accumulators; j0/j1 index into K
 __device__ __forceinline__ void k_pair(const int32_t* ar, double os, const float* bk, int j0, int j1,
-                                       double c, double sn, float* o0, float* o1) {
-    k_pair_v(ar[j0], ar[j1], os, bk != nullptr, bk ? bk[j0] : 0.0f, bk ? bk[j1] : 0.0f, c, sn, o0, o1);
+                                       double c, double sn, float* o0, float* o1,
+                                       const HeadNorm& hn = HeadNorm{}) {
+    k_pair_v(ar[j0], ar[j1], os, bk != nullptr, bk ? bk[j0] : 0.0f, bk ? bk[j1] : 0.0f, c, sn, o0, o1,
+             hn);
 }
 
 // ar points at the V part of the row's accumulators
@@ -314,12 +382,16 @@ __device__ __forceinline__ float v_val(const int32_t* ar, double os, const float
 // rows (decode): a row's items spread over several workgroups.
 constexpr int kRopeMaxHalf = 128;  // head_dim <= 256
 
+// With per-head norms the workgroup first forms the norm factor of every Q
+// and K head of its row (one thread per head, the dimension-order chain) into
+// LDS.
 __global__ __launch_bounds__(256) void qkv_rope_kernel(
     const int32_t* __restrict__ acc, const float* __restrict__ amax, float sq, float sk, float sv,
     const float* __restrict__ bq, const float* __restrict__ bk, const float* __restrict__ bv, int batch,
     int seq, const int* __restrict__ pos0, int msl, int heads, int kv_heads, int hd, double theta,
-    double* __restrict__ q, float* __restrict__ cache_k, float* __restrict__ cache_v) {
+    double* __restrict__ q, float* __restrict__ cache_k, float* __restrict__ cache_v, QkNorm qk) {
     __shared__ double rc[kRopeMaxHalf], rs[kRopeMaxHalf];
+    __shared__ double inv_s[kQkNormMaxHeads];
     const int half = hd >> 1;
     const int q_dim = heads * hd, kv_dim = kv_heads * hd;
     const int qp = heads * half, kp = kv_heads * half;
@@ -329,10 +401,21 @@ __global__ __launch_bounds__(256) void qkv_rope_kernel(
     const int base = *pos0;
     const int pos = base + s;
     for (int d = threadIdx.x; d < half; d += blockDim.x) rope_angle(pos, d, hd, theta, &rc[d], &rs[d]);
-    __syncthreads();
     const int32_t* ar = acc + (size_t)row * (q_dim + 2 * kv_dim);
     const float am = amax[row];
     const double osq = output_scale(sq, am), osk = output_scale(sk, am), osv = output_scale(sv, am);
+    const bool qn = qk.q != nullptr, kn = qk.k != nullptr;
+    if (qn || kn) {  // uniform
+        for (int t = threadIdx.x; t < heads + kv_heads; t += blockDim.x) {
+            if (t < heads) {
+                if (qn) inv_s[t] = qk_inv_rms(head_sum_sq<false>(ar, osq, bq, t * hd, hd), hd, qk.eps);
+            } else if (kn) {
+                const int h = t - heads;
+                inv_s[t] = qk_inv_rms(head_sum_sq<true>(ar + q_dim, osk, bk, h * hd, hd), hd, qk.eps);
+            }
+        }
+    }
+    __syncthreads();
     cache_k += (size_t)b * msl * kv_dim;
     cache_v += (size_t)b * msl * kv_dim;
     const bool latest = pos + msl >= base + seq;
@@ -343,12 +426,16 @@ __global__ __launch_bounds__(256) void qkv_rope_kernel(
         if (r < qp) {
             const int h = r / half, d = r % half;
             const int j0 = h * hd + d, j1 = j0 + half;
-            q_pair(ar, osq, bq, j0, j1, rc[d], rs[d], &qr[j0], &qr[j1]);
+            const HeadNorm hn = head_norm(qn, qn ? inv_s[h] : 0.0, qk.q, qk.q_len, heads, hd, h, d,
+                                          d + half);
+            q_pair(ar, osq, bq, j0, j1, rc[d], rs[d], &qr[j0], &qr[j1], hn);
         } else if (r < qp + kp) {
             const int t = r - qp;
             const int h = t / half, d = t % half;
             const int j0 = h * hd + d, j1 = j0 + half;
-            if (latest) k_pair(ar + q_dim, osk, bk, j0, j1, rc[d], rs[d], &kr[j0], &kr[j1]);
+            const HeadNorm hn = head_norm(kn, kn ? inv_s[heads + h] : 0.0, qk.k, qk.k_len, kv_heads, hd,
+                                          h, d, d + half);
+            if (latest) k_pair(ar + q_dim, osk, bk, j0, j1, rc[d], rs[d], &kr[j0], &kr[j1], hn);
         } else {
             const int j = r - qp - kp;
             if (latest) vr[j] = v_val(ar + q_dim + kv_dim, osv, bv, j);
@@ -359,16 +446,17 @@ __global__ __launch_bounds__(256) void qkv_rope_kernel(
 hipError_t launch_qkv_rope(const int32_t* acc, const float* amax, float sq, float sk, float sv,
                            const float* bq, const float* bk, const float* bv, int batch, int seq,
                            const int* pos0, int msl, int heads, int kv_heads, int hd, double theta,
-                           double* q, float* cache_k, float* cache_v, hipStream_t s) {
+                           double* q, float* cache_k, float* cache_v, hipStream_t s, const QkNorm& qk) {
     const long rows = (long)batch * seq;
     if (rows <= 0) return hipSuccess;
     if (hd % 2 != 0 || hd / 2 > kRopeMaxHalf) return hipErrorInvalidValue;
+    if ((qk.q || qk.k) && heads + kv_heads > kQkNormMaxHeads) return hipErrorInvalidValue;
     if (theta <= 0.0) theta = 10000.0;
     const int per_row = heads * (hd / 2) + kv_heads * (hd / 2) + kv_heads * hd;
     const int parts = rows >= 256 ? 1 : ceil_div(per_row, 256);
     hipLaunchKernelGGL(qkv_rope_kernel, dim3((unsigned)rows, parts), dim3(256), 0, s, acc, amax, sq,
                        sk, sv, bq, bk, bv, batch, seq, pos0, msl, heads, kv_heads, hd, theta, q,
-                       cache_k, cache_v);
+                       cache_k, cache_v, qk);
     return hipGetLastError();
 }
 
@@ -1162,7 +1250,18 @@ struct RopeArgs {
     const float* bv;
     double theta;
     double* q_tap;  // debug tap: Q rows after bias and RoPE (rows x q_dim), written by chunk 0
+    QkNorm qk;      // per-head Q/K norms (the QKN kernels only)
 };
+
+// The norm factor of one head from its squares in LDS (sq[0..hd)): every lane
+// forms the dimension-order chain itself (the same address for all lanes).
+template <int HD>
+__device__ __forceinline__ double lds_head_inv(const double* sq, double eps) {
+    double s = 0.0;
+#pragma unroll 16
+    for (int d = 0; d < HD; ++d) s = s + sq[d];
+    return qk_inv_rms(s, HD, eps);
+}
 
 // strict part 1: the scores of one 64-position chunk for every query head of
 // one KV head, and each head's chunk maximum.  The chunk's K rows are copied
@@ -1175,8 +1274,10 @@ struct RopeArgs {
 // qkv_rope_kernel (each lane computes the rotation angle of its own pair), and
 // the workgroup whose chunk holds the new position writes that position's K
 // and V rows to the cache and takes the K row into LDS itself.  No other
-// workgroup reads that row.  grid (kv_heads, nchunk, rows), 256 threads.
-template <int HD, bool ROPE>
+// workgroup reads that row.  QKN: the per-head Q/K norms run before the
+// rotation (each head's squares staged in LDS, the chain formed by every lane
+// of the head's wave).  grid (kv_heads, nchunk, rows), 256 threads.
+template <int HD, bool ROPE, bool QKN = false>
 __global__ __launch_bounds__(256) void attn_scores_gqa_kernel(const double* __restrict__ q,
                                                               float* cache_k, float* cache_v,
                                                               const int* __restrict__ pos0, int msl,
@@ -1191,6 +1292,7 @@ __global__ __launch_bounds__(256) void attn_scores_gqa_kernel(const double* __re
     static_assert(NK * 256 == CH * PR4, "chunk geometry");
     __shared__ __align__(16) float ks[CH * KP];
     __shared__ double qs[4][HD];
+    __shared__ double nsq[QKN ? 4 : 1][QKN ? HD : 1];  // one head's squares per wave
     const int kvh = blockIdx.x, chunk = blockIdx.y, row = blockIdx.z;
     const int G = heads / kv_heads;
     const int b = row / seq, s = row % seq;
@@ -1223,6 +1325,18 @@ __global__ __launch_bounds__(256) void attn_scores_gqa_kernel(const double* __re
             rcos[a] = rsin[a] = 0.0;
             if (d < HALF) rope_angle(pos, d, HD, ra.theta, &rcos[a], &rsin[a]);
         }
+        double kinv = 0.0;
+        if (QKN && newrow && ra.qk.k) {  // uniform: the new K row's squares, then its norm factor
+            const double osk = output_scale(ra.sk, am);
+            for (int d = tid; d < HD; d += 256) {
+                const int j = q_dim + kvh * HD + d;
+                const double v = (double)(float)((double)ar[j] * osk + (ra.bk ? (double)ra.bk[j - q_dim] : 0.0));
+                nsq[0][d] = v * v;
+            }
+            __syncthreads();
+            kinv = lds_head_inv<HD>(nsq[0], ra.qk.eps);
+            __syncthreads();  // nsq is reused by the Q rounds
+        }
         if (newrow && wave == 0) {
             // the new position's K pairs (lane d: d, d + HD/2) and V values
             const double osk = output_scale(ra.sk, am), osv = output_scale(ra.sv, am);
@@ -1234,8 +1348,10 @@ __global__ __launch_bounds__(256) void attn_scores_gqa_kernel(const double* __re
                 const int d = lane + 64 * a;
                 if (d < HALF) {
                     float o0, o1;
+                    const HeadNorm hn = head_norm(QKN && ra.qk.k != nullptr, kinv, ra.qk.k, ra.qk.k_len,
+                                                  kv_heads, HD, kvh, d, d + HALF);
                     k_pair(ar + q_dim, osk, ra.bk, kvh * HD + d, kvh * HD + d + HALF, rcos[a], rsin[a],
-                           &o0, &o1);
+                           &o0, &o1, hn);
                     krow[d] = o0;
                     krow[d + HALF] = o1;
                     kl[d] = o0;
@@ -1262,6 +1378,18 @@ __global__ __launch_bounds__(256) void attn_scores_gqa_kernel(const double* __re
     for (int m0 = 0; m0 < G; m0 += 4) {
         const int member = m0 + wave;
         const int h = kvh * G + member;
+        double qinv = 0.0;
+        if (QKN && ra.qk.q) {  // uniform: the head's squares, then its norm factor
+            if (member < G) {
+                for (int d = lane; d < HD; d += 64) {
+                    const int j = h * HD + d;
+                    const double v = (double)ar[j] * osq + (ra.bq ? (double)ra.bq[j] : 0.0);
+                    nsq[wave][d] = v * v;
+                }
+            }
+            __syncthreads();
+            if (member < G) qinv = lds_head_inv<HD>(nsq[wave], ra.qk.eps);
+        }
         if (member < G) {
             if (ROPE) {
 #pragma unroll
@@ -1269,7 +1397,10 @@ __global__ __launch_bounds__(256) void attn_scores_gqa_kernel(const double* __re
                     const int d = lane + 64 * a;
                     if (d < HALF) {
                         double o0, o1;
-                        q_pair(ar, osq, ra.bq, h * HD + d, h * HD + d + HALF, rcos[a], rsin[a], &o0, &o1);
+                        const HeadNorm hn = head_norm(QKN && ra.qk.q != nullptr, qinv, ra.qk.q, ra.qk.q_len,
+                                                      heads, HD, h, d, d + HALF);
+                        q_pair(ar, osq, ra.bq, h * HD + d, h * HD + d + HALF, rcos[a], rsin[a], &o0, &o1,
+                               hn);
                         qs[wave][d] = o0;
                         qs[wave][d + HALF] = o1;
                         if (ra.q_tap && chunk == 0) {
@@ -1311,7 +1442,9 @@ __global__ __launch_bounds__(256) void attn_scores_gqa_kernel(const double* __re
     }
 }
 
-template <int HD, bool ROPE>
+// QKN (with ROPE): the per-head Q/K norms run before the rotation, as in
+// attn_scores_gqa_kernel.
+template <int HD, bool ROPE, bool QKN = false>
 __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict__ q, float* cache_k,
                                                        float* cache_v, const int* __restrict__ pos0,
                                                        int msl, int span, int heads, int kv_heads,
@@ -1326,6 +1459,7 @@ __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict_
     __shared__ double qs[4][HD];
     __shared__ double ps[4][CH];
     __shared__ double rc[ROPE ? HD / 2 : 1], rsn[ROPE ? HD / 2 : 1];
+    __shared__ double nsq[QKN ? 4 : 1][QKN ? HD : 1];  // one head's squares per wave
     const int kvh = blockIdx.x, chunk = blockIdx.y, row = blockIdx.z;
     const int G = heads / kv_heads;
     const int b = row / seq, s = row % seq;
@@ -1398,7 +1532,19 @@ __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict_
         *(float4*)&vs[r * KP + c4] = r >= n ? make_float4(0.0f, 0.0f, 0.0f, 0.0f) : vreg[j];
     }
     if (ROPE) {
-        __syncthreads();  // angles; the chunk's K/V rows in LDS
+        double kinv = 0.0;
+        if (QKN && newrow && ra.qk.k) {  // uniform: the new K row's squares, then its norm factor
+            const double osk = output_scale(ra.sk, am);
+            if (tid < HD / 2) {
+                const double v0 = (double)(float)((double)ka0 * osk + (ra.bk ? (double)kb0 : 0.0));
+                const double v1 = (double)(float)((double)ka1 * osk + (ra.bk ? (double)kb1 : 0.0));
+                nsq[0][tid] = v0 * v0;
+                nsq[0][tid + HD / 2] = v1 * v1;
+            }
+            __syncthreads();
+            kinv = lds_head_inv<HD>(nsq[0], ra.qk.eps);
+        }
+        __syncthreads();  // angles; the chunk's K/V rows in LDS; nsq reads done
         if (newrow) {
             const int rr = pos - k0;
             float* krow = cache_k + (size_t)b * msl * kv_dim + (size_t)(pos % msl) * kv_dim;
@@ -1406,8 +1552,10 @@ __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict_
             if (tid < HD / 2) {
                 const int j0 = kvh * HD + tid, j1 = j0 + HD / 2;
                 float o0, o1;
+                const HeadNorm hn = head_norm(QKN && ra.qk.k != nullptr, kinv, ra.qk.k, ra.qk.k_len, kv_heads,
+                                              HD, kvh, tid, tid + HD / 2);
                 k_pair_v(ka0, ka1, output_scale(ra.sk, am), ra.bk != nullptr, kb0, kb1, rc[tid], rsn[tid],
-                         &o0, &o1);
+                         &o0, &o1, hn);
                 ks[rr * KP + tid] = o0;
                 ks[rr * KP + tid + HD / 2] = o1;
                 krow[j0] = o0;
@@ -1428,6 +1576,19 @@ __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict_
         const bool act = g < G;
         const int h = kvh * G + g;
         const size_t rh = (size_t)row * heads + h;
+        double qinv = 0.0;
+        if (QKN && ra.qk.q) {  // uniform: the head's squares, then its norm factor
+            if (act) {
+                const double os = output_scale(ra.sq, am);
+                for (int d = lane; d < HD; d += 64) {
+                    const int j = h * HD + d;
+                    const double v = (double)ar[j] * os + (ra.bq ? (double)ra.bq[j] : 0.0);
+                    nsq[wave][d] = v * v;
+                }
+            }
+            __syncthreads();
+            if (act) qinv = lds_head_inv<HD>(nsq[wave], ra.qk.eps);
+        }
         if (act) {
             if (ROPE) {
                 const double os = output_scale(ra.sq, am);
@@ -1435,7 +1596,9 @@ __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict_
                 if (g0 == 0) {  // operands loaded with the K/V rows
                     if (lane < HD / 2) {
                         double o0, o1;
-                        q_pair_v(qa0, qa1, os, ra.bq != nullptr, qb0, qb1, rc[lane], rsn[lane], &o0, &o1);
+                        const HeadNorm hn = head_norm(QKN && ra.qk.q != nullptr, qinv, ra.qk.q, ra.qk.q_len,
+                                                      heads, HD, h, lane, lane + HD / 2);
+                        q_pair_v(qa0, qa1, os, ra.bq != nullptr, qb0, qb1, rc[lane], rsn[lane], &o0, &o1, hn);
                         qs[wave][lane] = o0;
                         qs[wave][lane + HD / 2] = o1;
                         if (qt) {
@@ -1447,7 +1610,9 @@ __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict_
                     for (int d = lane; d < HD / 2; d += 64) {
                         const int j0 = h * HD + d, j1 = j0 + HD / 2;
                         double o0, o1;
-                        q_pair(ar, os, ra.bq, j0, j1, rc[d], rsn[d], &o0, &o1);
+                        const HeadNorm hn = head_norm(QKN && ra.qk.q != nullptr, qinv, ra.qk.q, ra.qk.q_len,
+                                                      heads, HD, h, d, d + HD / 2);
+                        q_pair(ar, os, ra.bq, j0, j1, rc[d], rsn[d], &o0, &o1, hn);
                         qs[wave][d] = o0;
                         qs[wave][d + HD / 2] = o1;
                         if (qt) {
@@ -1976,7 +2141,10 @@ static hipError_t launch_strict_decode(const double* q, float* cache_k, float* c
     constexpr int DG = kChainCols;
 #define LAMD_SCORES(HDV)                                                                          \
     {                                                                                             \
-        if (ra.acc)                                                                               \
+        if (ra.acc && (ra.qk.q || ra.qk.k))                                                       \
+            hipLaunchKernelGGL((attn_scores_gqa_kernel<HDV, true, true>), gs, t, 0, s, q, cache_k,  \
+                               cache_v, pos0, msl, span, heads, kv_heads, seq, sc, ra);           \
+        else if (ra.acc)                                                                          \
             hipLaunchKernelGGL((attn_scores_gqa_kernel<HDV, true>), gs, t, 0, s, q, cache_k, cache_v, \
                                pos0, msl, span, heads, kv_heads, seq, sc, ra);                    \
         else                                                                                      \
@@ -2012,26 +2180,36 @@ hipError_t launch_attention_rope(const int32_t* acc, const float* amax, float sq
                                  const float* bq, const float* bk, const float* bv, double theta,
                                  int batch, const int* pos0, int msl, int span, int heads,
                                  int kv_heads, int hd, int strict, float* cache_k, float* cache_v,
-                                 double* scratch, double* out, hipStream_t s, double* q_tap) {
+                                 double* scratch, double* out, hipStream_t s, double* q_tap,
+                                 const QkNorm& qk) {
     if (batch <= 0) return hipSuccess;
     if (!attention_rope_ok(1, hd, strict, span) || span > msl || !scratch || !acc)
         return hipErrorInvalidValue;
     if (kv_heads <= 0 || heads % kv_heads != 0 || batch > kSplitMaxRows) return hipErrorInvalidValue;
     if (theta <= 0.0) theta = 10000.0;
     const DecodeScratch sc = decode_scratch(scratch, batch, heads, hd, span);
-    const RopeArgs ra{acc, amax, sq, sk, sv, bq, bk, bv, theta, q_tap};
+    const RopeArgs ra{acc, amax, sq, sk, sv, bq, bk, bv, theta, q_tap, qk};
+    const bool qkn = qk.q || qk.k;
     if (strict) {
         return launch_strict_decode(nullptr, cache_k, cache_v, pos0, msl, span, heads, kv_heads, hd, 1,
                                     batch, sc, ra, out, s);
     }
     const dim3 g(kv_heads, attn_nchunk32(span), batch), gc(heads, hd / 32, batch);
     if (hd == 128) {
-        hipLaunchKernelGGL((attn_gqa_kernel<128, true>), g, dim3(256), 0, s, nullptr, cache_k, cache_v,
-                           pos0, msl, span, heads, kv_heads, 1, sc, ra);
+        if (qkn)
+            hipLaunchKernelGGL((attn_gqa_kernel<128, true, true>), g, dim3(256), 0, s, nullptr, cache_k,
+                               cache_v, pos0, msl, span, heads, kv_heads, 1, sc, ra);
+        else
+            hipLaunchKernelGGL((attn_gqa_kernel<128, true>), g, dim3(256), 0, s, nullptr, cache_k, cache_v,
+                               pos0, msl, span, heads, kv_heads, 1, sc, ra);
         hipLaunchKernelGGL(attn_combine32_kernel<128>, gc, dim3(256), 0, s, pos0, span, heads, 1, sc, out);
     } else {
-        hipLaunchKernelGGL((attn_gqa_kernel<64, true>), g, dim3(256), 0, s, nullptr, cache_k, cache_v,
-                           pos0, msl, span, heads, kv_heads, 1, sc, ra);
+        if (qkn)
+            hipLaunchKernelGGL((attn_gqa_kernel<64, true, true>), g, dim3(256), 0, s, nullptr, cache_k,
+                               cache_v, pos0, msl, span, heads, kv_heads, 1, sc, ra);
+        else
+            hipLaunchKernelGGL((attn_gqa_kernel<64, true>), g, dim3(256), 0, s, nullptr, cache_k, cache_v,
+                               pos0, msl, span, heads, kv_heads, 1, sc, ra);
         hipLaunchKernelGGL(attn_combine32_kernel<64>, gc, dim3(256), 0, s, pos0, span, heads, 1, sc, out);
     }
     return hipGetLastError();

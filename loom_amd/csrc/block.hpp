@@ -22,13 +22,30 @@ hipError_t launch_rmsnorm_quant(const float* x, long ldx, int m, int n, const fl
                                 double eps, int strict, float* y, int8_t* xq, int ldq, float* amax,
                                 int32_t* xsum, hipStream_t s, double* totals = nullptr);
 
-// Rescale + bias + RoPE of the stacked Q/K/V accumulators (batch*seq rows of
-// q_dim + 2*kv_dim int32): Q rows to q (fp64, rows x q_dim), K/V rows into
-// the fp32 ring caches (batch slots of msl x kv_dim) at positions *pos0 + s.
+// Per-head Q/K RMSNorm weights (QNormWeight / KNormWeight of loom's MHA,
+// applyPerHeadRMSNorm*, poly/mha.go:584-646), device pointers: q (k) null
+// applies no norm to Q (K); *_len is the weights' length (head_dim: shared by
+// the heads, heads*head_dim: one block per head, any other: unit weights);
+// eps as mhaQKNormEpsilon (poly/mha.go:19-24).  At most kQkNormMaxHeads Q and
+// K heads together.
+constexpr int kQkNormMaxHeads = 512;
+struct QkNorm {
+    const float* q = nullptr;
+    int q_len = 0;
+    const float* k = nullptr;
+    int k_len = 0;
+    double eps = 1e-6;
+};
+
+// Rescale + bias (+ per-head Q/K norms) + RoPE of the stacked Q/K/V
+// accumulators (batch*seq rows of q_dim + 2*kv_dim int32): Q rows to q (fp64,
+// rows x q_dim), K/V rows into the fp32 ring caches (batch slots of msl x
+// kv_dim) at positions *pos0 + s.
 hipError_t launch_qkv_rope(const int32_t* acc, const float* amax, float sq, float sk, float sv,
                            const float* bq, const float* bk, const float* bv, int batch, int seq,
                            const int* pos0, int msl, int heads, int kv_heads, int hd, double theta,
-                           double* q, float* cache_k, float* cache_v, hipStream_t s);
+                           double* q, float* cache_k, float* cache_v, hipStream_t s,
+                           const QkNorm& qk = QkNorm{});
 
 // Causal attention of batch x seq queries at positions *pos0 + s over each
 // sequence's ring cache.  span >= *pos0 + seq must hold (LDS holds span
@@ -50,7 +67,7 @@ hipError_t launch_attention_rope(const int32_t* acc, const float* amax, float sq
                                  int batch, const int* pos0, int msl, int span, int heads,
                                  int kv_heads, int hd, int strict, float* cache_k, float* cache_v,
                                  double* scratch, double* out, hipStream_t s,
-                                 double* q_tap = nullptr);
+                                 double* q_tap = nullptr, const QkNorm& qk = QkNorm{});
 hipError_t launch_attention(const double* q, const float* cache_k, const float* cache_v,
                             int batch, int seq, const int* pos0, int msl, int span, int heads,
                             int kv_heads, int hd, int strict, int fast_qt, double* scratch, double* out,

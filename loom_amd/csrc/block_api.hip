@@ -28,6 +28,7 @@ struct BlockDev {
     float sq = 1.0f, sk = 1.0f, sv = 1.0f;
     float *norm1 = nullptr, *norm2 = nullptr, *attn_norm = nullptr, *ffn_norm = nullptr;
     float *bq = nullptr, *bk = nullptr, *bv = nullptr, *bo = nullptr;
+    QkNorm qk;  // per-head Q/K norms (device weights; none when null)
     float *cache_k = nullptr, *cache_v = nullptr;  // max_batch x msl x kv_dim
     void* weights = nullptr;
     void* params = nullptr;
@@ -206,6 +207,14 @@ static int build_block(int device, const loom_amd_block_desc* d, const loom_amd_
         return -1;
     }
     if (!w->norm1 || !w->norm2) return fail("norm1 and norm2 gains are required");
+    if (w->q_norm_len < 0 || w->k_norm_len < 0 || (w->q_norm_len > 0 && !w->q_norm) ||
+        (w->k_norm_len > 0 && !w->k_norm)) {
+        return fail("block weights: per-head norm weights and lengths disagree");
+    }
+    if ((w->q_norm_len > 0 || w->k_norm_len > 0) && B->heads + B->kv_heads > kQkNormMaxHeads) {
+        return fail("block desc: per-head Q/K norms support at most " + std::to_string(kQkNormMaxHeads) +
+                    " Q and K heads together");
+    }
     DeviceGuard guard(device);
 
     // weights: stacked [Q; K; V] then O, gate, up, down, each 256-byte aligned
@@ -255,6 +264,8 @@ static int build_block(int device, const loom_amd_block_desc* d, const loom_amd_
     const size_t p_bk = P.take(w->bias_k ? (size_t)B->kv_dim * 4 : 0);
     const size_t p_bv = P.take(w->bias_v ? (size_t)B->kv_dim * 4 : 0);
     const size_t p_bo = P.take(w->bias_o ? (size_t)H * 4 : 0);
+    const size_t p_qn = P.take((size_t)(w->q_norm_len > 0 ? w->q_norm_len : 0) * 4);
+    const size_t p_kn = P.take((size_t)(w->k_norm_len > 0 ? w->k_norm_len : 0) * 4);
     e = hipMalloc(&B->params, P.off);
     if (e != hipSuccess) {
         free_block(B);
@@ -274,6 +285,17 @@ static int build_block(int device, const loom_amd_block_desc* d, const loom_amd_
     up(&B->bk, w->bias_k, p_bk, B->kv_dim);
     up(&B->bv, w->bias_v, p_bv, B->kv_dim);
     up(&B->bo, w->bias_o, p_bo, H);
+    // QNormWeight / KNormWeight apply when non-empty (poly/mha.go:285-290),
+    // with eps from mhaQKNormEpsilon (poly/mha.go:19-24)
+    float* qn = nullptr;
+    float* kn = nullptr;
+    if (w->q_norm_len > 0) up(&qn, w->q_norm, p_qn, (size_t)w->q_norm_len);
+    if (w->k_norm_len > 0) up(&kn, w->k_norm, p_kn, (size_t)w->k_norm_len);
+    B->qk.q = qn;
+    B->qk.q_len = w->q_norm_len;
+    B->qk.k = kn;
+    B->qk.k_len = w->k_norm_len;
+    B->qk.eps = d->attn_eps > 0 ? d->attn_eps : 1e-6;
 
     // KV rings, zeroed like a fresh loom cache
     const size_t cache_bytes = (size_t)B->max_batch * B->cache_slot() * 4;
@@ -351,11 +373,11 @@ static int block_forward_dev(const BlockDev& B, const Workspace& W, float* x, in
         e = launch_attention_rope(W.acc, W.amax, B.sq, B.sk, B.sv, B.bq, B.bk, B.bv, B.theta, batch, pos,
                                   B.msl, B.span(), B.heads, B.kv_heads, B.hd, B.strict, B.cache_k,
                                   B.cache_v,
-                                  W.scores, W.attn, s, T.q);
+                                  W.scores, W.attn, s, T.q, B.qk);
         if (e != hipSuccess) return fail_hip("block attention", e);
     } else {
         e = launch_qkv_rope(W.acc, W.amax, B.sq, B.sk, B.sv, B.bq, B.bk, B.bv, batch, seq, pos, B.msl,
-                            B.heads, B.kv_heads, B.hd, B.theta, W.q, B.cache_k, B.cache_v, s);
+                            B.heads, B.kv_heads, B.hd, B.theta, W.q, B.cache_k, B.cache_v, s, B.qk);
         if (e != hipSuccess) return fail_hip("block qkv rope", e);
         TAP(tap_copy(T.q, W.q, (size_t)R * B.q_dim * 8, s));
         e = launch_attention(W.q, B.cache_k, B.cache_v, batch, seq, pos, B.msl, B.span(), B.heads,

@@ -80,6 +80,11 @@ class BlockWeights:
     bias_k: np.ndarray | None = None
     bias_v: np.ndarray | None = None
     bias_o: np.ndarray | None = None
+    # per-head Q / K RMSNorm weights (loom's QNormWeight / KNormWeight,
+    # poly/mha.go:285-290): None or empty applies none; eps from attn_eps
+    # (mhaQKNormEpsilon: RMSNormEps, else 1e-6)
+    q_norm: np.ndarray | None = None
+    k_norm: np.ndarray | None = None
 
     def struct(self, keep: list) -> _lib.BlockWeights:
         def host(a):
@@ -93,7 +98,13 @@ class BlockWeights:
                                  self.gate.handle, self.up.handle, self.down.handle,
                                  host(self.norm1), host(self.norm2), host(self.attn_inner_norm),
                                  host(self.ffn_inner_norm), host(self.bias_q), host(self.bias_k),
-                                 host(self.bias_v), host(self.bias_o))
+                                 host(self.bias_v), host(self.bias_o),
+                                 host(self.q_norm), _length(self.q_norm),
+                                 host(self.k_norm), _length(self.k_norm))
+
+
+def _length(a) -> int:
+    return 0 if a is None else int(np.asarray(a).size)
 
 
 @dataclass

@@ -943,8 +943,65 @@ void orc_attn_out(const orc_matrix* o, const float* bias_o, const float* inner_n
     free(to);
 }
 
+/* mhaQKNormEpsilon (poly/mha.go:19-24): the layer's RMSNormEps when set,
+ * else 1e-6 (the inner norm's own default is 1e-5, poly/bitnet_cpu.go:868-874). */
+double orc_qk_norm_eps(double layer_eps) {
+    return layer_eps > 0 ? layer_eps : 1e-6;
+}
+
+/* The gamma element of dimension d of head h: gamma[d] when the weights hold
+ * one head, gamma[h*hd + d] when they hold every head, else 1 (both
+ * applyPerHeadRMSNorm variants, poly/mha.go:605-611, 634-640). */
+static double per_head_gamma(const float* gamma, int gamma_len, int heads, int hd, int h, int d) {
+    if (gamma_len == hd) return (double)gamma[d];
+    if (gamma_len == heads * hd) return (double)gamma[(size_t)h * hd + d];
+    return 1.0;
+}
+
+/* applyPerHeadRMSNormFloat64 (poly/mha.go:584-614): per head, the sequential
+ * fp64 sum of squares, rms = sqrt(sumSq/hd + eps) (eps <= 0 -> 1e-6), a head
+ * with rms == 0 left unchanged, then x = x * (1/rms) * gamma, left to right. */
+void orc_per_head_rmsnorm_f64(double* data, const float* gamma, int gamma_len, int heads,
+                              int hd, double eps) {
+    if (heads <= 0 || hd <= 0) return;
+    if (eps <= 0) eps = 1e-6;
+    for (int h = 0; h < heads; h++) {
+        double* x = data + (size_t)h * hd;
+        double sum_sq = 0.0;
+        for (int i = 0; i < hd; i++) sum_sq += x[i] * x[i];
+        const double rms = sqrt(sum_sq / (double)hd + eps);
+        if (rms == 0) continue;
+        const double inv = 1.0 / rms;
+        for (int d = 0; d < hd; d++) {
+            x[d] = x[d] * inv * per_head_gamma(gamma, gamma_len, heads, hd, h, d);
+        }
+    }
+}
+
+/* applyPerHeadRMSNormTensor for T = float32 (poly/mha.go:616-646): the same
+ * on fp32 values widened to fp64, each result rounded back to fp32. */
+void orc_per_head_rmsnorm_f32(float* data, const float* gamma, int gamma_len, int heads, int hd,
+                              double eps) {
+    if (heads <= 0 || hd <= 0) return;
+    if (eps <= 0) eps = 1e-6;
+    for (int h = 0; h < heads; h++) {
+        float* x = data + (size_t)h * hd;
+        double sum_sq = 0.0;
+        for (int i = 0; i < hd; i++) {
+            const double v = (double)x[i];
+            sum_sq += v * v;
+        }
+        const double rms = sqrt(sum_sq / (double)hd + eps);
+        if (rms == 0) continue;
+        const double inv = 1.0 / rms;
+        for (int d = 0; d < hd; d++) {
+            x[d] = (float)((double)x[d] * inv * per_head_gamma(gamma, gamma_len, heads, hd, h, d));
+        }
+    }
+}
+
 /* MHAForwardPackedTernaryCPU (poly/mha.go:204-371) for one batch row of
- * `seq` tokens.  Per-head Q/K norms are not supported (BitNet has none).
+ * `seq` tokens, with the optional per-head Q/K norms of poly/mha.go:285-290.
  * The KV cache is a ring of msl rows (pos % msl), prepared as
  * mhaPrepareKVForForward does (poly/mha_layout.go:62-70): a pass that is not
  * a warm single-token step resets kv_offset to 0. */
@@ -978,6 +1035,14 @@ void orc_mha_project(orc_mha* L, const float* in, int seq, int seq_base, int sim
         for (int i = 0; i < kv_dim; i++) {
             krow[i] = (float)(tk[i] + (L->bias_k ? (double)L->bias_k[i] : 0.0));
             vrow[i] = (float)(tv[i] + (L->bias_v ? (double)L->bias_v[i] : 0.0));
+        }
+        if (L->q_norm_len > 0) {
+            orc_per_head_rmsnorm_f64(Q + (size_t)s * q_dim, L->q_norm, L->q_norm_len, heads, hd,
+                                     orc_qk_norm_eps(L->eps));
+        }
+        if (L->k_norm_len > 0) {
+            orc_per_head_rmsnorm_f32(krow, L->k_norm, L->k_norm_len, kv_heads, hd,
+                                     orc_qk_norm_eps(L->eps));
         }
         for (int h = 0; h < heads; h++) {
             for (int d = 0; d < half; d++) {

@@ -139,6 +139,12 @@ typedef struct orc_mha {
     float* cache_k;            /* msl * kv_dim, caller-owned */
     float* cache_v;
     int kv_offset;             /* tokens already cached (in/out) */
+    /* per-head Q / K RMSNorm weights (QNormWeight / KNormWeight); a length of
+     * 0 applies no norm (poly/mha.go:285-290), eps from mhaQKNormEpsilon */
+    const float* q_norm;
+    int q_norm_len;
+    const float* k_norm;
+    int k_norm_len;
 } orc_mha;
 
 void orc_attention(const double* Q, const float* cache_k, const float* cache_v, int seq,
@@ -156,6 +162,11 @@ void orc_attn_out(const orc_matrix* o, const float* bias_o, const float* inner_n
  * `seq` rows at positions seq_base + s: shared quantization, Q (fp64 + bias),
  * K/V rows (fp32 + bias) into the ring caches, RoPE on Q and the cached K.
  * Q receives seq x q_dim; kv_offset is not changed. */
+void orc_per_head_rmsnorm_f64(double* data, const float* gamma, int gamma_len, int heads,
+                              int hd, double eps);
+void orc_per_head_rmsnorm_f32(float* data, const float* gamma, int gamma_len, int heads, int hd,
+                              double eps);
+double orc_qk_norm_eps(double layer_eps);
 void orc_mha_project(orc_mha* L, const float* in, int seq, int seq_base, int simd, int workers,
                      double* Q);
 void orc_mha_forward(orc_mha* L, const float* in, int seq, int simd, int workers,

@@ -84,6 +84,9 @@ def _declare(L: C.CDLL) -> None:
         "orc_attn_out": (None, [P, P, P, d, P, i, i, i, i, P, P]),
         "orc_mha_forward": (None, [P, P, i, i, i, P, P, P, P]),
         "orc_mha_project": (None, [P, P, i, i, i, i, P]),
+        "orc_per_head_rmsnorm_f64": (None, [P, P, i, i, i, d]),
+        "orc_per_head_rmsnorm_f32": (None, [P, P, i, i, i, d]),
+        "orc_qk_norm_eps": (d, [d]),
         "orc_dense_quantized": (None, [P, P, P, i, P, i, i, P]),
         "orc_swiglu_gate_rows": (None, [P, P, P, i, P, P, i, i, i, P]),
         "orc_block_forward": (None, [P, P, i, i, i]),
@@ -447,7 +450,8 @@ class _CMHA(C.Structure):
                 ("head_dim", C.c_int), ("msl", C.c_int), ("theta", C.c_double),
                 ("eps", C.c_double), ("q", P), ("k", P), ("v", P), ("o", P),
                 ("bias_q", P), ("bias_k", P), ("bias_v", P), ("bias_o", P),
-                ("inner_norm", P), ("cache_k", P), ("cache_v", P), ("kv_offset", C.c_int)]
+                ("inner_norm", P), ("cache_k", P), ("cache_v", P), ("kv_offset", C.c_int),
+                ("q_norm", P), ("q_norm_len", C.c_int), ("k_norm", P), ("k_norm_len", C.c_int)]
 
 
 class _CBlock(C.Structure):
@@ -471,6 +475,22 @@ def attention(q: np.ndarray, cache_k: np.ndarray, cache_v: np.ndarray, seq_base:
     out = np.empty_like(q)
     lib().orc_attention(_p(q), _p(ck), _p(cv), q.shape[0], seq_base, msl, num_heads,
                         num_kv_heads, head_dim, _p(out))
+    return out
+
+
+def per_head_rmsnorm(x: np.ndarray, gamma: np.ndarray | None, heads: int, head_dim: int,
+                     eps: float) -> np.ndarray:
+    """applyPerHeadRMSNormFloat64 (fp64 rows) or applyPerHeadRMSNormTensor
+    (fp32 rows) of poly/mha.go:584-646 on a copy of one row; gamma None or
+    empty: unit weights (any other length than head_dim or heads*head_dim
+    also means unit weights)."""
+    g = np.zeros(0, np.float32) if gamma is None else np.ascontiguousarray(gamma, np.float32)
+    out = np.array(x, copy=True)
+    if out.dtype == np.float64:
+        lib().orc_per_head_rmsnorm_f64(_p(out), _p(g), g.size, heads, head_dim, eps)
+    else:
+        out = np.ascontiguousarray(out, np.float32)
+        lib().orc_per_head_rmsnorm_f32(_p(out), _p(g), g.size, heads, head_dim, eps)
     return out
 
 
@@ -535,7 +555,11 @@ class MHA:
 
     def __init__(self, q: Matrix, k: Matrix, v: Matrix, o: Matrix, num_heads: int,
                  num_kv_heads: int, head_dim: int, msl: int, theta: float = 500000.0,
-                 eps: float = 1e-5, inner_norm: np.ndarray | None = None, simd: bool = True):
+                 eps: float = 1e-5, inner_norm: np.ndarray | None = None, simd: bool = True,
+                 q_norm: np.ndarray | None = None, k_norm: np.ndarray | None = None):
+        """eps is the layer's RMSNormEps (<= 0: the inner norm takes 1e-5 and
+        the per-head Q/K norms 1e-6, poly/mha.go:19-24); q_norm / k_norm are
+        QNormWeight / KNormWeight (None or empty: no per-head norm)."""
         self.mats = (q, k, v, o)
         self.simd = simd
         self.d_model = q.cols
@@ -546,10 +570,14 @@ class MHA:
         self.cache_v = np.zeros(msl * kv_dim, np.float32)
         self.inner_norm = None if inner_norm is None else np.ascontiguousarray(inner_norm, np.float32)
         self._cm = [_cmat(m, simd) for m in self.mats]
+        self.q_norm = None if q_norm is None else np.ascontiguousarray(q_norm, np.float32)
+        self.k_norm = None if k_norm is None else np.ascontiguousarray(k_norm, np.float32)
         self.c = _CMHA(self.d_model, num_heads, num_kv_heads, head_dim, msl, theta, eps,
                        *(C.cast(C.pointer(cm), P) for cm in self._cm),
                        None, None, None, None, _p(self.inner_norm), _p(self.cache_k),
-                       _p(self.cache_v), 0)
+                       _p(self.cache_v), 0,
+                       _p(self.q_norm), 0 if self.q_norm is None else self.q_norm.size,
+                       _p(self.k_norm), 0 if self.k_norm is None else self.k_norm.size)
 
     @property
     def kv_offset(self) -> int:

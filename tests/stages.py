@@ -46,8 +46,14 @@ BITNET_2B = Shape(2560, 20, 5, 128, 6912, 640)  # BitNet-b1.58-2B block (config 
 class Weights:
     """Oracle matrices + fp32 vectors of one block (seeded)."""
 
-    def __init__(self, orc, sh: Shape, seed: int, act: int = ACT_RELU2, bias: bool = False):
+    def __init__(self, orc, sh: Shape, seed: int, act: int = ACT_RELU2, bias: bool = False,
+                 qk: str | None = None, attn_eps: float = 1e-5):
+        """qk: per-head Q/K norm weights (poly/mha.go:285-290): None, "shared"
+        (length head_dim), "per_head" (heads*head_dim and kv_heads*head_dim),
+        "odd" (a Q norm of another length: unit weights; no K norm).
+        attn_eps: the MHA layer's RMSNormEps (0: inner 1e-5, Q/K 1e-6)."""
         self.sh, self.act = sh, act
+        self.attn_eps = attn_eps
         self.q = orc.random_matrix(sh.q_dim, sh.hidden, seed)
         self.k = orc.random_matrix(sh.kv_dim, sh.hidden, seed + 1)
         self.v = orc.random_matrix(sh.kv_dim, sh.hidden, seed + 2)
@@ -63,6 +69,17 @@ class Weights:
         if bias:
             self.bias = [orc.normal_f32(n, seed + 11 + i) * np.float32(0.1)
                          for i, n in enumerate([sh.q_dim, sh.kv_dim, sh.kv_dim, sh.hidden])]
+        self.qn = self.kn = None
+        if qk == "shared":
+            self.qn = orc.uniform_f32(sh.hd, 0.5, 1.5, seed + 20)
+            self.kn = orc.uniform_f32(sh.hd, 0.5, 1.5, seed + 21)
+        elif qk == "per_head":
+            self.qn = orc.uniform_f32(sh.q_dim, 0.5, 1.5, seed + 20)
+            self.kn = orc.uniform_f32(sh.kv_dim, 0.5, 1.5, seed + 21)
+        elif qk == "odd":
+            self.qn = orc.uniform_f32(sh.hd + 3, 0.5, 1.5, seed + 20)
+        elif qk is not None:
+            raise ValueError(qk)
 
     def gpu(self, tf):
         from loom_amd.bitnet import TernaryMatrix
@@ -72,18 +89,21 @@ class Weights:
 
         b = self.bias or [None] * 4
         return tf.BlockWeights(m(self.q), m(self.k), m(self.v), m(self.o), m(self.g), m(self.u),
-                               m(self.d), self.n1, self.n2, self.an, self.fn, *b)
+                               m(self.d), self.n1, self.n2, self.an, self.fn, *b,
+                               q_norm=self.qn, k_norm=self.kn)
 
     def cfg(self, tf, norm="strict", max_batch=1):
         sh = self.sh
         return tf.BlockConfig(sh.hidden, sh.heads, sh.kv, sh.hd, sh.inter, max_seq_len=sh.msl,
                               max_batch=max_batch, rope_theta=sh.theta, norm_eps=1e-5,
-                              attn_eps=1e-5, ffn_eps=1e-5, ffn_activation=self.act, norm=norm)
+                              attn_eps=self.attn_eps, ffn_eps=1e-5, ffn_activation=self.act,
+                              norm=norm)
 
     def oracle_mha(self, orc):
         sh = self.sh
         m = orc.MHA(self.q, self.k, self.v, self.o, sh.heads, sh.kv, sh.hd, sh.msl,
-                    theta=sh.theta, eps=1e-5, inner_norm=self.an)
+                    theta=sh.theta, eps=self.attn_eps, inner_norm=self.an, q_norm=self.qn,
+                    k_norm=self.kn)
         if self.bias:
             # the oracle MHA wrapper has no bias arguments: set them on its C struct
             self._bias_keep = [np.ascontiguousarray(b, np.float32) for b in self.bias]

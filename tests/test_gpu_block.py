@@ -423,6 +423,69 @@ def test_greedy_sample_semantics(orc, torch_dev, tf):
         assert got == orc.argmax_first(row), m
 
 
+# ---------------------------------------------------------------- per-head Q/K norms
+# MHAForwardPackedTernaryCPU normalizes Q (fp64) and the fp32 K cache row per
+# head before RoPE when QNormWeight / KNormWeight are set (poly/mha.go:285-290,
+# 584-646).  The stage checks pin them bit for bit at position 0 (rotation the
+# identity) and within the RoPE bar elsewhere; the prefill runs qkv_rope_kernel,
+# the single-token calls the fused decode attention (strict: the scores kernel,
+# fast: the GQA chunk kernel).
+@pytest.mark.parametrize("norm", ["strict", "fast"])
+@pytest.mark.parametrize("qk", ["shared", "per_head"])
+def test_block_stages_qk_norm(orc, torch_dev, tf, norm, qk):
+    w = Weights(orc, SMALL, seed=191, qk=qk)
+    run_block_case(orc, torch_dev, tf, w, [9, 1, 1], seed=1910, strict=norm == "strict")
+
+
+@pytest.mark.parametrize("norm", ["strict", "fast"])
+def test_block_stages_qk_norm_default_eps_bias_odd_length(orc, torch_dev, tf, norm):
+    # RMSNormEps unset: Q/K eps 1e-6 (mhaQKNormEpsilon), inner norm 1e-5; a Q
+    # norm of another length than head_dim / q_dim applies unit weights; biases
+    w = Weights(orc, SMALL, seed=193, act=ACT_SILU, bias=True, qk="odd", attn_eps=0.0)
+    run_block_case(orc, torch_dev, tf, w, [5, 1, 1], seed=1930, strict=norm == "strict")
+
+
+@pytest.mark.parametrize("norm", ["strict", "fast"])
+def test_block_stages_qk_norm_bitnet_2b_shape(orc, torch_dev, tf, norm):
+    w = Weights(orc, BITNET_2B, seed=195, qk="per_head")
+    run_block_case(orc, torch_dev, tf, w, [70, 1, 1], seed=1950, strict=norm == "strict")
+
+
+def test_block_stages_qk_norm_head_dims(orc, torch_dev, tf):
+    # strict decode scores kernels at head_dim 32 and 256
+    for i, sh in enumerate([Shape(128, 4, 4, 32, 256, 48), Shape(512, 4, 2, 256, 512, 48)]):
+        w = Weights(orc, sh, seed=197 + i, qk="shared")
+        run_block_case(orc, torch_dev, tf, w, [6, 1, 1], seed=1970 + 10 * i)
+
+
+@pytest.mark.parametrize("shape,norm", [("small", "fast"), ("bitnet2b", "fast"),
+                                        ("small", "strict"), ("bitnet2b", "strict")])
+def test_decode_qk_norm_fused_equals_separate(orc, torch_dev, tf, shape, norm, monkeypatch):
+    # the norms inside the fused decode attention equal qkv_rope_kernel's
+    # (LOOM_AMD_UNFUSED_ROPE=1), outputs and caches bit for bit, batch 2
+    torch = torch_dev
+    sh = {"small": SMALL, "bitnet2b": BITNET_2B}[shape]
+    w = Weights(orc, sh, seed=1261, bias=True, qk="per_head")
+    gw = w.gpu(tf)
+    fused = tf.BitNetBlock(w.cfg(tf, norm, max_batch=2), gw)
+    monkeypatch.setenv("LOOM_AMD_UNFUSED_ROPE", "1")
+    plain = tf.BitNetBlock(w.cfg(tf, norm, max_batch=2), gw)
+    monkeypatch.delenv("LOOM_AMD_UNFUSED_ROPE")
+    for i, seq in enumerate([min(62, sh.msl - 8), 1, 1, 1]):
+        x_in = orc.normal_f32(2 * seq * sh.hidden, 1500 + i).reshape(2, seq, sh.hidden)
+        a = to_dev(torch, x_in.reshape(2 * seq, sh.hidden)).reshape(2, seq, sh.hidden)
+        b = a.clone()
+        fused.forward(a)
+        plain.forward(b)
+        torch.cuda.synchronize()
+        assert a.cpu().numpy().tobytes() == b.cpu().numpy().tobytes(), f"call {i}"
+        for slot in (0, 1):
+            for t_a, t_b in zip(fused.kv_cache(slot), plain.kv_cache(slot)):
+                assert t_a.cpu().numpy().tobytes() == t_b.cpu().numpy().tobytes(), f"cache call {i}"
+    fused.release()
+    plain.release()
+
+
 @pytest.mark.parametrize("shape,norm", [("small", "fast"), ("bitnet2b", "fast"),
                                         ("small", "strict"), ("bitnet2b", "strict"),
                                         ("mha32", "strict")])

@@ -95,7 +95,7 @@ def build(tmp_path, rng, dense_o: bool, untied: bool):
     return str(d), ref
 
 
-def direct_model(ref, norm: str, msl: int):
+def direct_model(ref, norm: str, msl: int, attn_eps: float = 1e-5, qk: bool = True):
     from loom_amd import transformer as tf
     from loom_amd.bitnet import TernaryMatrix
     q = HEADS * HD
@@ -112,9 +112,11 @@ def direct_model(ref, norm: str, msl: int):
         layers.append(tf.BlockWeights(m["q_proj"], m["k_proj"], m["v_proj"], m["o_proj"], m["gate_proj"],
                                       m["up_proj"], m["down_proj"], L["input_layernorm"],
                                       L["post_attention_layernorm"], L["self_attn.attn_sub_norm"],
-                                      L["mlp.ffn_sub_norm"]))
+                                      L["mlp.ffn_sub_norm"],
+                                      q_norm=L.get("q_norm") if qk else None,
+                                      k_norm=L.get("k_norm") if qk else None))
     cfg = tf.BlockConfig(H, HEADS, KV, HD, INTER, max_seq_len=msl, rope_theta=THETA, norm_eps=RMS_EPS,
-                         attn_eps=1e-5, ffn_eps=1e-5, ffn_activation=6, norm=norm)
+                         attn_eps=attn_eps, ffn_eps=1e-5, ffn_activation=6, norm=norm)
     return tf.Transformer(cfg, layers, ref["emb"], ref["fnorm"], lm_head=ref.get("lm"), vocab=VOCAB,
                           final_norm_eps=1e-6)
 
@@ -142,16 +144,41 @@ def test_hf_checkpoint_equals_direct_model(torch_dev, tmp_path, dense_o, untied,
     want.release()
 
 
-def test_hf_checkpoint_refuses_qk_norm(torch_dev, tmp_path):
+@pytest.mark.parametrize("norm", ["strict", "fast"])
+def test_hf_checkpoint_qk_norm(torch_dev, tmp_path, norm):
+    # q_norm / k_norm tensors become the layers' QNormWeight / KNormWeight
+    # (poly/prefix_safetensor.go:240-244, 425-434), applied with eps 1e-6: the
+    # import leaves the MHA layer's RMSNormEps unset (poly/hf_decoder.go:43-51,
+    # poly/mha.go:19-24).  The model equals the directly built one with the
+    # same norms and attn_eps 0 (both defaults), and differs from it without
+    # them.
     from loom_amd import checkpoint as ck
     rng = np.random.default_rng(7)
-    path, _ = build(tmp_path, rng, False, False)
+    path, ref = build(tmp_path, rng, False, False)
     import glob
     import os
     f = sorted(glob.glob(os.path.join(path, "*.safetensors")))[0]
     t = {n: (s.dtype, s.shape, np.array(s.raw)) for n, s in ck.read_safetensors(f).items()}
-    qn = bf16_bits(np.ones(HD))
-    t["model.layers.0.self_attn.q_norm.weight"] = ("BF16", qn.shape, qn)
+    qn = [bf16_bits(rng.uniform(0.5, 1.5, HD)) for _ in range(LAYERS)]
+    kn = [bf16_bits(rng.uniform(0.5, 1.5, KV * HD)) for _ in range(LAYERS)]
+    for li in range(LAYERS):
+        t[f"model.layers.{li}.self_attn.q_norm.weight"] = ("BF16", qn[li].shape, qn[li])
+        t[f"model.layers.{li}.self_attn.k_norm.weight"] = ("BF16", kn[li].shape, kn[li])
     ck.write_safetensors(f, t)
-    with pytest.raises(NotImplementedError):
-        ck.load_hf_checkpoint(path, max_seq_len=64)
+    msl = 96
+    got, _ = ck.load_hf_checkpoint(path, norm=norm, max_seq_len=msl)
+    for li in range(LAYERS):
+        ref["layers"][li]["q_norm"] = bf16_value(qn[li])
+        ref["layers"][li]["k_norm"] = bf16_value(kn[li])
+    want = direct_model(ref, norm, msl, attn_eps=0.0)
+    plain = direct_model(ref, norm, msl, attn_eps=0.0, qk=False)
+    ids = rng.integers(0, VOCAB, (1, 30)).astype(np.int32)
+    la = got.prefill(ids, logits=True)
+    lb = want.prefill(ids, logits=True)
+    lc = plain.prefill(ids, logits=True)
+    torch_dev.cuda.synchronize()
+    assert la.cpu().numpy().tobytes() == lb.cpu().numpy().tobytes()
+    assert la.cpu().numpy().tobytes() != lc.cpu().numpy().tobytes()
+    assert np.array_equal(got.generate(ids, 8), want.generate(ids, 8))
+    for m in (got, want, plain):
+        m.release()

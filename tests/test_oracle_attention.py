@@ -385,3 +385,163 @@ def test_attention_chains_detect_another_order(orc):
     assert np.count_nonzero(rev != got) > got.size // 4
     assert np.count_nonzero(tree != got) > got.size // 4
     assert np.max(np.abs(rev - got)) < 1e-13  # same values, other roundings
+
+
+# ---------------------------------------------------------------- per-head Q/K RMSNorm
+def test_qk_norm_eps_rule(orc):
+    # mhaQKNormEpsilon (poly/mha.go:19-24): RMSNormEps when set, else 1e-6
+    assert orc.lib().orc_qk_norm_eps(0.0) == 1e-6
+    assert orc.lib().orc_qk_norm_eps(-1.0) == 1e-6
+    assert orc.lib().orc_qk_norm_eps(1e-5) == 1e-5
+
+
+def test_per_head_rmsnorm_constant_head_closed_form(orc):
+    # a constant head c (a power of two: every square and partial sum exact):
+    # rms = sqrt(c^2 + eps), x = c * (1/rms) * g (poly/mha.go:584-614)
+    heads, hd, c = 3, 64, 0.25
+    for eps in (1e-5, 1e-6):
+        x = np.full(heads * hd, c)
+        got = orc.per_head_rmsnorm(x, None, heads, hd, eps)
+        inv = 1.0 / math.sqrt((hd * (c * c)) / hd + eps)
+        assert np.all(got == c * inv * 1.0)
+    # eps <= 0 inside the helper -> 1e-6
+    a = orc.per_head_rmsnorm(np.full(hd, c), None, 1, hd, 0.0)
+    b = orc.per_head_rmsnorm(np.full(hd, c), None, 1, hd, 1e-6)
+    assert np.array_equal(a, b)
+
+
+def test_per_head_rmsnorm_gamma_lengths(orc):
+    # gamma of length head_dim is shared by every head; of length
+    # heads*head_dim, one block per head; any other length -> unit weights
+    rng = np.random.default_rng(91)
+    heads, hd = 4, 32
+    x = rng.standard_normal(heads * hd)
+    g1 = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    shared = orc.per_head_rmsnorm(x, g1, heads, hd, 1e-6)
+    tiled = orc.per_head_rmsnorm(x, np.tile(g1, heads), heads, hd, 1e-6)
+    assert np.array_equal(shared, tiled)
+    gh = rng.uniform(0.5, 1.5, heads * hd).astype(np.float32)
+    per = orc.per_head_rmsnorm(x, gh, heads, hd, 1e-6)
+    unit = orc.per_head_rmsnorm(x, None, heads, hd, 1e-6)
+    odd = orc.per_head_rmsnorm(x, gh[:hd + 1], heads, hd, 1e-6)
+    assert np.array_equal(odd, unit)
+    for h in range(heads):
+        sl = slice(h * hd, (h + 1) * hd)
+        xs = x[sl]
+        s = 0.0
+        for v in xs:
+            s += v * v
+        inv = 1.0 / math.sqrt(s / hd + 1e-6)
+        assert per[sl].tolist() == [float(a) * inv * float(g) for a, g in zip(xs, gh[sl])]
+        assert unit[sl].tolist() == [float(a) * inv * 1.0 for a in xs]
+
+
+def test_per_head_rmsnorm_order_and_association(orc):
+    # the sum of squares is the dimension-order chain: 2^27 then 63 ones
+    # (each 1 is lost against 2^54 in order; a pairwise sum keeps 64)
+    hd = 64
+    x = np.ones(hd)
+    x[0] = 2.0**27
+    got = orc.per_head_rmsnorm(x, None, 1, hd, 1e-6)
+    inv_chain = 1.0 / math.sqrt(2.0**54 / hd + 1e-6)
+    inv_pair = 1.0 / math.sqrt((2.0**54 + 64) / hd + 1e-6)
+    assert inv_chain != inv_pair
+    assert got[1] == 1.0 * inv_chain * 1.0
+    # x * inv * g is (x * inv) * g: probes where x * (inv * g) rounds differently
+    rng = np.random.default_rng(92)
+    found = 0
+    for _ in range(200):
+        xs = rng.standard_normal(hd)
+        g = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+        out = orc.per_head_rmsnorm(xs, g, 1, hd, 1e-6)
+        s = 0.0
+        for v in xs:
+            s += v * v
+        inv = 1.0 / math.sqrt(s / hd + 1e-6)
+        left = [(float(a) * inv) * float(b) for a, b in zip(xs, g)]
+        right = [float(a) * (inv * float(b)) for a, b in zip(xs, g)]
+        assert out.tolist() == left
+        found += sum(1 for a, b in zip(left, right) if a != b)
+    assert found > 50
+
+
+def test_per_head_rmsnorm_f32_rounds_each_result(orc):
+    # applyPerHeadRMSNormTensor[float32]: fp64 arithmetic on the widened
+    # values, each result rounded to fp32
+    rng = np.random.default_rng(93)
+    heads, hd = 2, 16
+    x = rng.standard_normal(heads * hd).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    got = orc.per_head_rmsnorm(x, g, heads, hd, 1e-6)
+    assert got.dtype == np.float32
+    for h in range(heads):
+        xs = x[h * hd:(h + 1) * hd]
+        s = 0.0
+        for v in xs:
+            s += float(v) * float(v)
+        inv = 1.0 / math.sqrt(s / hd + 1e-6)
+        want = np.array([float(a) * inv * float(b) for a, b in zip(xs, g)], np.float32)
+        assert got[h * hd:(h + 1) * hd].tobytes() == want.tobytes()
+
+
+def _make_mha_qk(orc, seed, q_norm, k_norm, eps=1e-5):
+    q = orc.random_matrix(HEADS * HD, HID, seed=seed)
+    k = orc.random_matrix(KV * HD, HID, seed=seed + 1)
+    v = orc.random_matrix(KV * HD, HID, seed=seed + 2)
+    o = orc.random_matrix(HID, HEADS * HD, seed=seed + 3)
+    wn = orc.uniform_f32(HEADS * HD, 0.5, 1.5, seed=seed + 4)
+    return orc.MHA(q, k, v, o, HEADS, KV, HD, MSL, theta=500000.0, eps=eps, inner_norm=wn,
+                   q_norm=q_norm, k_norm=k_norm)
+
+
+def test_mha_qk_norm_before_rope(orc):
+    # MHAForwardPackedTernaryCPU (poly/mha.go:281-314): Q (fp64, after bias)
+    # and the fp32 K cache row are normalized per head, then rotated.  At
+    # position 0 the rotation is the identity, so Q and K equal the norms of
+    # the plain projections bit for bit; at later positions they equal the
+    # rotation (numpy complex multiply) of the normalized rows within 1e-12,
+    # and differ from normalizing the rotated rows (gamma is per dimension).
+    gq = orc.uniform_f32(HD, 0.5, 1.5, seed=94)
+    gk = orc.uniform_f32(KV * HD, 0.5, 1.5, seed=95)
+    for eps, qk_eps in ((1e-5, 1e-5), (0.0, 1e-6)):
+        x = orc.normal_f32(HID, 96).reshape(1, HID)
+        plain = _make_mha_qk(orc, 97, None, None, eps=eps)
+        q_raw = plain.project(x, 0)[0]
+        k_raw = plain.cache_k[:KV * HD].copy()
+        m = _make_mha_qk(orc, 97, gq, gk, eps=eps)
+        q0 = m.project(x, 0)[0]
+        assert q0.tobytes() == orc.per_head_rmsnorm(q_raw, gq, HEADS, HD, qk_eps).tobytes()
+        assert m.cache_k[:KV * HD].tobytes() == orc.per_head_rmsnorm(k_raw, gk, KV, HD, qk_eps).tobytes()
+        assert np.array_equal(m.cache_v[:KV * HD], plain.cache_v[:KV * HD])  # V untouched
+        pos, half = 37, HD // 2
+        qp = m.project(x, pos)[0]
+        qn = orc.per_head_rmsnorm(q_raw, gq, HEADS, HD, qk_eps)
+
+        def rope(row):
+            out = np.empty_like(row)
+            for h in range(HEADS):
+                d = np.arange(half)
+                ang = pos / np.power(500000.0, 2 * d / HD)
+                z = (row[h * HD:h * HD + half] + 1j * row[h * HD + half:(h + 1) * HD]) * np.exp(1j * ang)
+                out[h * HD:h * HD + half], out[h * HD + half:(h + 1) * HD] = z.real, z.imag
+            return out
+        want = rope(qn)
+        assert np.abs(qp - want).max() <= 1e-12 * np.abs(want).max()
+        other = orc.per_head_rmsnorm(rope(q_raw), gq, HEADS, HD, qk_eps)
+        assert np.abs(qp - other).max() > 1e-6 * np.abs(want).max()
+
+
+def test_mha_qk_norm_forward_composes(orc):
+    # a whole forward with Q/K norms equals its stages: project (with the
+    # norms), attention over the caches, output stage
+    gq = orc.uniform_f32(HEADS * HD, 0.5, 1.5, seed=98)
+    gk = orc.uniform_f32(HD, 0.5, 1.5, seed=99)
+    m = _make_mha_qk(orc, 101, gq, gk)
+    S = 6
+    x = orc.normal_f32(S * HID, 102).reshape(S, HID)
+    pre, post, q, attn = m.forward(x)
+    m2 = _make_mha_qk(orc, 101, gq, gk)
+    q2 = m2.project(x, 0)
+    assert np.array_equal(q2, q)
+    ck, cv = m2.cache_k.reshape(MSL, KV * HD), m2.cache_v.reshape(MSL, KV * HD)
+    assert np.array_equal(orc.attention(q2, ck, cv, 0, MSL, HEADS, KV, HD), attn)
