@@ -129,6 +129,13 @@ int loom_amd_norm_quant_rows(float* h, int m, int n, const float* weight, double
 int loom_amd_ordered_sum_rows(const double* terms, int m, int n, double s0, double* out,
                               int threads, void* stream);
 
+/* Re-reads the LOOM_AMD_* tuning variables (the tuning table of the
+ * library's documentation), which the library otherwise reads once, when it
+ * first plans a launch.  No counterpart in the reference: for tuning runs and
+ * tests that change the variables within one process.  Must not run while
+ * another thread launches work through the library.  Returns 0. */
+int loom_amd_reload_tuning(void);
+
 /* y[i] = exp(x[i]) for n fp64 values (device pointers), with the device exp
  * that every kernel of the library calls: the attention probabilities
  * exp(score - max) of MHAForwardPackedTernaryCPU (poly/mha.go:339-342), the
@@ -162,8 +169,12 @@ int loom_amd_dense_forward(const loom_amd_matrix* w, const float* x, int m, int 
  * growable scratch arena: m * (256*ceil(k/256) + 8) plus alignment must fit
  * 8 MiB (larger calls fail with a message; four rows or fewer need no staging).
  * Every call on one GPU shares that array: calls overlapping on one GPU race
- * and must be serialized by the caller.  Same outputs as
- * loom_amd_dense_forward, without taps. */
+ * and must be serialized by the caller.  Like every direct loom_amd_* call,
+ * it also shares the GPU's split-K partial sums and arrival counters with
+ * the other entry points and with plugin infers on that GPU (which hold a
+ * per-device lock the direct calls do not take): a direct call must not
+ * overlap a plugin infer or another direct call on the same GPU.  Same
+ * outputs as loom_amd_dense_forward, without taps. */
 int loom_amd_dense_forward_noalloc(const loom_amd_matrix* w, const float* x, int m,
                                    int activation, float* pre, float* post,
                                    const float* residual, void* stream);

@@ -105,6 +105,7 @@ SIGNATURES = {
     "loom_amd_norm_quant_rows": (i32, [P, i32, i32, P, f64, i32, P, i32, P, P, P]),
     "loom_amd_ordered_sum_rows": (i32, [P, i32, i32, f64, P, i32, P]),
     "loom_amd_exp_rows": (i32, [P, C.c_long, P, P]),
+    "loom_amd_reload_tuning": (i32, []),
     "loom_amd_dense_forward": (i32, [P, P, i32, i32, P, P, P, C.POINTER(DenseTaps), P]),
     "loom_amd_dense_forward_noalloc": (i32, [P, P, i32, i32, P, P, P, P]),
     "loom_amd_swiglu_forward": (i32, [P, P, P, P, P, f64, i32, i32, P, i32, P, P, P,

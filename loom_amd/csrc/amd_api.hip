@@ -8,6 +8,8 @@
 #include <math.h>
 
 #include <algorithm>
+#include <atomic>
+#include <memory>
 #include <mutex>
 #include <thread>
 #include <string>
@@ -186,6 +188,58 @@ int create_matrix_ms_offline(int device, const uint8_t* packed, int rows, int co
     }
     *out = w;
     return 0;
+}
+
+namespace {
+
+const char* const kTuneNames[] = {
+    "LOOM_AMD_GEMM_TILE",   "LOOM_AMD_GEMM_SPLIT",   "LOOM_AMD_GEMM_GROUP",   "LOOM_AMD_SMALLM",
+    "LOOM_AMD_SKINNY_NT",   "LOOM_AMD_SKINNY_NTR",   "LOOM_AMD_FUSED_NTR",    "LOOM_AMD_FUSED_WAVES",
+    "LOOM_AMD_GEMV_STREAM", "LOOM_AMD_STREAM_WAVES", "LOOM_AMD_STREAM_DEPTH", "LOOM_AMD_ATTN_QT",
+    "LOOM_AMD_UNFUSED_ROPE", "LOOM_AMD_UNFUSED_NORM"};
+constexpr int kTuneCount = (int)(sizeof(kTuneNames) / sizeof(kTuneNames[0]));
+
+struct TuneSnapshot {
+    bool set[kTuneCount];
+    int value[kTuneCount];
+};
+
+std::mutex g_tune_mu;
+std::atomic<const TuneSnapshot*> g_tune{nullptr};
+std::vector<std::unique_ptr<TuneSnapshot>> g_tune_all;  // every snapshot lives until exit
+
+const TuneSnapshot* read_tuning_locked() {
+    auto t = std::make_unique<TuneSnapshot>();
+    for (int i = 0; i < kTuneCount; ++i) {
+        const char* v = getenv(kTuneNames[i]);
+        t->set[i] = v && *v;
+        t->value[i] = t->set[i] ? atoi(v) : 0;
+    }
+    g_tune_all.push_back(std::move(t));
+    return g_tune_all.back().get();
+}
+
+}  // namespace
+
+int tune_int(const char* name, int dflt) {
+    const TuneSnapshot* t = g_tune.load(std::memory_order_acquire);
+    if (!t) {
+        std::lock_guard<std::mutex> lock(g_tune_mu);
+        t = g_tune.load(std::memory_order_acquire);
+        if (!t) {
+            t = read_tuning_locked();
+            g_tune.store(t, std::memory_order_release);
+        }
+    }
+    for (int i = 0; i < kTuneCount; ++i) {
+        if (strcmp(name, kTuneNames[i]) == 0) return t->set[i] ? t->value[i] : dflt;
+    }
+    return dflt;
+}
+
+void reload_tuning() {
+    std::lock_guard<std::mutex> lock(g_tune_mu);
+    g_tune.store(read_tuning_locked(), std::memory_order_release);
 }
 
 }  // namespace lamd
@@ -412,6 +466,11 @@ int loom_amd_ordered_sum_rows(const double* terms, int m, int n, double s0, doub
     if (threads != 64 && threads != 256 && threads != 512) return fail("threads must be 64, 256 or 512");
     hipError_t e = launch_ordered_sum_rows(terms, m, n, s0, out, threads, (hipStream_t)stream);
     return e == hipSuccess ? 0 : fail_hip("ordered_sum_rows", e);
+}
+
+int loom_amd_reload_tuning(void) {
+    reload_tuning();
+    return 0;
 }
 
 int loom_amd_exp_rows(const double* x, long n, double* y, void* stream) {

@@ -2100,8 +2100,7 @@ size_t attention_lds_bytes(int hd, int span) {
 }
 
 int attention_fast_two_pass_qt() {
-    const char* v = getenv("LOOM_AMD_ATTN_QT");
-    const int qt = v ? atoi(v) : 0;
+    const int qt = tune_int("LOOM_AMD_ATTN_QT", 0);
     return qt == 2 || qt == 4 ? qt : 0;
 }
 

@@ -193,11 +193,9 @@ static int build_block(int device, const loom_amd_block_desc* d, const loom_amd_
     B->attn_qt = attention_fast_two_pass_qt();
     // LOOM_AMD_UNFUSED_ROPE=1 keeps the separate Q/K/V epilogue launch in
     // decode (the tests compare both paths)
-    const char* unfused = getenv("LOOM_AMD_UNFUSED_ROPE");
-    B->fuse_rope = !(unfused && unfused[0] == '1');
+    B->fuse_rope = tune_int("LOOM_AMD_UNFUSED_ROPE", 0) != 1;
     // LOOM_AMD_UNFUSED_NORM=1 keeps the separate norm launches in decode
-    const char* unfused_norm = getenv("LOOM_AMD_UNFUSED_NORM");
-    B->fuse_norm = !(unfused_norm && unfused_norm[0] == '1');
+    B->fuse_norm = tune_int("LOOM_AMD_UNFUSED_NORM", 0) != 1;
     const int H = B->hidden;
     if (expect_shape(w->q, "q", B->q_dim, H, device) || expect_shape(w->k, "k", B->kv_dim, H, device) ||
         expect_shape(w->v, "v", B->kv_dim, H, device) || expect_shape(w->o, "o", H, B->q_dim, device) ||

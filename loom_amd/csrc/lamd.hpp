@@ -160,4 +160,13 @@ const char* kernel_variant(int m);  // name of the matmul path chosen for M rows
 // matrix is created there, never by a matmul call).
 hipError_t gemm_prepare(int device);
 
+// Tuning overrides (the LOOM_AMD_* variables of the library's tuning table):
+// read from the environment once, when the library first needs one, and
+// again by loom_amd_reload_tuning(); never per launch (getenv costs host time
+// on microsecond launches and is unsafe against setenv on other threads).
+// tune_int returns the variable's integer value when it is set and not
+// empty, else dflt.
+int tune_int(const char* name, int dflt);
+void reload_tuning();
+
 }  // namespace lamd

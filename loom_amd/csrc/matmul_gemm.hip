@@ -706,11 +706,6 @@ constexpr int kSplitTarget = 240;
 constexpr int kMinSplitKtiles = 6;
 constexpr int kMaxSplit = 4;
 
-static int env_int(const char* name, int dflt) {
-    const char* v = getenv(name);
-    return v && *v ? atoi(v) : dflt;
-}
-
 struct GemmPlan {
     int mi, ksplit, sps;
 };
@@ -719,8 +714,8 @@ static GemmPlan plan_gemm(int m, int ntiles, int ktiles, int nmat, int device) {
     const int ngroups = ceil_div(ntiles, 16 / nmat);
     // LOOM_AMD_GEMM_TILE=128|64 and LOOM_AMD_GEMM_SPLIT=n override the choice
     // (tuning and tests)
-    const int force_tile = env_int("LOOM_AMD_GEMM_TILE", 0);
-    const int force_split = env_int("LOOM_AMD_GEMM_SPLIT", 0);
+    const int force_tile = tune_int("LOOM_AMD_GEMM_TILE", 0);
+    const int force_split = tune_int("LOOM_AMD_GEMM_SPLIT", 0);
     if (force_tile == 128) return GemmPlan{4, 1, ktiles};
     // large grids take 128-token tiles (never split)
     if (force_tile != 64 && force_split == 0 && ceil_div(m, 128) * ngroups >= kTile128MinTiles)
@@ -750,7 +745,7 @@ static hipError_t launch_gemm_tile(const MatArgs& p, const GemmPlan& pl, int dev
     gg.ngroups = ceil_div(p.ntiles, 16 / NMAT);
     gg.ksplit = pl.ksplit;
     gg.sps = pl.sps;
-    gg.group = env_int("LOOM_AMD_GEMM_GROUP", 8);
+    gg.group = tune_int("LOOM_AMD_GEMM_GROUP", 8);
     const SplitWs ws = pl.ksplit > 1 ? split_ws(device) : SplitWs{};
     gg.part = ws.part;
     gg.ctr = ws.ctr;

@@ -924,8 +924,7 @@ static void launch_fused_w(const MatArgs& p, size_t shm, hipStream_t s) {
     // 1, 2 or 4 overrides (tests and tuning; four tiles only with two float4
     // slots a thread).
     if constexpr (NMAT == 1 && WAVES <= 8) {
-        const char* env = getenv("LOOM_AMD_FUSED_NTR");
-        const int ntr = env && *env ? atoi(env) : 2;
+        const int ntr = tune_int("LOOM_AMD_FUSED_NTR", 2);
         if (p.e.m == 1 && groups <= (size_t)2 * WAVES * 64 && ntr == 2) {
             hipLaunchKernelGGL((skinny_kernel<NMAT, 1, WAVES, true, NORM_NONE, 0, 2, 1, 2>),
                                dim3(ceil_div(p.ntiles, 2)), block, shm, s, p);
@@ -969,9 +968,8 @@ static hipError_t launch_skinny(const MatArgs& p, hipStream_t s) {
         if (w == 8 && p.e.m == 1 && (size_t)p.k / 4 <= (size_t)4 * 4 * 64) w = 4;
     }
     if constexpr (FUSEQ) {
-        const char* fw = getenv("LOOM_AMD_FUSED_WAVES");  // tuning override (1..16)
-        if (fw && *fw) {
-            const int v = atoi(fw);
+        const int v = tune_int("LOOM_AMD_FUSED_WAVES", 0);  // tuning override (1..16)
+        if (v != 0) {
             if (v == 1 || v == 2 || v == 4 || v == 8 || (v == 16 && kCap == 16)) w = v;
             while (w < kCap && (size_t)p.e.m * p.k > (size_t)4 * kFusedVec * 64 * w) w <<= 1;
         }
@@ -992,8 +990,7 @@ static hipError_t launch_skinny(const MatArgs& p, hipStream_t s) {
         // per workgroup share the rows' loads (BitNet-2B up shape: M = 1
         // 4.10 -> 3.91 us, M = 8 4.77 -> 4.43, M = 16 5.59 -> 4.89).
         // LOOM_AMD_SKINNY_NTR = 1 takes one tile (tests and tuning).
-        const char* env = getenv("LOOM_AMD_SKINNY_NTR");
-        if (w == 8 && !(env && atoi(env) == 1)) {
+        if (w == 8 && tune_int("LOOM_AMD_SKINNY_NTR", 0) != 1) {
             hipLaunchKernelGGL((skinny_kernel<NMAT, MSUB, 8, FUSEQ, NORM_NONE, 0, kFusedVec, kFusedMaxRows, 2>),
                                dim3(ceil_div(p.ntiles, 2)), dim3(512), shm, s, p);
             return hipGetLastError();
@@ -1027,8 +1024,7 @@ static hipError_t launch_skinny(const MatArgs& p, hipStream_t s) {
 // halved workgroup count lengthens each wave's serial K loop and one tile is
 // faster.  LOOM_AMD_SKINNY_NT = 1, 2 or 4 overrides (1 = skinny_kernel).
 static int skinny_nt(int ntiles, int ktiles) {
-    const char* v = getenv("LOOM_AMD_SKINNY_NT");
-    const int nt = v && *v ? atoi(v) : 0;
+    const int nt = tune_int("LOOM_AMD_SKINNY_NT", 0);
     if (nt == 1 || nt == 2 || nt == 4) return nt;
     return ktiles <= 16 && ntiles >= 256 ? 2 : 1;
 }
@@ -1049,11 +1045,6 @@ static hipError_t launch_skinny_nt(const MatArgs& p, hipStream_t s) {
     return hipGetLastError();
 }
 
-static int env_int(const char* name, int dflt) {
-    const char* v = getenv(name);
-    return v && *v ? atoi(v) : dflt;
-}
-
 // small_split_kernel for one matrix when its workspace holds the row groups.
 // Its K-slice exchange costs a few microseconds (three device-scope round
 // trips), so it pays only where full-K workgroups pull the most activation
@@ -1062,7 +1053,7 @@ static int env_int(const char* name, int dflt) {
 // at every M).  LOOM_AMD_SMALLM = 1 always takes it, 0 never.
 template <int MSUB>
 static bool launch_small_split(const MatArgs& p, int device, hipStream_t s, hipError_t* e) {
-    const int mode = env_int("LOOM_AMD_SMALLM", -1);
+    const int mode = tune_int("LOOM_AMD_SMALLM", -1);
     if (mode == 0 || (mode != 1 && (p.ktiles <= 16 || p.e.m <= 24))) return false;
     const int groups = ceil_div(p.ntiles, kSmallNT);
     const int S = ceil_div(p.ktiles, kSmallKps);

@@ -282,8 +282,7 @@ bool stream_ok(int m, int k, int n_tiles, bool fused, const Epilogue& epi) {
     const bool plain = epi.kind == EPI_DENSE && !epi.bias0 && !epi.residual && !epi.post && !epi.acc0;
     const bool acc_only = epi.kind == EPI_ACC && epi.acc0;
     if (!plain && !acc_only) return false;
-    const char* v = getenv("LOOM_AMD_GEMV_STREAM");
-    const int force = v && *v ? atoi(v) : -1;
+    const int force = tune_int("LOOM_AMD_GEMV_STREAM", -1);
     if (m < 1 || m > kStreamMaxRows || k % 4 != 0) return false;
     if (ceil_div(k, kTileCols) * 2 < kStreamDepth) return false;  // <= 2 row tiles end per group
     if ((size_t)m * pad_cols(k) > (fused ? (size_t)60 * 1024 - 256 : (size_t)16 * 1024)) return false;
@@ -295,14 +294,9 @@ bool stream_ok(int m, int k, int n_tiles, bool fused, const Epilogue& epi) {
 
 // Tuning overrides: LOOM_AMD_STREAM_WAVES (waves in the grid) and
 // LOOM_AMD_STREAM_DEPTH (K tiles in flight per wave: 8, 12 or 16).
-static int env_int(const char* name, int dflt) {
-    const char* v = getenv(name);
-    return v && *v ? atoi(v) : dflt;
-}
-
 template <bool FUSEQ, int FV, int QV>
 static void launch_stream_t(const MatArgs& p, int grid, size_t shm, hipStream_t s) {
-    const int depth = env_int("LOOM_AMD_STREAM_DEPTH", kStreamDepth);
+    const int depth = tune_int("LOOM_AMD_STREAM_DEPTH", kStreamDepth);
     const dim3 g(grid), b(kStreamWaves * 64);
     if (depth == 8 && p.ktiles * 2 >= 8) {
         hipLaunchKernelGGL((stream_kernel<8, FUSEQ, FV, QV>), g, b, shm, s, p);
@@ -314,7 +308,7 @@ static void launch_stream_t(const MatArgs& p, int grid, size_t shm, hipStream_t 
 }
 
 hipError_t launch_stream(const MatArgs& p, bool fuseq, hipStream_t s) {
-    const int gw = env_int("LOOM_AMD_STREAM_WAVES", kStreamGridWaves);
+    const int gw = tune_int("LOOM_AMD_STREAM_WAVES", kStreamGridWaves);
     const int cap = gw >= kStreamWaves ? gw : kStreamGridWaves;
     const int waves = p.ntiles < cap ? p.ntiles : cap;
     const int grid = (waves + kStreamWaves - 1) / kStreamWaves;

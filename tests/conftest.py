@@ -26,3 +26,34 @@ def amd_lib():
     if not os.path.exists(_lib.LIB_PATH):
         build.build()
     return _lib.lib()
+
+
+@pytest.fixture
+def tuning():
+    """Sets LOOM_AMD_* tuning variables for one test: tuning(name, value)
+    (value None unsets).  The library reads them once and again on
+    loom_amd_reload_tuning(), which this fixture calls after every change and
+    after restoring the variables at the end of the test."""
+    saved = {}
+
+    def reload():
+        from loom_amd import _lib
+        _lib.lib().loom_amd_reload_tuning()
+
+    def set_(name, value):
+        if name not in saved:
+            saved[name] = os.environ.get(name)
+        if value is None:
+            os.environ.pop(name, None)
+        else:
+            os.environ[name] = str(value)
+        reload()
+
+    yield set_
+    for name, old in saved.items():
+        if old is None:
+            os.environ.pop(name, None)
+        else:
+            os.environ[name] = old
+    if saved:
+        reload()

@@ -206,7 +206,7 @@ def test_block_refuses_decode_batch_other_than_warm_cache(orc, torch_dev, tf):
 
 
 @pytest.mark.parametrize("hd,seq", [(128, 300), (64, 200)])
-def test_fast_prefill_attention_kernels_agree(orc, torch_dev, tf, monkeypatch, hd, seq):
+def test_fast_prefill_attention_kernels_agree(orc, torch_dev, tf, tuning, hd, seq):
     # the two-pass fast prefill kernel with 32 or 64 queries per workgroup
     # sums in the same order: identical bytes for the block output and its K/V
     # caches, ragged last query tile included.  The default one-pass kernel
@@ -219,7 +219,7 @@ def test_fast_prefill_attention_kernels_agree(orc, torch_dev, tf, monkeypatch, h
     x = orc.normal_f32(seq * sh.hidden, seed=452).reshape(seq, sh.hidden)
     outs, attn, kv = [], [], []
     for qt in ("2", "4", ""):
-        monkeypatch.setenv("LOOM_AMD_ATTN_QT", qt)
+        tuning("LOOM_AMD_ATTN_QT", qt)
         blk = tf.BitNetBlock(w.cfg(tf, norm="fast"), w.gpu(tf))
         xd = to_dev(torch, x)
         _, T = blk.forward(xd, taps=True)
@@ -460,7 +460,7 @@ def test_block_stages_qk_norm_head_dims(orc, torch_dev, tf):
 
 @pytest.mark.parametrize("shape,norm", [("small", "fast"), ("bitnet2b", "fast"),
                                         ("small", "strict"), ("bitnet2b", "strict")])
-def test_decode_qk_norm_fused_equals_separate(orc, torch_dev, tf, shape, norm, monkeypatch):
+def test_decode_qk_norm_fused_equals_separate(orc, torch_dev, tf, shape, norm, tuning):
     # the norms inside the fused decode attention equal qkv_rope_kernel's
     # (LOOM_AMD_UNFUSED_ROPE=1), outputs and caches bit for bit, batch 2
     torch = torch_dev
@@ -468,9 +468,9 @@ def test_decode_qk_norm_fused_equals_separate(orc, torch_dev, tf, shape, norm, m
     w = Weights(orc, sh, seed=1261, bias=True, qk="per_head")
     gw = w.gpu(tf)
     fused = tf.BitNetBlock(w.cfg(tf, norm, max_batch=2), gw)
-    monkeypatch.setenv("LOOM_AMD_UNFUSED_ROPE", "1")
+    tuning("LOOM_AMD_UNFUSED_ROPE", "1")
     plain = tf.BitNetBlock(w.cfg(tf, norm, max_batch=2), gw)
-    monkeypatch.delenv("LOOM_AMD_UNFUSED_ROPE")
+    tuning("LOOM_AMD_UNFUSED_ROPE", None)
     for i, seq in enumerate([min(62, sh.msl - 8), 1, 1, 1]):
         x_in = orc.normal_f32(2 * seq * sh.hidden, 1500 + i).reshape(2, seq, sh.hidden)
         a = to_dev(torch, x_in.reshape(2 * seq, sh.hidden)).reshape(2, seq, sh.hidden)
@@ -489,7 +489,7 @@ def test_decode_qk_norm_fused_equals_separate(orc, torch_dev, tf, shape, norm, m
 @pytest.mark.parametrize("shape,norm", [("small", "fast"), ("bitnet2b", "fast"),
                                         ("small", "strict"), ("bitnet2b", "strict"),
                                         ("mha32", "strict")])
-def test_decode_rope_fused_attention(orc, torch_dev, tf, shape, norm, monkeypatch):
+def test_decode_rope_fused_attention(orc, torch_dev, tf, shape, norm, tuning):
     # Single-token decode runs the Q/K/V epilogue (RoPE, K/V cache write)
     # inside the attention launch (fast: the GQA chunk kernel; strict: the
     # scores kernel); with LOOM_AMD_UNFUSED_ROPE=1 a block keeps the separate
@@ -500,9 +500,9 @@ def test_decode_rope_fused_attention(orc, torch_dev, tf, shape, norm, monkeypatc
     w = Weights(orc, sh, seed=1251, bias=True)
     gw = w.gpu(tf)
     fused = tf.BitNetBlock(w.cfg(tf, norm, max_batch=2), gw)
-    monkeypatch.setenv("LOOM_AMD_UNFUSED_ROPE", "1")
+    tuning("LOOM_AMD_UNFUSED_ROPE", "1")
     plain = tf.BitNetBlock(w.cfg(tf, norm, max_batch=2), gw)
-    monkeypatch.delenv("LOOM_AMD_UNFUSED_ROPE")
+    tuning("LOOM_AMD_UNFUSED_ROPE", None)
     for i, seq in enumerate([min(62, sh.msl - 8), 1, 1, 1, 1]):
         x_in = orc.normal_f32(2 * seq * sh.hidden, 1400 + i).reshape(2, seq, sh.hidden)
         a = to_dev(torch, x_in.reshape(2 * seq, sh.hidden)).reshape(2, seq, sh.hidden)
@@ -520,7 +520,7 @@ def test_decode_rope_fused_attention(orc, torch_dev, tf, shape, norm, monkeypatc
 
 @pytest.mark.parametrize("shape,norm", [("small", "strict"), ("small", "fast"),
                                         ("bitnet2b", "strict"), ("bitnet2b", "fast")])
-def test_block_decode_norm_fused_and_staged(orc, torch_dev, tf, shape, norm, monkeypatch):
+def test_block_decode_norm_fused_and_staged(orc, torch_dev, tf, shape, norm, tuning):
     # A decode row is normalized inside each matmul that consumes it (RMSNorm1
     # -> QKV, attention inner norm -> O, RMSNorm2 -> gate/up, FFN inner norm
     # -> down); LOOM_AMD_UNFUSED_NORM=1 keeps the separate norm launches.  Both
@@ -532,9 +532,9 @@ def test_block_decode_norm_fused_and_staged(orc, torch_dev, tf, shape, norm, mon
     w = Weights(orc, sh, seed=1201, act=ACT_SILU)
     gw = w.gpu(tf)
     fused = tf.BitNetBlock(w.cfg(tf, norm), gw)
-    monkeypatch.setenv("LOOM_AMD_UNFUSED_NORM", "1")
+    tuning("LOOM_AMD_UNFUSED_NORM", "1")
     staged = tf.BitNetBlock(w.cfg(tf, norm), gw)
-    monkeypatch.delenv("LOOM_AMD_UNFUSED_NORM")
+    tuning("LOOM_AMD_UNFUSED_NORM", None)
     refs = {"fused": w.oracle_mha(orc), "staged": w.oracle_mha(orc)}
     base = 0
     for i, seq in enumerate([6, 1, 1, 1]):

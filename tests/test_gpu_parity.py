@@ -529,7 +529,7 @@ def test_plugin_bitnet_swiglu_biases(orc, torch_dev, with_norm):
 @pytest.mark.parametrize("force", ["1", ""])
 @pytest.mark.parametrize("n,k", [(6912, 2560), (2560, 6912), (6900, 2570), (1000, 1792),
                                  (70000, 2560)])
-def test_stream_gemv_matches_oracle(orc, torch_dev, bn, monkeypatch, force, n, k):
+def test_stream_gemv_matches_oracle(orc, torch_dev, bn, tuning, force, n, k):
     # The streaming GEMV (fixed grid of waves, each walking its 16-row tiles'
     # K tiles through a ring of in-flight loads): forced on every shape
     # (LOOM_AMD_GEMV_STREAM=1) and by default (large N only).  Fused
@@ -537,7 +537,7 @@ def test_stream_gemv_matches_oracle(orc, torch_dev, bn, monkeypatch, force, n, k
     # amax and fp32 outputs bit-exact against the oracle.
     torch = torch_dev
     if force:
-        monkeypatch.setenv("LOOM_AMD_GEMV_STREAM", force)
+        tuning("LOOM_AMD_GEMV_STREAM", force)
     m = orc.random_matrix(n, k, seed=n + 3 * k)
     w = gpu_matrix(bn, m)
     for M in (1, 2, 3, 4):
@@ -669,7 +669,7 @@ def test_library_errors_are_loud(orc, torch_dev, bn):
 
 
 @pytest.mark.parametrize("path", ["skinny", "stream"])
-def test_fused_quant_near_ties(orc, torch_dev, bn, monkeypatch, path):
+def test_fused_quant_near_ties(orc, torch_dev, bn, tuning, path):
     # The quantizers decide in fp32 when the fp32 product lies farther than
     # 3.1e-5 from a rounding boundary k + 1/2 (it is within 1.52e-5 of loom's
     # fp64 product) and take loom's fp64 path otherwise: rows built on exact
@@ -678,7 +678,7 @@ def test_fused_quant_near_ties(orc, torch_dev, bn, monkeypatch, path):
     # (skinny or streaming kernel) and the stand-alone quantization kernel.
     torch = torch_dev
     if path == "stream":
-        monkeypatch.setenv("LOOM_AMD_GEMV_STREAM", "1")
+        tuning("LOOM_AMD_GEMV_STREAM", "1")
     rng = np.random.default_rng(7)
     K = 4096
     m = orc.random_matrix(32, K, seed=71)
@@ -748,21 +748,21 @@ def test_gemm_split_k(orc, torch_dev, bn, shape, M):
 
 @pytest.mark.parametrize("tile,split", [("64", "1"), ("64", "2"), ("64", "3"), ("64", "27"),
                                         ("128", "0")])
-def test_gemm_forced_plans(orc, torch_dev, bn, monkeypatch, tile, split):
+def test_gemm_forced_plans(orc, torch_dev, bn, tuning, tile, split):
     # every tile height and split width, including one K tile per workgroup
     # (27 ranges of the down shape), against the oracle
-    monkeypatch.setenv("LOOM_AMD_GEMM_TILE", tile)
-    monkeypatch.setenv("LOOM_AMD_GEMM_SPLIT", split)
+    tuning("LOOM_AMD_GEMM_TILE", tile)
+    tuning("LOOM_AMD_GEMM_SPLIT", split)
     m = orc.random_matrix(2560, 6912, seed=3)
     x = orc.normal_f32(70 * 6912, seed=4).reshape(70, 6912)
     _check_dense(orc, torch_dev, bn, m, x)
 
 
 @pytest.mark.parametrize("group", ["0", "3", "8"])
-def test_gemm_tile_order_groups(orc, torch_dev, bn, monkeypatch, group):
+def test_gemm_tile_order_groups(orc, torch_dev, bn, tuning, group):
     # the GEMM's tile order: weight-row group fastest (0), or groups of 3
     # token tiles (the last group partial: 5 token tiles) or 8
-    monkeypatch.setenv("LOOM_AMD_GEMM_GROUP", group)
+    tuning("LOOM_AMD_GEMM_GROUP", group)
     m = orc.random_matrix(6900, 2560, seed=61)
     x = orc.normal_f32(300 * 2560, seed=62).reshape(300, 2560)
     _check_dense(orc, torch_dev, bn, m, x)
@@ -770,13 +770,13 @@ def test_gemm_tile_order_groups(orc, torch_dev, bn, monkeypatch, group):
 
 @pytest.mark.parametrize("ntr", ["1", "2", "4"])
 @pytest.mark.parametrize("rows,cols", [(6912, 2560), (2560, 6912), (1000, 2560), (40, 1000), (33, 260)])
-def test_fused_row_tiles_per_workgroup(orc, torch_dev, bn, monkeypatch, ntr, rows, cols):
+def test_fused_row_tiles_per_workgroup(orc, torch_dev, bn, tuning, ntr, rows, cols):
     # M = 1 with the quantization fused: one, two or four 16-row weight tiles
     # per workgroup (ragged last groups: 63 and 3 tiles, a partial last tile
     # of 33 rows), plain and with residual + ReLU: bit-exact
-    monkeypatch.setenv("LOOM_AMD_FUSED_NTR", ntr)
+    tuning("LOOM_AMD_FUSED_NTR", ntr)
     if ntr == "4":
-        monkeypatch.setenv("LOOM_AMD_FUSED_WAVES", "8")  # four tiles: eight-wave workgroups
+        tuning("LOOM_AMD_FUSED_WAVES", "8")  # four tiles: eight-wave workgroups
     m = orc.random_matrix(rows, cols, seed=rows + cols)
     x = orc.normal_f32(cols, seed=cols + 1).reshape(1, cols)
     res = orc.normal_f32(rows, seed=rows + 2).reshape(1, rows)
@@ -786,12 +786,12 @@ def test_fused_row_tiles_per_workgroup(orc, torch_dev, bn, monkeypatch, ntr, row
 
 @pytest.mark.parametrize("ntr", ["1", "2"])
 @pytest.mark.parametrize("rows,cols,M", [(6912, 2560, 5), (6912, 2560, 16), (1000, 2560, 8), (40, 1000, 13)])
-def test_prequantized_row_tiles_per_workgroup(orc, torch_dev, bn, monkeypatch, ntr, rows, cols, M):
+def test_prequantized_row_tiles_per_workgroup(orc, torch_dev, bn, tuning, ntr, rows, cols, M):
     # 4 < M <= 16 (quantized by its own kernel, then the skinny GEMV on the
     # int8 rows, read branch-free: rows past M fall past the buffer's end):
     # one or two 16-row weight tiles per workgroup (ragged last groups of 63
     # and 3 tiles), plain and with residual + ReLU: bit-exact
-    monkeypatch.setenv("LOOM_AMD_SKINNY_NTR", ntr)
+    tuning("LOOM_AMD_SKINNY_NTR", ntr)
     m = orc.random_matrix(rows, cols, seed=rows + M)
     x = orc.normal_f32(M * cols, seed=M + 3).reshape(M, cols)
     res = orc.normal_f32(M * rows, seed=M + 4).reshape(M, rows)
@@ -802,26 +802,26 @@ def test_prequantized_row_tiles_per_workgroup(orc, torch_dev, bn, monkeypatch, n
 @pytest.mark.parametrize("nt", ["split", "1", "2", "4"])
 @pytest.mark.parametrize("rows,cols,M", [(6912, 2560, 64), (2560, 6912, 40), (1000, 2570, 17),
                                          (6900, 2560, 33), (40000, 512, 20)])
-def test_small_m_tiles_per_workgroup(orc, torch_dev, bn, monkeypatch, nt, rows, cols, M):
+def test_small_m_tiles_per_workgroup(orc, torch_dev, bn, tuning, nt, rows, cols, M):
     # 16 < M <= 64: the K-split kernel (default; 40000 rows exceed its
     # workspace and take the single-workgroup kernels), and the skinny kernels
     # with one, two or four 16-row tiles per workgroup (ragged last group and
     # K slice included): int32 accumulators and fp32 outputs bit-exact
     if nt == "split":
-        monkeypatch.setenv("LOOM_AMD_SMALLM", "1")
+        tuning("LOOM_AMD_SMALLM", "1")
     else:
-        monkeypatch.setenv("LOOM_AMD_SMALLM", "0")
-        monkeypatch.setenv("LOOM_AMD_SKINNY_NT", nt)
+        tuning("LOOM_AMD_SMALLM", "0")
+        tuning("LOOM_AMD_SKINNY_NT", nt)
     m = orc.random_matrix(rows, cols, seed=rows + M)
     x = orc.normal_f32(M * cols, seed=M + 7).reshape(M, cols)
     _check_dense(orc, torch_dev, bn, m, x)
 
 
-def test_small_m_split_repeatable(orc, torch_dev, bn, monkeypatch):
+def test_small_m_split_repeatable(orc, torch_dev, bn, tuning):
     # the K-split kernel leaves its accumulators and arrival counters at zero:
     # back-to-back launches of two shapes (different row groups and slices),
     # residual epilogue included, all give the oracle's bytes
-    monkeypatch.setenv("LOOM_AMD_SMALLM", "1")
+    tuning("LOOM_AMD_SMALLM", "1")
     torch = torch_dev
     cases = []
     for rows, cols, M in ((2560, 6912, 64), (6912, 2560, 29)):
@@ -840,9 +840,9 @@ def test_small_m_split_repeatable(orc, torch_dev, bn, monkeypatch):
 
 
 @pytest.mark.parametrize("nt", ["1", "2"])
-def test_small_m_swiglu_tiles_per_workgroup(orc, torch_dev, bn, monkeypatch, nt):
+def test_small_m_swiglu_tiles_per_workgroup(orc, torch_dev, bn, tuning, nt):
     # gate|up with M = 48 and one or two tiles per workgroup
-    monkeypatch.setenv("LOOM_AMD_SKINNY_NT", nt)
+    tuning("LOOM_AMD_SKINNY_NT", nt)
     _swiglu_case(orc, torch_dev, bn, hidden=2560, inter=6912, M=48, seed=131, norm="strict",
                  with_norm_w=True)
 

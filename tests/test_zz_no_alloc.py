@@ -103,3 +103,55 @@ def test_noalloc_refuses_more_than_its_array(orc, torch_dev):
     ref = orc.dense_forward(m, xs[rows], simd=True)
     assert got.cpu().numpy()[rows].tobytes() == ref.pre.tobytes()
     w.release()
+
+
+def test_noalloc_allocates_nothing(orc, torch_dev):
+    # The promise itself: once its kernels are loaded, a call that stages
+    # quantized rows (300 rows: past the fused prologue's 4) leaves the
+    # device's free memory unchanged -- while a call through
+    # loom_amd_dense_forward at a size its arena has not seen grows the arena,
+    # which the same measurement sees -- and the call can be captured into a
+    # HIP graph (global capture mode refuses allocations) whose replays, with
+    # eager work and synchronizations between them, equal eager calls.
+    from loom_amd import _lib, bitnet as bn
+    torch = torch_dev
+    n, k, M = 2560, 6912, 300
+    m = orc.random_matrix(n, k, seed=21)
+    w = bn.TernaryMatrix.from_words(m.words, n, k, m.scale)
+    xs = [torch.from_numpy(orc.normal_f32(M * k, seed=22 + i).reshape(M, k)).cuda() for i in range(4)]
+    got, _ = _noalloc(torch, w, xs[0])                 # loads the kernels, looks up the array
+    want, _ = bn.dense_forward_packed_ternary(w, xs[0])
+    torch.cuda.synchronize()
+    assert got.cpu().numpy().tobytes() == want.cpu().numpy().tobytes()
+    free0 = torch.cuda.mem_get_info()[0]
+    for x in xs[1:]:
+        _noalloc(torch, w, x)
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0, "the no-allocation entry point allocated"
+    # more rows than any other test stages through the arena (config 4's
+    # 16384), so the arena grows whatever ran before in this process
+    big = torch.zeros((24576, k), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    free1 = torch.cuda.mem_get_info()[0]
+    bn.dense_forward_packed_ternary(w, big)
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] < free1, "the measurement does not see the arena grow"
+    # graph capture of the call on fixed buffers, replayed on new inputs
+    x_in = xs[0].clone()
+    pre = torch.empty((M, n), dtype=torch.float32, device="cuda")
+    lib = _lib.lib()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        s = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+        rc = lib.loom_amd_dense_forward_noalloc(w.handle, C.c_void_p(x_in.data_ptr()), M, -1,
+                                                C.c_void_p(pre.data_ptr()), None, None, s)
+    assert rc == 0, lib.loom_amd_last_error()
+    for i, x in enumerate(xs[1:] + xs[:1]):
+        x_in.copy_(x)
+        eager, _ = bn.dense_forward_packed_ternary(w, x)  # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert pre.cpu().numpy().tobytes() == eager.cpu().numpy().tobytes(), f"replay {i}"
+    del g
+    w.release()
