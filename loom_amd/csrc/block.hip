@@ -642,32 +642,42 @@ __global__ __launch_bounds__(256) void attention_kernel(const double* __restrict
 }
 
 // ---- prefill path: query tiles -------------------------------------------
-// One workgroup per (head, tile of kTileQ consecutive queries, sequence).  K
-// and V chunks of kChunkP positions are staged through LDS (the next chunk is
-// prefetched into registers while the current one is used), so each cached
-// row is read once per tile instead of once per query.  Pass 1 forms every
-// score of the tile (each lane a 2 x 2 block of d-order chains), keeps each
-// query's maximum and stores the scores in `sc` (rows x heads x span);
-// pass 2 reads them back, takes p = exp(score - max), adds expSum on one lane
-// per query and sum(p * v) on one lane per (query, d), all in position order.
-// Every sum therefore has the reference's order and, with FMA false, the
-// reference's roundings: exact.  FMA true (fast mode) contracts each
-// multiply-add of the dot and value chains into one rounding.  Positions past
-// a query's own position are skipped (never added).
+// Strict prefill attention.  One workgroup per (head, tile of kTileQ
+// consecutive queries, sequence).  K and V chunks of kChunkP positions are
+// staged through LDS in fp64 (converted once as they are staged; the next
+// chunk is prefetched into registers while the current one is used), so each
+// cached row is read once per tile instead of once per query.  Pass 1 forms
+// every score of the tile, each lane a 2 x 2 block of d-order chains (two
+// queries x two positions; K rows at an odd pitch, so the 16 positions a
+// wave reads at one d fall in distinct banks).  It keeps each query's maximum
+// and stores the scores in `sc` (rows x heads x span).  Pass 2 reads them
+// back, takes p = exp(score - max), adds expSum on one lane per query and
+// sum(p * v) on one lane per (query, column pair or pairs: d = 2l, 2l+1 and
+// 64+2l, 64+2l+1, so a wave's 16-byte value reads are contiguous), all in
+// position order.  Every sum
+// therefore has the reference's order and roundings (a product, then a sum,
+// each rounded): exact.  Positions past a query's own position are skipped
+// (never added).
 constexpr int kTileQ = 32;
 constexpr int kAttnFastQt = 2;  // 16-query tiles per workgroup of the fast prefill kernel
 constexpr int kChunkP = 32;
 
 template <int HD>
 struct TileLds {
-    double q[kTileQ][HD];
-    float kv[kChunkP][HD + 1];  // K chunk (pass 1) or V chunk (pass 2); +1: conflict-free rows
-    double p[kTileQ][kChunkP];
-    double mx[kTileQ];
+    static constexpr int QP = HD + 2;  // q row pitch (doubles): the query pairs' rows in distinct banks
+    static constexpr int KP = HD + 1;  // K row pitch (doubles, odd): 16 rows at one d in distinct banks
+    double q[kTileQ * QP];
+    union {
+        double k[kChunkP * KP];        // pass 1: K chunk, position-major
+        double v[kChunkP * HD];        // pass 2: V chunk, position-major
+    };
+    // probabilities; odd row pitch: the expSum lanes (one query each) and the
+    // two query groups of a wave's value lanes read distinct banks
+    double p[kTileQ][kChunkP + 1];
     double es[kTileQ];
 };
 
-template <int HD, bool FMA>
+template <int HD>
 __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict__ q,
                                                         const float* __restrict__ cache_k,
                                                         const float* __restrict__ cache_v,
@@ -675,10 +685,13 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict
                                                         int span, int heads, int kv_heads, int seq,
                                                         double* __restrict__ sc_all,
                                                         double* __restrict__ out) {
+    using Lds = TileLds<HD>;
+    constexpr int QP = Lds::QP, KP = Lds::KP;
     constexpr int DB = HD / 32;                       // value columns per PV lane
     constexpr int F4 = kChunkP * HD / 4 / 256;        // float4 per thread per chunk
     static_assert(F4 >= 1 && kChunkP * HD == F4 * 4 * 256, "chunk geometry");
-    __shared__ TileLds<HD> sm;
+    static_assert(DB == 2 || DB == 4, "head_dim 64 or 128");
+    __shared__ __align__(16) Lds sm;
     const int tid = threadIdx.x;
     const int h = blockIdx.x;
     const int tile = gridDim.y - 1 - blockIdx.y;  // longest tiles first
@@ -699,29 +712,17 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict
     const float* vb = cache_v + (size_t)b * msl * kv_dim + (size_t)kvh * HD;
     for (int i = tid; i < kTileQ * HD; i += 256) {
         const int qi = i / HD;
-        sm.q[qi][i % HD] = qi < nq ? q[(row0 + qi) * q_dim + (size_t)h * HD + i % HD] : 0.0;
+        sm.q[qi * QP + i % HD] = qi < nq ? q[(row0 + qi) * q_dim + (size_t)h * HD + i % HD] : 0.0;
     }
-    // chunk loads: branch-free (rows clamped into the ring)
+    // chunk loads: branch-free (rows clamped into the ring); thread t takes
+    // float4 (t + 256 j): position e / HD, columns e % HD .. +3
     float4 rk[F4];
-    auto load = [&](const float* src, int c) {
-#pragma unroll
-        for (int j = 0; j < F4; ++j) {
-            const int e = (tid + j * 256) * 4;
-            const int k = min(c * kChunkP + e / HD, msl - 1);
-            rk[j] = *(const float4*)(src + (size_t)k * kv_dim + e % HD);
-        }
-    };
-    auto store = [&]() {
-#pragma unroll
-        for (int j = 0; j < F4; ++j) {
-            const int e = (tid + j * 256) * 4;
-            float* d = &sm.kv[e / HD][e % HD];
-            d[0] = rk[j].x;
-            d[1] = rk[j].y;
-            d[2] = rk[j].z;
-            d[3] = rk[j].w;
-        }
-    };
+#define LAMD_TILE_LOAD(SRC, C)                                                      \
+    _Pragma("unroll") for (int j = 0; j < F4; ++j) {                                \
+        const int e = (tid + j * 256) * 4;                                          \
+        const int k = min((C) * kChunkP + e / HD, msl - 1);                         \
+        rk[j] = *(const float4*)((SRC) + (size_t)k * kv_dim + e % HD);              \
+    }
     // score lanes: queries qa = 2*qp, qa+1 x chunk positions 2*pp, 2*pp+1;
     // their scores live at sca[k], sca[span + k] (rows qa, qa+1 of the tile)
     const int qp = tid >> 4, pp = tid & 15;
@@ -736,32 +737,37 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict
 
     // ---- pass 1: scores and maxima ---------------------------------------
     double m0 = -1e9, m1 = -1e9;
-    load(kb, 0);
+    LAMD_TILE_LOAD(kb, 0)
     for (int c = 0; c < nch; ++c) {
         __syncthreads();  // previous chunk fully read
-        store();
-        load(kb, c + 1);  // prefetch (clamped past the last chunk)
+#pragma unroll
+        for (int j = 0; j < F4; ++j) {  // K chunk: k[position][d]
+            const int e = (tid + j * 256) * 4;
+            double* d = &sm.k[(e / HD) * KP + e % HD];
+            d[0] = (double)rk[j].x;
+            d[1] = (double)rk[j].y;
+            d[2] = (double)rk[j].z;
+            d[3] = (double)rk[j].w;
+        }
+        LAMD_TILE_LOAD(kb, c + 1)  // prefetch (clamped past the last chunk)
         __syncthreads();
         double d00 = 0.0, d01 = 0.0, d10 = 0.0, d11 = 0.0;
-        const float* k0 = sm.kv[2 * pp];
-        const float* k1 = sm.kv[2 * pp + 1];
-        const double* q0 = sm.q[qa];
-        const double* q1 = sm.q[qa + 1];
+        const double* q0 = &sm.q[qa * QP];
+        const double* q1 = q0 + QP;
+        const double* k0 = &sm.k[(2 * pp) * KP];
+        const double* k1 = k0 + KP;
 #pragma unroll 8
-        for (int d = 0; d < HD; ++d) {
-            const double a0 = q0[d], a1 = q1[d];
-            const double b0 = (double)k0[d], b1 = (double)k1[d];
-            if (FMA) {
-                d00 = fma(a0, b0, d00);
-                d01 = fma(a0, b1, d01);
-                d10 = fma(a1, b0, d10);
-                d11 = fma(a1, b1, d11);
-            } else {
-                d00 += a0 * b0;
-                d01 += a0 * b1;
-                d10 += a1 * b0;
-                d11 += a1 * b1;
-            }
+        for (int d = 0; d < HD; d += 2) {
+            const double2 a0 = *(const double2*)(q0 + d), a1 = *(const double2*)(q1 + d);
+            const double b00 = k0[d], b10 = k1[d], b01 = k0[d + 1], b11 = k1[d + 1];
+            d00 += a0.x * b00;
+            d01 += a0.x * b10;
+            d10 += a1.x * b00;
+            d11 += a1.x * b10;
+            d00 += a0.y * b01;
+            d01 += a0.y * b11;
+            d10 += a1.y * b01;
+            d11 += a1.y * b11;
         }
         const double s00 = d00 * scale, s01 = d01 * scale, s10 = d10 * scale, s11 = d11 * scale;
         const int k = c * kChunkP + 2 * pp;
@@ -782,7 +788,9 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict
         m1 = o1 > m1 ? o1 : m1;
     }
     // ---- pass 2: probabilities, expSum, PV --------------------------------
-    const int pq = tid >> 5, dl = tid & 31;  // PV lanes: queries 4*pq..+3, columns dl + 32*j
+    // PV lanes: queries 4*pq .. +3; columns 2*dl, 2*dl+1 (and 64 + those
+    // when HD = 128)
+    const int pq = tid >> 5, dl = tid & 31;
     double acc[4][DB];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -797,18 +805,24 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict
         sv0 = *(const double2*)(sca + kk);
         sv1 = *(const double2*)(sca + sc_next + kk);
     };
-    __syncthreads();  // pass-1 reads of sm.kv done before V overwrites it
-    load(vb, 0);
+    __syncthreads();  // pass-1 reads of sm.k done before V overwrites it
+    LAMD_TILE_LOAD(vb, 0)
     load_scores(0);
     for (int c = 0; c < nch; ++c) {
         __syncthreads();  // previous chunk's PV reads done
-        store();          // V chunk c
+#pragma unroll
+        for (int j = 0; j < F4; ++j) {  // V chunk, row-major: v[position][d]
+            const int e = (tid + j * 256) * 4;
+            double* d = &sm.v[(e / HD) * HD + e % HD];
+            *(double2*)d = make_double2((double)rk[j].x, (double)rk[j].y);
+            *(double2*)(d + 2) = make_double2((double)rk[j].z, (double)rk[j].w);
+        }
         const int k = c * kChunkP + 2 * pp;
         sm.p[qa][2 * pp] = k <= lim_a ? exp(sv0.x - m0) : 0.0;
         sm.p[qa][2 * pp + 1] = k + 1 <= lim_a ? exp(sv0.y - m0) : 0.0;
         sm.p[qa + 1][2 * pp] = k <= lim_a + 1 ? exp(sv1.x - m1) : 0.0;
         sm.p[qa + 1][2 * pp + 1] = k + 1 <= lim_a + 1 ? exp(sv1.y - m1) : 0.0;
-        load(vb, c + 1);   // next V chunk
+        LAMD_TILE_LOAD(vb, c + 1)  // next V chunk
         load_scores(c + 1);
         __syncthreads();
         const int kc = c * kChunkP;
@@ -821,16 +835,27 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict
         for (int i = 0; i < 4; ++i) {
             const int qi = 4 * pq + i;
             const int n = min(kChunkP, base + s0 + qi + 1 - kc);  // valid positions of this chunk
+            const double* vr = &sm.v[2 * dl];
             for (int kk = 0; kk < n; ++kk) {
                 const double pk = sm.p[qi][kk];
-#pragma unroll
-                for (int j = 0; j < DB; ++j) {
-                    const double v = (double)sm.kv[kk][dl + 32 * j];
-                    acc[i][j] = FMA ? fma(pk, v, acc[i][j]) : acc[i][j] + pk * v;
+                double v[DB];
+                if constexpr (DB == 4) {
+                    const double2 va = *(const double2*)(vr + kk * HD), vc = *(const double2*)(vr + kk * HD + 64);
+                    v[0] = va.x;
+                    v[1] = va.y;
+                    v[2] = vc.x;
+                    v[3] = vc.y;
+                } else {
+                    const double2 va = *(const double2*)(vr + kk * HD);
+                    v[0] = va.x;
+                    v[1] = va.y;
                 }
+#pragma unroll
+                for (int j = 0; j < DB; ++j) acc[i][j] = acc[i][j] + pk * v[j];
             }
         }
     }
+#undef LAMD_TILE_LOAD
     if (tid < kTileQ) sm.es[tid] = es;
     __syncthreads();
 #pragma unroll
@@ -840,7 +865,7 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict
             const double e = sm.es[qi];
 #pragma unroll
             for (int j = 0; j < DB; ++j)
-                out[(row0 + qi) * q_dim + (size_t)h * HD + dl + 32 * j] = acc[i][j] / e;
+                out[(row0 + qi) * q_dim + (size_t)h * HD + 64 * (j >> 1) + 2 * dl + (j & 1)] = acc[i][j] / e;
         }
     }
 }
@@ -2281,8 +2306,8 @@ hipError_t launch_attention(const double* q, const float* cache_k, const float* 
         }
         if (!scratch || span % 2 != 0) return hipErrorInvalidValue;
         const dim3 grid(heads, ceil_div(seq, kTileQ), batch);
-#define LAMD_TILE(HDV, F)                                                                          \
-    hipLaunchKernelGGL((attn_tile_kernel<HDV, F>), grid, dim3(256), 0, s, q, cache_k, cache_v, pos0, \
+#define LAMD_TILE(HDV)                                                                             \
+    hipLaunchKernelGGL((attn_tile_kernel<HDV>), grid, dim3(256), 0, s, q, cache_k, cache_v, pos0,    \
                        msl, span, heads, kv_heads, seq, scratch, out)
         const dim3 gridf(heads, ceil_div(seq, 16 * (qt ? qt : 2)), batch);
 #define LAMD_FAST(HDV, QTV)                                                                          \
@@ -2290,7 +2315,7 @@ hipError_t launch_attention(const double* q, const float* cache_k, const float* 
                        pos0, msl, span, heads, kv_heads, seq, scratch, out)
         if (hd == 128) {
             if (strict) {
-                LAMD_TILE(128, false);
+                LAMD_TILE(128);
             } else if (qt == 4) {
                 LAMD_FAST(128, 4);
             } else {
@@ -2298,7 +2323,7 @@ hipError_t launch_attention(const double* q, const float* cache_k, const float* 
             }
         } else {
             if (strict) {
-                LAMD_TILE(64, false);
+                LAMD_TILE(64);
             } else if (qt == 4) {
                 LAMD_FAST(64, 4);
             } else {
