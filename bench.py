@@ -55,6 +55,19 @@ def pmc_traffic():
         return None
 
 
+def traced_step():
+    """The timed kernel's figures from the committed rocprofv3 kernel trace of
+    this same command (profiles/gemv_m1_up_trace.json): average dispatch
+    duration over the timed launches, and their span (first start to last end)
+    per launch, which the tracer's own per-dispatch work lengthens."""
+    path = os.path.join(ROOT, "profiles", "gemv_m1_up_trace.json")
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
+
 def gemv_bytes(m: int, n: int, k: int) -> int:
     return n * ((k + 15) // 16) * 4 + 4 * m * (k + n)
 
@@ -607,6 +620,16 @@ def main() -> int:
                                         f"same rotation: the per-launch latency floor at this size",
                      "sustained": sustained},
     }
+    tr = traced_step()
+    if tr:
+        # frac from the profile's per-dispatch duration, next to the one from
+        # this run's HIP events (`frac`, the line's figure)
+        us = tr["us_per_dispatch"]
+        result["roofline"]["traced"] = {
+            "us_per_dispatch": us, "frac": round(b1 / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "us_span_per_launch": tr["us_span_per_launch"],
+            "us_per_step_hip_events_traced": tr["us_per_step_hip_events_traced"],
+            "source": "profiles/gemv_m1_up_kernel_trace.md (rocprofv3 --kernel-trace of this command)"}
 
     # ---------------- config-1 sweep ----------------------------------------------
     if not args.no_sweep:
