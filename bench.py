@@ -402,6 +402,10 @@ def bench_model(args, torch, timer, log):
     fnorm = rng.uniform(0.5, 1.5, h).astype(np.float32)
     log(f"model weights generated in {time.perf_counter() - t0:.1f}s")
     res3, res4 = [], []
+    # one prompt (and one config-4 batch) for both norm modes, so their tokens compare
+    ids1 = rng.integers(0, c["vocab"], size=(1, prompt)).astype(np.int32)
+    ids8 = rng.integers(0, c["vocab"], size=(batch, prompt)).astype(np.int32)
+    gen_tokens = {}
     for norm in args.model_norms.split(","):
         cfg = tf.BlockConfig(h, c["heads"], c["kv_heads"], c["head_dim"], inter, max_seq_len=msl,
                              max_batch=batch, rope_theta=c["theta"], norm_eps=1e-5,
@@ -410,7 +414,6 @@ def bench_model(args, torch, timer, log):
         model = tf.Transformer(cfg, layers, emb, fnorm, vocab=c["vocab"], final_norm_eps=1e-5,
                                max_tokens=msl + 1, max_prefill=prompt)
         log(f"model ({norm}) on device in {time.perf_counter() - t1:.1f}s")
-        ids1 = rng.integers(0, c["vocab"], size=(1, prompt)).astype(np.int32)
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         # config 3: prefill 2048, then 256 greedy tokens through the captured step
         model.prefill(ids1)
@@ -427,6 +430,7 @@ def bench_model(args, torch, timer, log):
         torch.cuda.synchronize()
         t_dec = ev0.elapsed_time(ev1)
         toks = model.tokens()
+        gen_tokens[norm] = toks[0, prompt + 1:prompt + 1 + gen].copy()
         tok_s = gen / (t_dec * 1e-3)
         gbs = decode_bytes_per_token(c, prompt + gen / 2) * tok_s / 1e9
         res3.append({"norm": norm, "decode_tok_s": round(tok_s, 2),
@@ -436,7 +440,6 @@ def bench_model(args, torch, timer, log):
                      "last_tokens": toks[0, -4:].tolist()})
         log(f"config3 decode {res3[-1]}")
         # config 4: batch 8 x 2048 prefill
-        ids8 = rng.integers(0, c["vocab"], size=(batch, prompt)).astype(np.int32)
         model.prefill(ids8)
         torch.cuda.synchronize()
         reps = 2
@@ -456,8 +459,16 @@ def bench_model(args, torch, timer, log):
         out["cpu_prefill_slice"] = cpu_prefill_slice(c, cpu_cores(), log)
     out["decode"] = {"config": f"config3: {c['layers']} layers, vocab {c['vocab']}, tied fp32 "
                                f"LM head, greedy, {prompt}-token random prompt, {gen} tokens, "
-                               "one HIP graph per token, positions on device",
+                               "one HIP graph per token, positions on device; the same prompt "
+                               "for both norm modes",
                      "runs": res3}
+    if "fast" in gen_tokens and "strict" in gen_tokens:
+        # greedy tokens of the two summation modes, position by position: they
+        # agree until a near-tie of two logits flips (then the sequences part)
+        same = gen_tokens["fast"] == gen_tokens["strict"]
+        first = int(np.argmin(same)) if not same.all() else len(same)
+        out["decode"]["fast_strict_tokens"] = {"equal": int(same.sum()), "of": int(same.size),
+                                               "first_difference_at": first}
     out["prefill"] = {"config": f"config4: batch {batch} x {prompt} random ids, M={batch * prompt} "
                                 "rows per ternary GEMM, KV cache per sequence",
                       "runs": res4}

@@ -3,9 +3,10 @@
 Config 3 (poly/transformer.go:434-485 Generate, poly/mha.go:316-354
 attention over the whole cache, poly/transformer.go:664-719 LM head): a
 BitNet-2B block after a 2048-token prompt, single-token steps checked stage
-by stage over a 2048+ position cache, and a model with vocab 128256 whose
+by stage over a 2048+ position cache, and models with vocab 128256 (two
+layers after a 2048-token prompt; all 30 layers after a 64-token prompt) whose
 graph-replayed decode steps give the oracle's logits (both of loom's LM-head
-orders) and argmax tokens, its hidden rows equal to the same blocks chained
+orders) and argmax tokens, their hidden rows equal to the same blocks chained
 stage-checked.
 
 Config 4 (batch 8 x 2048, M = 16384 rows per ternary GEMM): the GEMM's int32
@@ -128,6 +129,59 @@ def test_config3_model_graph_decode(orc, torch_dev, tf, norm):
         assert fin.tobytes() == hids[call].tobytes(), f"final hidden of call {call}"
         base += x.shape[0]
         x = table[toks[PROMPT + call]][None].copy()
+    for b in blocks:
+        b.release()
+
+
+@pytest.mark.parametrize("norm", ["strict", "fast"])
+def test_config3_model_30_layers(orc, torch_dev, tf, norm):
+    # config 3's full depth: 30 BitNet-2B layers, vocab 128256 (tied fp32
+    # head), a 64-token prompt and 8 graph-replayed decode steps.  Each step's
+    # logits equal the oracle's LM head of the model's final hidden row and
+    # its token their argmax; the final hidden rows equal the same 30 blocks
+    # chained (prompt and generated tokens fed in), every block call checked
+    # stage by stage, then the oracle's final RMSNorm.
+    torch = torch_dev
+    L, P = 30, 64
+    shape = Shape(2560, 20, 5, 128, 6912, P + 16)
+    layers = [Weights(orc, shape, 3501 + 100 * i, act=ACT_SILU) for i in range(L)]
+    rng = np.random.default_rng(3507)
+    emb = rng.standard_normal(VOCAB * shape.hidden, dtype=np.float32) * np.float32(0.02)
+    fn = orc.uniform_f32(shape.hidden, 0.5, 1.5, 3508)
+    table = emb.reshape(VOCAB, shape.hidden)
+    model = tf.Transformer(layers[0].cfg(tf, norm=norm), [w.gpu(tf) for w in layers], emb, fn,
+                           vocab=VOCAB, final_norm_eps=1e-6, max_tokens=P + 12, max_prefill=P)
+    prompt = rng.integers(0, VOCAB, P).astype(np.int32)
+    lg = model.prefill(prompt, logits=True).cpu().numpy()[0]
+    hids = [model.last_hidden().cpu().numpy()[0]]
+    assert lg.tobytes() == orc.lm_head(hids[0], emb, simd=True).tobytes()
+    assert model.tokens()[0, P] == orc.argmax_first(lg)
+    for step in range(8):
+        lg = model.decode(1, use_graph=True, logits=True).cpu().numpy()[0]
+        h = model.last_hidden().cpu().numpy()[0]
+        assert lg.tobytes() == orc.lm_head(h, emb, simd=True).tobytes(), f"step {step} logits"
+        assert model.tokens()[0, P + 1 + step] == orc.argmax_first(lg), f"step {step} token"
+        hids.append(h)
+    toks = model.tokens()[0]
+    model.release()
+    blocks = [tf.BitNetBlock(w.cfg(tf, norm), w.gpu(tf)) for w in layers]
+    refs = [w.oracle_mha(orc) for w in layers]
+    x = table[toks[:P]].copy()
+    base = 0
+    for call in range(9):
+        print(f"  chain call {call}: rows={x.shape[0]} base={base}", flush=True)
+        for li, (blk, w) in enumerate(zip(blocks, layers)):
+            xd = to_dev(torch, x)
+            _, t = blk.forward(xd, taps=True)
+            torch.cuda.synchronize()
+            out = xd.cpu().numpy()
+            ck, cv = (a.cpu().numpy() for a in blk.kv_cache(0))
+            check_stages(orc, w, refs[li], x, t.numpy(), out, ck, cv, base, norm == "strict")
+            x = out
+        fin = orc.rmsnorm_forward(x[-1:], fn, 1e-6)[0]
+        assert fin.tobytes() == hids[call].tobytes(), f"final hidden of call {call}"
+        base += x.shape[0]
+        x = table[toks[P + call]][None].copy()
     for b in blocks:
         b.release()
 
