@@ -645,16 +645,21 @@ __global__ __launch_bounds__(256) void attention_kernel(const double* __restrict
 // Strict prefill attention.  One workgroup per (head, tile of kTileQ
 // consecutive queries, sequence).  K and V chunks of kChunkP positions are
 // staged through LDS in fp64 (converted once as they are staged; the next
-// chunk is prefetched into registers while the current one is used), so each
-// cached row is read once per tile instead of once per query.  Pass 1 forms
-// every score of the tile, each lane a 2 x 2 block of d-order chains (two
-// queries x two positions; K rows at an odd pitch, so the 16 positions a
-// wave reads at one d fall in distinct banks).  It keeps each query's maximum
-// and stores the scores in `sc` (rows x heads x span).  Pass 2 reads them
-// back, takes p = exp(score - max), adds expSum on one lane per query and
-// sum(p * v) on one lane per (query, column pair or pairs: d = 2l, 2l+1 and
-// 64+2l, 64+2l+1, so a wave's 16-byte value reads are contiguous), all in
-// position order.  Every sum
+// chunk is loaded into registers while the current one is used, and the
+// barriers between chunks wait for LDS operations only, so those loads stay
+// in flight), so each cached row is read once per tile instead of once per
+// query.  Pass 1 forms every score of the tile, each lane a 2 x 2 block of
+// d-order chains (queries 2 qp, 2 qp + 1 x chunk positions pp, pp + 16),
+// reading two dimensions of a Q or K row per 16-byte LDS read (row pitch
+// HD + 2: the 16 positions a wave reads at one d fall in distinct banks).
+// It keeps each query's maximum and stores the scores in `sc` (rows x heads x
+// span).  Pass 2 reads them back, takes p = exp(score - max), adds expSum on
+// one lane per query and sum(p * v) on one lane per (four queries, column
+// pair or pairs: d = 2l, 2l+1 and 64+2l, 64+2l+1, so a wave's 16-byte value
+// reads are contiguous), all in position order; a chunk that every query of
+// the tile sees whole is walked position by position for a lane's four
+// queries at once (each value read serves four queries), and wave 0 adds the
+// expSum chains in the same walk.  Every sum
 // therefore has the reference's order and roundings (a product, then a sum,
 // each rounded): exact.  Positions past a query's own position are skipped
 // (never added).
@@ -665,17 +670,69 @@ constexpr int kChunkP = 32;
 template <int HD>
 struct TileLds {
     static constexpr int QP = HD + 2;  // q row pitch (doubles): the query pairs' rows in distinct banks
-    static constexpr int KP = HD + 1;  // K row pitch (doubles, odd): 16 rows at one d in distinct banks
+    static constexpr int KP = HD + 2;  // K row pitch (doubles): 16 consecutive rows in distinct banks
+    static constexpr int PP = kChunkP + 2;  // probability row pitch: 16-byte pairs
     double q[kTileQ * QP];
     union {
         double k[kChunkP * KP];        // pass 1: K chunk, position-major
         double v[kChunkP * HD];        // pass 2: V chunk, position-major
     };
-    // probabilities; odd row pitch: the expSum lanes (one query each) and the
-    // two query groups of a wave's value lanes read distinct banks
-    double p[kTileQ][kChunkP + 1];
+    double p[kTileQ * PP];
     double es[kTileQ];
 };
+
+// Workgroup barrier for LDS only: this wave's LDS operations have completed
+// (lgkmcnt(0)), then s_barrier.  Unlike __syncthreads it does not wait for
+// the wave's outstanding global loads (its release fence would), so a chunk
+// prefetched into registers stays in flight across it.  The asm statements
+// keep the compiler from moving LDS accesses across the barrier.
+__device__ __forceinline__ void tile_lds_barrier() {
+    __asm__ __volatile__("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_s_barrier();
+    __asm__ __volatile__("" ::: "memory");
+}
+
+// PV over one chunk that every query of the tile sees whole: position by
+// position for the lane's four queries (each value read serves all four);
+// with ES the lane also adds its expSum query's probabilities (row `pe`) in
+// position order.  Each (query, column) chain adds in position order.
+template <int HD, bool ES>
+__device__ __forceinline__ void tile_pv_whole(const double* __restrict__ pr, const double* __restrict__ pe,
+                                              const double* __restrict__ vr, double (&acc)[4][HD / 32],
+                                              double& es) {
+    constexpr int DB = HD / 32;
+    constexpr int PP = kChunkP + 2;
+#pragma unroll 2
+    for (int kk = 0; kk < kChunkP; kk += 2) {
+        double2 pk[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pk[i] = *(const double2*)(pr + i * PP + kk);
+        if constexpr (ES) {
+            const double2 e = *(const double2*)(pe + kk);
+            es += e.x;
+            es += e.y;
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            double v[DB];
+            const double2 va = *(const double2*)(vr + (kk + u) * HD);
+            v[0] = va.x;
+            v[1] = va.y;
+            if constexpr (DB == 4) {
+                const double2 vc = *(const double2*)(vr + (kk + u) * HD + 64);
+                v[2] = vc.x;
+                v[3] = vc.y;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const double pv = u ? pk[i].y : pk[i].x;
+#pragma unroll
+                for (int j = 0; j < DB; ++j) acc[i][j] = acc[i][j] + pv * v[j];
+            }
+        }
+    }
+}
 
 template <int HD>
 __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict__ q,
@@ -686,7 +743,7 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict
                                                         double* __restrict__ sc_all,
                                                         double* __restrict__ out) {
     using Lds = TileLds<HD>;
-    constexpr int QP = Lds::QP, KP = Lds::KP;
+    constexpr int QP = Lds::QP, KP = Lds::KP, PP = Lds::PP;
     constexpr int DB = HD / 32;                       // value columns per PV lane
     constexpr int F4 = kChunkP * HD / 4 / 256;        // float4 per thread per chunk
     static_assert(F4 >= 1 && kChunkP * HD == F4 * 4 * 256, "chunk geometry");
@@ -723,8 +780,8 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict
         const int k = min((C) * kChunkP + e / HD, msl - 1);                         \
         rk[j] = *(const float4*)((SRC) + (size_t)k * kv_dim + e % HD);              \
     }
-    // score lanes: queries qa = 2*qp, qa+1 x chunk positions 2*pp, 2*pp+1;
-    // their scores live at sca[k], sca[span + k] (rows qa, qa+1 of the tile)
+    // score lanes: queries qa = 2*qp, qa+1 x chunk positions pp, pp+16; their
+    // scores live at sca[k], sca[sc_next + k] (rows qa, qa+1 of the tile)
     const int qp = tid >> 4, pp = tid & 15;
     const int qa = 2 * qp;
     const int lim_a = base + s0 + qa;  // last position query qa sees
@@ -738,47 +795,50 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict
     // ---- pass 1: scores and maxima ---------------------------------------
     double m0 = -1e9, m1 = -1e9;
     LAMD_TILE_LOAD(kb, 0)
+    __syncthreads();  // Q rows staged
     for (int c = 0; c < nch; ++c) {
-        __syncthreads();  // previous chunk fully read
 #pragma unroll
         for (int j = 0; j < F4; ++j) {  // K chunk: k[position][d]
             const int e = (tid + j * 256) * 4;
             double* d = &sm.k[(e / HD) * KP + e % HD];
-            d[0] = (double)rk[j].x;
-            d[1] = (double)rk[j].y;
-            d[2] = (double)rk[j].z;
-            d[3] = (double)rk[j].w;
+            *(double2*)d = make_double2((double)rk[j].x, (double)rk[j].y);
+            *(double2*)(d + 2) = make_double2((double)rk[j].z, (double)rk[j].w);
         }
         LAMD_TILE_LOAD(kb, c + 1)  // prefetch (clamped past the last chunk)
-        __syncthreads();
+        tile_lds_barrier();        // chunk c staged
         double d00 = 0.0, d01 = 0.0, d10 = 0.0, d11 = 0.0;
         const double* q0 = &sm.q[qa * QP];
         const double* q1 = q0 + QP;
-        const double* k0 = &sm.k[(2 * pp) * KP];
-        const double* k1 = k0 + KP;
+        const double* k0 = &sm.k[pp * KP];
+        const double* k1 = k0 + 16 * KP;
 #pragma unroll 8
         for (int d = 0; d < HD; d += 2) {
             const double2 a0 = *(const double2*)(q0 + d), a1 = *(const double2*)(q1 + d);
-            const double b00 = k0[d], b10 = k1[d], b01 = k0[d + 1], b11 = k1[d + 1];
-            d00 += a0.x * b00;
-            d01 += a0.x * b10;
-            d10 += a1.x * b00;
-            d11 += a1.x * b10;
-            d00 += a0.y * b01;
-            d01 += a0.y * b11;
-            d10 += a1.y * b01;
-            d11 += a1.y * b11;
+            const double2 b0 = *(const double2*)(k0 + d), b1 = *(const double2*)(k1 + d);
+            d00 += a0.x * b0.x;
+            d01 += a0.x * b1.x;
+            d10 += a1.x * b0.x;
+            d11 += a1.x * b1.x;
+            d00 += a0.y * b0.y;
+            d01 += a0.y * b1.y;
+            d10 += a1.y * b0.y;
+            d11 += a1.y * b1.y;
         }
         const double s00 = d00 * scale, s01 = d01 * scale, s10 = d10 * scale, s11 = d11 * scale;
-        const int k = c * kChunkP + 2 * pp;
-        if (k + 1 < span) {
-            if (w0) *(double2*)(sca + k) = make_double2(s00, s01);
-            if (w1) *(double2*)(sca + sc_next + k) = make_double2(s10, s11);
+        const int k = c * kChunkP + pp;  // positions k and k + 16
+        if (k < span) {
+            if (w0) sca[k] = s00;
+            if (w1) sca[sc_next + k] = s10;
+        }
+        if (k + 16 < span) {
+            if (w0) sca[k + 16] = s01;
+            if (w1) sca[sc_next + k + 16] = s11;
         }
         if (k <= lim_a && s00 > m0) m0 = s00;
-        if (k + 1 <= lim_a && s01 > m0) m0 = s01;
+        if (k + 16 <= lim_a && s01 > m0) m0 = s01;
         if (k <= lim_a + 1 && s10 > m1) m1 = s10;
-        if (k + 1 <= lim_a + 1 && s11 > m1) m1 = s11;
+        if (k + 16 <= lim_a + 1 && s11 > m1) m1 = s11;
+        tile_lds_barrier();  // chunk c read before chunk c + 1 overwrites it
     }
     // maximum over the 16 lanes of each query pair (order-free)
 #pragma unroll
@@ -798,18 +858,24 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict
         for (int j = 0; j < DB; ++j) acc[i][j] = 0.0;
     double es = 0.0;  // lane tid < kTileQ: query tid
     // this lane's four scores of chunk c (clamped past the end; surplus unused)
-    double2 sv0, sv1;
+    double sv00, sv01, sv10, sv11;
     auto load_scores = [&](int c) {
-        const int k = min(c, nch - 1) * kChunkP + 2 * pp;
-        const int kk = min(k, span - 2);
-        sv0 = *(const double2*)(sca + kk);
-        sv1 = *(const double2*)(sca + sc_next + kk);
+        const int k = min(c, nch - 1) * kChunkP + pp;
+        const int k0c = min(k, span - 1), k1c = min(k + 16, span - 1);
+        sv00 = sca[k0c];
+        sv01 = sca[k1c];
+        sv10 = sca[sc_next + k0c];
+        sv11 = sca[sc_next + k1c];
     };
-    __syncthreads();  // pass-1 reads of sm.k done before V overwrites it
+    // the stored scores are read back by the lanes that wrote them; the full
+    // barrier also orders those stores before the loads
+    __syncthreads();
     LAMD_TILE_LOAD(vb, 0)
     load_scores(0);
+    // every query of the tile sees every position of chunks before this one
+    const int whole_ch = (base + s0 + 1) / kChunkP;
+    const double* pe = &sm.p[min(tid, kTileQ - 1) * PP];  // expSum row (wave 0)
     for (int c = 0; c < nch; ++c) {
-        __syncthreads();  // previous chunk's PV reads done
 #pragma unroll
         for (int j = 0; j < F4; ++j) {  // V chunk, row-major: v[position][d]
             const int e = (tid + j * 256) * 4;
@@ -817,43 +883,51 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const double* __restrict
             *(double2*)d = make_double2((double)rk[j].x, (double)rk[j].y);
             *(double2*)(d + 2) = make_double2((double)rk[j].z, (double)rk[j].w);
         }
-        const int k = c * kChunkP + 2 * pp;
-        sm.p[qa][2 * pp] = k <= lim_a ? exp(sv0.x - m0) : 0.0;
-        sm.p[qa][2 * pp + 1] = k + 1 <= lim_a ? exp(sv0.y - m0) : 0.0;
-        sm.p[qa + 1][2 * pp] = k <= lim_a + 1 ? exp(sv1.x - m1) : 0.0;
-        sm.p[qa + 1][2 * pp + 1] = k + 1 <= lim_a + 1 ? exp(sv1.y - m1) : 0.0;
+        const int k = c * kChunkP + pp;
+        sm.p[qa * PP + pp] = k <= lim_a ? exp(sv00 - m0) : 0.0;
+        sm.p[qa * PP + pp + 16] = k + 16 <= lim_a ? exp(sv01 - m0) : 0.0;
+        sm.p[(qa + 1) * PP + pp] = k <= lim_a + 1 ? exp(sv10 - m1) : 0.0;
+        sm.p[(qa + 1) * PP + pp + 16] = k + 16 <= lim_a + 1 ? exp(sv11 - m1) : 0.0;
         LAMD_TILE_LOAD(vb, c + 1)  // next V chunk
         load_scores(c + 1);
-        __syncthreads();
+        tile_lds_barrier();  // chunk c's values and probabilities staged
         const int kc = c * kChunkP;
-        if (tid < kTileQ) {
-            const int lim = base + s0 + tid;
-            for (int kk = 0; kk < kChunkP; ++kk)
-                if (kc + kk <= lim) es += sm.p[tid][kk];
-        }
+        const double* vr = &sm.v[2 * dl];
+        if (c < whole_ch) {  // wave-uniform
+            if (tid < 64)
+                tile_pv_whole<HD, true>(&sm.p[4 * pq * PP], pe, vr, acc, es);
+            else
+                tile_pv_whole<HD, false>(&sm.p[4 * pq * PP], pe, vr, acc, es);
+        } else {
+            if (tid < kTileQ) {
+                const int lim = base + s0 + tid;
+                for (int kk = 0; kk < kChunkP; kk += 2) {
+                    const double2 pk = *(const double2*)(pe + kk);
+                    if (kc + kk <= lim) es += pk.x;
+                    if (kc + kk + 1 <= lim) es += pk.y;
+                }
+            }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int qi = 4 * pq + i;
-            const int n = min(kChunkP, base + s0 + qi + 1 - kc);  // valid positions of this chunk
-            const double* vr = &sm.v[2 * dl];
-            for (int kk = 0; kk < n; ++kk) {
-                const double pk = sm.p[qi][kk];
-                double v[DB];
-                if constexpr (DB == 4) {
-                    const double2 va = *(const double2*)(vr + kk * HD), vc = *(const double2*)(vr + kk * HD + 64);
-                    v[0] = va.x;
-                    v[1] = va.y;
-                    v[2] = vc.x;
-                    v[3] = vc.y;
-                } else {
+            for (int i = 0; i < 4; ++i) {
+                const int qi = 4 * pq + i;
+                const int n = min(kChunkP, base + s0 + qi + 1 - kc);  // valid positions of this chunk
+                for (int kk = 0; kk < n; ++kk) {
+                    const double pk = sm.p[qi * PP + kk];
+                    double v[DB];
                     const double2 va = *(const double2*)(vr + kk * HD);
                     v[0] = va.x;
                     v[1] = va.y;
-                }
+                    if constexpr (DB == 4) {
+                        const double2 vc = *(const double2*)(vr + kk * HD + 64);
+                        v[2] = vc.x;
+                        v[3] = vc.y;
+                    }
 #pragma unroll
-                for (int j = 0; j < DB; ++j) acc[i][j] = acc[i][j] + pk * v[j];
+                    for (int j = 0; j < DB; ++j) acc[i][j] = acc[i][j] + pk * v[j];
+                }
             }
         }
+        tile_lds_barrier();  // chunk c's reads done before chunk c + 1 is staged
     }
 #undef LAMD_TILE_LOAD
     if (tid < kTileQ) sm.es[tid] = es;
