@@ -150,9 +150,9 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 // s_waitcnt lgkmcnt(0) only (vmcnt and expcnt at their maxima)
 __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
 
-template <int NMAT, int EPI, int MI>
+template <int NMAT, int EPI, int MI, int NJ>
 __global__ __launch_bounds__(256, 2) void gemm_lds_kernel(MatArgs p, GemmGrid gg) {
-    constexpr int NJ = 2 / NMAT;
+    static_assert(NJ >= 1 && NJ * NMAT <= 2, "32-row weight blocks per wave and matrix");
     constexpr int BM = 32 * MI;
     constexpr int NA = BM / 16;  // copies per thread per stage
     constexpr int NSTEP = 8;     // MFMA K steps per 256-column stage
@@ -423,7 +423,7 @@ __global__ __launch_bounds__(256, 2) void gemm_lds_kernel(MatArgs p, GemmGrid gg
         }
         if (tid == 0) __hip_atomic_store(&gg.ctr[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    static_assert(MI != 2 || NMAT * MI * NJ * 16 * 256 == kSplitSlotInts, "a split slot holds one 64-token tile");
+    static_assert(MI != 2 || NMAT * MI * NJ * 16 * 256 <= kSplitSlotInts, "a split slot holds one 64-token tile");
 
     // Epilogue from the accumulators: value v of block (i, j) is token row
     // 32i + 8(v/4) + 4h + v%4, output column (nb0 + j)*32 + l32.
@@ -701,26 +701,39 @@ __global__ __launch_bounds__(256, 2) void gemm_lds_kernel(MatArgs p, GemmGrid gg
 // at most kSplitMaxTiles tiles, about kSplitTarget workgroups in all, at least
 // kMinSplitKtiles K tiles per range, at most kMaxSplit ranges.
 constexpr int kTile128MinTiles = 1024;
+// Half-width tiles (64 tokens x 128 weight rows, one workgroup of four waves
+// each owning one 32-row block) on one matrix when the full-width 64-token
+// grid has fewer tiles than the chip has CUs: twice the workgroups, so the
+// CUs that would sit idle or run one wave per SIMD run two (measured at
+// K = 2560 / 6912: M = 128 up 10.6 -> 7.6 us, down 12.4 -> 9.3; M = 256
+// 10.6 -> 7.9 / 13.4 -> 10.6; M = 512 down 16.6 -> 15.4, up unchanged;
+// M = 1024 up 21.7 -> 22.8, so that grid keeps full-width tiles).
+constexpr int kHalfWidthMaxTiles = 256;
 constexpr int kSplitMaxTilesPlan = 96;
 constexpr int kSplitTarget = 240;
 constexpr int kMinSplitKtiles = 6;
 constexpr int kMaxSplit = 4;
 
 struct GemmPlan {
-    int mi, ksplit, sps;
+    int mi, ksplit, sps, nj;
 };
 
 static GemmPlan plan_gemm(int m, int ntiles, int ktiles, int nmat, int device) {
     const int ngroups = ceil_div(ntiles, 16 / nmat);
-    // LOOM_AMD_GEMM_TILE=128|64 and LOOM_AMD_GEMM_SPLIT=n override the choice
-    // (tuning and tests)
+    // LOOM_AMD_GEMM_TILE=128|64, LOOM_AMD_GEMM_SPLIT=n and LOOM_AMD_GEMM_NJ=1|2
+    // override the choice (tuning and tests)
     const int force_tile = tune_int("LOOM_AMD_GEMM_TILE", 0);
     const int force_split = tune_int("LOOM_AMD_GEMM_SPLIT", 0);
-    if (force_tile == 128) return GemmPlan{4, 1, ktiles};
+    const int force_nj = tune_int("LOOM_AMD_GEMM_NJ", 0);
+    if (force_tile == 128) return GemmPlan{4, 1, ktiles, 2 / nmat};
     // large grids take 128-token tiles (never split)
-    if (force_tile != 64 && force_split == 0 && ceil_div(m, 128) * ngroups >= kTile128MinTiles)
-        return GemmPlan{4, 1, ktiles};
-    const int tiles = ceil_div(m, 64) * ngroups;
+    if (force_tile != 64 && force_split == 0 && force_nj == 0 && ceil_div(m, 128) * ngroups >= kTile128MinTiles)
+        return GemmPlan{4, 1, ktiles, 2 / nmat};
+    // one matrix on a grid of fewer full-width tiles than CUs: half-width
+    // tiles (128 weight rows, one 32-row block per wave)
+    int nj = 2 / nmat;
+    if (nmat == 1 && (force_nj == 1 || (force_nj == 0 && ceil_div(m, 64) * ngroups < kHalfWidthMaxTiles))) nj = 1;
+    const int tiles = ceil_div(m, 64) * (nj == 1 && nmat == 1 ? ceil_div(ntiles, 8) : ngroups);
     int want = 1;
     if (force_split > 0) {
         want = force_split;
@@ -735,14 +748,14 @@ static GemmPlan plan_gemm(int m, int ntiles, int ktiles, int nmat, int device) {
     int ks = ceil_div(ktiles, sps);
     const SplitWs ws = split_ws(device);
     if (ks > 1 && (!ws.part || tiles > kSplitTiles || tiles * ks > kSplitSlots)) ks = 1;
-    return GemmPlan{2, ks, ks > 1 ? sps : ktiles};
+    return GemmPlan{2, ks, ks > 1 ? sps : ktiles, nj};
 }
 
-template <int NMAT, int EPI, int MI>
+template <int NMAT, int EPI, int MI, int NJ>
 static hipError_t launch_gemm_tile(const MatArgs& p, const GemmPlan& pl, int device, hipStream_t s) {
     GemmGrid gg;
     gg.mtiles = ceil_div(p.e.m, 32 * MI);
-    gg.ngroups = ceil_div(p.ntiles, 16 / NMAT);
+    gg.ngroups = ceil_div(p.ntiles, 8 * NJ);  // 16-row tiles per workgroup: 4 waves x NJ 32-row blocks
     gg.ksplit = pl.ksplit;
     gg.sps = pl.sps;
     gg.group = tune_int("LOOM_AMD_GEMM_GROUP", 8);
@@ -751,15 +764,18 @@ static hipError_t launch_gemm_tile(const MatArgs& p, const GemmPlan& pl, int dev
     gg.ctr = ws.ctr;
     const int total = gg.mtiles * gg.ngroups * gg.ksplit;
     const int grid = ceil_div(total, kXcds) * kXcds;
-    hipLaunchKernelGGL((gemm_lds_kernel<NMAT, EPI, MI>), dim3(grid), dim3(256), 0, s, p, gg);
+    hipLaunchKernelGGL((gemm_lds_kernel<NMAT, EPI, MI, NJ>), dim3(grid), dim3(256), 0, s, p, gg);
     return hipGetLastError();
 }
 
 template <int NMAT, int EPI>
 static hipError_t launch_gemm_planned(const MatArgs& p, int device, hipStream_t s) {
     const GemmPlan pl = plan_gemm(p.e.m, p.ntiles, p.ktiles, NMAT, device);
-    if (pl.mi == 4) return launch_gemm_tile<NMAT, EPI, 4>(p, pl, device, s);
-    return launch_gemm_tile<NMAT, EPI, 2>(p, pl, device, s);
+    if (pl.mi == 4) return launch_gemm_tile<NMAT, EPI, 4, 2 / NMAT>(p, pl, device, s);
+    if constexpr (NMAT == 1) {
+        if (pl.nj == 1) return launch_gemm_tile<1, EPI, 2, 1>(p, pl, device, s);
+    }
+    return launch_gemm_tile<NMAT, EPI, 2, 2 / NMAT>(p, pl, device, s);
 }
 
 static bool plain_dense(const EpiDev& e) {

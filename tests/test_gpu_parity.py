@@ -758,6 +758,23 @@ def test_gemm_forced_plans(orc, torch_dev, bn, tuning, tile, split):
     _check_dense(orc, torch_dev, bn, m, x)
 
 
+@pytest.mark.parametrize("nj,split", [("1", "1"), ("1", "2"), ("1", "3"), ("2", "1")])
+@pytest.mark.parametrize("rows,cols,M", [(6912, 2560, 512), (2560, 6912, 200), (6900, 2560, 130),
+                                         (1000, 2000, 129)])
+def test_gemm_half_width_tiles(orc, torch_dev, bn, tuning, nj, split, rows, cols, M):
+    # 64-token tiles of 128 (half width) or 256 weight rows per workgroup, with
+    # and without split K (ranges of unequal length), ragged weight rows
+    # (6900 = 431.25 tiles, 1000 = 62.5) and token rows, plain and with
+    # residual + ReLU: bit-exact
+    tuning("LOOM_AMD_GEMM_NJ", nj)
+    tuning("LOOM_AMD_GEMM_SPLIT", split)
+    m = orc.random_matrix(rows, cols, seed=rows + cols + M)
+    x = orc.normal_f32(M * cols, seed=M + 11).reshape(M, cols)
+    res = orc.normal_f32(M * rows, seed=M + 12).reshape(M, rows)
+    _check_dense(orc, torch_dev, bn, m, x)
+    _check_dense(orc, torch_dev, bn, m, x, activation=0, residual=res)
+
+
 @pytest.mark.parametrize("group", ["0", "3", "8"])
 def test_gemm_tile_order_groups(orc, torch_dev, bn, tuning, group):
     # the GEMM's tile order: weight-row group fastest (0), or groups of 3
