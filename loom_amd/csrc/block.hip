@@ -214,6 +214,11 @@ template <int STRICT>
 static hipError_t launch_rmsnorm_t(const float* x, long ldx, int m, int n, const float* gain,
                                    double eps, float* y, int8_t* xq, int ldq, float* amax,
                                    int32_t* xsum, const double* totals, hipStream_t s) {
+    if (xq) {  // (the final norm without quantization keeps the workgroup kernel)
+        const RowNormArgs a{x, ldx, m, n, gain, eps, y, nullptr, xq, ldq, amax, xsum, totals};
+        hipError_t e = hipSuccess;
+        if (launch_row_norm_wave(kRowRms, STRICT, a, s, &e)) return e;
+    }
     const size_t shm = STRICT && !totals ? (size_t)ordered_sum_slots(n, 4) * sizeof(double) : 0;
     const dim3 g(m), b(256);
 #define LAMD_RMS(VPT)                                                                          \
@@ -2509,6 +2514,11 @@ template <int STRICT>
 static hipError_t launch_norm_f64_t(double* a, int m, int n, const float* w, double eps, float* pre,
                                     int8_t* xq, int ldq, float* amax, int32_t* xsum, int keep,
                                     const double* totals, hipStream_t s) {
+    {
+        const RowNormArgs ra{a, n, m, n, w, eps, pre, keep ? a : nullptr, xq, ldq, amax, xsum, totals};
+        hipError_t e = hipSuccess;
+        if (launch_row_norm_wave(kRowInnerF64, STRICT, ra, s, &e)) return e;
+    }
     const size_t shm = STRICT && !totals ? (size_t)ordered_sum_slots(n, 4) * sizeof(double) : 0;
     const dim3 g(m), b(256);
 #define LAMD_NF64(VPT)                                                                          \

@@ -138,6 +138,36 @@ hipError_t launch_matmul_norm(const Matrix* w0, const Matrix* w1, const float* x
 hipError_t launch_norm_quant(float* h, int ldh, int m, int n, const float* weight, double eps,
                              int strict, int8_t* hq, int ldq, float* amax, int32_t* xsum,
                              hipStream_t s, bool keep_rows = true, double* totals = nullptr);
+// Row norms + requantization of many rows with one wave per row (prefill):
+// kRowRms = RMSNorm layer (y = fp32((x / rms) * gain), poly/norm.go:102-138),
+// kRowInner = SwiGLU inner norm (x = fp32(x * scale * w), poly/bitnet_cpu.go:893-913),
+// kRowInnerF64 = MHA inner norm on fp64 rows (x = x * (scale * w),
+// poly/bitnet_cpu.go:868-887), each followed by the int8 quantization of the
+// normalized row.  Fast mode sums the squares in the same tree as the
+// one-workgroup-per-row kernels (thread t of 256 sums columns t, t + 256, ...;
+// then t += t + w for w = 128, 64, ..., 1), so both give the same bits; strict
+// mode takes the rows' ordered sums from `totals`.
+constexpr int kRowRms = 0, kRowInner = 1, kRowInnerF64 = 2;
+struct RowNormArgs {
+    const void* x;       // m rows (fp32, fp64 for kRowInnerF64), row stride ldx elements
+    long ldx;
+    int m, n;
+    const float* w;      // gain / weight (n floats) or null (unit weights)
+    double eps;
+    float* yf;           // kRowRms: y (stride n); kRowInner: x itself (stride ldx); kRowInnerF64: fp32 copy (stride n); or null
+    double* keep64;      // kRowInnerF64: x itself (stride ldx), or null
+    int8_t* xq;          // quantized rows, stride ldq (zero past n)
+    int ldq;
+    float* amax;
+    int32_t* xsum;
+    const double* totals;  // strict: the rows' ordered sums of squares
+};
+// Launches the one-wave kernel and returns true, or returns false (nothing
+// launched) when the rows do not qualify: fewer than 1024 rows, n % 4 != 0,
+// rows or outputs not 16-byte aligned, n beyond the kernel's register budget,
+// strict without totals, or LOOM_AMD_ROWNORM_WAVE=0.
+bool launch_row_norm_wave(int kind, int strict, const RowNormArgs& a, hipStream_t s, hipError_t* e);
+
 // Strict ordered sums of squares of m fp32 rows (one lane per row, in element
 // order) into totals when m is large enough and the rows are 16-byte aligned;
 // returns false (nothing launched) otherwise.

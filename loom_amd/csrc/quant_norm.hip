@@ -1,5 +1,7 @@
 // quant_norm.hip -- weight repack, activation quantization and the SwiGLU
 // inner RMSNorm + requantization (gfx950).
+#include <type_traits>
+
 #include "device_common.hpp"
 
 namespace lamd {
@@ -282,10 +284,212 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(float* __restrict__ h, 
     }
 }
 
+// ------------------------------------------------------------------------
+// Row norm + requantization, one wave per row (many rows: prefill).  Lane l
+// holds columns 256 j + 4 l .. + 3 (16-byte loads and stores, the four int8
+// codes as one 32-bit store), i.e. the values of threads 4 l .. 4 l + 3 of
+// the one-workgroup-per-row kernels.  Fast mode keeps their tree: each of
+// the four partial sums runs over j in order, then the pairs (t, t + w) for
+// w = 128 .. 4 are lanes (l, l + w/4) and w = 2, 1 the lane's own partials,
+// so the sum is the same bits with no barrier.  The maximum and the code sum
+// are order-free.
+// ------------------------------------------------------------------------
+
+template <int KIND, int STRICT, int NB>
+__global__ __launch_bounds__(256) void row_norm_wave_kernel(RowNormArgs a) {
+    using T = typename std::conditional<KIND == kRowInnerF64, double, float>::type;
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= a.m) return;  // wave-uniform
+    const int n = a.n;
+    const T* xr = (const T*)a.x + (size_t)row * a.ldx;
+    T v[NB][4];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const int c = 256 * j + 4 * lane;
+        if (c < n) {
+            if constexpr (KIND == kRowInnerF64) {
+                const double2 p0 = *(const double2*)(xr + c), p1 = *(const double2*)(xr + c + 2);
+                v[j][0] = p0.x;
+                v[j][1] = p0.y;
+                v[j][2] = p1.x;
+                v[j][3] = p1.y;
+            } else {
+                const float4 p0 = *(const float4*)(xr + c);
+                v[j][0] = p0.x;
+                v[j][1] = p0.y;
+                v[j][2] = p0.z;
+                v[j][3] = p0.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[j][i] = (T)0;
+        }
+    }
+    double total;
+    if (STRICT) {
+        total = a.totals[row];
+    } else {
+        double p[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const double f = (double)v[j][i];
+                p[i] = p[i] + f * f;
+            }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) p[i] = p[i] + __shfl_down(p[i], off, 64);
+        total = __shfl((p[0] + p[2]) + (p[1] + p[3]), 0, 64);
+        // the values again as they were loaded: without this the compiler
+        // keeps their fp64 conversions from the sum live for the scaling
+        // below, twice the registers (one wave per SIMD at n = 6912)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) __asm__ volatile("" : "+v"(v[j][i]));
+    }
+    double rms = 0.0, scale = 0.0;
+    if (KIND == kRowRms)
+        rms = sqrt(total / (double)n + a.eps);
+    else
+        scale = 1.0 / sqrt(total / (double)n + a.eps);
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const int c = 256 * j + 4 * lane;
+        if (c < n) {
+            float4 w4 = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+            if (a.w) w4 = *(const float4*)(a.w + c);
+            const float wf[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if constexpr (KIND == kRowRms) {
+                    const double normed = (double)v[j][i] / rms;
+                    v[j][i] = (float)(normed * (double)wf[i]);
+                    m = max_nan_skip(m, fabsf((float)v[j][i]));
+                } else if constexpr (KIND == kRowInner) {
+                    const double w = a.w ? (double)wf[i] : 1.0;
+                    v[j][i] = (float)((double)v[j][i] * scale * w);
+                    m = max_nan_skip(m, fabsf((float)v[j][i]));
+                } else {
+                    const double w = a.w ? (double)wf[i] : 1.0;
+                    v[j][i] = v[j][i] * (scale * w);
+                    m = max_nan_skip(m, (float)fabs((double)v[j][i]));
+                }
+            }
+            if constexpr (KIND == kRowRms) {
+                if (a.yf) *(float4*)(a.yf + (size_t)row * n + c) = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
+            } else if constexpr (KIND == kRowInner) {
+                if (a.yf) *(float4*)(a.yf + (size_t)row * a.ldx + c) = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
+            } else {
+                if (a.keep64) {
+                    double* kr = a.keep64 + (size_t)row * a.ldx + c;
+                    *(double2*)kr = make_double2(v[j][0], v[j][1]);
+                    *(double2*)(kr + 2) = make_double2(v[j][2], v[j][3]);
+                }
+                if (a.yf)
+                    *(float4*)(a.yf + (size_t)row * n + c) =
+                        make_float4((float)v[j][0], (float)v[j][1], (float)v[j][2], (float)v[j][3]);
+            }
+        }
+    }
+    m = wave_max(m);
+    if (m < 1e-5f) m = 1e-5f;
+    const double qs = 127.0 / (double)m;
+    const float qs32 = (float)qs;
+    int sum = 0;
+    int8_t* qr = a.xq + (size_t)row * a.ldq;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const int c = 256 * j + 4 * lane;
+        if (c < a.ldq) {
+            int q[4] = {0, 0, 0, 0};
+            if (c < n) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if constexpr (KIND == kRowInnerF64)
+                        q[i] = quant_one(v[j][i], qs);
+                    else
+                        q[i] = quant_f32(v[j][i], qs32, qs);
+                    sum += q[i];
+                }
+            }
+            *(uint32_t*)(qr + c) = pack4(q[0], q[1], q[2], q[3]);
+        }
+    }
+    for (int c = 256 * NB + 4 * lane; c < a.ldq; c += 256) *(uint32_t*)(qr + c) = 0u;
+    sum = wave_sum_i(sum);
+    if (lane == 0) {
+        a.amax[row] = m;
+        a.xsum[row] = sum;
+    }
+}
+
+constexpr int kRowWaveMinRows = 1024;
+
+bool launch_row_norm_wave(int kind, int strict, const RowNormArgs& a, hipStream_t s, hipError_t* e) {
+    if (tune_int("LOOM_AMD_ROWNORM_WAVE", 1) == 0) return false;
+    // fewer rows leave too few waves to cover a row's load latency (512 rows
+    // of 6912: 20 us against 14 us for the workgroup kernel; 2048 rows: 30
+    // against 37 us)
+    if (a.m < kRowWaveMinRows || a.n <= 0 || a.n % 4 != 0 || a.ldq % 4 != 0 || a.ldq < a.n) return false;
+    if (strict && !a.totals) return false;
+    const size_t es = kind == kRowInnerF64 ? 8 : 4;
+    auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    if (!al16(a.x) || ((size_t)a.ldx * es) % 16 != 0 || !al16(a.w) || !al16(a.yf) || !al16(a.keep64) ||
+        ((uintptr_t)a.xq & 3) != 0)
+        return false;
+    const int nb = (a.n + 255) / 256;
+    const int lim = kind == kRowInnerF64 ? 16 : 32;
+    if (nb > lim) return false;
+    const dim3 g((a.m + 3) / 4), b(256);
+#define LAMD_RNW(K, S, NB) hipLaunchKernelGGL((row_norm_wave_kernel<K, S, NB>), g, b, 0, s, a)
+#define LAMD_RNW_NB(K, S)                   \
+    if (nb <= 8) {                          \
+        LAMD_RNW(K, S, 8);                  \
+    } else if (nb <= 12) {                  \
+        LAMD_RNW(K, S, 12);                 \
+    } else if (nb <= 16) {                  \
+        LAMD_RNW(K, S, 16);                 \
+    } else if constexpr (K != kRowInnerF64) { \
+        if (nb <= 28) {                     \
+            LAMD_RNW(K, S, 28);             \
+        } else {                            \
+            LAMD_RNW(K, S, 32);             \
+        }                                   \
+    }
+    auto go = [&](auto kc, auto sc) {
+        constexpr int K = decltype(kc)::value, S = decltype(sc)::value;
+        LAMD_RNW_NB(K, S)
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    if (kind == kRowRms) {
+        strict ? go(I0{}, I1{}) : go(I0{}, I0{});
+    } else if (kind == kRowInner) {
+        strict ? go(I1{}, I1{}) : go(I1{}, I0{});
+    } else {
+        strict ? go(I2{}, I1{}) : go(I2{}, I0{});
+    }
+#undef LAMD_RNW_NB
+#undef LAMD_RNW
+    *e = hipGetLastError();
+    return true;
+}
+
 template <int STRICT>
 static hipError_t launch_norm_t(float* h, int ldh, int m, int n, const float* weight, double eps,
                                 int8_t* hq, int ldq, float* amax, int32_t* xsum, int keep,
                                 const double* totals, hipStream_t s) {
+    {
+        const RowNormArgs a{h, ldh, m, n, weight, eps, keep ? h : nullptr, nullptr, hq, ldq, amax, xsum, totals};
+        hipError_t e = hipSuccess;
+        if (launch_row_norm_wave(kRowInner, STRICT, a, s, &e)) return e;
+    }
     const size_t shm = STRICT && !totals ? (size_t)ordered_sum_slots(n, 4) * sizeof(double)
                                          : 256 * sizeof(double);
     const dim3 g(m), b(256);

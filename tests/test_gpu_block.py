@@ -556,6 +556,33 @@ def test_block_decode_norm_fused_and_staged(orc, torch_dev, tf, shape, norm, tun
     staged.release()
 
 
+@pytest.mark.parametrize("norm,seq", [("fast", 300), ("fast", 1100), ("strict", 1100)])
+def test_prefill_row_norms_one_wave_equal_workgroup(orc, torch_dev, tf, tuning, norm, seq):
+    # The prefill row norms (RMSNorm1 and 2, the MHA fp64 inner norm, the
+    # SwiGLU inner norm) run one wave per row: fast mode in the same summation
+    # tree as the one-workgroup-per-row kernels, strict mode with 1024 or more
+    # rows on the rows' ordered sums.  LOOM_AMD_ROWNORM_WAVE=0 keeps the
+    # workgroup kernels; every tap and the block output must be the same bytes.
+    torch = torch_dev
+    sh = Shape(2560, 20, 5, 128, 6912, 1152)
+    w = Weights(orc, sh, seed=1401, act=ACT_SILU)
+    gw = w.gpu(tf)
+    x_in = orc.normal_f32(seq * sh.hidden, 1402).reshape(seq, sh.hidden)
+    outs = {}
+    for mode in ("wave", "workgroup"):
+        tuning("LOOM_AMD_ROWNORM_WAVE", None if mode == "wave" else "0")
+        blk = tf.BitNetBlock(w.cfg(tf, norm), gw)
+        x = to_dev(torch, x_in)
+        _, t = blk.forward(x, taps=True)
+        torch.cuda.synchronize()
+        outs[mode] = (x.cpu().numpy(), t.numpy())
+        blk.release()
+    a, b = outs["wave"], outs["workgroup"]
+    for f in tf.BlockTaps.FIELDS:
+        assert a[1][f].tobytes() == b[1][f].tobytes(), f
+    assert a[0].tobytes() == b[0].tobytes(), "block output"
+
+
 @pytest.mark.parametrize("norm", ["strict", "fast"])
 def test_block_decode_many_positions(orc, torch_dev, tf, norm):
     # single-token steps after a prefill, across decode-attention chunk

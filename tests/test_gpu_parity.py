@@ -775,6 +775,35 @@ def test_gemm_half_width_tiles(orc, torch_dev, bn, tuning, nj, split, rows, cols
     _check_dense(orc, torch_dev, bn, m, x, activation=0, residual=res)
 
 
+@pytest.mark.parametrize("n", [2560, 6912, 1000, 260, 8192, 4, 1001])
+def test_norm_quant_rows_one_wave_equal_workgroup(orc, torch_dev, bn, tuning, n):
+    # fast inner norm + requantization of 1024 or more rows, one wave per row,
+    # against the one-workgroup-per-row kernel (LOOM_AMD_ROWNORM_WAVE=0): the
+    # same normalized rows, codes (zero padding included), amax and sum(xq),
+    # on rows with NaN, +-Inf, zeros, tiny and huge values; n = 1001 (not a
+    # multiple of 4) takes the workgroup kernel in both runs
+    torch = torch_dev
+    m = 1030
+    h0 = orc.normal_f32(m * n, seed=n + 70).reshape(m, n) * np.float32(3.0)
+    h0[1, :] = 0.0
+    h0[2, n // 2] = np.nan
+    h0[3, 0] = np.inf
+    h0[4, -1] = -np.inf
+    h0[5, :] *= np.float32(1e-30)
+    h0[6, :] *= np.float32(1e30)
+    wt = orc.uniform_f32(n, 0.5, 1.5, seed=n + 71)
+    outs = {}
+    for mode in ("wave", "workgroup"):
+        tuning("LOOM_AMD_ROWNORM_WAVE", None if mode == "wave" else "0")
+        for weight in (wt, None):
+            h = to_dev(torch, h0)
+            q = bn.norm_quant_rows(h, None if weight is None else to_dev(torch, weight), eps=1e-5, norm="fast")
+            outs[(mode, weight is None)] = [a.cpu().numpy().tobytes() for a in (h, q.xq, q.amax, q.xsum)]
+    for unit in (False, True):
+        for name, a, b in zip(("rows", "codes", "amax", "xsum"), outs[("wave", unit)], outs[("workgroup", unit)]):
+            assert a == b, (name, unit)
+
+
 @pytest.mark.parametrize("group", ["0", "3", "8"])
 def test_gemm_tile_order_groups(orc, torch_dev, bn, tuning, group):
     # the GEMM's tile order: weight-row group fastest (0), or groups of 3
