@@ -1050,7 +1050,8 @@ static hipError_t launch_skinny_nt(const MatArgs& p, hipStream_t s) {
 // trips), so it pays only where full-K workgroups pull the most activation
 // bytes: long K (more than 16 K tiles) and M > 24 (measured at M = 17..64:
 // K = 6912 13.8 vs 16.2 us at M = 64, 9.4 vs 9.7 at M = 32; K = 2560 slower
-// at every M).  LOOM_AMD_SMALLM = 1 always takes it, 0 never.
+// at every M).  LOOM_AMD_SMALLM = 1 always takes it, 0 never (2: the GEMM
+// kernel for every 16 < M <= 64).
 template <int MSUB>
 static bool launch_small_split(const MatArgs& p, int device, hipStream_t s, hipError_t* e) {
     const int mode = tune_int("LOOM_AMD_SMALLM", -1);
@@ -1071,9 +1072,17 @@ static bool launch_small_split(const MatArgs& p, int device, hipStream_t s, hipE
 }
 
 // (four tiles of both SwiGLU matrices do not fit the register file)
+// 32 < M <= 64 on one matrix with long K (more than 16 K tiles) or M > 56:
+// the GEMM kernel (one 64-token tile: half-width tiles split over K), which
+// beats both small-M kernels there (measured, one box: down shape M = 64
+// 13.1 -> 10.2 us, M = 48 11.4 -> 10.8, M = 33 11.2 -> 10.5; up shape M = 64
+// 9.85 -> 9.0, but M = 48 8.7 -> 9.5, so shorter K keeps the skinny kernels).
 template <int NMAT, int MSUB>
 static hipError_t launch_small_m(const MatArgs& p, int device, hipStream_t s) {
     hipError_t e = hipSuccess;
+    const int mode = tune_int("LOOM_AMD_SMALLM", -1);
+    if (mode == 2 || (mode == -1 && NMAT == 1 && MSUB == 4 && (p.ktiles > 16 || p.e.m > 56)))
+        return launch_gemm(p, NMAT == 2, device, s);
     if (NMAT == 1 && launch_small_split<MSUB>(p, device, s, &e)) return e;
     const int nt = skinny_nt(p.ntiles, p.ktiles);
     if constexpr (NMAT == 1) {
@@ -1087,7 +1096,8 @@ const char* kernel_variant(int m) {
     if (m <= kFusedMaxRows) return "skinny_m16_fusedq";
     if (m <= 16) return "skinny_m16";
     if (m <= 32) return "skinny_m32";
-    if (m <= 64) return "skinny_m64";
+    if (m <= 56) return "skinny_m64";  // (the GEMM when K exceeds 16 K tiles)
+    if (m <= 64) return "gemm_m64";
     return "gemm";  // gemm_lds_kernel (64- or 128-token tiles): 32x32x32 MFMA, split K
 }
 

@@ -845,15 +845,22 @@ def test_prequantized_row_tiles_per_workgroup(orc, torch_dev, bn, tuning, ntr, r
     _check_dense(orc, torch_dev, bn, m, x, activation=0, residual=res)
 
 
-@pytest.mark.parametrize("nt", ["split", "1", "2", "4"])
+@pytest.mark.parametrize("nt", ["default", "gemm", "split", "1", "2", "4"])
 @pytest.mark.parametrize("rows,cols,M", [(6912, 2560, 64), (2560, 6912, 40), (1000, 2570, 17),
-                                         (6900, 2560, 33), (40000, 512, 20)])
+                                         (6900, 2560, 33), (40000, 512, 20), (2560, 6912, 64),
+                                         (6900, 6912, 57)])
 def test_small_m_tiles_per_workgroup(orc, torch_dev, bn, tuning, nt, rows, cols, M):
-    # 16 < M <= 64: the K-split kernel (default; 40000 rows exceed its
+    # 16 < M <= 64: the default choice, the GEMM kernel on one partial
+    # 64-token tile (LOOM_AMD_SMALLM=2: half-width tiles split over K, rows
+    # past M never stored), the K-split kernel (40000 rows exceed its
     # workspace and take the single-workgroup kernels), and the skinny kernels
     # with one, two or four 16-row tiles per workgroup (ragged last group and
     # K slice included): int32 accumulators and fp32 outputs bit-exact
-    if nt == "split":
+    if nt == "default":
+        pass
+    elif nt == "gemm":
+        tuning("LOOM_AMD_SMALLM", "2")
+    elif nt == "split":
         tuning("LOOM_AMD_SMALLM", "1")
     else:
         tuning("LOOM_AMD_SMALLM", "0")
