@@ -294,7 +294,10 @@ void loom_amd_block_release(loom_amd_block* b);
  * seq == 1 on a warm cache continues at the current position; any other
  * call restarts at position 0.  Each of the batch sequences has its own KV
  * cache; all of them advance together, so a single-token call on a warm
- * cache must carry the batch that filled it (another batch is refused).  Replaces the block loop body of
+ * cache must carry the batch that filled it (another batch is refused).
+ * loom's own 3-D batch semantics -- the batch's sequences share one KV
+ * timeline from position 0 (poly/mha.go:251-371) -- are this call with
+ * batch = 1 and seq = batch * seq over the same rows.  Replaces the block loop body of
  * forwardOnCPUNormal (poly/transformer_forward.go:228-245) for BitNet layers
  * (MHAForwardPackedTernaryCPU, poly/mha.go:204-371, and
  * SwiGLUForwardPackedTernaryCPU, poly/bitnet_cpu.go:915-1002).  May grow the

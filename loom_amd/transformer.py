@@ -153,9 +153,16 @@ class BitNetBlock:
     def kv_offset(self) -> int:
         return _lib.lib().loom_amd_block_kv_offset(self._h)
 
-    def forward(self, x, taps: bool = False):
+    def forward(self, x, taps: bool = False, shared_timeline: bool = False):
         """In place on x (torch float32 CUDA tensor, [seq, hidden] or
-        [batch, seq, hidden]); returns (x, BlockTaps or None)."""
+        [batch, seq, hidden]); returns (x, BlockTaps or None).
+
+        A 3-D batch runs as separate sequences, each with its own KV ring.
+        shared_timeline=True gives loom's semantics for a 3-D input instead
+        (poly/mha.go:251-371): the batch's sequences form one KV timeline from
+        position 0, sequence b at positions b*seq .., each attending to every
+        earlier position of the timeline -- the batch's rows run as one
+        sequence of batch*seq tokens."""
         torch = _torch()
         if x.dtype != torch.float32 or not x.is_cuda or not x.is_contiguous():
             raise ValueError("x must be a contiguous float32 device tensor")
@@ -165,6 +172,8 @@ class BitNetBlock:
             batch, seq = x.shape[0], x.shape[1]
         else:
             raise ValueError("x must be [seq, hidden] or [batch, seq, hidden]")
+        if shared_timeline:
+            batch, seq = 1, batch * seq
         if x.shape[-1] != self.cfg.hidden:
             raise ValueError(f"hidden is {x.shape[-1]}, block expects {self.cfg.hidden}")
         rows = batch * seq

@@ -593,6 +593,35 @@ class MHA:
                               workers or (os.cpu_count() or 1), _p(q))
         return q
 
+    def forward_batch(self, x: np.ndarray, workers: int = 0):
+        """loom's 3-D input [batch, seq, d_model], its batch loop restated
+        literally (poly/mha.go:251-371 with mhaPrepareKVForForward,
+        poly/mha_layout.go:62-70): unless the call is a warm single-token step
+        (batch 1, seq 1, kv_offset > 0) the caches are zeroed and kv_offset
+        restarts at 0; sequence b's rows take positions kv_start + b*seq + s,
+        its K/V rows are written, then each of its queries attends to every
+        position up to its own -- those of the sequences before it included;
+        kv_offset ends at kv_start + batch*seq.  Returns (pre, post) as
+        [batch, seq, d_model] fp32."""
+        x = np.ascontiguousarray(x, np.float32)
+        batch, seq = x.shape[0], x.shape[1]
+        x = x.reshape(batch, seq, self.d_model)
+        if not (batch == 1 and seq == 1 and self.c.kv_offset > 0):
+            self.cache_k[:] = 0.0
+            self.cache_v[:] = 0.0
+            self.c.kv_offset = 0
+        kv_start = self.c.kv_offset
+        pre = np.empty((batch, seq, self.d_model), np.float32)
+        post = np.empty((batch, seq, self.mats[3].rows), np.float32)
+        for b in range(batch):
+            seq_base = kv_start + b * seq
+            q = self.project(x[b], seq_base, workers)
+            attn = attention(q, self.cache_k, self.cache_v, seq_base, self.msl, self.num_heads,
+                             self.num_kv_heads, self.head_dim)
+            pre[b], post[b] = attn_out(self.mats[3], attn, self.inner_norm, self.c.eps, simd=self.simd)
+        self.c.kv_offset = kv_start + batch * seq
+        return pre, post
+
     def forward(self, x: np.ndarray, workers: int = 0):
         """Returns (pre, post, q_after_rope, attn_before_norm)."""
         x = np.ascontiguousarray(x, np.float32).reshape(-1, self.d_model)

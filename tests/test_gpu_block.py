@@ -584,6 +584,39 @@ def test_prefill_row_norms_one_wave_equal_workgroup(orc, torch_dev, tf, tuning, 
 
 
 @pytest.mark.parametrize("norm", ["strict", "fast"])
+def test_block_shared_timeline_is_loom_batch(orc, torch_dev, tf, norm):
+    # loom's [batch, seq, hidden] call (poly/mha.go:251-371): one KV timeline
+    # from position 0 shared by the batch's sequences -- the oracle's literal
+    # batch loop equals its call on the rows concatenated (pinned in
+    # tests/test_oracle_attention.py), so the shared-timeline call is checked
+    # stage by stage as one sequence of batch*seq rows; a warm single-token
+    # step then continues the timeline
+    torch = torch_dev
+    B, S = 3, 7
+    sh = SMALL
+    w = Weights(orc, sh, seed=1501, act=ACT_SILU)
+    blk = tf.BitNetBlock(w.cfg(tf, norm), w.gpu(tf))
+    mha_ref = w.oracle_mha(orc)
+    x_in = orc.normal_f32(B * S * sh.hidden, 1502).reshape(B, S, sh.hidden)
+    x = to_dev(torch, x_in)
+    _, t = blk.forward(x, taps=True, shared_timeline=True)
+    torch.cuda.synchronize()
+    assert blk.kv_offset == B * S
+    ck, cv = (a.cpu().numpy() for a in blk.kv_cache(0))
+    check_stages(orc, w, mha_ref, x_in.reshape(B * S, sh.hidden), t.numpy(),
+                 x.cpu().numpy().reshape(B * S, sh.hidden), ck, cv, 0, strict=norm == "strict")
+    x1_in = orc.normal_f32(sh.hidden, 1503).reshape(1, sh.hidden)
+    x1 = to_dev(torch, x1_in)
+    _, t1 = blk.forward(x1, taps=True)
+    torch.cuda.synchronize()
+    assert blk.kv_offset == B * S + 1
+    ck, cv = (a.cpu().numpy() for a in blk.kv_cache(0))
+    check_stages(orc, w, mha_ref, x1_in, t1.numpy(), x1.cpu().numpy(), ck, cv, B * S,
+                 strict=norm == "strict")
+    blk.release()
+
+
+@pytest.mark.parametrize("norm", ["strict", "fast"])
 def test_block_decode_many_positions(orc, torch_dev, tf, norm):
     # single-token steps after a prefill, across decode-attention chunk
     # borders (32-position chunks in fast mode), checked stage by stage

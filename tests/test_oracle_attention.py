@@ -545,3 +545,34 @@ def test_mha_qk_norm_forward_composes(orc):
     assert np.array_equal(q2, q)
     ck, cv = m2.cache_k.reshape(MSL, KV * HD), m2.cache_v.reshape(MSL, KV * HD)
     assert np.array_equal(orc.attention(q2, ck, cv, 0, MSL, HEADS, KV, HD), attn)
+
+
+def test_mha_batch_is_one_timeline(orc):
+    # loom's [batch, seq, d_model] input (poly/mha.go:251-371): the batch's
+    # sequences share one KV timeline from position 0, so the literal batch
+    # loop equals one call on the batch's rows concatenated -- the mapping the
+    # device block's shared-timeline call uses.  Both then continue the same
+    # way with warm single-token steps, and a later batch call restarts.
+    B, S = 3, 5
+    x = orc.normal_f32(B * S * HID, 201).reshape(B, S, HID)
+    mb, mf = make_mha(orc, seed=202), make_mha(orc, seed=202)
+    pre_b, post_b = mb.forward_batch(x)
+    pre_f, post_f, _, _ = mf.forward(x.reshape(B * S, HID))
+    assert np.array_equal(pre_b.reshape(B * S, HID), pre_f)
+    assert np.array_equal(post_b.reshape(B * S, HID), post_f)
+    assert mb.kv_offset == mf.kv_offset == B * S
+    assert np.array_equal(mb.cache_k, mf.cache_k) and np.array_equal(mb.cache_v, mf.cache_v)
+    # the last sequence's first query attends to the earlier sequences' rows:
+    # running that sequence alone (its own timeline from 0) gives other values
+    alone = make_mha(orc, seed=202)
+    _, post_alone, _, _ = alone.forward(x[B - 1])
+    assert not np.array_equal(post_alone, post_b[B - 1])
+    for step in range(3):
+        x1 = orc.normal_f32(HID, 210 + step).reshape(1, 1, HID)
+        _, pb = mb.forward_batch(x1)
+        _, pf, _, _ = mf.forward(x1.reshape(1, HID))
+        assert np.array_equal(pb.reshape(1, HID), pf)
+    assert mb.kv_offset == B * S + 3
+    pre_b2, post_b2 = mb.forward_batch(x)  # not a single-token step: restarts at 0
+    assert mb.kv_offset == B * S
+    assert np.array_equal(post_b2, post_b)
