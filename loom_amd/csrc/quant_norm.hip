@@ -430,6 +430,34 @@ __global__ __launch_bounds__(256) void row_norm_wave_kernel(RowNormArgs a) {
 
 constexpr int kRowWaveMinRows = 1024;
 
+// The kernel instance for nb 256-column blocks: NB of 8, 12, 16, 28 or 32
+// (fp64 rows up to 16, the register budget).
+template <int KIND, int STRICT>
+static void launch_row_norm_nb(int nb, const RowNormArgs& a, hipStream_t s) {
+    const dim3 g((a.m + 3) / 4), b(256);
+    if (nb <= 8) {
+        hipLaunchKernelGGL((row_norm_wave_kernel<KIND, STRICT, 8>), g, b, 0, s, a);
+    } else if (nb <= 12) {
+        hipLaunchKernelGGL((row_norm_wave_kernel<KIND, STRICT, 12>), g, b, 0, s, a);
+    } else if (nb <= 16 || KIND == kRowInnerF64) {
+        hipLaunchKernelGGL((row_norm_wave_kernel<KIND, STRICT, 16>), g, b, 0, s, a);
+    } else if constexpr (KIND != kRowInnerF64) {
+        if (nb <= 28) {
+            hipLaunchKernelGGL((row_norm_wave_kernel<KIND, STRICT, 28>), g, b, 0, s, a);
+        } else {
+            hipLaunchKernelGGL((row_norm_wave_kernel<KIND, STRICT, 32>), g, b, 0, s, a);
+        }
+    }
+}
+
+template <int KIND>
+static void launch_row_norm_kind(int strict, int nb, const RowNormArgs& a, hipStream_t s) {
+    if (strict)
+        launch_row_norm_nb<KIND, 1>(nb, a, s);
+    else
+        launch_row_norm_nb<KIND, 0>(nb, a, s);
+}
+
 bool launch_row_norm_wave(int kind, int strict, const RowNormArgs& a, hipStream_t s, hipError_t* e) {
     if (tune_int("LOOM_AMD_ROWNORM_WAVE", 1) == 0) return false;
     // fewer rows leave too few waves to cover a row's load latency (512 rows
@@ -443,40 +471,13 @@ bool launch_row_norm_wave(int kind, int strict, const RowNormArgs& a, hipStream_
         ((uintptr_t)a.xq & 3) != 0)
         return false;
     const int nb = (a.n + 255) / 256;
-    const int lim = kind == kRowInnerF64 ? 16 : 32;
-    if (nb > lim) return false;
-    const dim3 g((a.m + 3) / 4), b(256);
-#define LAMD_RNW(K, S, NB) hipLaunchKernelGGL((row_norm_wave_kernel<K, S, NB>), g, b, 0, s, a)
-#define LAMD_RNW_NB(K, S)                   \
-    if (nb <= 8) {                          \
-        LAMD_RNW(K, S, 8);                  \
-    } else if (nb <= 12) {                  \
-        LAMD_RNW(K, S, 12);                 \
-    } else if (nb <= 16) {                  \
-        LAMD_RNW(K, S, 16);                 \
-    } else if constexpr (K != kRowInnerF64) { \
-        if (nb <= 28) {                     \
-            LAMD_RNW(K, S, 28);             \
-        } else {                            \
-            LAMD_RNW(K, S, 32);             \
-        }                                   \
-    }
-    auto go = [&](auto kc, auto sc) {
-        constexpr int K = decltype(kc)::value, S = decltype(sc)::value;
-        LAMD_RNW_NB(K, S)
-    };
-    using I0 = std::integral_constant<int, 0>;
-    using I1 = std::integral_constant<int, 1>;
-    using I2 = std::integral_constant<int, 2>;
-    if (kind == kRowRms) {
-        strict ? go(I0{}, I1{}) : go(I0{}, I0{});
-    } else if (kind == kRowInner) {
-        strict ? go(I1{}, I1{}) : go(I1{}, I0{});
-    } else {
-        strict ? go(I2{}, I1{}) : go(I2{}, I0{});
-    }
-#undef LAMD_RNW_NB
-#undef LAMD_RNW
+    if (nb > (kind == kRowInnerF64 ? 16 : 32)) return false;
+    if (kind == kRowRms)
+        launch_row_norm_kind<kRowRms>(strict, nb, a, s);
+    else if (kind == kRowInner)
+        launch_row_norm_kind<kRowInner>(strict, nb, a, s);
+    else
+        launch_row_norm_kind<kRowInnerF64>(strict, nb, a, s);
     *e = hipGetLastError();
     return true;
 }
