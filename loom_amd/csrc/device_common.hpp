@@ -148,9 +148,18 @@ __device__ __forceinline__ int quant_f32(float v, float s32, double s) {
     return quant_one((double)v, s);
 }
 
+// Low bytes of a, b, c, d as bytes 0..3.  v_perm_b32(S0, S1, sel): byte i of
+// the result is byte sel_i of the pair {S0:S1} (0..3 from S1, 4..7 from S0),
+// and selector 0x0c gives a zero byte.
 __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
-    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
-           ((uint32_t)(d & 0xff) << 24);
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x0c0c0400u);
+    return lo | (hi << 16);
+}
+
+// Sum of the four signed bytes of w plus acc (v_dot4 against 0x01010101).
+__device__ __forceinline__ int byte_sum_i8(uint32_t w, int acc) {
+    return __builtin_amdgcn_sdot4((int)w, 0x01010101, acc, false);
 }
 
 // loom's "a > maxAbs" update: NaN never replaces the running maximum.
@@ -230,6 +239,18 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
     LAMD_MAX_STEP(kDppBcast31)
 #undef LAMD_MAX_STEP
     return __int_as_float(__builtin_amdgcn_readlane(b, 63));
+}
+
+// unsigned maximum over the wave (lanes shifted in from outside a row read 0)
+__device__ __forceinline__ unsigned wave_umax_dpp(unsigned v) {
+    int b = (int)v;
+    b = (int)max((unsigned)b, (unsigned)dpp_i<kDppShr1>(b, 0));
+    b = (int)max((unsigned)b, (unsigned)dpp_i<kDppShr2>(b, 0));
+    b = (int)max((unsigned)b, (unsigned)dpp_i<kDppShr4>(b, 0));
+    b = (int)max((unsigned)b, (unsigned)dpp_i<kDppShr8>(b, 0));
+    b = (int)max((unsigned)b, (unsigned)dpp_i<kDppBcast15>(b, 0));
+    b = (int)max((unsigned)b, (unsigned)dpp_i<kDppBcast31>(b, 0));
+    return (unsigned)__builtin_amdgcn_readlane(b, 63);
 }
 
 // s + p[base] + ... + p[base + 15] in index order, the terms past n replaced

@@ -55,6 +55,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
     __shared__ int xsum_s[kFusedMaxRows];
     __shared__ double nsum[NORM != NORM_NONE ? WAVES : 1][kFusedMaxRows];
     __shared__ float wmax[FUSEQ ? WAVES : 1][kFusedMaxRows];
+    __shared__ unsigned wmaxb[FUSEQ ? WAVES : 1][kFusedMaxRows];
     __shared__ int wsum[FUSEQ ? WAVES : 1][kFusedMaxRows];
     const int nt = blockIdx.x * NTR;  // first weight tile of the workgroup
     const int tid = threadIdx.x;
@@ -291,86 +292,215 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
             }
             __syncthreads();
         }
-        // bitNetActivationMaxAbs per row (poly/bitnet_cpu.go:45-71).
-        float lm[MR];
+        // bitNetActivationMaxAbs per row (poly/bitnet_cpu.go:45-71).  fp32
+        // rows first take the largest |x| bit pattern: the unsigned order of
+        // non-negative floats' bits is their value order, and NaN (either
+        // sign) sorts above every finite value and infinity, so the same
+        // maximum says whether a row holds a value that is not finite.  Such
+        // rows (a workgroup-uniform decision) take loom's NaN-skipping
+        // maximum in a second pass, as fp64 rows always do.
+        unsigned amb[MR];
+        bool general = F64;
+        if constexpr (!F64) {
+            unsigned lb[MR];
 #pragma unroll
-        for (int rr = 0; rr < MR; ++rr) lm[rr] = 0.0f;
+            for (int rr = 0; rr < MR; ++rr) lb[rr] = 0u;
 #pragma unroll
-        for (int j = 0; j < FV; ++j) {
-            const int idx = tid + j * T;
-            if (idx < n4) {
-                float a;
-                if (F64) {
-                    a = max_nan_skip(0.0f, (float)fabs(xd[j][0]));
-                    a = max_nan_skip(a, (float)fabs(xd[j][1]));
-                    a = max_nan_skip(a, (float)fabs(xd[j][2]));
-                    a = max_nan_skip(a, (float)fabs(xd[j][3]));
-                } else {
-                    a = max_nan_skip(0.0f, fabsf(xv[j].x));
-                    a = max_nan_skip(a, fabsf(xv[j].y));
-                    a = max_nan_skip(a, fabsf(xv[j].z));
-                    a = max_nan_skip(a, fabsf(xv[j].w));
+            for (int j = 0; j < FV; ++j) {
+                const int idx = tid + j * T;
+                if (idx < n4) {
+                    const unsigned a = max(max(__float_as_uint(xv[j].x) & 0x7fffffffu, __float_as_uint(xv[j].y) & 0x7fffffffu),
+                                           max(__float_as_uint(xv[j].z) & 0x7fffffffu, __float_as_uint(xv[j].w) & 0x7fffffffu));
+                    const int row = row_of<MR>(idx, row4);
+#pragma unroll
+                    for (int rr = 0; rr < MR; ++rr)
+                        if (rr == row) lb[rr] = max(lb[rr], a);
                 }
-                const int row = row_of<MR>(idx, row4);
+            }
 #pragma unroll
-                for (int rr = 0; rr < MR; ++rr)
-                    if (rr == row) lm[rr] = max_nan_skip(lm[rr], a);
+            for (int rr = 0; rr < MR; ++rr) {
+                if (rr < M) {
+                    const unsigned wm = wave_umax_dpp(lb[rr]);
+                    if (lane == 0) wmaxb[wave][rr] = wm;
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int rr = 0; rr < MR; ++rr) {
+                unsigned m = 0u;
+                if (rr < M)
+                    for (int w = 0; w < WAVES; ++w) m = max(m, wmaxb[w][rr]);
+                amb[rr] = m;
+                if (m > 0x7f7fffffu) general = true;  // NaN or infinity in row rr
             }
         }
+        if (general) {
+            float lm[MR];
 #pragma unroll
-        for (int rr = 0; rr < MR; ++rr) {
-            if (rr < M) {
-                const float wm = wave_max_dpp(lm[rr]);
-                if (lane == 0) wmax[wave][rr] = wm;
+            for (int rr = 0; rr < MR; ++rr) lm[rr] = 0.0f;
+#pragma unroll
+            for (int j = 0; j < FV; ++j) {
+                const int idx = tid + j * T;
+                if (idx < n4) {
+                    float a;
+                    if (F64) {
+                        a = max_nan_skip(0.0f, (float)fabs(xd[j][0]));
+                        a = max_nan_skip(a, (float)fabs(xd[j][1]));
+                        a = max_nan_skip(a, (float)fabs(xd[j][2]));
+                        a = max_nan_skip(a, (float)fabs(xd[j][3]));
+                    } else {
+                        a = max_nan_skip(0.0f, fabsf(xv[j].x));
+                        a = max_nan_skip(a, fabsf(xv[j].y));
+                        a = max_nan_skip(a, fabsf(xv[j].z));
+                        a = max_nan_skip(a, fabsf(xv[j].w));
+                    }
+                    const int row = row_of<MR>(idx, row4);
+#pragma unroll
+                    for (int rr = 0; rr < MR; ++rr)
+                        if (rr == row) lm[rr] = max_nan_skip(lm[rr], a);
+                }
+            }
+#pragma unroll
+            for (int rr = 0; rr < MR; ++rr) {
+                if (rr < M) {
+                    const float wm = wave_max_dpp(lm[rr]);
+                    if (lane == 0) wmax[wave][rr] = wm;
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int rr = 0; rr < MR; ++rr) {
+                float am = 0.0f;
+                if (rr < M) {
+                    for (int w = 0; w < WAVES; ++w) am = max_nan_skip(am, wmax[w][rr]);
+                }
+                amb[rr] = __float_as_uint(am);
             }
         }
-        __syncthreads();
         // bitNetQuantizedActivation (poly/bitnet_cpu.go:73-95) into LDS.
-        double sc[MR];
-        float sc32[MR];
+        float amc[MR], scf[MR];
 #pragma unroll
         for (int rr = 0; rr < MR; ++rr) {
-            float am = 0.0f;
-            if (rr < M) {
-                for (int w = 0; w < WAVES; ++w) am = max_nan_skip(am, wmax[w][rr]);
-            }
-            if (tid == rr) amax_bits[rr] = __float_as_uint(am);  // read after the main loop
+            float am = __uint_as_float(amb[rr]);
+            if (tid == rr) amax_bits[rr] = amb[rr];  // read after the main loop
             if (am < 1e-5f) am = 1e-5f;
-            sc[rr] = rr < M ? 127.0 / (double)am : 0.0;
-            sc32[rr] = (float)sc[rr];
+            amc[rr] = am;
+            scf[rr] = rr < M ? 127.0f / am : 0.0f;  // (fp32 division, correctly rounded)
         }
+        // loom's fp64 scales 127 / am and their fp32 roundings (formed where a
+        // branch needs them, off the fp32 path)
+        auto scales64 = [&](double (&sc)[MR], float (&sc32)[MR]) {
+#pragma unroll
+            for (int rr = 0; rr < MR; ++rr) {
+                sc[rr] = rr < M ? 127.0 / (double)amc[rr] : 0.0;
+                sc32[rr] = (float)sc[rr];
+            }
+        };
         int ls[MR];
 #pragma unroll
         for (int rr = 0; rr < MR; ++rr) ls[rr] = 0;
+        if constexpr (!F64) {
+            if (!general) {
+                // Finite rows, rounded in fp32 with sf = fl32(127 / am) (an
+                // fp32 division, so loom's fp64 scale stays off this path):
+                // sf is within 2^-24 + 2^-53 (relative) of loom's scale s, so
+                // p = fl32(x sf) is, as in quant_f32, within
+                // 127 (2^-23 + 2^-47) < 1.52e-5 of loom's fp64 product x s,
+                // and 3.1e-5 from every boundary j + 1/2 decides.  Every
+                // |x| <= amax <= am, so |p| < 127.5 and rintf needs no clamp.
+                // The test 0.5f - |p - r| > 3.1e-5f holds for all of a
+                // thread's values iff it holds for the largest |p - r|
+                // (fl(0.5f - d) does not increase with d): one test per thread
+                // instead of a branch per value, and a thread with a value
+                // nearer a boundary redoes its values with quant_f32.
+                float dmax = 0.0f;
+                uint32_t pk[FV];
 #pragma unroll
-        for (int j = 0; j < FV; ++j) {
-            const int idx = tid + j * T;
-            if (idx < n4) {
-                const int row = row_of<MR>(idx, row4);
-                double s = sc[0];
-                float s32 = sc32[0];
+                for (int j = 0; j < FV; ++j) {
+                    const int idx = tid + j * T;
+                    pk[j] = 0u;
+                    if (idx < n4) {
+                        const int row = row_of<MR>(idx, row4);
+                        float s32 = scf[0];
 #pragma unroll
-                for (int rr = 1; rr < MR; ++rr)
-                    if (rr == row) {
-                        s = sc[rr];
-                        s32 = sc32[rr];
+                        for (int rr = 1; rr < MR; ++rr)
+                            if (rr == row) s32 = scf[rr];
+                        const float p0 = xv[j].x * s32, p1 = xv[j].y * s32, p2 = xv[j].z * s32, p3 = xv[j].w * s32;
+                        const float r0 = rintf(p0), r1 = rintf(p1), r2 = rintf(p2), r3 = rintf(p3);
+                        dmax = fmaxf(dmax, fmaxf(fmaxf(fabsf(p0 - r0), fabsf(p1 - r1)),
+                                                 fmaxf(fabsf(p2 - r2), fabsf(p3 - r3))));
+                        pk[j] = pack4((int)r0, (int)r1, (int)r2, (int)r3);
                     }
-                int q0, q1, q2, q3;
-                if (F64) {
-                    q0 = quant_one(xd[j][0], s);
-                    q1 = quant_one(xd[j][1], s);
-                    q2 = quant_one(xd[j][2], s);
-                    q3 = quant_one(xd[j][3], s);
-                } else {
-                    q0 = quant_f32(xv[j].x, s32, s);
-                    q1 = quant_f32(xv[j].y, s32, s);
-                    q2 = quant_f32(xv[j].z, s32, s);
-                    q3 = quant_f32(xv[j].w, s32, s);
                 }
-                *(uint32_t*)(xq_s + row * p.ldq + 4 * (idx - row * row4)) = pack4(q0, q1, q2, q3);
+                if (!(0.5f - dmax > 3.1e-5f)) {
+                    double sc[MR];
+                    float sc32[MR];
+                    scales64(sc, sc32);
 #pragma unroll
-                for (int rr = 0; rr < MR; ++rr)
-                    if (rr == row) ls[rr] += q0 + q1 + q2 + q3;
+                    for (int j = 0; j < FV; ++j) {
+                        const int idx = tid + j * T;
+                        if (idx < n4) {
+                            const int row = row_of<MR>(idx, row4);
+                            double s = sc[0];
+                            float s32 = sc32[0];
+#pragma unroll
+                            for (int rr = 1; rr < MR; ++rr)
+                                if (rr == row) {
+                                    s = sc[rr];
+                                    s32 = sc32[rr];
+                                }
+                            pk[j] = pack4(quant_f32(xv[j].x, s32, s), quant_f32(xv[j].y, s32, s),
+                                          quant_f32(xv[j].z, s32, s), quant_f32(xv[j].w, s32, s));
+                        }
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < FV; ++j) {
+                    const int idx = tid + j * T;
+                    if (idx < n4) {
+                        const int row = row_of<MR>(idx, row4);
+                        *(uint32_t*)(xq_s + row * p.ldq + 4 * (idx - row * row4)) = pk[j];
+#pragma unroll
+                        for (int rr = 0; rr < MR; ++rr)
+                            if (rr == row) ls[rr] = byte_sum_i8(pk[j], ls[rr]);
+                    }
+                }
+            }
+        }
+        if (general) {  // fp64 rows, and fp32 rows with a NaN or infinity
+            double sc[MR];
+            float sc32[MR];
+            scales64(sc, sc32);
+#pragma unroll
+            for (int j = 0; j < FV; ++j) {
+                const int idx = tid + j * T;
+                if (idx < n4) {
+                    const int row = row_of<MR>(idx, row4);
+                    double s = sc[0];
+                    float s32 = sc32[0];
+#pragma unroll
+                    for (int rr = 1; rr < MR; ++rr)
+                        if (rr == row) {
+                            s = sc[rr];
+                            s32 = sc32[rr];
+                        }
+                    int q0, q1, q2, q3;
+                    if (F64) {
+                        q0 = quant_one(xd[j][0], s);
+                        q1 = quant_one(xd[j][1], s);
+                        q2 = quant_one(xd[j][2], s);
+                        q3 = quant_one(xd[j][3], s);
+                    } else {
+                        q0 = quant_f32(xv[j].x, s32, s);
+                        q1 = quant_f32(xv[j].y, s32, s);
+                        q2 = quant_f32(xv[j].z, s32, s);
+                        q3 = quant_f32(xv[j].w, s32, s);
+                    }
+                    *(uint32_t*)(xq_s + row * p.ldq + 4 * (idx - row * row4)) = pack4(q0, q1, q2, q3);
+#pragma unroll
+                    for (int rr = 0; rr < MR; ++rr)
+                        if (rr == row) ls[rr] += q0 + q1 + q2 + q3;
+                }
             }
         }
         // zero the padding columns k .. ldq of every row

@@ -246,6 +246,39 @@ def test_dense_fused_quant_edge_rows(orc, torch_dev, bn, M):
         assert pre.cpu().numpy().tobytes() == ref.pre.tobytes()
 
 
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_dense_fused_quant_rounding_ties(orc, torch_dev, bn, M):
+    # The fused prologue rounds in fp32 and takes loom's fp64 rounding for any
+    # thread holding a product within 3.1e-5 of a boundary j + 1/2.  With a
+    # row maximum of 127 the scale is exactly 1, so x = j + 1/2 is a tie
+    # (math.Round: away from zero, where rintf would pick the even neighbour);
+    # rows hold single ties, a run of ties, and near-ties on either side.
+    k = 2560
+    m = orc.random_matrix(96, k, seed=21)
+    rows = []
+    for i in range(M):
+        r = orc.normal_f32(k, 40 + i) * np.float32(20.0)
+        r[0] = np.float32(127.0)
+        r[7 + 64 * i] = np.float32(2.5)
+        r[900 + i] = np.float32(-0.5)
+        r[1500 + i] = np.nextafter(np.float32(6.5), np.float32(7.0))
+        r[1700 + i] = np.nextafter(np.float32(-6.5), np.float32(0.0))
+        if i % 2:
+            r[1000:1100] = np.arange(100, dtype=np.float32) - np.float32(49.5)
+        rows.append(r)
+    x = np.stack(rows)
+    assert np.abs(x).max() == np.float32(127.0)
+    ref = orc.dense_forward(m, x, simd=True)
+    assert ref.xq[0, 7] == 3 and ref.xq[0, 900] == -1  # the ties went away from zero
+    w = gpu_matrix(bn, m)
+    pre, _, taps = bn.dense_forward_packed_ternary(w, to_dev(torch_dev, x), taps=True)
+    torch_dev.cuda.synchronize()
+    assert np.array_equal(taps.xq.cpu().numpy(), ref.xq)
+    assert taps.amax.cpu().numpy().tobytes() == ref.amax.tobytes()
+    assert np.array_equal(taps.acc.cpu().numpy(), ref.acc)
+    assert pre.cpu().numpy().tobytes() == ref.pre.tobytes()
+
+
 @pytest.mark.parametrize("act", [0, 1, 2, 3, 4, 5, 6])
 def test_dense_activation_and_residual(orc, torch_dev, bn, act):
     m = orc.random_matrix(96, 160, seed=5)
