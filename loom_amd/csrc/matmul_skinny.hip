@@ -1049,12 +1049,14 @@ static void launch_fused_w(const MatArgs& p, size_t shm, hipStream_t s) {
     const size_t groups = (size_t)p.e.m * (p.k / 4);
     const dim3 grid(p.ntiles), block(WAVES * 64);
     // One row, one matrix: a workgroup takes two adjacent weight tiles, so
-    // the row's loads and quantization serve both (the Dense step at the
-    // BitNet-2B up shape, eight waves: 5.58 -> 5.24 us).  LOOM_AMD_FUSED_NTR =
-    // 1, 2 or 4 overrides (tests and tuning; four tiles only with two float4
-    // slots a thread).
+    // the row's loads and quantization serve both, while the paired grid
+    // still spans half the CUs (the Dense step at the BitNet-2B up shape,
+    // 432 tiles, eight waves: 5.58 -> 5.24 us; at the down shape, 160 tiles,
+    // pairs are slower: 4.96 -> 5.72 us).  LOOM_AMD_FUSED_NTR = 1, 2 or 4
+    // overrides (tests and tuning; four tiles only with two float4 slots a
+    // thread).
     if constexpr (NMAT == 1 && WAVES <= 8) {
-        const int ntr = tune_int("LOOM_AMD_FUSED_NTR", 2);
+        const int ntr = tune_int("LOOM_AMD_FUSED_NTR", ceil_div(p.ntiles, 2) >= 128 ? 2 : 1);
         if (p.e.m == 1 && groups <= (size_t)2 * WAVES * 64 && ntr == 2) {
             hipLaunchKernelGGL((skinny_kernel<NMAT, 1, WAVES, true, NORM_NONE, 0, 2, 1, 2>),
                                dim3(ceil_div(p.ntiles, 2)), block, shm, s, p);
@@ -1091,11 +1093,18 @@ static hipError_t launch_skinny(const MatArgs& p, hipStream_t s) {
     }
     const size_t shm = FUSEQ ? (size_t)p.e.m * p.ldq : 0;
     const dim3 grid(p.ntiles);
-    if constexpr (FUSEQ && NMAT == 1) {
-        // One row that four waves hold in four float4 slots a thread: four-wave
-        // workgroups with two weight tiles each instead of eight-wave ones
-        // (BitNet-2B up shape: 5.15 -> 4.81 us per Dense step; two waves 7.40)
-        if (w == 8 && p.e.m == 1 && (size_t)p.k / 4 <= (size_t)4 * 4 * 64) w = 4;
+    if constexpr (FUSEQ) {
+        // One row: the fewest waves, at least four, that hold it in four
+        // float4 slots a thread (BitNet-2B shapes, M = 1: the up projection's
+        // Dense step 5.15 -> 4.81 us with four waves instead of eight, two
+        // waves 7.40; the down projection's 5.61 -> 4.96 us with eight
+        // instead of sixteen; the SwiGLU FFN's fused gate|up pair takes the
+        // FFN from 19.2 to 17.0 us with four waves instead of eight).
+        if (p.e.m == 1) {
+            int w1 = 4;
+            while (w1 < w && (size_t)p.k / 4 > (size_t)4 * 64 * w1) w1 <<= 1;
+            if (w1 < w) w = w1;
+        }
     }
     if constexpr (FUSEQ) {
         const int v = tune_int("LOOM_AMD_FUSED_WAVES", 0);  // tuning override (1..16)

@@ -847,13 +847,15 @@ def test_gemm_tile_order_groups(orc, torch_dev, bn, tuning, group):
     _check_dense(orc, torch_dev, bn, m, x)
 
 
-@pytest.mark.parametrize("ntr", ["1", "2", "4"])
+@pytest.mark.parametrize("ntr", ["default", "1", "2", "4"])
 @pytest.mark.parametrize("rows,cols", [(6912, 2560), (2560, 6912), (1000, 2560), (40, 1000), (33, 260)])
 def test_fused_row_tiles_per_workgroup(orc, torch_dev, bn, tuning, ntr, rows, cols):
-    # M = 1 with the quantization fused: one, two or four 16-row weight tiles
-    # per workgroup (ragged last groups: 63 and 3 tiles, a partial last tile
-    # of 33 rows), plain and with residual + ReLU: bit-exact
-    tuning("LOOM_AMD_FUSED_NTR", ntr)
+    # M = 1 with the quantization fused: the dispatcher's choice, or one, two
+    # or four 16-row weight tiles per workgroup (ragged last groups: 63 and 3
+    # tiles, a partial last tile of 33 rows), plain and with residual + ReLU:
+    # bit-exact
+    if ntr != "default":
+        tuning("LOOM_AMD_FUSED_NTR", ntr)
     if ntr == "4":
         tuning("LOOM_AMD_FUSED_WAVES", "8")  # four tiles: eight-wave workgroups
     m = orc.random_matrix(rows, cols, seed=rows + cols)
