@@ -86,10 +86,20 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
         const uint32_t xb = (uint32_t)n4 * (F64 ? 32u : 16u);
         const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(F64 ? (const void*)p.x64 : (const void*)p.x, xb);
         const __amdgpu_buffer_rsrc_t gr = buffer_rsrc(p.nw, p.nw ? (uint32_t)row4 * 16u : 0u);
+        // Plain rows on eight or more waves skip the slots that lie wholly
+        // past the rows for the wave (a wave-uniform test; measured at the
+        // BitNet-2B down shape, M = 1: 4.95 -> 4.17 us per Dense step; with
+        // four waves, or with a norm fused, issuing every slot measured
+        // faster).
+        constexpr bool kSkipIdle = NORM == NORM_NONE && WAVES >= 8;
 #pragma unroll
         for (int j = 0; j < FV; ++j) {
             const int idx = tid + j * T;
             const bool ok = idx < n4;
+            if (kSkipIdle && j > 0 && __builtin_amdgcn_readfirstlane(wave) * 64 + j * T >= n4) {
+                xv[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                continue;
+            }
             if (F64) {
                 const uint32_t o = ok ? (uint32_t)idx * 32u : xb;
                 const double2 a = __builtin_bit_cast(double2, buffer_load16(xr, o));
@@ -242,22 +252,72 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
                 const double ms = tot[rr] / (double)k + p.neps;
                 f[rr] = NORM == NORM_RMS ? sqrt(ms) : 1.0 / sqrt(ms);  // rms, or scale
             }
+            if constexpr (NORM == NORM_RMS) {
+                // loom's float32((v / rms) * gain), each step in fp64.  With
+                // y = 1 / rms (one correctly rounded division per row), p =
+                // (v y) g lies within 5 * 2^-53 |p| of loom's fp64 value P
+                // (three roundings here, two there); if p - t and p + t, t =
+                // |p| 2^-50, round to the same float, so does P (fp64 and
+                // fp32 rounding are monotone) and that float is the result.
+                // A thread with a value whose bracket holds an fp32 rounding
+                // boundary (or is NaN) redoes its values with the divisions.
+                double y[MR];
+#pragma unroll
+                for (int rr = 0; rr < MR; ++rr) y[rr] = 1.0 / f[rr];
+                float4 nv[FV];
+                bool redo = false;
+                auto bracket = [&](float v, double yr, float g) {
+                    const double q = ((double)v * yr) * (double)g;
+                    const double t = fabs(q) * 0x1p-50;
+                    const float lo = (float)(q - t), hi = (float)(q + t);
+                    redo |= !(lo == hi);
+                    return lo;
+                };
+#pragma unroll
+                for (int j = 0; j < FV; ++j) {
+                    const int idx = tid + j * T;
+                    nv[j] = xv[j];
+                    if (idx < n4) {
+                        const int row = row_of<MR>(idx, row4);
+                        double yr = y[0];
+#pragma unroll
+                        for (int rr = 1; rr < MR; ++rr)
+                            if (rr == row) yr = y[rr];
+                        nv[j] = make_float4(bracket(xv[j].x, yr, gv[j].x), bracket(xv[j].y, yr, gv[j].y),
+                                            bracket(xv[j].z, yr, gv[j].z), bracket(xv[j].w, yr, gv[j].w));
+                    }
+                }
+                if (redo) {
+#pragma unroll
+                    for (int j = 0; j < FV; ++j) {
+                        const int idx = tid + j * T;
+                        if (idx < n4) {
+                            const int row = row_of<MR>(idx, row4);
+                            double fr = f[0];
+#pragma unroll
+                            for (int rr = 1; rr < MR; ++rr)
+                                if (rr == row) fr = f[rr];
+                            nv[j].x = (float)(((double)xv[j].x / fr) * (double)gv[j].x);
+                            nv[j].y = (float)(((double)xv[j].y / fr) * (double)gv[j].y);
+                            nv[j].z = (float)(((double)xv[j].z / fr) * (double)gv[j].z);
+                            nv[j].w = (float)(((double)xv[j].w / fr) * (double)gv[j].w);
+                        }
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < FV; ++j) xv[j] = nv[j];
+            }
 #pragma unroll
             for (int j = 0; j < FV; ++j) {
                 const int idx = tid + j * T;
-                if (idx < n4) {
+                if (NORM != NORM_RMS && idx < n4) {
                     const int row = row_of<MR>(idx, row4);
                     double fr = f[0];
 #pragma unroll
                     for (int rr = 1; rr < MR; ++rr)
                         if (rr == row) fr = f[rr];
                     const double g0 = gv[j].x, g1 = gv[j].y, g2 = gv[j].z, g3 = gv[j].w;
-                    if (NORM == NORM_RMS) {
-                        xv[j].x = (float)(((double)xv[j].x / fr) * g0);
-                        xv[j].y = (float)(((double)xv[j].y / fr) * g1);
-                        xv[j].z = (float)(((double)xv[j].z / fr) * g2);
-                        xv[j].w = (float)(((double)xv[j].w / fr) * g3);
-                    } else if (NORM == NORM_INNER_F32) {
+                    if (NORM == NORM_INNER_F32) {
                         xv[j].x = (float)((double)xv[j].x * fr * g0);
                         xv[j].y = (float)((double)xv[j].y * fr * g1);
                         xv[j].z = (float)((double)xv[j].z * fr * g2);
@@ -1330,6 +1390,9 @@ static hipError_t launch_norm_fv(const MatArgs& p, size_t shm, hipStream_t s) {
     const size_t groups = (size_t)p.e.m * (p.k / 4);
     if (p.ntiles > 256 && groups <= 4 * 256) {
         if (groups <= 2 * 256) return launch_norm_t<NMAT, NORM, STRICT, 4, 2>(p, shm, s);
+        // (three slots a thread where they hold the row: the BitNet-2B
+        // RMSNorm2 -> gate|up step 7.98 -> 7.68 us fast, 13.90 -> 13.37 strict)
+        if (groups <= 3 * 256) return launch_norm_t<NMAT, NORM, STRICT, 4, 3>(p, shm, s);
         return launch_norm_t<NMAT, NORM, STRICT, 4, 4>(p, shm, s);
     }
     if (groups <= 2 * kNormThreads) return launch_norm_t<NMAT, NORM, STRICT, kNormWaves, 2>(p, shm, s);

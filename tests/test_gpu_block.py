@@ -556,6 +556,44 @@ def test_block_decode_norm_fused_and_staged(orc, torch_dev, tf, shape, norm, tun
     staged.release()
 
 
+@pytest.mark.parametrize("norm", ["strict", "fast"])
+def test_decode_rmsnorm_rounding_tie(orc, torch_dev, tf, norm):
+    # The norm-fused decode matmul forms loom's float32((v / rms) * gain) from
+    # one reciprocal per row and takes the divisions for any value within
+    # 2^-50 (relative) of an fp32 rounding boundary.  This row makes rms
+    # exactly 1 (127 ones, two values 1 + 2^-12, zeros: every partial sum of
+    # squares is exact in any order, and eps tops the mean up to 1), so v =
+    # 1 + 2^-12 with gain 1 + 2^-12 gives 1 + 2^-11 + 2^-24, a tie (to even:
+    # 1 + 2^-11), while gain 1 + 2^-11 gives a product that is an fp32 value.
+    torch = torch_dev
+    sh = SMALL
+    w = Weights(orc, sh, seed=1401, act=ACT_SILU)
+    e = np.float32(1.0 + 2.0 ** -12)
+    w.n1 = np.ones(sh.hidden, np.float32)
+    w.n1[5] = e
+    w.n1[77] = np.float32(1.0 + 2.0 ** -11)
+    x = np.zeros((1, sh.hidden), np.float32)
+    x[0, 128:255] = 1.0
+    x[0, 5] = e
+    x[0, 77] = e
+    tot = 127.0 + 2 * float(e) ** 2
+    eps = 1.0 - tot / sh.hidden
+    assert tot / sh.hidden + eps == 1.0
+    cfg = tf.BlockConfig(sh.hidden, sh.heads, sh.kv, sh.hd, sh.inter, max_seq_len=sh.msl, max_batch=1,
+                         rope_theta=sh.theta, norm_eps=eps, attn_eps=1e-5, ffn_eps=1e-5,
+                         ffn_activation=ACT_SILU, norm=norm)
+    blk = tf.BitNetBlock(cfg, w.gpu(tf))
+    _, t = blk.forward(to_dev(torch, x), taps=True)
+    torch.cuda.synchronize()
+    T = t.numpy()
+    want = orc.rmsnorm_forward(x, w.n1, eps)
+    assert want[0, 5] == np.float32(1.0 + 2.0 ** -11)
+    assert T["y1"].tobytes() == want.tobytes()
+    q_ref, a_ref = orc.quant_rows(T["y1"])
+    assert np.array_equal(T["xq1"], q_ref) and T["amax1"].tobytes() == a_ref.tobytes()
+    blk.release()
+
+
 @pytest.mark.parametrize("norm,seq", [("fast", 300), ("fast", 1100), ("strict", 1100)])
 def test_prefill_row_norms_one_wave_equal_workgroup(orc, torch_dev, tf, tuning, norm, seq):
     # The prefill row norms (RMSNorm1 and 2, the MHA fp64 inner norm, the
