@@ -49,7 +49,8 @@ int loom_amd_device_count(void);
 
 /* Kernel family the matmul dispatcher uses for m token rows
  * ("skinny_m16_fusedq" -- quantization fused into the matmul launch when the
- * fp32 rows allow it --, "skinny_m16", "skinny_m32", "skinny_m64", "gemm"). */
+ * fp32 rows allow it: m <= 4, or m <= 8 with k <= 4096 --, "skinny_m16",
+ * "skinny_m32", "skinny_m64", "gemm_m64", "gemm"). */
 const char* loom_amd_kernel_variant(int m);
 
 /* ---- weights --------------------------------------------------------- */
@@ -167,7 +168,8 @@ int loom_amd_dense_forward(const loom_amd_matrix* w, const float* x, int m, int 
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Quantized
  * rows are staged in a fixed 8 MiB device array per GPU instead of the
  * growable scratch arena: m * (256*ceil(k/256) + 8) plus alignment must fit
- * 8 MiB (larger calls fail with a message; four rows or fewer need no staging).
+ * 8 MiB (larger calls fail with a message; rows the matmul quantizes itself,
+ * up to four, or eight for k <= 4096, need no staging).
  * Every call on one GPU shares that array: calls overlapping on one GPU race
  * and must be serialized by the caller.  Like every direct loom_amd_* call,
  * it also shares the GPU's split-K partial sums and arrival counters with

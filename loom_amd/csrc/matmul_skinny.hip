@@ -19,6 +19,9 @@ bool stream_ok(int m, int k, int n_tiles, bool fused, const Epilogue& epi);
 hipError_t launch_stream(const MatArgs& p, bool fuseq, hipStream_t s);
 
 constexpr int kFusedMaxRows = 4;
+// 4 < M <= kFusedWaveRows fp32 rows fuse their quantization too, one row per
+// wave (MR = kFusedWaveRows selects that prologue).
+constexpr int kFusedWaveRows = 8;
 // strict norm rows this long form their sum on eight waves (fewer terms per lane)
 constexpr int kSumWideCols = 4096;
 constexpr int kFusedVec = 16;  // float4 per thread in the fused prologue (max)
@@ -51,8 +54,10 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
     constexpr int U = 4 / MSUB;  // K tiles per batch per wave
     extern __shared__ __align__(16) int8_t xq_s[];  // FUSEQ: M rows x ldq (STRICT: k squares first)
     __shared__ int red[NTR][NMAT][MSUB * 16][16];
-    __shared__ unsigned amax_bits[kFusedMaxRows];
-    __shared__ int xsum_s[kFusedMaxRows];
+    constexpr bool RPW = FUSEQ && MR > kFusedMaxRows;  // one row per wave
+    static_assert(!RPW || (NORM == NORM_NONE && MR <= WAVES && MSUB == 1), "row-per-wave prologue");
+    __shared__ unsigned amax_bits[MR > kFusedMaxRows ? MR : kFusedMaxRows];
+    __shared__ int xsum_s[MR > kFusedMaxRows ? MR : kFusedMaxRows];
     __shared__ double nsum[NORM != NORM_NONE ? WAVES : 1][kFusedMaxRows];
     __shared__ float wmax[FUSEQ ? WAVES : 1][kFusedMaxRows];
     __shared__ unsigned wmaxb[FUSEQ ? WAVES : 1][kFusedMaxRows];
@@ -91,11 +96,12 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
         // BitNet-2B down shape, M = 1: 4.95 -> 4.17 us per Dense step; with
         // four waves, or with a norm fused, issuing every slot measured
         // faster).
-        constexpr bool kSkipIdle = NORM == NORM_NONE && WAVES >= 8;
+        constexpr bool kSkipIdle = !RPW && NORM == NORM_NONE && WAVES >= 8;
 #pragma unroll
         for (int j = 0; j < FV; ++j) {
-            const int idx = tid + j * T;
-            const bool ok = idx < n4;
+            // (one row per wave: lane l takes element groups l + 64 j of row `wave`)
+            const int idx = RPW ? wave * row4 + lane + 64 * j : tid + j * T;
+            const bool ok = RPW ? wave < M && lane + 64 * j < row4 : idx < n4;
             if (kSkipIdle && j > 0 && __builtin_amdgcn_readfirstlane(wave) * 64 + j * T >= n4) {
                 xv[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 continue;
@@ -160,7 +166,99 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
     }
 
     for (int i = tid; i < NTR * NMAT * MSUB * 16 * 16; i += T) (&red[0][0][0][0])[i] = 0;
-    if (FUSEQ) {
+    if constexpr (RPW) {
+        // One row per wave: the row's amax, rounding and sum(xq) are the
+        // wave's alone (DPP reductions, no exchange), so the prologue's only
+        // workgroup barrier is the last one, before the MFMAs read the LDS
+        // copy.  Rounding as below: the largest |x| bit pattern flags a row
+        // holding NaN or infinity (loom's NaN-skipping maximum and per-value
+        // fp64 rounding for it); finite rows round in fp32 with one exactness
+        // test per slot of four values, redoing only the undecided slots.
+        if (wave < M) {  // uniform
+            const int r = wave;
+            unsigned lb = 0u;
+#pragma unroll
+            for (int j = 0; j < FV; ++j) {
+                if (lane + 64 * j < row4) {
+                    lb = max(lb, max(max(__float_as_uint(xv[j].x) & 0x7fffffffu, __float_as_uint(xv[j].y) & 0x7fffffffu),
+                                     max(__float_as_uint(xv[j].z) & 0x7fffffffu, __float_as_uint(xv[j].w) & 0x7fffffffu)));
+                }
+            }
+            unsigned amb = wave_umax_dpp(lb);
+            const bool gen = amb > 0x7f7fffffu;  // (wave-uniform)
+            if (gen) {
+                float lm = 0.0f;
+#pragma unroll
+                for (int j = 0; j < FV; ++j) {
+                    if (lane + 64 * j < row4) {
+                        float a = max_nan_skip(0.0f, fabsf(xv[j].x));
+                        a = max_nan_skip(a, fabsf(xv[j].y));
+                        a = max_nan_skip(a, fabsf(xv[j].z));
+                        a = max_nan_skip(a, fabsf(xv[j].w));
+                        lm = max_nan_skip(lm, a);
+                    }
+                }
+                amb = __float_as_uint(wave_max_dpp(lm));
+            }
+            if (lane == 0) amax_bits[r] = amb;  // read after the main loop
+            float am = __uint_as_float(amb);
+            if (am < 1e-5f) am = 1e-5f;
+            uint32_t pk[FV];
+            bool undecided[FV];  // slot j holds a value the fp32 test leaves to fp64
+            bool any = gen;
+#pragma unroll
+            for (int j = 0; j < FV; ++j) {
+                pk[j] = 0u;
+                undecided[j] = gen;
+            }
+            if (!gen) {
+                const float sf = 127.0f / am;  // (fp32 division, correctly rounded)
+#pragma unroll
+                for (int j = 0; j < FV; ++j) {
+                    if (lane + 64 * j < row4) {
+                        const float p0 = xv[j].x * sf, p1 = xv[j].y * sf, p2 = xv[j].z * sf, p3 = xv[j].w * sf;
+                        const float r0 = rintf(p0), r1 = rintf(p1), r2 = rintf(p2), r3 = rintf(p3);
+                        const float d = fmaxf(fmaxf(fabsf(p0 - r0), fabsf(p1 - r1)), fmaxf(fabsf(p2 - r2), fabsf(p3 - r3)));
+                        undecided[j] = !(0.5f - d > 3.1e-5f);
+                        any |= undecided[j];
+                        pk[j] = pack4((int)r0, (int)r1, (int)r2, (int)r3);
+                    }
+                }
+            }
+            if (any) {  // (per lane) loom's fp64 rounding for the undecided slots
+                const double s = 127.0 / (double)am;
+                const float s32 = (float)s;
+#pragma unroll
+                for (int j = 0; j < FV; ++j) {
+                    if (undecided[j] && lane + 64 * j < row4)
+                        pk[j] = pack4(quant_f32(xv[j].x, s32, s), quant_f32(xv[j].y, s32, s),
+                                      quant_f32(xv[j].z, s32, s), quant_f32(xv[j].w, s32, s));
+                }
+            }
+            int8_t* qr = xq_s + r * p.ldq;
+            int ls = 0;
+#pragma unroll
+            for (int j = 0; j < FV; ++j) {
+                if (lane + 64 * j < row4) {
+                    *(uint32_t*)(qr + 4 * (lane + 64 * j)) = pk[j];
+                    ls = byte_sum_i8(pk[j], ls);
+                }
+            }
+            for (int c = k + 4 * lane; c < p.ldq; c += 256) *(uint32_t*)(qr + c) = 0u;  // padding
+            const int v = wave_sum_i_dpp(ls);
+            if (lane == 0) xsum_s[r] = v;  // read after the main loop
+        }
+        __syncthreads();
+        if (blockIdx.x == 0) {
+            if (p.xq_tap) {
+                for (int i = tid; i < M * k; i += T) p.xq_tap[i] = xq_s[(i / k) * p.ldq + (i % k)];
+            }
+            if (p.amax_tap && tid < M) {
+                float am = __uint_as_float(amax_bits[tid]);
+                p.amax_tap[tid] = am < 1e-5f ? 1e-5f : am;
+            }
+        }
+    } else if (FUSEQ) {
         if (NORM != NORM_NONE) {
             // ---- sum of squares per row -----------------------------------
             double tot[MR];
@@ -472,7 +570,9 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
                 // thread's values iff it holds for the largest |p - r|
                 // (fl(0.5f - d) does not increase with d): one test per thread
                 // instead of a branch per value, and a thread with a value
-                // nearer a boundary redoes its values with quant_f32.
+                // nearer a boundary redoes its values with quant_f32 (up to
+                // four rows of 640 or fewer float4 a thread: a near-tie in a
+                // thread is rare enough that tracking slots cost more).
                 float dmax = 0.0f;
                 uint32_t pk[FV];
 #pragma unroll
@@ -1142,10 +1242,39 @@ static void launch_fused_w(const MatArgs& p, size_t shm, hipStream_t s) {
     }
 }
 
+// 4 < M <= kFusedWaveRows fused rows: eight waves, one row each, the row's
+// element groups in FV slots a lane (10 for K <= 2560, 16 for K <= 4096); two
+// weight tiles per workgroup (one matrix) while the paired grid still spans
+// half the CUs, as for one row (BitNet-2B up shape, M = 8: 6.0 us per Dense
+// step; one tile 7.5, four 7.5; the separate quantization launch took 8.0).
+// LOOM_AMD_FUSED_NTR = 1 or 2 overrides.
+template <int NMAT, int FV>
+static void launch_fused_rows_fv(const MatArgs& p, size_t shm, hipStream_t s) {
+    const int ntr = NMAT == 1 ? tune_int("LOOM_AMD_FUSED_NTR", ceil_div(p.ntiles, 2) >= 128 ? 2 : 1) : 1;
+    if (NMAT == 1 && ntr == 2) {
+        hipLaunchKernelGGL((skinny_kernel<NMAT, 1, 8, true, NORM_NONE, 0, FV, kFusedWaveRows, 2>),
+                           dim3(ceil_div(p.ntiles, 2)), dim3(512), shm, s, p);
+    } else {
+        hipLaunchKernelGGL((skinny_kernel<NMAT, 1, 8, true, NORM_NONE, 0, FV, kFusedWaveRows, 1>),
+                           dim3(p.ntiles), dim3(512), shm, s, p);
+    }
+}
+
 template <int NMAT, int MSUB, bool FUSEQ>
 static hipError_t launch_skinny(const MatArgs& p, hipStream_t s) {
     // 1024-thread workgroups leave 128 VGPRs per lane: only the one-matrix kernels fit.
     constexpr int kCap = NMAT == 1 ? 16 : 8;
+    if constexpr (FUSEQ) {
+        if (p.e.m > kFusedMaxRows) {  // one row per wave (fused_quant_ok: K <= 4096)
+            const size_t shm = (size_t)p.e.m * p.ldq;
+            if (p.k / 4 <= 10 * 64) {
+                launch_fused_rows_fv<NMAT, 10>(p, shm, s);
+            } else {
+                launch_fused_rows_fv<NMAT, 16>(p, shm, s);
+            }
+            return hipGetLastError();
+        }
+    }
     int w = pick_waves(p.ntiles, p.ktiles, kCap);
     if (FUSEQ) {
         // the fused prologue holds M*K/4 float4 over kFusedVec registers per thread
@@ -1292,7 +1421,7 @@ static hipError_t launch_small_m(const MatArgs& p, int device, hipStream_t s) {
 }
 
 const char* kernel_variant(int m) {
-    if (m <= kFusedMaxRows) return "skinny_m16_fusedq";
+    if (m <= kFusedWaveRows) return "skinny_m16_fusedq";  // (K <= 4096 from M = 5 on)
     if (m <= 16) return "skinny_m16";
     if (m <= 32) return "skinny_m32";
     if (m <= 56) return "skinny_m64";  // (the GEMM when K exceeds 16 K tiles)
@@ -1344,8 +1473,11 @@ hipError_t launch_matmul(const Matrix* w0, const Matrix* w1, const QuantAct& a, 
 // The fused prologue holds the M x K rows in registers (kFusedVec float4 per
 // thread of a 512-thread workgroup) and their int8 copy in LDS.
 bool fused_quant_ok(int m, int k, const float* x) {
-    return m >= 1 && m <= kFusedMaxRows && k % 4 == 0 && ((uintptr_t)x & 15) == 0 &&
-           (size_t)m * k <= (size_t)4 * kFusedVec * 512 && pad_cols(k) * (size_t)m <= 64 * 1024;
+    if (m < 1 || k % 4 != 0 || ((uintptr_t)x & 15) != 0) return false;
+    if (m <= kFusedMaxRows)
+        return (size_t)m * k <= (size_t)4 * kFusedVec * 512 && pad_cols(k) * (size_t)m <= 64 * 1024;
+    // one row per wave: a row in at most 16 float4 slots of a wave's lanes
+    return m <= kFusedWaveRows && k <= 16 * 64 * 4 && pad_cols(k) * (size_t)m <= 64 * 1024;
 }
 
 // ---- norm-fused decode matmuls ------------------------------------------------

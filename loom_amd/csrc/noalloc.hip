@@ -4,7 +4,8 @@
 // hipMalloc).  It has no counterpart in loom.
 //
 // Where loom_amd_dense_forward stages the quantized rows (int8 rows, amax,
-// sum(xq)) of more than four token rows in the per-device scratch arena,
+// sum(xq)) of token rows the matmul launch does not quantize itself (more
+// than four, or than eight for K <= 4096) in the per-device scratch arena,
 // which grows with hipMalloc, this entry point stages them in `scratch`, a
 // fixed device array of kNoAllocScratchBytes that every GPU the library runs
 // on holds until the process ends.  Its device address is looked up once per

@@ -90,7 +90,9 @@ def test_amd_extension_errors_without_gpu(amd_lib):
     assert amd_lib.loom_amd_matrix_create(0, words, 4, 1, 64, 4, 1.0, C.byref(out)) == -1
     assert b"not visible" in amd_lib.loom_amd_last_error()
     assert amd_lib.loom_amd_kernel_variant(1) == b"skinny_m16_fusedq"
-    assert amd_lib.loom_amd_kernel_variant(5) == b"skinny_m16"
+    assert amd_lib.loom_amd_kernel_variant(5) == b"skinny_m16_fusedq"
+    assert amd_lib.loom_amd_kernel_variant(8) == b"skinny_m16_fusedq"
+    assert amd_lib.loom_amd_kernel_variant(9) == b"skinny_m16"
     assert amd_lib.loom_amd_kernel_variant(56) == b"skinny_m64"
     assert amd_lib.loom_amd_kernel_variant(64) == b"gemm_m64"
     assert amd_lib.loom_amd_kernel_variant(65) == b"gemm"

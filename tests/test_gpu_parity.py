@@ -217,11 +217,12 @@ def test_dense_batch_edges(orc, torch_dev, bn, M):
     _check_dense(orc, torch_dev, bn, m, x)
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
 def test_dense_fused_quant_edge_rows(orc, torch_dev, bn, M):
-    # M <= 4 with K % 4 == 0 quantizes inside the matmul launch: the same
-    # loom edge semantics as the standalone quantizer (zero row -> 1e-5 floor,
-    # NaN ignored by amax and quantized to -128, inf amax -> scale 0).
+    # M <= 8 with K % 4 == 0 (K <= 4096 from M = 5 on, one row per wave)
+    # quantizes inside the matmul launch: the same loom edge semantics as the
+    # standalone quantizer (zero row -> 1e-5 floor, NaN ignored by amax and
+    # quantized to -128, inf amax -> scale 0).
     assert bn._lib.lib().loom_amd_kernel_variant(M) == b"skinny_m16_fusedq"
     k = 2560
     m = orc.random_matrix(96, k, seed=12)
@@ -246,7 +247,7 @@ def test_dense_fused_quant_edge_rows(orc, torch_dev, bn, M):
         assert pre.cpu().numpy().tobytes() == ref.pre.tobytes()
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
 def test_dense_fused_quant_rounding_ties(orc, torch_dev, bn, M):
     # The fused prologue rounds in fp32 and takes loom's fp64 rounding for any
     # thread holding a product within 3.1e-5 of a boundary j + 1/2.  With a
@@ -447,7 +448,7 @@ def test_swiglu_biases_bitnet_2b_shape(orc, torch_dev, bn, M):
                  with_norm_w=True, with_bias=True)
 
 
-@pytest.mark.parametrize("M", [1, 64, 256])
+@pytest.mark.parametrize("M", [1, 8, 64, 256])
 def test_swiglu_bitnet_2b_shape(orc, torch_dev, bn, M):
     hg, ref = _swiglu_case(orc, torch_dev, bn, hidden=2560, inter=6912, M=M, seed=1234 + M,
                            norm="strict", with_norm_w=True)
