@@ -196,7 +196,8 @@ const char* const kTuneNames[] = {
     "LOOM_AMD_GEMM_TILE",   "LOOM_AMD_GEMM_SPLIT",   "LOOM_AMD_GEMM_GROUP",   "LOOM_AMD_SMALLM",
     "LOOM_AMD_SKINNY_NT",   "LOOM_AMD_SKINNY_NTR",   "LOOM_AMD_FUSED_NTR",    "LOOM_AMD_FUSED_WAVES",
     "LOOM_AMD_GEMV_STREAM", "LOOM_AMD_STREAM_WAVES", "LOOM_AMD_STREAM_DEPTH", "LOOM_AMD_ATTN_QT",
-    "LOOM_AMD_UNFUSED_ROPE", "LOOM_AMD_UNFUSED_NORM", "LOOM_AMD_GEMM_NJ", "LOOM_AMD_ROWNORM_WAVE"};
+    "LOOM_AMD_UNFUSED_ROPE", "LOOM_AMD_UNFUSED_NORM", "LOOM_AMD_GEMM_NJ", "LOOM_AMD_ROWNORM_WAVE",
+    "LOOM_AMD_QUANT_GROUPS"};
 constexpr int kTuneCount = (int)(sizeof(kTuneNames) / sizeof(kTuneNames[0]));
 
 struct TuneSnapshot {

@@ -148,11 +148,134 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const T* __restrict__ x,
     }
 }
 
+// fp32 rows, 16-byte groups: thread t holds element groups t + 256 j (G4 a
+// thread, k <= 1024 G4), 16-byte loads and one 32-bit store of four codes.
+// The maximum is taken on |x| bit patterns (unsigned order is value order for
+// non-negative floats, and NaN sorts above infinity, so it also flags a row
+// holding NaN or infinity: such a row takes loom's NaN-skipping maximum and
+// per-value rounding).  Finite rows round in fp32 with sf = fl32(127 / m),
+// within 2^-24 + 2^-53 of loom's fp64 scale, so a value's fp32 product is
+// within 127 (2^-23 + 2^-47) < 1.52e-5 of loom's fp64 one: one test
+// 0.5f - |p - r| > 3.1e-5f per group of four (on their largest |p - r|)
+// decides them, and only the undecided groups take quant_f32.  |x| <= m, so
+// |p| < 127.5 and rintf needs no clamp.
+template <int G4>
+__global__ __launch_bounds__(256) void act_quant_rows_kernel(const float* __restrict__ x, int ldx, int k,
+                                                             int ldq, int8_t* __restrict__ xq,
+                                                             float* __restrict__ amax_out,
+                                                             int32_t* __restrict__ xsum_out) {
+    __shared__ unsigned shu[4];
+    __shared__ float shf[4];
+    __shared__ int shi[4];
+    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int k4 = k >> 2;
+    const float4* xr = (const float4*)(x + (size_t)row * ldx);
+    float4 v[G4];
+#pragma unroll
+    for (int j = 0; j < G4; ++j) {
+        const int g = tid + 256 * j;
+        v[j] = g < k4 ? xr[g] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    unsigned lb = 0u;
+#pragma unroll
+    for (int j = 0; j < G4; ++j)
+        lb = max(lb, max(max(__float_as_uint(v[j].x) & 0x7fffffffu, __float_as_uint(v[j].y) & 0x7fffffffu),
+                         max(__float_as_uint(v[j].z) & 0x7fffffffu, __float_as_uint(v[j].w) & 0x7fffffffu)));
+    lb = wave_umax_dpp(lb);
+    if (lane == 0) shu[wave] = lb;
+    __syncthreads();
+    unsigned mb = max(max(shu[0], shu[1]), max(shu[2], shu[3]));
+    const bool gen = mb > 0x7f7fffffu;  // NaN or infinity in the row (uniform)
+    float m = __uint_as_float(mb);
+    if (gen) {
+        float lm = 0.0f;
+#pragma unroll
+        for (int j = 0; j < G4; ++j) {
+            lm = max_nan_skip(lm, fabsf(v[j].x));
+            lm = max_nan_skip(lm, fabsf(v[j].y));
+            lm = max_nan_skip(lm, fabsf(v[j].z));
+            lm = max_nan_skip(lm, fabsf(v[j].w));
+        }
+        m = block_max(lm, shf);
+    }
+    if (m < 1e-5f) m = 1e-5f;
+    uint32_t pk[G4];
+    bool undecided[G4];
+    bool any = gen;
+#pragma unroll
+    for (int j = 0; j < G4; ++j) {
+        pk[j] = 0u;
+        undecided[j] = gen;
+    }
+    if (!gen) {
+        const float sf = 127.0f / m;  // (fp32 division, correctly rounded)
+#pragma unroll
+        for (int j = 0; j < G4; ++j) {
+            const float p0 = v[j].x * sf, p1 = v[j].y * sf, p2 = v[j].z * sf, p3 = v[j].w * sf;
+            const float r0 = rintf(p0), r1 = rintf(p1), r2 = rintf(p2), r3 = rintf(p3);
+            const float d = fmaxf(fmaxf(fabsf(p0 - r0), fabsf(p1 - r1)), fmaxf(fabsf(p2 - r2), fabsf(p3 - r3)));
+            undecided[j] = !(0.5f - d > 3.1e-5f);
+            any |= undecided[j];
+            pk[j] = pack4((int)r0, (int)r1, (int)r2, (int)r3);
+        }
+    }
+    if (any) {  // (per thread) loom's fp64 rounding for the undecided groups
+        const double scale = 127.0 / (double)m;
+        const float scale32 = (float)scale;
+#pragma unroll
+        for (int j = 0; j < G4; ++j) {
+            if (undecided[j])
+                pk[j] = pack4(quant_f32(v[j].x, scale32, scale), quant_f32(v[j].y, scale32, scale),
+                              quant_f32(v[j].z, scale32, scale), quant_f32(v[j].w, scale32, scale));
+        }
+    }
+    uint32_t* qr = (uint32_t*)(xq + (size_t)row * ldq);
+    int sum = 0;
+#pragma unroll
+    for (int j = 0; j < G4; ++j) {
+        const int g = tid + 256 * j;
+        if (g < k4) {
+            qr[g] = pk[j];
+            sum = byte_sum_i8(pk[j], sum);
+        }
+    }
+    for (int g = k4 + tid; g < (ldq >> 2); g += 256) qr[g] = 0u;  // padding columns
+    sum = block_sum_i(sum, shi);
+    if (tid == 0) {
+        amax_out[row] = m;
+        xsum_out[row] = sum;
+    }
+}
+
 template <typename T>
 static hipError_t launch_quant_t(const T* x, int ldx, int m, int k, int8_t* xq, int ldq,
                                  float* amax, int32_t* xsum, hipStream_t s) {
     if (m <= 0) return hipSuccess;
     const dim3 g(m), b(256);
+    if constexpr (sizeof(T) == 4) {
+        // 16-byte rows: the group kernel (measured against act_quant_kernel at
+        // the BitNet-2B up shape; its tiers follow the float4 slots a thread)
+        const bool v16 = k % 4 == 0 && ldx % 4 == 0 && ldq % 4 == 0 && ((uintptr_t)x & 15) == 0 &&
+                         ((uintptr_t)xq & 3) == 0;
+        if (v16 && tune_int("LOOM_AMD_QUANT_GROUPS", 1) != 0) {
+            if (k <= 1024 * 2) {
+                hipLaunchKernelGGL((act_quant_rows_kernel<2>), g, b, 0, s, x, ldx, k, ldq, xq, amax, xsum);
+                return hipGetLastError();
+            }
+            if (k <= 1024 * 3) {
+                hipLaunchKernelGGL((act_quant_rows_kernel<3>), g, b, 0, s, x, ldx, k, ldq, xq, amax, xsum);
+                return hipGetLastError();
+            }
+            if (k <= 1024 * 4) {
+                hipLaunchKernelGGL((act_quant_rows_kernel<4>), g, b, 0, s, x, ldx, k, ldq, xq, amax, xsum);
+                return hipGetLastError();
+            }
+            if (k <= 1024 * 8) {
+                hipLaunchKernelGGL((act_quant_rows_kernel<8>), g, b, 0, s, x, ldx, k, ldq, xq, amax, xsum);
+                return hipGetLastError();
+            }
+        }
+    }
     if (k <= 256 * 4) {
         hipLaunchKernelGGL((act_quant_kernel<T, 4>), g, b, 0, s, x, ldx, k, ldq, xq, amax, xsum);
     } else if (k <= 256 * 8) {

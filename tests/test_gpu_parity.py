@@ -84,6 +84,44 @@ def test_quantize_rows_bit_exact(orc, torch_dev, bn):
     assert not q.xq[:, k:].any().item() if q.xq.shape[1] > k else True
 
 
+@pytest.mark.parametrize("k", [64, 2048, 2560, 4096, 6912, 8192, 1001])
+def test_quantize_rows_group_kernel(orc, torch_dev, bn, tuning, k):
+    # fp32 rows with k % 4 == 0 take the 16-byte group quantizer (two, three,
+    # four or eight float4 a thread); LOOM_AMD_QUANT_GROUPS=0 keeps the
+    # value-per-thread kernel, which k = 1001 always takes.  Both against the
+    # oracle: normal rows, ties (amax 127: scale 1), near-ties, NaN, inf, zero.
+    torch = torch_dev
+    rows = [orc.normal_f32(k, 500 + i) for i in range(3)]
+    t = orc.normal_f32(k, 510) * np.float32(20.0)
+    t[0] = np.float32(127.0)
+    t[1 % k] = np.float32(2.5)
+    t[2 % k] = np.nextafter(np.float32(-6.5), np.float32(0.0))
+    rows.append(t)
+    r = orc.normal_f32(k, 511)
+    r[k // 2] = np.nan
+    rows.append(r)
+    r = orc.normal_f32(k, 512)
+    r[k - 1] = -np.inf
+    rows.append(r)
+    rows.append(np.zeros(k, np.float32))
+    x = np.stack(rows)
+    outs = {}
+    for mode in ("groups", "values"):
+        tuning("LOOM_AMD_QUANT_GROUPS", None if mode == "groups" else "0")
+        q = bn.quantize_activation(to_dev(torch, x))
+        torch.cuda.synchronize()
+        outs[mode] = [a.cpu().numpy().tobytes() for a in (q.xq, q.amax, q.xsum)]
+        xq = q.unpadded().cpu().numpy()
+        for i, row in enumerate(rows):
+            eq, eamax = orc.quant_act(row)
+            assert np.array_equal(xq[i], eq), (mode, i)
+            assert np.float32(q.amax[i].item()).tobytes() == np.float32(eamax).tobytes(), (mode, i)
+            assert int(q.xsum[i].item()) == int(eq.astype(np.int64).sum()), (mode, i)
+        if q.xq.shape[1] > k:
+            assert not q.xq[:, k:].any().item(), mode
+    assert outs["groups"] == outs["values"]
+
+
 def test_quantize_rows_f64_bit_exact(orc, torch_dev, bn):
     torch = torch_dev
     k = 640
