@@ -594,6 +594,46 @@ def test_decode_rmsnorm_rounding_tie(orc, torch_dev, tf, norm):
     blk.release()
 
 
+@pytest.mark.parametrize("norm", ["strict", "fast"])
+@pytest.mark.parametrize("seq", [5, 1030])
+def test_prefill_rmsnorm_rounding_tie(orc, torch_dev, tf, norm, seq):
+    # The prefill RMSNorm kernels (one workgroup per row below 1024 rows, one
+    # wave per row from 1024) on loom's float32((v / rms) * gain) at an exact
+    # fp32 tie: row 0 is the tie row of the decode test (rms exactly 1), the
+    # other rows are random.
+    torch = torch_dev
+    sh = Shape(256, 4, 2, 64, 512, 1100)
+    w = Weights(orc, sh, seed=1402, act=ACT_SILU)
+    e = np.float32(1.0 + 2.0 ** -12)
+    w.n1 = orc.uniform_f32(sh.hidden, 0.5, 1.5, 1403)
+    w.n1[5] = e
+    x = orc.normal_f32(seq * sh.hidden, 1404).reshape(seq, sh.hidden)
+    x[0] = 0.0
+    x[0, 128:255] = 1.0
+    x[0, 5] = e
+    x[0, 77] = e
+    tot = 127.0 + 2 * float(e) ** 2
+    eps = 1.0 - tot / sh.hidden
+    cfg = tf.BlockConfig(sh.hidden, sh.heads, sh.kv, sh.hd, sh.inter, max_seq_len=sh.msl, max_batch=1,
+                         rope_theta=sh.theta, norm_eps=eps, attn_eps=1e-5, ffn_eps=1e-5,
+                         ffn_activation=ACT_SILU, norm=norm)
+    blk = tf.BitNetBlock(cfg, w.gpu(tf))
+    _, t = blk.forward(to_dev(torch, x), taps=True)
+    torch.cuda.synchronize()
+    T = t.numpy()
+    want = orc.rmsnorm_forward(x, w.n1, eps)
+    assert want[0, 5] == np.float32(1.0 + 2.0 ** -11)
+    y1 = T["y1"]
+    assert y1[0].tobytes() == want[0].tobytes()
+    if norm == "strict":
+        assert y1.tobytes() == want.tobytes()
+    else:
+        assert ulp_diff_f32(y1, want).max() <= 1
+    q_ref, a_ref = orc.quant_rows(y1)
+    assert np.array_equal(T["xq1"], q_ref) and T["amax1"].tobytes() == a_ref.tobytes()
+    blk.release()
+
+
 @pytest.mark.parametrize("norm,seq", [("fast", 300), ("fast", 1100), ("strict", 1100)])
 def test_prefill_row_norms_one_wave_equal_workgroup(orc, torch_dev, tf, tuning, norm, seq):
     # The prefill row norms (RMSNorm1 and 2, the MHA fp64 inner norm, the
