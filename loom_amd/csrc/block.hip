@@ -1735,7 +1735,7 @@ __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict_
             const float* kr = &ks[pl * KP + half * DH];
             const double* qq = &qs[wave][half * DH];
             double c0 = 0.0, c1 = 0.0, c2 = 0.0, c3 = 0.0;
-#pragma unroll 4
+#pragma unroll
             for (int d = 0; d < DH; d += 4) {
                 const float4 k4 = *(const float4*)(kr + d);
                 c0 = fma(qq[d], (double)k4.x, c0);
@@ -1743,22 +1743,20 @@ __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict_
                 c2 = fma(qq[d + 2], (double)k4.z, c2);
                 c3 = fma(qq[d + 3], (double)k4.w, c3);
             }
+            // (DPP lane moves instead of LDS-crossbar shuffles: the pair
+            // exchange is quad_perm 1,0,3,2; the maximum and expSum the fixed
+            // row_shr / row_bcast pattern, lane 63 holding the result)
             const double part = (c0 + c1) + (c2 + c3);
-            const double oth = __shfl_xor(part, 1, 64);
+            const double oth = dpp_d<kDppQuadSwap1>(part, 0.0);
             const double dot = half ? oth + part : part + oth;
             const double scv = dot * inv_sqrt;
             const bool valid = pl < n;
             double m = valid ? (scv > -1e9 ? scv : -1e9) : -1e9;  // NaN never wins
-            for (int off = 32; off > 0; off >>= 1) {
-                const double t = __shfl_xor(m, off, 64);
-                m = t > m ? t : m;
-            }
+            m = wave_max_f64_dpp(m);
             mc = m;
             const double pr = valid ? exp(scv - mc) : 0.0;
             if (half == 0) ps[wave][pl] = pr;
-            double e = half == 0 ? pr : 0.0;
-            for (int off = 32; off > 0; off >>= 1) e = e + __shfl_down(e, off, 64);
-            es = __shfl(e, 0, 64);
+            es = wave_sum_f64_dpp(half == 0 ? pr : 0.0);
         }
         __syncthreads();
         if (act) {
@@ -1823,10 +1821,7 @@ __global__ __launch_bounds__(256) void attn_combine32_kernel(const int* __restri
         const double v = sc.cmax[rh * nchunk + c];
         M = v > M ? v : M;
     }
-    for (int off = 32; off > 0; off >>= 1) {
-        const double t = __shfl_xor(M, off, 64);
-        M = t > M ? t : M;
-    }
+    M = wave_max_f64_dpp(M);
     if (lane == 0) wm[wave] = M;
     __syncthreads();
     M = wm[0];
@@ -1861,13 +1856,16 @@ __global__ __launch_bounds__(256) void attn_combine32_kernel(const int* __restri
             }
         }
     }
-    // fixed tree over the 8 threads of the dim (consecutive lanes)
-#pragma unroll
-    for (int off = 1; off < 8; off <<= 1) {
-        t = t + __shfl_down(t, off, 64);
-        e = e + __shfl_down(e, off, 64);
-    }
-    if (j == 0) {
+    // fixed tree over the 8 threads of the dim (consecutive lanes), as DPP
+    // row shifts: lane j = 7 ends with ((t7+t6)+(t5+t4))+((t3+t2)+(t1+t0)),
+    // the bits of ((t0+t1)+(t2+t3))+((t4+t5)+(t6+t7)) (every node commutes)
+    t = t + dpp_d<kDppShr1>(t, 0.0);
+    e = e + dpp_d<kDppShr1>(e, 0.0);
+    t = t + dpp_d<kDppShr2>(t, 0.0);
+    e = e + dpp_d<kDppShr2>(e, 0.0);
+    t = t + dpp_d<kDppShr4>(t, 0.0);
+    e = e + dpp_d<kDppShr4>(e, 0.0);
+    if (j == 7) {
         double* orow = out + (size_t)row * heads * HD + (size_t)h * HD;
         orow[d] = Lt > span ? __builtin_nan("") : t / e;
     }

@@ -194,6 +194,7 @@ __device__ __forceinline__ double dpp_d(double v, double identity) {
 }
 constexpr int kDppShr1 = 0x111, kDppShr2 = 0x112, kDppShr4 = 0x114, kDppShr8 = 0x118;
 constexpr int kDppBcast15 = 0x142, kDppBcast31 = 0x143;
+constexpr int kDppQuadSwap1 = 0xB1;  // quad_perm 1,0,3,2: the value of lane ^ 1
 
 __device__ __forceinline__ double readlane63_d(double v) {
     const long long b = __double_as_longlong(v);
@@ -210,6 +211,24 @@ __device__ __forceinline__ double wave_sum_f64_dpp(double v) {
     v = v + dpp_d<kDppShr8>(v, 0.0);
     v = v + dpp_d<kDppBcast15>(v, 0.0);
     v = v + dpp_d<kDppBcast31>(v, 0.0);
+    return readlane63_d(v);
+}
+
+// maximum over the wave of values compared with `>` (NaN never replaces the
+// running maximum; lanes without a source compare against -1e9), broadcast
+__device__ __forceinline__ double wave_max_f64_dpp(double v) {
+#define LAMD_MAXD_STEP(C)                         \
+    {                                             \
+        const double o = dpp_d<C>(v, -1e9);       \
+        v = o > v ? o : v;                        \
+    }
+    LAMD_MAXD_STEP(kDppShr1)
+    LAMD_MAXD_STEP(kDppShr2)
+    LAMD_MAXD_STEP(kDppShr4)
+    LAMD_MAXD_STEP(kDppShr8)
+    LAMD_MAXD_STEP(kDppBcast15)
+    LAMD_MAXD_STEP(kDppBcast31)
+#undef LAMD_MAXD_STEP
     return readlane63_d(v);
 }
 
