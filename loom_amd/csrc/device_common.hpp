@@ -165,17 +165,6 @@ __device__ __forceinline__ int byte_sum_i8(uint32_t w, int acc) {
 // loom's "a > maxAbs" update: NaN never replaces the running maximum.
 __device__ __forceinline__ float max_nan_skip(float m, float a) { return a > m ? a : m; }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = max_nan_skip(v, __shfl_xor(v, off, 64));
-    return v;
-}
-
-__device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
 
 // DPP wave reductions (full-rate VALU lane moves instead of LDS-crossbar
 // shuffles).  The pattern is fixed: row_shr 1, 2, 4, 8 inside each 16-lane
@@ -259,6 +248,11 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
 #undef LAMD_MAX_STEP
     return __int_as_float(__builtin_amdgcn_readlane(b, 63));
 }
+
+// Wave maximum of non-negative floats (NaN never wins) and wave integer sum,
+// broadcast to every lane (order-free: the DPP forms above).
+__device__ __forceinline__ float wave_max(float v) { return wave_max_dpp(v); }
+__device__ __forceinline__ int wave_sum_i(int v) { return wave_sum_i_dpp(v); }
 
 // unsigned maximum over the wave (lanes shifted in from outside a row read 0)
 __device__ __forceinline__ unsigned wave_umax_dpp(unsigned v) {

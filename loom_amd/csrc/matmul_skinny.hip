@@ -33,14 +33,6 @@ __device__ __forceinline__ int row_of(int idx, int row4) {
     return (idx >= row4) + (idx >= 2 * row4) + (idx >= 3 * row4);
 }
 
-// Fixed-order wave sum: lane 0 gets ((v0+v32)+(v16..))... the same tree in
-// every workgroup.
-__device__ __forceinline__ double wave_sum_f64_lane0(double v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = v + __shfl_down(v, off, 64);
-    return v;
-}
-
 // NORM: RowNorm applied before the quantization (FUSEQ only).  STRICT sums
 // the squares of the (single) row in element order on one lane, from LDS.
 // FV: element groups (4 values) per thread.  NTR: adjacent 16-row weight
