@@ -1558,7 +1558,13 @@ __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict_
     constexpr int DP = HD / 64;  // output dims per lane
     constexpr int KP = HD + 4;   // padded LDS row (floats)
     constexpr int PR4 = HD / 4;
-    __shared__ __align__(16) float ks[CH * KP];
+    // K rows: the two dimension halves a position's lane pair reads start 32
+    // banks apart (half offset KHO = 32 mod 64 words) and rows 4 banks apart
+    // (KPK = 4 mod 64), so the 16 lanes of one 128-bit LDS read pass (eight
+    // positions, both halves) hit 64 distinct banks
+    constexpr int KHO = (HD / 2) % 64 == 0 ? HD / 2 + 32 : HD / 2;
+    constexpr int KPK = ((KHO + HD / 2 + 63) / 64) * 64 + 4;
+    __shared__ __align__(16) float ks[CH * KPK];
     __shared__ __align__(16) float vs[CH * KP];
     __shared__ double qs[4][HD];
     __shared__ double ps[4][CH];
@@ -1632,7 +1638,7 @@ __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict_
     for (int j = 0; j < NKV; ++j) {
         const int i = tid + j * 256;
         const int r = i / PR4, c4 = (i % PR4) * 4;
-        *(float4*)&ks[r * KP + c4] = kreg[j];
+        *(float4*)&ks[r * KPK + (c4 < HD / 2 ? c4 : c4 - HD / 2 + KHO)] = kreg[j];
         *(float4*)&vs[r * KP + c4] = r >= n ? make_float4(0.0f, 0.0f, 0.0f, 0.0f) : vreg[j];
     }
     if (ROPE) {
@@ -1660,8 +1666,8 @@ __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict_
                                               HD, kvh, tid, tid + HD / 2);
                 k_pair_v(ka0, ka1, output_scale(ra.sk, am), ra.bk != nullptr, kb0, kb1, rc[tid], rsn[tid],
                          &o0, &o1, hn);
-                ks[rr * KP + tid] = o0;
-                ks[rr * KP + tid + HD / 2] = o1;
+                ks[rr * KPK + tid] = o0;
+                ks[rr * KPK + tid + KHO] = o1;
                 krow[j0] = o0;
                 krow[j1] = o1;
             }
@@ -1732,7 +1738,7 @@ __global__ __launch_bounds__(256) void attn_gqa_kernel(const double* __restrict_
         __syncthreads();
         double mc = -1e9, es = 0.0;
         if (act) {
-            const float* kr = &ks[pl * KP + half * DH];
+            const float* kr = &ks[pl * KPK + half * KHO];
             const double* qq = &qs[wave][half * DH];
             double c0 = 0.0, c1 = 0.0, c2 = 0.0, c3 = 0.0;
 #pragma unroll
