@@ -197,7 +197,7 @@ const char* const kTuneNames[] = {
     "LOOM_AMD_SKINNY_NT",   "LOOM_AMD_SKINNY_NTR",   "LOOM_AMD_FUSED_NTR",    "LOOM_AMD_FUSED_WAVES",
     "LOOM_AMD_GEMV_STREAM", "LOOM_AMD_STREAM_WAVES", "LOOM_AMD_STREAM_DEPTH", "LOOM_AMD_ATTN_QT",
     "LOOM_AMD_UNFUSED_ROPE", "LOOM_AMD_UNFUSED_NORM", "LOOM_AMD_GEMM_NJ", "LOOM_AMD_ROWNORM_WAVE",
-    "LOOM_AMD_QUANT_GROUPS"};
+    "LOOM_AMD_QUANT_GROUPS", "LOOM_AMD_LM_SCREEN"};
 constexpr int kTuneCount = (int)(sizeof(kTuneNames) / sizeof(kTuneNames[0]));
 
 struct TuneSnapshot {

@@ -2766,10 +2766,12 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __rest
 }
 
 // stage 2: combine the partials of one row and store the token
+// (lkey, when set: the screened head's threshold, cleared for the next pick)
 __global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restrict__ logits, int n,
                                                           const float2* __restrict__ part, int parts,
                                                           int* __restrict__ tokens, int cap,
-                                                          const int* __restrict__ pos0, int offset) {
+                                                          const int* __restrict__ pos0, int offset,
+                                                          unsigned long long* __restrict__ lkey) {
     const float2* pr = part + (size_t)blockIdx.x * parts;
     float best = -INFINITY;
     int idx = 0x7fffffff;
@@ -2795,6 +2797,7 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restric
         if (first != first || r == 0x7fffffff) r = 0;  // NaN at 0, or nothing comparable
         const int p = (pos0 ? *pos0 : 0) + offset;
         if (p < cap) tokens[(size_t)blockIdx.x * cap + p] = r;
+        if (lkey) *lkey = 0ull;
     }
 }
 
@@ -2807,7 +2810,269 @@ hipError_t launch_argmax(const float* logits, int n, int rows, float2* part, int
     const int chunk = ceil_div(n, parts);
     hipLaunchKernelGGL(argmax_partial_kernel, dim3(parts, rows), dim3(256), 0, s, logits, n, chunk, part);
     hipLaunchKernelGGL(argmax_final_kernel, dim3(rows), dim3(64), 0, s, logits, n, part, parts, tokens,
-                       cap, pos0, offset);
+                       cap, pos0, offset, nullptr);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------
+// Greedy token of the fp32 LM head for one row, by screening.  Greedy
+// decoding needs the argmax of the logits, not every logit.  A bf16 copy of
+// the table (each entry rounded to nearest even: |w - h| <= 2^-8 |h| + 2^-134;
+// an entry too large for bf16 becomes Inf, a NaN stays NaN) gives for every
+// vocab row v, reading half the bytes,
+//   A_v = sum_j x_j h_vj  and  S_v = sum_j |x_j| |h_vj|
+// (fp32 chains per lane, fp64 across lanes) and, with X1 = sum_j |x_j|, the
+// bound |F_v - A_v| <= B_v = k1 S_v + k2 X1 + 2^-150 on loom's logit
+// F_v = fp32(fp64 sum of x_j w_vj in its order): k1 gathers the fp32 and fp64
+// summation errors (g_p = n 2^-p / (1 - n 2^-p), n = hidden + 64), the bf16
+// rounding (2^-8) and the final rounding to fp32 (2^-24); k2 the bf16
+// rounding below the normal range.  Every row with A_v + B_v >= L, where
+// L = max_u (A_u - B_u), is a candidate: the greedy pick g is one, since
+// A_g + B_g >= F_g >= F_u >= A_u - B_u for every row u, and so is every row
+// tying with it.  So are row 0 (the greedy rule reads logit 0) and every row
+// whose A, S or bound is not finite or reaches 2^127 (its logit may be
+// non-finite or overflow; such rows also stay out of L).  The candidates'
+// logits are computed exactly as lm_head_kernel computes them, from the fp32
+// table, and the greedy pick over them is the pick over all logits.  Only
+// the candidates' logits are written; a caller that wants every logit runs
+// lm_head_kernel.  L crosses the grid as a monotone 64-bit key (device-scope
+// atomic maximum); the final pick clears it for the next call.
+// ------------------------------------------------------------------------
+
+// order-preserving key of a non-NaN double (0 is below every key: "none")
+__device__ __forceinline__ unsigned long long lm_order_key(double v) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+    return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
+}
+__device__ __forceinline__ double lm_key_value(unsigned long long k) {
+    if (k == 0ull) return -INFINITY;
+    const unsigned long long b = (k >> 63) ? (k & 0x7fffffffffffffffull) : ~k;
+    return __longlong_as_double((long long)b);
+}
+
+__global__ void bf16_round_kernel(const float* __restrict__ w, size_t n, uint16_t* __restrict__ h) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        const unsigned u = __float_as_uint(w[i]);
+        const unsigned r = (u & 0x7fffffffu) > 0x7f800000u ? (u >> 16) | 0x40u  // NaN stays NaN
+                                                           : (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+        h[i] = (uint16_t)r;
+    }
+}
+
+hipError_t launch_bf16_round(const float* w, size_t n, uint16_t* h, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    const size_t blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(bf16_round_kernel, dim3((unsigned)(blocks < 8192 ? blocks : 8192)), dim3(256), 0, s, w,
+                       n, h);
+    return hipGetLastError();
+}
+
+constexpr int kScreenMaxChunks = 6;  // 512-column chunks per row
+constexpr int kScreenMaxHidden = 2816;  // the pick's x and four staged rows within 64 KB of LDS
+constexpr int kScreenBlocks = 512;
+constexpr int kScreenRows = 1;       // rows in flight per wave (two waves per SIMD: 2 or 4 were slower)
+constexpr int kPickRows = 256;       // vocab rows per workgroup of the pick
+
+bool lm_screen_ok(int hidden) { return hidden > 0 && hidden % 8 == 0 && hidden <= kScreenMaxHidden; }
+static_assert(kScreenMaxHidden <= 512 * kScreenMaxChunks, "screening chunks cover the row");
+int lm_screen_parts(int vocab) { return ceil_div(vocab, kPickRows); }
+
+// A wave per vocab row (RU rows in flight): lane l holds x at the 16-byte
+// groups l, l + 64, ... of the row and reads the same groups of the bf16 row.
+template <int NCH, int RU>
+__global__ __launch_bounds__(256) void lm_screen_kernel(const uint4* __restrict__ hb, int vocab, int hidden,
+                                                        const float* __restrict__ x, double k1, double k2,
+                                                        double* __restrict__ hi,
+                                                        unsigned long long* __restrict__ lkey) {
+    __shared__ double wl[4];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int q8 = hidden / 8;
+    float xr[NCH][8];
+    double x1 = 0.0;
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) {
+        const int g = 64 * k + lane;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            xr[k][e] = g < q8 ? x[8 * g + e] : 0.0f;
+            x1 += fabs((double)xr[k][e]);
+        }
+    }
+    x1 = wave_sum_f64_dpp(x1);
+    const double tail = k2 * x1 + 0x1p-150;
+    double best = -INFINITY;  // largest A - B of this wave's finite rows
+    auto row_sums = [&](const uint4 (&w)[NCH], double* A, double* S) {
+        float a = 0.0f, sa = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NCH; ++k) {
+            const unsigned c[4] = {w[k].x, w[k].y, w[k].z, w[k].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float f0 = __uint_as_float(c[e] << 16), f1 = __uint_as_float(c[e] & 0xffff0000u);
+                a = fmaf(xr[k][2 * e], f0, a);
+                sa = fmaf(fabsf(xr[k][2 * e]), fabsf(f0), sa);
+                a = fmaf(xr[k][2 * e + 1], f1, a);
+                sa = fmaf(fabsf(xr[k][2 * e + 1]), fabsf(f1), sa);
+            }
+        }
+        *A = wave_sum_f64_dpp((double)a);
+        *S = wave_sum_f64_dpp((double)sa);
+    };
+    auto finish = [&](int v, double A, double S) {
+        const double B = (k1 * S + tail) * (1.0 + 0x1p-30);
+        const bool ok = fabs(A) + B < 0x1p127;  // false for NaN and Inf too
+        if (ok) best = A - B > best ? A - B : best;
+        if (lane == 0) hi[v] = ok ? A + B : INFINITY;
+    };
+    const int nw = gridDim.x * 4;
+    for (int v = blockIdx.x * 4 + wave; v < vocab; v += RU * nw) {  // wave-uniform
+        uint4 w[RU][NCH];
+#pragma unroll
+        for (int u = 0; u < RU; ++u) {
+            const uint4* r = hb + (size_t)min(v + u * nw, vocab - 1) * q8;
+#pragma unroll
+            for (int k = 0; k < NCH; ++k) {
+                const int g = 64 * k + lane;
+                w[u][k] = g < q8 ? load16_nt(r + g) : make_uint4(0u, 0u, 0u, 0u);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < RU; ++u) {
+            if (v + u * nw < vocab) {
+                double A, S;
+                row_sums(w[u], &A, &S);
+                finish(v + u * nw, A, S);
+            }
+        }
+    }
+    if (lane == 0) wl[wave] = best;
+    __syncthreads();
+    if (tid == 0) {
+        double m = wl[0];
+        for (int w = 1; w < 4; ++w) m = wl[w] > m ? wl[w] : m;
+        if (m > -INFINITY) __hip_atomic_fetch_max(lkey, lm_order_key(m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// kPickRows rows per workgroup: the candidates among them, their exact
+// logits and the workgroup's greedy pick into part[blockIdx.x].  A wave takes
+// one candidate at a time: it stages the candidate's fp32 row in its own LDS
+// region (16-byte loads, one round trip), then lanes 0-7 run the eight
+// DotTile chains (or lane 0 the sequential chain) from LDS.
+template <bool DOTTILE>
+__global__ __launch_bounds__(256) void lm_pick_kernel(const float* __restrict__ table, int vocab, int hidden,
+                                                      const float* __restrict__ x, const double* __restrict__ hi,
+                                                      const unsigned long long* __restrict__ lkey,
+                                                      float* __restrict__ logits, float2* __restrict__ part) {
+    extern __shared__ float xs[];  // x, then one row region per wave: 5 x hidden
+    __shared__ int cand[kPickRows];
+    __shared__ int ncand;
+    __shared__ double pp[4][8];
+    __shared__ float bv[256];
+    __shared__ int bi[256];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    if (tid == 0) ncand = 0;
+    const int h4 = hidden / 4;
+    for (int i = tid; i < h4; i += 256) ((float4*)xs)[i] = ((const float4*)x)[i];  // (loads with hi[v])
+    __syncthreads();
+    const double L = lm_key_value(*lkey);
+    const int v = blockIdx.x * kPickRows + tid;
+    if (v < vocab && (v == 0 || hi[v] >= L)) cand[atomicAdd(&ncand, 1)] = v;
+    __syncthreads();
+    const int nc = ncand;
+    float best = -INFINITY;
+    int bidx = 0x7fffffff;
+    if (nc > 0) {  // uniform
+        float* rw = xs + (size_t)(1 + wave) * hidden;
+        for (int ci = wave; ci < nc; ci += 4) {  // wave-uniform
+            const int vv = cand[ci];
+            const float4* src = (const float4*)(table + (size_t)vv * hidden);
+            for (int i = lane; i < h4; i += 64) ((float4*)rw)[i] = src[i];
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // the wave's row stores are done before its lanes read
+            __builtin_amdgcn_wave_barrier();
+            double r = 0.0;
+            if constexpr (DOTTILE) {
+                const int nk = hidden / 8;
+                if (lane < 8) {
+                    double p = 0.0;
+#pragma unroll 16
+                    for (int k = 0; k < nk; ++k) p = fma((double)xs[8 * k + lane], (double)rw[8 * k + lane], p);
+                    pp[wave][lane] = p;
+                }
+                __builtin_amdgcn_s_waitcnt(0xc07f);
+                __builtin_amdgcn_wave_barrier();
+                if (lane == 0) {
+                    r = (((pp[wave][0] + pp[wave][4]) + (pp[wave][2] + pp[wave][6])) +
+                         ((pp[wave][1] + pp[wave][5]) + (pp[wave][3] + pp[wave][7]))) + 0.0;
+                    for (int c = 8 * nk; c < hidden; ++c) r = fma((double)xs[c], (double)rw[c], r);
+                }
+            } else if (lane == 0) {
+#pragma unroll 8
+                for (int c = 0; c < hidden; ++c) r = fma((double)xs[c], (double)rw[c], r);
+            }
+            if (lane == 0) {
+                const float f = (float)r;
+                logits[vv] = f;
+                if (beats(f, vv, best, bidx)) {
+                    best = f;
+                    bidx = vv;
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+            __builtin_amdgcn_wave_barrier();  // the region and pp are rewritten by the next candidate
+        }
+    }
+    bv[tid] = best;
+    bi[tid] = bidx;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (tid < w && beats(bv[tid + w], bi[tid + w], bv[tid], bi[tid])) {
+            bv[tid] = bv[tid + w];
+            bi[tid] = bi[tid + w];
+        }
+        __syncthreads();
+    }
+    if (tid == 0) part[blockIdx.x] = make_float2(bv[0], __int_as_float(bi[0]));
+}
+
+template <int NCH>
+static void launch_screen_nch(const uint16_t* hb, int vocab, int hidden, const float* x, double k1, double k2,
+                              double* hi, unsigned long long* lkey, hipStream_t s) {
+    const int blocks = min(kScreenBlocks, ceil_div(vocab, 4));
+    hipLaunchKernelGGL((lm_screen_kernel<NCH, kScreenRows>), dim3(blocks), dim3(256), 0, s, (const uint4*)hb, vocab,
+                       hidden, x, k1, k2, hi, lkey);
+}
+
+hipError_t launch_lm_greedy_screened(const float* table, const uint16_t* table_bf16, int vocab, int hidden,
+                                     const float* x, int sequential, double* hi, unsigned long long* lkey,
+                                     float* logits, float2* part, int* tokens, int cap, const int* pos0,
+                                     int offset, hipStream_t s) {
+    if (vocab <= 0 || !lm_screen_ok(hidden) || ((uintptr_t)table_bf16 & 15) != 0)
+        return hipErrorInvalidValue;
+    const double n = (double)hidden + 64.0;
+    const double g32 = n * 0x1p-24 / (1.0 - n * 0x1p-24);
+    const double g64 = n * 0x1p-53 / (1.0 - n * 0x1p-53);
+    const double k1 = (g32 + 0x1p-8 + g64 * (1.0 + 0x1p-8) + 0x1p-24 * (1.0 + 0x1p-8) * (1.0 + g64)) /
+                      (1.0 - g32) * (1.0 + 0x1p-20);
+    const double k2 = 0x1p-134 * (1.0 + g64) * (1.0 + 0x1p-24) * (1.0 + 0x1p-20);
+    switch (ceil_div(hidden, 512)) {
+        case 1: launch_screen_nch<1>(table_bf16, vocab, hidden, x, k1, k2, hi, lkey, s); break;
+        case 2: launch_screen_nch<2>(table_bf16, vocab, hidden, x, k1, k2, hi, lkey, s); break;
+        case 3: launch_screen_nch<3>(table_bf16, vocab, hidden, x, k1, k2, hi, lkey, s); break;
+        case 4: launch_screen_nch<4>(table_bf16, vocab, hidden, x, k1, k2, hi, lkey, s); break;
+        case 5: launch_screen_nch<5>(table_bf16, vocab, hidden, x, k1, k2, hi, lkey, s); break;
+        default: launch_screen_nch<6>(table_bf16, vocab, hidden, x, k1, k2, hi, lkey, s); break;
+    }
+    const int parts = lm_screen_parts(vocab);
+    const size_t shm = (size_t)5 * hidden * sizeof(float);  // x and four staged rows
+    if (sequential)
+        hipLaunchKernelGGL(lm_pick_kernel<false>, dim3(parts), dim3(256), shm, s, table, vocab, hidden, x, hi, lkey,
+                           logits, part);
+    else
+        hipLaunchKernelGGL(lm_pick_kernel<true>, dim3(parts), dim3(256), shm, s, table, vocab, hidden, x, hi, lkey,
+                           logits, part);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(64), 0, s, logits, vocab, part, parts, tokens, cap, pos0,
+                       offset, lkey);
     return hipGetLastError();
 }
 

@@ -506,6 +506,13 @@ struct loom_amd_model {
     float* logits = nullptr;      // max_batch x vocab
     int* tokens = nullptr;        // max_batch x max_tokens
     float2* argmax_part = nullptr;  // max_batch x kArgmaxMaxParts
+    // screened greedy head (fp32 table, one row): bf16 copy of the table,
+    // each row's upper bound, the threshold key and per-workgroup picks
+    uint16_t* lm_bf16 = nullptr;  // vocab x hidden
+    double* screen_hi = nullptr;  // vocab
+    unsigned long long* screen_key = nullptr;
+    float2* screen_part = nullptr;  // lm_screen_parts(vocab)
+    bool head_screened = false;   // the last head left only the candidates' logits
     int* pos = nullptr;           // device position shared by every layer
     void* misc = nullptr;
     // Pinned staging for the ids that cross the boundary (prompt upload,
@@ -707,6 +714,12 @@ int loom_amd_model_create(int device, const loom_amd_model_desc* desc,
     const size_t o_lg = L.take((size_t)max_batch * desc->vocab * 4);
     const size_t o_tok = L.take((size_t)max_batch * max_tokens * 4);
     const size_t o_part = L.take((size_t)max_batch * kArgmaxMaxParts * sizeof(float2));
+    // ternary_head: the packed matrix replaces the fp32 head
+    const bool screen = !ternary_head && lm_screen_ok(H);
+    const size_t o_hb = L.take(screen ? (size_t)desc->vocab * H * 2 : 0);
+    const size_t o_hi = L.take(screen ? (size_t)desc->vocab * 8 : 0);
+    const size_t o_key = L.take(screen ? 8 : 0);
+    const size_t o_sp = L.take(screen ? (size_t)lm_screen_parts(desc->vocab) * sizeof(float2) : 0);
     const size_t o_pos = L.take(4);
     hipError_t e = hipMalloc(&m->misc, L.off);
     if (e != hipSuccess) {
@@ -722,6 +735,12 @@ int loom_amd_model_create(int device, const loom_amd_model_desc* desc,
     m->logits = (float*)(base + o_lg);
     m->tokens = (int*)(base + o_tok);
     m->argmax_part = (float2*)(base + o_part);
+    if (screen) {
+        m->lm_bf16 = (uint16_t*)(base + o_hb);
+        m->screen_hi = (double*)(base + o_hi);
+        m->screen_key = (unsigned long long*)(base + o_key);
+        m->screen_part = (float2*)(base + o_sp);
+    }
     m->pos = (int*)(base + o_pos);
     e = hipMemcpy(m->embeddings, embeddings, (size_t)desc->vocab * H * 4, hipMemcpyHostToDevice);
     if (e == hipSuccess && fp32_head) {
@@ -732,6 +751,8 @@ int loom_amd_model_create(int device, const loom_amd_model_desc* desc,
     }
     if (e == hipSuccess) e = hipMemset(m->tokens, 0, (size_t)max_batch * max_tokens * 4);
     if (e == hipSuccess) e = hipMemset(m->pos, 0, sizeof(int));
+    if (e == hipSuccess && screen) e = hipMemset(m->screen_key, 0, 8);
+    if (e == hipSuccess && screen) e = launch_bf16_round(m->lm_head, (size_t)desc->vocab * H, m->lm_bf16, nullptr);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&m->own, hipStreamNonBlocking);
     if (e == hipSuccess) {
         e = hipHostMalloc((void**)&m->host_ids, (size_t)max_batch * max_tokens * 4,
@@ -800,16 +821,33 @@ static int model_head(loom_amd_model* m, const float* last, long ld, int batch, 
             }
         }
         if (e != hipSuccess) return fail_hip("model ternary lm head", e);
+    } else if (m->lm_bf16 && batch == 1 && tune_int("LOOM_AMD_LM_SCREEN", 1) != 0) {
+        // greedy pick from a bf16 screening pass and the candidates' exact logits
+        e = launch_lm_greedy_screened(m->lm_head, m->lm_bf16, m->vocab, m->hidden, h, m->lm_sequential,
+                                      m->screen_hi, m->screen_key, m->logits, m->screen_part, m->tokens,
+                                      m->max_tokens, m->pos, offset, s);
+        if (e != hipSuccess) return fail_hip("model screened lm head", e);
+        m->head_screened = true;
+        return 0;
     } else {
         e = m->lm_sequential
                 ? launch_lm_head_seq(m->lm_head, m->vocab, m->hidden, h, batch, m->logits, s)
                 : launch_lm_head(m->lm_head, m->vocab, m->hidden, h, batch, m->logits, s);
         if (e != hipSuccess) return fail_hip("model lm head", e);
     }
+    m->head_screened = false;
     e = launch_argmax(m->logits, m->vocab, batch, m->argmax_part, m->tokens, m->max_tokens, m->pos,
                       offset, s);
     if (e != hipSuccess) return fail_hip("model argmax", e);
     return 0;
+}
+
+// every logit of the last head call (the screened head leaves only its
+// candidates' logits): the full fp32 head over the final rows still in fin
+static hipError_t model_full_logits(loom_amd_model* m, int batch, hipStream_t s) {
+    if (!m->head_screened) return hipSuccess;
+    return m->lm_sequential ? launch_lm_head_seq(m->lm_head, m->vocab, m->hidden, m->fin, batch, m->logits, s)
+                            : launch_lm_head(m->lm_head, m->vocab, m->hidden, m->fin, batch, m->logits, s);
 }
 
 int loom_amd_model_prefill(loom_amd_model* m, const int32_t* ids, int batch, int n,
@@ -846,6 +884,7 @@ int loom_amd_model_prefill(loom_amd_model* m, const int32_t* ids, int batch, int
     }
     if (model_head(m, m->x + (size_t)(n - 1) * m->hidden, (long)n * m->hidden, batch, n, s)) return -1;
     e = launch_add_int(m->pos, n, s);
+    if (e == hipSuccess && logits) e = model_full_logits(m, batch, s);
     if (e == hipSuccess && logits) {
         e = hipMemcpyAsync(logits, m->logits, (size_t)batch * m->vocab * 4, hipMemcpyDeviceToDevice, s);
     }
@@ -919,7 +958,9 @@ int loom_amd_model_decode(loom_amd_model* m, int steps, int use_graph, float* lo
         }
     }
     if (logits) {
-        e = hipMemcpyAsync(logits, m->logits, (size_t)m->batch * m->vocab * 4, hipMemcpyDeviceToDevice, s);
+        e = model_full_logits(m, m->batch, s);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(logits, m->logits, (size_t)m->batch * m->vocab * 4, hipMemcpyDeviceToDevice, s);
         if (e != hipSuccess) return fail_hip("model logits", e);
     }
     m->shadow += steps;

@@ -306,6 +306,93 @@ def test_model_decode_graph_matches_eager(orc, torch_dev, tf):
     assert model.position == 32
 
 
+def _screen_table(orc, case, vocab, hidden):
+    """LM-head tables around the screened head's cases: (table, query row id)."""
+    rng = np.random.default_rng(7)
+    e = (rng.standard_normal((vocab, hidden)) * 0.5).astype(np.float32)
+    q = np.abs(e[11]) + np.float32(0.25)  # positive entries
+    e[11] = q
+    if case == "below_bf16":
+        # three rows whose bf16 copies are the query's: the exact logits order them
+        e[100] = q * np.float32(1 + 2.0 ** -20)
+        e[2000] = q * np.float32(1 + 2.0 ** -19)
+    elif case == "ties":
+        for r in (700, 300, 2500):
+            e[r] = q * np.float32(1.5)
+    elif case == "zero_query":
+        e[11] = 0.0
+    elif case == "nan_at_0":
+        e[0, 3] = np.nan
+        e[40] = q * np.float32(2)
+    elif case == "nan_and_inf":
+        e[5, 9] = np.nan
+        e[7, 20] = np.inf
+    elif case == "overflow":
+        e[9] = np.float32(3e37)
+    elif case == "near_max":
+        # many rows within the screening bound of the maximum
+        e[1000:1400] = q * np.float32(1.2) + (rng.standard_normal((400, hidden)) * 1e-4).astype(np.float32)
+    return e, 11
+
+
+@pytest.mark.parametrize("case", ["random", "below_bf16", "ties", "zero_query", "nan_at_0", "nan_and_inf",
+                                  "overflow", "near_max", "sequential", "final_norm"])
+def test_model_screened_greedy_head(orc, torch_dev, tf, case, tuning):
+    # One row's greedy token comes from a bf16 screening pass and the exact
+    # logits of its candidates; LOOM_AMD_LM_SCREEN=0 runs the full fp32 head.
+    # Same token in both, equal to the oracle's pick over every logit, on
+    # tables built around the bound: rows equal below bf16 precision, exact
+    # ties, an all-zero query (every row a candidate), NaN at row 0 and
+    # elsewhere, an Inf entry, a logit that overflows fp32, 400 rows near the
+    # maximum; loom's sequential order; a final norm.
+    vocab, hidden = 3000, 256
+    table, qid = _screen_table(orc, "random" if case in ("sequential", "final_norm") else case, vocab, hidden)
+    cfg = tf.BlockConfig(hidden, 4, 2, 64, 512, max_seq_len=64, norm="fast")
+    fn = orc.uniform_f32(hidden, 0.5, 1.5, 91) if case == "final_norm" else None
+    model = tf.Transformer(cfg, [], table, fn, vocab=vocab, final_norm_eps=1e-6, max_tokens=8,
+                           simd_forward=case != "sequential")
+    picks = []
+    for screen in (None, "0"):
+        tuning("LOOM_AMD_LM_SCREEN", screen)
+        lg = model.prefill([3, qid], logits=True).cpu().numpy()[0]
+        tok_lg = int(model.tokens()[0, 2])
+        model.prefill([3, qid])
+        picks.append((int(model.tokens()[0, 2]), tok_lg, lg))
+    tuning("LOOM_AMD_LM_SCREEN", None)
+    (t_s, t_s2, lg_s), (t_f, t_f2, lg_f) = picks
+    want = orc.argmax_first(lg_f)
+    print(f"  {case}: screened {t_s}, full {t_f}, oracle {want}", flush=True)
+    assert lg_s.tobytes() == lg_f.tobytes()  # logits asked for are every logit, both ways
+    assert t_s == t_s2 == t_f == t_f2 == want
+    if case == "ties":
+        assert want == 300
+    if case == "below_bf16":
+        assert want == 2000
+    if case in ("zero_query", "nan_at_0"):
+        assert want == 0
+    if case == "overflow":
+        assert want == 9
+    model.release()
+
+
+def test_model_screened_head_decode(orc, torch_dev, tf, tuning):
+    # 40 graph-replayed decode steps of a two-layer model: the screened head's
+    # tokens equal the full head's (each model captures its graph under its
+    # own setting)
+    M = Model(orc, SMALL, layers=2, vocab=1000, seed=411)
+    prompt = (np.arange(7) * 53 + 1) % 1000
+    toks = []
+    for screen in (None, "0"):
+        tuning("LOOM_AMD_LM_SCREEN", screen)
+        model = M.gpu(tf, max_tokens=64, norm="fast")
+        model.prefill(prompt)
+        model.decode(40, use_graph=True)
+        toks.append(model.tokens())
+        model.release()
+    tuning("LOOM_AMD_LM_SCREEN", None)
+    assert np.array_equal(toks[0], toks[1])
+
+
 def test_model_decode_step_equals_block_chain(orc, torch_dev, tf):
     # one decode step == embedding of the newest token through the same
     # blocks (warm caches), final norm, LM head
