@@ -2816,27 +2816,29 @@ hipError_t launch_argmax(const float* logits, int n, int rows, float2* part, int
 
 // ------------------------------------------------------------------------
 // Greedy token of the fp32 LM head for one row, by screening.  Greedy
-// decoding needs the argmax of the logits, not every logit.  A bf16 copy of
-// the table (each entry rounded to nearest even: |w - h| <= 2^-8 |h| + 2^-134;
-// an entry too large for bf16 becomes Inf, a NaN stays NaN) gives for every
-// vocab row v, reading half the bytes,
-//   A_v = sum_j x_j h_vj  and  S_v = sum_j |x_j| |h_vj|
-// (fp32 chains per lane, fp64 across lanes) and, with X1 = sum_j |x_j|, the
-// bound |F_v - A_v| <= B_v = k1 S_v + k2 X1 + 2^-150 on loom's logit
-// F_v = fp32(fp64 sum of x_j w_vj in its order): k1 gathers the fp32 and fp64
-// summation errors (g_p = n 2^-p / (1 - n 2^-p), n = hidden + 64), the bf16
-// rounding (2^-8) and the final rounding to fp32 (2^-24); k2 the bf16
-// rounding below the normal range.  Every row with A_v + B_v >= L, where
-// L = max_u (A_u - B_u), is a candidate: the greedy pick g is one, since
-// A_g + B_g >= F_g >= F_u >= A_u - B_u for every row u, and so is every row
-// tying with it.  So are row 0 (the greedy rule reads logit 0) and every row
-// whose A, S or bound is not finite or reaches 2^127 (its logit may be
-// non-finite or overflow; such rows also stay out of L).  The candidates'
-// logits are computed exactly as lm_head_kernel computes them, from the fp32
-// table, and the greedy pick over them is the pick over all logits.  Only
-// the candidates' logits are written; a caller that wants every logit runs
-// lm_head_kernel.  L crosses the grid as a monotone 64-bit key (device-scope
-// atomic maximum); the final pick clears it for the next call.
+// decoding needs the argmax of the logits, not every logit.  An int8 copy of
+// the table (per vocab row v a scale s_v = max_j |w_vj| / 127 and codes
+// q_vj = round(w_vj / s_v), so |w_vj - s_v q_vj| <= s_v (1/2 + 2^-14)) gives
+// for every row, reading a quarter of the bytes,
+//   A_v = s_v * sum_j x_j q_vj   (fp32 chains per lane, fp64 across lanes)
+// and, with X1 = sum_j |x_j|, the bound |F_v - A_v| <= B_v on loom's logit
+// F_v = fp32(fp64 sum of x_j w_vj in its order):
+//   B_v = s_v X1 (1/2 + 2^-14 + 127 (g32 + g64)) + 2^-24 (|A_v| + s_v X1)
+//         + 2^-150, widened by 2^-20,
+// which covers the codes' rounding, the fp32 and fp64 summation errors
+// (g_p = n 2^-p / (1 - n 2^-p), n = hidden + 64; |q| <= 127 and
+// |w| <= 127.01 s) and the final rounding to fp32.  Every row with
+// A_v + B_v >= L, where L = max_u (A_u - B_u), is a candidate: the greedy pick
+// g is one, since A_g + B_g >= F_g >= F_u >= A_u - B_u for every row u, and so
+// is every row tying with it.  So are row 0 (the greedy rule reads logit 0)
+// and every row whose scale, sum or bound is not finite or reaches 2^127 (a
+// non-finite entry makes its scale NaN; its logit may be non-finite or
+// overflow; such rows stay out of L).  The candidates' logits are computed
+// exactly as lm_head_kernel computes them, from the fp32 table, and the
+// greedy pick over them is the pick over all logits.  Only the candidates'
+// logits are written; a caller that wants every logit runs lm_head_kernel.
+// L crosses the grid as a monotone 64-bit key (device-scope atomic maximum);
+// the final pick clears it for the next call.
 // ------------------------------------------------------------------------
 
 // order-preserving key of a non-NaN double (0 is below every key: "none")
@@ -2850,100 +2852,112 @@ __device__ __forceinline__ double lm_key_value(unsigned long long k) {
     return __longlong_as_double((long long)b);
 }
 
-__global__ void bf16_round_kernel(const float* __restrict__ w, size_t n, uint16_t* __restrict__ h) {
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
-        const unsigned u = __float_as_uint(w[i]);
-        const unsigned r = (u & 0x7fffffffu) > 0x7f800000u ? (u >> 16) | 0x40u  // NaN stays NaN
-                                                           : (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-        h[i] = (uint16_t)r;
+// one workgroup per vocab row: the row's scale (NaN when an entry is not
+// finite) and codes
+__global__ __launch_bounds__(256) void lm_quant_rows_kernel(const float* __restrict__ w, int hidden,
+                                                            int8_t* __restrict__ q, float* __restrict__ scale) {
+    __shared__ float red[4];
+    __shared__ int bad[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float* row = w + (size_t)blockIdx.x * hidden;
+    float m = 0.0f;
+    int nf = 0;
+    for (int j = tid; j < hidden; j += 256) {
+        const float v = row[j];
+        nf |= !(fabsf(v) <= 3.4028235e38f);  // NaN or Inf
+        m = fmaxf(m, fabsf(v));
     }
+    m = wave_max(m);
+    nf = wave_sum_i(nf);
+    if (lane == 0) {
+        red[wave] = m;
+        bad[wave] = nf;
+    }
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    nf = bad[0] | bad[1] | bad[2] | bad[3];
+    const float s = m / 127.0f;
+    // a scale below the normal range rounds too coarsely for the bound: such a
+    // row (and one with a non-finite entry) gets scale NaN, i.e. is always a
+    // candidate
+    const bool bad_row = nf || (m > 0.0f && s < 1.17549435e-38f);
+    int8_t* qr = q + (size_t)blockIdx.x * hidden;
+    for (int j = tid; j < hidden; j += 256) {
+        const float r = (bad_row || s == 0.0f) ? 0.0f : rintf(row[j] / s);
+        qr[j] = (int8_t)fminf(fmaxf(r, -127.0f), 127.0f);
+    }
+    if (tid == 0) scale[blockIdx.x] = bad_row ? __builtin_nanf("") : s;
 }
 
-hipError_t launch_bf16_round(const float* w, size_t n, uint16_t* h, hipStream_t s) {
-    if (n == 0) return hipSuccess;
-    const size_t blocks = (n + 255) / 256;
-    hipLaunchKernelGGL(bf16_round_kernel, dim3((unsigned)(blocks < 8192 ? blocks : 8192)), dim3(256), 0, s, w,
-                       n, h);
+hipError_t launch_lm_quant_rows(const float* w, int vocab, int hidden, int8_t* q, float* scale, hipStream_t s) {
+    if (vocab <= 0 || hidden <= 0) return hipSuccess;
+    hipLaunchKernelGGL(lm_quant_rows_kernel, dim3(vocab), dim3(256), 0, s, w, hidden, q, scale);
     return hipGetLastError();
 }
 
-constexpr int kScreenMaxChunks = 6;  // 512-column chunks per row
+constexpr int kScreenMaxChunks = 3;     // 1024-column chunks per row
 constexpr int kScreenMaxHidden = 2816;  // the pick's x and four staged rows within 64 KB of LDS
-constexpr int kScreenBlocks = 512;
-constexpr int kScreenRows = 1;       // rows in flight per wave (two waves per SIMD: 2 or 4 were slower)
-constexpr int kPickRows = 256;       // vocab rows per workgroup of the pick
+constexpr int kScreenBlocks = 1024;  // 512, 2048 and 4096 measured slower
+constexpr int kPickRows = 256;          // vocab rows per workgroup of the pick
 
-bool lm_screen_ok(int hidden) { return hidden > 0 && hidden % 8 == 0 && hidden <= kScreenMaxHidden; }
-static_assert(kScreenMaxHidden <= 512 * kScreenMaxChunks, "screening chunks cover the row");
+bool lm_screen_ok(int hidden) { return hidden > 0 && hidden % 16 == 0 && hidden <= kScreenMaxHidden; }
+static_assert(kScreenMaxHidden <= 1024 * kScreenMaxChunks, "screening chunks cover the row");
 int lm_screen_parts(int vocab) { return ceil_div(vocab, kPickRows); }
 
-// A wave per vocab row (RU rows in flight): lane l holds x at the 16-byte
-// groups l, l + 64, ... of the row and reads the same groups of the bf16 row.
-template <int NCH, int RU>
-__global__ __launch_bounds__(256) void lm_screen_kernel(const uint4* __restrict__ hb, int vocab, int hidden,
-                                                        const float* __restrict__ x, double k1, double k2,
+// A wave per vocab row: lane l holds x at the 16-column groups l, l + 64, ...
+// of the row and reads the same groups of the codes.  (Loading the next row
+// while summing the current one, or two rows at once, measured slower.)
+template <int NCH>
+__global__ __launch_bounds__(256) void lm_screen_kernel(const uint4* __restrict__ qt, const float* __restrict__ scale,
+                                                        int vocab, int hidden, const float* __restrict__ x, double k1,
                                                         double* __restrict__ hi,
                                                         unsigned long long* __restrict__ lkey) {
     __shared__ double wl[4];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int q8 = hidden / 8;
-    float xr[NCH][8];
+    const int q16 = hidden / 16;
+    float xr[NCH][16];
     double x1 = 0.0;
 #pragma unroll
     for (int k = 0; k < NCH; ++k) {
         const int g = 64 * k + lane;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            xr[k][e] = g < q8 ? x[8 * g + e] : 0.0f;
+        for (int e = 0; e < 16; ++e) {
+            xr[k][e] = g < q16 ? x[16 * g + e] : 0.0f;
             x1 += fabs((double)xr[k][e]);
         }
     }
     x1 = wave_sum_f64_dpp(x1);
-    const double tail = k2 * x1 + 0x1p-150;
     double best = -INFINITY;  // largest A - B of this wave's finite rows
-    auto row_sums = [&](const uint4 (&w)[NCH], double* A, double* S) {
-        float a = 0.0f, sa = 0.0f;
+    const int nw = gridDim.x * 4;
+    for (int v = blockIdx.x * 4 + wave; v < vocab; v += nw) {  // wave-uniform
+        const uint4* r = qt + (size_t)v * q16;
+        const float sv = scale[v];
+        uint4 w[NCH];
+#pragma unroll
+        for (int k = 0; k < NCH; ++k) {
+            const int g = 64 * k + lane;
+            w[k] = g < q16 ? load16_nt(r + g) : make_uint4(0u, 0u, 0u, 0u);
+        }
+        float a = 0.0f;
 #pragma unroll
         for (int k = 0; k < NCH; ++k) {
             const unsigned c[4] = {w[k].x, w[k].y, w[k].z, w[k].w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float f0 = __uint_as_float(c[e] << 16), f1 = __uint_as_float(c[e] & 0xffff0000u);
-                a = fmaf(xr[k][2 * e], f0, a);
-                sa = fmaf(fabsf(xr[k][2 * e]), fabsf(f0), sa);
-                a = fmaf(xr[k][2 * e + 1], f1, a);
-                sa = fmaf(fabsf(xr[k][2 * e + 1]), fabsf(f1), sa);
+#pragma unroll
+                for (int bb = 0; bb < 4; ++bb) {
+                    const float qv = (float)(int8_t)(c[e] >> (8 * bb));
+                    a = fmaf(xr[k][4 * e + bb], qv, a);
+                }
             }
         }
-        *A = wave_sum_f64_dpp((double)a);
-        *S = wave_sum_f64_dpp((double)sa);
-    };
-    auto finish = [&](int v, double A, double S) {
-        const double B = (k1 * S + tail) * (1.0 + 0x1p-30);
+        const double s = (double)sv;
+        const double A = s * wave_sum_f64_dpp((double)a);
+        const double sx = s * x1;
+        const double B = (k1 * sx + 0x1p-24 * (fabs(A) + sx) + 0x1p-150) * (1.0 + 0x1p-20);
         const bool ok = fabs(A) + B < 0x1p127;  // false for NaN and Inf too
         if (ok) best = A - B > best ? A - B : best;
         if (lane == 0) hi[v] = ok ? A + B : INFINITY;
-    };
-    const int nw = gridDim.x * 4;
-    for (int v = blockIdx.x * 4 + wave; v < vocab; v += RU * nw) {  // wave-uniform
-        uint4 w[RU][NCH];
-#pragma unroll
-        for (int u = 0; u < RU; ++u) {
-            const uint4* r = hb + (size_t)min(v + u * nw, vocab - 1) * q8;
-#pragma unroll
-            for (int k = 0; k < NCH; ++k) {
-                const int g = 64 * k + lane;
-                w[u][k] = g < q8 ? load16_nt(r + g) : make_uint4(0u, 0u, 0u, 0u);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < RU; ++u) {
-            if (v + u * nw < vocab) {
-                double A, S;
-                row_sums(w[u], &A, &S);
-                finish(v + u * nw, A, S);
-            }
-        }
     }
     if (lane == 0) wl[wave] = best;
     __syncthreads();
@@ -3036,32 +3050,26 @@ __global__ __launch_bounds__(256) void lm_pick_kernel(const float* __restrict__ 
 }
 
 template <int NCH>
-static void launch_screen_nch(const uint16_t* hb, int vocab, int hidden, const float* x, double k1, double k2,
+static void launch_screen_nch(const int8_t* qt, const float* scale, int vocab, int hidden, const float* x, double k1,
                               double* hi, unsigned long long* lkey, hipStream_t s) {
     const int blocks = min(kScreenBlocks, ceil_div(vocab, 4));
-    hipLaunchKernelGGL((lm_screen_kernel<NCH, kScreenRows>), dim3(blocks), dim3(256), 0, s, (const uint4*)hb, vocab,
-                       hidden, x, k1, k2, hi, lkey);
+    hipLaunchKernelGGL(lm_screen_kernel<NCH>, dim3(blocks), dim3(256), 0, s, (const uint4*)qt, scale, vocab, hidden,
+                       x, k1, hi, lkey);
 }
 
-hipError_t launch_lm_greedy_screened(const float* table, const uint16_t* table_bf16, int vocab, int hidden,
-                                     const float* x, int sequential, double* hi, unsigned long long* lkey,
-                                     float* logits, float2* part, int* tokens, int cap, const int* pos0,
-                                     int offset, hipStream_t s) {
-    if (vocab <= 0 || !lm_screen_ok(hidden) || ((uintptr_t)table_bf16 & 15) != 0)
-        return hipErrorInvalidValue;
+hipError_t launch_lm_greedy_screened(const float* table, const int8_t* table_q, const float* scale, int vocab,
+                                     int hidden, const float* x, int sequential, double* hi,
+                                     unsigned long long* lkey, float* logits, float2* part, int* tokens, int cap,
+                                     const int* pos0, int offset, hipStream_t s) {
+    if (vocab <= 0 || !lm_screen_ok(hidden) || ((uintptr_t)table_q & 15) != 0) return hipErrorInvalidValue;
     const double n = (double)hidden + 64.0;
     const double g32 = n * 0x1p-24 / (1.0 - n * 0x1p-24);
     const double g64 = n * 0x1p-53 / (1.0 - n * 0x1p-53);
-    const double k1 = (g32 + 0x1p-8 + g64 * (1.0 + 0x1p-8) + 0x1p-24 * (1.0 + 0x1p-8) * (1.0 + g64)) /
-                      (1.0 - g32) * (1.0 + 0x1p-20);
-    const double k2 = 0x1p-134 * (1.0 + g64) * (1.0 + 0x1p-24) * (1.0 + 0x1p-20);
-    switch (ceil_div(hidden, 512)) {
-        case 1: launch_screen_nch<1>(table_bf16, vocab, hidden, x, k1, k2, hi, lkey, s); break;
-        case 2: launch_screen_nch<2>(table_bf16, vocab, hidden, x, k1, k2, hi, lkey, s); break;
-        case 3: launch_screen_nch<3>(table_bf16, vocab, hidden, x, k1, k2, hi, lkey, s); break;
-        case 4: launch_screen_nch<4>(table_bf16, vocab, hidden, x, k1, k2, hi, lkey, s); break;
-        case 5: launch_screen_nch<5>(table_bf16, vocab, hidden, x, k1, k2, hi, lkey, s); break;
-        default: launch_screen_nch<6>(table_bf16, vocab, hidden, x, k1, k2, hi, lkey, s); break;
+    const double k1 = 0.5 + 0x1p-14 + 127.0 * (g32 + g64) * (1.0 + 0x1p-10);
+    switch (ceil_div(hidden, 1024)) {
+        case 1: launch_screen_nch<1>(table_q, scale, vocab, hidden, x, k1, hi, lkey, s); break;
+        case 2: launch_screen_nch<2>(table_q, scale, vocab, hidden, x, k1, hi, lkey, s); break;
+        default: launch_screen_nch<3>(table_q, scale, vocab, hidden, x, k1, hi, lkey, s); break;
     }
     const int parts = lm_screen_parts(vocab);
     const size_t shm = (size_t)5 * hidden * sizeof(float);  // x and four staged rows

@@ -103,19 +103,20 @@ int argmax_parts(int n);
 hipError_t launch_argmax(const float* logits, int n, int rows, float2* part, int* tokens, int cap,
                          const int* pos0, int offset, hipStream_t s);
 
-// Greedy token of the fp32 LM head for ONE row by screening with a bf16 copy
-// of the table (launch_bf16_round) and exact logits for the candidates only
-// (hidden a multiple of 8, at most 2816: lm_screen_ok).  hi holds vocab
-// doubles, part lm_screen_parts(vocab) entries; *lkey must be 0 before the
-// first call (each call leaves it 0).  Writes the token as launch_argmax does;
-// only the candidates' logits are written.
+// Greedy token of the fp32 LM head for ONE row by screening with an int8 copy
+// of the table (launch_lm_quant_rows: per-row scale and codes) and exact
+// logits for the candidates only (hidden a multiple of 16, at most 2816:
+// lm_screen_ok).  hi holds vocab doubles, part lm_screen_parts(vocab)
+// entries; *lkey must be 0 before the first call (each call leaves it 0).
+// Writes the token as launch_argmax does; only the candidates' logits are
+// written.
 bool lm_screen_ok(int hidden);
 int lm_screen_parts(int vocab);
-hipError_t launch_bf16_round(const float* w, size_t n, uint16_t* h, hipStream_t s);
-hipError_t launch_lm_greedy_screened(const float* table, const uint16_t* table_bf16, int vocab, int hidden,
-                                     const float* x, int sequential, double* hi, unsigned long long* lkey,
-                                     float* logits, float2* part, int* tokens, int cap, const int* pos0,
-                                     int offset, hipStream_t s);
+hipError_t launch_lm_quant_rows(const float* w, int vocab, int hidden, int8_t* q, float* scale, hipStream_t s);
+hipError_t launch_lm_greedy_screened(const float* table, const int8_t* table_q, const float* scale, int vocab,
+                                     int hidden, const float* x, int sequential, double* hi,
+                                     unsigned long long* lkey, float* logits, float2* part, int* tokens, int cap,
+                                     const int* pos0, int offset, hipStream_t s);
 
 hipError_t launch_set_int(int* p, int v, hipStream_t s);
 hipError_t launch_add_int(int* p, int v, hipStream_t s);

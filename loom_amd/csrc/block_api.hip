@@ -506,9 +506,11 @@ struct loom_amd_model {
     float* logits = nullptr;      // max_batch x vocab
     int* tokens = nullptr;        // max_batch x max_tokens
     float2* argmax_part = nullptr;  // max_batch x kArgmaxMaxParts
-    // screened greedy head (fp32 table, one row): bf16 copy of the table,
-    // each row's upper bound, the threshold key and per-workgroup picks
-    uint16_t* lm_bf16 = nullptr;  // vocab x hidden
+    // screened greedy head (fp32 table, one row): int8 codes and per-row
+    // scales of the table, each row's upper bound, the threshold key and
+    // per-workgroup picks
+    int8_t* lm_q = nullptr;       // vocab x hidden
+    float* lm_qscale = nullptr;   // vocab
     double* screen_hi = nullptr;  // vocab
     unsigned long long* screen_key = nullptr;
     float2* screen_part = nullptr;  // lm_screen_parts(vocab)
@@ -716,7 +718,8 @@ int loom_amd_model_create(int device, const loom_amd_model_desc* desc,
     const size_t o_part = L.take((size_t)max_batch * kArgmaxMaxParts * sizeof(float2));
     // ternary_head: the packed matrix replaces the fp32 head
     const bool screen = !ternary_head && lm_screen_ok(H);
-    const size_t o_hb = L.take(screen ? (size_t)desc->vocab * H * 2 : 0);
+    const size_t o_hb = L.take(screen ? (size_t)desc->vocab * H : 0);
+    const size_t o_qs = L.take(screen ? (size_t)desc->vocab * 4 : 0);
     const size_t o_hi = L.take(screen ? (size_t)desc->vocab * 8 : 0);
     const size_t o_key = L.take(screen ? 8 : 0);
     const size_t o_sp = L.take(screen ? (size_t)lm_screen_parts(desc->vocab) * sizeof(float2) : 0);
@@ -736,7 +739,8 @@ int loom_amd_model_create(int device, const loom_amd_model_desc* desc,
     m->tokens = (int*)(base + o_tok);
     m->argmax_part = (float2*)(base + o_part);
     if (screen) {
-        m->lm_bf16 = (uint16_t*)(base + o_hb);
+        m->lm_q = (int8_t*)(base + o_hb);
+        m->lm_qscale = (float*)(base + o_qs);
         m->screen_hi = (double*)(base + o_hi);
         m->screen_key = (unsigned long long*)(base + o_key);
         m->screen_part = (float2*)(base + o_sp);
@@ -752,7 +756,7 @@ int loom_amd_model_create(int device, const loom_amd_model_desc* desc,
     if (e == hipSuccess) e = hipMemset(m->tokens, 0, (size_t)max_batch * max_tokens * 4);
     if (e == hipSuccess) e = hipMemset(m->pos, 0, sizeof(int));
     if (e == hipSuccess && screen) e = hipMemset(m->screen_key, 0, 8);
-    if (e == hipSuccess && screen) e = launch_bf16_round(m->lm_head, (size_t)desc->vocab * H, m->lm_bf16, nullptr);
+    if (e == hipSuccess && screen) e = launch_lm_quant_rows(m->lm_head, desc->vocab, H, m->lm_q, m->lm_qscale, nullptr);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&m->own, hipStreamNonBlocking);
     if (e == hipSuccess) {
         e = hipHostMalloc((void**)&m->host_ids, (size_t)max_batch * max_tokens * 4,
@@ -821,9 +825,9 @@ static int model_head(loom_amd_model* m, const float* last, long ld, int batch, 
             }
         }
         if (e != hipSuccess) return fail_hip("model ternary lm head", e);
-    } else if (m->lm_bf16 && batch == 1 && tune_int("LOOM_AMD_LM_SCREEN", 1) != 0) {
-        // greedy pick from a bf16 screening pass and the candidates' exact logits
-        e = launch_lm_greedy_screened(m->lm_head, m->lm_bf16, m->vocab, m->hidden, h, m->lm_sequential,
+    } else if (m->lm_q && batch == 1 && tune_int("LOOM_AMD_LM_SCREEN", 1) != 0) {
+        // greedy pick from an int8 screening pass and the candidates' exact logits
+        e = launch_lm_greedy_screened(m->lm_head, m->lm_q, m->lm_qscale, m->vocab, m->hidden, h, m->lm_sequential,
                                       m->screen_hi, m->screen_key, m->logits, m->screen_part, m->tokens,
                                       m->max_tokens, m->pos, offset, s);
         if (e != hipSuccess) return fail_hip("model screened lm head", e);

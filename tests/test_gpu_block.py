@@ -312,8 +312,8 @@ def _screen_table(orc, case, vocab, hidden):
     e = (rng.standard_normal((vocab, hidden)) * 0.5).astype(np.float32)
     q = np.abs(e[11]) + np.float32(0.25)  # positive entries
     e[11] = q
-    if case == "below_bf16":
-        # three rows whose bf16 copies are the query's: the exact logits order them
+    if case == "below_code":
+        # three rows whose int8 codes and scales are the query's: the exact logits order them
         e[100] = q * np.float32(1 + 2.0 ** -20)
         e[2000] = q * np.float32(1 + 2.0 ** -19)
     elif case == "ties":
@@ -329,26 +329,36 @@ def _screen_table(orc, case, vocab, hidden):
         e[7, 20] = np.inf
     elif case == "overflow":
         e[9] = np.float32(3e37)
+    elif case == "tiny_rows":
+        # with the final norm -1 the query is -1 in every column: every row of
+        # positive entries has a negative logit, an all-zero row gives -0 and a
+        # row of negative subnormals (its scale would round coarsely) leads
+        e[:] = np.abs(e)
+        e[11] = 1.0
+        e[13] = np.float32(-1e-41)
+        e[14] = 0.0
     elif case == "near_max":
         # many rows within the screening bound of the maximum
         e[1000:1400] = q * np.float32(1.2) + (rng.standard_normal((400, hidden)) * 1e-4).astype(np.float32)
     return e, 11
 
 
-@pytest.mark.parametrize("case", ["random", "below_bf16", "ties", "zero_query", "nan_at_0", "nan_and_inf",
-                                  "overflow", "near_max", "sequential", "final_norm"])
+@pytest.mark.parametrize("case", ["random", "below_code", "ties", "zero_query", "nan_at_0", "nan_and_inf",
+                                  "overflow", "tiny_rows", "near_max", "sequential", "final_norm"])
 def test_model_screened_greedy_head(orc, torch_dev, tf, case, tuning):
-    # One row's greedy token comes from a bf16 screening pass and the exact
+    # One row's greedy token comes from an int8 screening pass and the exact
     # logits of its candidates; LOOM_AMD_LM_SCREEN=0 runs the full fp32 head.
     # Same token in both, equal to the oracle's pick over every logit, on
-    # tables built around the bound: rows equal below bf16 precision, exact
-    # ties, an all-zero query (every row a candidate), NaN at row 0 and
-    # elsewhere, an Inf entry, a logit that overflows fp32, 400 rows near the
-    # maximum; loom's sequential order; a final norm.
+    # tables built around the bound: rows equal below the codes' precision,
+    # exact ties, an all-zero query (every row a candidate), NaN at row 0 and
+    # elsewhere, an Inf entry, a logit that overflows fp32, subnormal and zero
+    # rows, 400 rows near the maximum; loom's sequential order; a final norm.
     vocab, hidden = 3000, 256
     table, qid = _screen_table(orc, "random" if case in ("sequential", "final_norm") else case, vocab, hidden)
     cfg = tf.BlockConfig(hidden, 4, 2, 64, 512, max_seq_len=64, norm="fast")
     fn = orc.uniform_f32(hidden, 0.5, 1.5, 91) if case == "final_norm" else None
+    if case == "tiny_rows":
+        fn = np.full(hidden, -1.0, np.float32)
     model = tf.Transformer(cfg, [], table, fn, vocab=vocab, final_norm_eps=1e-6, max_tokens=8,
                            simd_forward=case != "sequential")
     picks = []
@@ -366,12 +376,14 @@ def test_model_screened_greedy_head(orc, torch_dev, tf, case, tuning):
     assert t_s == t_s2 == t_f == t_f2 == want
     if case == "ties":
         assert want == 300
-    if case == "below_bf16":
+    if case == "below_code":
         assert want == 2000
     if case in ("zero_query", "nan_at_0"):
         assert want == 0
     if case == "overflow":
         assert want == 9
+    if case == "tiny_rows":
+        assert want == 13
     model.release()
 
 
