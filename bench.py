@@ -225,13 +225,16 @@ def ternary_ops_per_token(c) -> float:
 
 
 def decode_bytes_per_token(c, ctx: float) -> float:
-    """HBM bytes one decode step must read: packed ternary weights, the fp32
-    LM head, the K and V rows of `ctx` cached positions, the norm vectors."""
+    """HBM bytes one decode step must read: packed ternary weights, the LM
+    head's int8 screening copy (codes and per-row scales: the greedy head reads
+    the fp32 rows of its candidates only, about a hundred rows here, which
+    are not counted), the K and V rows of `ctx` cached positions, the norm
+    vectors."""
     h, q, kv, f = c["hidden"], c["heads"] * c["head_dim"], c["kv_heads"] * c["head_dim"], c["inter"]
     packed = (q + 2 * kv) * ((h + 15) // 16) * 4 + h * ((q + 15) // 16) * 4 \
         + 2 * f * ((h + 15) // 16) * 4 + h * ((f + 15) // 16) * 4
     norms = (2 * h + q + f) * 4
-    return c["layers"] * (packed + norms + 2 * kv * 4 * ctx) + c["vocab"] * h * 4
+    return c["layers"] * (packed + norms + 2 * kv * 4 * ctx) + c["vocab"] * (h + 4)
 
 
 def cpu_decode_sample(c, cores, log):
