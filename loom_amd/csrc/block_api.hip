@@ -825,12 +825,17 @@ static int model_head(loom_amd_model* m, const float* last, long ld, int batch, 
             }
         }
         if (e != hipSuccess) return fail_hip("model ternary lm head", e);
-    } else if (m->lm_q && batch == 1 && tune_int("LOOM_AMD_LM_SCREEN", 1) != 0) {
-        // greedy pick from an int8 screening pass and the candidates' exact logits
-        e = launch_lm_greedy_screened(m->lm_head, m->lm_q, m->lm_qscale, m->vocab, m->hidden, h, m->lm_sequential,
-                                      m->screen_hi, m->screen_key, m->logits, m->screen_part, m->tokens,
-                                      m->max_tokens, m->pos, offset, s);
-        if (e != hipSuccess) return fail_hip("model screened lm head", e);
+    } else if (m->lm_q && tune_int("LOOM_AMD_LM_SCREEN", 1) != 0) {
+        // greedy pick from an int8 screening pass and the candidates' exact
+        // logits, one row after the other (the bounds and the threshold are
+        // per row; every call leaves the threshold cleared)
+        for (int b = 0; b < batch; ++b) {
+            e = launch_lm_greedy_screened(m->lm_head, m->lm_q, m->lm_qscale, m->vocab, m->hidden,
+                                          h + (size_t)b * m->hidden, m->lm_sequential, m->screen_hi,
+                                          m->screen_key, m->logits + (size_t)b * m->vocab, m->screen_part,
+                                          m->tokens + (size_t)b * m->max_tokens, m->max_tokens, m->pos, offset, s);
+            if (e != hipSuccess) return fail_hip("model screened lm head", e);
+        }
         m->head_screened = true;
         return 0;
     } else {

@@ -387,16 +387,20 @@ def test_model_screened_greedy_head(orc, torch_dev, tf, case, tuning):
     model.release()
 
 
-def test_model_screened_head_decode(orc, torch_dev, tf, tuning):
-    # 40 graph-replayed decode steps of a two-layer model: the screened head's
+@pytest.mark.parametrize("batch", [1, 2])
+def test_model_screened_head_decode(orc, torch_dev, tf, tuning, batch):
+    # 40 graph-replayed decode steps of a two-layer model, one or two
+    # sequences (the screened head runs row after row): the screened head's
     # tokens equal the full head's (each model captures its graph under its
     # own setting)
     M = Model(orc, SMALL, layers=2, vocab=1000, seed=411)
     prompt = (np.arange(7) * 53 + 1) % 1000
+    if batch == 2:
+        prompt = np.stack([prompt, (np.arange(7) * 31 + 5) % 1000])
     toks = []
     for screen in (None, "0"):
         tuning("LOOM_AMD_LM_SCREEN", screen)
-        model = M.gpu(tf, max_tokens=64, norm="fast")
+        model = M.gpu(tf, max_tokens=64, max_batch=batch, norm="fast")
         model.prefill(prompt)
         model.decode(40, use_graph=True)
         toks.append(model.tokens())
