@@ -2881,13 +2881,18 @@ __global__ __launch_bounds__(256) void lm_quant_rows_kernel(const float* __restr
     // row (and one with a non-finite entry) gets scale NaN, i.e. is always a
     // candidate
     const bool bad_row = nf || (m > 0.0f && s < 1.17549435e-38f);
-    int8_t* qr = q + (size_t)blockIdx.x * hidden;
+    // interleaved layout: 16-column group t of row v at byte
+    // ((v / 64 * (hidden / 16) + t) * 64 + v % 64) * 16
+    const int v = blockIdx.x;
+    int8_t* qb = q + ((size_t)(v >> 6) * (hidden / 16) * 64 + (v & 63)) * 16;
     for (int j = tid; j < hidden; j += 256) {
         const float r = (bad_row || s == 0.0f) ? 0.0f : rintf(row[j] / s);
-        qr[j] = (int8_t)fminf(fmaxf(r, -127.0f), 127.0f);
+        qb[(size_t)(j >> 4) * 1024 + (j & 15)] = (int8_t)fminf(fmaxf(r, -127.0f), 127.0f);
     }
-    if (tid == 0) scale[blockIdx.x] = bad_row ? __builtin_nanf("") : s;
+    if (tid == 0) scale[v] = bad_row ? __builtin_nanf("") : s;
 }
+
+size_t lm_screen_code_bytes(int vocab, int hidden) { return (size_t)ceil_div(vocab, 64) * 64 * hidden; }
 
 hipError_t launch_lm_quant_rows(const float* w, int vocab, int hidden, int8_t* q, float* scale, hipStream_t s) {
     if (vocab <= 0 || hidden <= 0) return hipSuccess;
@@ -2895,70 +2900,75 @@ hipError_t launch_lm_quant_rows(const float* w, int vocab, int hidden, int8_t* q
     return hipGetLastError();
 }
 
-constexpr int kScreenMaxChunks = 3;     // 1024-column chunks per row
 constexpr int kScreenMaxHidden = 2816;  // the pick's x and four staged rows within 64 KB of LDS
-constexpr int kScreenBlocks = 1024;  // 512, 2048 and 4096 measured slower
+constexpr int kScreenBlocks = 1024;
 constexpr int kPickRows = 256;          // vocab rows per workgroup of the pick
 
 bool lm_screen_ok(int hidden) { return hidden > 0 && hidden % 16 == 0 && hidden <= kScreenMaxHidden; }
-static_assert(kScreenMaxHidden <= 1024 * kScreenMaxChunks, "screening chunks cover the row");
 int lm_screen_parts(int vocab) { return ceil_div(vocab, kPickRows); }
 
-// A wave per vocab row: lane l holds x at the 16-column groups l, l + 64, ...
-// of the row and reads the same groups of the codes.  (Loading the next row
-// while summing the current one, or two rows at once, measured slower.)
-template <int NCH>
+// wave maximum of doubles (no NaN), -inf where no lane has a value
+__device__ __forceinline__ double wave_max_f64_ninf(double v) {
+#define LAMD_MAXSTEP(C)                                   \
+    {                                                     \
+        const double o = dpp_d<C>(v, -INFINITY);          \
+        v = o > v ? o : v;                                \
+    }
+    LAMD_MAXSTEP(kDppShr1) LAMD_MAXSTEP(kDppShr2) LAMD_MAXSTEP(kDppShr4) LAMD_MAXSTEP(kDppShr8)
+    LAMD_MAXSTEP(kDppBcast15) LAMD_MAXSTEP(kDppBcast31)
+#undef LAMD_MAXSTEP
+    return readlane63_d(v);
+}
+
+// A wave per 64 vocab rows, lane l owning row 64 * blk + l: in the interleaved
+// code layout the wave's 16-byte loads of one 16-column group cover 1 KB
+// contiguously, and every lane reads the same x values from LDS (broadcast),
+// so no sum crosses lanes.  A row past the vocabulary (the last block's
+// padding) is summed but never stored.
 __global__ __launch_bounds__(256) void lm_screen_kernel(const uint4* __restrict__ qt, const float* __restrict__ scale,
                                                         int vocab, int hidden, const float* __restrict__ x, double k1,
                                                         double* __restrict__ hi,
                                                         unsigned long long* __restrict__ lkey) {
+    extern __shared__ float xs[];  // hidden
     __shared__ double wl[4];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int q16 = hidden / 16;
-    float xr[NCH][16];
+    const int T = hidden / 16;
+    for (int i = tid; i < hidden / 4; i += 256) ((float4*)xs)[i] = ((const float4*)x)[i];
+    __syncthreads();
     double x1 = 0.0;
-#pragma unroll
-    for (int k = 0; k < NCH; ++k) {
-        const int g = 64 * k + lane;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            xr[k][e] = g < q16 ? x[16 * g + e] : 0.0f;
-            x1 += fabs((double)xr[k][e]);
-        }
-    }
+    for (int i = lane; i < hidden; i += 64) x1 += fabs((double)xs[i]);
     x1 = wave_sum_f64_dpp(x1);
     double best = -INFINITY;  // largest A - B of this wave's finite rows
-    const int nw = gridDim.x * 4;
-    for (int v = blockIdx.x * 4 + wave; v < vocab; v += nw) {  // wave-uniform
-        const uint4* r = qt + (size_t)v * q16;
-        const float sv = scale[v];
-        uint4 w[NCH];
-#pragma unroll
-        for (int k = 0; k < NCH; ++k) {
-            const int g = 64 * k + lane;
-            w[k] = g < q16 ? load16_nt(r + g) : make_uint4(0u, 0u, 0u, 0u);
-        }
+    const int nblk = (vocab + 63) / 64;
+    for (int blk = blockIdx.x * 4 + wave; blk < nblk; blk += gridDim.x * 4) {  // wave-uniform
+        const uint4* src = qt + (size_t)blk * T * 64 + lane;
         float a = 0.0f;
-#pragma unroll
-        for (int k = 0; k < NCH; ++k) {
-            const unsigned c[4] = {w[k].x, w[k].y, w[k].z, w[k].w};
+#pragma unroll 8
+        for (int t = 0; t < T; ++t) {
+            const uint4 w = load16_nt(src + (size_t)t * 64);
+            const float4* xt = (const float4*)(xs + 16 * t);
+            const float4 xa[4] = {xt[0], xt[1], xt[2], xt[3]};
+            const unsigned c[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-#pragma unroll
-                for (int bb = 0; bb < 4; ++bb) {
-                    const float qv = (float)(int8_t)(c[e] >> (8 * bb));
-                    a = fmaf(xr[k][4 * e + bb], qv, a);
-                }
+                a = fmaf(xa[e].x, (float)(int8_t)(c[e]), a);
+                a = fmaf(xa[e].y, (float)(int8_t)(c[e] >> 8), a);
+                a = fmaf(xa[e].z, (float)(int8_t)(c[e] >> 16), a);
+                a = fmaf(xa[e].w, (float)(int8_t)(c[e] >> 24), a);
             }
         }
-        const double s = (double)sv;
-        const double A = s * wave_sum_f64_dpp((double)a);
-        const double sx = s * x1;
-        const double B = (k1 * sx + 0x1p-24 * (fabs(A) + sx) + 0x1p-150) * (1.0 + 0x1p-20);
-        const bool ok = fabs(A) + B < 0x1p127;  // false for NaN and Inf too
-        if (ok) best = A - B > best ? A - B : best;
-        if (lane == 0) hi[v] = ok ? A + B : INFINITY;
+        const int v = blk * 64 + lane;
+        if (v < vocab) {
+            const double s = (double)scale[v];
+            const double A = s * (double)a;
+            const double sx = s * x1;
+            const double B = (k1 * sx + 0x1p-24 * (fabs(A) + sx) + 0x1p-150) * (1.0 + 0x1p-20);
+            const bool ok = fabs(A) + B < 0x1p127;  // false for NaN and Inf too
+            if (ok) best = A - B > best ? A - B : best;
+            hi[v] = ok ? A + B : INFINITY;
+        }
     }
+    best = wave_max_f64_ninf(best);
     if (lane == 0) wl[wave] = best;
     __syncthreads();
     if (tid == 0) {
@@ -3049,14 +3059,6 @@ __global__ __launch_bounds__(256) void lm_pick_kernel(const float* __restrict__ 
     if (tid == 0) part[blockIdx.x] = make_float2(bv[0], __int_as_float(bi[0]));
 }
 
-template <int NCH>
-static void launch_screen_nch(const int8_t* qt, const float* scale, int vocab, int hidden, const float* x, double k1,
-                              double* hi, unsigned long long* lkey, hipStream_t s) {
-    const int blocks = min(kScreenBlocks, ceil_div(vocab, 4));
-    hipLaunchKernelGGL(lm_screen_kernel<NCH>, dim3(blocks), dim3(256), 0, s, (const uint4*)qt, scale, vocab, hidden,
-                       x, k1, hi, lkey);
-}
-
 hipError_t launch_lm_greedy_screened(const float* table, const int8_t* table_q, const float* scale, int vocab,
                                      int hidden, const float* x, int sequential, double* hi,
                                      unsigned long long* lkey, float* logits, float2* part, int* tokens, int cap,
@@ -3066,11 +3068,9 @@ hipError_t launch_lm_greedy_screened(const float* table, const int8_t* table_q, 
     const double g32 = n * 0x1p-24 / (1.0 - n * 0x1p-24);
     const double g64 = n * 0x1p-53 / (1.0 - n * 0x1p-53);
     const double k1 = 0.5 + 0x1p-14 + 127.0 * (g32 + g64) * (1.0 + 0x1p-10);
-    switch (ceil_div(hidden, 1024)) {
-        case 1: launch_screen_nch<1>(table_q, scale, vocab, hidden, x, k1, hi, lkey, s); break;
-        case 2: launch_screen_nch<2>(table_q, scale, vocab, hidden, x, k1, hi, lkey, s); break;
-        default: launch_screen_nch<3>(table_q, scale, vocab, hidden, x, k1, hi, lkey, s); break;
-    }
+    const int blocks = min(kScreenBlocks, ceil_div(ceil_div(vocab, 64), 4));
+    hipLaunchKernelGGL(lm_screen_kernel, dim3(blocks), dim3(256), (size_t)hidden * sizeof(float), s,
+                       (const uint4*)table_q, scale, vocab, hidden, x, k1, hi, lkey);
     const int parts = lm_screen_parts(vocab);
     const size_t shm = (size_t)5 * hidden * sizeof(float);  // x and four staged rows
     if (sequential)

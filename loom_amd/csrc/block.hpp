@@ -112,6 +112,9 @@ hipError_t launch_argmax(const float* logits, int n, int rows, float2* part, int
 // written.
 bool lm_screen_ok(int hidden);
 int lm_screen_parts(int vocab);
+// q holds lm_screen_code_bytes(vocab, hidden) bytes (rows in blocks of 64,
+// interleaved by 16-column group)
+size_t lm_screen_code_bytes(int vocab, int hidden);
 hipError_t launch_lm_quant_rows(const float* w, int vocab, int hidden, int8_t* q, float* scale, hipStream_t s);
 hipError_t launch_lm_greedy_screened(const float* table, const int8_t* table_q, const float* scale, int vocab,
                                      int hidden, const float* x, int sequential, double* hi,

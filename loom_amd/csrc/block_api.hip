@@ -718,7 +718,7 @@ int loom_amd_model_create(int device, const loom_amd_model_desc* desc,
     const size_t o_part = L.take((size_t)max_batch * kArgmaxMaxParts * sizeof(float2));
     // ternary_head: the packed matrix replaces the fp32 head
     const bool screen = !ternary_head && lm_screen_ok(H);
-    const size_t o_hb = L.take(screen ? (size_t)desc->vocab * H : 0);
+    const size_t o_hb = L.take(screen ? lm_screen_code_bytes(desc->vocab, H) : 0);
     const size_t o_qs = L.take(screen ? (size_t)desc->vocab * 4 : 0);
     const size_t o_hi = L.take(screen ? (size_t)desc->vocab * 8 : 0);
     const size_t o_key = L.take(screen ? 8 : 0);
@@ -756,6 +756,7 @@ int loom_amd_model_create(int device, const loom_amd_model_desc* desc,
     if (e == hipSuccess) e = hipMemset(m->tokens, 0, (size_t)max_batch * max_tokens * 4);
     if (e == hipSuccess) e = hipMemset(m->pos, 0, sizeof(int));
     if (e == hipSuccess && screen) e = hipMemset(m->screen_key, 0, 8);
+    if (e == hipSuccess && screen) e = hipMemset(m->lm_q, 0, lm_screen_code_bytes(desc->vocab, H));  // block padding
     if (e == hipSuccess && screen) e = launch_lm_quant_rows(m->lm_head, desc->vocab, H, m->lm_q, m->lm_qscale, nullptr);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&m->own, hipStreamNonBlocking);
     if (e == hipSuccess) {
