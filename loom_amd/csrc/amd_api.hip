@@ -558,12 +558,18 @@ int loom_amd_swiglu_forward(const loom_amd_matrix* gate, const loom_amd_matrix* 
         return fail("swiglu intermediate width is limited to 8192 (strict norm: 8064)");
     }
     DeviceGuard guard(G.device);
+    // a decode row: the down projection's workgroups normalize and quantize
+    // h themselves (as the decoder block does), reading the gate product from
+    // scratch and writing the normalized rows to h_out; LOOM_AMD_UNFUSED_NORM=1
+    // keeps the separate norm launch, which normalizes h in place
+    const bool fuse_down = tune_int("LOOM_AMD_UNFUSED_NORM", 0) != 1 && norm_fused_ok(m, inter, strict, true) &&
+                           ((uintptr_t)inner_norm & 15) == 0 && ((uintptr_t)h_out & 15) == 0;
     const int ldx = ld_for(hidden), ldh = ld_for(inter);
     Layout L;
     const size_t o_xq = L.take((size_t)m * ldx);
     const size_t o_am = L.take((size_t)m * 4);
     const size_t o_xs = L.take((size_t)m * 4);
-    const size_t o_h = L.take(h_out ? 0 : (size_t)m * inter * 4);
+    const size_t o_h = L.take(h_out && !fuse_down ? 0 : (size_t)m * inter * 4);
     const size_t o_hq = L.take((size_t)m * ldh);
     const size_t o_ham = L.take((size_t)m * 4);
     const size_t o_hs = L.take((size_t)m * 4);
@@ -573,7 +579,7 @@ int loom_amd_swiglu_forward(const loom_amd_matrix* gate, const loom_amd_matrix* 
     int8_t* xq = (int8_t*)(base + o_xq);
     float* am = (float*)(base + o_am);
     int32_t* xs = (int32_t*)(base + o_xs);
-    float* h = h_out ? h_out : (float*)(base + o_h);
+    float* h = h_out && !fuse_down ? h_out : (float*)(base + o_h);
     int8_t* hq = (int8_t*)(base + o_hq);
     float* ham = (float*)(base + o_ham);
     int32_t* hs = (int32_t*)(base + o_hs);
@@ -600,9 +606,6 @@ int loom_amd_swiglu_forward(const loom_amd_matrix* gate, const loom_amd_matrix* 
         e = launch_matmul(&G, &U, a, m, gu, s);
     }
     if (e != hipSuccess) return fail_hip("swiglu gate/up", e);
-    e = launch_norm_quant(h, inter, m, inter, inner_norm, eps, strict, hq, ldh, ham, hs, s);
-    if (e != hipSuccess) return fail_hip("swiglu inner norm", e);
-    QuantAct b{hq, ldh, ham, hs};
     Epilogue dn;
     dn.kind = EPI_DENSE;
     dn.activation = -1;
@@ -611,13 +614,28 @@ int loom_amd_swiglu_forward(const loom_amd_matrix* gate, const loom_amd_matrix* 
     dn.out = out;
     dn.ldo = hidden;
     dn.acc0 = taps ? taps->acc_down : nullptr;
-    e = launch_matmul(&D, nullptr, b, m, dn, s);
-    if (e != hipSuccess) return fail_hip("swiglu down", e);
+    if (fuse_down) {
+        NormTaps nt;
+        nt.rows = h_out;
+        nt.xq = taps ? taps->hq : nullptr;
+        nt.amax = taps ? taps->hamax : nullptr;
+        e = launch_matmul_norm(&D, nullptr, h, nullptr, m, NORM_INNER_F32, strict, inner_norm,
+                               eps <= 0.0 ? 1e-5 : eps, dn, nullptr, s, &nt);  // (launch_norm_quant's default eps)
+        if (e != hipSuccess) return fail_hip("swiglu inner norm + down", e);
+    } else {
+        e = launch_norm_quant(h, inter, m, inter, inner_norm, eps, strict, hq, ldh, ham, hs, s);
+        if (e != hipSuccess) return fail_hip("swiglu inner norm", e);
+        QuantAct b{hq, ldh, ham, hs};
+        e = launch_matmul(&D, nullptr, b, m, dn, s);
+        if (e != hipSuccess) return fail_hip("swiglu down", e);
+    }
     if (taps) {
         if (!fused && taps->xq) e = hipMemcpy2DAsync(taps->xq, hidden, xq, ldx, hidden, m, hipMemcpyDeviceToDevice, s);
         if (e == hipSuccess && !fused && taps->amax) e = hipMemcpyAsync(taps->amax, am, (size_t)m * 4, hipMemcpyDeviceToDevice, s);
-        if (e == hipSuccess && taps->hq) e = hipMemcpy2DAsync(taps->hq, inter, hq, ldh, inter, m, hipMemcpyDeviceToDevice, s);
-        if (e == hipSuccess && taps->hamax) e = hipMemcpyAsync(taps->hamax, ham, (size_t)m * 4, hipMemcpyDeviceToDevice, s);
+        if (e == hipSuccess && !fuse_down && taps->hq)
+            e = hipMemcpy2DAsync(taps->hq, inter, hq, ldh, inter, m, hipMemcpyDeviceToDevice, s);
+        if (e == hipSuccess && !fuse_down && taps->hamax)
+            e = hipMemcpyAsync(taps->hamax, ham, (size_t)m * 4, hipMemcpyDeviceToDevice, s);
         if (e != hipSuccess) return fail_hip("swiglu taps", e);
     }
     return 0;

@@ -486,6 +486,25 @@ def test_swiglu_biases_bitnet_2b_shape(orc, torch_dev, bn, M):
                  with_norm_w=True, with_bias=True)
 
 
+@pytest.mark.parametrize("norm", ["strict", "fast"])
+@pytest.mark.parametrize("shape", [(64, 160), (2560, 6912)])
+def test_swiglu_row_norm_in_down(orc, torch_dev, bn, norm, shape, tuning):
+    # One row: the down projection's workgroups normalize and quantize h
+    # themselves and write the normalized rows to h_out; with
+    # LOOM_AMD_UNFUSED_NORM=1 the separate inner-norm launch does it.  Both
+    # pass every stage check against the oracle; strict sums give the same
+    # normalized rows byte for byte.
+    hidden, inter = shape
+    got = {}
+    for unfused in (None, "1"):
+        tuning("LOOM_AMD_UNFUSED_NORM", unfused)
+        got[unfused] = _swiglu_case(orc, torch_dev, bn, hidden=hidden, inter=inter, M=1, seed=1310 + hidden,
+                                    norm=norm, with_norm_w=True, with_bias=True)[0]
+    tuning("LOOM_AMD_UNFUSED_NORM", None)
+    if norm == "strict":
+        assert got[None].tobytes() == got["1"].tobytes()
+
+
 @pytest.mark.parametrize("M", [1, 8, 64, 256])
 def test_swiglu_bitnet_2b_shape(orc, torch_dev, bn, M):
     hg, ref = _swiglu_case(orc, torch_dev, bn, hidden=2560, inter=6912, M=M, seed=1234 + M,
