@@ -2207,9 +2207,17 @@ size_t attention_lds_bytes(int hd, int span) {
     return ((size_t)((hd + 1) & ~1) + (size_t)span) * sizeof(double);
 }
 
+// Fast prefill attention: 0 picks per call (the two-pass kernel for up to
+// kAutoTwoPassRows rows when the one-pass grid has fewer workgroups than the
+// chip has CUs: at one BitNet-2B sequence of 512 the block took 209.5 against
+// 229.6 us), 1 the one-pass kernel always, 2 or 4 the two-pass kernel with
+// that many 16-query tiles per workgroup.
+constexpr int kAutoTwoPassRows = 1024;
+constexpr int kAutoTwoPassGrid = 256;
+
 int attention_fast_two_pass_qt() {
     const int qt = tune_int("LOOM_AMD_ATTN_QT", 0);
-    return qt == 2 || qt == 4 ? qt : 0;
+    return qt == 1 || qt == 2 || qt == 4 ? qt : 0;
 }
 
 size_t attention_scratch_bytes(int rows, int heads, int hd, int span, int strict, int fast_qt) {
@@ -2217,7 +2225,8 @@ size_t attention_scratch_bytes(int rows, int heads, int hd, int span, int strict
     // every row (rows x heads x span fp64); the one-pass kernel needs none
     if (rows > kSplitMaxRows) {
         if (hd != 64 && hd != 128) return 0;
-        if (!strict && fast_qt == 0) return 0;
+        if (!strict && fast_qt == 1) return 0;
+        if (!strict && fast_qt == 0) rows = rows < kAutoTwoPassRows ? rows : kAutoTwoPassRows;
         return (size_t)rows * heads * span * 8;
     }
     // (room for 32-position chunks; the 64-position kernels use a prefix of each region)
@@ -2366,12 +2375,15 @@ hipError_t launch_attention(const double* q, const float* cache_k, const float* 
         return hipGetLastError();
     }
     if (hd == 64 || hd == 128) {
-        const int qt = fast_qt == 2 || fast_qt == 4 ? fast_qt : 0;
+        // one-pass grid: heads sharing one KV head go to one workgroup, up to four
+        const int group = heads / kv_heads;
+        const int hpw = group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
+        const dim3 gridh(heads / hpw, ceil_div(seq, 64 / hpw), batch);
+        int qt = fast_qt == 2 || fast_qt == 4 ? fast_qt : 0;
+        if (fast_qt == 0 && (long)gridh.x * gridh.y * gridh.z < kAutoTwoPassGrid && rows <= kAutoTwoPassRows &&
+            scratch && span % 2 == 0)
+            qt = 2;  // too few one-pass workgroups to fill the chip
         if (!strict && qt == 0) {
-            // heads sharing one KV head go to one workgroup, up to four
-            const int group = heads / kv_heads;
-            const int hpw = group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
-            const dim3 gridh(heads / hpw, ceil_div(seq, 64 / hpw), batch);
 #define LAMD_FLASH(HDV, HPWV)                                                                    \
     hipLaunchKernelGGL((attn_flash_mfma_kernel<HDV, HPWV>), gridh, dim3(256), 0, s, q, cache_k, \
                        cache_v, pos0, msl, span, heads, kv_heads, seq, out)

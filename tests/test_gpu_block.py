@@ -209,16 +209,17 @@ def test_block_refuses_decode_batch_other_than_warm_cache(orc, torch_dev, tf):
 def test_fast_prefill_attention_kernels_agree(orc, torch_dev, tf, tuning, hd, seq):
     # the two-pass fast prefill kernel with 32 or 64 queries per workgroup
     # sums in the same order: identical bytes for the block output and its K/V
-    # caches, ragged last query tile included.  The default one-pass kernel
-    # (running maximum) sums in another fixed order: its attention rows are
-    # within the fast bar (1e-12 of the row scale) of the two-pass rows, and
-    # its K/V caches are the same bytes.
+    # caches, ragged last query tile included.  The one-pass kernel (running
+    # maximum; LOOM_AMD_ATTN_QT=1 forces it) sums in another fixed order: its
+    # attention rows are within the fast bar (1e-12 of the row scale) of the
+    # two-pass rows, and its K/V caches are the same bytes.  Unset, a grid this
+    # small takes the two-pass kernel: the same bytes as "2".
     torch = torch_dev
     sh = Shape(hd * 4, 4, 2, hd, 512, 512)
     w = Weights(orc, sh, seed=451)
     x = orc.normal_f32(seq * sh.hidden, seed=452).reshape(seq, sh.hidden)
     outs, attn, kv = [], [], []
-    for qt in ("2", "4", ""):
+    for qt in ("2", "4", "1", ""):
         tuning("LOOM_AMD_ATTN_QT", qt)
         blk = tf.BitNetBlock(w.cfg(tf, norm="fast"), w.gpu(tf))
         xd = to_dev(torch, x)
@@ -228,11 +229,11 @@ def test_fast_prefill_attention_kernels_agree(orc, torch_dev, tf, tuning, hd, se
         attn.append(T.numpy()["attn"])
         kv.append(b"".join(c.cpu().numpy().tobytes() for c in blk.kv_cache()))
         blk.release()
-    assert outs[0] == outs[1] and kv[0] == kv[1] == kv[2]
-    assert np.array_equal(attn[0], attn[1])
+    assert outs[0] == outs[1] == outs[3] and kv[0] == kv[1] == kv[2] == kv[3]
+    assert np.array_equal(attn[0], attn[1]) and np.array_equal(attn[0], attn[3])
     scale = np.abs(attn[0]).max(axis=-1, keepdims=True)
     assert np.all(np.abs(attn[2] - attn[0]) <= 1e-12 * scale)
-    assert not np.array_equal(attn[2], np.zeros_like(attn[2]))
+    assert not np.array_equal(attn[2], attn[0])  # (the one-pass kernel did run)
 
 
 # ---------------------------------------------------------------- model / decode loop
