@@ -2832,7 +2832,7 @@ hipError_t launch_argmax(const float* logits, int n, int rows, float2* part, int
 // the table (per vocab row v a scale s_v = max_j |w_vj| / 127 and codes
 // q_vj = round(w_vj / s_v), so |w_vj - s_v q_vj| <= s_v (1/2 + 2^-14)) gives
 // for every row, reading a quarter of the bytes,
-//   A_v = s_v * sum_j x_j q_vj   (fp32 chains per lane, fp64 across lanes)
+//   A_v = s_v * sum_j x_j q_vj   (one fp32 multiply-add chain per row, then an fp64 product)
 // and, with X1 = sum_j |x_j|, the bound |F_v - A_v| <= B_v on loom's logit
 // F_v = fp32(fp64 sum of x_j w_vj in its order):
 //   B_v = s_v X1 (1/2 + 2^-14 + 127 (g32 + g64)) + 2^-24 (|A_v| + s_v X1)
